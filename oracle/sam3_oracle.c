@@ -1,0 +1,606 @@
+/*
+ * oracle/sam3_oracle.c - CPU restatement of sam3.c's matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and CPU baseline ("port")
+ * for the HIP backend. Nothing in the product path calls this file.
+ *
+ * Each routine restates the x86 scalar branch of the cited reference
+ * code with the same per-element operation order (no FP contraction,
+ * built -std=c11 -O2 -ffp-contract=off), so outputs are bit-identical to
+ * the reference's own x86 build. Paths are relative to /root/reference.
+ *
+ * Parity pins, per function (tests/test_oracle.py):
+ *   q8 quantize/dequantize, block count/nbytes: golden vectors from the
+ *     reference, direct _ref comparison, tests/test_quant.c known answers,
+ *     |q| <= 127 and scale == amax/127 invariants.
+ *   fp16/bf16 conversions: exhaustive 65536-pattern sweeps and a 2^20
+ *     f32 sweep against _ref's cpu_kernel_cast; golden vectors.
+ *   matmul f32/bf16/f16/q8: golden vectors, _ref comparison, the
+ *     reference tests' known answers (58,64,139,154; identity), one-hot
+ *     rows and float64 brute force.
+ *   matmul_q8_nt: per output column it must equal the reference Q8
+ *     kernel run with B = W[n,:] viewed as [K,1] (same memory, same
+ *     arithmetic); checked bit-exactly against _ref and golden vectors.
+ *   matmul_f16_acc32 (no reference counterpart: the reference f16 GEMM
+ *     accumulates in fp16): pinned by float64 brute force, by equality
+ *     with the bf16 kernel's structure on inputs exactly representable in
+ *     both formats, and by identity/one-hot closed forms.
+ *   bias add / gelu: golden vectors and _ref comparison.
+ *   batched bf16: per-slice equality with the 2-D kernel and _ref.
+ */
+#include "sam3_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* Bit casts (src/core/half.h:33-47 use memcpy for the same purpose).   */
+/* ------------------------------------------------------------------ */
+static inline float bits_to_f32(uint32_t u)
+{
+	float f;
+	memcpy(&f, &u, 4);
+	return f;
+}
+
+static inline uint32_t f32_to_bits(float f)
+{
+	uint32_t u;
+	memcpy(&u, &f, 4);
+	return u;
+}
+
+/* ------------------------------------------------------------------ */
+/* fp16 <-> f32 (src/core/half.h:58-161)                               */
+/* ------------------------------------------------------------------ */
+float oracle_fp16_to_f32(uint16_t h)
+{
+	uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+	uint32_t e = (h >> 10) & 0x1Fu;
+	uint32_t m = h & 0x3FFu;
+
+	if (e == 0x1Fu)                       /* inf / nan */
+		return bits_to_f32(s | 0x7F800000u | (m << 13));
+	if (e != 0u)                          /* normal: rebias 15 -> 127 */
+		return bits_to_f32(s | ((e + 112u) << 23) | (m << 13));
+	if (m == 0u)                          /* signed zero */
+		return bits_to_f32(s);
+	/* subnormal: shift the leading one up to bit 10 */
+	uint32_t e32 = 113u;
+	while (!(m & 0x400u)) {
+		m <<= 1;
+		e32--;
+	}
+	return bits_to_f32(s | (e32 << 23) | ((m & 0x3FFu) << 13));
+}
+
+uint16_t oracle_f32_to_fp16(float f)
+{
+	uint32_t u = f32_to_bits(f);
+	uint32_t s = (u >> 16) & 0x8000u;
+	uint32_t e8 = (u >> 23) & 0xFFu;
+	uint32_t m = u & 0x7FFFFFu;
+	int32_t e = (int32_t)e8 - 112;        /* rebias 127 -> 15 */
+
+	if (e >= 31) {
+		if (e8 == 0xFFu)              /* inf, or nan with payload kept */
+			return (uint16_t)(s | 0x7C00u |
+					  (m ? ((m >> 13) | 1u) : 0u));
+		return (uint16_t)(s | 0x7C00u);  /* overflow */
+	}
+	if (e <= 0) {
+		if (e < -10)
+			return (uint16_t)s;   /* underflow to signed zero */
+		m = (m | 0x800000u) >> (1 - e);
+		uint32_t half = m & 0x1000u, rest = m & 0x0FFFu;
+		m >>= 13;
+		if (half && (rest || (m & 1u)))
+			m++;          /* may carry into the smallest normal */
+		return (uint16_t)(s | m);
+	}
+	uint32_t half = m & 0x1000u, rest = m & 0x0FFFu;
+	m >>= 13;
+	if (half && (rest || (m & 1u))) {
+		m++;
+		if (m == 0x400u) {
+			m = 0;
+			if (++e >= 31)
+				return (uint16_t)(s | 0x7C00u);
+		}
+	}
+	return (uint16_t)(s | ((uint32_t)e << 10) | m);
+}
+
+/* ------------------------------------------------------------------ */
+/* bf16 <-> f32 (src/core/half.h:173-210)                              */
+/* ------------------------------------------------------------------ */
+float oracle_bf16_to_f32(uint16_t b)
+{
+	return bits_to_f32((uint32_t)b << 16);
+}
+
+uint16_t oracle_f32_to_bf16(float f)
+{
+	uint32_t u = f32_to_bits(f);
+
+	if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu))
+		return (uint16_t)((u >> 16) | 0x40u);   /* quiet NaN */
+	uint32_t t = u >> 16;
+	if (((u >> 15) & 1u) && ((u & 0x7FFFu) || (t & 1u)))
+		t++;                                    /* round half even */
+	return (uint16_t)t;
+}
+
+void oracle_cast_f32_to_bf16(const float *src, uint16_t *dst, int n)
+{
+	for (int i = 0; i < n; i++)
+		dst[i] = oracle_f32_to_bf16(src[i]);
+}
+
+void oracle_cast_f32_to_fp16(const float *src, uint16_t *dst, int n)
+{
+	for (int i = 0; i < n; i++)
+		dst[i] = oracle_f32_to_fp16(src[i]);
+}
+
+void oracle_cast_bf16_to_f32(const uint16_t *src, float *dst, int n)
+{
+	for (int i = 0; i < n; i++)
+		dst[i] = oracle_bf16_to_f32(src[i]);
+}
+
+void oracle_cast_fp16_to_f32(const uint16_t *src, float *dst, int n)
+{
+	for (int i = 0; i < n; i++)
+		dst[i] = oracle_fp16_to_f32(src[i]);
+}
+
+/* ------------------------------------------------------------------ */
+/* Q8_0 (src/core/quant.h:22-33, src/core/quant.c:29-165)              */
+/* A block is 36 bytes: f32 scale then 32 int8 values.                  */
+/* ------------------------------------------------------------------ */
+struct q8blk {
+	float  d;
+	int8_t q[ORACLE_Q8_BLOCK];
+};
+
+int oracle_q8_block_count(int nelems)
+{
+	return (nelems + ORACLE_Q8_BLOCK - 1) / ORACLE_Q8_BLOCK;
+}
+
+size_t oracle_q8_nbytes(int nelems)
+{
+	return (size_t)oracle_q8_block_count(nelems) * sizeof(struct q8blk);
+}
+
+/* x86 branch of quant.c:67-130: amax by fabsf, scale = amax/127,
+ * q = clamp((int)roundf(x * (1/scale)), -127, 127); zero block -> all 0. */
+void oracle_q8_quantize(const float *src, void *dst_blocks, int nelems)
+{
+	struct q8blk *dst = dst_blocks;
+	int nb = oracle_q8_block_count(nelems);
+
+	for (int b = 0; b < nb; b++) {
+		const float *x = src + (size_t)b * ORACLE_Q8_BLOCK;
+		int n = nelems - b * ORACLE_Q8_BLOCK;
+		if (n > ORACLE_Q8_BLOCK)
+			n = ORACLE_Q8_BLOCK;
+
+		float amax = 0.0f;
+		for (int i = 0; i < n; i++)
+			if (fabsf(x[i]) > amax)
+				amax = fabsf(x[i]);
+
+		struct q8blk *o = &dst[b];
+		o->d = amax / 127.0f;
+		memset(o->q, 0, sizeof(o->q));
+		if (o->d == 0.0f)
+			continue;
+
+		float inv = 1.0f / o->d;
+		for (int i = 0; i < n; i++) {
+			int v = (int)roundf(x[i] * inv);
+			o->q[i] = (int8_t)(v > 127 ? 127 : (v < -127 ? -127 : v));
+		}
+	}
+}
+
+/* quant.c:134-165: x = (float)q * scale. */
+void oracle_q8_dequantize(const void *src_blocks, float *dst, int nelems)
+{
+	const struct q8blk *src = src_blocks;
+
+	for (int i = 0; i < nelems; i++) {
+		const struct q8blk *blk = &src[i / ORACLE_Q8_BLOCK];
+		dst[i] = (float)blk->q[i % ORACLE_Q8_BLOCK] * blk->d;
+	}
+}
+
+/* ------------------------------------------------------------------ */
+/* Fork-join row split, as sam3_threadpool_parallel_for drives the      */
+/* kernels (src/util/threadpool.c:236-281 with the per-kernel split     */
+/* chunk = M / n_tasks, last task takes the remainder, e.g.             */
+/* src/backend/cpu/kernels/cpu_matmul_q8.c:145-157). Rows are           */
+/* independent, so the split never changes results.                     */
+/* ------------------------------------------------------------------ */
+typedef void (*rows_fn)(void *ctx, int m0, int m1);
+
+struct split_task {
+	rows_fn fn;
+	void   *ctx;
+	int     m0, m1;
+};
+
+static void *split_worker(void *arg)
+{
+	struct split_task *t = arg;
+	t->fn(t->ctx, t->m0, t->m1);
+	return NULL;
+}
+
+static void run_rows(rows_fn fn, void *ctx, int M, int n_threads)
+{
+	if (n_threads <= 1 || M < 2) {
+		fn(ctx, 0, M);
+		return;
+	}
+	if (n_threads > 256)
+		n_threads = 256;
+
+	struct split_task tasks[256];
+	pthread_t tids[256];
+	int chunk = M / n_threads;
+
+	for (int t = 0; t < n_threads; t++) {
+		tasks[t].fn = fn;
+		tasks[t].ctx = ctx;
+		tasks[t].m0 = t * chunk;
+		tasks[t].m1 = (t == n_threads - 1) ? M : (t + 1) * chunk;
+	}
+	int started[256] = {0};
+	for (int t = 1; t < n_threads; t++)
+		if (tasks[t].m0 < tasks[t].m1)
+			started[t] = pthread_create(&tids[t], NULL,
+						    split_worker, &tasks[t]) == 0;
+	/* the caller runs task 0, and any task whose thread failed */
+	if (tasks[0].m0 < tasks[0].m1)
+		fn(ctx, tasks[0].m0, tasks[0].m1);
+	for (int t = 1; t < n_threads; t++) {
+		if (started[t])
+			pthread_join(tids[t], NULL);
+		else if (tasks[t].m0 < tasks[t].m1)
+			fn(ctx, tasks[t].m0, tasks[t].m1);
+	}
+}
+
+struct mm_ctx {
+	const void *a, *b;
+	void       *c;
+	int         M, K, N;
+};
+
+/* Tile sizes of the reference kernels (cpu_matmul*.c: TILE_M/N/K). */
+#define TM 8
+#define TN 8
+#define TK 64
+
+static inline int imin(int x, int y) { return x < y ? x : y; }
+
+/* ---- f32: cpu_matmul.c:40-63 (scalar; C zeroed, then c += a*b) ---- */
+static void mm_f32_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const float *a = x->a, *b = x->b;
+	float *c = x->c;
+	int K = x->K, N = x->N;
+
+	memset(c + (size_t)m0 * N, 0, (size_t)(m1 - m0) * N * sizeof(float));
+	for (int i0 = m0; i0 < m1; i0 += TM)
+		for (int j0 = 0; j0 < N; j0 += TN)
+			for (int k0 = 0; k0 < K; k0 += TK)
+				for (int i = i0; i < imin(i0 + TM, m1); i++)
+					for (int k = k0; k < imin(k0 + TK, K); k++) {
+						float av = a[(size_t)i * K + k];
+						for (int j = j0; j < imin(j0 + TN, N); j++)
+							c[(size_t)i * N + j] +=
+								av * b[(size_t)k * N + j];
+					}
+}
+
+void oracle_matmul_f32(const float *a, const float *b, float *c,
+		       int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, b, c, M, K, N };
+	run_rows(mm_f32_rows, &x, M, n_threads);
+}
+
+/* ---- bf16: cpu_matmul_bf16.c:103-141 (f32 tile acc, one RNE out) ---- */
+static void mm_bf16_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const uint16_t *a = x->a, *b = x->b;
+	uint16_t *c = x->c;
+	int K = x->K, N = x->N;
+
+	for (int i0 = m0; i0 < m1; i0 += TM) {
+		int i1 = imin(i0 + TM, m1);
+		for (int j0 = 0; j0 < N; j0 += TN) {
+			int j1 = imin(j0 + TN, N);
+			float acc[TM][TN] = {{0}};
+			for (int k0 = 0; k0 < K; k0 += TK)
+				for (int i = i0; i < i1; i++)
+					for (int k = k0; k < imin(k0 + TK, K); k++) {
+						float av = oracle_bf16_to_f32(
+							a[(size_t)i * K + k]);
+						for (int j = j0; j < j1; j++)
+							acc[i - i0][j - j0] += av *
+								oracle_bf16_to_f32(
+								b[(size_t)k * N + j]);
+					}
+			for (int i = i0; i < i1; i++)
+				for (int j = j0; j < j1; j++)
+					c[(size_t)i * N + j] =
+						oracle_f32_to_bf16(acc[i - i0][j - j0]);
+		}
+	}
+}
+
+void oracle_matmul_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c,
+			int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, b, c, M, K, N };
+	run_rows(mm_bf16_rows, &x, M, n_threads);
+}
+
+/* ---- f16: cpu_matmul_f16.c:73-101 (fp16 accumulator, rounded each k) ---- */
+static void mm_f16_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const uint16_t *a = x->a, *b = x->b;
+	uint16_t *c = x->c;
+	int K = x->K, N = x->N;
+
+	memset(c + (size_t)m0 * N, 0, (size_t)(m1 - m0) * N * sizeof(uint16_t));
+	for (int i0 = m0; i0 < m1; i0 += TM)
+		for (int j0 = 0; j0 < N; j0 += TN)
+			for (int k0 = 0; k0 < K; k0 += TK)
+				for (int i = i0; i < imin(i0 + TM, m1); i++)
+					for (int k = k0; k < imin(k0 + TK, K); k++) {
+						float av = oracle_fp16_to_f32(
+							a[(size_t)i * K + k]);
+						for (int j = j0; j < imin(j0 + TN, N); j++) {
+							uint16_t *cp = &c[(size_t)i * N + j];
+							float cur = oracle_fp16_to_f32(*cp);
+							float bv = oracle_fp16_to_f32(
+								b[(size_t)k * N + j]);
+							*cp = oracle_f32_to_fp16(cur + av * bv);
+						}
+					}
+}
+
+void oracle_matmul_f16(const uint16_t *a, const uint16_t *b, uint16_t *c,
+		       int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, b, c, M, K, N };
+	run_rows(mm_f16_rows, &x, M, n_threads);
+}
+
+/* ---- f16 with an f32 accumulator: the bf16 kernel's structure
+ * (cpu_matmul_bf16.c:103-141) with the fp16 converters of half.h. No
+ * reference kernel computes this; it is the f16 parity target. ---- */
+static void mm_f16acc32_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const uint16_t *a = x->a, *b = x->b;
+	uint16_t *c = x->c;
+	int K = x->K, N = x->N;
+
+	for (int i0 = m0; i0 < m1; i0 += TM) {
+		int i1 = imin(i0 + TM, m1);
+		for (int j0 = 0; j0 < N; j0 += TN) {
+			int j1 = imin(j0 + TN, N);
+			float acc[TM][TN] = {{0}};
+			for (int k0 = 0; k0 < K; k0 += TK)
+				for (int i = i0; i < i1; i++)
+					for (int k = k0; k < imin(k0 + TK, K); k++) {
+						float av = oracle_fp16_to_f32(
+							a[(size_t)i * K + k]);
+						for (int j = j0; j < j1; j++)
+							acc[i - i0][j - j0] += av *
+								oracle_fp16_to_f32(
+								b[(size_t)k * N + j]);
+					}
+			for (int i = i0; i < i1; i++)
+				for (int j = j0; j < j1; j++)
+					c[(size_t)i * N + j] =
+						oracle_f32_to_fp16(acc[i - i0][j - j0]);
+		}
+	}
+}
+
+void oracle_matmul_f16_acc32(const uint16_t *a, const uint16_t *b,
+			     uint16_t *c, int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, b, c, M, K, N };
+	run_rows(mm_f16acc32_rows, &x, M, n_threads);
+}
+
+/* ---- Q8: cpu_matmul_q8.c:39-134, x86 scalar loop :124-131.
+ * B[K,N] is one flat array of blocks over the linear index k*N + n.
+ * Per output element: c += (a * (float)q) * scale, k ascending. ---- */
+static void mm_q8_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const float *a = x->a;
+	const struct q8blk *blk = x->b;
+	float *c = x->c;
+	int K = x->K, N = x->N;
+
+	for (int i = m0; i < m1; i++) {
+		float *crow = c + (size_t)i * N;
+		memset(crow, 0, (size_t)N * sizeof(float));
+		for (int k = 0; k < K; k++) {
+			float av = a[(size_t)i * K + k];
+			size_t lin = (size_t)k * N;
+			for (int j = 0; j < N; j++, lin++) {
+				const struct q8blk *bb = &blk[lin / ORACLE_Q8_BLOCK];
+				crow[j] += av * (float)bb->q[lin % ORACLE_Q8_BLOCK]
+					   * bb->d;
+			}
+		}
+	}
+}
+
+void oracle_matmul_q8(const float *a, const void *b_blocks, float *c,
+		      int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, b_blocks, c, M, K, N };
+	run_rows(mm_q8_rows, &x, M, n_threads);
+}
+
+/* ---- Q8 with W[N,K] (blocks along K, linear index n*K + k). Column n
+ * is exactly the reference Q8 kernel with B = W[n,:] as a [K,1] tensor:
+ * c[n] += (a[k] * (float)q) * scale, k ascending. ---- */
+static void mm_q8_nt_rows(void *p, int m0, int m1)
+{
+	struct mm_ctx *x = p;
+	const float *a = x->a;
+	const struct q8blk *blk = x->b;
+	float *c = x->c;
+	int K = x->K, N = x->N;
+
+	for (int i = m0; i < m1; i++) {
+		const float *arow = a + (size_t)i * K;
+		for (int j = 0; j < N; j++) {
+			float acc = 0.0f;
+			size_t lin = (size_t)j * K;
+			for (int k = 0; k < K; k++, lin++) {
+				const struct q8blk *bb = &blk[lin / ORACLE_Q8_BLOCK];
+				acc += arow[k] * (float)bb->q[lin % ORACLE_Q8_BLOCK]
+				       * bb->d;
+			}
+			c[(size_t)i * N + j] = acc;
+		}
+	}
+}
+
+void oracle_matmul_q8_nt(const float *a, const void *w_blocks, float *c,
+			 int M, int K, int N, int n_threads)
+{
+	struct mm_ctx x = { a, w_blocks, c, M, K, N };
+	run_rows(mm_q8_nt_rows, &x, M, n_threads);
+}
+
+/* ------------------------------------------------------------------ */
+/* Transpose: cpu_transpose.c:355-366 (2-D swap of the last two dims,   */
+/* a plain element copy).                                               */
+/* ------------------------------------------------------------------ */
+void oracle_transpose_u16(const uint16_t *src, uint16_t *dst, int R, int C)
+{
+	for (int r = 0; r < R; r++)
+		for (int c = 0; c < C; c++)
+			dst[(size_t)c * R + r] = src[(size_t)r * C + c];
+}
+
+void oracle_transpose_f32(const float *src, float *dst, int R, int C)
+{
+	for (int r = 0; r < R; r++)
+		for (int c = 0; c < C; c++)
+			dst[(size_t)c * R + r] = src[(size_t)r * C + c];
+}
+
+/* ------------------------------------------------------------------ */
+/* Bias add: out = x + bias[j] over the last dim                        */
+/* (cpu_elementwise.c:28-63 + add_f32_scalar; cpu_add_bf16.c:62-63,     */
+/* 86-98; cpu_add_f16.c:87-95: convert, add in f32, round once).         */
+/* ------------------------------------------------------------------ */
+void oracle_bias_add_f32(const float *x, const float *bias, float *out,
+			 int rows, int N)
+{
+	for (int r = 0; r < rows; r++)
+		for (int j = 0; j < N; j++)
+			out[(size_t)r * N + j] = x[(size_t)r * N + j] + bias[j];
+}
+
+void oracle_bias_add_bf16(const uint16_t *x, const uint16_t *bias,
+			  uint16_t *out, int rows, int N)
+{
+	for (int r = 0; r < rows; r++)
+		for (int j = 0; j < N; j++)
+			out[(size_t)r * N + j] = oracle_f32_to_bf16(
+				oracle_bf16_to_f32(x[(size_t)r * N + j]) +
+				oracle_bf16_to_f32(bias[j]));
+}
+
+void oracle_bias_add_f16(const uint16_t *x, const uint16_t *bias,
+			 uint16_t *out, int rows, int N)
+{
+	for (int r = 0; r < rows; r++)
+		for (int j = 0; j < N; j++)
+			out[(size_t)r * N + j] = oracle_f32_to_fp16(
+				oracle_fp16_to_f32(x[(size_t)r * N + j]) +
+				oracle_fp16_to_f32(bias[j]));
+}
+
+/* ------------------------------------------------------------------ */
+/* tanh-GELU: cpu_gelu.c:23-38, cpu_gelu_bf16.c:62-64,                  */
+/* cpu_gelu_f16.c:52-54. Same operation order as the reference:          */
+/* inner = c0 * (x + ((c1*x)*x)*x); out = (0.5*x) * (1 + tanhf(inner)). */
+/* ------------------------------------------------------------------ */
+static inline float gelu_tanh(float x)
+{
+	float cube = 0.044715f * x * x * x;
+	float inner = 0.7978845608f * (x + cube);
+	return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+void oracle_gelu_f32(const float *x, float *out, int n)
+{
+	for (int i = 0; i < n; i++)
+		out[i] = gelu_tanh(x[i]);
+}
+
+void oracle_gelu_bf16(const uint16_t *x, uint16_t *out, int n)
+{
+	for (int i = 0; i < n; i++)
+		out[i] = oracle_f32_to_bf16(gelu_tanh(oracle_bf16_to_f32(x[i])));
+}
+
+void oracle_gelu_f16(const uint16_t *x, uint16_t *out, int n)
+{
+	for (int i = 0; i < n; i++)
+		out[i] = oracle_f32_to_fp16(gelu_tanh(oracle_fp16_to_f32(x[i])));
+}
+
+/* ------------------------------------------------------------------ */
+/* Batched bf16: the reference has no batched matmul (the kernels use  */
+/* only the last two dims, cpu_matmul_bf16.c:213-236), so attention's   */
+/* QK^T / PV are restated as the 2-D kernel per slice, with a per-slice */
+/* transpose for B stored [N,K] (gh_transpose + gh_matmul).             */
+/* ------------------------------------------------------------------ */
+void oracle_matmul_bf16_batched(const uint16_t *a, const uint16_t *b,
+				uint16_t *c, int batch, int M, int K, int N,
+				int b_nt, int n_threads)
+{
+	uint16_t *tmp = NULL;
+
+	if (b_nt) {
+		tmp = malloc((size_t)K * N * sizeof(uint16_t));
+		if (!tmp)
+			return;
+	}
+	for (int s = 0; s < batch; s++) {
+		const uint16_t *as = a + (size_t)s * M * K;
+		const uint16_t *bs = b + (size_t)s * K * N;
+		uint16_t *cs = c + (size_t)s * M * N;
+		if (b_nt) {
+			oracle_transpose_u16(bs, tmp, N, K);
+			bs = tmp;
+		}
+		oracle_matmul_bf16(as, bs, cs, M, K, N, n_threads);
+	}
+	free(tmp);
+}

@@ -1,0 +1,152 @@
+"""Write the golden vectors for the matmul path from the REAL reference.
+
+Run in the build container (where /root/reference exists):
+
+    make -C oracle ref && python tests/golden/make_golden.py
+
+It loads oracle/_ref/libsam3ref.so -- the reference's own CPU sources
+compiled in place by oracle/Makefile -- and drives its kernels the way the
+reference tests do (hand-built sam3_node, cpu_kernel_*(node, pool)). Inputs
+come from sam3_amd.synth (seeded SplitMix64/Box-Muller) or from the
+reference tests' own formulas (tests/test_matmul_q8.c:73-76). Inputs and
+outputs are stored together in matmul_golden.npz, so the GPU box (which has
+no /root/reference) can check the oracle and the HIP path against them.
+"""
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent))
+
+from oracle_bind import Ref  # noqa: E402
+from sam3_amd import abi, synth  # noqa: E402
+
+
+def bf16_bits(ref, x):
+    return ref.cast(np.asarray(x, np.float32), abi.F32, abi.BF16, np.uint16).reshape(np.shape(x))
+
+
+def fp16_bits(ref, x):
+    return ref.cast(np.asarray(x, np.float32), abi.F32, abi.F16, np.uint16).reshape(np.shape(x))
+
+
+def main():
+    R = Ref()
+    g = {}
+
+    # -- Q8 quantize: random, a zero block, a ragged tail and exact .5 ties
+    # (scale 1.0 makes x*inv == x; x86 roundf rounds ties away from zero,
+    # src/core/quant.c:118-124).
+    x = synth.randn(11, 200, 0.02)
+    x[32:64] = 0.0
+    ties = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5] + [0.25] * 24, np.float32)
+    qx = np.concatenate([x, ties, synth.randn(12, 45, 3.0)]).astype(np.float32)
+    g["quant_x"] = qx
+    g["quant_blocks"] = R.q8_quantize(qx)
+    g["quant_deq"] = R.q8_dequantize(g["quant_blocks"], qx.size)
+
+    # -- Q8 matmul, kernel contract B[K,N] with blocks over the flat index.
+    cases_q8 = [
+        ("q8_a", 64, 256, 96, 21),   # N % 32 != 0: blocks straddle k-rows
+        ("q8_b", 5, 33, 7, 22),      # K*N % 32 != 0: zero-padded tail block
+        ("q8_c", 1, 128, 64, 23),    # M == 1 (serial path, cpu_matmul_q8.c:226)
+    ]
+    for name, M, K, N, seed in cases_q8:
+        a = synth.randn(synth.tensor_seed(seed, 0), (M, K))
+        w = synth.randn(synth.tensor_seed(seed, 1), (K, N), 0.02)
+        b = R.q8_quantize(w)
+        g[f"{name}_a"], g[f"{name}_b"] = a, b
+        g[f"{name}_shape"] = np.array([M, K, N])
+        g[f"{name}_c"] = R.matmul_q8(a, b, K, N, threads=4)
+
+    # the reference test's own small case (tests/test_matmul_q8.c:66-116)
+    M, K, N = 4, 64, 4
+    a = (np.sin(np.arange(M * K, dtype=np.float32) * np.float32(0.1)) * np.float32(0.5)).reshape(M, K)
+    w = (np.cos(np.arange(K * N, dtype=np.float32) * np.float32(0.1)) * np.float32(0.5)).reshape(K, N)
+    b = R.q8_quantize(w.astype(np.float32))
+    g["q8_t_a"], g["q8_t_b"], g["q8_t_shape"] = a.astype(np.float32), b, np.array([M, K, N])
+    g["q8_t_c"] = R.matmul_q8(a.astype(np.float32), b, K, N)
+
+    # -- Q8 with W stored [N,K] (blocks along K): column n is the reference
+    # kernel with B = W[n,:] viewed as [K,1].
+    M, K, N = 16, 256, 40
+    a = synth.randn(synth.tensor_seed(31, 0), (M, K))
+    w = synth.randn(synth.tensor_seed(31, 1), (N, K), 0.02)
+    wb = R.q8_quantize(w)
+    row = K // 32 * 36
+    cols = [R.matmul_q8(a, wb[n * row:(n + 1) * row], K, 1) for n in range(N)]
+    g["q8nt_a"], g["q8nt_w"], g["q8nt_shape"] = a, wb, np.array([M, K, N])
+    g["q8nt_c"] = np.concatenate(cols, axis=1)
+
+    # -- bf16 / f16 / f32 dense GEMMs
+    M, K, N = 37, 96, 80
+    a32 = synth.randn(synth.tensor_seed(41, 0), (M, K))
+    b32 = synth.randn(synth.tensor_seed(41, 1), (K, N))
+    ab, bb = bf16_bits(R, a32), bf16_bits(R, b32)
+    g["bf16_a"], g["bf16_b"] = ab, bb
+    g["bf16_c"] = R.matmul_bf16(ab, bb, threads=3)
+    M2, K2, N2 = 19, 70, 23
+    ah = fp16_bits(R, synth.randn(synth.tensor_seed(42, 0), (M2, K2)))
+    bh = fp16_bits(R, synth.randn(synth.tensor_seed(42, 1), (K2, N2)))
+    g["f16_a"], g["f16_b"] = ah, bh
+    g["f16_c"] = R.matmul_f16(ah, bh, threads=3)
+    af = synth.randn(synth.tensor_seed(43, 0), (7, 13))
+    bf = synth.randn(synth.tensor_seed(43, 1), (13, 5))
+    g["f32_a"], g["f32_b"] = af, bf
+    g["f32_c"] = R.matmul_f32(af, bf)
+    af2 = synth.randn(synth.tensor_seed(44, 0), (33, 200))
+    bf2 = synth.randn(synth.tensor_seed(44, 1), (200, 65))
+    g["f32b_a"], g["f32b_b"] = af2, bf2
+    g["f32b_c"] = R.matmul_f32(af2, bf2, threads=4)
+
+    # -- epilogues. The x86 scalar broadcast add only covers the first
+    # `rows` elements (split in rows, loop in elements:
+    # cpu_elementwise.c:70-78 vs :357-371, cpu_add_bf16.c:86-98 vs
+    # :120-135), so the bias is tiled to full shape and the same-shape path
+    # (which applies the identical per-element formula) is recorded.
+    rows, N = 24, 96
+    x = synth.randn(51, (rows, N), 2.0)
+    bias = synth.randn(52, N, 0.5)
+    tiled = np.tile(bias, rows).reshape(rows, N)
+
+    def add_same(xx, bbias, dt, npt, fn):
+        rc, out = R.run(fn, abi.OP_ADD, [(dt, [rows, N], np.ascontiguousarray(xx, npt)),
+                                         (dt, [rows, N], np.ascontiguousarray(bbias, npt))],
+                        dt, (rows, N), npt)
+        assert rc == 0
+        return out
+
+    g["ep_x"], g["ep_bias"] = x, bias
+    g["ep_add_f32"] = add_same(x, tiled, abi.F32, np.float32, "cpu_kernel_add")
+    xb, bb_ = bf16_bits(R, x), bf16_bits(R, bias)
+    g["ep_add_bf16"] = add_same(xb, np.tile(bb_, rows).reshape(rows, N), abi.BF16, np.uint16,
+                                "cpu_kernel_add_bf16")
+    xh, bh_ = fp16_bits(R, x), fp16_bits(R, bias)
+    g["ep_add_f16"] = R.add(xh, bh_, "f16")   # f16 broadcast path is row-wise (correct)
+    gx = np.linspace(-8.0, 8.0, 4097, dtype=np.float32)
+    g["gelu_x"] = gx
+    g["gelu_f32"] = R.gelu(gx, "f32")
+    g["gelu_bf16"] = R.gelu(bf16_bits(R, gx), "bf16")
+    g["gelu_f16"] = R.gelu(fp16_bits(R, gx), "f16")
+
+    # -- conversions: a sample of f32 bit patterns incl. specials
+    rng = np.random.default_rng(61)
+    pats = rng.integers(0, 2 ** 32, 4096, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001,
+                         0x33000000, 0x387FC000, 0x477FE000, 0x477FF000, 0x3F808000,
+                         0x3F818000, 0x00000001, 0x007FFFFF], np.uint32)
+    pats = np.concatenate([specials, pats]).view(np.float32)
+    g["cvt_f32"] = pats
+    g["cvt_bf16"] = R.cast(pats, abi.F32, abi.BF16, np.uint16)
+    g["cvt_fp16"] = R.cast(pats, abi.F32, abi.F16, np.uint16)
+
+    R.close()
+    out = HERE / "matmul_golden.npz"
+    np.savez_compressed(out, **g)
+    print(f"wrote {out} ({out.stat().st_size} bytes, {len(g)} arrays)")
+
+
+if __name__ == "__main__":
+    main()

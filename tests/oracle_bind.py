@@ -1,0 +1,296 @@
+"""ctypes bindings for the CPU checkers (test infrastructure only).
+
+* ``Oracle`` wraps oracle/liboracle.so, the C11 restatement of the
+  reference's CPU matmul path (oracle/sam3_oracle.c).
+* ``Ref`` wraps oracle/_ref/libsam3ref.so, the reference's own CPU sources
+  compiled in place by oracle/Makefile when /root/reference exists. Its
+  kernels are driven exactly the way the reference tests drive them: a
+  hand-built ``sam3_node`` passed to ``cpu_kernel_*(node, pool)``
+  (tests/test_matmul_q8.c:66-116).
+"""
+import ctypes as C
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "sam3.c_amd"))
+
+from sam3_amd import abi  # noqa: E402
+
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libsam3ref.so"
+
+_vp = C.c_void_p
+_i = C.c_int
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_vp)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not Path(path).exists():
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(str(path))
+        for name in ["oracle_matmul_f32", "oracle_matmul_bf16", "oracle_matmul_f16",
+                     "oracle_matmul_f16_acc32", "oracle_matmul_q8", "oracle_matmul_q8_nt"]:
+            getattr(L, name).argtypes = [_vp, _vp, _vp, _i, _i, _i, _i]
+            getattr(L, name).restype = None
+        L.oracle_q8_quantize.argtypes = [_vp, _vp, _i]
+        L.oracle_q8_dequantize.argtypes = [_vp, _vp, _i]
+        L.oracle_q8_block_count.argtypes = [_i]
+        L.oracle_q8_nbytes.argtypes = [_i]
+        L.oracle_q8_nbytes.restype = C.c_size_t
+        L.oracle_f32_to_bf16.argtypes = [C.c_float]
+        L.oracle_f32_to_bf16.restype = C.c_uint16
+        L.oracle_f32_to_fp16.argtypes = [C.c_float]
+        L.oracle_f32_to_fp16.restype = C.c_uint16
+        for name in ["oracle_cast_f32_to_bf16", "oracle_cast_f32_to_fp16",
+                     "oracle_cast_bf16_to_f32", "oracle_cast_fp16_to_f32",
+                     "oracle_gelu_f32", "oracle_gelu_bf16", "oracle_gelu_f16"]:
+            getattr(L, name).argtypes = [_vp, _vp, _i]
+        for name in ["oracle_bias_add_f32", "oracle_bias_add_bf16", "oracle_bias_add_f16"]:
+            getattr(L, name).argtypes = [_vp, _vp, _vp, _i, _i]
+        L.oracle_transpose_u16.argtypes = [_vp, _vp, _i, _i]
+        L.oracle_transpose_f32.argtypes = [_vp, _vp, _i, _i]
+        L.oracle_matmul_bf16_batched.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i]
+
+    # ---- Q8 ----
+    def q8_quantize(self, x):
+        x = _c(x, np.float32).ravel()
+        out = np.zeros(abi.q8_nbytes(x.size), dtype=np.uint8)
+        self.lib.oracle_q8_quantize(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def q8_dequantize(self, blocks, n):
+        blocks = _c(blocks, np.uint8)
+        out = np.empty(n, dtype=np.float32)
+        self.lib.oracle_q8_dequantize(_ptr(blocks), _ptr(out), n)
+        return out
+
+    # ---- conversions ----
+    def _cast(self, name, x, in_t, out_t):
+        x = _c(x, in_t).ravel()
+        out = np.empty(x.size, dtype=out_t)
+        getattr(self.lib, name)(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f32_to_bf16(self, x):
+        return self._cast("oracle_cast_f32_to_bf16", x, np.float32, np.uint16)
+
+    def f32_to_fp16(self, x):
+        return self._cast("oracle_cast_f32_to_fp16", x, np.float32, np.uint16)
+
+    def bf16_to_f32(self, x):
+        return self._cast("oracle_cast_bf16_to_f32", x, np.uint16, np.float32)
+
+    def fp16_to_f32(self, x):
+        return self._cast("oracle_cast_fp16_to_f32", x, np.uint16, np.float32)
+
+    # ---- GEMMs ----
+    def _mm(self, name, a, b, M, K, N, out_t, in_a, in_b, threads):
+        a = _c(a, in_a)
+        b = _c(b, in_b)
+        c = np.empty((M, N), dtype=out_t)
+        getattr(self.lib, name)(_ptr(a), _ptr(b), _ptr(c), M, K, N, threads)
+        return c
+
+    def matmul_f32(self, a, b, threads=1):
+        (M, K), N = a.shape, b.shape[1]
+        return self._mm("oracle_matmul_f32", a, b, M, K, N, np.float32, np.float32, np.float32, threads)
+
+    def matmul_bf16(self, a, b, threads=1):
+        (M, K), N = a.shape, b.shape[1]
+        return self._mm("oracle_matmul_bf16", a, b, M, K, N, np.uint16, np.uint16, np.uint16, threads)
+
+    def matmul_f16(self, a, b, threads=1):
+        (M, K), N = a.shape, b.shape[1]
+        return self._mm("oracle_matmul_f16", a, b, M, K, N, np.uint16, np.uint16, np.uint16, threads)
+
+    def matmul_f16_acc32(self, a, b, threads=1):
+        (M, K), N = a.shape, b.shape[1]
+        return self._mm("oracle_matmul_f16_acc32", a, b, M, K, N, np.uint16, np.uint16, np.uint16, threads)
+
+    def matmul_q8(self, a, b_blocks, K, N, threads=1):
+        M = a.shape[0]
+        return self._mm("oracle_matmul_q8", a, b_blocks, M, K, N, np.float32, np.float32, np.uint8, threads)
+
+    def matmul_q8_nt(self, a, w_blocks, K, N, threads=1):
+        M = a.shape[0]
+        return self._mm("oracle_matmul_q8_nt", a, w_blocks, M, K, N, np.float32, np.float32, np.uint8, threads)
+
+    def matmul_bf16_batched(self, a, b, b_nt=False, threads=1):
+        batch, M, K = a.shape
+        N = b.shape[1] if b_nt else b.shape[2]
+        a = _c(a, np.uint16)
+        b = _c(b, np.uint16)
+        c = np.empty((batch, M, N), dtype=np.uint16)
+        self.lib.oracle_matmul_bf16_batched(_ptr(a), _ptr(b), _ptr(c), batch, M, K, N,
+                                            int(b_nt), threads)
+        return c
+
+    def transpose_u16(self, x):
+        R, Cc = x.shape
+        x = _c(x, np.uint16)
+        out = np.empty((Cc, R), dtype=np.uint16)
+        self.lib.oracle_transpose_u16(_ptr(x), _ptr(out), R, Cc)
+        return out
+
+    # ---- epilogues ----
+    def bias_add(self, x, bias, kind):
+        x = np.ascontiguousarray(x)
+        rows, N = x.shape
+        t = np.float32 if kind == "f32" else np.uint16
+        x = _c(x, t)
+        bias = _c(bias, t)
+        out = np.empty_like(x)
+        getattr(self.lib, f"oracle_bias_add_{kind}")(_ptr(x), _ptr(bias), _ptr(out), rows, N)
+        return out
+
+    def gelu(self, x, kind):
+        t = np.float32 if kind == "f32" else np.uint16
+        x = _c(x, t)
+        out = np.empty_like(x)
+        getattr(self.lib, f"oracle_gelu_{kind}")(_ptr(x), _ptr(out), x.size)
+        return out
+
+
+class Ref:
+    """The reference's own kernels, called through hand-built nodes."""
+
+    def __init__(self, path=REF_SO):
+        if not Path(path).exists():
+            raise FileNotFoundError(str(path))
+        L = self.lib = C.CDLL(str(path))
+        for name in ["cpu_kernel_matmul", "cpu_kernel_matmul_bf16", "cpu_kernel_matmul_f16",
+                     "cpu_kernel_matmul_q8", "cpu_kernel_add", "cpu_kernel_add_bf16",
+                     "cpu_kernel_add_f16", "cpu_kernel_gelu", "cpu_kernel_gelu_bf16",
+                     "cpu_kernel_gelu_f16", "cpu_kernel_cast", "cpu_kernel_transpose"]:
+            getattr(L, name).argtypes = [_vp, _vp]
+            getattr(L, name).restype = C.c_int
+        L.cpu_dispatch_node.argtypes = [_vp, _vp, _vp]
+        L.cpu_dispatch_node.restype = C.c_int
+        L.sam3_q8_quantize.argtypes = [_vp, _vp, _i]
+        L.sam3_q8_dequantize.argtypes = [_vp, _vp, _i]
+        L.sam3_q8_block_count.argtypes = [_i]
+        L.sam3_q8_nbytes.argtypes = [_i]
+        L.sam3_q8_nbytes.restype = C.c_size_t
+        L.sam3_threadpool_create.argtypes = [_i]
+        L.sam3_threadpool_create.restype = _vp
+        L.sam3_threadpool_free.argtypes = [_vp]
+        self._pools = {}
+
+    def pool(self, n):
+        """None -> serial (pool NULL), 0 -> all online CPUs, n -> n threads."""
+        if n is None:
+            return None
+        if n not in self._pools:
+            self._pools[n] = self.lib.sam3_threadpool_create(n)
+        return self._pools[n]
+
+    def close(self):
+        for p in self._pools.values():
+            self.lib.sam3_threadpool_free(p)
+        self._pools.clear()
+
+    def q8_quantize(self, x):
+        x = _c(x, np.float32).ravel()
+        out = np.zeros(abi.q8_nbytes(x.size), dtype=np.uint8)
+        self.lib.sam3_q8_quantize(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def q8_dequantize(self, blocks, n):
+        blocks = _c(blocks, np.uint8)
+        out = np.empty(n, dtype=np.float32)
+        self.lib.sam3_q8_dequantize(_ptr(blocks), _ptr(out), n)
+        return out
+
+    def run(self, fn, op, ins, out_dtype, out_dims, out_np_dtype, threads=None, params=(0, 0, 0, 0)):
+        """ins: list of (sam3 dtype, dims, numpy array)."""
+        keep = []
+        tens = []
+        for dt, dims, arr in ins:
+            arr = np.ascontiguousarray(arr)
+            keep.append(arr)
+            tens.append(abi.make_tensor(dt, dims, arr.ctypes.data, arr.nbytes))
+        out = np.zeros(out_dims, dtype=out_np_dtype)
+        tout = abi.make_tensor(out_dtype, list(out_dims), out.ctypes.data, out.nbytes)
+        node = abi.make_node(op, tens, tout, params)
+        if fn == "dispatch":
+            scratch = (C.c_char * 64)()
+            rc = self.lib.cpu_dispatch_node(C.byref(node), C.byref(scratch), self.pool(threads))
+        else:
+            rc = getattr(self.lib, fn)(C.byref(node), self.pool(threads))
+        return rc, out
+
+    def matmul_f32(self, a, b, threads=None):
+        (M, K), N = a.shape, b.shape[1]
+        rc, c = self.run("cpu_kernel_matmul", abi.OP_MATMUL,
+                         [(abi.F32, [M, K], _c(a, np.float32)), (abi.F32, [K, N], _c(b, np.float32))],
+                         abi.F32, (M, N), np.float32, threads)
+        assert rc == 0
+        return c
+
+    def matmul_bf16(self, a, b, threads=None):
+        (M, K), N = a.shape, b.shape[1]
+        rc, c = self.run("cpu_kernel_matmul_bf16", abi.OP_MATMUL,
+                         [(abi.BF16, [M, K], _c(a, np.uint16)), (abi.BF16, [K, N], _c(b, np.uint16))],
+                         abi.BF16, (M, N), np.uint16, threads)
+        assert rc == 0
+        return c
+
+    def matmul_f16(self, a, b, threads=None):
+        (M, K), N = a.shape, b.shape[1]
+        rc, c = self.run("cpu_kernel_matmul_f16", abi.OP_MATMUL,
+                         [(abi.F16, [M, K], _c(a, np.uint16)), (abi.F16, [K, N], _c(b, np.uint16))],
+                         abi.F16, (M, N), np.uint16, threads)
+        assert rc == 0
+        return c
+
+    def matmul_q8(self, a, b_blocks, K, N, threads=None):
+        M = a.shape[0]
+        rc, c = self.run("cpu_kernel_matmul_q8", abi.OP_MATMUL,
+                         [(abi.F32, [M, K], _c(a, np.float32)),
+                          (abi.Q8_0, [K, N], _c(b_blocks, np.uint8))],
+                         abi.F32, (M, N), np.float32, threads)
+        assert rc == 0
+        return c
+
+    def cast(self, x, in_dtype, out_dtype, out_np):
+        x = np.ascontiguousarray(x).ravel()
+        # params[0] names the target dtype (cpu_cast.c:170-180)
+        rc, out = self.run("cpu_kernel_cast", abi.OP_CAST, [(in_dtype, [x.size], x)],
+                           out_dtype, (x.size,), out_np, params=(out_dtype, 0, 0, 0))
+        assert rc == 0
+        return out
+
+    def add(self, x, bias, kind):
+        rows, N = x.shape
+        dt = {"f32": abi.F32, "bf16": abi.BF16, "f16": abi.F16}[kind]
+        npt = np.float32 if kind == "f32" else np.uint16
+        fn = {"f32": "cpu_kernel_add", "bf16": "cpu_kernel_add_bf16", "f16": "cpu_kernel_add_f16"}[kind]
+        rc, out = self.run(fn, abi.OP_ADD, [(dt, [rows, N], _c(x, npt)), (dt, [N], _c(bias, npt))],
+                           dt, (rows, N), npt)
+        assert rc == 0
+        return out
+
+    def gelu(self, x, kind):
+        dt = {"f32": abi.F32, "bf16": abi.BF16, "f16": abi.F16}[kind]
+        npt = np.float32 if kind == "f32" else np.uint16
+        fn = {"f32": "cpu_kernel_gelu", "bf16": "cpu_kernel_gelu_bf16", "f16": "cpu_kernel_gelu_f16"}[kind]
+        x = _c(x, npt).ravel()
+        rc, out = self.run(fn, abi.OP_GELU, [(dt, [x.size], x)], dt, (x.size,), npt)
+        assert rc == 0
+        return out
+
+
+def have_ref():
+    return REF_SO.exists()

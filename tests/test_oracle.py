@@ -1,0 +1,252 @@
+"""Pins the CPU oracle (oracle/sam3_oracle.c) before it is trusted.
+
+Three kinds of evidence, so that a dropped term, a wrong sign/index or a
+transposed operand fails at least one:
+  1. golden vectors written by the real reference (tests/golden/), bit-exact;
+  2. direct bit-exact comparison with oracle/_ref/libsam3ref.so (the
+     reference's sources compiled in place) on fresh seeded inputs, when
+     that library is built (skipped on the GPU box, which has no sources);
+  3. closed forms: the reference tests' known answers, identity and
+     one-hot products, exhaustive conversion sweeps, float64 brute force.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_bind import Oracle, Ref, have_ref
+from sam3_amd import abi, synth
+
+GOLD = np.load(Path(__file__).parent / "golden" / "matmul_golden.npz")
+
+
+@pytest.fixture(scope="module")
+def O():
+    return Oracle()
+
+
+@pytest.fixture(scope="module")
+def R():
+    if not have_ref():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    r = Ref()
+    yield r
+    r.close()
+
+
+def bits32(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- golden
+def test_golden_q8_quantize(O):
+    qx = GOLD["quant_x"]
+    assert np.array_equal(O.q8_quantize(qx), GOLD["quant_blocks"])
+    assert np.array_equal(bits32(O.q8_dequantize(GOLD["quant_blocks"], qx.size)),
+                          bits32(GOLD["quant_deq"]))
+
+
+@pytest.mark.parametrize("name", ["q8_a", "q8_b", "q8_c", "q8_t"])
+def test_golden_q8_matmul(O, name):
+    M, K, N = GOLD[f"{name}_shape"]
+    for threads in (1, 3):
+        c = O.matmul_q8(GOLD[f"{name}_a"], GOLD[f"{name}_b"], int(K), int(N), threads)
+        assert np.array_equal(bits32(c), bits32(GOLD[f"{name}_c"]))
+
+
+def test_golden_q8_nt(O):
+    M, K, N = (int(v) for v in GOLD["q8nt_shape"])
+    c = O.matmul_q8_nt(GOLD["q8nt_a"], GOLD["q8nt_w"], K, N, threads=2)
+    assert np.array_equal(bits32(c), bits32(GOLD["q8nt_c"]))
+
+
+def test_golden_dense(O):
+    assert np.array_equal(O.matmul_bf16(GOLD["bf16_a"], GOLD["bf16_b"], 2), GOLD["bf16_c"])
+    assert np.array_equal(O.matmul_f16(GOLD["f16_a"], GOLD["f16_b"], 2), GOLD["f16_c"])
+    assert np.array_equal(bits32(O.matmul_f32(GOLD["f32_a"], GOLD["f32_b"])), bits32(GOLD["f32_c"]))
+    assert np.array_equal(bits32(O.matmul_f32(GOLD["f32b_a"], GOLD["f32b_b"], 4)),
+                          bits32(GOLD["f32b_c"]))
+
+
+def test_golden_epilogues(O):
+    x, bias = GOLD["ep_x"], GOLD["ep_bias"]
+    assert np.array_equal(bits32(O.bias_add(x, bias, "f32")), bits32(GOLD["ep_add_f32"]))
+    xb, bb = O.f32_to_bf16(x).reshape(x.shape), O.f32_to_bf16(bias)
+    assert np.array_equal(O.bias_add(xb, bb, "bf16"), GOLD["ep_add_bf16"])
+    xh, bh = O.f32_to_fp16(x).reshape(x.shape), O.f32_to_fp16(bias)
+    assert np.array_equal(O.bias_add(xh, bh, "f16"), GOLD["ep_add_f16"])
+    gx = GOLD["gelu_x"]
+    assert np.array_equal(bits32(O.gelu(gx, "f32")), bits32(GOLD["gelu_f32"]))
+    assert np.array_equal(O.gelu(O.f32_to_bf16(gx), "bf16"), GOLD["gelu_bf16"])
+    assert np.array_equal(O.gelu(O.f32_to_fp16(gx), "f16"), GOLD["gelu_f16"])
+
+
+def test_golden_conversions(O):
+    p = GOLD["cvt_f32"]
+    assert np.array_equal(O.f32_to_bf16(p), GOLD["cvt_bf16"])
+    assert np.array_equal(O.f32_to_fp16(p), GOLD["cvt_fp16"])
+
+
+# ------------------------------------------------------ reference (_ref)
+def test_ref_conversions_exhaustive(O, R):
+    allp = np.arange(65536, dtype=np.uint16)
+    assert np.array_equal(bits32(O.bf16_to_f32(allp)),
+                          bits32(R.cast(allp, abi.BF16, abi.F32, np.float32)))
+    assert np.array_equal(bits32(O.fp16_to_f32(allp)),
+                          bits32(R.cast(allp, abi.F16, abi.F32, np.float32)))
+    rng = np.random.default_rng(5)
+    pats = rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    assert np.array_equal(O.f32_to_bf16(pats), R.cast(pats, abi.F32, abi.BF16, np.uint16))
+    assert np.array_equal(O.f32_to_fp16(pats), R.cast(pats, abi.F32, abi.F16, np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", [(33, 160, 64), (8, 64, 33), (1, 1024, 96), (70, 96, 1)])
+def test_ref_q8(O, R, M, K, N):
+    a = synth.randn(100 + M, (M, K))
+    w = synth.randn(200 + N, (K, N), 0.02)
+    b = R.q8_quantize(w)
+    assert np.array_equal(O.q8_quantize(w), b)
+    assert np.array_equal(bits32(O.matmul_q8(a, b, K, N, 4)), bits32(R.matmul_q8(a, b, K, N, 4)))
+
+
+def test_ref_q8_nt_columns(O, R):
+    M, K, N = 9, 192, 17
+    a = synth.randn(300, (M, K))
+    w = synth.randn(301, (N, K), 0.05)
+    wb = O.q8_quantize(w)
+    c = O.matmul_q8_nt(a, wb, K, N)
+    row = K // 32 * 36
+    for n in range(N):
+        assert np.array_equal(bits32(c[:, n:n + 1]), bits32(R.matmul_q8(a, wb[n * row:(n + 1) * row], K, 1)))
+
+
+@pytest.mark.parametrize("M,K,N", [(17, 130, 9), (64, 64, 64)])
+def test_ref_dense(O, R, M, K, N):
+    a32 = synth.randn(400 + K, (M, K))
+    b32 = synth.randn(500 + N, (K, N))
+    ab, bb = O.f32_to_bf16(a32).reshape(M, K), O.f32_to_bf16(b32).reshape(K, N)
+    assert np.array_equal(O.matmul_bf16(ab, bb, 3), R.matmul_bf16(ab, bb, 3))
+    ah, bh = O.f32_to_fp16(a32).reshape(M, K), O.f32_to_fp16(b32).reshape(K, N)
+    assert np.array_equal(O.matmul_f16(ah, bh, 3), R.matmul_f16(ah, bh, 3))
+    assert np.array_equal(bits32(O.matmul_f32(a32, b32, 3)), bits32(R.matmul_f32(a32, b32, 3)))
+
+
+def test_ref_dispatch_q8_routing(R):
+    """tests/test_dispatch_q8.c:28-81: F32 x Q8_0 routes to the Q8 kernel;
+    a BF16 x Q8_0 node is refused with SAM3_EDTYPE (cpu_dispatch.c:643-655)."""
+    M, K, N = 4, 32, 4
+    a = (np.arange(M * K, dtype=np.float32) * np.float32(0.01)).reshape(M, K)
+    w = (np.arange(K * N, dtype=np.float32) * np.float32(0.01)).reshape(K, N)
+    b = R.q8_quantize(w)
+    rc, c = R.run("dispatch", abi.OP_MATMUL, [(abi.F32, [M, K], a), (abi.Q8_0, [K, N], b)],
+                  abi.F32, (M, N), np.float32)
+    assert rc == abi.OK and np.count_nonzero(c) > 0
+    ab = np.zeros((M, K), np.uint16)
+    rc, _ = R.run("dispatch", abi.OP_MATMUL, [(abi.BF16, [M, K], ab), (abi.Q8_0, [K, N], b)],
+                  abi.BF16, (M, N), np.uint16)
+    assert rc == abi.EDTYPE
+
+
+# ------------------------------------------------------------ closed forms
+def test_known_answer_f32(O):
+    """tests/test_cpu_kernels.c:474-500: [1,2,3;4,5,6]@[7,8;9,10;11,12]."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    assert O.matmul_f32(a, b).tolist() == [[58, 64], [139, 154]]
+
+
+def test_identity_all_dtypes(O):
+    a = synth.randn(7, (12, 12))
+    eye = np.eye(12, dtype=np.float32)
+    assert np.array_equal(O.matmul_f32(a, eye), a)
+    ab = O.f32_to_bf16(a).reshape(12, 12)
+    assert np.array_equal(O.matmul_bf16(ab, O.f32_to_bf16(eye).reshape(12, 12)), ab)
+    ah = O.f32_to_fp16(a).reshape(12, 12)
+    assert np.array_equal(O.matmul_f16_acc32(ah, O.f32_to_fp16(eye).reshape(12, 12)), ah)
+
+
+def test_q8_invariants(O):
+    x = synth.randn(8, 32 * 40, 0.3)
+    blk = O.q8_quantize(x).reshape(-1, 36)
+    scale = blk[:, :4].copy().view(np.float32).ravel()
+    q = blk[:, 4:].view(np.int8).astype(np.int32)
+    amax = np.abs(x.reshape(-1, 32)).max(1)
+    assert np.array_equal(scale, (amax / np.float32(127.0)).astype(np.float32))
+    assert np.abs(q).max() <= 127
+    # the element reaching amax quantizes to +-127
+    idx = np.abs(x.reshape(-1, 32)).argmax(1)
+    assert np.all(np.abs(q[np.arange(len(idx)), idx]) == 127)
+    # tests/test_quant.c:36-59 block counts / sizes
+    assert [O.lib.oracle_q8_block_count(n) for n in (32, 64, 1024, 1, 33, 63)] == [1, 2, 32, 1, 2, 2]
+    assert [O.lib.oracle_q8_nbytes(n) for n in (32, 64, 33)] == [36, 72, 72]
+    # zero block -> scale 0 and zero data (tests/test_quant.c:80-94)
+    z = O.q8_quantize(np.zeros(32, np.float32))
+    assert np.all(z == 0)
+    # hand-built blocks dequantize exactly (tests/test_metal.c:950-1011)
+    hb = np.zeros((2, 36), np.uint8)
+    hb[0, :4] = np.frombuffer(np.float32(0.5).tobytes(), np.uint8)
+    hb[0, 4:] = np.arange(32, dtype=np.int8).view(np.uint8)
+    hb[1, :4] = np.frombuffer(np.float32(0.25).tobytes(), np.uint8)
+    hb[1, 4:] = (-(np.arange(32) + 1)).astype(np.int8).view(np.uint8)
+    exp = np.concatenate([np.arange(32) * 0.5, -(np.arange(32) + 1) * 0.25]).astype(np.float32)
+    assert np.array_equal(O.q8_dequantize(hb.ravel(), 64), exp)
+
+
+def test_q8_one_hot_rows_pick_dequantized_weights(O):
+    """A = e_k picks row k of deq(B) exactly: 1*q*s == q*s in f32."""
+    K, N = 96, 70
+    w = synth.randn(9, (K, N), 0.02)
+    b = O.q8_quantize(w)
+    deq = O.q8_dequantize(b, K * N).reshape(K, N)
+    a = np.eye(K, dtype=np.float32)[[0, 5, 31, 32, 95]]
+    assert np.array_equal(O.matmul_q8(a, b, K, N), deq[[0, 5, 31, 32, 95]])
+    wn = synth.randn(10, (N, K), 0.02)
+    bn = O.q8_quantize(wn)
+    deqn = O.q8_dequantize(bn, K * N).reshape(N, K)
+    assert np.array_equal(O.matmul_q8_nt(a, bn, K, N), deqn[:, [0, 5, 31, 32, 95]].T)
+
+
+def test_q8_brute_force_float64(O):
+    M, K, N = 6, 128, 24
+    a = synth.randn(11, (M, K))
+    w = synth.randn(12, (N, K), 0.02)
+    bn = O.q8_quantize(w)
+    deq = O.q8_dequantize(bn, N * K).reshape(N, K).astype(np.float64)
+    exact = a.astype(np.float64) @ deq.T
+    got = O.matmul_q8_nt(a, bn, K, N)
+    assert np.max(np.abs(got - exact)) <= 1e-5 * np.max(np.abs(exact))
+
+
+def test_f16_acc32_pins(O):
+    """No reference kernel accumulates fp16 in f32, so: (1) small-integer
+    operands make every product and partial sum exact, giving an integer
+    closed form that fails on any index/transposition slip; (2) float64
+    brute force at K=4096 with a bound an fp16 accumulator cannot meet."""
+    rng = np.random.default_rng(3)
+    M, K, N = 9, 64, 11
+    ai = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    bi = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    got = O.fp16_to_f32(O.matmul_f16_acc32(O.f32_to_fp16(ai).reshape(M, K),
+                                           O.f32_to_fp16(bi).reshape(K, N))).reshape(M, N)
+    assert np.array_equal(got, ai @ bi)
+    M, K, N = 4, 4096, 6
+    a = O.f32_to_fp16(synth.randn(13, (M, K))).reshape(M, K)
+    b = O.f32_to_fp16(synth.randn(14, (K, N), 0.02)).reshape(K, N)
+    exact = (O.fp16_to_f32(a).reshape(M, K).astype(np.float64) @
+             O.fp16_to_f32(b).reshape(K, N).astype(np.float64))
+    got = O.fp16_to_f32(O.matmul_f16_acc32(a, b)).reshape(M, N)
+    ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 0.5 * ulp + 1e-6 * np.abs(exact).max())
+    ref16 = O.fp16_to_f32(O.matmul_f16(a, b)).reshape(M, N)
+    assert np.max(np.abs(ref16 - exact)) > np.max(np.abs(got - exact))
+
+
+def test_batched_equals_slices(O):
+    B, M, K, N = 3, 20, 16, 24
+    a = O.f32_to_bf16(synth.randn(15, (B, M, K))).reshape(B, M, K)
+    b_kn = O.f32_to_bf16(synth.randn(16, (B, K, N))).reshape(B, K, N)
+    c = O.matmul_bf16_batched(a, b_kn, b_nt=False)
+    for s in range(B):
+        assert np.array_equal(c[s], O.matmul_bf16(a[s], b_kn[s]))
+    b_nk = np.ascontiguousarray(np.transpose(b_kn, (0, 2, 1)))
+    assert np.array_equal(O.matmul_bf16_batched(a, b_nk, b_nt=True), c)
