@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X matmul backend for sam3.c (one GPU).
+
+Headline (the JSON line's `value`): BASELINE.json configs[1], the bf16
+ViT-L MLP fc1 GEMM C[5184,4096] = A[5184,1024] * W[4096,1024]^T with f32
+accumulation, in TFLOP/s (2*M*N*K per step), inputs resident in HBM. One
+step = one GEMM launch. The other BASELINE configs are measured too and
+reported under "extra":
+  config 1  Q8 matmul, f32 activations, 5184x1024x1024
+  config 2  bf16/f16 fc1 and fc2, plain and with fused bias+GELU
+  config 3  32 ViT-L layers x {qkv, proj, fc1, fc2}, Q8 weights (distinct
+            per layer, 453 MB streamed from HBM), bf16 activations
+  config 4  skinny Q8 GEMVs (M in {1,8,32,77}) over a rotating pool of
+            >256 MB of weight copies, reported in HBM GB/s
+  config 5  batched attention QK^T / PV, windowed (1296 x 576 x 64)
+`roofline` is for the headline kernel; `cpu_baseline` times the reference
+CPU bf16 kernel (oracle/_ref, compiled from the reference's own sources)
+on the GPU box's host cores over a bounded row sample of the same GEMM.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "sam3.c_amd"))
+sys.path.insert(0, str(ROOT / "tests"))
+
+from sam3_amd import abi, hip, synth  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def bf16_bits(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def f16_bits(x):
+    return np.ascontiguousarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.e0, self.e1 = hip.Event(), hip.Event()
+
+    def run(self, fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        hip.check(hip.load().sam3_hip_stream_synchronize(self.stream), "sync")
+        self.e0.record(self.stream)
+        for _ in range(steps):
+            fn()
+        self.e1.record(self.stream)
+        hip.check(hip.load().sam3_hip_stream_synchronize(self.stream), "sync")
+        return self.e0.elapsed_ms(self.e1) / steps
+
+
+def gemm_case(stream, timer, a_dt, a, b_dt, b, c_dt, M, N, K, flags, steps, warmup, bias=None):
+    da, db = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(b)
+    dc = hip.DeviceBuffer(M * N * (4 if c_dt == abi.F32 else 2))
+    dbias = hip.DeviceBuffer.of(bias) if bias is not None else None
+    bp = dbias.ptr if dbias else None
+
+    def step():
+        hip.matmul_dev(a_dt, da.ptr, b_dt, db.ptr, c_dt, dc.ptr, M, N, K, bp, flags, stream)
+
+    ms = timer.run(step, steps, warmup)
+    for buf in (da, db, dc, dbias):
+        if buf:
+            buf.free()
+    return ms
+
+
+def tflops(M, N, K, ms):
+    return 2.0 * M * N * K / (ms * 1e-3) / 1e12
+
+
+def cpu_baseline(a_bits, w_bits, M, N, K, target_s=10.0):
+    """Reference CPU bf16 kernel (cpu_kernel_matmul_bf16 via oracle/_ref, B
+    as [K,N] per its contract) on all allowed host cores, on a row sample
+    of the headline GEMM sized to ~target_s seconds."""
+    from oracle_bind import Oracle, Ref, have_ref
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    b_kn = np.ascontiguousarray(w_bits.T)
+    if have_ref():
+        R, kind = Ref(), "reference"
+        fn = lambda a: R.matmul_bf16(a, b_kn, threads)  # noqa: E731
+    else:
+        R, kind = Oracle(), "port"
+        fn = lambda a: R.matmul_bf16(a, b_kn, threads)  # noqa: E731
+    probe = max(threads, 32)
+    t0 = time.perf_counter()
+    fn(a_bits[:probe])
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(min(M, max(probe, target_s / max(per_row, 1e-9))))
+    rows -= rows % threads if rows > threads else 0
+    t0 = time.perf_counter()
+    fn(a_bits[:rows])
+    dt = time.perf_counter() - t0
+    if kind == "reference":
+        R.close()
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tflops(rows, N, K, dt * 1e3), 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": kind,
+            "sample": f"bf16 GEMM rows 0..{rows - 1} of {M} (x {N}x{K}), one call, "
+                      f"{dt:.2f} s, cpu_kernel_matmul_bf16 with a {threads}-thread pool"
+                      + (f", {model}" if model else "")}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline only, no extra configs")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this backend is measured on one GPU only; multi-GPU sharding is a "
+              "design note (row/column/split-K split, see the design document), not a run.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    lib = hip.load()
+    if lib.sam3_hip_device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    arch = lib.sam3_hip_device_arch(0).decode()
+    log("device", arch)
+    sp = hip.C.c_void_p()
+    hip.check(lib.sam3_hip_stream_create(hip.C.byref(sp)), "stream_create")
+    stream = sp.value
+    timer = Timer(stream)
+    K_, W_ = args.steps, args.warmup
+
+    # ---------------- headline: config 2 fc1, bf16, C = A W^T
+    M, N, K = 5184, 4096, 1024
+    a32 = synth.randn(synth.tensor_seed(2, 0), (M, K))
+    w32 = synth.randn(synth.tensor_seed(2, 1), (N, K), 0.02)
+    a_bf, w_bf = bf16_bits(a32), bf16_bits(w32)
+    log("headline bf16 fc1", M, N, K)
+    ms = gemm_case(stream, timer, abi.BF16, a_bf, abi.BF16, w_bf, abi.BF16, M, N, K, hip.B_NT, K_, W_)
+    value = tflops(M, N, K, ms)
+    log(f"  {ms * 1e3:.1f} us/step  {value:.1f} TFLOP/s")
+
+    extra = {}
+    if not args.quick:
+        steps2, warm2 = max(10, K_ // 4), max(3, W_ // 2)
+        bias = bf16_bits(synth.randn(synth.tensor_seed(2, 2), N, 0.01))
+        log("config 2 variants")
+        ms_e = gemm_case(stream, timer, abi.BF16, a_bf, abi.BF16, w_bf, abi.BF16, M, N, K,
+                         hip.B_NT | hip.BIAS | hip.GELU, steps2, warm2, bias=bias)
+        extra["cfg2_bf16_fc1_bias_gelu_tflops"] = round(tflops(M, N, K, ms_e), 2)
+        ms_nn = gemm_case(stream, timer, abi.BF16, a_bf, abi.BF16, np.ascontiguousarray(w_bf.T),
+                          abi.BF16, M, N, K, 0, steps2, warm2)
+        extra["cfg2_bf16_fc1_kn_layout_tflops"] = round(tflops(M, N, K, ms_nn), 2)
+        a2 = bf16_bits(synth.randn(synth.tensor_seed(2, 3), (M, 4096)))
+        w2 = bf16_bits(synth.randn(synth.tensor_seed(2, 4), (1024, 4096), 0.02))
+        ms2 = gemm_case(stream, timer, abi.BF16, a2, abi.BF16, w2, abi.BF16, M, 1024, 4096,
+                        hip.B_NT, steps2, warm2)
+        extra["cfg2_bf16_fc2_tflops"] = round(tflops(M, 1024, 4096, ms2), 2)
+        ms_h = gemm_case(stream, timer, abi.F16, f16_bits(a32), abi.F16, f16_bits(w32), abi.F16,
+                         M, N, K, hip.B_NT, steps2, warm2)
+        extra["cfg2_f16_fc1_tflops"] = round(tflops(M, N, K, ms_h), 2)
+        del a2, w2
+
+        log("config 1 / Q8")
+        from oracle_bind import Oracle  # the quantizer only prepares inputs
+        O = Oracle()
+        a1 = synth.randn(0, (5184, 1024))
+        wq1 = O.q8_quantize(synth.randn(1, (1024, 1024), 0.02))
+        ms1 = gemm_case(stream, timer, abi.F32, a1, abi.Q8_0, wq1, abi.F32, 5184, 1024, 1024,
+                        hip.B_NT, steps2, warm2)
+        bytes1 = 5184 * 1024 * 4 * 2 + wq1.nbytes
+        extra["cfg1_q8_f32act_5184x1024x1024"] = {
+            "us": round(ms1 * 1e3, 2), "tflops": round(tflops(5184, 1024, 1024, ms1), 2),
+            "gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)}
+        wq_fc1 = O.q8_quantize(w32)
+        msq = gemm_case(stream, timer, abi.BF16, a_bf, abi.Q8_0, wq_fc1, abi.F32, M, N, K,
+                        hip.B_NT, steps2, warm2)
+        extra["q8_bf16act_fc1_5184x1024x4096_tflops"] = round(tflops(M, N, K, msq), 2)
+
+        log("config 3: 32 layers, distinct Q8 weights")
+        shapes = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
+        wbase = {s: O.q8_quantize(synth.randn(synth.tensor_seed(3, i), s, 0.02))
+                 for i, s in enumerate(shapes)}
+        layers = [[hip.DeviceBuffer.of(wbase[s]) for s in shapes] for _ in range(32)]
+        act1 = hip.DeviceBuffer.of(bf16_bits(synth.randn(synth.tensor_seed(3, 9), (M, 1024))))
+        act4 = hip.DeviceBuffer.of(bf16_bits(synth.randn(synth.tensor_seed(3, 10), (M, 4096))))
+        out = hip.DeviceBuffer(M * 4096 * 4)
+
+        def encoder():
+            for L in layers:
+                for (n_, k_), wb in zip(shapes, L):
+                    hip.matmul_dev(abi.BF16, (act4 if k_ == 4096 else act1).ptr, abi.Q8_0, wb.ptr,
+                                   abi.F32, out.ptr, M, n_, k_, None, hip.B_NT, stream)
+
+        ms3 = timer.run(encoder, 3, 1)
+        flops3 = 32 * sum(2.0 * M * n_ * k_ for n_, k_ in shapes)
+        extra["cfg3_q8_32layers"] = {"ms": round(ms3, 3),
+                                     "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
+                                     "weights_mb": round(32 * sum(w.nbytes for w in wbase.values()) / 1e6, 1)}
+        for L in layers:
+            for b in L:
+                b.free()
+        act1.free(); act4.free(); out.free()  # noqa: E702
+
+        log("config 4: skinny Q8 stream")
+        sk = {}
+        for (kk, nn) in [(4096, 1024), (1024, 4096), (1024, 1024), (256, 2048), (256, 256)]:
+            wq = O.q8_quantize(synth.randn(synth.tensor_seed(4, kk + nn), (nn, kk), 0.02))
+            copies = max(8, int(300e6 // wq.nbytes) + 1)
+            copies = min(copies, 4096)
+            pool = hip.DeviceBuffer(wq.nbytes * copies)
+            for i in range(copies):
+                hip.check(lib.sam3_hip_memcpy_h2d(pool.ptr + i * wq.nbytes, wq.ctypes.data,
+                                                  wq.nbytes), "h2d")
+            for m in (1, 8, 32, 77):
+                xa = hip.DeviceBuffer.of(synth.randn(synth.tensor_seed(4, m), (m, kk)))
+                yc = hip.DeviceBuffer(m * nn * 4)
+
+                def stream_calls():
+                    for i in range(copies):
+                        hip.matmul_dev(abi.F32, xa.ptr, abi.Q8_0, pool.ptr + i * wq.nbytes,
+                                       abi.F32, yc.ptr, m, nn, kk, None, hip.B_NT, stream)
+
+                msk = timer.run(stream_calls, 2, 1) / copies
+                byts = wq.nbytes + 4 * m * kk + 4 * m * nn
+                sk[f"M{m}_K{kk}_N{nn}"] = {"us_per_call": round(msk * 1e3, 3),
+                                           "gbs": round(byts / (msk * 1e-3) / 1e9, 1)}
+                xa.free(); yc.free()  # noqa: E702
+            pool.free()
+        extra["cfg4_skinny_q8_stream"] = sk
+
+        log("config 5: attention matmuls (windowed)")
+        BH, S, D = 1296, 576, 64
+        qk = bf16_bits(synth.randn(synth.tensor_seed(5, 0), (BH, S, D)) / 8)
+        dq, dk = hip.DeviceBuffer.of(qk), hip.DeviceBuffer.of(qk)
+        ds = hip.DeviceBuffer(BH * S * S * 2)
+        do = hip.DeviceBuffer(BH * S * D * 2)
+
+        def qkt():
+            hip.check(lib.sam3_hip_matmul_batched(abi.BF16, dq.ptr, dk.ptr, ds.ptr, BH, S, S, D,
+                                                  S * D, S * D, S * S, hip.B_NT, stream), "qkt")
+
+        def pv():
+            hip.check(lib.sam3_hip_matmul_batched(abi.BF16, ds.ptr, dq.ptr, do.ptr, BH, S, D, S,
+                                                  S * S, S * D, S * D, 0, stream), "pv")
+
+        ms_qk = timer.run(qkt, 5, 2)
+        ms_pv = timer.run(pv, 5, 2)
+        bytes_qk = BH * (2 * S * D * 2 + S * S * 2)
+        extra["cfg5_attn_windowed"] = {
+            "qkt_us": round(ms_qk * 1e3, 1), "qkt_tflops": round(tflops(BH * S, S, D, ms_qk), 1),
+            "qkt_gbs": round(bytes_qk / (ms_qk * 1e-3) / 1e9, 1),
+            "pv_us": round(ms_pv * 1e3, 1), "pv_tflops": round(tflops(BH * S, D, S, ms_pv), 1),
+            "pv_gbs": round(bytes_qk / (ms_pv * 1e-3) / 1e9, 1)}
+        for b in (dq, dk, ds, do):
+            b.free()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (reference bf16 kernel, row sample)")
+        cpu = cpu_baseline(a_bf, w_bf, M, N, K)
+        log("  ", cpu)
+
+    line = {
+        "metric": "TFLOP/s, bf16 GEMM 5184x1024x4096 (ViT-L fc1, f32 accumulate)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K_,
+        "warmup": W_,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded SplitMix64/Box-Muller, A N(0,1), W N(0,0.02)",
+        "config": {"workload": "BASELINE configs[1] fc1: C[5184,4096] = A[5184,1024] W[4096,1024]^T, "
+                               "bf16 in/out, f32 accumulate, one GEMM launch per step",
+                   "M": M, "N": N, "K": K, "arch": arch},
+        "roofline": {"bound": "mfma", "achieved": round(value, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(value / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,186 @@
+/*
+ * include/sam3_hip.h - MI355X (gfx950) matmul backend for sam3.c: C ABI.
+ *
+ * A drop-in for the matmul path of sam3.c's backend interface. Every
+ * entry point is extern "C", takes plain pointers and sizes, and returns
+ * enum sam3_error. Reference interfaces each one replaces are cited as
+ * <path>:<line> in the sam3.c source tree.
+ *
+ * Pointers: the node-level kernels and the sam3_hip_matmul* entry points
+ * take DEVICE pointers (HBM) and run asynchronously on `stream` (a
+ * hipStream_t, NULL = the default stream); the stream plays the role the
+ * CPU kernels' thread pool plays. The backend vtable (graph_eval) takes
+ * sam3.c's ordinary graphs over host tensors and moves data itself.
+ */
+#ifndef SAM3_HIP_H
+#define SAM3_HIP_H
+
+#include "sam3_hip_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Backend object                                                       */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Ops table of the HIP backend. Replaces sam3_cpu_backend_ops()
+ * (src/backend/cpu/cpu_backend.c:160-170) / sam3_metal_backend_ops()
+ * (src/backend/metal/metal_backend.c:2114-2133) behind
+ * struct sam3_backend_ops (src/backend/backend.h:31-56). graph_eval runs
+ * MATMUL nodes (F32, F16, BF16, F32 x Q8_0) on the GPU, fusing
+ * TRANSPOSE(W) -> MATMUL -> ADD(bias) -> GELU chains, and runs ADD,
+ * GELU and 2-D TRANSPOSE on the GPU as well; other ops go to the host
+ * dispatcher set with sam3_hip_backend_set_host_dispatch, or fail with
+ * SAM3_EDTYPE when none is set (as cpu_dispatch_node does for an op with
+ * no kernel, src/backend/cpu/cpu_dispatch.c:664-669).
+ */
+const struct sam3_backend_ops *sam3_hip_backend_ops(void);
+
+/*
+ * Create and init a HIP backend on `device` (the role of
+ * sam3_backend_init(SAM3_BACKEND_CPU), src/backend/backend.c:30-77).
+ * Returns NULL on failure (no device, out of memory).
+ */
+struct sam3_backend *sam3_hip_backend_create(int device);
+
+/* Free a backend made by sam3_hip_backend_create (backend.c:79-85). */
+void sam3_hip_backend_destroy(struct sam3_backend *be);
+
+/*
+ * Host dispatcher for ops the HIP backend does not run: called with host
+ * tensors, same signature role as cpu_dispatch_node
+ * (src/backend/cpu/cpu_dispatch.c:591-686). In sam3.c this is a wrapper
+ * around cpu_dispatch_node(node, scratch, pool).
+ */
+typedef enum sam3_error (*sam3_hip_host_dispatch_fn)(const struct sam3_node *node,
+						     void *ctx);
+void sam3_hip_backend_set_host_dispatch(struct sam3_backend *be,
+					sam3_hip_host_dispatch_fn fn, void *ctx);
+
+/* The backend's HIP stream (hipStream_t). */
+void *sam3_hip_backend_stream(struct sam3_backend *be);
+
+/* Counters of the last graph_eval (for tests and profiling). */
+struct sam3_hip_eval_stats {
+	int gpu_nodes;     /* nodes run by HIP kernels                        */
+	int fused_nodes;   /* nodes folded into another node's kernel          */
+	int host_nodes;    /* nodes handed to the host dispatcher              */
+	int uploads;       /* host -> device copies                            */
+	int cache_hits;    /* inputs found resident from an earlier eval       */
+	int downloads;     /* device -> host copies                            */
+};
+void sam3_hip_backend_last_stats(struct sam3_backend *be,
+				 struct sam3_hip_eval_stats *out);
+
+/* ------------------------------------------------------------------ */
+/* Node-level kernels. Same contract as the reference CPU kernels       */
+/* (shapes from the last two dims, B = [K,N], K mismatch or output size */
+/* mismatch -> SAM3_EINVAL, wrong dtypes -> SAM3_EINVAL), with device   */
+/* data pointers and a stream in place of the thread pool.             */
+/* ------------------------------------------------------------------ */
+
+/* F32 [M,K] x F32 [K,N] -> F32. Replaces cpu_kernel_matmul
+ * (src/backend/cpu/kernels/cpu_kernels.h:27-29, cpu_matmul.c:178-257). */
+enum sam3_error sam3_hip_kernel_matmul(const struct sam3_node *node, void *stream);
+
+/* F16 x F16 -> F16, f32 accumulation. Replaces cpu_kernel_matmul_f16
+ * (cpu_kernels.h:90-91, cpu_matmul_f16.c:167-244), whose accumulator is
+ * fp16; this kernel keeps f32 and rounds once. */
+enum sam3_error sam3_hip_kernel_matmul_f16(const struct sam3_node *node, void *stream);
+
+/* BF16 x BF16 -> BF16, f32 accumulation. Replaces cpu_kernel_matmul_bf16
+ * (cpu_kernels.h:115-116, cpu_matmul_bf16.c:183-251). */
+enum sam3_error sam3_hip_kernel_matmul_bf16(const struct sam3_node *node, void *stream);
+
+/* F32 [M,K] x Q8_0 [K,N] (blocks over the flat index) -> F32. Replaces
+ * cpu_kernel_matmul_q8 (cpu_kernels.h:134-135, cpu_matmul_q8.c:168-235). */
+enum sam3_error sam3_hip_kernel_matmul_q8(const struct sam3_node *node, void *stream);
+
+/* Route one node by op and dtype. Replaces cpu_dispatch_node
+ * (src/backend/cpu/cpu_dispatch.c:591-686): same mixed F32 x Q8_0 rule,
+ * same SAM3_EDTYPE for mismatched dtypes or an (op, dtype) without a
+ * kernel. Runs MATMUL, ADD, GELU and 2-D TRANSPOSE. */
+enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Plain-pointer matmul. No counterpart in the reference: the node      */
+/* kernels above unpack to these; they add the [N,K] weight layout, a   */
+/* fused epilogue and strided batches, which the graph builder reaches  */
+/* through TRANSPOSE/ADD/GELU nodes (src/model/graph_helpers.c:297-320, */
+/* 1258-1276) and per-head attention slices (graph_helpers.c:808-843).  */
+/* ------------------------------------------------------------------ */
+#define SAM3_HIP_BIAS 1   /* C += bias[N] (bias dtype = c_dtype)           */
+#define SAM3_HIP_GELU 2   /* C = tanh-GELU(C) (cpu_gelu.c:23-38)            */
+#define SAM3_HIP_B_NT 4   /* B stored [N,K] (PyTorch [out,in]); else [K,N]  */
+
+/*
+ * C[M,N] = A[M,K] * B (+bias) (GELU). Dtypes are enum sam3_dtype:
+ *   a F32/F16/BF16 with b of the same dtype, c = a's dtype or F32;
+ *   a F32/F16/BF16 with b Q8_0, c F32/F16/BF16. Q8_0 B is [K,N] with
+ *   blocks over the flat index (the kernel contract) or, with
+ *   SAM3_HIP_B_NT, W[N,K] quantized flat (blocks along K).
+ * Rows are dense (lda = K, ldb = N or K, ldc = N).
+ */
+enum sam3_error sam3_hip_matmul(int a_dtype, const void *a,
+				int b_dtype, const void *b,
+				int c_dtype, void *c,
+				int M, int N, int K,
+				const void *bias, int flags, void *stream);
+
+/*
+ * Strided batch: for s in [0, batch): C_s = A_s * B_s, with element
+ * strides stride_a/b/c between slices (bytes for a Q8_0 B). dtype is F16
+ * or BF16 (c has the same dtype) or F32. With SAM3_HIP_B_NT, B_s is
+ * [N,K] (attention's Q K^T), else [K,N] (attention's P V).
+ */
+enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b, void *c,
+					int batch, int M, int N, int K,
+					long long stride_a, long long stride_b,
+					long long stride_c, int flags, void *stream);
+
+/* Which kernel sam3_hip_matmul would launch for this problem:
+ * 1 = tiled MFMA, 2 = skinny (small-M Q8), 3 = generic, 0 = none. */
+int sam3_hip_matmul_path(int a_dtype, int b_dtype, int c_dtype,
+			 int M, int N, int K, int flags);
+
+/* sam3_hip_matmul on a forced kernel path (1, 2 or 3 as above), for
+ * cross-checking the paths against each other. SAM3_EINVAL if that path
+ * cannot run the problem. */
+enum sam3_error sam3_hip_matmul_on_path(int path, int a_dtype, const void *a,
+					int b_dtype, const void *b,
+					int c_dtype, void *c,
+					int M, int N, int K,
+					const void *bias, int flags, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Device memory, streams and events for FFI callers (no counterpart    */
+/* in the reference, whose tensors are host memory).                    */
+/* ------------------------------------------------------------------ */
+int  sam3_hip_device_count(void);
+enum sam3_error sam3_hip_set_device(int device);
+enum sam3_error sam3_hip_malloc(void **ptr, size_t nbytes);
+enum sam3_error sam3_hip_free(void *ptr);
+enum sam3_error sam3_hip_memcpy_h2d(void *dst, const void *src, size_t nbytes);
+enum sam3_error sam3_hip_memcpy_d2h(void *dst, const void *src, size_t nbytes);
+enum sam3_error sam3_hip_memcpy_d2d(void *dst, const void *src, size_t nbytes);
+enum sam3_error sam3_hip_synchronize(void);
+enum sam3_error sam3_hip_stream_create(void **stream);
+enum sam3_error sam3_hip_stream_destroy(void *stream);
+enum sam3_error sam3_hip_stream_synchronize(void *stream);
+enum sam3_error sam3_hip_event_create(void **event);
+enum sam3_error sam3_hip_event_destroy(void *event);
+enum sam3_error sam3_hip_event_record(void *event, void *stream);
+enum sam3_error sam3_hip_event_elapsed_ms(float *ms, void *start, void *stop);
+/* gcnArchName of the device (e.g. "gfx950:sramecc+:xnack-"), or "". */
+const char *sam3_hip_device_arch(int device);
+/* Message of the last failure on this thread ("" if none). */
+const char *sam3_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3_HIP_H */

@@ -1,0 +1,94 @@
+/*
+ * s3k.h - launch interface between the C11 host (sam3_hip_backend.c) and
+ * the HIP kernels (gemm.hip, skinny.hip, aux.hip).
+ *
+ * Everything here is plain C: the host side is compiled by gcc as C11,
+ * the kernel side by hipcc for gfx950. Launchers return a hipError_t
+ * value as int (0 = success) and never allocate device memory.
+ */
+#ifndef SAM3_S3K_H
+#define SAM3_S3K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element kinds; the numbering is sam3_dtype's (sam3_types.h:45-52). */
+enum s3k_kind {
+	S3K_F32  = 0,
+	S3K_F16  = 1,
+	S3K_BF16 = 2,
+	S3K_Q8   = 5,
+};
+
+/* Epilogue / layout flags. */
+#define S3K_EPI_BIAS 1  /* out += bias[n] (bias has the output's kind)    */
+#define S3K_EPI_GELU 2  /* out = tanh-GELU(out)                           */
+#define S3K_B_NT     4  /* B stored [N,K] (k contiguous), else [K,N]      */
+
+/*
+ * One (optionally strided-batched) GEMM: C[M,N] = A[M,K] * B, row-major.
+ * A kind: F32 | F16 | BF16. B kind: F32 | F16 | BF16 | Q8 (Q8 must be
+ * S3K_B_NT with K % 32 == 0: the rows of W[N,K] are whole 36-byte blocks).
+ * C kind: F32 | F16 | BF16.  lda/ldb/ldc are in elements (for Q8 B the
+ * row pitch is implied: K/32 blocks of 36 bytes).
+ */
+struct s3k_gemm {
+	const void *a;
+	const void *b;
+	void       *c;
+	const void *bias;
+	int         M, N, K;
+	int         lda, ldb, ldc;
+	long long   stride_a, stride_b, stride_c; /* per batch: elements;
+						   * bytes for a Q8 B      */
+	int         batch;
+	int         a_kind, b_kind, c_kind;
+	int         flags;
+};
+
+/* Which kernel s3k_gemm_launch would pick (for tests and the bench). */
+enum s3k_path {
+	S3K_PATH_NONE    = 0,
+	S3K_PATH_MFMA    = 1, /* LDS-tiled MFMA GEMM                        */
+	S3K_PATH_SKINNY  = 2, /* bandwidth-bound small-M Q8 kernel          */
+	S3K_PATH_GENERIC = 3, /* one thread per output, reference order      */
+};
+
+int s3k_gemm_path(const struct s3k_gemm *g);
+int s3k_gemm_launch(const struct s3k_gemm *g, void *stream);
+
+/* Force one path (testing): returns hipErrorInvalidValue if it cannot run
+ * this problem. */
+int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *stream);
+
+/*
+ * Q8 [K,N] with blocks over the flat index k*N+n (the reference kernel
+ * contract) -> f16 W^T[N,K] (q*scale rounded to f16), so the Q8 NN case
+ * runs on the f16 NT GEMM. Any K, N.
+ */
+int s3k_q8_kn_to_f16_nk(const void *blocks, void *out, int K, int N,
+			void *stream);
+/* Q8 [N,K] with blocks over the flat index n*K+k (any K) -> f16 [N,K]. */
+int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N,
+			void *stream);
+
+/* Elementwise ops the fused graph paths fall back to when they cannot
+ * fuse (reference semantics, one rounding per op). */
+int s3k_bias_add(int kind, const void *x, const void *bias, void *out,
+		 long long rows, int n, void *stream);
+int s3k_add_same(int kind, const void *x, const void *y, void *out,
+		 long long n, void *stream);
+int s3k_gelu(int kind, const void *x, void *out, long long n, void *stream);
+/* batch slices of [rows, cols] -> [cols, rows] */
+int s3k_transpose2d(int esize, const void *src, void *dst, int batch, int rows,
+		    int cols, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3_S3K_H */

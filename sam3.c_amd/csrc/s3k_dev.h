@@ -1,0 +1,136 @@
+/*
+ * s3k_dev.h - device-side helpers shared by the gfx950 kernels.
+ *
+ * Conversions follow the rounding the reference CPU path uses
+ * (src/core/half.h:58-210 of sam3.c): f32 -> bf16 and f32 -> f16 round
+ * to nearest even; a NaN converted to bf16 stays a quiet NaN. The GELU
+ * is the tanh form of the reference CPU kernel (cpu_gelu.c:23-38).
+ */
+#ifndef SAM3_S3K_DEV_H
+#define SAM3_S3K_DEV_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __attribute__((ext_vector_type(8))) __bf16 s3k_bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 s3k_f16x8;
+typedef __attribute__((ext_vector_type(16))) float s3k_f32x16;
+typedef __attribute__((ext_vector_type(4))) float s3k_f32x4;
+
+namespace s3k {
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b)
+{
+	return __uint_as_float(b << 16);
+}
+
+/* Round to nearest even; NaN -> quiet NaN with the sign kept. */
+__device__ __forceinline__ uint32_t f32_to_bf16(float f)
+{
+	uint32_t u = __float_as_uint(f);
+	if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu))
+		return ((u >> 16) | 0x40u) & 0xFFFFu;
+	u += 0x7FFFu + ((u >> 16) & 1u);
+	return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h)
+{
+	return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+/* Hardware conversion: round to nearest even, f16 subnormals kept. */
+__device__ __forceinline__ uint32_t f32_to_f16(float f)
+{
+	return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float round_bf16(float f)
+{
+	return bf16_to_f32(f32_to_bf16(f));
+}
+
+__device__ __forceinline__ float round_f16(float f)
+{
+	return (float)(_Float16)f;
+}
+
+/* 0.5*x*(1 + tanh(sqrt(2/pi)*(x + 0.044715*x^3))), the reference's
+ * operation order. */
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+	float cube = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
+	float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, cube));
+	return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
+/* Pack two f32 as two f16 (RNE) in one dword, lo first. */
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi)
+{
+	return f32_to_f16(lo) | (f32_to_f16(hi) << 16);
+}
+
+/* Four signed bytes of w, each times s, as four f16 in two dwords. The
+ * product q*s is formed in f32 (exact rounding of the true product) and
+ * rounded once to f16. */
+__device__ __forceinline__ uint2 dequant4_f16(uint32_t w, float s)
+{
+	float f0 = (float)(int)(int8_t)(w & 0xFFu);
+	float f1 = (float)(int)(int8_t)((w >> 8) & 0xFFu);
+	float f2 = (float)(int)(int8_t)((w >> 16) & 0xFFu);
+	float f3 = (float)(int)(int8_t)(w >> 24);
+	uint2 r;
+	r.x = pack_f16x2(f0 * s, f1 * s);
+	r.y = pack_f16x2(f2 * s, f3 * s);
+	return r;
+}
+
+/* Output epilogue with the reference's rounding points: the matmul
+ * result, the bias add and the GELU each round to the output type, as
+ * MATMUL -> ADD -> GELU nodes do on the CPU backend. */
+template <int CK>
+__device__ __forceinline__ float epilogue(float acc, float bias, int flags)
+{
+	float v = acc;
+	if (CK == 2) { /* BF16 */
+		v = round_bf16(v);
+		if (flags & 1)
+			v = round_bf16(__fadd_rn(v, bias));
+		if (flags & 2)
+			v = round_bf16(gelu_tanh(v));
+	} else if (CK == 1) { /* F16 */
+		v = round_f16(v);
+		if (flags & 1)
+			v = round_f16(__fadd_rn(v, bias));
+		if (flags & 2)
+			v = round_f16(gelu_tanh(v));
+	} else {
+		if (flags & 1)
+			v = __fadd_rn(v, bias);
+		if (flags & 2)
+			v = gelu_tanh(v);
+	}
+	return v;
+}
+
+__device__ __forceinline__ float load_as_f32(const void *p, long long i, int kind)
+{
+	if (kind == 0)
+		return ((const float *)p)[i];
+	uint32_t h = ((const uint16_t *)p)[i];
+	return kind == 2 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, long long i, int kind, float v)
+{
+	if (kind == 0)
+		((float *)p)[i] = v;
+	else if (kind == 2)
+		((uint16_t *)p)[i] = (uint16_t)f32_to_bf16(v);
+	else
+		((uint16_t *)p)[i] = (uint16_t)f32_to_f16(v);
+}
+
+} /* namespace s3k */
+
+#endif /* SAM3_S3K_DEV_H */

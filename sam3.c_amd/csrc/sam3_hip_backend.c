@@ -1,0 +1,736 @@
+/*
+ * sam3_hip_backend.c - the HIP backend object behind sam3.c's backend
+ * vtable (src/backend/backend.h:31-62): init, free, alloc_tensor,
+ * graph_eval, arena_reset, cache_invalidate.
+ *
+ * graph_eval walks g->nodes in order, as cpu_graph_eval does
+ * (src/backend/cpu/cpu_backend.c:124-151), and stops at the first failing
+ * node. MATMUL runs on the GPU; so do ADD, GELU and last-two-dims
+ * TRANSPOSE. Chains the graph builder emits for a linear layer
+ * (gh_linear: TRANSPOSE(W) -> MATMUL -> ADD(bias), graph_helpers.c:
+ * 297-320) and an MLP (gh_mlp: ... -> GELU, graph_helpers.c:1258-1276)
+ * run as one GEMM launch: the transpose becomes the [N,K] weight layout,
+ * the bias and GELU the epilogue. The folding applies only when each
+ * folded intermediate has exactly one consumer in the graph; folded
+ * intermediates are not materialised. Any other op is handed to the host
+ * dispatcher (sam3.c's cpu_dispatch_node in an integration), or fails
+ * with SAM3_EDTYPE when none is set.
+ *
+ * Memory. sam3.c tensors point at host memory (the CPU arena or the
+ * read-only .sam3 mmap, graph_helpers.c:122-145). Each host buffer gets a
+ * device shadow in HBM, tracked by a residency entry {host ptr, device
+ * ptr, which copy is current}:
+ *   - an input not yet on the device is uploaded once; non-ephemeral
+ *     inputs (weights) keep their shadow across graph_eval calls until
+ *     cache_invalidate / arena_reset drops it (tensor.h:31-38,
+ *     backend.h:50-55);
+ *   - outputs are written to the shadow and copied back to the host when
+ *     the eval ends (kept on the device only with g->no_readback);
+ *   - before a host-dispatched node, its inputs are copied back first.
+ * Tensors whose data already is device memory are used in place.
+ * alloc_tensor hands out pinned host memory (hipHostMalloc), so the
+ * copies above run at full PCIe/xGMI rate and asynchronously.
+ */
+#include "sam3_hip.h"
+#include "sam3_hip_internal.h"
+#include "s3k.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define S3H_ARENA_DEFAULT (256UL << 20)
+#define S3H_ARENA_ALIGN 256
+
+struct s3h_res {
+	const char *host;
+	size_t nbytes;
+	void *dev;
+	unsigned char dev_valid;
+	unsigned char host_valid;
+	unsigned char keep;      /* survives the end of this eval            */
+	unsigned char produced;  /* written by a GPU node in this eval        */
+};
+
+struct sam3_hip_backend {
+	struct sam3_backend base; /* must be first (backend.h:59-62) */
+	int device;
+	hipStream_t stream;
+	struct s3h_res *res;
+	int n_res, cap_res;
+	char *arena;
+	size_t arena_size, arena_off;
+	sam3_hip_host_dispatch_fn host_fn;
+	void *host_ctx;
+	struct sam3_hip_eval_stats stats;
+};
+
+/* ------------------------------------------------------------------ */
+/* Residency table                                                      */
+/* ------------------------------------------------------------------ */
+static struct s3h_res *res_find(struct sam3_hip_backend *hb, const void *host)
+{
+	for (int i = 0; i < hb->n_res; i++)
+		if (hb->res[i].host == host)
+			return &hb->res[i];
+	return NULL;
+}
+
+static void res_drop_at(struct sam3_hip_backend *hb, int i)
+{
+	if (hb->res[i].dev)
+		(void)hipFreeAsync(hb->res[i].dev, hb->stream);
+	hb->res[i] = hb->res[hb->n_res - 1];
+	hb->n_res--;
+}
+
+static void res_drop_range(struct sam3_hip_backend *hb, const char *lo, const char *hi)
+{
+	for (int i = hb->n_res - 1; i >= 0; i--) {
+		const char *s = hb->res[i].host, *e = s + hb->res[i].nbytes;
+		if (s < hi && e > lo)
+			res_drop_at(hb, i);
+	}
+}
+
+static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
+			       size_t nbytes, struct s3h_res **out)
+{
+	if (hb->n_res == hb->cap_res) {
+		int cap = hb->cap_res ? hb->cap_res * 2 : 256;
+		struct s3h_res *r = realloc(hb->res, (size_t)cap * sizeof(*r));
+		if (!r) {
+			s3h_error("graph_eval: out of host memory for the residency table");
+			return SAM3_ENOMEM;
+		}
+		hb->res = r;
+		hb->cap_res = cap;
+	}
+	struct s3h_res *e = &hb->res[hb->n_res];
+	memset(e, 0, sizeof(*e));
+	e->host = t->data;
+	e->nbytes = nbytes;
+	enum sam3_error err = s3h_hip(hipMallocAsync(&e->dev, nbytes ? nbytes : 1, hb->stream),
+				      "graph_eval: device shadow");
+	if (err != SAM3_OK)
+		return err;
+	e->host_valid = 1;
+	e->keep = !t->ephemeral;
+	hb->n_res++;
+	*out = e;
+	return SAM3_OK;
+}
+
+static int is_device_ptr(const void *p)
+{
+	hipPointerAttribute_t attr;
+	memset(&attr, 0, sizeof(attr));
+	hipError_t e = hipPointerGetAttributes(&attr, p);
+	if (e != hipSuccess) {
+		(void)hipGetLastError();
+		return 0;
+	}
+	return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+/* Device address of tensor t's data, uploading it if needed. */
+static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
+			      void **out)
+{
+	if (!t || !t->data) {
+		s3h_error("graph_eval: input tensor without data");
+		return SAM3_EINVAL;
+	}
+	if (is_device_ptr(t->data)) {
+		*out = t->data;
+		return SAM3_OK;
+	}
+	size_t nbytes = s3h_tensor_bytes(t);
+	struct s3h_res *e = res_find(hb, t->data);
+	if (e && e->nbytes < nbytes) {
+		res_drop_at(hb, (int)(e - hb->res));
+		e = NULL;
+	}
+	if (!e) {
+		enum sam3_error err = res_new(hb, t, nbytes, &e);
+		if (err != SAM3_OK)
+			return err;
+	}
+	if (!e->dev_valid) {
+		enum sam3_error err = s3h_hip(hipMemcpyAsync(e->dev, e->host, e->nbytes,
+							     hipMemcpyHostToDevice, hb->stream),
+					      "graph_eval: upload");
+		if (err != SAM3_OK)
+			return err;
+		e->dev_valid = 1;
+		hb->stats.uploads++;
+	} else if (!e->produced) {
+		hb->stats.cache_hits++;
+	}
+	if (t->ephemeral)
+		e->keep = 0;
+	*out = e->dev;
+	return SAM3_OK;
+}
+
+/* Device address the output of a GPU node is written to. */
+static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
+			       void **out)
+{
+	if (!t || !t->data) {
+		s3h_error("graph_eval: output tensor without data");
+		return SAM3_EINVAL;
+	}
+	if (is_device_ptr(t->data)) {
+		*out = t->data;
+		return SAM3_OK;
+	}
+	size_t nbytes = s3h_tensor_bytes(t);
+	struct s3h_res *e = res_find(hb, t->data);
+	if (e && e->nbytes < nbytes) {
+		res_drop_at(hb, (int)(e - hb->res));
+		e = NULL;
+	}
+	if (!e) {
+		enum sam3_error err = res_new(hb, t, nbytes, &e);
+		if (err != SAM3_OK)
+			return err;
+	}
+	e->dev_valid = 1;
+	e->host_valid = 0;
+	e->produced = 1;
+	e->keep = 1;
+	*out = e->dev;
+	return SAM3_OK;
+}
+
+static enum sam3_error download(struct sam3_hip_backend *hb, struct s3h_res *e)
+{
+	enum sam3_error err = s3h_hip(hipMemcpyAsync((void *)e->host, e->dev, e->nbytes,
+						     hipMemcpyDeviceToHost, hb->stream),
+				      "graph_eval: download");
+	if (err == SAM3_OK) {
+		e->host_valid = 1;
+		hb->stats.downloads++;
+	}
+	return err;
+}
+
+/* ------------------------------------------------------------------ */
+/* Graph analysis: how many inputs reference each tensor header.        */
+/* ------------------------------------------------------------------ */
+struct use_map {
+	const struct sam3_tensor **key;
+	int *count;
+	size_t mask;
+};
+
+static size_t ptr_hash(const void *p)
+{
+	uint64_t x = (uint64_t)(uintptr_t)p;
+	x ^= x >> 33;
+	x *= 0xff51afd7ed558ccdULL;
+	x ^= x >> 33;
+	return (size_t)x;
+}
+
+static int *use_slot(struct use_map *m, const struct sam3_tensor *t)
+{
+	size_t i = ptr_hash(t) & m->mask;
+	while (m->key[i] && m->key[i] != t)
+		i = (i + 1) & m->mask;
+	m->key[i] = t;
+	return &m->count[i];
+}
+
+static int uses_of(struct use_map *m, const struct sam3_tensor *t)
+{
+	size_t i = ptr_hash(t) & m->mask;
+	while (m->key[i]) {
+		if (m->key[i] == t)
+			return m->count[i];
+		i = (i + 1) & m->mask;
+	}
+	return 0;
+}
+
+static enum sam3_error build_uses(const struct sam3_graph *g, struct use_map *m)
+{
+	size_t want = 16;
+	while (want < (size_t)g->n_nodes * 2 * (SAM3_NODE_MAX_INPUTS + 1))
+		want <<= 1;
+	m->key = calloc(want, sizeof(*m->key));
+	m->count = calloc(want, sizeof(*m->count));
+	m->mask = want - 1;
+	if (!m->key || !m->count) {
+		free(m->key);
+		free(m->count);
+		s3h_error("graph_eval: out of host memory");
+		return SAM3_ENOMEM;
+	}
+	for (int i = 0; i < g->n_nodes; i++) {
+		const struct sam3_node *n = &g->nodes[i];
+		for (int j = 0; j < n->n_inputs && j < SAM3_NODE_MAX_INPUTS; j++)
+			if (n->inputs[j])
+				(*use_slot(m, n->inputs[j]))++;
+	}
+	return SAM3_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* Node execution                                                       */
+/* ------------------------------------------------------------------ */
+static int float_dt(int dt)
+{
+	return dt == SAM3_DTYPE_F32 || dt == SAM3_DTYPE_F16 || dt == SAM3_DTYPE_BF16;
+}
+
+/* A 2-D TRANSPOSE whose only consumer is a later MATMUL's B operand. */
+static int transpose_folds(const struct sam3_graph *g, int i, struct use_map *uses)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->n_inputs < 1 || !n->inputs[0] || !n->output || n->inputs[0]->n_dims != 2 ||
+	    !s3h_transpose_is_swap(n) || uses_of(uses, n->output) != 1)
+		return 0;
+	for (int j = i + 1; j < g->n_nodes; j++) {
+		const struct sam3_node *m = &g->nodes[j];
+		for (int k = 0; k < m->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++) {
+			if (m->inputs[k] != n->output)
+				continue;
+			return m->op == SAM3_OP_MATMUL && k == 1 && m->n_inputs >= 2 &&
+			       m->inputs[0] && (m->inputs[0]->dtype == n->inputs[0]->dtype ||
+						n->inputs[0]->dtype == SAM3_DTYPE_Q8_0);
+		}
+	}
+	return 0;
+}
+
+static const struct sam3_tensor *folded_source(const struct sam3_graph *g, int upto,
+					       const unsigned char *folded,
+					       const struct sam3_tensor *t)
+{
+	for (int j = upto - 1; j >= 0; j--)
+		if (folded[j] && g->nodes[j].output == t)
+			return g->nodes[j].inputs[0];
+	return NULL;
+}
+
+/* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
+ * Returns the number of nodes consumed in *used. */
+static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3_graph *g,
+				  int i, const unsigned char *folded, struct use_map *uses,
+				  int *used)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->n_inputs < 2 || !n->inputs[0] || !n->inputs[1] || !n->output) {
+		s3h_error("matmul: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *a = n->inputs[0], *b = n->inputs[1];
+	const struct sam3_tensor *w = folded_source(g, i, folded, b);
+	const int nt = w != NULL;
+	const struct sam3_tensor *bsrc = nt ? w : b;
+	int a_dt = a->dtype, b_dt = bsrc->dtype;
+
+	/* the same routing as cpu_dispatch_node (cpu_dispatch.c:621-655) */
+	if (b_dt == SAM3_DTYPE_Q8_0 ? a_dt != SAM3_DTYPE_F32 : a_dt != b_dt) {
+		s3h_error("graph_eval: matmul dtype mismatch a=%d b=%d", a_dt, b_dt);
+		return SAM3_EDTYPE;
+	}
+	if (!float_dt(a_dt)) {
+		s3h_error("graph_eval: no matmul kernel for dtype %d", a_dt);
+		return SAM3_EDTYPE;
+	}
+	int M, K, N;
+	M = a->n_dims >= 2 ? a->dims[a->n_dims - 2] : 1;
+	K = a->n_dims >= 1 ? a->dims[a->n_dims - 1] : 0;
+	int kb;
+	if (nt) { /* w is [N,K] */
+		N = w->dims[0];
+		kb = w->dims[1];
+	} else {
+		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
+		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
+	}
+	if (a->n_dims < 1 || kb != K) {
+		s3h_error("matmul: K mismatch %d != %d", K, kb);
+		return SAM3_EINVAL;
+	}
+	if (s3h_nelems(n->output) != (long long)M * N) {
+		s3h_error("matmul: output size mismatch");
+		return SAM3_EINVAL;
+	}
+	const int c_dt = b_dt == SAM3_DTYPE_Q8_0 ? SAM3_DTYPE_F32 : a_dt;
+
+	/* epilogue folding */
+	int flags = nt ? SAM3_HIP_B_NT : 0;
+	const struct sam3_tensor *out = n->output, *bias = NULL;
+	int j = i + 1;
+	if (j < g->n_nodes && g->nodes[j].op == SAM3_OP_ADD && g->nodes[j].n_inputs == 2 &&
+	    g->nodes[j].inputs[0] == out && g->nodes[j].inputs[1] &&
+	    g->nodes[j].inputs[1] != out && uses_of(uses, out) == 1 &&
+	    (int)g->nodes[j].inputs[1]->dtype == c_dt && s3h_nelems(g->nodes[j].inputs[1]) == N &&
+	    g->nodes[j].output && s3h_nelems(g->nodes[j].output) == (long long)M * N) {
+		bias = g->nodes[j].inputs[1];
+		out = g->nodes[j].output;
+		flags |= SAM3_HIP_BIAS;
+		j++;
+	}
+	if (j < g->n_nodes && g->nodes[j].op == SAM3_OP_GELU && g->nodes[j].n_inputs >= 1 &&
+	    g->nodes[j].inputs[0] == out && uses_of(uses, out) == 1 && g->nodes[j].output &&
+	    s3h_nelems(g->nodes[j].output) == (long long)M * N) {
+		out = g->nodes[j].output;
+		flags |= SAM3_HIP_GELU;
+		j++;
+	}
+
+	void *da, *db, *dc, *dbias = NULL;
+	enum sam3_error err = dev_in(hb, a, &da);
+	if (err == SAM3_OK)
+		err = dev_in(hb, bsrc, &db);
+	if (err == SAM3_OK && bias)
+		err = dev_in(hb, bias, &dbias);
+	if (err == SAM3_OK)
+		err = dev_out(hb, out, &dc);
+	if (err != SAM3_OK)
+		return err;
+	err = sam3_hip_matmul(a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags, hb->stream);
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.fused_nodes += j - i - 1;
+		*used = j - i;
+	}
+	return err;
+}
+
+/* ADD / GELU / TRANSPOSE on device copies of the node's tensors. */
+static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct sam3_node *n)
+{
+	struct sam3_tensor tin[SAM3_NODE_MAX_INPUTS], tout;
+	struct sam3_node dn = *n;
+	enum sam3_error err = SAM3_OK;
+	for (int k = 0; k < n->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++) {
+		if (!n->inputs[k])
+			continue;
+		tin[k] = *n->inputs[k];
+		err = dev_in(hb, n->inputs[k], &tin[k].data);
+		if (err != SAM3_OK)
+			return err;
+		dn.inputs[k] = &tin[k];
+	}
+	if (!n->output) {
+		s3h_error("graph_eval: NULL output");
+		return SAM3_EINVAL;
+	}
+	tout = *n->output;
+	err = dev_out(hb, n->output, &tout.data);
+	if (err != SAM3_OK)
+		return err;
+	dn.output = &tout;
+	if (n->op == SAM3_OP_ADD)
+		err = s3h_add(&dn, hb->stream);
+	else if (n->op == SAM3_OP_GELU)
+		err = s3h_gelu(&dn, hb->stream);
+	else
+		err = s3h_transpose(&dn, hb->stream);
+	if (err == SAM3_OK)
+		hb->stats.gpu_nodes++;
+	return err;
+}
+
+static int runs_on_gpu(const struct sam3_node *n)
+{
+	if (n->n_inputs < 1 || !n->inputs[0])
+		return 0;
+	const int dt = n->inputs[0]->dtype;
+	for (int k = 1; k < n->n_inputs; k++)
+		if (n->inputs[k] && (int)n->inputs[k]->dtype != dt)
+			return 0;
+	switch (n->op) {
+	case SAM3_OP_ADD:
+	case SAM3_OP_GELU:
+		return float_dt(dt);
+	case SAM3_OP_TRANSPOSE:
+		return s3h_dtype_size(dt) != 0 && s3h_transpose_is_swap(n);
+	default:
+		return 0;
+	}
+}
+
+static enum sam3_error run_host(struct sam3_hip_backend *hb, const struct sam3_node *n)
+{
+	if (!hb->host_fn) {
+		s3h_error("graph_eval: no HIP kernel for op=%d and no host dispatcher", n->op);
+		return SAM3_EDTYPE;
+	}
+	enum sam3_error err = SAM3_OK;
+	for (int k = 0; k < n->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++) {
+		if (!n->inputs[k] || !n->inputs[k]->data)
+			continue;
+		struct s3h_res *e = res_find(hb, n->inputs[k]->data);
+		if (e && e->dev_valid && !e->host_valid)
+			err = download(hb, e);
+		if (err != SAM3_OK)
+			return err;
+	}
+	err = s3h_hip(hipStreamSynchronize(hb->stream), "graph_eval: sync before host op");
+	if (err != SAM3_OK)
+		return err;
+	err = hb->host_fn(n, hb->host_ctx);
+	if (err != SAM3_OK)
+		return err;
+	if (n->output && n->output->data) {
+		struct s3h_res *e = res_find(hb, n->output->data);
+		if (e) {
+			e->dev_valid = 0;
+			e->host_valid = 1;
+			e->produced = 0;
+		}
+	}
+	hb->stats.host_nodes++;
+	return SAM3_OK;
+}
+
+static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph *g)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	enum sam3_error err;
+
+	if (!be || !g) {
+		s3h_error("graph_eval: NULL argument");
+		return SAM3_EINVAL;
+	}
+	memset(&hb->stats, 0, sizeof(hb->stats));
+	if (g->n_nodes <= 0)
+		return SAM3_OK;
+	err = s3h_hip(hipSetDevice(hb->device), "graph_eval: set device");
+	if (err != SAM3_OK)
+		return err;
+
+	struct use_map uses;
+	err = build_uses(g, &uses);
+	if (err != SAM3_OK)
+		return err;
+	unsigned char *folded = calloc((size_t)g->n_nodes, 1);
+	if (!folded) {
+		free(uses.key);
+		free(uses.count);
+		s3h_error("graph_eval: out of host memory");
+		return SAM3_ENOMEM;
+	}
+	for (int i = 0; i < hb->n_res; i++)
+		hb->res[i].produced = 0;
+
+	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
+		const struct sam3_node *n = &g->nodes[i];
+		int used = 1;
+		if (n->op == SAM3_OP_NONE) {
+			err = SAM3_OK;
+		} else if (n->op == SAM3_OP_TRANSPOSE && transpose_folds(g, i, &uses)) {
+			folded[i] = 1;
+			hb->stats.fused_nodes++;
+		} else if (n->op == SAM3_OP_MATMUL) {
+			err = run_matmul(hb, g, i, folded, &uses, &used);
+		} else if (runs_on_gpu(n)) {
+			err = run_elementwise(hb, n);
+		} else {
+			err = run_host(hb, n);
+		}
+		if (err != SAM3_OK)
+			s3h_error("hip_graph_eval: node %d (op=%d) failed", i, n->op);
+		i += used;
+	}
+
+	if (err == SAM3_OK && !g->no_readback) {
+		for (int i = 0; i < hb->n_res && err == SAM3_OK; i++) {
+			struct s3h_res *e = &hb->res[i];
+			if (e->produced && e->dev_valid && !e->host_valid)
+				err = download(hb, e);
+		}
+	}
+	enum sam3_error serr = s3h_hip(hipStreamSynchronize(hb->stream), "graph_eval: sync");
+	if (err == SAM3_OK)
+		err = serr;
+	for (int i = hb->n_res - 1; i >= 0; i--)
+		if (!hb->res[i].keep)
+			res_drop_at(hb, i);
+	free(folded);
+	free(uses.key);
+	free(uses.count);
+	return err;
+}
+
+/* ------------------------------------------------------------------ */
+/* vtable                                                               */
+/* ------------------------------------------------------------------ */
+static enum sam3_error hip_init(struct sam3_backend *be)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	int n = 0;
+	if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+		(void)hipGetLastError();
+		s3h_error("hip backend: no HIP device");
+		return SAM3_EBACKEND;
+	}
+	if (hb->device < 0 || hb->device >= n) {
+		s3h_error("hip backend: device %d out of range (%d devices)", hb->device, n);
+		return SAM3_EINVAL;
+	}
+	enum sam3_error err = s3h_hip(hipSetDevice(hb->device), "hip backend: set device");
+	if (err == SAM3_OK)
+		err = s3h_hip(hipStreamCreateWithFlags(&hb->stream, hipStreamNonBlocking),
+			      "hip backend: stream");
+	return err;
+}
+
+static void hip_free(struct sam3_backend *be)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (!hb)
+		return;
+	(void)hipSetDevice(hb->device);
+	while (hb->n_res)
+		res_drop_at(hb, hb->n_res - 1);
+	free(hb->res);
+	hb->res = NULL;
+	hb->cap_res = 0;
+	if (hb->stream) {
+		(void)hipStreamSynchronize(hb->stream);
+		(void)hipStreamDestroy(hb->stream);
+		hb->stream = NULL;
+	}
+	if (hb->arena) {
+		(void)hipHostFree(hb->arena);
+		hb->arena = NULL;
+	}
+}
+
+/* Same contract as cpu_alloc_tensor (cpu_backend.c:84-118): n_dims in
+ * [1, 4], a dtype with an element size, fills data/nbytes/strides; memory
+ * is pinned host memory from the backend's arena. */
+static enum sam3_error hip_alloc_tensor(struct sam3_backend *be, struct sam3_tensor *t)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (!t) {
+		s3h_error("HIP alloc_tensor: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	if (t->n_dims < 1 || t->n_dims > SAM3_MAX_DIMS) {
+		s3h_error("HIP alloc_tensor: invalid n_dims=%d", t->n_dims);
+		return SAM3_EINVAL;
+	}
+	size_t es = s3h_dtype_size(t->dtype);
+	if (es == 0) {
+		s3h_error("HIP alloc_tensor: unknown dtype=%d", t->dtype);
+		return SAM3_EINVAL;
+	}
+	if (!hb->arena) {
+		const char *env = getenv("SAM3_HIP_ARENA_MB");
+		size_t sz = env ? (size_t)strtoull(env, NULL, 10) << 20 : S3H_ARENA_DEFAULT;
+		if (!sz)
+			sz = S3H_ARENA_DEFAULT;
+		enum sam3_error err = s3h_hip(hipHostMalloc((void **)&hb->arena, sz,
+							    hipHostMallocDefault),
+					      "HIP alloc_tensor: pinned arena");
+		if (err != SAM3_OK)
+			return err;
+		hb->arena_size = sz;
+		hb->arena_off = 0;
+	}
+	size_t nbytes = (size_t)s3h_nelems(t) * es;
+	size_t off = (hb->arena_off + S3H_ARENA_ALIGN - 1) & ~(size_t)(S3H_ARENA_ALIGN - 1);
+	if (off + nbytes > hb->arena_size) {
+		s3h_error("HIP alloc_tensor: OOM (%zu bytes requested, %zu / %zu used)", nbytes,
+			  hb->arena_off, hb->arena_size);
+		return SAM3_ENOMEM;
+	}
+	t->data = hb->arena + off;
+	hb->arena_off = off + nbytes;
+	t->nbytes = nbytes;
+	int s = 1;
+	for (int i = t->n_dims - 1; i >= 0; i--) {
+		t->strides[i] = s;
+		s *= t->dims[i];
+	}
+	return SAM3_OK;
+}
+
+static void hip_arena_reset(struct sam3_backend *be)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (hb->arena)
+		res_drop_range(hb, hb->arena, hb->arena + hb->arena_size);
+	hb->arena_off = 0;
+}
+
+static void hip_cache_invalidate(struct sam3_backend *be, const void *start, size_t len)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	res_drop_range(hb, (const char *)start, (const char *)start + len);
+}
+
+static const struct sam3_backend_ops hip_ops = {
+	.init             = hip_init,
+	.free             = hip_free,
+	.alloc_tensor     = hip_alloc_tensor,
+	.graph_eval       = hip_graph_eval,
+	.arena_reset      = hip_arena_reset,
+	.cache_invalidate = hip_cache_invalidate,
+};
+
+const struct sam3_backend_ops *sam3_hip_backend_ops(void)
+{
+	return &hip_ops;
+}
+
+struct sam3_backend *sam3_hip_backend_create(int device)
+{
+	struct sam3_hip_backend *hb = calloc(1, sizeof(*hb));
+	if (!hb) {
+		s3h_error("hip backend: out of host memory");
+		return NULL;
+	}
+	/* sam3.c's enum has CPU and METAL only; the object is told apart by
+	 * its ops table, and `type` stays CPU so model code keeps its
+	 * host-memory behaviour (image_encoder.c:703 checks METAL). */
+	hb->base.type = SAM3_BACKEND_CPU;
+	hb->base.ops = &hip_ops;
+	hb->device = device;
+	if (hip_ops.init(&hb->base) != SAM3_OK) {
+		hip_free(&hb->base);
+		free(hb);
+		return NULL;
+	}
+	return &hb->base;
+}
+
+void sam3_hip_backend_destroy(struct sam3_backend *be)
+{
+	if (!be)
+		return;
+	be->ops->free(be);
+	free(be);
+}
+
+void sam3_hip_backend_set_host_dispatch(struct sam3_backend *be, sam3_hip_host_dispatch_fn fn,
+					void *ctx)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (!hb)
+		return;
+	hb->host_fn = fn;
+	hb->host_ctx = ctx;
+}
+
+void *sam3_hip_backend_stream(struct sam3_backend *be)
+{
+	return be ? (void *)((struct sam3_hip_backend *)be)->stream : NULL;
+}
+
+void sam3_hip_backend_last_stats(struct sam3_backend *be, struct sam3_hip_eval_stats *out)
+{
+	if (!be || !out)
+		return;
+	*out = ((struct sam3_hip_backend *)be)->stats;
+}

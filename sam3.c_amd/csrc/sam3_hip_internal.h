@@ -1,0 +1,26 @@
+/*
+ * sam3_hip_internal.h - helpers shared by the C11 host files of the HIP
+ * backend (not part of the exported ABI).
+ */
+#ifndef SAM3_HIP_INTERNAL_H
+#define SAM3_HIP_INTERNAL_H
+
+#include "sam3_hip.h"
+
+/* Record (and unless SAM3_HIP_QUIET, print) the last failure. */
+void s3h_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+/* hipError_t -> sam3_error (OK / ENOMEM / EBACKEND), recording failures. */
+enum sam3_error s3h_hip(int hip_error, const char *what);
+
+size_t s3h_dtype_size(int dtype);
+long long s3h_nelems(const struct sam3_tensor *t);
+size_t s3h_tensor_bytes(const struct sam3_tensor *t);
+
+/* Device-pointer elementwise nodes used by the dispatcher and graph_eval. */
+enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
+enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
+enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
+int s3h_transpose_is_swap(const struct sam3_node *node);
+
+#endif /* SAM3_HIP_INTERNAL_H */

@@ -1,0 +1,622 @@
+/*
+ * sam3_hip_ops.c - C11 host side of the HIP matmul path: argument and
+ * dtype checks, node-level kernels, the per-node dispatcher and the
+ * device helpers exported through include/sam3_hip.h.
+ *
+ * Error behaviour follows the reference CPU path (sam3.c):
+ *   - node kernels: NULL tensors, wrong dtypes, K mismatch and output size
+ *     mismatch -> SAM3_EINVAL (src/backend/cpu/kernels/cpu_matmul.c:
+ *     178-229, cpu_matmul_q8.c:168-213);
+ *   - dispatcher: mixed dtypes other than F32 x Q8_0 -> SAM3_EDTYPE, an
+ *     (op, dtype) without a kernel -> SAM3_EDTYPE
+ *     (src/backend/cpu/cpu_dispatch.c:591-686);
+ *   - HIP failures -> SAM3_EBACKEND, device out of memory -> SAM3_ENOMEM.
+ * Nothing here aborts; the message of the last failure is kept per thread
+ * (sam3_hip_last_error) and printed to stderr unless SAM3_HIP_QUIET is set.
+ */
+#include "sam3_hip.h"
+#include "sam3_hip_internal.h"
+#include "s3k.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static _Thread_local char g_last_error[320];
+
+void s3h_error(const char *fmt, ...)
+{
+	va_list ap;
+	va_start(ap, fmt);
+	vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+	va_end(ap);
+	if (!getenv("SAM3_HIP_QUIET"))
+		fprintf(stderr, "[sam3_hip] %s\n", g_last_error);
+}
+
+const char *sam3_hip_last_error(void)
+{
+	return g_last_error;
+}
+
+enum sam3_error s3h_hip(int e, const char *what)
+{
+	if (e == hipSuccess)
+		return SAM3_OK;
+	s3h_error("%s: %s", what, hipGetErrorString((hipError_t)e));
+	return e == hipErrorOutOfMemory ? SAM3_ENOMEM : SAM3_EBACKEND;
+}
+
+/* ------------------------------------------------------------------ */
+/* dtype helpers                                                        */
+/* ------------------------------------------------------------------ */
+size_t s3h_dtype_size(int dt)
+{
+	switch (dt) {
+	case SAM3_DTYPE_F32:
+	case SAM3_DTYPE_I32:
+		return 4;
+	case SAM3_DTYPE_F16:
+	case SAM3_DTYPE_BF16:
+		return 2;
+	case SAM3_DTYPE_I8:
+		return 1;
+	default:
+		return 0; /* Q8_0 has no element size (src/core/tensor.c:40) */
+	}
+}
+
+long long s3h_nelems(const struct sam3_tensor *t)
+{
+	long long n = 1;
+	for (int i = 0; i < t->n_dims; i++)
+		n *= t->dims[i];
+	return n;
+}
+
+size_t s3h_tensor_bytes(const struct sam3_tensor *t)
+{
+	long long n = s3h_nelems(t);
+	if (t->dtype == SAM3_DTYPE_Q8_0)
+		return (size_t)((n + 31) / 32) * 36;
+	return (size_t)n * s3h_dtype_size(t->dtype);
+}
+
+static int is_float_dtype(int dt)
+{
+	return dt == SAM3_DTYPE_F32 || dt == SAM3_DTYPE_F16 || dt == SAM3_DTYPE_BF16;
+}
+
+/* ------------------------------------------------------------------ */
+/* Plain-pointer matmul                                                 */
+/* ------------------------------------------------------------------ */
+static enum sam3_error check_kinds(int a_dt, int b_dt, int c_dt)
+{
+	if (b_dt == SAM3_DTYPE_Q8_0) {
+		if (!is_float_dtype(a_dt) || !is_float_dtype(c_dt)) {
+			s3h_error("matmul: Q8_0 needs F32/F16/BF16 activations and output "
+				  "(a=%d c=%d)", a_dt, c_dt);
+			return SAM3_EDTYPE;
+		}
+		return SAM3_OK;
+	}
+	if (!is_float_dtype(a_dt) || a_dt != b_dt ||
+	    (c_dt != a_dt && c_dt != SAM3_DTYPE_F32)) {
+		s3h_error("matmul: unsupported dtypes a=%d b=%d c=%d", a_dt, b_dt, c_dt);
+		return SAM3_EDTYPE;
+	}
+	return SAM3_OK;
+}
+
+static void fill_gemm(struct s3k_gemm *g, int a_dt, const void *a, int b_dt, const void *b,
+		      int c_dt, void *c, int M, int N, int K, const void *bias, int flags)
+{
+	memset(g, 0, sizeof(*g));
+	g->a = a;
+	g->b = b;
+	g->c = c;
+	g->bias = bias;
+	g->M = M;
+	g->N = N;
+	g->K = K;
+	g->lda = K;
+	g->ldb = (flags & SAM3_HIP_B_NT) ? K : N;
+	g->ldc = N;
+	g->batch = 1;
+	g->a_kind = a_dt;
+	g->b_kind = b_dt;
+	g->c_kind = c_dt;
+	g->flags = flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT);
+}
+
+/* Q8 layouts the tiled kernels cannot stream (blocks over the [K,N] flat
+ * index, or [N,K] rows that split blocks): unpack to f16 [N,K] in
+ * stream-ordered scratch and run the f16 NT GEMM on it. */
+static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
+{
+	const int nt = g->flags & S3K_B_NT;
+	const size_t bytes = (size_t)g->N * g->K * 2;
+	void *w16 = NULL;
+	enum sam3_error err;
+
+	err = s3h_hip(hipMallocAsync(&w16, bytes, (hipStream_t)stream), "matmul_q8 scratch");
+	if (err != SAM3_OK)
+		return err;
+	int e = nt ? s3k_q8_nk_to_f16_nk(g->b, w16, g->K, g->N, stream)
+		   : s3k_q8_kn_to_f16_nk(g->b, w16, g->K, g->N, stream);
+	err = s3h_hip(e, "matmul_q8 unpack");
+	if (err == SAM3_OK) {
+		struct s3k_gemm h = *g;
+		h.b = w16;
+		h.b_kind = S3K_F16;
+		h.ldb = g->K;
+		h.flags |= S3K_B_NT;
+		if (h.a_kind == S3K_F16 || s3k_gemm_path(&h) == S3K_PATH_MFMA)
+			err = s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8 gemm");
+		else
+			err = s3h_hip(s3k_gemm_launch_path(g, S3K_PATH_GENERIC, stream),
+				      "matmul_q8 generic");
+	}
+	enum sam3_error ferr = s3h_hip(hipFreeAsync(w16, (hipStream_t)stream),
+				       "matmul_q8 scratch free");
+	return err != SAM3_OK ? err : ferr;
+}
+
+static int q8_needs_unpack(const struct s3k_gemm *g)
+{
+	if (g->b_kind != S3K_Q8)
+		return 0;
+	if ((g->flags & S3K_B_NT) && g->K % 32 == 0)
+		return 0;
+	/* large enough for a GEMM to pay for the unpack pass */
+	return g->K % 8 == 0 && g->M >= 64 && (long long)g->M * g->N * g->K >= (1LL << 21);
+}
+
+static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, const void *b,
+				   int c_dt, void *c, int M, int N, int K, const void *bias,
+				   int flags, void *stream)
+{
+	enum sam3_error err;
+
+	if (M < 0 || N < 0 || K < 0) {
+		s3h_error("matmul: negative size M=%d N=%d K=%d", M, N, K);
+		return SAM3_EINVAL;
+	}
+	if (M == 0 || N == 0)
+		return SAM3_OK;
+	if (!a || !b || !c || ((flags & SAM3_HIP_BIAS) && !bias)) {
+		s3h_error("matmul: NULL pointer");
+		return SAM3_EINVAL;
+	}
+	err = check_kinds(a_dt, b_dt, c_dt);
+	if (err != SAM3_OK)
+		return err;
+
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, c_dt, c, M, N, K, bias, flags);
+
+	if (path == 0) {
+		if (q8_needs_unpack(&g))
+			return q8_unpacked(&g, stream);
+		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
+	}
+	if (path < S3K_PATH_MFMA || path > S3K_PATH_GENERIC) {
+		s3h_error("matmul: unknown path %d", path);
+		return SAM3_EINVAL;
+	}
+	if (path == S3K_PATH_MFMA && q8_needs_unpack(&g))
+		return q8_unpacked(&g, stream);
+	int e = s3k_gemm_launch_path(&g, path, stream);
+	if (e == hipErrorInvalidValue) {
+		s3h_error("matmul: path %d cannot run M=%d N=%d K=%d", path, M, N, K);
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(e, "matmul");
+}
+
+enum sam3_error sam3_hip_matmul(int a_dtype, const void *a, int b_dtype, const void *b,
+				int c_dtype, void *c, int M, int N, int K,
+				const void *bias, int flags, void *stream)
+{
+	return matmul_impl(0, a_dtype, a, b_dtype, b, c_dtype, c, M, N, K, bias, flags, stream);
+}
+
+enum sam3_error sam3_hip_matmul_on_path(int path, int a_dtype, const void *a,
+					int b_dtype, const void *b, int c_dtype, void *c,
+					int M, int N, int K, const void *bias, int flags,
+					void *stream)
+{
+	return matmul_impl(path, a_dtype, a, b_dtype, b, c_dtype, c, M, N, K, bias, flags, stream);
+}
+
+int sam3_hip_matmul_path(int a_dtype, int b_dtype, int c_dtype, int M, int N, int K, int flags)
+{
+	static const char dummy[64] __attribute__((aligned(64)));
+	if (check_kinds(a_dtype, b_dtype, c_dtype) != SAM3_OK || M <= 0 || N <= 0 || K < 0)
+		return S3K_PATH_NONE;
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dtype, dummy, b_dtype, dummy, c_dtype, (void *)dummy, M, N, K,
+		  dummy, flags);
+	if (q8_needs_unpack(&g))
+		return S3K_PATH_MFMA;
+	return s3k_gemm_path(&g);
+}
+
+enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b, void *c,
+					int batch, int M, int N, int K,
+					long long stride_a, long long stride_b,
+					long long stride_c, int flags, void *stream)
+{
+	if (batch < 0 || M < 0 || N < 0 || K < 0) {
+		s3h_error("matmul_batched: negative size");
+		return SAM3_EINVAL;
+	}
+	if (batch == 0 || M == 0 || N == 0)
+		return SAM3_OK;
+	if (!a || !b || !c) {
+		s3h_error("matmul_batched: NULL pointer");
+		return SAM3_EINVAL;
+	}
+	if (!is_float_dtype(dtype)) {
+		s3h_error("matmul_batched: unsupported dtype %d", dtype);
+		return SAM3_EDTYPE;
+	}
+	if (flags & SAM3_HIP_BIAS) {
+		s3h_error("matmul_batched: bias is not supported on batches");
+		return SAM3_EINVAL;
+	}
+	struct s3k_gemm g;
+	fill_gemm(&g, dtype, a, dtype, b, dtype, c, M, N, K, NULL, flags);
+	g.batch = batch;
+	g.stride_a = stride_a;
+	g.stride_b = stride_b;
+	g.stride_c = stride_c;
+	return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_batched");
+}
+
+/* ------------------------------------------------------------------ */
+/* Node-level kernels                                                   */
+/* ------------------------------------------------------------------ */
+
+/* Shapes as the reference reads them: M = dims[n-2] (1 for 1-D), K =
+ * dims[n-1]; B: K = dims[n-2], N = dims[n-1] (cpu_matmul_q8.c:187-213). */
+static enum sam3_error node_shape(const struct sam3_node *node, const char *who,
+				  int a_dt, int b_dt, int *M, int *N, int *K)
+{
+	if (!node || node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] ||
+	    !node->output) {
+		s3h_error("%s: NULL tensor", who);
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *a = node->inputs[0], *b = node->inputs[1];
+	const struct sam3_tensor *c = node->output;
+	if ((int)a->dtype != a_dt || (int)b->dtype != b_dt) {
+		s3h_error("%s: unsupported dtype (a=%d b=%d)", who, a->dtype, b->dtype);
+		return SAM3_EINVAL;
+	}
+	if (b_dt == SAM3_DTYPE_Q8_0 && c->dtype != SAM3_DTYPE_F32) {
+		s3h_error("%s: expected F32 x Q8_0 -> F32", who);
+		return SAM3_EINVAL;
+	}
+	if (a->n_dims < 1 || b->n_dims < 1) {
+		s3h_error("%s: need at least 1D tensors", who);
+		return SAM3_EINVAL;
+	}
+	int ka, kb;
+	if (a->n_dims == 1) {
+		*M = 1;
+		ka = a->dims[0];
+	} else {
+		*M = a->dims[a->n_dims - 2];
+		ka = a->dims[a->n_dims - 1];
+	}
+	if (b->n_dims == 1) {
+		kb = b->dims[0];
+		*N = 1;
+	} else {
+		kb = b->dims[b->n_dims - 2];
+		*N = b->dims[b->n_dims - 1];
+	}
+	if (ka != kb) {
+		s3h_error("%s: K mismatch %d != %d", who, ka, kb);
+		return SAM3_EINVAL;
+	}
+	*K = ka;
+	if (s3h_nelems(c) != (long long)(*M) * (*N)) {
+		s3h_error("%s: output size mismatch %lld != %lld", who, s3h_nelems(c),
+			  (long long)(*M) * (*N));
+		return SAM3_EINVAL;
+	}
+	return SAM3_OK;
+}
+
+static enum sam3_error node_matmul(const struct sam3_node *node, const char *who, int dt_a,
+				   int dt_b, int dt_c, void *stream)
+{
+	int M, N, K;
+	enum sam3_error err = node_shape(node, who, dt_a, dt_b, &M, &N, &K);
+	if (err != SAM3_OK)
+		return err;
+	return sam3_hip_matmul(dt_a, node->inputs[0]->data, dt_b, node->inputs[1]->data, dt_c,
+			       node->output->data, M, N, K, NULL, 0, stream);
+}
+
+enum sam3_error sam3_hip_kernel_matmul(const struct sam3_node *node, void *stream)
+{
+	return node_matmul(node, "matmul", SAM3_DTYPE_F32, SAM3_DTYPE_F32, SAM3_DTYPE_F32, stream);
+}
+
+enum sam3_error sam3_hip_kernel_matmul_f16(const struct sam3_node *node, void *stream)
+{
+	return node_matmul(node, "matmul_f16", SAM3_DTYPE_F16, SAM3_DTYPE_F16, SAM3_DTYPE_F16,
+			   stream);
+}
+
+enum sam3_error sam3_hip_kernel_matmul_bf16(const struct sam3_node *node, void *stream)
+{
+	return node_matmul(node, "matmul_bf16", SAM3_DTYPE_BF16, SAM3_DTYPE_BF16,
+			   SAM3_DTYPE_BF16, stream);
+}
+
+enum sam3_error sam3_hip_kernel_matmul_q8(const struct sam3_node *node, void *stream)
+{
+	return node_matmul(node, "matmul_q8", SAM3_DTYPE_F32, SAM3_DTYPE_Q8_0, SAM3_DTYPE_F32,
+			   stream);
+}
+
+/* ADD: same shape, or y broadcast over the last dim of x (a bias). */
+enum sam3_error s3h_add(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] || !node->output) {
+		s3h_error("add: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *x = node->inputs[0], *y = node->inputs[1];
+	const long long nx = s3h_nelems(x), ny = s3h_nelems(y);
+	const int last = x->n_dims >= 1 ? x->dims[x->n_dims - 1] : 1;
+	if (s3h_nelems(node->output) != nx) {
+		s3h_error("add: output size mismatch");
+		return SAM3_EINVAL;
+	}
+	if (ny == nx)
+		return s3h_hip(s3k_add_same(x->dtype, x->data, y->data, node->output->data, nx,
+					    stream), "add");
+	if (ny == last && last > 0)
+		return s3h_hip(s3k_bias_add(x->dtype, x->data, y->data, node->output->data,
+					    nx / last, last, stream), "add");
+	s3h_error("add: broadcast of %lld over %lld elements is not supported", ny, nx);
+	return SAM3_EINVAL;
+}
+
+enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("gelu: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const long long n = s3h_nelems(node->inputs[0]);
+	if (s3h_nelems(node->output) != n) {
+		s3h_error("gelu: output size mismatch");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_gelu(node->inputs[0]->dtype, node->inputs[0]->data,
+				node->output->data, n, stream), "gelu");
+}
+
+/* TRANSPOSE of the last two dims (params all zero, or the permutation
+ * that swaps the last two axes; cpu_transpose.c:330-348). Other
+ * permutations are not run here. */
+int s3h_transpose_is_swap(const struct sam3_node *node)
+{
+	const struct sam3_tensor *in = node->inputs[0];
+	const int nd = in->n_dims;
+	if (nd < 2 || nd > SAM3_MAX_DIMS)
+		return 0;
+	int zero = 1;
+	for (int i = 0; i < nd; i++)
+		if (node->params[i] != 0)
+			zero = 0;
+	if (zero)
+		return 1;
+	for (int i = 0; i < nd - 2; i++)
+		if (node->params[i] != i)
+			return 0;
+	return node->params[nd - 2] == nd - 1 && node->params[nd - 1] == nd - 2;
+}
+
+enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("transpose: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *in = node->inputs[0];
+	if (!s3h_transpose_is_swap(node) || s3h_dtype_size(in->dtype) == 0) {
+		s3h_error("transpose: only last-two-dims swaps of element dtypes run on HIP");
+		return SAM3_EDTYPE;
+	}
+	const int rows = in->dims[in->n_dims - 2], cols = in->dims[in->n_dims - 1];
+	const long long batch = rows && cols ? s3h_nelems(in) / ((long long)rows * cols) : 0;
+	if (s3h_nelems(node->output) != s3h_nelems(in)) {
+		s3h_error("transpose: output size mismatch");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_transpose2d((int)s3h_dtype_size(in->dtype), in->data,
+				       node->output->data, (int)batch, rows, cols, stream),
+		       "transpose");
+}
+
+enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream)
+{
+	if (!node) {
+		s3h_error("hip_dispatch: NULL node");
+		return SAM3_EINVAL;
+	}
+	if (node->op == SAM3_OP_NONE)
+		return SAM3_OK;
+	if (node->n_inputs < 1 || !node->inputs[0]) {
+		s3h_error("hip_dispatch: node op=%d has no inputs", node->op);
+		return SAM3_EINVAL;
+	}
+	int dtype = node->inputs[0]->dtype;
+	const int mixed_q8 = node->op == SAM3_OP_MATMUL && node->n_inputs >= 2 &&
+			     node->inputs[1] && node->inputs[1]->dtype == SAM3_DTYPE_Q8_0 &&
+			     dtype == SAM3_DTYPE_F32;
+	if (mixed_q8) {
+		dtype = SAM3_DTYPE_Q8_0;
+	} else {
+		for (int i = 1; i < node->n_inputs; i++) {
+			if (node->inputs[i] && (int)node->inputs[i]->dtype != dtype) {
+				s3h_error("hip_dispatch: dtype mismatch input[0]=%d input[%d]=%d",
+					  dtype, i, node->inputs[i]->dtype);
+				return SAM3_EDTYPE;
+			}
+		}
+	}
+	if ((unsigned)node->op >= (unsigned)SAM3_OP_COUNT ||
+	    (unsigned)dtype >= (unsigned)SAM3_DTYPE_COUNT) {
+		s3h_error("hip_dispatch: out-of-range op=%d dtype=%d", node->op, dtype);
+		return SAM3_EDTYPE;
+	}
+	switch (node->op) {
+	case SAM3_OP_MATMUL:
+		switch (dtype) {
+		case SAM3_DTYPE_F32:  return sam3_hip_kernel_matmul(node, stream);
+		case SAM3_DTYPE_F16:  return sam3_hip_kernel_matmul_f16(node, stream);
+		case SAM3_DTYPE_BF16: return sam3_hip_kernel_matmul_bf16(node, stream);
+		case SAM3_DTYPE_Q8_0: return sam3_hip_kernel_matmul_q8(node, stream);
+		default: break;
+		}
+		break;
+	case SAM3_OP_ADD:
+		if (is_float_dtype(dtype))
+			return s3h_add(node, stream);
+		break;
+	case SAM3_OP_GELU:
+		if (is_float_dtype(dtype))
+			return s3h_gelu(node, stream);
+		break;
+	case SAM3_OP_TRANSPOSE:
+		if (s3h_dtype_size(dtype) && s3h_transpose_is_swap(node))
+			return s3h_transpose(node, stream);
+		break;
+	default:
+		break;
+	}
+	s3h_error("hip_dispatch: no kernel for op=%d dtype=%d", node->op, dtype);
+	return SAM3_EDTYPE;
+}
+
+/* ------------------------------------------------------------------ */
+/* Device helpers                                                       */
+/* ------------------------------------------------------------------ */
+int sam3_hip_device_count(void)
+{
+	int n = 0;
+	if (hipGetDeviceCount(&n) != hipSuccess)
+		return 0;
+	return n;
+}
+
+enum sam3_error sam3_hip_set_device(int device)
+{
+	return s3h_hip(hipSetDevice(device), "set_device");
+}
+
+enum sam3_error sam3_hip_malloc(void **ptr, size_t nbytes)
+{
+	if (!ptr) {
+		s3h_error("malloc: NULL out pointer");
+		return SAM3_EINVAL;
+	}
+	*ptr = NULL;
+	return s3h_hip(hipMalloc(ptr, nbytes ? nbytes : 1), "malloc");
+}
+
+enum sam3_error sam3_hip_free(void *ptr)
+{
+	return s3h_hip(hipFree(ptr), "free");
+}
+
+enum sam3_error sam3_hip_memcpy_h2d(void *dst, const void *src, size_t nbytes)
+{
+	return s3h_hip(hipMemcpy(dst, src, nbytes, hipMemcpyHostToDevice), "memcpy_h2d");
+}
+
+enum sam3_error sam3_hip_memcpy_d2h(void *dst, const void *src, size_t nbytes)
+{
+	return s3h_hip(hipMemcpy(dst, src, nbytes, hipMemcpyDeviceToHost), "memcpy_d2h");
+}
+
+enum sam3_error sam3_hip_memcpy_d2d(void *dst, const void *src, size_t nbytes)
+{
+	return s3h_hip(hipMemcpy(dst, src, nbytes, hipMemcpyDeviceToDevice), "memcpy_d2d");
+}
+
+enum sam3_error sam3_hip_synchronize(void)
+{
+	return s3h_hip(hipDeviceSynchronize(), "synchronize");
+}
+
+enum sam3_error sam3_hip_stream_create(void **stream)
+{
+	if (!stream) {
+		s3h_error("stream_create: NULL out pointer");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(hipStreamCreateWithFlags((hipStream_t *)stream, hipStreamNonBlocking),
+		       "stream_create");
+}
+
+enum sam3_error sam3_hip_stream_destroy(void *stream)
+{
+	return s3h_hip(hipStreamDestroy((hipStream_t)stream), "stream_destroy");
+}
+
+enum sam3_error sam3_hip_stream_synchronize(void *stream)
+{
+	return s3h_hip(hipStreamSynchronize((hipStream_t)stream), "stream_synchronize");
+}
+
+enum sam3_error sam3_hip_event_create(void **event)
+{
+	if (!event) {
+		s3h_error("event_create: NULL out pointer");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(hipEventCreate((hipEvent_t *)event), "event_create");
+}
+
+enum sam3_error sam3_hip_event_destroy(void *event)
+{
+	return s3h_hip(hipEventDestroy((hipEvent_t)event), "event_destroy");
+}
+
+enum sam3_error sam3_hip_event_record(void *event, void *stream)
+{
+	return s3h_hip(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "event_record");
+}
+
+enum sam3_error sam3_hip_event_elapsed_ms(float *ms, void *start, void *stop)
+{
+	if (!ms) {
+		s3h_error("event_elapsed: NULL out pointer");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop),
+		       "event_elapsed");
+}
+
+const char *sam3_hip_device_arch(int device)
+{
+	static _Thread_local char arch[64];
+	hipDeviceProp_t prop;
+	arch[0] = 0;
+	if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+		strncpy(arch, prop.gcnArchName, sizeof(arch) - 1);
+		arch[sizeof(arch) - 1] = 0;
+	}
+	return arch;
+}

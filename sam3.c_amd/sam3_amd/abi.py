@@ -104,3 +104,13 @@ def make_node(op, inputs, output, params=(0, 0, 0, 0)):
     for i, p in enumerate(params):
         n.params[i] = p
     return n
+
+
+class BackendOps(C.Structure):
+    """struct sam3_backend_ops (src/backend/backend.h:31-56)."""
+    _fields_ = [("init", C.CFUNCTYPE(C.c_int, C.c_void_p)),
+                ("free", C.CFUNCTYPE(None, C.c_void_p)),
+                ("alloc_tensor", C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Tensor))),
+                ("graph_eval", C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Graph))),
+                ("arena_reset", C.CFUNCTYPE(None, C.c_void_p)),
+                ("cache_invalidate", C.CFUNCTYPE(None, C.c_void_p, C.c_void_p, C.c_size_t))]

@@ -1,0 +1,260 @@
+"""ctypes binding of libsam3hip.so, the MI355X matmul backend (C ABI in
+include/sam3_hip.h).
+
+This plays the part of sam3.c's own Python binding (bindings/python/sam3/
+_lib.py loads libsam3 through cffi): it loads the shared library built
+in-tree by ``make -C sam3.c_amd/csrc`` and declares every exported entry
+point. There is no fallback: if the library is missing or cannot be
+loaded, ``load()`` raises, so nothing silently runs elsewhere.
+"""
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from . import abi
+
+LIB_PATH = Path(__file__).resolve().parent / "libsam3hip.so"
+
+_vp, _i, _ll, _sz = C.c_void_p, C.c_int, C.c_longlong, C.c_size_t
+_P = C.POINTER
+
+# name -> (restype, argtypes); mirrors include/sam3_hip.h
+SIGNATURES = {
+    "sam3_hip_backend_ops": (_vp, []),
+    "sam3_hip_backend_create": (_vp, [_i]),
+    "sam3_hip_backend_destroy": (None, [_vp]),
+    "sam3_hip_backend_set_host_dispatch": (None, [_vp, _vp, _vp]),
+    "sam3_hip_backend_stream": (_vp, [_vp]),
+    "sam3_hip_backend_last_stats": (None, [_vp, _vp]),
+    "sam3_hip_kernel_matmul": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_matmul_f16": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_matmul_bf16": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_matmul_q8": (_i, [_vp, _vp]),
+    "sam3_hip_dispatch_node": (_i, [_vp, _vp]),
+    "sam3_hip_matmul": (_i, [_i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),
+    "sam3_hip_matmul_path": (_i, [_i, _i, _i, _i, _i, _i, _i]),
+    "sam3_hip_matmul_on_path": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "sam3_hip_device_count": (_i, []),
+    "sam3_hip_set_device": (_i, [_i]),
+    "sam3_hip_malloc": (_i, [_P(_vp), _sz]),
+    "sam3_hip_free": (_i, [_vp]),
+    "sam3_hip_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "sam3_hip_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "sam3_hip_memcpy_d2d": (_i, [_vp, _vp, _sz]),
+    "sam3_hip_synchronize": (_i, []),
+    "sam3_hip_stream_create": (_i, [_P(_vp)]),
+    "sam3_hip_stream_destroy": (_i, [_vp]),
+    "sam3_hip_stream_synchronize": (_i, [_vp]),
+    "sam3_hip_event_create": (_i, [_P(_vp)]),
+    "sam3_hip_event_destroy": (_i, [_vp]),
+    "sam3_hip_event_record": (_i, [_vp, _vp]),
+    "sam3_hip_event_elapsed_ms": (_i, [_P(C.c_float), _vp, _vp]),
+    "sam3_hip_device_arch": (C.c_char_p, [_i]),
+    "sam3_hip_last_error": (C.c_char_p, []),
+}
+
+# kernel paths (sam3_hip_matmul_path)
+PATH_NONE, PATH_MFMA, PATH_SKINNY, PATH_GENERIC = 0, 1, 2, 3
+BIAS, GELU, B_NT = 1, 2, 4
+
+
+class EvalStats(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("gpu_nodes", "fused_nodes", "host_nodes",
+                                       "uploads", "cache_hits", "downloads")]
+
+
+class HipError(RuntimeError):
+    def __init__(self, code, what, msg):
+        super().__init__(f"{what} failed: {abi.ERROR_NAMES.get(code, code)} ({msg})")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Load libsam3hip.so once and declare its entry points. Raises if the
+    library is absent (build it with `make -C sam3.c_amd/csrc`)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not Path(path).exists():
+        raise FileNotFoundError(f"{path} not built: run `make -C sam3.c_amd/csrc`")
+    lib = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc, what):
+    if rc != abi.OK:
+        msg = load().sam3_hip_last_error().decode(errors="replace")
+        raise HipError(rc, what, msg)
+
+
+# ---------------------------------------------------------------- memory
+class DeviceBuffer:
+    """A device allocation (hipMalloc) with numpy upload/download."""
+
+    def __init__(self, nbytes):
+        self.lib = load()
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(self.lib.sam3_hip_malloc(C.byref(p), self.nbytes), "malloc")
+        self.ptr = p.value
+
+    @classmethod
+    def of(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(max(arr.nbytes, 1))
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(self.lib.sam3_hip_memcpy_h2d(self.ptr, arr.ctypes.data, arr.nbytes), "memcpy_h2d")
+
+    def download(self, dtype, shape):
+        out = np.empty(shape, dtype=dtype)
+        check(self.lib.sam3_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "memcpy_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            check(self.lib.sam3_hip_free(self.ptr), "free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize():
+    check(load().sam3_hip_synchronize(), "synchronize")
+
+
+def device_count():
+    return load().sam3_hip_device_count()
+
+
+class Event:
+    def __init__(self):
+        self.lib = load()
+        p = C.c_void_p()
+        check(self.lib.sam3_hip_event_create(C.byref(p)), "event_create")
+        self.ptr = p.value
+
+    def record(self, stream=None):
+        check(self.lib.sam3_hip_event_record(self.ptr, stream), "event_record")
+
+    def elapsed_ms(self, end):
+        ms = C.c_float()
+        check(self.lib.sam3_hip_event_elapsed_ms(C.byref(ms), self.ptr, end.ptr), "event_elapsed")
+        return ms.value
+
+    def __del__(self):
+        try:
+            self.lib.sam3_hip_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+# --------------------------------------------------------------- matmul
+def matmul_dev(a_dtype, a_ptr, b_dtype, b_ptr, c_dtype, c_ptr, M, N, K, bias_ptr=None,
+               flags=0, stream=None, path=0):
+    lib = load()
+    if path:
+        rc = lib.sam3_hip_matmul_on_path(path, a_dtype, a_ptr, b_dtype, b_ptr, c_dtype, c_ptr,
+                                         M, N, K, bias_ptr, flags, stream)
+    else:
+        rc = lib.sam3_hip_matmul(a_dtype, a_ptr, b_dtype, b_ptr, c_dtype, c_ptr, M, N, K,
+                                 bias_ptr, flags, stream)
+    check(rc, "sam3_hip_matmul")
+
+
+_NP = {abi.F32: np.float32, abi.F16: np.uint16, abi.BF16: np.uint16}
+
+
+def matmul(a, a_dtype, b, b_dtype, c_dtype, M, N, K, bias=None, flags=0, path=0):
+    """Host arrays in, host array out (uploads, runs, downloads)."""
+    da, db = DeviceBuffer.of(a), DeviceBuffer.of(b)
+    dc = DeviceBuffer(M * N * (4 if c_dtype == abi.F32 else 2))
+    dbias = DeviceBuffer.of(bias) if bias is not None else None
+    matmul_dev(a_dtype, da.ptr, b_dtype, db.ptr, c_dtype, dc.ptr, M, N, K,
+               dbias.ptr if dbias else None, flags, None, path)
+    synchronize()
+    return dc.download(_NP[c_dtype], (M, N))
+
+
+def matmul_path(a_dtype, b_dtype, c_dtype, M, N, K, flags=0):
+    return load().sam3_hip_matmul_path(a_dtype, b_dtype, c_dtype, M, N, K, flags)
+
+
+def batched(dtype, a, b, batch, M, N, K, b_nt):
+    lib = load()
+    es = 4 if dtype == abi.F32 else 2
+    da, db = DeviceBuffer.of(a), DeviceBuffer.of(b)
+    dc = DeviceBuffer(batch * M * N * es)
+    check(lib.sam3_hip_matmul_batched(dtype, da.ptr, db.ptr, dc.ptr, batch, M, N, K,
+                                      M * K, K * N, M * N, B_NT if b_nt else 0, None),
+          "matmul_batched")
+    synchronize()
+    return dc.download(_NP[dtype], (batch, M, N))
+
+
+# --------------------------------------------------------------- backend
+HOST_DISPATCH_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p)
+
+
+class Backend:
+    """sam3_hip_backend_create / graph_eval through the ops vtable."""
+
+    def __init__(self, device=0):
+        self.lib = load()
+        self.be = self.lib.sam3_hip_backend_create(device)
+        if not self.be:
+            raise HipError(abi.EBACKEND, "sam3_hip_backend_create",
+                           self.lib.sam3_hip_last_error().decode(errors="replace"))
+        ops = C.cast(self.lib.sam3_hip_backend_ops(), C.POINTER(abi.BackendOps)).contents
+        self.ops = ops
+        self._host_fn = None
+
+    def alloc_tensor(self, t):
+        return self.ops.alloc_tensor(self.be, C.byref(t))
+
+    def graph_eval(self, g):
+        return self.ops.graph_eval(self.be, C.byref(g))
+
+    def arena_reset(self):
+        self.ops.arena_reset(self.be)
+
+    def cache_invalidate(self, start, length):
+        self.ops.cache_invalidate(self.be, start, length)
+
+    def set_host_dispatch(self, fn):
+        self._host_fn = HOST_DISPATCH_FN(fn) if fn else None
+        self.lib.sam3_hip_backend_set_host_dispatch(self.be, self._host_fn, None)
+
+    def stats(self):
+        s = EvalStats()
+        self.lib.sam3_hip_backend_last_stats(self.be, C.byref(s))
+        return s
+
+    def close(self):
+        if self.be:
+            self.lib.sam3_hip_backend_destroy(self.be)
+            self.be = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,161 @@
+"""CPU-side checks of the C ABI (no GPU needed): the library loads, exports
+every entry point include/*.h declares, the mirrored structs have sam3.c's
+sizes, kernel-path selection, and the argument/dtype error behaviour that
+mirrors the reference CPU path (all of these return before any device
+call)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from sam3_amd import abi, hip
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(autouse=True)
+def quiet(monkeypatch):
+    monkeypatch.setenv("SAM3_HIP_QUIET", "1")
+
+
+def declared_entry_points():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(sam3_hip_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_exports_every_declared_symbol():
+    lib = hip.load()
+    names = declared_entry_points()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding declares each of them
+    assert set(names) <= set(hip.SIGNATURES), set(names) - set(hip.SIGNATURES)
+
+
+def test_struct_layouts_match_reference_sizes():
+    # x86-64 sizes of sam3.c's structs (src/core/tensor.h:24-49, graph.h:77-90)
+    assert C.sizeof(abi.Tensor) == 64
+    assert C.sizeof(abi.Node) == 104
+    assert C.sizeof(abi.Graph) == 104 * 16384 + 8
+    assert C.sizeof(abi.BackendOps) == 6 * 8
+
+
+@pytest.mark.parametrize("args,path", [
+    ((abi.BF16, abi.BF16, abi.BF16, 5184, 4096, 1024, hip.B_NT), hip.PATH_MFMA),
+    ((abi.BF16, abi.BF16, abi.BF16, 5184, 4096, 1024, 0), hip.PATH_MFMA),
+    ((abi.F16, abi.F16, abi.F16, 5184, 1024, 4096, hip.B_NT), hip.PATH_MFMA),
+    ((abi.F32, abi.Q8_0, abi.F32, 5184, 1024, 1024, hip.B_NT), hip.PATH_MFMA),
+    ((abi.BF16, abi.Q8_0, abi.F32, 5184, 3072, 1024, hip.B_NT), hip.PATH_MFMA),
+    ((abi.F32, abi.Q8_0, abi.F32, 1, 1024, 4096, hip.B_NT), hip.PATH_SKINNY),
+    ((abi.F32, abi.Q8_0, abi.F32, 77, 256, 256, hip.B_NT), hip.PATH_SKINNY),
+    ((abi.F32, abi.Q8_0, abi.F32, 4, 4, 64, 0), hip.PATH_GENERIC),
+    ((abi.F32, abi.Q8_0, abi.F32, 512, 512, 512, 0), hip.PATH_MFMA),   # unpacked to f16
+    ((abi.F32, abi.F32, abi.F32, 7, 5, 13, 0), hip.PATH_GENERIC),
+    ((abi.F16, abi.F16, abi.F16, 19, 23, 70, 0), hip.PATH_GENERIC),
+    ((abi.BF16, abi.Q8_0, abi.BF16, 8, 8, 8, 0), hip.PATH_GENERIC),
+    ((abi.F32, abi.BF16, abi.F32, 8, 8, 8, 0), hip.PATH_NONE),      # mixed dense dtypes
+    ((abi.I32, abi.I32, abi.I32, 8, 8, 8, 0), hip.PATH_NONE),
+])
+def test_path_selection(args, path):
+    assert hip.matmul_path(*args) == path
+
+
+def test_plain_entry_argument_errors():
+    lib = hip.load()
+    ok = 16  # any non-NULL address: these calls fail before touching it
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.F32, ok, abi.F32, ok, -1, 4, 4, None, 0, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.F32, ok, abi.F32, ok, 0, 4, 4, None, 0, None) == abi.OK
+    assert lib.sam3_hip_matmul(abi.F32, None, abi.F32, ok, abi.F32, ok, 4, 4, 4, None, 0, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.F32, ok, abi.F32, ok, 4, 4, 4, None, hip.BIAS, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.BF16, ok, abi.F32, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul(abi.I8, ok, abi.I8, ok, abi.I8, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul(abi.BF16, ok, abi.BF16, ok, abi.F16, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.Q8_0, ok, abi.Q8_0, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul_on_path(9, abi.F32, ok, abi.F32, ok, abi.F32, ok, 4, 4, 4, None, 0, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul_batched(abi.BF16, ok, ok, ok, 2, 4, 4, 4, 16, 16, 16, hip.BIAS, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul_batched(abi.I32, ok, ok, ok, 2, 4, 4, 4, 16, 16, 16, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul_batched(abi.BF16, ok, ok, ok, 0, 4, 4, 4, 16, 16, 16, 0, None) == abi.OK
+    assert lib.sam3_hip_matmul(abi.F32, ok, abi.BF16, ok, abi.F32, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
+    assert b"unsupported dtypes" in lib.sam3_hip_last_error()
+
+
+def _node(op, ins, out, params=(0, 0, 0, 0)):
+    return abi.make_node(op, ins, out, params)
+
+
+def _t(dtype, dims):
+    return abi.make_tensor(dtype, dims, 4096)  # fake data address: never touched
+
+
+def test_node_kernel_shape_and_dtype_errors():
+    """cpu_kernel_matmul*: NULL, wrong dtype, K mismatch and output size
+    mismatch are SAM3_EINVAL (cpu_matmul.c:178-229, cpu_matmul_q8.c:168-213)."""
+    lib = hip.load()
+    a, b, c = _t(abi.F32, [4, 8]), _t(abi.F32, [9, 3]), _t(abi.F32, [4, 3])
+    assert lib.sam3_hip_kernel_matmul(C.byref(_node(abi.OP_MATMUL, [a, b], c)), None) == abi.EINVAL
+    b = _t(abi.F32, [8, 3])
+    c_bad = _t(abi.F32, [4, 4])
+    assert lib.sam3_hip_kernel_matmul(C.byref(_node(abi.OP_MATMUL, [a, b], c_bad)), None) == abi.EINVAL
+    assert lib.sam3_hip_kernel_matmul_bf16(C.byref(_node(abi.OP_MATMUL, [a, b], c)), None) == abi.EINVAL
+    assert lib.sam3_hip_kernel_matmul_f16(C.byref(_node(abi.OP_MATMUL, [a, b], c)), None) == abi.EINVAL
+    q = _t(abi.Q8_0, [8, 3])
+    cb = _t(abi.BF16, [4, 3])
+    assert lib.sam3_hip_kernel_matmul_q8(C.byref(_node(abi.OP_MATMUL, [a, q], cb)), None) == abi.EINVAL
+    n1 = abi.Node()
+    n1.n_inputs = 2
+    assert lib.sam3_hip_kernel_matmul(C.byref(n1), None) == abi.EINVAL
+
+
+def test_dispatch_routing_errors():
+    """cpu_dispatch_node routing (cpu_dispatch.c:591-686): NONE is a no-op,
+    BF16 x Q8_0 and other mixed dtypes are SAM3_EDTYPE, an op without a
+    kernel is SAM3_EDTYPE, a node without inputs is SAM3_EINVAL."""
+    lib = hip.load()
+    d = lib.sam3_hip_dispatch_node
+    assert d(C.byref(abi.Node()), None) == abi.OK  # OP_NONE
+    none_in = abi.Node()
+    none_in.op = abi.OP_MATMUL
+    assert d(C.byref(none_in), None) == abi.EINVAL
+    ab, q, cb = _t(abi.BF16, [4, 32]), _t(abi.Q8_0, [32, 4]), _t(abi.BF16, [4, 4])
+    assert d(C.byref(_node(abi.OP_MATMUL, [ab, q], cb)), None) == abi.EDTYPE
+    a32, b16 = _t(abi.F32, [4, 8]), _t(abi.F16, [8, 4])
+    assert d(C.byref(_node(abi.OP_MATMUL, [a32, b16], _t(abi.F32, [4, 4]))), None) == abi.EDTYPE
+    x = _t(abi.F32, [4, 4])
+    assert d(C.byref(_node(abi.OP_SOFTMAX, [x], _t(abi.F32, [4, 4]))), None) == abi.EDTYPE
+    assert d(C.byref(_node(abi.OP_MATMUL, [_t(abi.I32, [2, 2]), _t(abi.I32, [2, 2])],
+                           _t(abi.I32, [2, 2]))), None) == abi.EDTYPE
+    # a transpose with a permutation other than a last-two-dims swap
+    t3 = _t(abi.F32, [2, 3, 4])
+    assert d(C.byref(_node(abi.OP_TRANSPOSE, [t3], _t(abi.F32, [3, 2, 4]), (1, 0, 2, 0))),
+             None) == abi.EDTYPE
+    # shape errors inside a routed matmul
+    assert d(C.byref(_node(abi.OP_MATMUL, [_t(abi.F32, [4, 8]), _t(abi.Q8_0, [9, 4])],
+                           _t(abi.F32, [4, 4]))), None) == abi.EINVAL
+
+
+def test_backend_create_without_device_fails_cleanly():
+    lib = hip.load()
+    if lib.sam3_hip_device_count() > 0:
+        pytest.skip("a device is present")
+    assert not lib.sam3_hip_backend_create(0)
+    assert b"device" in lib.sam3_hip_last_error()
+    ops = C.cast(lib.sam3_hip_backend_ops(), C.POINTER(abi.BackendOps)).contents
+    assert ops.graph_eval and ops.alloc_tensor and ops.cache_invalidate and ops.arena_reset
+
+
+def test_no_oracle_in_product_path():
+    """The product library neither links nor names the CPU oracle, and no
+    product source loads it."""
+    data = (ROOT / "sam3.c_amd" / "sam3_amd" / "libsam3hip.so").read_bytes()
+    assert b"oracle_" not in data and b"liboracle" not in data
+    for p in (ROOT / "sam3.c_amd").rglob("*"):
+        if p.suffix in (".py", ".c", ".h", ".hip"):
+            text = p.read_text()
+            assert "oracle_bind" not in text and "liboracle" not in text and \
+                "sam3_oracle" not in text, p

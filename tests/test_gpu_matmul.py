@@ -1,0 +1,383 @@
+"""GPU parity of the HIP matmul path against the CPU oracle, through the C ABI.
+
+Every case runs the HIP kernels on seeded inputs and compares with the
+oracle (oracle/sam3_oracle.c, itself pinned to the reference in
+tests/test_oracle.py) or with the reference's golden vectors:
+  - generic path: bit-exact with the reference (same per-element order);
+  - tiled MFMA / skinny paths: f32 outputs within 1e-3 (relative, with an
+    rms floor), bf16 within max(2e-2, 1 ulp), f16 within max(5e-3, 2 ulp).
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from gpu_util import (assert_bf16_close, assert_f16_close, assert_f32_close, oracle,
+                      ref_linear, ref_q8, require_gpu, bf16_to_f32)
+from sam3_amd import abi, hip, synth
+
+pytestmark = pytest.mark.gpu
+
+GOLD = np.load(Path(__file__).parent / "golden" / "matmul_golden.npz")
+MFMA, SKINNY, GENERIC = hip.PATH_MFMA, hip.PATH_SKINNY, hip.PATH_GENERIC
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    require_gpu()
+
+
+def bits32(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def rnd(seed, shape, std=1.0):
+    return synth.randn(seed, shape, std)
+
+
+def q8(w):
+    return oracle().q8_quantize(w)
+
+
+# ------------------------------------------------------------ known answers
+def test_known_answer_f32_all_paths():
+    """tests/test_cpu_kernels.c:474-500: exact [58,64;139,154]."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    for path in (0, GENERIC):
+        c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, 2, 2, 3, path=path)
+        assert c.tolist() == [[58, 64], [139, 154]]
+
+
+def test_identity_bf16_f16_mfma():
+    """tests/test_matmul_bf16.c:126-181: X @ I == X, on the tiled path."""
+    O = oracle()
+    n = 64
+    x = rnd(1, (n, n))
+    eye = np.eye(n, dtype=np.float32)
+    xb, ib = O.f32_to_bf16(x).reshape(n, n), O.f32_to_bf16(eye).reshape(n, n)
+    assert np.array_equal(hip.matmul(xb, abi.BF16, ib, abi.BF16, abi.BF16, n, n, n, path=MFMA), xb)
+    xh, ih = O.f32_to_fp16(x).reshape(n, n), O.f32_to_fp16(eye).reshape(n, n)
+    assert np.array_equal(hip.matmul(xh, abi.F16, ih, abi.F16, abi.F16, n, n, n, path=MFMA), xh)
+
+
+# ---------------------------------------------------- golden vectors (reference)
+@pytest.mark.parametrize("name", ["q8_a", "q8_b", "q8_c", "q8_t"])
+def test_golden_q8_generic_bit_exact(name):
+    M, K, N = (int(v) for v in GOLD[f"{name}_shape"])
+    c = hip.matmul(GOLD[f"{name}_a"], abi.F32, GOLD[f"{name}_b"], abi.Q8_0, abi.F32, M, N, K,
+                   path=GENERIC)
+    assert np.array_equal(bits32(c), bits32(GOLD[f"{name}_c"]))
+
+
+@pytest.mark.parametrize("name", ["q8_a", "q8_b", "q8_c", "q8_t"])
+def test_golden_q8_auto_path(name):
+    M, K, N = (int(v) for v in GOLD[f"{name}_shape"])
+    c = hip.matmul(GOLD[f"{name}_a"], abi.F32, GOLD[f"{name}_b"], abi.Q8_0, abi.F32, M, N, K)
+    assert_f32_close(c, GOLD[f"{name}_c"], what=name)
+
+
+def test_golden_q8_nt_generic_bit_exact_and_fast_paths():
+    M, K, N = (int(v) for v in GOLD["q8nt_shape"])
+    a, w = GOLD["q8nt_a"], GOLD["q8nt_w"]
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=GENERIC)
+    assert np.array_equal(bits32(c), bits32(GOLD["q8nt_c"]))
+    for path in (MFMA, SKINNY):
+        c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=path)
+        assert_f32_close(c, GOLD["q8nt_c"], what=f"q8nt path {path}")
+
+
+def test_golden_dense_generic_bit_exact():
+    M, K = GOLD["bf16_a"].shape
+    N = GOLD["bf16_b"].shape[1]
+    c = hip.matmul(GOLD["bf16_a"], abi.BF16, GOLD["bf16_b"], abi.BF16, abi.BF16, M, N, K,
+                   path=GENERIC)
+    assert np.array_equal(c, GOLD["bf16_c"])
+    for name in ("f32", "f32b"):
+        a, b = GOLD[f"{name}_a"], GOLD[f"{name}_b"]
+        (M, K), N = a.shape, b.shape[1]
+        c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, M, N, K, path=GENERIC)
+        assert np.array_equal(bits32(c), bits32(GOLD[f"{name}_c"]))
+
+
+def test_golden_dense_tiled():
+    M, K = GOLD["bf16_a"].shape
+    N = GOLD["bf16_b"].shape[1]
+    c = hip.matmul(GOLD["bf16_a"], abi.BF16, GOLD["bf16_b"], abi.BF16, abi.BF16, M, N, K,
+                   path=MFMA)
+    assert_bf16_close(c, GOLD["bf16_c"], what="golden bf16")
+    a, b = GOLD["f32b_a"], GOLD["f32b_b"]
+    (M, K), N = a.shape, b.shape[1]
+    assert hip.matmul_path(abi.F32, abi.F32, abi.F32, M, N, K) == GENERIC  # N=65, K=200
+    a, b = GOLD["f32b_a"][:, :128], GOLD["f32b_b"][:128, :64]
+    c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, 33, 64, 128, path=MFMA)
+    assert_f32_close(c, oracle().matmul_f32(a, b), what="f32 tiled")
+
+
+def test_golden_f16_generic_equals_acc32_oracle():
+    """The reference f16 kernel accumulates in fp16; the HIP path
+    accumulates in f32 and equals the oracle's f32-accumulate
+    restatement bit for bit on the generic path, and stays closer to
+    float64 than the reference's fp16 accumulator does."""
+    a, b = GOLD["f16_a"], GOLD["f16_b"]
+    (M, K), N = a.shape, b.shape[1]
+    c = hip.matmul(a, abi.F16, b, abi.F16, abi.F16, M, N, K, path=GENERIC)
+    assert np.array_equal(c, oracle().matmul_f16_acc32(a, b))
+    exact = (a.view(np.float16).astype(np.float64) @ b.view(np.float16).astype(np.float64))
+    err_hip = np.abs(c.view(np.float16).astype(np.float64) - exact).max()
+    err_ref = np.abs(GOLD["f16_c"].view(np.float16).astype(np.float64) - exact).max()
+    assert err_hip <= err_ref
+
+
+# ------------------------------------------------------------- tiled GEMMs
+DENSE_SHAPES = [(256, 128, 64), (300, 200, 136), (5, 64, 40), (129, 257, 1032), (64, 512, 8)]
+
+
+@pytest.mark.parametrize("M,N,K", DENSE_SHAPES)
+@pytest.mark.parametrize("nt", [False, True])
+def test_bf16_tiled_vs_oracle(M, N, K, nt):
+    O = oracle()
+    a = O.f32_to_bf16(rnd(10 + M, (M, K))).reshape(M, K)
+    b32 = rnd(20 + N, (N, K) if nt else (K, N), 0.2)
+    b = O.f32_to_bf16(b32).reshape(b32.shape)
+    if hip.matmul_path(abi.BF16, abi.BF16, abi.BF16, M, N, K, hip.B_NT if nt else 0) != MFMA:
+        pytest.skip("NN tiles need N % 8 == 0")
+    c = hip.matmul(a, abi.BF16, b, abi.BF16, abi.BF16, M, N, K, flags=hip.B_NT if nt else 0,
+                   path=MFMA)
+    assert_bf16_close(c, ref_linear("bf16", a, b, b_nt=nt), what=f"bf16 {M}x{N}x{K} nt={nt}")
+
+
+@pytest.mark.parametrize("M,N,K", DENSE_SHAPES)
+@pytest.mark.parametrize("nt", [False, True])
+def test_f16_tiled_vs_oracle(M, N, K, nt):
+    O = oracle()
+    a = O.f32_to_fp16(rnd(30 + M, (M, K))).reshape(M, K)
+    b32 = rnd(40 + N, (N, K) if nt else (K, N), 0.2)
+    b = O.f32_to_fp16(b32).reshape(b32.shape)
+    if hip.matmul_path(abi.F16, abi.F16, abi.F16, M, N, K, hip.B_NT if nt else 0) != MFMA:
+        pytest.skip("NN tiles need N % 8 == 0")
+    c = hip.matmul(a, abi.F16, b, abi.F16, abi.F16, M, N, K, flags=hip.B_NT if nt else 0,
+                   path=MFMA)
+    assert_f16_close(c, ref_linear("f16", a, b, b_nt=nt), what=f"f16 {M}x{N}x{K} nt={nt}")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (100, 72, 36), (257, 130, 512)])
+@pytest.mark.parametrize("nt", [False, True])
+def test_f32_tiled_vs_oracle(M, N, K, nt):
+    a = rnd(50 + M, (M, K))
+    b = rnd(60 + N, (N, K) if nt else (K, N))
+    if hip.matmul_path(abi.F32, abi.F32, abi.F32, M, N, K, hip.B_NT if nt else 0) != MFMA:
+        pytest.skip("shape not on the tiled path")
+    c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, M, N, K, flags=hip.B_NT if nt else 0,
+                   path=MFMA)
+    assert_f32_close(c, ref_linear("f32", a, b, b_nt=nt), what=f"f32 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16", "f32"])
+def test_fused_bias_gelu(kind):
+    """MATMUL -> ADD(bias) -> GELU in one launch, rounded like the three
+    reference nodes (cpu_add_bf16.c:62-63, cpu_gelu_bf16.c:62-64)."""
+    O = oracle()
+    M, N, K = 200, 192, 256
+    a32, w32, b32 = rnd(70, (M, K)), rnd(71, (N, K), 0.05), rnd(72, N, 0.3)
+    if kind == "f32":
+        a, w, bias, dt = a32, w32, b32, abi.F32
+    elif kind == "bf16":
+        a, w, bias, dt = (O.f32_to_bf16(a32).reshape(M, K), O.f32_to_bf16(w32).reshape(N, K),
+                          O.f32_to_bf16(b32), abi.BF16)
+    else:
+        a, w, bias, dt = (O.f32_to_fp16(a32).reshape(M, K), O.f32_to_fp16(w32).reshape(N, K),
+                          O.f32_to_fp16(b32), abi.F16)
+    for flags in (hip.BIAS, hip.GELU, hip.BIAS | hip.GELU):
+        c = hip.matmul(a, dt, w, dt, dt, M, N, K, bias=bias if flags & hip.BIAS else None,
+                       flags=flags | hip.B_NT, path=MFMA)
+        ref = ref_linear(kind, a, w, bias if flags & hip.BIAS else None, bool(flags & hip.GELU),
+                         b_nt=True)
+        {"f32": lambda g, r: assert_f32_close(g, r, what=f"fused {kind} {flags}"),
+         "bf16": lambda g, r: assert_bf16_close(g, r, what=f"fused {kind} {flags}"),
+         "f16": lambda g, r: assert_f16_close(g, r, what=f"fused {kind} {flags}")}[kind](c, ref)
+
+
+def test_bf16_output_f32():
+    """bf16 operands with an f32 output (no rounding of C)."""
+    O = oracle()
+    M, N, K = 128, 128, 128
+    a = O.f32_to_bf16(rnd(80, (M, K))).reshape(M, K)
+    b = O.f32_to_bf16(rnd(81, (N, K))).reshape(N, K)
+    c = hip.matmul(a, abi.BF16, b, abi.BF16, abi.F32, M, N, K, flags=hip.B_NT, path=MFMA)
+    exact = bf16_to_f32(a).astype(np.float64) @ bf16_to_f32(b).astype(np.float64).T
+    assert_f32_close(c, exact, rtol=1e-4, what="bf16->f32")
+
+
+# ----------------------------------------------------------------- Q8 paths
+Q8_SHAPES = [(256, 256, 256), (300, 136, 512), (64, 1024, 1024), (130, 96, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", Q8_SHAPES)
+def test_q8_nt_tiled_f32_activations(M, N, K):
+    a = rnd(90 + M, (M, K))
+    w = q8(rnd(91 + N, (N, K), 0.02))
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=MFMA)
+    assert_f32_close(c, ref_q8(a, w, K, N, nt=True), what=f"q8 nt {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (77, 200, 1024)])
+def test_q8_nt_tiled_bf16_and_f16_activations(M, N, K):
+    """bf16 activations (config 3): the reference has no bf16 x Q8 kernel,
+    so the oracle upcasts the activations to f32 exactly first."""
+    O = oracle()
+    a32 = rnd(100 + M, (M, K))
+    w = q8(rnd(101 + N, (N, K), 0.02))
+    ab = O.f32_to_bf16(a32).reshape(M, K)
+    ref = ref_q8(bf16_to_f32(ab).reshape(M, K), w, K, N, nt=True)
+    for path in (MFMA, SKINNY):
+        c = hip.matmul(ab, abi.BF16, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=path)
+        assert_f32_close(c, ref, what=f"q8 bf16-act path {path}")
+    ah = O.f32_to_fp16(a32).reshape(M, K)
+    ref = ref_q8(ah.view(np.float16).astype(np.float32), w, K, N, nt=True)
+    c = hip.matmul(ah, abi.F16, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=MFMA)
+    assert_f32_close(c, ref, what="q8 f16-act")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 96, 256), (64, 100, 64), (200, 64, 72), (256, 100, 128)])
+def test_q8_kn_kernel_contract(M, N, K):
+    """B Q8_0 [K,N] with blocks over the flat index (the layout
+    cpu_kernel_matmul_q8 and tests/test_matmul_q8.c use), through the node
+    kernel: unpacked to f16 then the tiled GEMM, or the generic kernel."""
+    a = rnd(110 + M, (M, K))
+    b = q8(rnd(111 + N, (K, N), 0.02))
+    ref = ref_q8(a, b, K, N, nt=False)
+    c = hip.matmul(a, abi.F32, b, abi.Q8_0, abi.F32, M, N, K)
+    assert_f32_close(c, ref, what=f"q8 kn {M}x{N}x{K}")
+    g = hip.matmul(a, abi.F32, b, abi.Q8_0, abi.F32, M, N, K, path=GENERIC)
+    assert np.array_equal(bits32(g), bits32(ref))
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 77])
+@pytest.mark.parametrize("K,N", [(256, 256), (256, 2048), (1024, 1024), (1024, 4096), (4096, 1024)])
+def test_skinny_q8_config4(M, K, N):
+    """Config 4: prompt-decoder / text-encoder shapes on the skinny kernel."""
+    assert hip.matmul_path(abi.F32, abi.Q8_0, abi.F32, M, N, K, hip.B_NT) == SKINNY
+    a = rnd(120 + M, (M, K))
+    w = q8(rnd(121 + N + K, (N, K), 0.02))
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT)
+    assert_f32_close(c, ref_q8(a, w, K, N, nt=True), what=f"skinny M={M} K={K} N={N}")
+
+
+def test_skinny_bias_gelu_and_ragged_n():
+    M, N, K = 5, 37, 96
+    a = rnd(130, (M, K))
+    w = q8(rnd(131, (N, K), 0.05))
+    bias = rnd(132, N, 0.1)
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, bias=bias,
+                   flags=hip.B_NT | hip.BIAS | hip.GELU, path=SKINNY)
+    assert_f32_close(c, ref_q8(a, w, K, N, nt=True, bias=bias, gelu=True), what="skinny epi")
+
+
+def test_q8_nt_ragged_k_blocks_straddle_rows():
+    """W [N,K] with K % 32 != 0: blocks run over the flat index and cross
+    row boundaries (src/core/quant.c quantizes the tensor flat)."""
+    M, N, K = 70, 40, 72
+    a = rnd(140, (M, K))
+    w = q8(rnd(141, (N, K), 0.02))
+    ref = ref_q8(a, w, K, N, nt=True)
+    assert_f32_close(hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT),
+                     ref, what="q8 nt ragged")
+    g = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=GENERIC)
+    assert np.array_equal(bits32(g), bits32(ref))
+
+
+def test_q8_one_hot_rows_exact_dequant():
+    """A = e_k rows select dequantized weight rows: the skinny path's
+    q*scale in f32 is exact for one-hot A (1.0 is exact in f16)."""
+    O = oracle()
+    K, N = 128, 48
+    w = q8(rnd(150, (N, K), 0.02))
+    deq = O.q8_dequantize(w, N * K).reshape(N, K)
+    rows = [0, 31, 32, 127]
+    a = np.eye(K, dtype=np.float32)[rows]
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, len(rows), N, K, flags=hip.B_NT,
+                   path=SKINNY)
+    assert np.array_equal(c, deq[:, rows].T)
+
+
+def test_q8_paths_agree():
+    M, N, K = 96, 160, 512
+    a = rnd(160, (M, K))
+    w = q8(rnd(161, (N, K), 0.02))
+    outs = [hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=p)
+            for p in (MFMA, SKINNY, GENERIC)]
+    assert_f32_close(outs[0], outs[2], what="mfma vs generic")
+    assert_f32_close(outs[1], outs[2], what="skinny vs generic")
+
+
+# ------------------------------------------------------- batched attention
+@pytest.mark.parametrize("B,S,D", [(3, 64, 64), (2, 100, 64), (4, 576, 64)])
+def test_batched_attention_matmuls(B, S, D):
+    """QK^T ([B,S,D] x [B,S,D]^T) and PV ([B,S,S] x [B,S,D]) per slice,
+    as gh_multihead_attention builds them (graph_helpers.c:808-843)."""
+    O = oracle()
+    q = O.f32_to_bf16(rnd(170, (B, S, D)) / 8).reshape(B, S, D)
+    k = O.f32_to_bf16(rnd(171, (B, S, D)) / 8).reshape(B, S, D)
+    v = O.f32_to_bf16(rnd(172, (B, S, D)) / 8).reshape(B, S, D)
+    s = hip.batched(abi.BF16, q, k, B, S, S, D, b_nt=True)
+    assert_bf16_close(s, O.matmul_bf16_batched(q, k, b_nt=True, threads=8), what="QK^T")
+    p = O.f32_to_bf16(rnd(173, (B, S, S)) / 8).reshape(B, S, S)
+    o = hip.batched(abi.BF16, p, v, B, S, D, S, b_nt=False)
+    assert_bf16_close(o, O.matmul_bf16_batched(p, v, b_nt=False, threads=8), what="PV")
+
+
+# -------------------------------------------- full-size shapes, row sample
+def _row_sample(M, n=48, seed=7):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, n)]))
+
+
+@pytest.mark.parametrize("which", ["fc1", "fc2"])
+def test_config2_bf16_full_size_rows(which):
+    """Config 2 at full size on the tiled path; rows are independent, so
+    a row sample of A against the same W is checked with the oracle."""
+    O = oracle()
+    M, (K, N) = 5184, ((1024, 4096) if which == "fc1" else (4096, 1024))
+    a = O.f32_to_bf16(rnd(180, (M, K))).reshape(M, K)
+    w = O.f32_to_bf16(rnd(181, (N, K), 0.02)).reshape(N, K)
+    bias = O.f32_to_bf16(rnd(182, N, 0.01))
+    c = hip.matmul(a, abi.BF16, w, abi.BF16, abi.BF16, M, N, K, bias=bias,
+                   flags=hip.B_NT | hip.BIAS | hip.GELU)
+    rows = _row_sample(M)
+    ref = ref_linear("bf16", a[rows], w, bias, True, b_nt=True)
+    g, r = bf16_to_f32(c[rows]), bf16_to_f32(ref)
+    assert np.abs(g - r).max() <= 2e-2, f"max abs {np.abs(g - r).max()}"
+
+
+def test_config1_q8_full_size_rows():
+    M, N, K = 5184, 1024, 1024
+    a = rnd(0, (M, K))
+    w = q8(rnd(1, (N, K), 0.02))
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT)
+    rows = _row_sample(M)
+    assert_f32_close(c[rows], ref_q8(a[rows], w, K, N, nt=True), what="config 1")
+
+
+# ------------------------------------------------------------- edge cases
+def test_degenerate_sizes():
+    a = np.zeros((1, 1), np.float32)
+    lib = hip.load()
+    # M == 0 or N == 0 is a no-op
+    assert lib.sam3_hip_matmul(abi.F32, 1, abi.F32, 1, abi.F32, 1, 0, 4, 4, None, 0, None) == abi.OK
+    # K == 0: C = 0 (the reference zeroes C and adds nothing)
+    da, db, dc = hip.DeviceBuffer(16), hip.DeviceBuffer(16), hip.DeviceBuffer.of(np.ones(4, np.float32))
+    hip.matmul_dev(abi.F32, da.ptr, abi.F32, db.ptr, abi.F32, dc.ptr, 2, 2, 0)
+    hip.synchronize()
+    assert np.all(dc.download(np.float32, 4) == 0)
+    c = hip.matmul(np.float32([[2.0]]), abi.F32, np.float32([[3.0]]), abi.F32, abi.F32, 1, 1, 1)
+    assert c[0, 0] == 6.0
+    del a
+
+
+def test_one_by_n_and_n_by_one():
+    O = oracle()
+    a = rnd(190, (1, 300))
+    b = rnd(191, (300, 1))
+    c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, 1, 1, 300)
+    assert_f32_close(c, O.matmul_f32(a, b), what="1x1")
