@@ -131,6 +131,17 @@ def cpu_baseline(a_bits, w_bits, M, N, K, target_s=10.0):
                       + (f", {model}" if model else "")}
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of the headline kernel, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
+    by a copy kernel of known size); None when not recorded."""
+    try:
+        rec = json.loads((ROOT / "profiles" / "traffic.json").read_text())[key]
+        return int(rec["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,7 +318,7 @@ def main():
                    "M": M, "N": N, "K": K, "arch": arch},
         "roofline": {"bound": "mfma", "achieved": round(value, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(value / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("bf16_fc1_5184x4096x1024")},
         "cpu_baseline": cpu,
         "extra": extra,
     }

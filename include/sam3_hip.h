@@ -119,7 +119,7 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 /*
  * C[M,N] = A[M,K] * B (+bias) (GELU). Dtypes are enum sam3_dtype:
  *   a F32/F16/BF16 with b of the same dtype, c = a's dtype or F32;
- *   a F32/F16/BF16 with b Q8_0, c F32/F16/BF16. Q8_0 B is [K,N] with
+ *   a F32/F16/BF16 with b Q8_0, c F32. Q8_0 B is [K,N] with
  *   blocks over the flat index (the kernel contract) or, with
  *   SAM3_HIP_B_NT, W[N,K] quantized flat (blocks along K).
  * Rows are dense (lda = K, ldb = N or K, ldc = N).

@@ -40,7 +40,7 @@ __global__ void __launch_bounds__(256) bias_add_k(const void *x, const void *bia
 	const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
 	if (i >= rows * n)
 		return;
-	const float v = __fadd_rn(load_as_f32(x, i, KIND), load_as_f32(bias, i % n, KIND));
+	const float v = add_rn(load_as_f32(x, i, KIND), load_as_f32(bias, i % n, KIND));
 	store_from_f32(out, i, KIND, v);
 }
 
@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(256) add_same_k(const void *x, const void *y, 
 	const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
 	if (i >= n)
 		return;
-	store_from_f32(out, i, KIND, __fadd_rn(load_as_f32(x, i, KIND), load_as_f32(y, i, KIND)));
+	store_from_f32(out, i, KIND, add_rn(load_as_f32(x, i, KIND), load_as_f32(y, i, KIND)));
 }
 
 template <int KIND>

@@ -10,9 +10,9 @@
  *
  * Tiled kernel structure (one workgroup = 4 waves of 64 lanes):
  *   - A tile [BM x BK] and B tile [BN x BK] are staged in LDS with k
- *     contiguous, as 16-byte chunks whose index is XORed with (row & 7)
- *     so that the 128-bit LDS reads of 8 consecutive rows hit distinct
- *     banks. Two stages: global loads of tile k+1 are issued before the
+ *     contiguous, as 16-byte chunks whose index is XOR-permuted per row
+ *     (lds_swz) so that the 128-bit LDS reads of 8 or 16 consecutive rows
+ *     hit distinct banks. Two stages: global loads of tile k+1 are issued before the
  *     MFMAs of tile k and written to the other stage after them.
  *   - Loaders convert on the way in: f32 activations -> f16, bf16 -> f16,
  *     Q8_0 weight blocks {f32 scale, 32 x int8} -> f16 (q*scale), and
@@ -30,31 +30,14 @@
  *     each XCD receives a contiguous block of tiles, walked in groups of
  *     8 tile-rows so neighbouring workgroups share A and B in its L2.
  */
-#include "s3k.h"
-#include "s3k_dev.h"
+#include "gemm_common.h"
 
 namespace s3k {
-
-struct GemmArgs {
-	const char *a;
-	const char *b;
-	char       *c;
-	const char *bias;
-	int M, N, K;
-	long long lda_b, ldb_b, ldc;  /* A/B row pitch in bytes, C in elements */
-	long long sa_b, sb_b, sc;     /* batch strides: bytes, bytes, elements */
-	int flags;
-	int c_kind;
-	int bias_kind;
-	int vec_ok;   /* rows of C (and the base) allow 16-byte stores */
-	int tiles_m, tiles_n;
-};
 
 template <int CPR>
 __device__ __forceinline__ int lds_off(int row, int c)
 {
-	constexpr int SW = CPR < 8 ? CPR : 8;
-	return (row * CPR + (c ^ (row & (SW - 1)))) << 4;
+	return (row * CPR + (c ^ lds_swz<CPR>(row))) << 4;
 }
 
 /* ------------------------------------------------------------------ */
@@ -169,6 +152,12 @@ struct LoadRowsToF16 {
 	}
 };
 
+/* Component k (a compile-time constant after unrolling) of a uint4. */
+__device__ __forceinline__ uint32_t dword_of(const uint4 &q, int k)
+{
+	return k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w;
+}
+
 /* B stored [K,N] (n contiguous): each thread loads an E(k) x E(n) block
  * (E = elements per 16 bytes) and writes its transpose as E k-chunks. */
 template <int R, int CPR, int NT, int ESZ>
@@ -221,15 +210,15 @@ struct LoadColsT {
 				if (ESZ == 2) {
 #pragma unroll
 					for (int e = 0; e < 4; ++e) {
-						uint32_t x = ((const uint32_t *)&v[i][2 * e])[j >> 1];
-						uint32_t y = ((const uint32_t *)&v[i][2 * e + 1])[j >> 1];
+						const uint32_t x = dword_of(v[i][2 * e], j >> 1);
+						const uint32_t y = dword_of(v[i][2 * e + 1], j >> 1);
 						d[e] = (j & 1) ? ((x >> 16) | (y & 0xFFFF0000u))
 							       : ((x & 0xFFFFu) | (y << 16));
 					}
 				} else {
 #pragma unroll
 					for (int e = 0; e < 4; ++e)
-						d[e] = ((const uint32_t *)&v[i][e])[j];
+						d[e] = dword_of(v[i][e], j);
 				}
 				*(uint4 *)(lds + lds_off<CPR>(ng * E + j, kg)) =
 					make_uint4(d[0], d[1], d[2], d[3]);
@@ -296,103 +285,7 @@ struct LoadQ8NT {
 	}
 };
 
-/* ------------------------------------------------------------------ */
-/* MFMA families                                                        */
-/* ------------------------------------------------------------------ */
-enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };
-
-template <int FAM>
-__device__ __forceinline__ void mfma_chunk(s3k_f32x16 &acc, const uint4 &a, const uint4 &b)
-{
-	if constexpr (FAM == FAM_BF16) {
-		acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-			__builtin_bit_cast(s3k_bf16x8, a), __builtin_bit_cast(s3k_bf16x8, b),
-			acc, 0, 0, 0);
-	} else if constexpr (FAM == FAM_F16) {
-		acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-			__builtin_bit_cast(s3k_f16x8, a), __builtin_bit_cast(s3k_f16x8, b),
-			acc, 0, 0, 0);
-	} else {
-		/* k slot (l >> 5) of MFMA s holds element s of the lane's chunk */
-		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
-		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
-		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
-		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
-	}
-}
-
-/* Workgroup id -> (tile_m, tile_n): XCD-contiguous, then grouped by 8
- * tile-rows. */
-__device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int &tm, int &tn)
-{
-	const int nwg = tiles_m * tiles_n;
-	int t = wg;
-	if ((nwg & 7) == 0)
-		t = (wg & 7) * (nwg >> 3) + (wg >> 3);
-	const int G = 8;
-	const int per_group = G * tiles_n;
-	const int g = t / per_group;
-	const int first = g * G;
-	const int gsz = min(tiles_m - first, G);
-	const int in = t - g * per_group;
-	tm = first + in % gsz;
-	tn = in / gsz;
-}
-
-/* Bias, GELU and the store of C[m][n..n+7] from 8 f32 values (in LDS). */
-template <int CK>
-__device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int n, const float *v)
-{
-	const bool full = n + 8 <= p.N;
-	float x[8];
-#pragma unroll
-	for (int e = 0; e < 8; ++e) {
-		float bv = 0.0f;
-		if ((p.flags & S3K_EPI_BIAS) && (full || n + e < p.N))
-			bv = load_as_f32(p.bias, n + e, p.bias_kind);
-		x[e] = epilogue<CK>(v[e], bv, p.flags);
-	}
-	const long long o = (long long)m * p.ldc + n;
-	if (CK == S3K_F32) {
-		float *c = (float *)cb + o;
-		if (full && p.vec_ok) {
-			*(float4 *)c = make_float4(x[0], x[1], x[2], x[3]);
-			*(float4 *)(c + 4) = make_float4(x[4], x[5], x[6], x[7]);
-		} else {
-#pragma unroll
-			for (int e = 0; e < 8; ++e)
-				if (n + e < p.N)
-					c[e] = x[e];
-		}
-	} else {
-		uint32_t h[8];
-#pragma unroll
-		for (int e = 0; e < 8; ++e)
-			h[e] = CK == S3K_BF16 ? f32_to_bf16(x[e]) : f32_to_f16(x[e]);
-		uint16_t *c = (uint16_t *)cb + o;
-		if (full && p.vec_ok) {
-			*(uint4 *)c = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16),
-						 h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-		} else {
-#pragma unroll
-			for (int e = 0; e < 8; ++e)
-				if (n + e < p.N)
-					c[e] = (uint16_t)h[e];
-		}
-	}
-}
-
-__device__ __forceinline__ void store8(const GemmArgs &p, char *cb, int m, int n, const float *v)
-{
-	if (p.c_kind == S3K_F32)
-		finish8<S3K_F32>(p, cb, m, n, v);
-	else if (p.c_kind == S3K_BF16)
-		finish8<S3K_BF16>(p, cb, m, n, v);
-	else
-		finish8<S3K_F16>(p, cb, m, n, v);
-}
-
-template <int BM, int BN, int BK, int WGM, int WGN, int FAM, class LA, class LB>
+template <int BM, int BN, int BK, int WGM, int WGN, int FAM, int CK, class LA, class LB>
 __global__ void __launch_bounds__(256, 1) gemm_tiled(GemmArgs p)
 {
 	constexpr int NT = 256;
@@ -465,32 +358,8 @@ __global__ void __launch_bounds__(256, 1) gemm_tiled(GemmArgs p)
 		__syncthreads();
 	}
 
-	/* Epilogue, one 32-row strip of the wave tile at a time: the MFMA
-	 * layout (lane holds column l & 31 of rows 8*(r>>2) + 4*(l>>5) + (r&3))
-	 * is turned into row-contiguous runs of 8 columns through LDS, so each
-	 * lane finishes 8 outputs and writes them with one 16-byte store. */
-	constexpr int PITCH = WTN + 4; /* floats; keeps rows 16-B aligned */
-	static_assert(4 * 32 * PITCH * 4 <= 2 * STAGE, "epilogue staging fits");
-	float *stg = (float *)smem + wave * 32 * PITCH;
-	char *cb = p.c + (long long)bz * p.sc * (p.c_kind == 0 ? 4 : 2);
-#pragma unroll
-	for (int i = 0; i < FM; ++i) {
-#pragma unroll
-		for (int j = 0; j < FN; ++j)
-#pragma unroll
-			for (int r = 0; r < 16; ++r)
-				stg[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] =
-					acc[i][j][r];
-		__syncthreads();
-		for (int s = lane; s < 32 * WTN / 8; s += 64) {
-			const int row = s / (WTN / 8), c8 = (s % (WTN / 8)) * 8;
-			const int m = tm * BM + wm0 + i * 32 + row;
-			const int n = tn * BN + wn0 + c8;
-			if (m < p.M && n < p.N)
-				store8(p, cb, m, n, stg + row * PITCH + c8);
-		}
-		__syncthreads();
-	}
+	static_assert(4 * 32 * (WTN + 8) * 4 <= 2 * STAGE, "epilogue staging fits");
+	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
 /* ------------------------------------------------------------------ */
@@ -523,10 +392,10 @@ __global__ void __launch_bounds__(256) gemm_generic(GemmArgs p, int a_ld, int b_
 			const char *blk = B + (lin >> 5) * 36;
 			const float s = *(const float *)blk;
 			const float q = (float)(int)(int8_t)blk[4 + (lin & 31)];
-			acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(a, q), s));
+			acc = add_rn(acc, mul_rn(mul_rn(a, q), s));
 		} else {
 			const long long bi = nt ? (long long)n * b_ld + k : (long long)k * b_ld + n;
-			acc = __fadd_rn(acc, __fmul_rn(a, load_as_f32(B, bi, BK_)));
+			acc = add_rn(acc, mul_rn(a, load_as_f32(B, bi, BK_)));
 		}
 	}
 	float bv = 0.0f;
@@ -654,58 +523,72 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.bias_kind = g->c_kind;
 	p.vec_ok = aligned16(g->c) && g->ldc % 8 == 0 && (g->batch <= 1 || g->stride_c % 8 == 0);
 	p.tiles_m = p.tiles_n = 0;
+	p.a_extent = p.b_extent = 0;
 	return p;
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int FAM, class LA, class LB>
+template <int BM, int BN, int BK, int WGM, int WGN, int FAM, int CK, class LA, class LB>
 static int launch_tiled(GemmArgs p, int batch, hipStream_t st)
 {
 	p.tiles_m = (p.M + BM - 1) / BM;
 	p.tiles_n = (p.N + BN - 1) / BN;
 	dim3 grid(p.tiles_m * p.tiles_n, batch);
-	hipLaunchKernelGGL((gemm_tiled<BM, BN, BK, WGM, WGN, FAM, LA, LB>), grid, dim3(256), 0, st, p);
+	hipLaunchKernelGGL((gemm_tiled<BM, BN, BK, WGM, WGN, FAM, CK, LA, LB>), grid, dim3(256), 0, st, p);
 	return (int)hipGetLastError();
 }
 
-/* One tile shape, all operand kinds. */
+/* 16-bit operands of one kind: C is that kind or f32. */
+template <int BM, int BN, int BK, int WGM, int WGN, int FAM, int KIND, class LA, class LB>
+static int launch_tiled16(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	if (g->c_kind == S3K_F32)
+		return launch_tiled<BM, BN, BK, WGM, WGN, FAM, S3K_F32, LA, LB>(p, g->batch, st);
+	return launch_tiled<BM, BN, BK, WGM, WGN, FAM, KIND, LA, LB>(p, g->batch, st);
+}
+
+/* One tile shape, all operand kinds. Q8 and mixed f32/bf16 x f16 write
+ * f32 (the reference Q8 output, cpu_matmul_q8.c:181-185). */
 template <int BM, int BN, int WGM, int WGN>
 static int launch_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
 	const bool nt = g->flags & S3K_B_NT;
 	const int ak = g->a_kind, bk = g->b_kind;
 	constexpr int BK16 = 64, C16 = BK16 * 2 / 16;
-	if (bk == S3K_Q8) {
-		typedef LoadQ8NT<BN, C16, 256> LB;
-		if (ak == S3K_F32)
-			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
-				LoadRowsToF16<BM, C16, 256, false>, LB>(p, g->batch, st);
-		if (ak == S3K_BF16)
-			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
-				LoadRowsToF16<BM, C16, 256, true>, LB>(p, g->batch, st);
-		return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
-			LoadRows<BM, C16, 256, 2, false>, LB>(p, g->batch, st);
-	}
-	if (bk == S3K_F16 && ak != S3K_F16) {
+	if (bk == S3K_Q8 || (bk == S3K_F16 && ak != S3K_F16)) {
+		if (g->c_kind != S3K_F32)
+			return (int)hipErrorInvalidValue;
+		if (bk == S3K_Q8) {
+			typedef LoadQ8NT<BN, C16, 256> LB;
+			if (ak == S3K_F32)
+				return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F32,
+					LoadRowsToF16<BM, C16, 256, false>, LB>(p, g->batch, st);
+			if (ak == S3K_BF16)
+				return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F32,
+					LoadRowsToF16<BM, C16, 256, true>, LB>(p, g->batch, st);
+			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F32,
+				LoadRows<BM, C16, 256, 2, false>, LB>(p, g->batch, st);
+		}
 		typedef LoadRows<BN, C16, 256, 2, true> LB;
 		if (ak == S3K_F32)
-			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
+			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F32,
 				LoadRowsToF16<BM, C16, 256, false>, LB>(p, g->batch, st);
-		return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
+		return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F32,
 			LoadRowsToF16<BM, C16, 256, true>, LB>(p, g->batch, st);
 	}
+	typedef LoadRows<BM, C16, 256, 2, false> LA;
 	if (ak == S3K_BF16) {
 		if (nt)
-			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_BF16,
-				LoadRows<BM, C16, 256, 2, false>, LoadRows<BN, C16, 256, 2, true>>(p, g->batch, st);
-		return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_BF16,
-			LoadRows<BM, C16, 256, 2, false>, LoadColsT<BN, C16, 256, 2>>(p, g->batch, st);
+			return launch_tiled16<BM, BN, BK16, WGM, WGN, FAM_BF16, S3K_BF16, LA,
+				LoadRows<BN, C16, 256, 2, true>>(g, p, st);
+		return launch_tiled16<BM, BN, BK16, WGM, WGN, FAM_BF16, S3K_BF16, LA,
+			LoadColsT<BN, C16, 256, 2>>(g, p, st);
 	}
 	if (ak == S3K_F16) {
 		if (nt)
-			return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
-				LoadRows<BM, C16, 256, 2, false>, LoadRows<BN, C16, 256, 2, true>>(p, g->batch, st);
-		return launch_tiled<BM, BN, BK16, WGM, WGN, FAM_F16,
-			LoadRows<BM, C16, 256, 2, false>, LoadColsT<BN, C16, 256, 2>>(p, g->batch, st);
+			return launch_tiled16<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F16, LA,
+				LoadRows<BN, C16, 256, 2, true>>(g, p, st);
+		return launch_tiled16<BM, BN, BK16, WGM, WGN, FAM_F16, S3K_F16, LA,
+			LoadColsT<BN, C16, 256, 2>>(g, p, st);
 	}
 	return (int)hipErrorInvalidValue;
 }
@@ -716,9 +599,9 @@ static int launch_cfg_f32(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	const bool nt = g->flags & S3K_B_NT;
 	constexpr int BK = 32, C = BK * 4 / 16;
 	if (nt)
-		return launch_tiled<BM, BN, BK, WGM, WGN, FAM_F32,
+		return launch_tiled<BM, BN, BK, WGM, WGN, FAM_F32, S3K_F32,
 			LoadRows<BM, C, 256, 4, false>, LoadRows<BN, C, 256, 4, true>>(p, g->batch, st);
-	return launch_tiled<BM, BN, BK, WGM, WGN, FAM_F32,
+	return launch_tiled<BM, BN, BK, WGM, WGN, FAM_F32, S3K_F32,
 		LoadRows<BM, C, 256, 4, false>, LoadColsT<BN, C, 256, 4>>(p, g->batch, st);
 }
 
@@ -760,13 +643,19 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 		return launch_generic(g, p, st);
 	if (path != S3K_PATH_MFMA || !mfma_ok(g))
 		return (int)hipErrorInvalidValue;
+	if (s3k_dl_ok(g))
+		return s3k_dl_launch(g, p, st);
 	if (g->a_kind == S3K_F32 && g->b_kind == S3K_F32) {
 		switch (pick_cfg(g, true)) {
 		case 1:  return launch_cfg_f32<128, 128, 2, 2>(g, p, st);
 		default: return launch_cfg_f32<64, 64, 2, 2>(g, p, st);
 		}
 	}
-	switch (pick_cfg(g, false)) {
+	int cfg = pick_cfg(g, false);
+	/* the 256-row [K,N]-layout tile needs more than 256 VGPRs: use 128 */
+	if (cfg == 0 && !(g->flags & S3K_B_NT) && g->b_kind != S3K_Q8)
+		cfg = 1;
+	switch (cfg) {
 	case 0:  return launch_cfg<256, 128, 2, 2>(g, p, st);
 	case 1:  return launch_cfg<128, 128, 2, 2>(g, p, st);
 	default: return launch_cfg<64, 64, 2, 2>(g, p, st);

@@ -1,0 +1,207 @@
+/*
+ * gemm_common.h - pieces shared by the tiled GEMM kernels (gemm.hip,
+ * gemm_dl.hip): launch arguments, the MFMA step, the XCD-aware tile map
+ * and the LDS-staged epilogue (bias, tanh-GELU, rounding, 16-byte stores).
+ */
+#ifndef SAM3_GEMM_COMMON_H
+#define SAM3_GEMM_COMMON_H
+
+#include "s3k.h"
+#include "s3k_dev.h"
+
+namespace s3k {
+
+struct GemmArgs {
+	const char *a;
+	const char *b;
+	char       *c;
+	const char *bias;
+	int M, N, K;
+	long long lda_b, ldb_b, ldc;  /* A/B row pitch in bytes, C in elements */
+	long long sa_b, sb_b, sc;     /* batch strides: bytes, bytes, elements */
+	int flags;
+	int c_kind;
+	int bias_kind;
+	int vec_ok;   /* rows of C (and the base) allow 16-byte stores */
+	int tiles_m, tiles_n;
+	unsigned a_extent, b_extent; /* bytes of one batch slice (buffer range) */
+};
+
+enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };
+
+/* LDS tiles hold rows of CPR 16-byte k-chunks; the chunk index of row r
+ * is XORed with lds_swz(r). The MFMA operand reads have lane l fetch 16
+ * bytes of row (l & 31) at one logical chunk per half-wave. The two
+ * permutations below were chosen by measurement on gfx950
+ * (SQ_LDS_BANK_CONFLICT of a ds_read_b128 probe with exactly this lane
+ * pattern: zero conflict cycles, ~4 LDS cycles per instruction), against
+ * 3.2 (row&7, and other XORs that look conflict-free in a simple
+ * 64-bank model) to 22.4 extra cycles per read (no permutation):
+ *   CPR 4 (64-B rows):  c ^ ((r >> 2) & 3)
+ *   CPR 8 (128-B rows): c ^ ((r ^ (r >> 3)) & 7) */
+template <int CPR>
+__device__ __forceinline__ int lds_swz(int row)
+{
+	static_assert(CPR == 4 || CPR == 8, "LDS rows of 4 or 8 chunks");
+	if constexpr (CPR == 8)
+		return (row ^ (row >> 3)) & 7;
+	else
+		return (row >> 2) & 3;
+}
+
+/* One 16-k step (or 8-k for f32) of a 32x32 output tile. Lane l supplies
+ * row (l & 31) and the 16-byte k-chunk (l >> 5); A and B use the same
+ * (lane, slot) -> k map, so the MFMA computes the exact tile product. */
+template <int FAM>
+__device__ __forceinline__ void mfma_chunk(s3k_f32x16 &acc, const uint4 &a, const uint4 &b)
+{
+	if constexpr (FAM == FAM_BF16) {
+		acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+			__builtin_bit_cast(s3k_bf16x8, a), __builtin_bit_cast(s3k_bf16x8, b),
+			acc, 0, 0, 0);
+	} else if constexpr (FAM == FAM_F16) {
+		acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+			__builtin_bit_cast(s3k_f16x8, a), __builtin_bit_cast(s3k_f16x8, b),
+			acc, 0, 0, 0);
+	} else {
+		/* k slot (l >> 5) of MFMA s holds element s of the lane's chunk */
+		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+		acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+	}
+}
+
+/* Workgroup id -> (tile_m, tile_n). Workgroups are dealt round-robin to
+ * the 8 XCDs; ids are regrouped so each XCD gets a contiguous range of
+ * tiles, walked in groups of 8 tile-rows so that workgroups resident on
+ * one XCD share A rows and B columns in that XCD's L2. */
+__device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int &tm, int &tn)
+{
+	const int nwg = tiles_m * tiles_n;
+	int t = wg;
+	if ((nwg & 7) == 0)
+		t = (wg & 7) * (nwg >> 3) + (wg >> 3);
+	const int G = 8;
+	const int per_group = G * tiles_n;
+	const int g = t / per_group;
+	const int first = g * G;
+	const int gsz = min(tiles_m - first, G);
+	const int in = t - g * per_group;
+	tm = first + in % gsz;
+	tn = in / gsz;
+}
+
+/* Store of C[m][n..n+7] from 8 f32 values at v (LDS), output kind CK.
+ * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
+ * points; without it the values are only converted. */
+template <int CK, bool EPI>
+__device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int n, const float *v)
+{
+	const bool full = n + 8 <= p.N;
+	const float4 v0 = *(const float4 *)v, v1 = *(const float4 *)(v + 4);
+	float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+	if (EPI) {
+#pragma unroll
+		for (int e = 0; e < 8; ++e) {
+			float bv = 0.0f;
+			if ((p.flags & S3K_EPI_BIAS) && (full || n + e < p.N))
+				bv = load_as_f32(p.bias, n + e, p.bias_kind);
+			x[e] = epilogue<CK>(x[e], bv, p.flags);
+		}
+	}
+	const long long o = (long long)m * p.ldc + n;
+	if (CK == S3K_F32) {
+		float *c = (float *)cb + o;
+		if (full && p.vec_ok) {
+			*(float4 *)c = make_float4(x[0], x[1], x[2], x[3]);
+			*(float4 *)(c + 4) = make_float4(x[4], x[5], x[6], x[7]);
+		} else {
+#pragma unroll
+			for (int e = 0; e < 8; ++e)
+				if (n + e < p.N)
+					c[e] = x[e];
+		}
+	} else {
+		uint32_t h[8];
+#pragma unroll
+		for (int e = 0; e < 8; ++e)
+			h[e] = CK == S3K_BF16 ? f32_to_bf16(x[e]) : f32_to_f16(x[e]);
+		uint16_t *c = (uint16_t *)cb + o;
+		if (full && p.vec_ok) {
+			*(uint4 *)c = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16),
+						 h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+		} else {
+#pragma unroll
+			for (int e = 0; e < 8; ++e)
+				if (n + e < p.N)
+					c[e] = (uint16_t)h[e];
+		}
+	}
+}
+
+/* Epilogue of a wave tile, one 32-row strip at a time: the MFMA layout
+ * (lane holds column l & 31 of rows 8*(r>>2) + 4*(l>>5) + (r&3)) is turned
+ * into row-contiguous runs of 8 columns through LDS, so each lane finishes
+ * 8 outputs and writes them with one 16-byte store. `smem` must be free
+ * (all waves past their last LDS read) and hold NW*32*(WTN+8) floats.
+ * Every wave of the workgroup must call this (it contains barriers). The
+ * store loops are kept rolled: this code runs once per tile, and an
+ * unrolled epilogue would not fit the instruction cache. */
+template <int FM, int FN, int WTN, int CK>
+__device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&acc)[FM][FN],
+					      char *smem, int wave, int lane, int m0, int n0, int bz)
+{
+	constexpr int PITCH = WTN + 8; /* floats; 16-B aligned rows, rows 4 apart 32 banks apart */
+	float *stg = (float *)smem + wave * 32 * PITCH;
+	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
+	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU)) != 0;
+#pragma unroll
+	for (int i = 0; i < FM; ++i) {
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				stg[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] =
+					acc[i][j][r];
+		__syncthreads();
+		const int mrow = m0 + i * 32;
+		if (epi) {
+#pragma unroll 1
+			for (int s = lane; s < 32 * WTN / 8; s += 64) {
+				const int row = s / (WTN / 8), c8 = (s % (WTN / 8)) * 8;
+				if (mrow + row < p.M && n0 + c8 < p.N)
+					finish8<CK, true>(p, cb, mrow + row, n0 + c8, stg + row * PITCH + c8);
+			}
+		} else {
+#pragma unroll 1
+			for (int s = lane; s < 32 * WTN / 8; s += 64) {
+				const int row = s / (WTN / 8), c8 = (s % (WTN / 8)) * 8;
+				if (mrow + row < p.M && n0 + c8 < p.N)
+					finish8<CK, false>(p, cb, mrow + row, n0 + c8, stg + row * PITCH + c8);
+			}
+		}
+		__syncthreads();
+	}
+}
+
+/* Output kind chosen at run time (the register-staged kernels). */
+template <int FM, int FN, int WTN>
+__device__ __forceinline__ void write_tile(const GemmArgs &p, s3k_f32x16 (&acc)[FM][FN], char *smem,
+					   int wave, int lane, int m0, int n0, int bz)
+{
+	if (p.c_kind == S3K_F32)
+		write_tile_ck<FM, FN, WTN, S3K_F32>(p, acc, smem, wave, lane, m0, n0, bz);
+	else if (p.c_kind == S3K_BF16)
+		write_tile_ck<FM, FN, WTN, S3K_BF16>(p, acc, smem, wave, lane, m0, n0, bz);
+	else
+		write_tile_ck<FM, FN, WTN, S3K_F16>(p, acc, smem, wave, lane, m0, n0, bz);
+}
+
+} /* namespace s3k */
+
+/* Direct-to-LDS bf16/f16 NT GEMM (gemm_dl.hip). */
+bool s3k_dl_ok(const struct s3k_gemm *g);
+int s3k_dl_launch(const struct s3k_gemm *g, s3k::GemmArgs p, hipStream_t st);
+
+#endif /* SAM3_GEMM_COMMON_H */

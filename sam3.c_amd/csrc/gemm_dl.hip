@@ -1,0 +1,301 @@
+/*
+ * gemm_dl.hip - bf16/f16 GEMM C = A * W^T (A [M,K], W [N,K], both k
+ * contiguous) for gfx950 with direct global->LDS loads. This is the
+ * production layout of sam3.c's linear layers once gh_linear's weight
+ * transpose is folded (graph_helpers.c:297-320), and of attention's
+ * Q K^T per head. Reference kernel: cpu_matmul_bf16.c:103-141 (f32
+ * accumulate, one rounding of the output).
+ *
+ * Pipeline (per workgroup of NW waves, tile BM x BN, k-step BK):
+ *   - buffer_load_dwordx4 ... lds moves 16 bytes per lane straight into
+ *     LDS (no VGPR staging); a wave-instruction fills 1 KiB, i.e. 64
+ *     consecutive 16-byte chunks. Each lane picks the global chunk whose
+ *     swizzled LDS slot is lane-th of that KiB, so the LDS image has rows
+ *     of BK k-values with the chunk index XOR-permuted per row
+ *     (lds_swz: conflict-free 128-bit reads by 8 or 16 consecutive rows).
+ *   - Rows past M/N and chunks past K are given an out-of-range buffer
+ *     offset; the buffer unit returns zeros for them, so tails need no
+ *     branches.
+ *   - STAGES-deep ring: at step kt the loads of step kt+STAGES-1 are in
+ *     flight while step kt is multiplied. Completion is tracked with an
+ *     explicit s_waitcnt vmcnt(loads of the younger stages) followed by
+ *     s_barrier; HIP's __syncthreads would wait for every load.
+ *   - MFMA v_mfma_f32_32x32x16_{bf16,f16}, wave tile (BM/WGM) x (BN/WGN).
+ *   - Epilogue through LDS with 16-byte stores (gemm_common.h).
+ */
+#include "gemm_common.h"
+
+namespace s3k {
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef int s3k_i32x4 __attribute__((ext_vector_type(4)));
+
+/* Buffer descriptor of a raw byte range (gfx9 layout: base, stride 0,
+ * num_records = bytes, dword3 = 0x00020000); offsets >= bytes load 0. */
+__device__ __forceinline__ s3k_i32x4 buf_rsrc(const void *base, unsigned bytes)
+{
+	const unsigned long long a = (unsigned long long)base;
+	return (s3k_i32x4){(int)(unsigned)a, (int)(unsigned)(a >> 32), (int)bytes, 0x00020000};
+}
+
+/* 16 bytes per lane from global (rsrc + voff) into LDS at lds + 16*lane.
+ * Issued as inline asm so the compiler does not treat the LDS image as
+ * written here: the kernel orders it with explicit vmcnt waits and a
+ * barrier (the builtin form makes the compiler wait for every pending
+ * load before any LDS read). */
+__device__ __forceinline__ void dma16(const void *lds, s3k_i32x4 rsrc, unsigned voff)
+{
+	const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)lds);
+	asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+		     :: "s"(m0), "v"(voff), "s"(rsrc) : "memory");
+}
+
+/* s_waitcnt vmcnt(N) with lgkm/exp counters left alone. */
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+	static_assert(N >= 0 && N < 64, "vmcnt range");
+	__builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ void wg_barrier()
+{
+	asm volatile("s_barrier" ::: "memory");
+}
+
+template <int CPR>
+__device__ __forceinline__ int dl_off(int row, int c)
+{
+	return (row * CPR + (c ^ lds_swz<CPR>(row))) << 4;
+}
+
+#define S3K_OOB 0x80000000u /* buffer offset beyond any range: loads zero */
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int FAM, int CK, int OCC>
+__global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
+{
+	constexpr int NW = WGM * WGN;
+	constexpr int CPR = BK / 8;
+	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+	constexpr int SB = A_BYTES + B_BYTES;
+	constexpr int A_INS = BM * CPR / 64, B_INS = BN * CPR / 64; /* KiB per stage */
+	static_assert(A_INS % NW == 0 && B_INS % NW == 0, "loads split evenly over waves");
+	constexpr int A_PER = A_INS / NW, B_PER = B_INS / NW;
+	constexpr int LOADS = A_PER + B_PER; /* vm ops per wave per stage */
+	constexpr int WTM = BM / WGM, WTN = BN / WGN;
+	constexpr int FM = WTM / 32, FN = WTN / 32;
+	constexpr int KS = BK / 16;
+	static_assert(NW * 32 * (WTN + 8) * 4 <= STAGES * SB, "epilogue staging fits");
+	__shared__ __attribute__((aligned(1024))) char smem[STAGES * SB];
+
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+	const int bz = blockIdx.y;
+	int tm, tn;
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+
+	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+
+	/* Per-lane source of each load instruction (fixed across k). */
+	unsigned a_off[A_PER], b_off[B_PER];
+	int a_k[A_PER], b_k[B_PER];
+#pragma unroll
+	for (int j = 0; j < A_PER; ++j) {
+		const int s = (j * NW + wave) * 64 + lane;
+		const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+		const int g = tm * BM + row;
+		a_off[j] = g < p.M ? (unsigned)(g * p.lda_b + c * 16) : S3K_OOB;
+		a_k[j] = c * 8;
+	}
+#pragma unroll
+	for (int j = 0; j < B_PER; ++j) {
+		const int s = (j * NW + wave) * 64 + lane;
+		const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+		const int g = tn * BN + row;
+		b_off[j] = g < p.N ? (unsigned)(g * p.ldb_b + c * 16) : S3K_OOB;
+		b_k[j] = c * 8;
+	}
+
+	auto issue = [&](int kt) {
+		const int k0 = kt * BK;
+		const bool full = k0 + BK <= p.K;
+		char *st = smem + (kt % STAGES) * SB;
+#pragma unroll
+		for (int j = 0; j < A_PER; ++j) {
+			unsigned o = a_off[j];
+			if (o != S3K_OOB)
+				o = (full || k0 + a_k[j] < p.K) ? o + 2u * k0 : S3K_OOB;
+			dma16(st + (j * NW + wave) * 1024, ra, o);
+		}
+#pragma unroll
+		for (int j = 0; j < B_PER; ++j) {
+			unsigned o = b_off[j];
+			if (o != S3K_OOB)
+				o = (full || k0 + b_k[j] < p.K) ? o + 2u * k0 : S3K_OOB;
+			dma16(st + A_BYTES + (j * NW + wave) * 1024, rb, o);
+		}
+	};
+
+	s3k_f32x16 acc[FM][FN];
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+
+	const int nk = (p.K + BK - 1) / BK;
+#pragma unroll
+	for (int s = 0; s < STAGES - 1; ++s)
+		if (s < nk)
+			issue(s);
+
+	for (int kt = 0; kt < nk; ++kt) {
+		/* own loads of step kt done: at most the younger stages pending */
+		const int younger = min(nk - 1 - kt, STAGES - 2);
+		if (younger >= 2)
+			wait_vm<2 * LOADS>();
+		else if (younger == 1)
+			wait_vm<LOADS>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (kt + STAGES - 1 < nk)
+			issue(kt + STAGES - 1);
+
+		const char *As = smem + (kt % STAGES) * SB;
+		const char *Bs = As + A_BYTES;
+		/* fragments of k-step ks+1 are read while the MFMAs of ks run */
+		uint4 af[2][FM], bfr[2][FN];
+#pragma unroll
+		for (int i = 0; i < FM; ++i)
+			af[0][i] = *(const uint4 *)(As + dl_off<CPR>(wm0 + i * 32 + (lane & 31), lane >> 5));
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+			bfr[0][j] = *(const uint4 *)(Bs + dl_off<CPR>(wn0 + j * 32 + (lane & 31), lane >> 5));
+#pragma unroll
+		for (int ks = 0; ks < KS; ++ks) {
+			const int cur = ks & 1;
+			if (ks + 1 < KS) {
+				const int c = 2 * (ks + 1) + (lane >> 5);
+#pragma unroll
+				for (int i = 0; i < FM; ++i)
+					af[cur ^ 1][i] = *(const uint4 *)(As + dl_off<CPR>(wm0 + i * 32 + (lane & 31), c));
+#pragma unroll
+				for (int j = 0; j < FN; ++j)
+					bfr[cur ^ 1][j] = *(const uint4 *)(Bs + dl_off<CPR>(wn0 + j * 32 + (lane & 31), c));
+			}
+			__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+			for (int i = 0; i < FM; ++i)
+#pragma unroll
+				for (int j = 0; j < FN; ++j)
+					mfma_chunk<FAM>(acc[i][j], af[cur][i], bfr[cur][j]);
+			__builtin_amdgcn_s_setprio(0);
+		}
+	}
+
+	__syncthreads();
+	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int FAM, int CK, int OCC>
+static void launch_dl_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
+{
+	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	hipLaunchKernelGGL((gemm_dl<BM, BN, BK, WGM, WGN, STAGES, FAM, CK, OCC>), grid,
+			   dim3(64 * WGM * WGN), 0, st, p);
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int OCC>
+static int launch_dl_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	p.tiles_m = (p.M + BM - 1) / BM;
+	p.tiles_n = (p.N + BN - 1) / BN;
+	const bool f32_out = g->c_kind == S3K_F32;
+	if (g->a_kind == S3K_BF16) {
+		if (f32_out)
+			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_BF16, S3K_F32, OCC>(g, p, st);
+		else
+			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_BF16, S3K_BF16, OCC>(g, p, st);
+	} else {
+		if (f32_out)
+			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_F16, S3K_F32, OCC>(g, p, st);
+		else
+			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_F16, S3K_F16, OCC>(g, p, st);
+	}
+	return (int)hipGetLastError();
+}
+
+} /* namespace s3k */
+
+using namespace s3k;
+
+/* bf16 x bf16 or f16 x f16, B as [N,K], 16-byte aligned rows, each batch
+ * slice within a 2 GiB buffer range. */
+bool s3k_dl_ok(const struct s3k_gemm *g)
+{
+	if (!(g->flags & S3K_B_NT) || g->a_kind != g->b_kind ||
+	    (g->a_kind != S3K_BF16 && g->a_kind != S3K_F16))
+		return false;
+	if (g->M <= 0 || g->N <= 0 || g->K <= 0 || g->K % 8 || g->batch <= 0)
+		return false;
+	if (((uintptr_t)g->a | (uintptr_t)g->b) & 15u)
+		return false;
+	if ((g->lda * 2LL) % 16 || (g->ldb * 2LL) % 16)
+		return false;
+	if (g->batch > 1 && ((g->stride_a * 2) % 16 || (g->stride_b * 2) % 16))
+		return false;
+	if ((long long)g->M * g->lda * 2 > 0x7FFFFFF0LL || (long long)g->N * g->ldb * 2 > 0x7FFFFFF0LL)
+		return false;
+	return true;
+}
+
+/* Tile shape by a balance model: with two workgroups resident per CU,
+ * a launch of T tiles runs ceil(T / 512) rounds, so the useful fraction is
+ * T / (512 * rounds); the 128x128 tile re-reads more of A and B per flop
+ * (weight 0.93, from measurement on the ViT-L shapes). Candidates:
+ * 256x128 (cfg 0), 128x256 (cfg 3), 128x128 with BK 64 (cfg 4).
+ * SAM3_HIP_DL_CFG forces a configuration (tuning). */
+static int dl_cfg_env = -2;
+
+static double dl_fill(long long tiles)
+{
+	const long long slots = 512;
+	return (double)tiles / ((double)((tiles + slots - 1) / slots) * slots);
+}
+
+int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	if (!s3k_dl_ok(g))
+		return (int)hipErrorInvalidValue;
+	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
+	p.b_extent = (unsigned)((long long)g->N * g->ldb * 2);
+	if (dl_cfg_env == -2) {
+		const char *e = getenv("SAM3_HIP_DL_CFG");
+		dl_cfg_env = e ? atoi(e) : -1;
+	}
+	int cfg = dl_cfg_env;
+	if (cfg < 0) {
+		const long long b = g->batch;
+		const long long t0 = (long long)((g->M + 255) / 256) * ((g->N + 127) / 128) * b;
+		const long long t3 = (long long)((g->M + 127) / 128) * ((g->N + 255) / 256) * b;
+		const long long t4 = (long long)((g->M + 127) / 128) * ((g->N + 127) / 128) * b;
+		const double e0 = dl_fill(t0), e3 = dl_fill(t3), e4 = 0.93 * dl_fill(t4);
+		cfg = e0 >= e3 ? (e0 >= e4 ? 0 : 4) : (e3 >= e4 ? 3 : 4);
+		if (t4 < 64)
+			cfg = 2;
+	}
+	switch (cfg) {
+	case 0:  return launch_dl_cfg<256, 128, 32, 2, 2, 3, 2>(g, p, st);
+	case 1:  return launch_dl_cfg<128, 128, 32, 2, 2, 3, 2>(g, p, st);
+	case 2:  return launch_dl_cfg<64, 64, 32, 2, 2, 3, 2>(g, p, st);
+	case 3:  return launch_dl_cfg<128, 256, 32, 2, 2, 3, 2>(g, p, st);
+	case 4:  return launch_dl_cfg<128, 128, 64, 2, 2, 2, 2>(g, p, st);
+	case 5:  return launch_dl_cfg<256, 256, 32, 2, 2, 4, 1>(g, p, st);
+	case 6:  return launch_dl_cfg<192, 256, 32, 2, 2, 4, 1>(g, p, st);
+	default: return (int)hipErrorInvalidValue;
+	}
+}

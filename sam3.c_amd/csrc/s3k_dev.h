@@ -19,6 +19,20 @@ typedef __attribute__((ext_vector_type(4))) float s3k_f32x4;
 
 namespace s3k {
 
+/* One rounded f32 multiply / add that the compiler may not fuse into an
+ * FMA (clang's __fmul_rn/__fadd_rn are plain, contractable operators). */
+__device__ __forceinline__ float mul_rn(float a, float b)
+{
+#pragma clang fp contract(off)
+	return a * b;
+}
+
+__device__ __forceinline__ float add_rn(float a, float b)
+{
+#pragma clang fp contract(off)
+	return a + b;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t b)
 {
 	return __uint_as_float(b << 16);
@@ -55,13 +69,22 @@ __device__ __forceinline__ float round_f16(float f)
 	return (float)(_Float16)f;
 }
 
+/* tanh(u) = 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal:
+ * a few instructions instead of a library tanhf, relative error near
+ * 1e-7 in 1 + tanh(u), which is what GELU uses. */
+__device__ __forceinline__ float tanh_fast(float u)
+{
+	const float e = __builtin_amdgcn_exp2f(fminf(u, 30.0f) * 2.8853900817779268f); /* 2/ln2 */
+	return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 /* 0.5*x*(1 + tanh(sqrt(2/pi)*(x + 0.044715*x^3))), the reference's
- * operation order. */
+ * operation order (cpu_gelu.c:30-38) around the tanh. */
 __device__ __forceinline__ float gelu_tanh(float x)
 {
-	float cube = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
-	float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, cube));
-	return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+	float cube = mul_rn(mul_rn(mul_rn(0.044715f, x), x), x);
+	float inner = mul_rn(0.7978845608f, add_rn(x, cube));
+	return mul_rn(mul_rn(0.5f, x), add_rn(1.0f, tanh_fast(inner)));
 }
 
 /* Pack two f32 as two f16 (RNE) in one dword, lo first. */
@@ -95,18 +118,18 @@ __device__ __forceinline__ float epilogue(float acc, float bias, int flags)
 	if (CK == 2) { /* BF16 */
 		v = round_bf16(v);
 		if (flags & 1)
-			v = round_bf16(__fadd_rn(v, bias));
+			v = round_bf16(add_rn(v, bias));
 		if (flags & 2)
 			v = round_bf16(gelu_tanh(v));
 	} else if (CK == 1) { /* F16 */
 		v = round_f16(v);
 		if (flags & 1)
-			v = round_f16(__fadd_rn(v, bias));
+			v = round_f16(add_rn(v, bias));
 		if (flags & 2)
 			v = round_f16(gelu_tanh(v));
 	} else {
 		if (flags & 1)
-			v = __fadd_rn(v, bias);
+			v = add_rn(v, bias);
 		if (flags & 2)
 			v = gelu_tanh(v);
 	}

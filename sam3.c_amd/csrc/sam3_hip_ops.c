@@ -95,9 +95,10 @@ static int is_float_dtype(int dt)
 static enum sam3_error check_kinds(int a_dt, int b_dt, int c_dt)
 {
 	if (b_dt == SAM3_DTYPE_Q8_0) {
-		if (!is_float_dtype(a_dt) || !is_float_dtype(c_dt)) {
-			s3h_error("matmul: Q8_0 needs F32/F16/BF16 activations and output "
-				  "(a=%d c=%d)", a_dt, c_dt);
+		/* the Q8 kernels write F32, as cpu_matmul_q8.c:181-185 does */
+		if (!is_float_dtype(a_dt) || c_dt != SAM3_DTYPE_F32) {
+			s3h_error("matmul: Q8_0 needs F32/F16/BF16 activations and an F32 "
+				  "output (a=%d c=%d)", a_dt, c_dt);
 			return SAM3_EDTYPE;
 		}
 		return SAM3_OK;

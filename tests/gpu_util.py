@@ -34,21 +34,31 @@ def ulp_f16(x):
     return 2.0 ** (e - 10)
 
 
-def assert_f32_close(got, ref, rtol=1e-3, what=""):
-    """|g - r| <= rtol*|r| + rtol*rms(r) elementwise (the reference's
-    atol + rtol*|expected| form, tests/test_helpers.h:89-108, with the atol
-    set relative to the output's scale), plus cosine >= 0.9999
-    (tests/test_metal.c:252)."""
+def assert_f32_close(got, ref, rtol=1e-3, floor=2e-3, what=""):
+    """f32 outputs against the reference, three conditions:
+      1. max relative error (normwise) max|g - r| / max|r| <= rtol: the
+         north-star bound "max relative error 1e-3";
+      2. elementwise |g - r| <= rtol*|r| + floor*rms(r): the reference's
+         atol + rtol*|expected| form (tests/test_helpers.h:89-108) with
+         the atol tied to the output's scale, since a reordered sum has
+         unbounded relative error where the output crosses zero;
+      3. cosine >= 0.9999 (tests/test_metal.c:252).
+    The f16-operand Q8 GEMM rounds A and q*scale to f16 (2^-11 each), an
+    expected normwise error near 3e-4."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
-    rms = np.sqrt(np.mean(ref ** 2)) if ref.size else 0.0
+    if ref.size == 0:
+        return
     err = np.abs(got - ref)
-    lim = rtol * np.abs(ref) + rtol * rms
+    amax = max(np.abs(ref).max(), 1e-30)
+    assert err.max() <= rtol * amax, f"{what}: max normwise error {err.max() / amax:.3e} > {rtol}"
+    rms = np.sqrt(np.mean(ref ** 2))
+    lim = rtol * np.abs(ref) + floor * rms
     bad = err > lim
-    assert not bad.any(), (f"{what}: {bad.sum()} / {bad.size} outside tolerance; max err "
-                           f"{err.max():.3e}, max normwise {err.max() / max(np.abs(ref).max(), 1e-30):.3e}")
+    assert not bad.any(), (f"{what}: {bad.sum()} / {bad.size} outside elementwise bound; "
+                           f"max err {err.max():.3e}, max normwise {err.max() / amax:.3e}")
     if ref.size > 1 and rms > 0:
         cos = (got * ref).sum() / (np.linalg.norm(got) * np.linalg.norm(ref))
         assert cos >= 0.9999, f"{what}: cosine {cos}"

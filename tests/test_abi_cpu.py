@@ -58,7 +58,8 @@ def test_struct_layouts_match_reference_sizes():
     ((abi.F32, abi.Q8_0, abi.F32, 512, 512, 512, 0), hip.PATH_MFMA),   # unpacked to f16
     ((abi.F32, abi.F32, abi.F32, 7, 5, 13, 0), hip.PATH_GENERIC),
     ((abi.F16, abi.F16, abi.F16, 19, 23, 70, 0), hip.PATH_GENERIC),
-    ((abi.BF16, abi.Q8_0, abi.BF16, 8, 8, 8, 0), hip.PATH_GENERIC),
+    ((abi.BF16, abi.Q8_0, abi.F32, 8, 8, 8, 0), hip.PATH_GENERIC),
+    ((abi.BF16, abi.Q8_0, abi.BF16, 8, 8, 8, 0), hip.PATH_NONE),     # Q8 writes F32
     ((abi.F32, abi.BF16, abi.F32, 8, 8, 8, 0), hip.PATH_NONE),      # mixed dense dtypes
     ((abi.I32, abi.I32, abi.I32, 8, 8, 8, 0), hip.PATH_NONE),
 ])

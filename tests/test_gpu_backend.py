@@ -14,8 +14,11 @@ from sam3_amd import abi, hip, synth
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
+@pytest.fixture
 def be():
+    """A fresh backend per test: the weight cache is keyed by host address
+    and these tests free and reuse host buffers without calling
+    cache_invalidate (which sam3.c does when it recycles arena memory)."""
     require_gpu()
     b = hip.Backend(0)
     yield b

@@ -111,7 +111,7 @@ def test_golden_dense_tiled():
     assert hip.matmul_path(abi.F32, abi.F32, abi.F32, M, N, K) == GENERIC  # N=65, K=200
     a, b = GOLD["f32b_a"][:, :128], GOLD["f32b_b"][:128, :64]
     c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, 33, 64, 128, path=MFMA)
-    assert_f32_close(c, oracle().matmul_f32(a, b), what="f32 tiled")
+    assert_f32_close(c, oracle().matmul_f32(a, b), rtol=1e-5, floor=1e-5, what="f32 tiled")
 
 
 def test_golden_f16_generic_equals_acc32_oracle():
@@ -170,7 +170,8 @@ def test_f32_tiled_vs_oracle(M, N, K, nt):
         pytest.skip("shape not on the tiled path")
     c = hip.matmul(a, abi.F32, b, abi.F32, abi.F32, M, N, K, flags=hip.B_NT if nt else 0,
                    path=MFMA)
-    assert_f32_close(c, ref_linear("f32", a, b, b_nt=nt), what=f"f32 {M}x{N}x{K}")
+    assert_f32_close(c, ref_linear("f32", a, b, b_nt=nt), rtol=1e-5, floor=1e-5,
+                     what=f"f32 {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("kind", ["bf16", "f16", "f32"])
@@ -230,7 +231,7 @@ def test_q8_nt_tiled_bf16_and_f16_activations(M, N, K):
     w = q8(rnd(101 + N, (N, K), 0.02))
     ab = O.f32_to_bf16(a32).reshape(M, K)
     ref = ref_q8(bf16_to_f32(ab).reshape(M, K), w, K, N, nt=True)
-    for path in (MFMA, SKINNY):
+    for path in (MFMA, SKINNY) if M <= 128 else (MFMA,):
         c = hip.matmul(ab, abi.BF16, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=path)
         assert_f32_close(c, ref, what=f"q8 bf16-act path {path}")
     ah = O.f32_to_fp16(a32).reshape(M, K)
