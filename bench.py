@@ -10,8 +10,9 @@ reported under "extra":
   config 2  bf16/f16 fc1 and fc2, plain and with fused bias+GELU
   config 3  32 ViT-L layers x {qkv, proj, fc1, fc2}, Q8 weights (distinct
             per layer, 453 MB streamed from HBM), bf16 activations
-  config 4  skinny Q8 GEMVs (M in {1,8,32,77}) over a rotating pool of
-            >256 MB of weight copies, reported in HBM GB/s
+  config 4  skinny Q8 GEMVs (M in {1,8,32,77}) over a pool of >256 MB of
+            distinct weight copies, reported in HBM GB/s per launch (HIP graph
+            of one launch per copy) and for one batched launch
   config 5  batched attention QK^T / PV, windowed (1296 x 576 x 64)
 `roofline` is for the headline kernel; `cpu_baseline` times the reference
 CPU bf16 kernel (oracle/_ref, compiled from the reference's own sources)
@@ -142,6 +143,100 @@ def measured_traffic(key):
         return None
 
 
+class HipGraph:
+    """Stream capture into a HIP graph, through the HIP runtime our library
+    already loaded (bench plumbing: replaying a captured sequence of
+    launches removes the per-call host cost from the measurement)."""
+
+    def __init__(self, stream, record):
+        import ctypes as C
+        self.rt = rt = C.CDLL("libamdhip64.so.7")
+        vp = C.c_void_p
+        rt.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        rt.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+        rt.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, vp, C.c_size_t]
+        rt.hipGraphLaunch.argtypes = [vp, vp]
+        rt.hipGraphExecDestroy.argtypes = [vp]
+        rt.hipGraphDestroy.argtypes = [vp]
+        self.stream = stream
+        self.graph, self.exec = C.c_void_p(), C.c_void_p()
+        self._ok(rt.hipStreamBeginCapture(stream, 2), "begin capture")
+        try:
+            record()
+        finally:
+            self._ok(rt.hipStreamEndCapture(stream, C.byref(self.graph)), "end capture")
+        self._ok(rt.hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0),
+                 "instantiate")
+
+    @staticmethod
+    def _ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"HIP graph {what}: error {rc}")
+
+    def launch(self):
+        self._ok(self.rt.hipGraphLaunch(self.exec, self.stream), "launch")
+
+    def close(self):
+        self.rt.hipGraphExecDestroy(self.exec)
+        self.rt.hipGraphDestroy(self.graph)
+
+
+def skinny_stream(lib, stream, O, use_graph=True):
+    """Q8 weights [N,K] (36-byte blocks), f32
+    activations [M,K], M in {1,8,32,77}. Each shape streams `copies`
+    distinct weight copies (> 256 MB in total, so the MALL cannot hold
+    them) and reports bytes / time with bytes = W + 4MK + 4MN per call:
+      graph_*    one launch per weight copy, the launches captured in a HIP
+                 graph and replayed (what a decoder layer loop sees); with
+                 use_graph False the launches are issued one by one instead
+                 ("eager_*", host launch cost included);
+      batched_*  all copies in one sam3_hip_matmul_q8_batched launch (the
+                 kernel's streaming rate without per-launch cost);
+      launch_us  the difference per call: the per-launch cost."""
+    timer = Timer(stream)
+    out = {}
+    for (kk, nn) in [(4096, 1024), (1024, 4096), (1024, 1024), (256, 2048), (256, 256)]:
+        wq = O.q8_quantize(synth.randn(synth.tensor_seed(4, kk + nn), (nn, kk), 0.02))
+        wb = wq.nbytes
+        copies = min(4096, max(16, int(300e6 // wb) + 1))
+        pool = hip.DeviceBuffer(wb * copies)
+        for i in range(copies):
+            hip.check(lib.sam3_hip_memcpy_h2d(pool.ptr + i * wb, wq.ctypes.data, wb), "h2d")
+        for m in (1, 8, 32, 77):
+            xa = hip.DeviceBuffer.of(synth.randn(synth.tensor_seed(4, m), (m, kk)))
+            yc = hip.DeviceBuffer(m * nn * 4 * copies)
+
+            def calls():
+                for i in range(copies):
+                    hip.matmul_dev(abi.F32, xa.ptr, abi.Q8_0, pool.ptr + i * wb, abi.F32,
+                                   yc.ptr + i * m * nn * 4, m, nn, kk, None, hip.B_NT, stream)
+
+            if use_graph:
+                g = HipGraph(stream, calls)
+                ms_g = timer.run(g.launch, 3, 1) / copies
+                g.close()
+            else:
+                ms_g = timer.run(calls, 3, 1) / copies
+            mode = "graph" if use_graph else "eager"
+
+            def batched():
+                hip.q8_batched_dev(abi.F32, xa.ptr, pool.ptr, yc.ptr, copies, m, nn, kk,
+                                   0, wb, m * nn, None, 0, stream)
+
+            ms_b = timer.run(batched, 3, 1) / copies
+            byts = wb + 4 * m * kk + 4 * m * nn
+            out[f"M{m}_K{kk}_N{nn}"] = {
+                f"{mode}_us": round(ms_g * 1e3, 3),
+                f"{mode}_gbs": round(byts / (ms_g * 1e-3) / 1e9, 1),
+                "batched_us": round(ms_b * 1e3, 3),
+                "batched_gbs": round(byts / (ms_b * 1e-3) / 1e9, 1),
+                "launch_us": round((ms_g - ms_b) * 1e3, 3)}
+            log(f"  M{m} K{kk} N{nn}: {out[f'M{m}_K{kk}_N{nn}']}")
+            xa.free(); yc.free()  # noqa: E702
+        pool.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,7 +244,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only, no extra configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="config 4: issue the per-copy launches directly, not from a HIP graph")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5",
+                    help="comma list of extra sections to run (cfg1..cfg5)")
     args = ap.parse_args()
+    only = set(args.only.split(","))
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this backend is measured on one GPU only; multi-GPU sharding is a "
@@ -180,8 +280,8 @@ def main():
     log(f"  {ms * 1e3:.1f} us/step  {value:.1f} TFLOP/s")
 
     extra = {}
-    if not args.quick:
-        steps2, warm2 = max(10, K_ // 4), max(3, W_ // 2)
+    steps2, warm2 = max(10, K_ // 4), max(3, W_ // 2)
+    if not args.quick and "cfg2" in only:
         bias = bf16_bits(synth.randn(synth.tensor_seed(2, 2), N, 0.01))
         log("config 2 variants")
         ms_e = gemm_case(stream, timer, abi.BF16, a_bf, abi.BF16, w_bf, abi.BF16, M, N, K,
@@ -200,9 +300,9 @@ def main():
         extra["cfg2_f16_fc1_tflops"] = round(tflops(M, N, K, ms_h), 2)
         del a2, w2
 
+    O = hip  # Q8 weights are quantized on the device (sam3_hip_q8_quantize)
+    if not args.quick and "cfg1" in only:
         log("config 1 / Q8")
-        from oracle_bind import Oracle  # the quantizer only prepares inputs
-        O = Oracle()
         a1 = synth.randn(0, (5184, 1024))
         wq1 = O.q8_quantize(synth.randn(1, (1024, 1024), 0.02))
         ms1 = gemm_case(stream, timer, abi.F32, a1, abi.Q8_0, wq1, abi.F32, 5184, 1024, 1024,
@@ -216,6 +316,7 @@ def main():
                         hip.B_NT, steps2, warm2)
         extra["q8_bf16act_fc1_5184x1024x4096_tflops"] = round(tflops(M, N, K, msq), 2)
 
+    if not args.quick and "cfg3" in only:
         log("config 3: 32 layers, distinct Q8 weights")
         shapes = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
         wbase = {s: O.q8_quantize(synth.randn(synth.tensor_seed(3, i), s, 0.02))
@@ -241,33 +342,11 @@ def main():
                 b.free()
         act1.free(); act4.free(); out.free()  # noqa: E702
 
-        log("config 4: skinny Q8 stream")
-        sk = {}
-        for (kk, nn) in [(4096, 1024), (1024, 4096), (1024, 1024), (256, 2048), (256, 256)]:
-            wq = O.q8_quantize(synth.randn(synth.tensor_seed(4, kk + nn), (nn, kk), 0.02))
-            copies = max(8, int(300e6 // wq.nbytes) + 1)
-            copies = min(copies, 4096)
-            pool = hip.DeviceBuffer(wq.nbytes * copies)
-            for i in range(copies):
-                hip.check(lib.sam3_hip_memcpy_h2d(pool.ptr + i * wq.nbytes, wq.ctypes.data,
-                                                  wq.nbytes), "h2d")
-            for m in (1, 8, 32, 77):
-                xa = hip.DeviceBuffer.of(synth.randn(synth.tensor_seed(4, m), (m, kk)))
-                yc = hip.DeviceBuffer(m * nn * 4)
+    if not args.quick and "cfg4" in only:
+        log("config 4: skinny Q8 (stream of distinct weight copies)")
+        extra["cfg4_skinny_q8"] = skinny_stream(lib, stream, O, not args.no_graph)
 
-                def stream_calls():
-                    for i in range(copies):
-                        hip.matmul_dev(abi.F32, xa.ptr, abi.Q8_0, pool.ptr + i * wq.nbytes,
-                                       abi.F32, yc.ptr, m, nn, kk, None, hip.B_NT, stream)
-
-                msk = timer.run(stream_calls, 2, 1) / copies
-                byts = wq.nbytes + 4 * m * kk + 4 * m * nn
-                sk[f"M{m}_K{kk}_N{nn}"] = {"us_per_call": round(msk * 1e3, 3),
-                                           "gbs": round(byts / (msk * 1e-3) / 1e9, 1)}
-                xa.free(); yc.free()  # noqa: E702
-            pool.free()
-        extra["cfg4_skinny_q8_stream"] = sk
-
+    if not args.quick and "cfg5" in only:
         log("config 5: attention matmuls (windowed)")
         BH, S, D = 1296, 576, 64
         qk = bf16_bits(synth.randn(synth.tensor_seed(5, 0), (BH, S, D)) / 8)

@@ -141,6 +141,23 @@ enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b,
 					long long stride_a, long long stride_b,
 					long long stride_c, int flags, void *stream);
 
+/*
+ * Strided batch of Q8_0 weight matmuls: for s in [0, batch),
+ * C_s[M,N] (F32) = A_s[M,K] * W_s^T (+bias) (GELU), with W_s[N,K] Q8_0
+ * blocks along k (K % 32 == 0) at a byte stride stride_w, A_s at element
+ * stride stride_a (a_dtype F32, F16 or BF16), C_s at element stride
+ * stride_c, one bias[N] (F32) for every slice. Small M (<= 128) runs as
+ * one launch of the bandwidth-bound kernel over all slices; otherwise one
+ * launch per slice. No counterpart in the reference: it runs a stream of
+ * layers' or heads' weights (graph_helpers.c:297-320 once per weight)
+ * without a launch per weight. flags: SAM3_HIP_BIAS | SAM3_HIP_GELU.
+ */
+enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const void *w,
+					   void *c, int batch, int M, int N, int K,
+					   long long stride_a, long long stride_w,
+					   long long stride_c, const void *bias, int flags,
+					   void *stream);
+
 /* Which kernel sam3_hip_matmul would launch for this problem:
  * 1 = tiled MFMA, 2 = skinny (small-M Q8), 3 = generic, 0 = none. */
 int sam3_hip_matmul_path(int a_dtype, int b_dtype, int c_dtype,
@@ -154,6 +171,22 @@ enum sam3_error sam3_hip_matmul_on_path(int path, int a_dtype, const void *a,
 					int c_dtype, void *c,
 					int M, int N, int K,
 					const void *bias, int flags, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Q8_0 format on the device (device pointers, async on `stream`).      */
+/* ------------------------------------------------------------------ */
+
+/* Quantize nelems f32 values into ceil(nelems/32) 36-byte blocks over the
+ * flat index. Replaces sam3_q8_quantize (src/core/quant.c:67-130),
+ * bit-exact with its x86 build (roundf, halves away from zero). Pointers
+ * 4-byte aligned. */
+enum sam3_error sam3_hip_q8_quantize(const float *src, void *dst_blocks, int nelems,
+				     void *stream);
+
+/* x = (float)q * scale for nelems values. Replaces sam3_q8_dequantize
+ * (src/core/quant.c:134-165). Pointers 4-byte aligned. */
+enum sam3_error sam3_hip_q8_dequantize(const void *src_blocks, float *dst, int nelems,
+				       void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Device memory, streams and events for FFI callers (no counterpart    */

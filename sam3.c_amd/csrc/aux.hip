@@ -6,11 +6,15 @@
  *     reference kernel contract, cpu_matmul_q8.c:29-35) and W[N,K] with
  *     K % 32 != 0 (blocks straddle rows). Output is f16 [N,K], value
  *     q*scale rounded once to f16 (src/core/quant.c:134-165 gives q*scale).
+ *   - Q8_0 quantize / dequantize of flat f32 arrays on the device
+ *     (src/core/quant.c:67-165), bit-exact with the reference's x86 build;
  *   - bias add over the last dim, same-shape add, tanh-GELU and 2-D
  *     transpose, with the reference's per-op rounding
  *     (cpu_elementwise.c:28-63, cpu_add_bf16.c:62-63, cpu_gelu.c:23-38,
  *     cpu_transpose.c:355-366), used when a graph pattern cannot fuse.
  */
+#include <limits.h>
+
 #include "s3k.h"
 #include "s3k_dev.h"
 
@@ -31,6 +35,80 @@ __global__ void __launch_bounds__(256) q8_to_f16_nk(const char *blk, uint16_t *o
 	const float s = *(const float *)b;
 	const float q = (float)(int)(int8_t)b[4 + (lin & 31)];
 	out[i] = (uint16_t)f32_to_f16(q * s);
+}
+
+/*
+ * Q8_0 quantization of a flat f32 array, the x86 branch of
+ * sam3_q8_quantize (src/core/quant.c:67-130): per block of 32,
+ * amax = max |x| over the block's elements (NaN never wins, as with
+ * `if (a > amax)`), scale = amax / 127.0f, and if scale != 0,
+ * q = clamp((int)roundf(x * (1.0f / scale)), -127, 127) with roundf
+ * rounding halves away from zero. (int) of a NaN or of a value outside the
+ * int range gives INT_MIN there (cvttss2si), which the clamp maps to -127;
+ * the same rule is applied here. Elements past n, and whole blocks with a
+ * zero scale, store q = 0. Eight lanes per block, four elements per lane:
+ * the block's amax is a max over the 8 lanes (exact in any order), and
+ * each lane stores its four q as one dword.
+ */
+__global__ void __launch_bounds__(256) q8_quantize_k(const float *src, char *dst, int n)
+{
+	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+	const long long b = t >> 3;
+	const int part = (int)(t & 7);
+	if (b >= ((long long)n + 31) / 32)
+		return; /* whole 8-lane groups leave together */
+	const long long e0 = b * 32 + part * 4;
+	float x[4];
+	float amax = 0.0f;
+#pragma unroll
+	for (int i = 0; i < 4; ++i) {
+		x[i] = e0 + i < n ? src[e0 + i] : 0.0f;
+		const float a = fabsf(x[i]);
+		if (e0 + i < n && a > amax)
+			amax = a;
+	}
+#pragma unroll
+	for (int o = 1; o < 8; o <<= 1) {
+		const float v = __shfl_xor(amax, o, 8);
+		if (v > amax)
+			amax = v;
+	}
+	const float scale = amax / 127.0f;
+	char *blk = dst + b * 36;
+	if (part == 0)
+		*(float *)blk = scale;
+	uint32_t word = 0;
+	if (scale != 0.0f) {
+		const float inv = 1.0f / scale;
+#pragma unroll
+		for (int i = 0; i < 4; ++i) {
+			if (e0 + i >= n)
+				continue;
+			const float r = roundf(x[i] * inv);
+			int q = (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : INT_MIN;
+			q = q > 127 ? 127 : q < -127 ? -127 : q;
+			word |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
+		}
+	}
+	*(uint32_t *)(blk + 4 + 4 * part) = word;
+}
+
+/* x = (float)q * scale (src/core/quant.c:134-165), four per lane. */
+__global__ void __launch_bounds__(256) q8_dequantize_k(const char *src, float *dst, int n)
+{
+	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+	const long long b = t >> 3;
+	const int part = (int)(t & 7);
+	if (b >= ((long long)n + 31) / 32)
+		return;
+	const char *blk = src + b * 36;
+	const float s = *(const float *)blk;
+	const uint32_t w = *(const uint32_t *)(blk + 4 + 4 * part);
+	const long long e0 = b * 32 + part * 4;
+#pragma unroll
+	for (int i = 0; i < 4; ++i)
+		if (e0 + i < n)
+			dst[e0 + i] = (float)(int)(int8_t)(w >> (8 * i)) * s;
 }
 
 template <int KIND>
@@ -110,6 +188,26 @@ extern "C" int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N, 
 		return 0;
 	hipLaunchKernelGGL(q8_to_f16_nk<false>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
 			   (const char *)blocks, (uint16_t *)out, K, N);
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_q8_quantize(const void *src, void *dst, int n, void *stream)
+{
+	if (n <= 0)
+		return 0;
+	const long long lanes = ((long long)n + 31) / 32 * 8;
+	hipLaunchKernelGGL(q8_quantize_k, grid1(lanes), dim3(256), 0, (hipStream_t)stream,
+			   (const float *)src, (char *)dst, n);
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream)
+{
+	if (n <= 0)
+		return 0;
+	const long long lanes = ((long long)n + 31) / 32 * 8;
+	hipLaunchKernelGGL(q8_dequantize_k, grid1(lanes), dim3(256), 0, (hipStream_t)stream,
+			   (const char *)src, (float *)dst, n);
 	return (int)hipGetLastError();
 }
 

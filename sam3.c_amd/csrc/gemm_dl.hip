@@ -24,52 +24,15 @@
  *   - Epilogue through LDS with 16-byte stores (gemm_common.h).
  */
 #include "gemm_common.h"
+#include "lds_dma.h"
 
 namespace s3k {
-
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-typedef int s3k_i32x4 __attribute__((ext_vector_type(4)));
-
-/* Buffer descriptor of a raw byte range (gfx9 layout: base, stride 0,
- * num_records = bytes, dword3 = 0x00020000); offsets >= bytes load 0. */
-__device__ __forceinline__ s3k_i32x4 buf_rsrc(const void *base, unsigned bytes)
-{
-	const unsigned long long a = (unsigned long long)base;
-	return (s3k_i32x4){(int)(unsigned)a, (int)(unsigned)(a >> 32), (int)bytes, 0x00020000};
-}
-
-/* 16 bytes per lane from global (rsrc + voff) into LDS at lds + 16*lane.
- * Issued as inline asm so the compiler does not treat the LDS image as
- * written here: the kernel orders it with explicit vmcnt waits and a
- * barrier (the builtin form makes the compiler wait for every pending
- * load before any LDS read). */
-__device__ __forceinline__ void dma16(const void *lds, s3k_i32x4 rsrc, unsigned voff)
-{
-	const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)lds);
-	asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-		     :: "s"(m0), "v"(voff), "s"(rsrc) : "memory");
-}
-
-/* s_waitcnt vmcnt(N) with lgkm/exp counters left alone. */
-template <int N>
-__device__ __forceinline__ void wait_vm()
-{
-	static_assert(N >= 0 && N < 64, "vmcnt range");
-	__builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-__device__ __forceinline__ void wg_barrier()
-{
-	asm volatile("s_barrier" ::: "memory");
-}
 
 template <int CPR>
 __device__ __forceinline__ int dl_off(int row, int c)
 {
 	return (row * CPR + (c ^ lds_swz<CPR>(row))) << 4;
 }
-
-#define S3K_OOB 0x80000000u /* buffer offset beyond any range: loads zero */
 
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int FAM, int CK, int OCC>
 __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)

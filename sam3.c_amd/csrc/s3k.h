@@ -78,6 +78,9 @@ int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N,
 
 /* Elementwise ops the fused graph paths fall back to when they cannot
  * fuse (reference semantics, one rounding per op). */
+/* Q8_0 quantize / dequantize of n f32 values (blocks over the flat index). */
+int s3k_q8_quantize(const void *src, void *dst, int n, void *stream);
+int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream);
 int s3k_bias_add(int kind, const void *x, const void *bias, void *out,
 		 long long rows, int n, void *stream);
 int s3k_add_same(int kind, const void *x, const void *y, void *out,

@@ -22,6 +22,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <stdint.h>
 #include <string.h>
 
 static _Thread_local char g_last_error[320];
@@ -275,6 +276,83 @@ enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b,
 	g.stride_b = stride_b;
 	g.stride_c = stride_c;
 	return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_batched");
+}
+
+enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const void *w,
+					   void *c, int batch, int M, int N, int K,
+					   long long stride_a, long long stride_w,
+					   long long stride_c, const void *bias, int flags,
+					   void *stream)
+{
+	if (batch < 0 || M < 0 || N < 0 || K < 0 || stride_a < 0 || stride_w < 0 || stride_c < 0) {
+		s3h_error("matmul_q8_batched: negative size or stride");
+		return SAM3_EINVAL;
+	}
+	if (batch == 0 || M == 0 || N == 0)
+		return SAM3_OK;
+	if (!a || !w || !c || ((flags & SAM3_HIP_BIAS) && !bias)) {
+		s3h_error("matmul_q8_batched: NULL pointer");
+		return SAM3_EINVAL;
+	}
+	if (!is_float_dtype(a_dtype)) {
+		s3h_error("matmul_q8_batched: unsupported activation dtype %d", a_dtype);
+		return SAM3_EDTYPE;
+	}
+	if (K % 32) {
+		s3h_error("matmul_q8_batched: K=%d is not a multiple of 32", K);
+		return SAM3_EINVAL;
+	}
+	flags = (flags & (SAM3_HIP_BIAS | SAM3_HIP_GELU)) | SAM3_HIP_B_NT;
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dtype, a, SAM3_DTYPE_Q8_0, w, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
+	g.batch = batch;
+	g.stride_a = stride_a;
+	g.stride_b = stride_w;
+	g.stride_c = stride_c;
+	if (s3k_gemm_path(&g) == S3K_PATH_SKINNY)
+		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched");
+	/* one launch per slice on the kernel sam3_hip_matmul picks */
+	const size_t es = s3h_dtype_size(a_dtype);
+	for (int s = 0; s < batch; ++s) {
+		enum sam3_error err = matmul_impl(
+			0, a_dtype, (const char *)a + (size_t)s * stride_a * es, SAM3_DTYPE_Q8_0,
+			(const char *)w + (size_t)s * stride_w, SAM3_DTYPE_F32,
+			(float *)c + (size_t)s * stride_c, M, N, K, bias, flags, stream);
+		if (err != SAM3_OK)
+			return err;
+	}
+	return SAM3_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* Q8_0 format on the device                                            */
+/* ------------------------------------------------------------------ */
+enum sam3_error sam3_hip_q8_quantize(const float *src, void *dst_blocks, int nelems,
+				     void *stream)
+{
+	if (nelems < 0 || (nelems > 0 && (!src || !dst_blocks))) {
+		s3h_error("q8_quantize: NULL pointer or negative size");
+		return SAM3_EINVAL;
+	}
+	if (((uintptr_t)src & 3u) || ((uintptr_t)dst_blocks & 3u)) {
+		s3h_error("q8_quantize: pointers must be 4-byte aligned");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_q8_quantize(src, dst_blocks, nelems, stream), "q8_quantize");
+}
+
+enum sam3_error sam3_hip_q8_dequantize(const void *src_blocks, float *dst, int nelems,
+				       void *stream)
+{
+	if (nelems < 0 || (nelems > 0 && (!src_blocks || !dst))) {
+		s3h_error("q8_dequantize: NULL pointer or negative size");
+		return SAM3_EINVAL;
+	}
+	if (((uintptr_t)src_blocks & 3u) || ((uintptr_t)dst & 3u)) {
+		s3h_error("q8_dequantize: pointers must be 4-byte aligned");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_q8_dequantize(src_blocks, dst, nelems, stream), "q8_dequantize");
 }
 
 /* ------------------------------------------------------------------ */

@@ -7,25 +7,43 @@
  * 374-422), i.e. the weight of gh_linear after its transpose is fused.
  * Reference arithmetic: cpu_matmul_q8.c:124-131, c += (a*q)*scale.
  *
- * Layout of the work:
- *   - a workgroup owns 16*NTW weight rows (n) and WV waves; wave w walks
- *     the k-blocks w, w+WV, ..., so the WV waves of a workgroup read
- *     neighbouring 36-byte blocks of the same rows together;
- *   - per k-block a lane (n = l & 15, k-group g = l >> 4) reads the f32
- *     scale and 8 int8 of row n, turns them into exact f16 integers with
- *     one byte permute and one packed f16 subtract per pair (the bytes are
- *     biased by 128 and placed under the f16 exponent of 1024, then
- *     1152 is subtracted), and feeds v_mfma_f32_16x16x32_f16 against the
- *     A chunk of each 16-row m-tile (f32/bf16 -> f16 in registers);
- *   - the block's scale is applied in f32 to the MFMA result
- *     (acc += s * sum_k a*q), so q is exact and only A is rounded to f16;
- *   - the WV partial sums are reduced through LDS in a fixed order
- *     (deterministic), then bias/GELU are applied and C is written.
- * HBM traffic is the weight stream (36 bytes per 32 weights) plus A once
- * per workgroup (from L2) and C once.
+ * Both kernels feed v_mfma_f32_16x16x32_f16 with exact integers: per
+ * k-block a lane takes the f32 scale and 8 int8 of one weight row and
+ * turns the bytes into f16 with one byte permute and one packed f16
+ * subtract per pair (the bytes are biased by 128 and placed under the f16
+ * exponent of 1024, then 1152 is subtracted). The block's scale is applied
+ * in f32 to the MFMA result (acc += s * sum_k a*q), so q is exact and only
+ * A is rounded to f16. Partial sums of the waves of a workgroup are reduced
+ * through LDS in a fixed order, so results are deterministic.
+ *
+ * q8_stream (K % 256 == 0, 16-byte aligned W): the streaming kernel.
+ *   - A workgroup owns NR = 16*NT weight rows and MR activation rows and
+ *     walks k in chunks of KC = 8 or 16 blocks (256 or 512 k). Per chunk
+ *     it moves the raw 36-byte blocks of its rows (KC * 36 contiguous
+ *     bytes per row) and the A chunk (MR rows) straight into LDS with
+ *     buffer_load ... lds, 16 bytes per lane, no VGPR staging; rows past
+ *     N or M read zeros. The 16 waves of a workgroup share the loads and
+ *     split the chunk's k-blocks; a wave issues all its MFMAs before the
+ *     scale FMAs, so the blocks' latencies overlap.
+ *   - A ring of ST chunks keeps the whole LDS budget in flight (waits are
+ *     explicit vmcnt counts, so a wave only waits for its own oldest
+ *     chunk).
+ *   - The A image is XOR-swizzled per row (16-byte slot ^ (row & 15)), so
+ *     the fragment reads of 16 rows hit 16 different bank groups.
+ *   - M > MR is split over workgroups; the workgroups that share weight
+ *     rows are given ids on the same XCD so the re-reads hit its L2.
+ *   - The grid's y dimension walks a batch of independent problems
+ *     (weights at a byte stride), which is how a stream of layers or heads
+ *     runs in one launch.
+ * q8_skinny (other K or alignment): per k-block global loads, one
+ * workgroup per 16*NTW rows.
  */
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "s3k.h"
 #include "s3k_dev.h"
+#include "lds_dma.h"
 
 namespace s3k {
 
@@ -165,13 +183,282 @@ __global__ void __launch_bounds__(WV * 64) q8_skinny(SkinnyArgs p)
 	}
 }
 
+
+/* ------------------------------------------------------------------ */
+/* q8_stream                                                            */
+/* ------------------------------------------------------------------ */
+
+struct StreamArgs {
+	const char *a;
+	const char *w;
+	char       *c;
+	const char *bias;
+	int M, N, K;
+	int lda_b;                 /* A row pitch, bytes                      */
+	long long ldc;             /* C row pitch, elements                   */
+	long long sa_b, sw_b, sc;  /* batch strides: bytes, bytes, elements   */
+	unsigned w_ext;            /* bytes of one weight matrix (< 2 GiB)    */
+	int flags;
+	int groups;                /* weight-row groups: ceil(N / NR)         */
+	int zsplit;                /* activation-row groups: ceil(M / MR)     */
+};
+
+template <int AK, int MR, int NT, int KC>
+struct StreamCfg {
+	static constexpr int ES = AK == S3K_F32 ? 4 : 2;
+	static constexpr int WV = 16;                    /* waves per workgroup      */
+	static constexpr int CW = WV < KC ? WV : KC;     /* waves that multiply      */
+	static constexpr int U = KC / CW;                /* k-blocks per wave, chunk */
+	static constexpr int NR = 16 * NT;               /* weight rows              */
+	static constexpr int MT = (MR + 15) / 16;        /* 16-row MFMA tiles of A   */
+	static constexpr int GPRW = KC * 36 / 16;        /* 16-B slots of a W row    */
+	static constexpr int PW = GPRW + 1;              /* LDS row pitch, slots     */
+	static constexpr int GW = NR * PW;
+	static constexpr int IW = (GW + 63) / 64;        /* KiB of W per chunk       */
+	static constexpr int GAR = KC * 32 * ES / 16;    /* 16-B slots per A row     */
+	static constexpr int GA = MR * GAR;
+	static constexpr int IA = (GA + 63) / 64;        /* KiB of A per chunk       */
+	static constexpr int I = IW + IA;
+	static constexpr int NPW = (I + WV - 1) / WV;    /* loads per wave per chunk */
+	static constexpr int SW = IW * 1024, SB = I * 1024;
+	/* ring budget ~76 KiB: two workgroups per CU, so one's start hides
+	 * the other's drain (a deeper ring measured no faster) */
+	static constexpr int ST0 = (76 * 1024) / SB;
+	static constexpr int ST1 = ST0 < 2 ? 2 : ST0 > 16 ? 16 : ST0;
+	static constexpr int ST = (ST1 - 1) * NPW > 63 ? 63 / NPW + 1 : ST1; /* ring depth */
+	static constexpr int RED = WV * NT * MT * 1024;
+	static constexpr int LDS = ST * SB + 1024 > RED ? ST * SB + 1024 : RED;
+	static_assert(KC == 8 || KC == 16, "chunk of 8 or 16 k-blocks");
+	static_assert(GAR >= 16 && (GAR & (GAR - 1)) == 0, "A rows hold 2^n >= 16 slots");
+	static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+template <int AK, int MR, int NT, int KC>
+__global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
+{
+	using C = StreamCfg<AK, MR, NT, KC>;
+	constexpr int WV = C::WV;
+	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int g16 = lane >> 4, l16 = lane & 15;
+
+	/* workgroup -> (row group gi, activation group z); the zsplit
+	 * workgroups of one row group get ids = x (mod 8), i.e. one XCD. */
+	int gi, z;
+	{
+		const int id = blockIdx.x, Z = p.zsplit, G8 = (p.groups / 8) * 8;
+		if (id < G8 * Z) {
+			const int x = id % 8, r = id / 8;
+			gi = (r / Z) * 8 + x;
+			z = r % Z;
+		} else {
+			const int rem = id - G8 * Z;
+			gi = G8 + rem / Z;
+			z = rem % Z;
+		}
+	}
+	const int n0 = gi * C::NR, m0 = z * MR;
+	const int Mz = min(MR, p.M - m0);
+	const int KB = p.K / 32;
+	const unsigned rowbytes = (unsigned)KB * 36u;
+	const char *abase = p.a + blockIdx.y * p.sa_b + (long long)m0 * p.lda_b;
+	const s3k_i32x4 rw = buf_rsrc(p.w + blockIdx.y * p.sw_b, p.w_ext);
+	const s3k_i32x4 ra = buf_rsrc(abase, (unsigned)((Mz - 1) * p.lda_b + p.K * C::ES));
+
+	/* Source of each of this lane's loads for chunk 0. Load j of a chunk
+	 * is wave j % WV's (j / WV)-th; j < IW moves W rows (PW slots each,
+	 * the last one a zero pad that spreads the rows over the LDS banks),
+	 * then A rows, then padding loads (zeros into a spare KiB) keep every
+	 * wave at NPW loads per chunk. */
+	unsigned off[C::NPW];
+#pragma unroll
+	for (int t = 0; t < C::NPW; ++t) {
+		const int j = t * C::WV + wave;
+		unsigned o = S3K_OOB;
+		if (j < C::IW) {
+			const int i = j * 64 + lane;
+			const int r = i / C::PW, q = i % C::PW;
+			if (i < C::GW && q < C::GPRW && n0 + r < p.N)
+				o = (unsigned)(n0 + r) * rowbytes + (unsigned)q * 16u;
+		} else if (j < C::I) {
+			const int i = (j - C::IW) * 64 + lane;
+			const int m = i / C::GAR, sl = i % C::GAR;
+			if (m < Mz)
+				o = (unsigned)(m * p.lda_b) + (unsigned)((sl ^ (m & 15)) * 16);
+		}
+		off[t] = o;
+	}
+
+	auto issue = [&](int ch) {
+		char *st = smem + (ch % C::ST) * C::SB;
+		const unsigned wi = (unsigned)ch * (KC * 36);
+		const unsigned ai = (unsigned)ch * (KC * 32 * C::ES);
+#pragma unroll
+		for (int t = 0; t < C::NPW; ++t) {
+			const int j = t * C::WV + wave;
+			if (j < C::IW)
+				dma16(st + j * 1024, rw, off[t] + wi);
+			else if (j < C::I)
+				dma16(st + C::SW + (j - C::IW) * 1024, ra, off[t] + ai);
+			else
+				dma16(smem + C::ST * C::SB, rw, S3K_OOB);
+		}
+	};
+
+	s3k_f32x4 acc[NT][C::MT];
+#pragma unroll
+	for (int t = 0; t < NT; ++t)
+#pragma unroll
+		for (int mt = 0; mt < C::MT; ++mt)
+			acc[t][mt] = (s3k_f32x4){0.f, 0.f, 0.f, 0.f};
+
+	const int nch = p.K / (KC * 32);
+#pragma unroll
+	for (int s = 0; s < C::ST - 1; ++s)
+		if (s < nch)
+			issue(s);
+
+	for (int ch = 0; ch < nch; ++ch) {
+		/* this wave's loads of chunk ch done (younger chunks may fly) */
+		if (ch + C::ST - 2 < nch)
+			wait_vm<(C::ST - 2) * C::NPW>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (ch + C::ST - 1 < nch)
+			issue(ch + C::ST - 1);
+
+		if (C::CW < WV && wave >= C::CW)
+			continue;
+		const char *Ws = smem + (ch % C::ST) * C::SB;
+		const char *As = Ws + C::SW;
+		/* operands of this wave's U k-blocks first, then all MFMAs, then
+		 * the scale FMAs: independent chains instead of one per block */
+		uint4 af[C::U][C::MT], wf[C::U][NT];
+		float sc[C::U][NT];
+#pragma unroll
+		for (int u = 0; u < C::U; ++u) {
+			const int kb = u * C::CW + wave;
+#pragma unroll
+			for (int mt = 0; mt < C::MT; ++mt) {
+				const int m = mt * 16 + l16;
+				af[u][mt] = make_uint4(0, 0, 0, 0);
+				if (m < MR) {
+					const char *row = As + m * (C::GAR * 16);
+					if constexpr (AK == S3K_F32) {
+						const int q0 = kb * 8 + 2 * g16;
+						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
+						const uint4 y = *(const uint4 *)(row + (((q0 + 1) ^ (m & 15)) << 4));
+						af[u][mt] = make_uint4(
+							pack_f16x2(__uint_as_float(x.x), __uint_as_float(x.y)),
+							pack_f16x2(__uint_as_float(x.z), __uint_as_float(x.w)),
+							pack_f16x2(__uint_as_float(y.x), __uint_as_float(y.y)),
+							pack_f16x2(__uint_as_float(y.z), __uint_as_float(y.w)));
+					} else {
+						const int q0 = kb * 4 + g16;
+						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
+						if constexpr (AK == S3K_BF16)
+							af[u][mt] = make_uint4(
+								pack_f16x2(bf16_to_f32(x.x & 0xFFFF), bf16_to_f32(x.x >> 16)),
+								pack_f16x2(bf16_to_f32(x.y & 0xFFFF), bf16_to_f32(x.y >> 16)),
+								pack_f16x2(bf16_to_f32(x.z & 0xFFFF), bf16_to_f32(x.z >> 16)),
+								pack_f16x2(bf16_to_f32(x.w & 0xFFFF), bf16_to_f32(x.w >> 16)));
+						else
+							af[u][mt] = x;
+					}
+				}
+			}
+#pragma unroll
+			for (int t = 0; t < NT; ++t) {
+				const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
+				sc[u][t] = *(const float *)blk;
+				const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16) ^ 0x80808080u;
+				const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16) ^ 0x80808080u;
+				wf[u][t].x = q8pair_to_f16(w0, 0x04010400u);
+				wf[u][t].y = q8pair_to_f16(w0, 0x04030402u);
+				wf[u][t].z = q8pair_to_f16(w1, 0x04010400u);
+				wf[u][t].w = q8pair_to_f16(w1, 0x04030402u);
+			}
+		}
+		s3k_f32x4 part[C::U][NT][C::MT];
+#pragma unroll
+		for (int u = 0; u < C::U; ++u)
+#pragma unroll
+			for (int t = 0; t < NT; ++t)
+#pragma unroll
+				for (int mt = 0; mt < C::MT; ++mt)
+					part[u][t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+						__builtin_bit_cast(s3k_f16x8, af[u][mt]),
+						__builtin_bit_cast(s3k_f16x8, wf[u][t]),
+						(s3k_f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+		for (int u = 0; u < C::U; ++u)
+#pragma unroll
+			for (int t = 0; t < NT; ++t)
+#pragma unroll
+				for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+					for (int j = 0; j < 4; ++j)
+						acc[t][mt][j] += part[u][t][mt][j] * sc[u][t];
+	}
+
+	/* Cross-wave reduction in a fixed order, then bias/GELU and store. */
+	constexpr int NV = NT * C::MT * 4;
+	wait_vm<0>();
+	wg_barrier();
+	float *red = (float *)smem;
+#pragma unroll
+	for (int t = 0; t < NT; ++t)
+#pragma unroll
+		for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+			for (int j = 0; j < 4; ++j)
+				red[((wave * NV) + (t * C::MT + mt) * 4 + j) * 64 + lane] = acc[t][mt][j];
+	__syncthreads();
+
+	float *cb = (float *)p.c + blockIdx.y * p.sc;
+#pragma unroll 1
+	for (int v = threadIdx.x; v < NV * 64; v += C::WV * 64) {
+		float s = 0.0f;
+#pragma unroll
+		for (int w = 0; w < C::WV; ++w)
+			s += red[w * NV * 64 + v];
+		const int ln = v & 63, slot = v >> 6;
+		const int j = slot & 3, tm = slot >> 2;
+		const int mt = tm % C::MT, t = tm / C::MT;
+		const int m = mt * 16 + 4 * (ln >> 4) + j;
+		const int n = n0 + t * 16 + (ln & 15);
+		if (m >= Mz || n >= p.N)
+			continue;
+		const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
+		cb[(long long)(m0 + m) * p.ldc + n] = epilogue<0>(s, bv, p.flags);
+	}
+}
+
 } /* namespace s3k */
 
 using namespace s3k;
 
+/* q8_stream's requirements: whole 256-k chunks, 16-byte aligned weight
+ * rows (K % 256 == 0 makes the row pitch a multiple of 16), every buffer
+ * range under 2 GiB. */
+static bool stream_ok(const struct s3k_gemm *g)
+{
+	const int es = g->a_kind == S3K_F32 ? 4 : 2;
+	if (g->K % 256 || ((uintptr_t)g->b & 15u))
+		return false;
+	const long long wext = (long long)g->N * (g->K / 32) * 36;
+	const long long aext = (long long)(g->M - 1) * g->lda * es + (long long)g->K * es;
+	if (wext > 0x7FFFFFF0LL || aext > 0x7FFFFFF0LL)
+		return false;
+	if (g->batch > 1 && (g->stride_b % 16 || (g->stride_a * es) % 16))
+		return false;
+	return true;
+}
+
 extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 {
-	if (g->b_kind != S3K_Q8 || !(g->flags & S3K_B_NT) || g->batch != 1)
+	if (g->b_kind != S3K_Q8 || !(g->flags & S3K_B_NT) || g->c_kind != S3K_F32 || g->batch < 1)
 		return 0;
 	if (g->M < 1 || g->M > 128 || g->N < 1 || g->K < 32 || g->K % 32)
 		return 0;
@@ -179,6 +466,8 @@ extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 		return 0;
 	const int es = g->a_kind == S3K_F32 ? 4 : 2;
 	if (((uintptr_t)g->a & 15u) || ((long long)g->lda * es) % 16 || ((uintptr_t)g->b & 3u))
+		return 0;
+	if (g->batch > 1 && !stream_ok(g))
 		return 0;
 	return 1;
 }
@@ -235,8 +524,155 @@ static int launch_mt(const SkinnyArgs &p, hipStream_t st)
 	}
 }
 
+template <int AK, int MR, int NT, int KC>
+static int launch_stream_k(const struct s3k_gemm *g, void *stream)
+{
+	const int es = AK == S3K_F32 ? 4 : 2;
+	StreamArgs p;
+	p.a = (const char *)g->a;
+	p.w = (const char *)g->b;
+	p.c = (char *)g->c;
+	p.bias = (const char *)g->bias;
+	p.M = g->M;
+	p.N = g->N;
+	p.K = g->K;
+	p.lda_b = g->lda * es;
+	p.ldc = g->ldc;
+	p.sa_b = g->stride_a * es;
+	p.sw_b = g->stride_b;
+	p.sc = g->stride_c;
+	p.w_ext = (unsigned)((long long)g->N * (g->K / 32) * 36);
+	p.flags = g->flags;
+	p.groups = (g->N + 16 * NT - 1) / (16 * NT);
+	p.zsplit = (g->M + MR - 1) / MR;
+	dim3 grid(p.groups * p.zsplit, g->batch);
+	hipLaunchKernelGGL((q8_stream<AK, MR, NT, KC>), grid,
+			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), 0, (hipStream_t)stream, p);
+	return (int)hipGetLastError();
+}
+
+template <int AK, int KC>
+static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *stream)
+{
+#define S3K_SK(MR_)                                                              \
+	case MR_:                                                                \
+		return nt == 1 ? launch_stream_k<AK, MR_, 1, KC>(g, stream)     \
+		     : nt == 2 ? launch_stream_k<AK, MR_, 2, KC>(g, stream)     \
+			       : launch_stream_k<AK, MR_, 4, KC>(g, stream);
+	switch (mr) {
+	S3K_SK(1)
+	S3K_SK(4)
+	S3K_SK(8)
+	S3K_SK(16)
+	case 32:
+		if constexpr (KC == 8)
+			return nt == 1 ? launch_stream_k<AK, 32, 1, KC>(g, stream)
+			     : nt == 2 ? launch_stream_k<AK, 32, 2, KC>(g, stream)
+				       : launch_stream_k<AK, 32, 4, KC>(g, stream);
+		return (int)hipErrorInvalidValue;
+	default: return (int)hipErrorInvalidValue;
+	}
+#undef S3K_SK
+}
+
+/*
+ * Shape choice for q8_stream: activation rows per workgroup MR (M is
+ * split over ceil(M / MR) workgroups) and weight rows 16 * NT.
+ *   - Many workgroups (a batch, or >= 512 workgroups of 64 rows): NT = 4
+ *     and MR = M rounded up to 1/4/8/16/32; wide row groups amortize each
+ *     workgroup's start and end (measured best on every config-4 shape).
+ *   - One small launch, M <= 32: its time is one workgroup's latency, so
+ *     rows go to as many CUs as possible (NT = 1), with M split when that
+ *     evens out the bytes a CU moves. Estimate: the largest of per-CU time
+ *     ceil(WGs/256) * bytes per WG / 32 B/clk, HBM time weight bytes /
+ *     2600 B/clk (about 6.2 TB/s) and L2 time WGs * bytes per WG /
+ *     10000 B/clk; ties go to more workgroups.
+ *   - One small launch, M > 32: MR = 32 with NT = 4 when that still makes
+ *     128 workgroups, else MR = 16 with NT = 2.
+ * SAM3_HIP_SK_CFG="mr,nt" forces a shape.
+ */
+static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
+{
+	const char *e = getenv("SAM3_HIP_SK_CFG");
+	if (e) {
+		int mr = 0, nt = 0;
+		if (sscanf(e, "%d,%d", &mr, &nt) == 2 && (nt == 1 || nt == 2 || nt == 4) &&
+		    (mr == 1 || mr == 4 || mr == 8 || mr == 16 || mr == 32)) {
+			*mr_out = mr;
+			*nt_out = nt;
+			return;
+		}
+	}
+	static const int mrs[5] = {1, 4, 8, 16, 32};
+	int mr_all = 32;
+	for (int i = 0; i < 5; ++i)
+		if (mrs[i] >= g->M) {
+			mr_all = mrs[i];
+			break;
+		}
+	const long long z_all = (g->M + mr_all - 1) / mr_all;
+	const long long groups4 = (g->N + 63) / 64;
+	if (g->batch > 1 || groups4 * z_all >= 512) {
+		*mr_out = mr_all;
+		*nt_out = 4;
+		return;
+	}
+	if (g->M > 32) {
+		const bool wide = groups4 * z_all >= 128;
+		*mr_out = wide ? 32 : 16;
+		*nt_out = wide ? 4 : 2;
+		return;
+	}
+	const int es = g->a_kind == S3K_F32 ? 4 : 2;
+	const double K = g->K, N = g->N, M = g->M;
+	double best_t = 1e300;
+	long long best_w = 0;
+	int best_mr = mr_all;
+	for (int i = 0; i < 5; ++i) {
+		const int mr = mrs[i];
+		if (i > 0 && mrs[i - 1] >= g->M)
+			break; /* a smaller MR already covers M */
+		const long long z = (g->M + mr - 1) / mr;
+		if (z > 8)
+			continue;
+		const double per = 16.0 * K * 1.125 + (mr < M ? mr : M) * K * es;
+		const long long wgs = (long long)((g->N + 15) / 16) * z;
+		double t = (double)((wgs + 255) / 256) * per / 32.0;
+		const double th = N * K * 1.125 / 2600.0, tl = (double)wgs * per / 10000.0;
+		t = t > th ? t : th;
+		t = t > tl ? t : tl;
+		if (t < best_t * 0.97 || (t <= best_t * 1.03 && wgs > best_w && wgs <= 512)) {
+			best_t = t;
+			best_w = wgs;
+			best_mr = mr;
+		}
+	}
+	*mr_out = best_mr;
+	*nt_out = 1;
+}
+
 extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 {
+	if (stream_ok(g)) {
+		int mr, nt;
+		stream_pick(g, &mr, &nt);
+		/* 16-block chunks where K allows and the LDS ring stays deep
+		 * enough; 8-block chunks otherwise */
+		const bool k16 = g->K % 512 == 0 && mr <= 16;
+		switch (g->a_kind) {
+		case S3K_F32:
+			return k16 ? launch_stream_a<S3K_F32, 16>(g, mr, nt, stream)
+				   : launch_stream_a<S3K_F32, 8>(g, mr, nt, stream);
+		case S3K_BF16:
+			return k16 ? launch_stream_a<S3K_BF16, 16>(g, mr, nt, stream)
+				   : launch_stream_a<S3K_BF16, 8>(g, mr, nt, stream);
+		default:
+			return k16 ? launch_stream_a<S3K_F16, 16>(g, mr, nt, stream)
+				   : launch_stream_a<S3K_F16, 8>(g, mr, nt, stream);
+		}
+	}
+	if (g->batch != 1)
+		return (int)hipErrorInvalidValue;
 	SkinnyArgs p;
 	p.a = (const char *)g->a;
 	p.w = (const char *)g->b;

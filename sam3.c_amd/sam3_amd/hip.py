@@ -34,6 +34,10 @@ SIGNATURES = {
     "sam3_hip_dispatch_node": (_i, [_vp, _vp]),
     "sam3_hip_matmul": (_i, [_i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),
+    "sam3_hip_matmul_q8_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll,
+                                        _vp, _i, _vp]),
+    "sam3_hip_q8_quantize": (_i, [_vp, _vp, _i, _vp]),
+    "sam3_hip_q8_dequantize": (_i, [_vp, _vp, _i, _vp]),
     "sam3_hip_matmul_path": (_i, [_i, _i, _i, _i, _i, _i, _i]),
     "sam3_hip_matmul_on_path": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_device_count": (_i, []),
@@ -208,6 +212,43 @@ def batched(dtype, a, b, batch, M, N, K, b_nt):
           "matmul_batched")
     synchronize()
     return dc.download(_NP[dtype], (batch, M, N))
+
+
+def q8_batched_dev(a_dtype, a_ptr, w_ptr, c_ptr, batch, M, N, K, stride_a, stride_w, stride_c,
+                   bias_ptr=None, flags=0, stream=None):
+    check(load().sam3_hip_matmul_q8_batched(a_dtype, a_ptr, w_ptr, c_ptr, batch, M, N, K,
+                                            stride_a, stride_w, stride_c, bias_ptr, flags,
+                                            stream), "matmul_q8_batched")
+
+
+def q8_quantize(x):
+    """f32 host array -> Q8_0 blocks (uint8 host array), quantized on the
+    device (sam3_hip_q8_quantize)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    n = x.size
+    out = np.zeros(((n + 31) // 32) * 36, np.uint8)
+    if n == 0:
+        return out
+    dx = DeviceBuffer.of(x)
+    dq = DeviceBuffer(out.nbytes)
+    check(load().sam3_hip_q8_quantize(dx.ptr, dq.ptr, n, None), "q8_quantize")
+    synchronize()
+    out = dq.download(np.uint8, (out.nbytes,))
+    dx.free(); dq.free()  # noqa: E702
+    return out
+
+
+def q8_dequantize(blocks, n):
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    if n == 0:
+        return np.zeros(0, np.float32)
+    db = DeviceBuffer.of(blocks)
+    dx = DeviceBuffer(n * 4)
+    check(load().sam3_hip_q8_dequantize(db.ptr, dx.ptr, n, None), "q8_dequantize")
+    synchronize()
+    out = dx.download(np.float32, (n,))
+    db.free(); dx.free()  # noqa: E702
+    return out
 
 
 # --------------------------------------------------------------- backend

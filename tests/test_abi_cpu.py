@@ -84,6 +84,17 @@ def test_plain_entry_argument_errors():
     assert lib.sam3_hip_matmul_batched(abi.BF16, ok, ok, ok, 0, 4, 4, 4, 16, 16, 16, 0, None) == abi.OK
     assert lib.sam3_hip_matmul(abi.F32, ok, abi.BF16, ok, abi.F32, ok, 4, 4, 4, None, 0, None) == abi.EDTYPE
     assert b"unsupported dtypes" in lib.sam3_hip_last_error()
+    # Q8 batched, quantize, dequantize: argument checks before any device call
+    assert lib.sam3_hip_matmul_q8_batched(abi.F32, ok, ok, ok, 2, 4, 4, 33, 16, 36, 16, None, 0, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul_q8_batched(abi.I8, ok, ok, ok, 2, 4, 4, 32, 16, 36, 16, None, 0, None) == abi.EDTYPE
+    assert lib.sam3_hip_matmul_q8_batched(abi.F32, ok, ok, ok, 2, 4, 4, 32, 16, 36, 16, None, hip.BIAS, None) == abi.EINVAL
+    assert lib.sam3_hip_matmul_q8_batched(abi.F32, ok, ok, ok, 0, 4, 4, 32, 16, 36, 16, None, 0, None) == abi.OK
+    assert lib.sam3_hip_q8_quantize(None, ok, 5, None) == abi.EINVAL
+    assert lib.sam3_hip_q8_quantize(ok, ok, -1, None) == abi.EINVAL
+    assert lib.sam3_hip_q8_quantize(ok + 2, ok, 5, None) == abi.EINVAL
+    assert lib.sam3_hip_q8_quantize(ok, ok, 0, None) == abi.OK
+    assert lib.sam3_hip_q8_dequantize(ok, None, 5, None) == abi.EINVAL
+    assert lib.sam3_hip_q8_dequantize(ok, ok, 0, None) == abi.OK
 
 
 def _node(op, ins, out, params=(0, 0, 0, 0)):

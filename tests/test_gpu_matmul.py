@@ -39,6 +39,61 @@ def q8(w):
     return oracle().q8_quantize(w)
 
 
+# ------------------------------------------------------------ Q8_0 format
+def _cpu_quantizer():
+    """The reference's own quantizer when oracle/_ref is built, else the
+    restatement (pinned to it in test_oracle.py)."""
+    from oracle_bind import Ref, have_ref
+    return Ref() if have_ref() else oracle()
+
+
+def test_q8_quantize_golden_bit_exact():
+    qx = GOLD["quant_x"]
+    assert np.array_equal(hip.q8_quantize(qx), GOLD["quant_blocks"])
+    assert np.array_equal(bits32(hip.q8_dequantize(GOLD["quant_blocks"], qx.size)),
+                          bits32(GOLD["quant_deq"]))
+
+
+def q8_edge_values():
+    """Blocks that exercise every branch of sam3_q8_quantize: exact .5 ties
+    after scaling (roundf rounds away from zero), a zero block, a block of
+    subnormals (its scale's reciprocal overflows), +-inf and NaN (the x86
+    conversion of NaN/inf gives INT_MIN, clamped to -127), huge values."""
+    blk = []
+    t = np.zeros(32, np.float32)
+    t[0] = 127.0
+    t[1:8] = [0.5, -0.5, 1.5, -2.5, 126.5, -126.5, 63.5]
+    blk.append(t)
+    blk.append(np.zeros(32, np.float32))
+    blk.append(np.full(32, 1e-40, np.float32) * np.arange(-16, 16, dtype=np.float32))
+    t = synth.randn(201, 32)
+    t[3], t[9] = np.inf, -np.inf
+    blk.append(t)
+    t = synth.randn(202, 32)
+    t[5] = np.nan
+    blk.append(t)
+    blk.append(synth.randn(203, 32) * np.float32(3e37))
+    return np.concatenate(blk).astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65537])
+def test_q8_quantize_matches_reference(n):
+    Q = _cpu_quantizer()
+    x = synth.randn(200 + n, n) * np.float32(0.02 if n % 2 else 3.0)
+    assert np.array_equal(hip.q8_quantize(x), Q.q8_quantize(x))
+    blocks = Q.q8_quantize(x)
+    assert np.array_equal(bits32(hip.q8_dequantize(blocks, n)), bits32(Q.q8_dequantize(blocks, n)))
+
+
+def test_q8_quantize_edge_blocks():
+    Q = _cpu_quantizer()
+    x = q8_edge_values()
+    got, ref = hip.q8_quantize(x), Q.q8_quantize(x)
+    assert np.array_equal(got, ref), np.nonzero(got != ref)[0][:16]
+    tie = got[:36]
+    assert list(tie[4:12].view(np.int8)) == [127, 1, -1, 2, -3, 127, -127, 64]
+
+
 # ------------------------------------------------------------ known answers
 def test_known_answer_f32_all_paths():
     """tests/test_cpu_kernels.c:474-500: exact [58,64;139,154]."""
@@ -273,6 +328,95 @@ def test_skinny_bias_gelu_and_ragged_n():
     c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, bias=bias,
                    flags=hip.B_NT | hip.BIAS | hip.GELU, path=SKINNY)
     assert_f32_close(c, ref_q8(a, w, K, N, nt=True, bias=bias, gelu=True), what="skinny epi")
+
+
+STREAM_CFGS = [(mr, nt) for mr in (1, 4, 8, 16, 32) for nt in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("K", [256, 1536])
+@pytest.mark.parametrize("mr,nt", STREAM_CFGS)
+def test_stream_kernel_every_shape(monkeypatch, mr, nt, K):
+    """q8_stream (K % 256 == 0) with each workgroup shape forced: M split
+    over ceil(M / mr) workgroups, ragged N (not a multiple of 16*nt), one
+    8-block chunk (K 256) or three 16-block chunks (K 1536; 8-block chunks
+    for mr 32), fused bias + GELU."""
+    monkeypatch.setenv("SAM3_HIP_SK_CFG", f"{mr},{nt}")
+    M, N = 37, 200
+    a = rnd(170, (M, K))
+    w = q8(rnd(171, (N, K), 0.02))
+    bias = rnd(172, N, 0.1)
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, M, N, K, bias=bias,
+                   flags=hip.B_NT | hip.BIAS | hip.GELU, path=SKINNY)
+    assert_f32_close(c, ref_q8(a, w, K, N, nt=True, bias=bias, gelu=True),
+                     what=f"stream mr={mr} nt={nt}")
+
+
+@pytest.mark.parametrize("K", [768, 1024])
+@pytest.mark.parametrize("a_dt", [abi.BF16, abi.F16])
+@pytest.mark.parametrize("mr,nt", [(1, 1), (8, 2), (32, 4)])
+def test_stream_kernel_16bit_activations(monkeypatch, a_dt, mr, nt, K):
+    monkeypatch.setenv("SAM3_HIP_SK_CFG", f"{mr},{nt}")
+    O = oracle()
+    M, N = 20, 72
+    a32 = rnd(175, (M, K))
+    if a_dt == abi.BF16:
+        a16 = O.f32_to_bf16(a32)
+        a_ref = O.bf16_to_f32(a16)
+    else:
+        a16 = O.f32_to_fp16(a32)
+        a_ref = O.fp16_to_f32(a16)
+    w = q8(rnd(176, (N, K), 0.02))
+    c = hip.matmul(a16, a_dt, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT, path=SKINNY)
+    assert_f32_close(c, ref_q8(np.asarray(a_ref, np.float32).reshape(M, K), w, K, N, nt=True),
+                     what=f"stream {a_dt} mr={mr} nt={nt}")
+
+
+def test_stream_kernel_one_hot_exact():
+    """One-hot A through q8_stream selects dequantized weights exactly:
+    q is exact in f16, 1.0 is exact, the scale is applied in f32."""
+    O = oracle()
+    K, N = 512, 80
+    w = q8(rnd(178, (N, K), 0.02))
+    deq = O.q8_dequantize(w, N * K).reshape(N, K)
+    rows = [0, 1, 255, 256, 300, 511]
+    a = np.eye(K, dtype=np.float32)[rows]
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, len(rows), N, K, flags=hip.B_NT,
+                   path=SKINNY)
+    assert np.array_equal(c, deq[:, rows].T)
+
+
+@pytest.mark.parametrize("shared_a", [False, True])
+def test_q8_batched_stream(shared_a):
+    """sam3_hip_matmul_q8_batched: distinct weights per slice in one launch,
+    against the oracle slice by slice (stride_a = 0 shares the activations)."""
+    B, M, N, K = 5, 8, 96, 512
+    a = rnd(180, (1 if shared_a else B, M, K))
+    ws = [q8(rnd(181 + s, (N, K), 0.02)) for s in range(B)]
+    wbytes = ws[0].nbytes
+    da = hip.DeviceBuffer.of(a)
+    dw = hip.DeviceBuffer.of(np.concatenate(ws))
+    dc = hip.DeviceBuffer(B * M * N * 4)
+    hip.q8_batched_dev(abi.F32, da.ptr, dw.ptr, dc.ptr, B, M, N, K,
+                       0 if shared_a else M * K, wbytes, M * N)
+    hip.synchronize()
+    c = dc.download(np.float32, (B, M, N))
+    for s in range(B):
+        ref = ref_q8(a[0 if shared_a else s], ws[s], K, N, nt=True)
+        assert_f32_close(c[s], ref, what=f"q8 batched slice {s}")
+
+
+def test_q8_batched_falls_back_per_slice():
+    """M > 128 is not a skinny problem: one launch per slice, same result."""
+    B, M, N, K = 2, 160, 64, 256
+    a = rnd(190, (B, M, K))
+    ws = [q8(rnd(191 + s, (N, K), 0.02)) for s in range(B)]
+    da, dw = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(np.concatenate(ws))
+    dc = hip.DeviceBuffer(B * M * N * 4)
+    hip.q8_batched_dev(abi.F32, da.ptr, dw.ptr, dc.ptr, B, M, N, K, M * K, ws[0].nbytes, M * N)
+    hip.synchronize()
+    c = dc.download(np.float32, (B, M, N))
+    for s in range(B):
+        assert_f32_close(c[s], ref_q8(a[s], ws[s], K, N, nt=True), what=f"fallback slice {s}")
 
 
 def test_q8_nt_ragged_k_blocks_straddle_rows():
