@@ -51,9 +51,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
 	static_assert(NW * 32 * (WTN + 8) * 4 <= STAGES * SB, "epilogue staging fits");
 	__shared__ __attribute__((aligned(1024))) char smem[STAGES * SB];
 
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
 	const int bz = blockIdx.y;
+	const unsigned lds0 = lds_addr_of(smem);
 	int tm, tn;
 	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
 
@@ -80,23 +82,30 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
 		b_k[j] = c * 8;
 	}
 
+	/* A whole k-step moves every lane's chunk by 2*k0 bytes: that goes in
+	 * the scalar offset (rows past M/N keep an offset past the range). Only
+	 * a k-step that crosses K selects chunks per lane. */
 	auto issue = [&](int kt) {
 		const int k0 = kt * BK;
-		const bool full = k0 + BK <= p.K;
-		char *st = smem + (kt % STAGES) * SB;
+		const unsigned st = lds0 + (unsigned)((kt % STAGES) * SB) + (unsigned)wave * 1024u;
+		if (k0 + BK <= p.K) {
 #pragma unroll
-		for (int j = 0; j < A_PER; ++j) {
-			unsigned o = a_off[j];
-			if (o != S3K_OOB)
-				o = (full || k0 + a_k[j] < p.K) ? o + 2u * k0 : S3K_OOB;
-			dma16(st + (j * NW + wave) * 1024, ra, o);
-		}
+			for (int j = 0; j < A_PER; ++j)
+				dma16s(st + j * NW * 1024, ra, a_off[j], 2u * k0);
 #pragma unroll
-		for (int j = 0; j < B_PER; ++j) {
-			unsigned o = b_off[j];
-			if (o != S3K_OOB)
-				o = (full || k0 + b_k[j] < p.K) ? o + 2u * k0 : S3K_OOB;
-			dma16(st + A_BYTES + (j * NW + wave) * 1024, rb, o);
+			for (int j = 0; j < B_PER; ++j)
+				dma16s(st + A_BYTES + j * NW * 1024, rb, b_off[j], 2u * k0);
+		} else {
+#pragma unroll
+			for (int j = 0; j < A_PER; ++j) {
+				const unsigned o = k0 + a_k[j] < p.K ? a_off[j] + 2u * k0 : S3K_OOB;
+				dma16s(st + j * NW * 1024, ra, o, 0u);
+			}
+#pragma unroll
+			for (int j = 0; j < B_PER; ++j) {
+				const unsigned o = k0 + b_k[j] < p.K ? b_off[j] + 2u * k0 : S3K_OOB;
+				dma16s(st + A_BYTES + j * NW * 1024, rb, o, 0u);
+			}
 		}
 	};
 
@@ -216,18 +225,17 @@ bool s3k_dl_ok(const struct s3k_gemm *g)
 	return true;
 }
 
-/* Tile shape by a balance model: with two workgroups resident per CU,
- * a launch of T tiles runs ceil(T / 512) rounds, so the useful fraction is
- * T / (512 * rounds); the 128x128 tile re-reads more of A and B per flop
- * (weight 0.93, from measurement on the ViT-L shapes). Candidates:
- * 256x128 (cfg 0), 128x256 (cfg 3), 128x128 with BK 64 (cfg 4).
- * SAM3_HIP_DL_CFG forces a configuration (tuning). */
-static int dl_cfg_env = -2;
-
-static double dl_fill(long long tiles)
+/* Tile shape, from measurements on the ViT-L shapes (bench-like data):
+ *   - 256x256 (cfg 9, 8 waves, one workgroup per CU) when the problem is
+ *     one nearly full round of 224..256 such tiles (qkv 5184x3072, 4096^2);
+ *   - 192x128 (cfg 10, 8 waves, two workgroups per CU) when that gives
+ *     at least 192 tiles (fc1, fc2, proj, batched attention);
+ *   - 128x128 (cfg 4, 4 waves) for mid-size problems, 64x64 (cfg 2) for
+ *     small ones.
+ * SAM3_HIP_DL_CFG forces a configuration (tuning and tests). */
+static long long dl_tiles(const struct s3k_gemm *g, int bm, int bn)
 {
-	const long long slots = 512;
-	return (double)tiles / ((double)((tiles + slots - 1) / slots) * slots);
+	return (long long)((g->M + bm - 1) / bm) * ((g->N + bn - 1) / bn) * g->batch;
 }
 
 int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
@@ -236,19 +244,17 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		return (int)hipErrorInvalidValue;
 	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
 	p.b_extent = (unsigned)((long long)g->N * g->ldb * 2);
-	if (dl_cfg_env == -2) {
-		const char *e = getenv("SAM3_HIP_DL_CFG");
-		dl_cfg_env = e ? atoi(e) : -1;
-	}
-	int cfg = dl_cfg_env;
+	const char *e = getenv("SAM3_HIP_DL_CFG");
+	int cfg = e ? atoi(e) : -1;
 	if (cfg < 0) {
-		const long long b = g->batch;
-		const long long t0 = (long long)((g->M + 255) / 256) * ((g->N + 127) / 128) * b;
-		const long long t3 = (long long)((g->M + 127) / 128) * ((g->N + 255) / 256) * b;
-		const long long t4 = (long long)((g->M + 127) / 128) * ((g->N + 127) / 128) * b;
-		const double e0 = dl_fill(t0), e3 = dl_fill(t3), e4 = 0.93 * dl_fill(t4);
-		cfg = e0 >= e3 ? (e0 >= e4 ? 0 : 4) : (e3 >= e4 ? 3 : 4);
-		if (t4 < 64)
+		const long long t9 = dl_tiles(g, 256, 256), t10 = dl_tiles(g, 192, 128);
+		if (t9 >= 224 && t9 <= 256)
+			cfg = 9;
+		else if (t10 >= 192)
+			cfg = 10;
+		else if (dl_tiles(g, 128, 128) >= 64)
+			cfg = 4;
+		else
 			cfg = 2;
 	}
 	switch (cfg) {
@@ -259,6 +265,13 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 4:  return launch_dl_cfg<128, 128, 64, 2, 2, 2, 2>(g, p, st);
 	case 5:  return launch_dl_cfg<256, 256, 32, 2, 2, 4, 1>(g, p, st);
 	case 6:  return launch_dl_cfg<192, 256, 32, 2, 2, 4, 1>(g, p, st);
+	case 7:  return launch_dl_cfg<192, 256, 64, 2, 4, 2, 1>(g, p, st);
+	case 8:  return launch_dl_cfg<256, 256, 32, 2, 4, 3, 1>(g, p, st);
+	case 9:  return launch_dl_cfg<256, 256, 64, 2, 4, 2, 1>(g, p, st);
+	case 10: return launch_dl_cfg<192, 128, 64, 2, 4, 2, 1>(g, p, st);
+	case 11: return launch_dl_cfg<256, 128, 64, 2, 4, 2, 1>(g, p, st);
+	case 12: return launch_dl_cfg<128, 256, 64, 2, 4, 2, 1>(g, p, st);
+	case 13: return launch_dl_cfg<256, 256, 32, 2, 4, 4, 1>(g, p, st);
 	default: return (int)hipErrorInvalidValue;
 	}
 }

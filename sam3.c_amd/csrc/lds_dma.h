@@ -39,6 +39,23 @@ __device__ __forceinline__ void dma16(const void *lds, s3k_i32x4 rsrc, unsigned 
 		     :: "s"(m0), "v"(voff), "s"(rsrc) : "memory");
 }
 
+/* The same with the LDS address already a wave-uniform 32-bit LDS byte
+ * address (no pointer arithmetic per load) and a scalar byte offset added
+ * to every lane's voff: lanes whose voff is at or past num_records still
+ * load zeros. */
+__device__ __forceinline__ void dma16s(unsigned lds_addr, s3k_i32x4 rsrc, unsigned voff,
+				       unsigned soff)
+{
+	asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+		     :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+}
+
+/* 32-bit LDS address of a __shared__ object. */
+__device__ __forceinline__ unsigned lds_addr_of(const void *p)
+{
+	return (unsigned)(size_t)(lds_ptr_t)p;
+}
+
 /* s_waitcnt vmcnt(N) with lgkm/exp counters left alone. */
 template <int N>
 __device__ __forceinline__ void wait_vm()

@@ -254,6 +254,23 @@ def test_fused_bias_gelu(kind):
          "f16": lambda g, r: assert_f16_close(g, r, what=f"fused {kind} {flags}")}[kind](c, ref)
 
 
+@pytest.mark.parametrize("cfg", list(range(13)))
+def test_dl_every_tile_config(monkeypatch, cfg):
+    """Each direct-to-LDS tile configuration (forced) on a ragged bf16 NT
+    problem with a k tail, bias and GELU, against the oracle."""
+    monkeypatch.setenv("SAM3_HIP_DL_CFG", str(cfg))
+    O = oracle()
+    M, N, K = 300, 520, 200
+    a = O.f32_to_bf16(rnd(210, (M, K))).reshape(M, K)
+    w = O.f32_to_bf16(rnd(211, (N, K), 0.05)).reshape(N, K)
+    bias = O.f32_to_bf16(rnd(212, N, 0.1))
+    assert hip.matmul_path(abi.BF16, abi.BF16, abi.BF16, M, N, K, hip.B_NT) == MFMA
+    c = hip.matmul(a, abi.BF16, w, abi.BF16, abi.BF16, M, N, K, bias=bias,
+                   flags=hip.B_NT | hip.BIAS | hip.GELU)
+    ref = ref_linear("bf16", a, w, bias=bias, gelu=True, b_nt=True)
+    assert_bf16_close(c, ref, what=f"dl cfg {cfg}")
+
+
 def test_bf16_output_f32():
     """bf16 operands with an f32 output (no rounding of C)."""
     O = oracle()
