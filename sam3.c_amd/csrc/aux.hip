@@ -111,6 +111,39 @@ __global__ void __launch_bounds__(256) q8_dequantize_k(const char *src, float *d
 			dst[e0 + i] = (float)(int)(int8_t)(w >> (8 * i)) * s;
 }
 
+/* f32 or bf16 -> f16 (round to nearest even), 8 values per thread; the
+ * f16 staging of activations for the Q8 GEMM. */
+template <bool BF16>
+__global__ void __launch_bounds__(256) cast_f16_k(const void *src, uint16_t *dst, long long n)
+{
+	const long long i0 = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+	if (i0 >= n)
+		return;
+	float x[8];
+	if (i0 + 8 <= n) {
+		if (BF16) {
+			const uint4 v = *(const uint4 *)((const uint16_t *)src + i0);
+			const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+			for (int e = 0; e < 4; ++e) {
+				x[2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
+				x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
+			}
+		} else {
+			const float4 a = *(const float4 *)((const float *)src + i0);
+			const float4 b = *(const float4 *)((const float *)src + i0 + 4);
+			x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+			x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+		}
+		*(uint4 *)(dst + i0) = make_uint4(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]),
+						  pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7]));
+	} else {
+		for (long long i = i0; i < n; ++i)
+			dst[i] = (uint16_t)f32_to_f16(BF16 ? bf16_to_f32(((const uint16_t *)src)[i])
+							  : ((const float *)src)[i]);
+	}
+}
+
 template <int KIND>
 __global__ void __launch_bounds__(256) bias_add_k(const void *x, const void *bias, void *out,
 						  long long rows, int n)
@@ -208,6 +241,24 @@ extern "C" int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream
 	const long long lanes = ((long long)n + 31) / 32 * 8;
 	hipLaunchKernelGGL(q8_dequantize_k, grid1(lanes), dim3(256), 0, (hipStream_t)stream,
 			   (const char *)src, (float *)dst, n);
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream)
+{
+	if (n <= 0)
+		return 0;
+	if (((uintptr_t)src | (uintptr_t)dst) & 15u)
+		return (int)hipErrorInvalidValue;
+	const dim3 grid((unsigned)((n + 2047) / 2048));
+	if (kind == S3K_BF16)
+		hipLaunchKernelGGL(cast_f16_k<true>, grid, dim3(256), 0, (hipStream_t)stream, src,
+				   (uint16_t *)dst, n);
+	else if (kind == S3K_F32)
+		hipLaunchKernelGGL(cast_f16_k<false>, grid, dim3(256), 0, (hipStream_t)stream, src,
+				   (uint16_t *)dst, n);
+	else
+		return (int)hipErrorInvalidValue;
 	return (int)hipGetLastError();
 }
 

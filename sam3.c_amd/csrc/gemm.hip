@@ -645,6 +645,8 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 		return (int)hipErrorInvalidValue;
 	if (s3k_dl_ok(g))
 		return s3k_dl_launch(g, p, st);
+	if (s3k_dlq8_ok(g))
+		return s3k_dlq8_launch(g, p, st);
 	if (g->a_kind == S3K_F32 && g->b_kind == S3K_F32) {
 		switch (pick_cfg(g, true)) {
 		case 1:  return launch_cfg_f32<128, 128, 2, 2>(g, p, st);

@@ -204,4 +204,8 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, s3k_f32x16 (&acc)[
 bool s3k_dl_ok(const struct s3k_gemm *g);
 int s3k_dl_launch(const struct s3k_gemm *g, s3k::GemmArgs p, hipStream_t st);
 
+/* Direct-to-LDS f16 x Q8_0 NT GEMM, f32 out (gemm_dlq8.hip). */
+bool s3k_dlq8_ok(const struct s3k_gemm *g);
+int s3k_dlq8_launch(const struct s3k_gemm *g, s3k::GemmArgs p, hipStream_t st);
+
 #endif /* SAM3_GEMM_COMMON_H */

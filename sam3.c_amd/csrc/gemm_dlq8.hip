@@ -1,0 +1,284 @@
+/*
+ * gemm_dlq8.hip - C[M,N] (f32) = A[M,K] (f16) * W^T with W[N,K] in sam3.c's
+ * Q8_0 blocks along k ({f32 scale; int8 q[32]}, 36 bytes, the converter's
+ * layout, cli_convert.c:374-422), for gfx950. Reference arithmetic:
+ * cpu_matmul_q8.c:124-131 (a * q * scale, f32 accumulate); f32 and bf16
+ * activations are converted to f16 once per call before this kernel.
+ *
+ * The weights are never expanded in memory:
+ *   - each k-step (BK = 64, two blocks) moves the raw 72-byte segment of
+ *     every weight row straight into LDS with buffer_load ... lds, as five
+ *     16-byte pieces at segment bytes 0, 16, 32, 48 and 56 (the last one
+ *     overlaps, so no piece leaves the row); an LDS row is 80 bytes and
+ *     segment byte b sits at b, or b + 8 for b >= 64;
+ *   - the A tile arrives the same way, XOR-swizzled per row (lds_swz);
+ *   - when a wave reads its B fragment (8 consecutive k of one row) it
+ *     turns the 8 int8 into exact f16 integers with one byte permute and
+ *     one packed subtract per pair (bytes biased by 128 under the f16
+ *     exponent of 1024, then 1152 subtracted) and multiplies them by the
+ *     block scale rounded to f16, so the MFMA sees q*scale in f16, as the
+ *     register-staged Q8 loader produces it;
+ *   - v_mfma_f32_32x32x16_f16, f32 accumulate; each wave covers 128 rows
+ *     of A so one dequantized B fragment serves 4 MFMAs.
+ * The ring, the waits and the epilogue follow gemm_dl.hip.
+ */
+#include "gemm_common.h"
+#include "lds_dma.h"
+
+namespace s3k {
+
+typedef __attribute__((ext_vector_type(2))) _Float16 q8h2_t;
+
+__device__ __forceinline__ uint32_t q8_pair_f16(uint32_t wx, uint32_t sel, q8h2_t s2)
+{
+	q8h2_t h = __builtin_bit_cast(q8h2_t, __builtin_amdgcn_perm(0x64646464u, wx, sel));
+	h = (h - (q8h2_t){(_Float16)1152.0f, (_Float16)1152.0f}) * s2;
+	return __builtin_bit_cast(uint32_t, h);
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, int OCC>
+__global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
+{
+	constexpr int NW = WGM * WGN;
+	constexpr int BK = 64, CPR = 8;
+	constexpr int A_BYTES = BM * BK * 2;
+	constexpr int A_INS = BM * CPR / 64;
+	constexpr int PW = 5;                             /* 16-B slots per W row */
+	constexpr int B_SLOTS = BN * PW;
+	constexpr int B_INS = (B_SLOTS + 63) / 64;
+	constexpr int SB = A_BYTES + B_INS * 1024;
+	constexpr int A_PER = (A_INS + NW - 1) / NW, B_PER = (B_INS + NW - 1) / NW;
+	constexpr int NPW = A_PER + B_PER;                /* loads per wave per stage */
+	constexpr int WTM = BM / WGM, WTN = BN / WGN;
+	constexpr int FM = WTM / 32, FN = WTN / 32;
+	constexpr int KS = BK / 16;
+	static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+	static_assert(NPW * (STAGES - 1) < 64, "vmcnt range");
+	static_assert(NW * 32 * (WTN + 8) * 4 <= STAGES * SB, "epilogue staging fits");
+	__shared__ __attribute__((aligned(1024))) char smem[STAGES * SB + 1024];
+
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+	const int bz = blockIdx.y;
+	const unsigned lds0 = lds_addr_of(smem);
+	int tm, tn;
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+
+	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+	const unsigned rowbytes = (unsigned)(p.K / 32) * 36u;
+
+	/* Source of each of this lane's loads for k-step 0. A wave issues A_PER
+	 * A chunks (load t*NW + wave) and B_PER W pieces; the last round of
+	 * either may run past the tile and then loads zeros into a spare KiB,
+	 * so every wave issues NPW loads per stage. */
+	unsigned a_off[A_PER], b_off[B_PER];
+	bool a_real[A_PER], b_real[B_PER];
+#pragma unroll
+	for (int t = 0; t < A_PER; ++t) {
+		const int j = t * NW + wave;
+		const int s = j * 64 + lane;
+		const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+		const int g = tm * BM + row;
+		a_real[t] = j < A_INS;
+		a_off[t] = (j < A_INS && g < p.M) ? (unsigned)(g * p.lda_b + c * 16) : S3K_OOB;
+	}
+#pragma unroll
+	for (int t = 0; t < B_PER; ++t) {
+		const int j = t * NW + wave;
+		const int s = j * 64 + lane;
+		const int row = s / PW, q = s % PW;
+		const int n = tn * BN + row;
+		b_real[t] = j < B_INS;
+		b_off[t] = (j < B_INS && s < B_SLOTS && n < p.N)
+			? (unsigned)n * rowbytes + (unsigned)(q < 4 ? q * 16 : 56) : S3K_OOB;
+	}
+	const unsigned trash = lds0 + STAGES * SB;
+
+	auto issue = [&](int kt) {
+		const unsigned st = lds0 + (unsigned)((kt % STAGES) * SB);
+#pragma unroll
+		for (int t = 0; t < A_PER; ++t)
+			dma16s(a_real[t] ? st + (t * NW + wave) * 1024 : trash, ra, a_off[t], 128u * kt);
+#pragma unroll
+		for (int t = 0; t < B_PER; ++t)
+			dma16s(b_real[t] ? st + A_BYTES + (t * NW + wave) * 1024 : trash, rb, b_off[t],
+			       72u * kt);
+	};
+
+	/* B fragments: lane (row n = lane & 31 of each 32-row tile, k half
+	 * h = lane >> 5) reads, for k-step ks, 8 q bytes at segment byte
+	 * b = 36*(ks>>1) + 4 + 16*(ks&1) + 8h (LDS b + 8 when b >= 64) and the
+	 * scale of block ks>>1. */
+	const int h = lane >> 5;
+	int qo[KS];
+#pragma unroll
+	for (int ks = 0; ks < KS; ++ks) {
+		const int b = 36 * (ks >> 1) + 4 + 16 * (ks & 1) + 8 * h;
+		qo[ks] = b + (b >= 64 ? 8 : 0);
+	}
+	int brow[FN];
+#pragma unroll
+	for (int j = 0; j < FN; ++j)
+		brow[j] = (wn0 + j * 32 + (lane & 31)) * (PW * 16);
+
+	s3k_f32x16 acc[FM][FN];
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+
+	const int nk = p.K / BK;
+#pragma unroll
+	for (int s = 0; s < STAGES - 1; ++s)
+		if (s < nk)
+			issue(s);
+
+	for (int kt = 0; kt < nk; ++kt) {
+		/* own loads of step kt done: at most the younger stages pending */
+		const int younger = min(nk - 1 - kt, STAGES - 2);
+		if (younger >= 2)
+			wait_vm<2 * NPW>();
+		else if (younger == 1)
+			wait_vm<NPW>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (kt + STAGES - 1 < nk)
+			issue(kt + STAGES - 1);
+
+		const char *As = smem + (kt % STAGES) * SB;
+		const char *Bs = As + A_BYTES;
+		/* dequantize this wave's B fragments of the whole k-step first */
+		uint4 bfr[KS][FN];
+#pragma unroll
+		for (int j = 0; j < FN; ++j) {
+			const char *row = Bs + brow[j];
+			q8h2_t s2[2];
+#pragma unroll
+			for (int blk = 0; blk < 2; ++blk) {
+				const _Float16 sh = (_Float16)*(const float *)(row + 36 * blk);
+				s2[blk] = (q8h2_t){sh, sh};
+			}
+#pragma unroll
+			for (int ks = 0; ks < KS; ++ks) {
+				const uint32_t w0 = *(const uint32_t *)(row + qo[ks]) ^ 0x80808080u;
+				const uint32_t w1 = *(const uint32_t *)(row + qo[ks] + 4) ^ 0x80808080u;
+				const q8h2_t sc = s2[ks >> 1];
+				bfr[ks][j] = make_uint4(q8_pair_f16(w0, 0x04010400u, sc),
+							q8_pair_f16(w0, 0x04030402u, sc),
+							q8_pair_f16(w1, 0x04010400u, sc),
+							q8_pair_f16(w1, 0x04030402u, sc));
+			}
+		}
+		uint4 af[2][FM];
+#pragma unroll
+		for (int i = 0; i < FM; ++i) {
+			const int r = wm0 + i * 32 + (lane & 31);
+			af[0][i] = *(const uint4 *)(As + ((r * CPR + (h ^ lds_swz<CPR>(r))) << 4));
+		}
+#pragma unroll
+		for (int ks = 0; ks < KS; ++ks) {
+			const int cur = ks & 1;
+			if (ks + 1 < KS) {
+				const int c = 2 * (ks + 1) + h;
+#pragma unroll
+				for (int i = 0; i < FM; ++i) {
+					const int r = wm0 + i * 32 + (lane & 31);
+					af[cur ^ 1][i] = *(const uint4 *)(As + ((r * CPR + (c ^ lds_swz<CPR>(r))) << 4));
+				}
+			}
+#pragma unroll
+			for (int i = 0; i < FM; ++i)
+#pragma unroll
+				for (int j = 0; j < FN; ++j)
+					mfma_chunk<FAM_F16>(acc[i][j], af[cur][i], bfr[ks][j]);
+		}
+	}
+
+	__syncthreads();
+	write_tile_ck<FM, FN, WTN, S3K_F32>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, int OCC>
+static int launch_dlq8_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	p.tiles_m = (p.M + BM - 1) / BM;
+	p.tiles_n = (p.N + BN - 1) / BN;
+	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	hipLaunchKernelGGL((gemm_dlq8<BM, BN, WGM, WGN, STAGES, OCC>), grid, dim3(64 * WGM * WGN), 0,
+			   st, p);
+	return (int)hipGetLastError();
+}
+
+} /* namespace s3k */
+
+using namespace s3k;
+
+/* f16 A [M,K] (16-byte aligned rows) times Q8_0 W [N,K] with K % 64 == 0,
+ * f32 C; each batch slice within a 2 GiB buffer range. */
+bool s3k_dlq8_ok(const struct s3k_gemm *g)
+{
+	if (g->b_kind != S3K_Q8 || !(g->flags & S3K_B_NT) || g->a_kind != S3K_F16 ||
+	    g->c_kind != S3K_F32)
+		return false;
+	if (g->M <= 0 || g->N <= 0 || g->K <= 0 || g->K % 64 || g->batch <= 0)
+		return false;
+	if (((uintptr_t)g->a & 15u) || (g->lda * 2LL) % 16 || ((uintptr_t)g->b & 3u))
+		return false;
+	if (g->batch > 1 && ((g->stride_a * 2) % 16 || g->stride_b % 4))
+		return false;
+	if ((long long)g->M * g->lda * 2 > 0x7FFFFFF0LL ||
+	    (long long)g->N * (g->K / 32) * 36 > 0x7FFFFFF0LL)
+		return false;
+	return true;
+}
+
+/*
+ * Tile choice: 128x128 with 4 waves of 128x32 (one dequantized weight
+ * fragment feeds 4 MFMAs) and two workgroups per CU measured fastest on
+ * every ViT-L shape (fc1/fc2/qkv/proj at M = 5184), ahead of 256x256 and
+ * 256x128 tiles with 8 waves and of 256-row waves. SAM3_HIP_DLQ8_CFG
+ * forces another configuration (tests and tuning).
+ */
+int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	if (!s3k_dlq8_ok(g))
+		return (int)hipErrorInvalidValue;
+	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
+	p.b_extent = (unsigned)((long long)g->N * (g->K / 32) * 36);
+	const char *e = getenv("SAM3_HIP_DLQ8_CFG");
+	int cfg = e ? atoi(e) : -1;
+	if (cfg < 0)
+		cfg = 2;
+	switch (cfg) {
+	case 0:  return launch_dlq8_cfg<256, 256, 2, 4, 3, 1>(g, p, st);
+	case 1:  return launch_dlq8_cfg<256, 128, 2, 4, 3, 1>(g, p, st);
+	case 2:  return launch_dlq8_cfg<128, 128, 1, 4, 3, 2>(g, p, st);
+	case 3:  return launch_dlq8_cfg<128, 256, 1, 8, 3, 1>(g, p, st);
+	case 4:  return launch_dlq8_cfg<256, 256, 1, 8, 3, 1>(g, p, st);
+	case 5:  return launch_dlq8_cfg<256, 128, 1, 4, 3, 1>(g, p, st);
+	case 6:  return launch_dlq8_cfg<256, 128, 1, 4, 2, 1>(g, p, st);
+	default: return (int)hipErrorInvalidValue;
+	}
+}
+
+extern "C" int s3k_dlq8_eligible(const struct s3k_gemm *g)
+{
+	if (g->batch != 1 && g->a_kind != S3K_F16)
+		return 0;
+	if (g->a_kind != S3K_F16 && (g->lda != g->K || ((uintptr_t)g->a & 15u)))
+		return 0;
+	/* f32 activations: the register-staged kernel, which converts them in
+	 * its loader, measured faster than a cast pass plus this kernel
+	 * (5184x1024x1024: 39.5 us against 46 us) */
+	if (g->a_kind != S3K_F16 && g->a_kind != S3K_BF16)
+		return 0;
+	struct s3k_gemm h = *g;
+	h.a_kind = S3K_F16;
+	return s3k_dlq8_ok(&h) ? 1 : 0;
+}

@@ -81,6 +81,11 @@ int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N,
 /* Q8_0 quantize / dequantize of n f32 values (blocks over the flat index). */
 int s3k_q8_quantize(const void *src, void *dst, int n, void *stream);
 int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream);
+/* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
+int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
+/* Whether the MFMA path of g (B Q8_0 [N,K]) runs the direct-to-LDS Q8
+ * GEMM: f16 A directly, bf16 A after a cast to f16. */
+int s3k_dlq8_eligible(const struct s3k_gemm *g);
 int s3k_bias_add(int kind, const void *x, const void *bias, void *out,
 		 long long rows, int n, void *stream);
 int s3k_add_same(int kind, const void *x, const void *y, void *out,

@@ -166,6 +166,37 @@ static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 	return err != SAM3_OK ? err : ferr;
 }
 
+/* f32/bf16 activations times Q8_0 [N,K] weights on the direct-to-LDS Q8
+ * GEMM: the activations are cast to f16 once into stream-ordered scratch
+ * (the value the register-staged loader would form), then the GEMM runs
+ * on f16 A. */
+static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
+{
+	const size_t bytes = (size_t)g->M * g->K * 2;
+	void *a16 = NULL;
+	enum sam3_error err = s3h_hip(hipMallocAsync(&a16, bytes, (hipStream_t)stream),
+				      "matmul_q8 activation scratch");
+	if (err != SAM3_OK)
+		return err;
+	err = s3h_hip(s3k_cast_f16(g->a_kind, g->a, a16, (long long)g->M * g->K, stream),
+		      "matmul_q8 activation cast");
+	if (err == SAM3_OK) {
+		struct s3k_gemm h = *g;
+		h.a = a16;
+		h.a_kind = S3K_F16;
+		h.lda = g->K;
+		err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+	}
+	enum sam3_error ferr = s3h_hip(hipFreeAsync(a16, (hipStream_t)stream),
+				       "matmul_q8 activation scratch free");
+	return err != SAM3_OK ? err : ferr;
+}
+
+static int q8_dl_wants_cast(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && g->a_kind != S3K_F16 && s3k_dlq8_eligible(g);
+}
+
 static int q8_needs_unpack(const struct s3k_gemm *g)
 {
 	if (g->b_kind != S3K_Q8)
@@ -202,6 +233,8 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	if (path == 0) {
 		if (q8_needs_unpack(&g))
 			return q8_unpacked(&g, stream);
+		if (s3k_gemm_path(&g) == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
+			return q8_dl_cast(&g, stream);
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
 	}
 	if (path < S3K_PATH_MFMA || path > S3K_PATH_GENERIC) {
@@ -210,6 +243,8 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	}
 	if (path == S3K_PATH_MFMA && q8_needs_unpack(&g))
 		return q8_unpacked(&g, stream);
+	if (path == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
+		return q8_dl_cast(&g, stream);
 	int e = s3k_gemm_launch_path(&g, path, stream);
 	if (e == hipErrorInvalidValue) {
 		s3h_error("matmul: path %d cannot run M=%d N=%d K=%d", path, M, N, K);

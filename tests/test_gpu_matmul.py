@@ -312,6 +312,50 @@ def test_q8_nt_tiled_bf16_and_f16_activations(M, N, K):
     assert_f32_close(c, ref, what="q8 f16-act")
 
 
+@pytest.mark.parametrize("cfg", list(range(7)))
+@pytest.mark.parametrize("a_dt", [abi.F32, abi.BF16, abi.F16])
+def test_q8_dl_every_config(monkeypatch, cfg, a_dt):
+    """Direct-to-LDS Q8 GEMM (raw 36-byte blocks in LDS, dequantized per
+    fragment) with each tile configuration forced, ragged M and N, bias +
+    GELU. bf16 activations go through the f16 cast first; f32 activations
+    run the register-staged kernel (the configuration does not apply)."""
+    monkeypatch.setenv("SAM3_HIP_DLQ8_CFG", str(cfg))
+    O = oracle()
+    M, N, K = 300, 200, 576
+    a32 = rnd(220, (M, K))
+    w = q8(rnd(221, (N, K), 0.02))
+    bias = rnd(222, N, 0.1)
+    if a_dt == abi.F32:
+        a, a_ref = a32, a32
+    elif a_dt == abi.BF16:
+        a = O.f32_to_bf16(a32).reshape(M, K)
+        a_ref = O.bf16_to_f32(a).reshape(M, K)
+    else:
+        a = O.f32_to_fp16(a32).reshape(M, K)
+        a_ref = O.fp16_to_f32(a).reshape(M, K)
+    c = hip.matmul(a, a_dt, w, abi.Q8_0, abi.F32, M, N, K, bias=bias,
+                   flags=hip.B_NT | hip.BIAS | hip.GELU, path=MFMA)
+    ref = ref_q8(np.asarray(a_ref, np.float32), w, K, N, nt=True, bias=bias, gelu=True)
+    assert_f32_close(c, ref, what=f"dlq8 cfg {cfg} a={a_dt}")
+
+
+def test_q8_dl_one_hot_rows():
+    """One-hot A rows select W rows: the result is q*scale rounded through
+    f16 (scale rounded to f16, product rounded to f16), within 2 f16 ulps of
+    the exact dequantized weight."""
+    O = oracle()
+    K, N = 256, 136
+    w = q8(rnd(225, (N, K), 0.02))
+    deq = O.q8_dequantize(w, N * K).reshape(N, K)
+    rows = list(range(0, 256, 8))
+    a = np.eye(K, dtype=np.float32)[rows]
+    a = np.concatenate([a, np.zeros((200 - len(rows), K), np.float32)])
+    c = hip.matmul(a, abi.F32, w, abi.Q8_0, abi.F32, 200, N, K, flags=hip.B_NT, path=MFMA)
+    got, ref = c[:len(rows)], deq[:, rows].T
+    assert np.all(np.abs(got - ref) <= 2 * np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32) + 1e-12)
+    assert np.all(c[len(rows):] == 0)
+
+
 @pytest.mark.parametrize("M,N,K", [(128, 96, 256), (64, 100, 64), (200, 64, 72), (256, 100, 128)])
 def test_q8_kn_kernel_contract(M, N, K):
     """B Q8_0 [K,N] with blocks over the flat index (the layout
