@@ -102,13 +102,37 @@ __device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int 
 	const float4 v0 = *(const float4 *)v, v1 = *(const float4 *)(v + 4);
 	float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 	if (EPI) {
+		float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+		if (p.flags & S3K_EPI_BIAS) {
+			/* n is a multiple of 8 here: 16-byte loads need only an
+			 * aligned bias base */
+			const bool vec = full && (((uintptr_t)p.bias & 15u) == 0) && (n & 7) == 0;
+			if (vec && p.bias_kind != S3K_F32) {
+				/* 8 bf16/f16 values in one 16-byte load */
+				const uint4 w = *(const uint4 *)((const uint16_t *)p.bias + n);
+				const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-		for (int e = 0; e < 8; ++e) {
-			float bv = 0.0f;
-			if ((p.flags & S3K_EPI_BIAS) && (full || n + e < p.N))
-				bv = load_as_f32(p.bias, n + e, p.bias_kind);
-			x[e] = epilogue<CK>(x[e], bv, p.flags);
+				for (int e = 0; e < 4; ++e) {
+					bv[2 * e] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] & 0xFFFFu)
+									     : f16_to_f32(d[e] & 0xFFFFu);
+					bv[2 * e + 1] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] >> 16)
+										 : f16_to_f32(d[e] >> 16);
+				}
+			} else if (vec) {
+				const float4 b0 = *(const float4 *)((const float *)p.bias + n);
+				const float4 b1 = *(const float4 *)((const float *)p.bias + n + 4);
+				bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+				bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+			} else {
+#pragma unroll
+				for (int e = 0; e < 8; ++e)
+					if (full || n + e < p.N)
+						bv[e] = load_as_f32(p.bias, n + e, p.bias_kind);
+			}
 		}
+#pragma unroll
+		for (int e = 0; e < 8; ++e)
+			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
 	}
 	const long long o = (long long)m * p.ldc + n;
 	if (CK == S3K_F32) {
