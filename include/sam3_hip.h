@@ -32,7 +32,7 @@ extern "C" {
  * struct sam3_backend_ops (src/backend/backend.h:31-56). graph_eval runs
  * MATMUL nodes (F32, F16, BF16, F32 x Q8_0) on the GPU, fusing
  * TRANSPOSE(W) -> MATMUL -> ADD(bias) -> GELU chains, and runs ADD,
- * GELU and 2-D TRANSPOSE on the GPU as well; other ops go to the host
+ * GELU, 2-D TRANSPOSE and SDPA on the GPU as well; other ops go to the host
  * dispatcher set with sam3_hip_backend_set_host_dispatch, or fail with
  * SAM3_EDTYPE when none is set (as cpu_dispatch_node does for an op with
  * no kernel, src/backend/cpu/cpu_dispatch.c:664-669).
@@ -99,10 +99,19 @@ enum sam3_error sam3_hip_kernel_matmul_bf16(const struct sam3_node *node, void *
  * cpu_kernel_matmul_q8 (cpu_kernels.h:134-135, cpu_matmul_q8.c:168-235). */
 enum sam3_error sam3_hip_kernel_matmul_q8(const struct sam3_node *node, void *stream);
 
+/* Fused attention, Q K V -> out = softmax(Q K^T / sqrt(hd) + mask) V.
+ * Replaces cpu_kernel_sdpa (src/backend/cpu/kernels/cpu_kernels.h:221,
+ * cpu_sdpa.c:216-288): same inputs (Q, K, V, optional mask [seq_q,
+ * seq_k] shared by all heads), params[0] = head_dim, 2-D [seq, hd] or 4-D
+ * [B, H, seq, hd] tensors. Q, K, V and out share one dtype (F32 as in the
+ * reference, or F16/BF16); the mask is F32. Other ranks are SAM3_EINVAL
+ * (the reference reads them as 2-D). */
+enum sam3_error sam3_hip_kernel_sdpa(const struct sam3_node *node, void *stream);
+
 /* Route one node by op and dtype. Replaces cpu_dispatch_node
  * (src/backend/cpu/cpu_dispatch.c:591-686): same mixed F32 x Q8_0 rule,
  * same SAM3_EDTYPE for mismatched dtypes or an (op, dtype) without a
- * kernel. Runs MATMUL, ADD, GELU and 2-D TRANSPOSE. */
+ * kernel. Runs MATMUL, ADD, GELU, 2-D TRANSPOSE and SDPA. */
 enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream);
 
 /* ------------------------------------------------------------------ */
@@ -171,6 +180,28 @@ enum sam3_error sam3_hip_matmul_on_path(int path, int a_dtype, const void *a,
 					int c_dtype, void *c,
 					int M, int N, int K,
 					const void *bias, int flags, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Plain-pointer attention (device pointers, async on `stream`).        */
+/* ------------------------------------------------------------------ */
+
+/* out[h] = softmax(q[h] k[h]^T / sqrt(D) + mask) v[h] for h < BH, the
+ * computation of cpu_kernel_sdpa (cpu_sdpa.c:49-159 per query row):
+ * q and out [BH, Sq, D], k and v [BH, Sk, D], contiguous, all of `dtype`
+ * (SAM3_DTYPE_F32, _F16 or _BF16); mask f32 [Sq, Sk] or NULL. A query
+ * whose scores are all -inf gets zeros, as there. D = 64 with 16-byte
+ * aligned tensors runs the MFMA kernel (f32 as three bf16 products per
+ * step: hi*hi + lo*hi + hi*lo); other D up to 512 run a one-wave-per-row
+ * f32 kernel. */
+enum sam3_error sam3_hip_sdpa(int dtype, const void *q, const void *k, const void *v,
+			      const float *mask, void *out, int BH, int Sq, int Sk, int D,
+			      void *stream);
+
+/* sam3_hip_sdpa on a forced kernel: 0 = best, 1 = MFMA (D = 64), 3 = the
+ * any-D kernel. SAM3_EINVAL if that kernel cannot run the problem. */
+enum sam3_error sam3_hip_sdpa_on_path(int path, int dtype, const void *q, const void *k,
+				      const void *v, const float *mask, void *out, int BH,
+				      int Sq, int Sk, int D, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Q8_0 format on the device (device pointers, async on `stream`).      */

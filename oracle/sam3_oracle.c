@@ -30,6 +30,7 @@
  */
 #include "sam3_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -603,4 +604,74 @@ void oracle_matmul_bf16_batched(const uint16_t *a, const uint16_t *b,
 		oracle_matmul_bf16(as, bs, cs, M, K, N, n_threads);
 	}
 	free(tmp);
+}
+
+/* ------------------------------------------------------------------ */
+/* SDPA: src/backend/cpu/kernels/cpu_sdpa.c:49-159 (x86 scalar branch)  */
+/* and :216-288. softmax(Q K^T / sqrt(hd) + mask) V per query row with  */
+/* the reference's online softmax: one key at a time, running max and   */
+/* sum, the output rescaled by expf(old_max - new_max) whenever the max */
+/* grows. Q [BH, Sq, D], K and V [BH, Sk, D], mask [Sq, Sk] (shared by  */
+/* all heads) or NULL, out [BH, Sq, D]. Rows split across threads.      */
+/* ------------------------------------------------------------------ */
+struct sdpa_ctx {
+	const float *q, *k, *v, *mask;
+	float *out;
+	int Sq, Sk, D;
+	float scale;
+};
+
+static void sdpa_row(const float *q, const float *K, const float *V, const float *mrow,
+		     float *out, int Sk, int D, float scale)
+{
+	float row_max = -FLT_MAX;
+	float row_sum = 0.0f;
+
+	memset(out, 0, (size_t)D * sizeof(float));
+	for (int j = 0; j < Sk; j++) {
+		const float *kj = K + (size_t)j * D;
+		float score = 0.0f;
+		for (int d = 0; d < D; d++)
+			score += q[d] * kj[d];
+		score *= scale;
+		if (mrow)
+			score += mrow[j];
+		if (score > row_max) {
+			float correction = expf(row_max - score);
+			row_sum *= correction;
+			for (int d = 0; d < D; d++)
+				out[d] *= correction;
+			row_max = score;
+		}
+		float w = expf(score - row_max);
+		const float *vj = V + (size_t)j * D;
+		for (int d = 0; d < D; d++)
+			out[d] += w * vj[d];
+		row_sum += w;
+	}
+	if (row_sum > 0.0f) {
+		float inv_sum = 1.0f / row_sum;
+		for (int d = 0; d < D; d++)
+			out[d] *= inv_sum;
+	}
+}
+
+static void sdpa_rows(void *p, int r0, int r1)
+{
+	struct sdpa_ctx *x = p;
+	for (int idx = r0; idx < r1; idx++) {
+		int bh = idx / x->Sq, i = idx % x->Sq;
+		const float *q = x->q + ((size_t)bh * x->Sq + i) * x->D;
+		const float *k = x->k + (size_t)bh * x->Sk * x->D;
+		const float *v = x->v + (size_t)bh * x->Sk * x->D;
+		const float *m = x->mask ? x->mask + (size_t)i * x->Sk : NULL;
+		sdpa_row(q, k, v, m, x->out + ((size_t)bh * x->Sq + i) * x->D, x->Sk, x->D, x->scale);
+	}
+}
+
+void oracle_sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
+		     float *out, int BH, int Sq, int Sk, int D, int n_threads)
+{
+	struct sdpa_ctx x = { q, k, v, mask, out, Sq, Sk, D, 1.0f / sqrtf((float)D) };
+	run_rows(sdpa_rows, &x, BH * Sq, n_threads);
 }

@@ -82,4 +82,9 @@ void oracle_matmul_bf16_batched(const uint16_t *a, const uint16_t *b,
 				uint16_t *c, int batch, int M, int K, int N,
 				int b_nt, int n_threads);
 
+/* ---- SDPA (src/backend/cpu/kernels/cpu_sdpa.c:49-159, 216-288) ---- */
+/* Q [BH,Sq,D], K/V [BH,Sk,D], mask [Sq,Sk] shared by all heads or NULL. */
+void oracle_sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
+		     float *out, int BH, int Sq, int Sk, int D, int n_threads);
+
 #endif /* SAM3_ORACLE_H */

@@ -83,6 +83,15 @@ int s3k_q8_quantize(const void *src, void *dst, int n, void *stream);
 int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream);
 /* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
 int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
+/* Fused attention out = softmax(Q K^T / sqrt(D) + mask) V over BH heads:
+ * Q and out [BH, Sq, D], K and V [BH, Sk, D], one dtype (S3K_F32, _BF16,
+ * _F16); mask f32 [Sq, Sk] or NULL. s3k_attn_path gives the kernel that
+ * runs the problem (0 = none); s3k_attn runs it on `path` (0 = best). */
+enum { S3K_ATTN_MFMA = 1, S3K_ATTN_GENERIC = 3 };
+int s3k_attn_path(int kind, const void *q, const void *k, const void *v, void *out,
+		  int BH, int Sq, int Sk, int D);
+int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
+	     const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream);
 /* Whether the MFMA path of g (B Q8_0 [N,K]) runs the direct-to-LDS Q8
  * GEMM: f16 A directly, bf16 A after a cast to f16. */
 int s3k_dlq8_eligible(const struct s3k_gemm *g);

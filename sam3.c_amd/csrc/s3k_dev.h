@@ -87,6 +87,17 @@ __device__ __forceinline__ float gelu_tanh(float x)
 	return mul_rn(mul_rn(0.5f, x), add_rn(1.0f, tanh_fast(inner)));
 }
 
+typedef __bf16 s3k_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float s3k_f32x2 __attribute__((ext_vector_type(2)));
+
+/* Pack two f32 as two bf16 (RNE, NaN stays NaN) in one dword, lo first:
+ * one v_cvt_pk_bf16_f32 on gfx950. */
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+	const s3k_f32x2 v = {lo, hi};
+	return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, s3k_bf16x2));
+}
+
 /* Pack two f32 as two f16 (RNE) in one dword, lo first. */
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi)
 {

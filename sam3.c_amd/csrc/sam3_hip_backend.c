@@ -404,7 +404,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	return err;
 }
 
-/* ADD / GELU / TRANSPOSE on device copies of the node's tensors. */
+/* ADD / GELU / TRANSPOSE / SDPA on device copies of the node's tensors. */
 static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct sam3_node *n)
 {
 	struct sam3_tensor tin[SAM3_NODE_MAX_INPUTS], tout;
@@ -432,6 +432,8 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 		err = s3h_add(&dn, hb->stream);
 	else if (n->op == SAM3_OP_GELU)
 		err = s3h_gelu(&dn, hb->stream);
+	else if (n->op == SAM3_OP_SDPA)
+		err = sam3_hip_kernel_sdpa(&dn, hb->stream);
 	else
 		err = s3h_transpose(&dn, hb->stream);
 	if (err == SAM3_OK)
@@ -443,6 +445,8 @@ static int runs_on_gpu(const struct sam3_node *n)
 {
 	if (n->n_inputs < 1 || !n->inputs[0])
 		return 0;
+	if (n->op == SAM3_OP_SDPA)
+		return s3h_sdpa_node_ok(n);
 	const int dt = n->inputs[0]->dtype;
 	for (int k = 1; k < n->n_inputs; k++)
 		if (n->inputs[k] && (int)n->inputs[k]->dtype != dt)

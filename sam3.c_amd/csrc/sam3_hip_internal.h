@@ -22,5 +22,7 @@ enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
 int s3h_transpose_is_swap(const struct sam3_node *node);
+/* Whether sam3_hip_kernel_sdpa takes this node (dtypes, ranks, head_dim). */
+int s3h_sdpa_node_ok(const struct sam3_node *node);
 
 #endif /* SAM3_HIP_INTERNAL_H */

@@ -360,6 +360,50 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 }
 
 /* ------------------------------------------------------------------ */
+/* Attention                                                            */
+/* ------------------------------------------------------------------ */
+enum sam3_error sam3_hip_sdpa_on_path(int path, int dtype, const void *q, const void *k,
+				      const void *v, const float *mask, void *out, int BH,
+				      int Sq, int Sk, int D, void *stream)
+{
+	if (BH < 0 || Sq < 0 || Sk < 0 || D <= 0) {
+		s3h_error("sdpa: negative size or head_dim <= 0");
+		return SAM3_EINVAL;
+	}
+	if (!is_float_dtype(dtype)) {
+		s3h_error("sdpa: dtype %d is not F32, F16 or BF16", dtype);
+		return SAM3_EDTYPE;
+	}
+	if ((long long)BH * Sq == 0)
+		return SAM3_OK;
+	if (!q || !out || (Sk > 0 && (!k || !v))) {
+		s3h_error("sdpa: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	if ((uintptr_t)mask & 3u) {
+		s3h_error("sdpa: mask must be 4-byte aligned");
+		return SAM3_EINVAL;
+	}
+	const int best = s3k_attn_path(dtype, q, k, v, out, BH, Sq, Sk, D);
+	if (!best) {
+		s3h_error("sdpa: no kernel for D=%d (D <= 512, element-aligned tensors)", D);
+		return SAM3_EINVAL;
+	}
+	if (path != 0 && path != S3K_ATTN_GENERIC && !(path == S3K_ATTN_MFMA && best == path)) {
+		s3h_error("sdpa: kernel %d cannot run this problem", path);
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_attn(path, dtype, q, k, v, mask, out, BH, Sq, Sk, D, stream), "sdpa");
+}
+
+enum sam3_error sam3_hip_sdpa(int dtype, const void *q, const void *k, const void *v,
+			      const float *mask, void *out, int BH, int Sq, int Sk, int D,
+			      void *stream)
+{
+	return sam3_hip_sdpa_on_path(0, dtype, q, k, v, mask, out, BH, Sq, Sk, D, stream);
+}
+
+/* ------------------------------------------------------------------ */
 /* Q8_0 format on the device                                            */
 /* ------------------------------------------------------------------ */
 enum sam3_error sam3_hip_q8_quantize(const float *src, void *dst_blocks, int nelems,
@@ -562,6 +606,70 @@ enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream)
 		       "transpose");
 }
 
+/* Shapes as cpu_kernel_sdpa reads them (cpu_sdpa.c:216-288): 4-D
+ * [B, H, seq, hd] or 2-D [seq, hd], head_dim = params[0]. */
+static enum sam3_error sdpa_shape(const struct sam3_node *node, int *BH, int *Sq, int *Sk,
+				  int *D, int quiet)
+{
+#define SDPA_FAIL(code, ...)                    \
+	do {                                    \
+		if (!quiet)                     \
+			s3h_error(__VA_ARGS__); \
+		return code;                    \
+	} while (0)
+	if (!node || node->n_inputs < 3 || !node->inputs[0] || !node->inputs[1] ||
+	    !node->inputs[2] || !node->output) {
+		SDPA_FAIL(SAM3_EINVAL, "sdpa: NULL tensor");
+	}
+	const struct sam3_tensor *Q = node->inputs[0], *K = node->inputs[1],
+				 *V = node->inputs[2], *O = node->output;
+	const struct sam3_tensor *M = node->n_inputs > 3 ? node->inputs[3] : NULL;
+	const int dt = Q->dtype;
+	if (!is_float_dtype(dt) || (int)K->dtype != dt || (int)V->dtype != dt ||
+	    (int)O->dtype != dt || (M && M->dtype != SAM3_DTYPE_F32)) {
+		SDPA_FAIL(SAM3_EDTYPE, "sdpa: Q, K, V and out need one of F32/F16/BF16, mask F32");
+	}
+	const int nd = Q->n_dims;
+	if ((nd != 2 && nd != 4) || K->n_dims != nd || V->n_dims != nd) {
+		SDPA_FAIL(SAM3_EINVAL, "sdpa: tensors must be 2-D [seq, hd] or 4-D [B, H, seq, hd]");
+	}
+	*D = node->params[0];
+	if (nd == 4) {
+		*BH = Q->dims[0] * Q->dims[1];
+		*Sq = Q->dims[2];
+		*Sk = K->dims[2];
+	} else {
+		*BH = 1;
+		*Sq = Q->dims[0];
+		*Sk = K->dims[0];
+	}
+	const long long nq = (long long)*BH * *Sq * *D, nk = (long long)*BH * *Sk * *D;
+	if (*D <= 0 || s3h_nelems(Q) < nq || s3h_nelems(O) < nq || s3h_nelems(K) < nk ||
+	    s3h_nelems(V) < nk || (M && s3h_nelems(M) < (long long)*Sq * *Sk)) {
+		SDPA_FAIL(SAM3_EINVAL, "sdpa: tensor sizes do not match head_dim %d", *D);
+	}
+	return SAM3_OK;
+#undef SDPA_FAIL
+}
+
+int s3h_sdpa_node_ok(const struct sam3_node *node)
+{
+	int BH, Sq, Sk, D;
+	return sdpa_shape(node, &BH, &Sq, &Sk, &D, 1) == SAM3_OK && D <= 512;
+}
+
+enum sam3_error sam3_hip_kernel_sdpa(const struct sam3_node *node, void *stream)
+{
+	int BH, Sq, Sk, D;
+	enum sam3_error err = sdpa_shape(node, &BH, &Sq, &Sk, &D, 0);
+	if (err != SAM3_OK)
+		return err;
+	const struct sam3_tensor *M = node->n_inputs > 3 ? node->inputs[3] : NULL;
+	return sam3_hip_sdpa(node->inputs[0]->dtype, node->inputs[0]->data, node->inputs[1]->data,
+			     node->inputs[2]->data, M ? (const float *)M->data : NULL,
+			     node->output->data, BH, Sq, Sk, D, stream);
+}
+
 enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream)
 {
 	if (!node) {
@@ -574,6 +682,9 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 		s3h_error("hip_dispatch: node op=%d has no inputs", node->op);
 		return SAM3_EINVAL;
 	}
+	/* Q, K, V share a dtype and the mask is F32 (checked by the kernel) */
+	if (node->op == SAM3_OP_SDPA)
+		return sam3_hip_kernel_sdpa(node, stream);
 	int dtype = node->inputs[0]->dtype;
 	const int mixed_q8 = node->op == SAM3_OP_MATMUL && node->n_inputs >= 2 &&
 			     node->inputs[1] && node->inputs[1]->dtype == SAM3_DTYPE_Q8_0 &&

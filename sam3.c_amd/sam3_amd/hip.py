@@ -31,11 +31,14 @@ SIGNATURES = {
     "sam3_hip_kernel_matmul_f16": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_bf16": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_q8": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_sdpa": (_i, [_vp, _vp]),
     "sam3_hip_dispatch_node": (_i, [_vp, _vp]),
     "sam3_hip_matmul": (_i, [_i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),
     "sam3_hip_matmul_q8_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll,
                                         _vp, _i, _vp]),
+    "sam3_hip_sdpa": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "sam3_hip_sdpa_on_path": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "sam3_hip_q8_quantize": (_i, [_vp, _vp, _i, _vp]),
     "sam3_hip_q8_dequantize": (_i, [_vp, _vp, _i, _vp]),
     "sam3_hip_matmul_path": (_i, [_i, _i, _i, _i, _i, _i, _i]),
@@ -236,6 +239,30 @@ def q8_quantize(x):
     out = dq.download(np.uint8, (out.nbytes,))
     dx.free(); dq.free()  # noqa: E702
     return out
+
+
+def sdpa(q, k, v, mask=None, dtype=None, path=0):
+    """Fused attention on the device: q [BH, Sq, D], k and v [BH, Sk, D]
+    host arrays of one dtype (float32, float16, or bfloat16 bits as uint16
+    with dtype=abi.BF16); mask float32 [Sq, Sk] or None. Returns out
+    [BH, Sq, D] with q's element type (uint16 bits for bf16)."""
+    if dtype is None:
+        dtype = {np.dtype(np.float32): abi.F32, np.dtype(np.float16): abi.F16}[q.dtype]
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    host_t = {abi.F32: np.float32, abi.F16: np.float16, abi.BF16: np.uint16}[dtype]
+    bufs = [DeviceBuffer.of(np.ascontiguousarray(x, host_t)) for x in (q, k, v)]
+    dm = DeviceBuffer.of(np.ascontiguousarray(mask, np.float32)) if mask is not None else None
+    do = DeviceBuffer(max(1, BH * Sq * D) * np.dtype(host_t).itemsize)
+    try:
+        check(load().sam3_hip_sdpa_on_path(path, dtype, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr,
+                                           dm.ptr if dm else None, do.ptr, BH, Sq, Sk, D, None),
+              "sdpa")
+        synchronize()
+        return do.download(host_t, (BH, Sq, D))
+    finally:
+        for b in bufs + [do] + ([dm] if dm else []):
+            b.free()
 
 
 def q8_dequantize(blocks, n):

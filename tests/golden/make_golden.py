@@ -142,6 +142,17 @@ def main():
     g["cvt_bf16"] = R.cast(pats, abi.F32, abi.BF16, np.uint16)
     g["cvt_fp16"] = R.cast(pats, abi.F32, abi.F16, np.uint16)
 
+    # -- SDPA (cpu_kernel_sdpa, cpu_sdpa.c:216-288): 4-D path, with and
+    # without the additive mask, ragged key count (not a multiple of the
+    # reference's 64-key tile), head_dim 64.
+    BH, Sq, Sk, D = 3, 37, 70, 64
+    g["sdpa_q"] = synth.randn(synth.tensor_seed(71, 0), (BH, Sq, D)) / 4
+    g["sdpa_k"] = synth.randn(synth.tensor_seed(71, 1), (BH, Sk, D)) / 4
+    g["sdpa_v"] = synth.randn(synth.tensor_seed(71, 2), (BH, Sk, D))
+    g["sdpa_mask"] = synth.randn(synth.tensor_seed(71, 3), (Sq, Sk), 2.0)
+    g["sdpa_out"] = R.sdpa(g["sdpa_q"], g["sdpa_k"], g["sdpa_v"], None, threads=3)
+    g["sdpa_out_mask"] = R.sdpa(g["sdpa_q"], g["sdpa_k"], g["sdpa_v"], g["sdpa_mask"], threads=3)
+
     R.close()
     out = HERE / "matmul_golden.npz"
     np.savez_compressed(out, **g)

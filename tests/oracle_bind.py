@@ -62,6 +62,7 @@ class Oracle:
         L.oracle_transpose_u16.argtypes = [_vp, _vp, _i, _i]
         L.oracle_transpose_f32.argtypes = [_vp, _vp, _i, _i]
         L.oracle_matmul_bf16_batched.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i]
+        L.oracle_sdpa_f32.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]
 
     # ---- Q8 ----
     def q8_quantize(self, x):
@@ -163,6 +164,21 @@ class Oracle:
         return out
 
 
+def _oracle_sdpa(self, q, k, v, mask=None, threads=1):
+    """q [BH,Sq,D], k/v [BH,Sk,D] f32, mask [Sq,Sk] f32 or None."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    m = _c(mask, np.float32) if mask is not None else None
+    out = np.empty_like(q)
+    self.lib.oracle_sdpa_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(m) if m is not None else None,
+                             _ptr(out), BH, Sq, Sk, D, threads)
+    return out
+
+
+Oracle.sdpa = _oracle_sdpa
+
+
 class Ref:
     """The reference's own kernels, called through hand-built nodes."""
 
@@ -176,6 +192,8 @@ class Ref:
                      "cpu_kernel_gelu_f16", "cpu_kernel_cast", "cpu_kernel_transpose"]:
             getattr(L, name).argtypes = [_vp, _vp]
             getattr(L, name).restype = C.c_int
+        L.cpu_kernel_sdpa.argtypes = [_vp, _vp]
+        L.cpu_kernel_sdpa.restype = C.c_int
         L.cpu_dispatch_node.argtypes = [_vp, _vp, _vp]
         L.cpu_dispatch_node.restype = C.c_int
         L.sam3_q8_quantize.argtypes = [_vp, _vp, _i]
@@ -290,6 +308,24 @@ class Ref:
         rc, out = self.run(fn, abi.OP_GELU, [(dt, [x.size], x)], dt, (x.size,), npt)
         assert rc == 0
         return out
+
+
+def _ref_sdpa(self, q, k, v, mask=None, threads=None):
+    """cpu_kernel_sdpa on Q [1,BH,Sq,D] (4-D path), or [Sq,D] when BH == 1
+    and `two_d` layouts are wanted by the caller (cpu_sdpa.c:216-288)."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    ins = [(abi.F32, [1, BH, Sq, D], q), (abi.F32, [1, BH, Sk, D], k), (abi.F32, [1, BH, Sk, D], v)]
+    if mask is not None:
+        ins.append((abi.F32, [Sq, Sk], _c(mask, np.float32)))
+    rc, out = self.run("cpu_kernel_sdpa", abi.OP_SDPA, ins, abi.F32, (1, BH, Sq, D), np.float32,
+                       threads, params=(D, 0, 0, 0))
+    assert rc == 0
+    return out.reshape(BH, Sq, D)
+
+
+Ref.sdpa = _ref_sdpa
 
 
 def have_ref():

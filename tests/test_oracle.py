@@ -250,3 +250,46 @@ def test_batched_equals_slices(O):
         assert np.array_equal(c[s], O.matmul_bf16(a[s], b_kn[s]))
     b_nk = np.ascontiguousarray(np.transpose(b_kn, (0, 2, 1)))
     assert np.array_equal(O.matmul_bf16_batched(a, b_nk, b_nt=True), c)
+
+
+# ------------------------------------------------------------------- SDPA
+def test_golden_sdpa(O):
+    q, k, v, m = GOLD["sdpa_q"], GOLD["sdpa_k"], GOLD["sdpa_v"], GOLD["sdpa_mask"]
+    for threads in (1, 4):
+        assert np.array_equal(bits32(O.sdpa(q, k, v, None, threads)), bits32(GOLD["sdpa_out"]))
+        assert np.array_equal(bits32(O.sdpa(q, k, v, m, threads)), bits32(GOLD["sdpa_out_mask"]))
+
+
+def test_ref_sdpa(O, R):
+    q = synth.randn(81, (2, 50, 64)) / 2
+    k = synth.randn(82, (2, 129, 64)) / 2
+    v = synth.randn(83, (2, 129, 64))
+    m = synth.randn(84, (50, 129))
+    for mask in (None, m):
+        assert np.array_equal(bits32(O.sdpa(q, k, v, mask, 3)), bits32(R.sdpa(q, k, v, mask, 2)))
+
+
+def test_sdpa_closed_forms(O):
+    """Zero queries give equal weights (the mean of V); one key gives that
+    V row; a mask of -inf on all keys but one selects that key's V row
+    exactly; random inputs match a float64 softmax."""
+    BH, Sk, D = 2, 40, 64
+    v = synth.randn(85, (BH, Sk, D))
+    k = synth.randn(86, (BH, Sk, D))
+    q0 = np.zeros((BH, 5, D), np.float32)
+    mean = v.astype(np.float64).mean(axis=1, keepdims=True)
+    assert np.allclose(O.sdpa(q0, k, v), np.broadcast_to(mean, (BH, 5, D)), atol=1e-6)
+    one = O.sdpa(q0[:, :1], k[:, :1], v[:, :1])
+    assert np.array_equal(one, v[:, :1])
+    mask = np.full((5, Sk), -np.inf, np.float32)
+    pick = [3, 0, 39, 17, 17]
+    for i, j in enumerate(pick):
+        mask[i, j] = 0.0
+    q = synth.randn(87, (BH, 5, D))
+    sel = O.sdpa(q, k, v, mask)
+    for i, j in enumerate(pick):
+        assert np.array_equal(sel[:, i], v[:, j])
+    s = np.einsum("bqd,bkd->bqk", q.astype(np.float64), k.astype(np.float64)) / 8.0
+    p = np.exp(s - s.max(axis=2, keepdims=True))
+    ref = np.einsum("bqk,bkd->bqd", p / p.sum(axis=2, keepdims=True), v.astype(np.float64))
+    assert np.max(np.abs(O.sdpa(q, k, v) - ref)) < 1e-5
