@@ -13,7 +13,9 @@ reported under "extra":
   config 4  skinny Q8 GEMVs (M in {1,8,32,77}) over a pool of >256 MB of
             distinct weight copies, reported in HBM GB/s per launch (HIP graph
             of one launch per copy) and for one batched launch
-  config 5  batched attention QK^T / PV, windowed (1296 x 576 x 64)
+  config 5  batched attention QK^T / PV, windowed (1296 x 576 x 64), and
+            the fused SDPA kernel (windowed 1296 x 576, global 16 x 5184;
+            bf16, f16, f32)
 `roofline` is for the headline kernel; `cpu_baseline` times the reference
 CPU bf16 kernel (oracle/_ref, compiled from the reference's own sources)
 on the GPU box's host cores over a bounded row sample of the same GEMM.
@@ -372,6 +374,34 @@ def main():
             "pv_gbs": round(bytes_qk / (ms_pv * 1e-3) / 1e9, 1)}
         for b in (dq, dk, ds, do):
             b.free()
+
+        log("config 5: fused attention (SDPA), windowed and global")
+        fused = {}
+        for name, BH, S in (("windowed", 1296, 576), ("global", 16, 5184)):
+            for dname, dt, es in (("bf16", abi.BF16, 2), ("f16", abi.F16, 2), ("f32", abi.F32, 4)):
+                n = BH * S * D
+                x = synth.randn(synth.tensor_seed(6, 0), (n,))
+                host = (bf16_bits(x) if dt == abi.BF16 else f16_bits(x) if dt == abi.F16
+                        else x)
+                bq = hip.DeviceBuffer.of(host)
+                bk = hip.DeviceBuffer.of(host[::-1].copy())
+                bv = hip.DeviceBuffer.of(host)
+                bo = hip.DeviceBuffer(n * es)
+
+                def sdpa():
+                    hip.check(lib.sam3_hip_sdpa(dt, bq.ptr, bk.ptr, bv.ptr, None, bo.ptr,
+                                                BH, S, S, D, stream), "sdpa")
+
+                ms_f = timer.run(sdpa, 5, 2)
+                tf = 4.0 * BH * S * S * D / (ms_f * 1e-3) / 1e12
+                fused[f"{name}_{dname}"] = {"us": round(ms_f * 1e3, 1), "tflops": round(tf, 1),
+                                            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+                for b in (bq, bk, bv, bo):
+                    b.free()
+        extra["cfg5_sdpa_fused"] = dict(
+            fused, note="one sam3_hip_sdpa launch over BH heads, D=64, no mask; "
+                        "4*S^2*D flops per head (Q K^T and P V)")
+        log("  ", extra["cfg5_sdpa_fused"])
 
     cpu = None
     if not args.no_cpu_baseline:

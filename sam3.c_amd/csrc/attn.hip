@@ -45,22 +45,25 @@ struct AttnArgs {
 	char *out;
 	int Sq, Sk;
 	long long hq, hk;       /* per-head strides, elements */
-	float scale_log2;       /* log2(e) / sqrt(D) */
-	unsigned k_extent;      /* bytes of one head's K (16-bit inputs) */
+	int BH, nqb;            /* heads, query blocks per head */
+	int mask_vec;           /* mask rows 16-byte aligned: float4 loads */
 };
 
-constexpr int AT_D = 64, AT_BQ = 128, AT_BKV = 64;
+constexpr int AT_D = 64, AT_BKV = 64;
 constexpr int AT_VT_PITCH = AT_BKV * 2 + 8;          /* bytes per V^T row */
 constexpr int AT_K_BYTES = AT_BKV * AT_D * 2;        /* 8 KiB per plane */
 constexpr int AT_VT_BYTES = AT_D * AT_VT_PITCH;      /* 8.5 KiB per plane */
 
-template <int DT>
+template <int DT, int NW>
 struct AtCfg {
 	static constexpr bool SPLIT = DT == S3K_F32;
 	static constexpr int NPL = SPLIT ? 2 : 1;        /* bf16 planes */
-	static constexpr int VT_OFF = NPL * AT_K_BYTES;
-	static constexpr int STAGE = NPL * (AT_K_BYTES + AT_VT_BYTES);
+	static constexpr int KS = NPL * AT_K_BYTES;      /* one K slot */
+	static constexpr int VS = NPL * AT_VT_BYTES;     /* one V^T slot */
+	static constexpr int LDS = 2 * KS + 2 * VS;      /* two of each */
 	static constexpr int FAM = DT == S3K_F16 ? FAM_F16 : FAM_BF16;
+	static constexpr int BQ = 32 * NW;                /* queries per workgroup */
+	static constexpr int KJ = (8 + NW - 1) / NW;      /* K loads per wave */
 };
 
 template <int DT>
@@ -70,6 +73,33 @@ __device__ __forceinline__ uint32_t at_pack2(float lo, float hi)
 		return pack_f16x2(lo, hi);
 	else
 		return pack_bf16x2(lo, hi);
+}
+
+/* f32 sum of the two 16-bit values of w, added to acc (v_dot2 with 1, 1) */
+template <int DT>
+__device__ __forceinline__ float at_sum2(uint32_t w, float acc)
+{
+	if constexpr (DT == S3K_F16) {
+		typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+		const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+		return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), one, acc, false);
+	} else {
+		const s3k_bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+		return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s3k_bf16x2, w), one, acc, false);
+	}
+}
+
+/* x combined with the value of lane ^ 32 (v_permlane32_swap) */
+__device__ __forceinline__ float at_max_pair(float x)
+{
+	const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+	return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float at_sum_pair(float x)
+{
+	const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+	return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 /* hi/lo bf16 planes of two f32 values, one dword each */
@@ -87,19 +117,62 @@ __device__ __forceinline__ void at_split8(const float4 &x, const float4 &y, uint
 	at_split2(y.z, y.w, hi.w, lo.w);
 }
 
-template <int DT>
-__global__ void __launch_bounds__(256, 2) attn_fwd(AttnArgs p)
+/* workgroups per CU the registers are budgeted for: four (16 waves) for
+ * the 16-bit kernel without a mask */
+template <int DT, int NW, bool MASK>
+constexpr int at_minb()
 {
-	using C = AtCfg<DT>;
-	__shared__ __attribute__((aligned(1024))) char smem[2 * C::STAGE];
+	return NW != 4 ? 1 : (DT == S3K_F32 || MASK) ? 2 : 4;
+}
+
+template <int N>
+struct at_int {
+	static constexpr int value = N;
+};
+
+/* The probabilities of a tile are formed against the running max m
+ * without first taking the tile's max: they are only recomputed (after
+ * moving m to the tile's max and rescaling the accumulators) when some
+ * lane's 32 probabilities sum past 2^15, which also catches the first
+ * tile (m = -FLT_MAX gives +inf). Every probability the MFMA sees is
+ * then below 2^15, inside the f16 range. */
+constexpr float AT_PSUM_MAX = 32768.0f;
+
+template <int DT, int NW, bool MASK>
+__global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(AttnArgs p)
+{
+	using C = AtCfg<DT, NW>;
+	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int h = lane >> 5, l32 = lane & 31;
-	const long long head = blockIdx.y;
-	const int q = blockIdx.x * AT_BQ + wave * 32 + l32;   /* this lane's query */
-	const unsigned lds0 = lds_addr_of(smem);
 
-	/* Q^T operand: query row q, d chunk 16c + 8h (hi and lo planes for f32) */
+	/* workgroup -> (head, query block): workgroups are dispatched to the 8
+	 * XCDs round-robin, so the nqb blocks of a head are given ids with
+	 * one residue mod 8 and run on one XCD, whose L2 then serves the
+	 * head's K and V to all of them (the heads past the last whole group
+	 * of 8 are laid out plainly) */
+	const unsigned L = blockIdx.x, nqb = (unsigned)p.nqb;
+	const unsigned g8 = (unsigned)(p.BH / 8) * 8u * nqb;
+	unsigned hh, qb;
+	if (L < g8) {
+		const unsigned sl = L >> 3;
+		hh = sl / nqb * 8u + (L & 7u);
+		qb = sl % nqb;
+	} else {
+		hh = (unsigned)(p.BH / 8) * 8u + (L - g8) / nqb;
+		qb = (L - g8) % nqb;
+	}
+	const long long head = hh;
+	const int q0w = (int)qb * C::BQ + wave * 32;         /* the wave's first query */
+	const int q = q0w + l32;                             /* this lane's query */
+	const bool wave_live = q0w < p.Sq;                   /* wave-uniform */
+	const bool stager = wave < 4;                        /* threads 0..255 stage K, V */
+	const unsigned lds0 = lds_addr_of(smem);
+	constexpr int ES = C::SPLIT ? 4 : 2;                 /* input element bytes */
+
+	/* Q^T operand, pre-multiplied by 1/sqrt(64) = 2^-3 (exact): query row
+	 * q, d chunk 16c + 8h (hi and lo planes for f32) */
 	uint4 qh[4], ql[4];
 #pragma unroll
 	for (int c = 0; c < 4; ++c) {
@@ -107,73 +180,94 @@ __global__ void __launch_bounds__(256, 2) attn_fwd(AttnArgs p)
 		if (q < p.Sq) {
 			if constexpr (C::SPLIT) {
 				const float *Q = (const float *)p.q + head * p.hq + (long long)q * AT_D + 16 * c + 8 * h;
-				at_split8(*(const float4 *)Q, *(const float4 *)(Q + 4), qh[c], ql[c]);
+				float4 x = *(const float4 *)Q, y = *(const float4 *)(Q + 4);
+				x.x *= 0.125f, x.y *= 0.125f, x.z *= 0.125f, x.w *= 0.125f;
+				y.x *= 0.125f, y.y *= 0.125f, y.z *= 0.125f, y.w *= 0.125f;
+				at_split8(x, y, qh[c], ql[c]);
 			} else {
 				const uint16_t *Q = (const uint16_t *)p.q + head * p.hq;
-				qh[c] = *(const uint4 *)(Q + (long long)q * AT_D + 16 * c + 8 * h);
+				const uint4 r = *(const uint4 *)(Q + (long long)q * AT_D + 16 * c + 8 * h);
+				const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+				uint32_t o4[4];
+#pragma unroll
+				for (int i = 0; i < 4; ++i) {
+					float lo, hi;
+					if constexpr (DT == S3K_F16) {
+						lo = f16_to_f32(w[i] & 0xFFFFu), hi = f16_to_f32(w[i] >> 16);
+					} else {
+						lo = bf16_to_f32(w[i] & 0xFFFFu), hi = bf16_to_f32(w[i] >> 16);
+					}
+					o4[i] = at_pack2<DT>(lo * 0.125f, hi * 0.125f);
+				}
+				qh[c] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
 			}
 		}
 	}
 
-	/* 16-bit K tile loads: 8 KiB = 8 instructions, 2 per wave; slot s of
-	 * load j holds row s/8, chunk (s%8) ^ swz(row) */
-	const s3k_i32x4 rk = buf_rsrc(p.k + head * p.hk * 2, p.k_extent);
-	unsigned k_off[2];
+	/* the head's K and V as buffers: loads past Sk rows return zeros */
+	const unsigned kv_bytes = (unsigned)((long long)p.Sk * AT_D * ES);
+	const s3k_i32x4 rk = buf_rsrc(p.k + head * p.hk * ES, kv_bytes);
+	const __amdgpu_buffer_rsrc_t bk = __builtin_amdgcn_make_buffer_rsrc(
+		(void *)(p.k + head * p.hk * ES), (short)0, (int)kv_bytes, 0x00020000);
+	const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
+		(void *)(p.v + head * p.hk * ES), (short)0, (int)kv_bytes, 0x00020000);
+	constexpr unsigned TILE_BYTES = AT_BKV * AT_D * ES;  /* one K or V tile in memory */
+
+	/* 16-bit K tile: 8 KiB = 8 direct-to-LDS instructions of 64 x 16
+	 * bytes; wave w issues instructions w, w + NW, ...; slot s of
+	 * instruction j holds row s/8, chunk (s%8) ^ swz(row). Rows past Sk
+	 * are given an offset past the buffer and read as zeros. */
+	unsigned k_off[C::KJ];
 #pragma unroll
-	for (int t = 0; t < 2; ++t) {
-		const int s = (t * 4 + wave) * 64 + lane;
+	for (int t = 0; t < C::KJ; ++t) {
+		const int s = (wave + t * NW) * 64 + lane;
 		const int row = s / 8, c = (s % 8) ^ lds_swz<8>(row);
 		k_off[t] = (unsigned)(row * AT_D * 2 + c * 16);
 	}
-	auto issue_k = [&](int kt) {
-		const unsigned st = lds0 + (unsigned)((kt & 1) * C::STAGE);
+	auto issue_k = [&](int kt, unsigned slot) {
 		const int rows_left = p.Sk - kt * AT_BKV;
 #pragma unroll
-		for (int t = 0; t < 2; ++t) {
-			const int row = ((t * 4 + wave) * 64 + lane) / 8;
-			const unsigned o = row < rows_left ? k_off[t] : S3K_OOB;
-			dma16s(st + (t * 4 + wave) * 1024, rk, o, (unsigned)(kt * AT_BKV * AT_D * 2));
+		for (int t = 0; t < C::KJ; ++t) {
+			const int j = wave + t * NW;
+			if (j < 8) {
+				const int row = (j * 64 + lane) / 8;
+				const unsigned o = row < rows_left ? k_off[t] : S3K_OOB;
+				dma16s(lds0 + slot + j * 1024, rk, o, (unsigned)kt * TILE_BYTES);
+			}
 		}
 	};
 
-	/* f32 K tile: thread t stages row t/4, d 16*(t%4)..+15 */
-	const int kr0 = threadIdx.x >> 2, kd0 = 16 * (threadIdx.x & 3);
-	/* V tile: thread t stages keys 4*(t/16)..+3, d 4*(t%16)..+3 */
-	const int vk0 = 4 * (threadIdx.x >> 4), vd0 = 4 * (threadIdx.x & 15);
-
-	/* registers carrying tile kt+1 from global memory to LDS */
+	/* staging through registers (threads 0..255): f32 K row t/4, d
+	 * 16*(t%4)..+15; V keys 4*(t/16)..+3, d 4*(t%16)..+3 */
+	const int kr0 = (threadIdx.x & 255) >> 2, kd0 = 16 * (threadIdx.x & 3);
+	const int vk0 = 4 * ((threadIdx.x & 255) >> 4), vd0 = 4 * (threadIdx.x & 15);
+	const unsigned kst_off = (unsigned)((kr0 * AT_D + kd0) * ES);
+	const unsigned vst_off = (unsigned)((vk0 * AT_D + vd0) * ES);
 	uint2 vr[4];
 	float4 vf[4], kf[4];
-	auto load_tile = [&](int kt) {
+	auto load_kv = [&](int kt) {
+		const int so = kt * (int)TILE_BYTES;
 		if constexpr (C::SPLIT) {
-			const float *K = (const float *)p.k + head * p.hk;
-			const float *V = (const float *)p.v + head * p.hk;
-			const int krow = kt * AT_BKV + kr0;
 #pragma unroll
 			for (int i = 0; i < 4; ++i)
-				kf[i] = krow < p.Sk ? *(const float4 *)(K + (long long)krow * AT_D + kd0 + 4 * i)
-						    : make_float4(0.f, 0.f, 0.f, 0.f);
+				kf[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+					bk, kst_off + 16 * i, so, 0));
 #pragma unroll
-			for (int i = 0; i < 4; ++i) {
-				const int key = kt * AT_BKV + vk0 + i;
-				vf[i] = key < p.Sk ? *(const float4 *)(V + (long long)key * AT_D + vd0)
-						   : make_float4(0.f, 0.f, 0.f, 0.f);
-			}
+			for (int i = 0; i < 4; ++i)
+				vf[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+					bv, vst_off + i * AT_D * 4, so, 0));
 		} else {
-			const uint16_t *V = (const uint16_t *)p.v + head * p.hk;
 #pragma unroll
-			for (int i = 0; i < 4; ++i) {
-				const int key = kt * AT_BKV + vk0 + i;
-				vr[i] = key < p.Sk ? *(const uint2 *)(V + (long long)key * AT_D + vd0)
-						   : make_uint2(0, 0);
-			}
+			for (int i = 0; i < 4; ++i)
+				vr[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+					bv, vst_off + i * AT_D * 2, so, 0));
 		}
 	};
-	auto store_tile = [&](int kt) {
-		char *st = smem + (kt & 1) * C::STAGE;
-		char *vt = st + C::VT_OFF;
+	auto store_kv = [&](unsigned kslot, unsigned vslot) {
+		char *vt = smem + vslot;
 		if constexpr (C::SPLIT) {
 			/* K hi/lo planes: logical chunks kd0/8 and kd0/8 + 1 of row kr0 */
+			char *st = smem + kslot;
 #pragma unroll
 			for (int u = 0; u < 2; ++u) {
 				uint4 hi, lo;
@@ -211,21 +305,38 @@ __global__ void __launch_bounds__(256, 2) attn_fwd(AttnArgs p)
 		}
 	};
 
+	/* LDS read addresses: K fragment (c, mb) of row 32mb + l32, chunk
+	 * (2c + h) ^ swz(row); V^T row 32md + l32 at key 4h */
+	unsigned ka[4][2];
+#pragma unroll
+	for (int c = 0; c < 4; ++c)
+#pragma unroll
+		for (int mb = 0; mb < 2; ++mb) {
+			const int row = 32 * mb + l32;
+			ka[c][mb] = lds0 + (unsigned)((row * 8 + ((2 * c + h) ^ lds_swz<8>(row))) << 4);
+		}
+	const unsigned va = lds0 + (unsigned)(l32 * AT_VT_PITCH + 8 * h);
+
+	const float *mrow = MASK ? p.mask + (long long)(q < p.Sq ? q : p.Sq - 1) * p.Sk : nullptr;
+
 	s3k_f32x16 o[2];
 #pragma unroll
 	for (int md = 0; md < 2; ++md)
 #pragma unroll
 		for (int r = 0; r < 16; ++r)
 			o[md][r] = 0.0f;
+	/* running max (base-2 exponent units) and running sum of this lane's
+	 * half of the query's keys */
 	float m_run = -3.402823466e38f, l_run = 0.0f;
-
+	constexpr float LOG2E = 1.44269504088896341f;
 	const int nkt = (p.Sk + AT_BKV - 1) / AT_BKV;
-	if constexpr (!C::SPLIT)
-		issue_k(0);
-	load_tile(0);
-	store_tile(0);
 
-	for (int kt = 0; kt < nkt; ++kt) {
+	/* One 64-key tile. P = stage parity (kt & 1), known at compile time so
+	 * that every LDS address is a register plus a constant. */
+	auto step = [&](auto par, int kt) {
+		constexpr int P = decltype(par)::value;
+		constexpr unsigned KSLOT = P * C::KS, VSLOT = 2 * C::KS + P * C::VS;
+		constexpr unsigned KNEXT = (1 - P) * C::KS, VNEXT = 2 * C::KS + (1 - P) * C::VS;
 		const bool more = kt + 1 < nkt;
 		/* K(kt) landed and V^T(kt) stored; every wave is past tile kt-1,
 		 * whose slots are refilled below */
@@ -233,125 +344,179 @@ __global__ void __launch_bounds__(256, 2) attn_fwd(AttnArgs p)
 		__syncthreads();
 		if (more) {
 			if constexpr (!C::SPLIT)
-				issue_k(kt + 1);
-			load_tile(kt + 1);
+				issue_k(kt + 1, KNEXT);
+			if (stager)
+				load_kv(kt + 1);
 		}
 
-		const char *Ks = smem + (kt & 1) * C::STAGE;
-		const char *Vt = Ks + C::VT_OFF;
-
-		/* S^T = K Q^T for keys 32*mb + (row), this lane's query */
-		s3k_f32x16 s[2];
+		if (wave_live) {
+			const int kbase = kt * AT_BKV;
+			/* mask of this tile: element 4g+e of block mb is key
+			 * kbase + 32mb + 8g + 4h + e */
+			float4 mk[2][4];
+			if constexpr (MASK) {
 #pragma unroll
-		for (int mb = 0; mb < 2; ++mb) {
+				for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-			for (int r = 0; r < 16; ++r)
-				s[mb][r] = 0.0f;
-			const int row = 32 * mb + l32;
-#pragma unroll
-			for (int c = 0; c < 4; ++c) {
-				const int off = (row * 8 + ((2 * c + h) ^ lds_swz<8>(row))) << 4;
-				const uint4 kh = *(const uint4 *)(Ks + off);
-				if constexpr (C::SPLIT) {
-					const uint4 kl = *(const uint4 *)(Ks + AT_K_BYTES + off);
-					mfma_chunk<C::FAM>(s[mb], kl, qh[c]);
-					mfma_chunk<C::FAM>(s[mb], kh, ql[c]);
-				}
-				mfma_chunk<C::FAM>(s[mb], kh, qh[c]);
+					for (int g = 0; g < 4; ++g) {
+						const int key0 = kbase + 32 * mb + 8 * g + 4 * h;
+						if (p.mask_vec) {
+							mk[mb][g] = key0 < p.Sk ? *(const float4 *)(mrow + key0)
+										: make_float4(0.f, 0.f, 0.f, 0.f);
+						} else {
+							const int last = p.Sk - 1;
+							mk[mb][g] = make_float4(mrow[min(key0, last)], mrow[min(key0 + 1, last)],
+										mrow[min(key0 + 2, last)], mrow[min(key0 + 3, last)]);
+						}
+					}
 			}
-		}
 
-		/* scale into base 2, mask, -inf past Sk; running max */
-		float mt = -3.402823466e38f;
-		const int kbase = kt * AT_BKV;
+			/* S^T = K Q^T / 8 for keys 32*mb + (row), this lane's query. The
+			 * tile is worked in two 32-key halves mb so that the matrix
+			 * cores and the VALU overlap inside the wave: scores of half 1
+			 * run while the probabilities of half 0 are formed, and P V of
+			 * half 0 while those of half 1 are. */
+			s3k_f32x16 s[2];
+			auto scores_half = [&](int mb) {
 #pragma unroll
-		for (int mb = 0; mb < 2; ++mb)
+				for (int r = 0; r < 16; ++r)
+					s[mb][r] = 0.0f;
 #pragma unroll
-			for (int g = 0; g < 4; ++g) {
-				const int key0 = kbase + 32 * mb + 8 * g + 4 * h;
-				float4 mk = make_float4(0.f, 0.f, 0.f, 0.f);
-				if (p.mask && q < p.Sq) {
-					const float *mrow = p.mask + (long long)q * p.Sk;
-					if (key0 + 4 <= p.Sk && (p.Sk & 3) == 0 && ((uintptr_t)p.mask & 15u) == 0)
-						mk = *(const float4 *)(mrow + key0);
-					else {
-						mk.x = key0 < p.Sk ? mrow[key0] : 0.f;
-						mk.y = key0 + 1 < p.Sk ? mrow[key0 + 1] : 0.f;
-						mk.z = key0 + 2 < p.Sk ? mrow[key0 + 2] : 0.f;
-						mk.w = key0 + 3 < p.Sk ? mrow[key0 + 3] : 0.f;
+				for (int c = 0; c < 4; ++c) {
+					const uint4 kh = *(const uint4 *)(smem + (ka[c][mb] - lds0) + KSLOT);
+					if constexpr (C::SPLIT) {
+						const uint4 kl = *(const uint4 *)(smem + (ka[c][mb] - lds0) + KSLOT + AT_K_BYTES);
+						mfma_chunk<C::FAM>(s[mb], kl, qh[c]);
+						mfma_chunk<C::FAM>(s[mb], kh, ql[c]);
+					}
+					mfma_chunk<C::FAM>(s[mb], kh, qh[c]);
+				}
+			};
+			/* mask and keys past Sk (last tile only) for half mb */
+			auto finish_half = [&](int mb) {
+				if constexpr (MASK) {
+#pragma unroll
+					for (int g = 0; g < 4; ++g) {
+						s[mb][4 * g] += mk[mb][g].x, s[mb][4 * g + 1] += mk[mb][g].y;
+						s[mb][4 * g + 2] += mk[mb][g].z, s[mb][4 * g + 3] += mk[mb][g].w;
 					}
 				}
-				const float mv[4] = {mk.x, mk.y, mk.z, mk.w};
+				if (kbase + AT_BKV > p.Sk) {
 #pragma unroll
-				for (int e = 0; e < 4; ++e) {
-					float v = s[mb][4 * g + e] * p.scale_log2 + mv[e] * 1.44269504088896341f;
-					if (key0 + e >= p.Sk)
-						v = -__builtin_inff();
-					s[mb][4 * g + e] = v;
-					mt = fmaxf(mt, v);
+					for (int r = 0; r < 16; ++r)
+						if (kbase + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3) >= p.Sk)
+							s[mb][r] = -__builtin_inff();
 				}
-			}
-		mt = fmaxf(mt, __shfl_xor(mt, 32));
-		const float m_new = fmaxf(m_run, mt);
-		const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-		m_run = m_new;
+			};
 
-		/* probabilities, packed as the P^T operand of each 16-key chunk */
-		uint4 ph[4], pl[4];
-		float lsum = 0.0f;
+			/* probabilities exp2(s*log2(e) - m) of half mb, packed as the
+			 * P^T operand of its two 16-key chunks, and their sum */
+			uint4 ph[4], pl[4];
+			auto probs = [&](int mb) {
+				const float nm = -m_run;
+				float ts = 0.0f;
 #pragma unroll
-		for (int mb = 0; mb < 2; ++mb)
+				for (int sub = 0; sub < 2; ++sub) {
+					float pv[8];
 #pragma unroll
-			for (int sub = 0; sub < 2; ++sub) {
-				float pv[8];
+					for (int e = 0; e < 8; ++e)
+						pv[e] = __builtin_amdgcn_exp2f(fmaf(s[mb][8 * sub + e], LOG2E, nm));
+					const int cc = 2 * mb + sub;
+					if constexpr (C::SPLIT) {
 #pragma unroll
-				for (int e = 0; e < 8; ++e) {
-					pv[e] = __builtin_amdgcn_exp2f(s[mb][8 * sub + e] - m_new);
-					lsum += pv[e];
+						for (int e = 0; e < 8; ++e)
+							ts += pv[e];
+						at_split8(make_float4(pv[0], pv[1], pv[2], pv[3]),
+							  make_float4(pv[4], pv[5], pv[6], pv[7]), ph[cc], pl[cc]);
+					} else {
+						/* the sum is of the rounded values the MFMA uses */
+						ph[cc] = make_uint4(at_pack2<DT>(pv[0], pv[1]), at_pack2<DT>(pv[2], pv[3]),
+								    at_pack2<DT>(pv[4], pv[5]), at_pack2<DT>(pv[6], pv[7]));
+						ts = at_sum2<DT>(ph[cc].x, ts);
+						ts = at_sum2<DT>(ph[cc].y, ts);
+						ts = at_sum2<DT>(ph[cc].z, ts);
+						ts = at_sum2<DT>(ph[cc].w, ts);
+					}
 				}
-				const int cc = 2 * mb + sub;
-				if constexpr (C::SPLIT) {
-					at_split8(make_float4(pv[0], pv[1], pv[2], pv[3]),
-						  make_float4(pv[4], pv[5], pv[6], pv[7]), ph[cc], pl[cc]);
-				} else {
-					ph[cc] = make_uint4(at_pack2<DT>(pv[0], pv[1]), at_pack2<DT>(pv[2], pv[3]),
-							    at_pack2<DT>(pv[4], pv[5]), at_pack2<DT>(pv[6], pv[7]));
+				return ts;
+			};
+			/* if some lane's sum passed the bound: move the max to the
+			 * tile's, rescale what is accumulated, redo half mb (rare) */
+			auto settle = [&](int mb, float ts) {
+				if (__builtin_amdgcn_ballot_w64(!(ts <= AT_PSUM_MAX))) {
+					float mt = s[0][0];
+#pragma unroll
+					for (int b = 0; b < 2; ++b)
+#pragma unroll
+						for (int r = 0; r < 16; ++r)
+							mt = fmaxf(mt, s[b][r]);
+					const float m_new = fmaxf(m_run, at_max_pair(mt) * LOG2E);
+					const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+					m_run = m_new;
+					l_run *= alpha;
+#pragma unroll
+					for (int md = 0; md < 2; ++md)
+#pragma unroll
+						for (int r = 0; r < 16; ++r)
+							o[md][r] *= alpha;
+					ts = probs(mb);
 				}
-			}
-		l_run = l_run * alpha + lsum;
+				l_run += ts;
+			};
+			/* O^T += V^T P^T over the chunks of half mb: A = V^T rows d,
+			 * keys 16cc + 4h + {0..3, 8..11}, as P^T holds them */
+			auto pv_half = [&](int mb) {
 #pragma unroll
-		for (int md = 0; md < 2; ++md)
+				for (int md = 0; md < 2; ++md) {
+					const char *vrow = smem + (va - lds0) + VSLOT + md * 32 * AT_VT_PITCH;
 #pragma unroll
-			for (int r = 0; r < 16; ++r)
-				o[md][r] *= alpha;
+					for (int cc = 2 * mb; cc < 2 * mb + 2; ++cc) {
+						const uint2 lo = *(const uint2 *)(vrow + 32 * cc);
+						const uint2 hi = *(const uint2 *)(vrow + 32 * cc + 16);
+						const uint4 vh = make_uint4(lo.x, lo.y, hi.x, hi.y);
+						if constexpr (C::SPLIT) {
+							const uint2 llo = *(const uint2 *)(vrow + AT_VT_BYTES + 32 * cc);
+							const uint2 lhi = *(const uint2 *)(vrow + AT_VT_BYTES + 32 * cc + 16);
+							mfma_chunk<C::FAM>(o[md], make_uint4(llo.x, llo.y, lhi.x, lhi.y), ph[cc]);
+							mfma_chunk<C::FAM>(o[md], vh, pl[cc]);
+						}
+						mfma_chunk<C::FAM>(o[md], vh, ph[cc]);
+					}
+				}
+			};
 
-		/* O^T += V^T P^T: A = V^T rows d, keys in the same permuted order */
-#pragma unroll
-		for (int md = 0; md < 2; ++md) {
-			const char *vrow = Vt + (32 * md + l32) * AT_VT_PITCH;
-#pragma unroll
-			for (int cc = 0; cc < 4; ++cc) {
-				const int key = 16 * cc + 4 * h;   /* = 32*mb + 16*sub + 4h */
-				const uint2 lo = *(const uint2 *)(vrow + key * 2);
-				const uint2 hi = *(const uint2 *)(vrow + (key + 8) * 2);
-				const uint4 vh = make_uint4(lo.x, lo.y, hi.x, hi.y);
-				if constexpr (C::SPLIT) {
-					const uint2 llo = *(const uint2 *)(vrow + AT_VT_BYTES + key * 2);
-					const uint2 lhi = *(const uint2 *)(vrow + AT_VT_BYTES + (key + 8) * 2);
-					mfma_chunk<C::FAM>(o[md], make_uint4(llo.x, llo.y, lhi.x, lhi.y), ph[cc]);
-					mfma_chunk<C::FAM>(o[md], vh, pl[cc]);
-				}
-				mfma_chunk<C::FAM>(o[md], vh, ph[cc]);
-			}
+			scores_half(0);
+			finish_half(0);
+			scores_half(1);
+			const float ts0 = probs(0);
+			settle(0, ts0);
+			finish_half(1);
+			pv_half(0);
+			const float ts1 = probs(1);
+			settle(1, ts1);
+			pv_half(1);
 		}
 
-		if (more)
-			store_tile(kt + 1);
+		if (more && stager)
+			store_kv(KNEXT, VNEXT);
+	};
+
+	/* prologue: tile 0 into slot 0 */
+	if constexpr (!C::SPLIT)
+		issue_k(0, 0);
+	if (stager) {
+		load_kv(0);
+		store_kv(0, 2 * C::KS);
+	}
+	for (int kt = 0; kt < nkt; kt += 2) {
+		step(at_int<0>{}, kt);
+		if (kt + 1 < nkt)
+			step(at_int<1>{}, kt + 1);
 	}
 
 	/* normalize (a query with no finite score keeps zeros, as the
 	 * reference's row_sum > 0 test leaves it) and store out[q][d] */
-	const float l_tot = l_run + __shfl_xor(l_run, 32);
+	const float l_tot = at_sum_pair(l_run);
 	const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 	if (q < p.Sq) {
 #pragma unroll
@@ -519,7 +684,7 @@ extern "C" int s3k_attn_path(int kind, const void *q, const void *k, const void 
 	const long long es = kind == S3K_F32 ? 4 : 2;
 	if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & (uintptr_t)(es - 1))
 		return 0;
-	if (D == AT_D && BH >= 1 && BH <= 65535 && Sq >= 1 && Sk >= 1 &&
+	if (D == AT_D && BH >= 1 && Sq >= 1 && Sk >= 1 && (long long)BH * ((Sq + 127) / 128) < (1LL << 31) &&
 	    !(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) &&
 	    (long long)Sk * AT_D * es <= 0x7FFFFFF0LL)
 		return S3K_ATTN_MFMA;
@@ -570,14 +735,42 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 	p.Sk = Sk;
 	p.hq = (long long)Sq * D;
 	p.hk = (long long)Sk * D;
-	p.scale_log2 = 1.44269504088896341f / sqrtf((float)D);
-	p.k_extent = (unsigned)((long long)Sk * D * 2);
-	const dim3 grid((Sq + AT_BQ - 1) / AT_BQ, BH);
-	if (kind == S3K_BF16)
-		hipLaunchKernelGGL(attn_fwd<S3K_BF16>, grid, dim3(256), 0, st, p);
-	else if (kind == S3K_F16)
-		hipLaunchKernelGGL(attn_fwd<S3K_F16>, grid, dim3(256), 0, st, p);
-	else
-		hipLaunchKernelGGL(attn_fwd<S3K_F32>, grid, dim3(256), 0, st, p);
+	p.mask_vec = mask && (Sk & 3) == 0 && ((uintptr_t)mask & 15u) == 0;
+	/* waves per workgroup: 4 (128 queries); 6 and 8 for measurements */
+	int nw = 4;
+	if (kind != S3K_F32) {
+		const char *env = getenv("SAM3_HIP_ATTN_NW");
+		if (env && (atoi(env) == 4 || atoi(env) == 6 || atoi(env) == 8))
+			nw = atoi(env);
+	}
+	p.BH = BH;
+	p.nqb = (Sq + 32 * nw - 1) / (32 * nw);
+	const dim3 grid((unsigned)((long long)p.nqb * BH));
+	const dim3 block(64 * nw);
+#define S3K_ATTN_GO(DT_, NW_)                                                               \
+	do {                                                                                 \
+		if (mask)                                                                    \
+			hipLaunchKernelGGL((attn_fwd<DT_, NW_, true>), grid, block, 0, st, p);   \
+		else                                                                         \
+			hipLaunchKernelGGL((attn_fwd<DT_, NW_, false>), grid, block, 0, st, p);  \
+	} while (0)
+	if (kind == S3K_F32)
+		S3K_ATTN_GO(S3K_F32, 4);
+	else if (kind == S3K_BF16) {
+		if (nw == 4)
+			S3K_ATTN_GO(S3K_BF16, 4);
+		else if (nw == 6)
+			S3K_ATTN_GO(S3K_BF16, 6);
+		else
+			S3K_ATTN_GO(S3K_BF16, 8);
+	} else {
+		if (nw == 4)
+			S3K_ATTN_GO(S3K_F16, 4);
+		else if (nw == 6)
+			S3K_ATTN_GO(S3K_F16, 6);
+		else
+			S3K_ATTN_GO(S3K_F16, 8);
+	}
+#undef S3K_ATTN_GO
 	return (int)hipGetLastError();
 }
