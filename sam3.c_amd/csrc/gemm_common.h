@@ -92,6 +92,16 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int &t
 	tn = in / gsz;
 }
 
+/* Orders this wave's LDS accesses before and after it (compiler fence at
+ * wavefront scope; the hardware performs one wave's LDS operations in
+ * order). */
+__device__ __forceinline__ void wave_lds_fence()
+{
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+	__builtin_amdgcn_wave_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 /* Store of C[m][n..n+7] from 8 f32 values at v (LDS), output kind CK.
  * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
  * points; without it the values are only converted. */
@@ -149,8 +159,11 @@ __device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int 
 	} else {
 		uint32_t h[8];
 #pragma unroll
-		for (int e = 0; e < 8; ++e)
-			h[e] = CK == S3K_BF16 ? f32_to_bf16(x[e]) : f32_to_f16(x[e]);
+		for (int e = 0; e < 8; e += 2) {
+			const uint32_t w = CK == S3K_BF16 ? pack_bf16x2(x[e], x[e + 1]) : pack_f16x2(x[e], x[e + 1]);
+			h[e] = w & 0xFFFFu;
+			h[e + 1] = w >> 16;
+		}
 		uint16_t *c = (uint16_t *)cb + o;
 		if (full && p.vec_ok) {
 			*(uint4 *)c = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16),
@@ -169,9 +182,12 @@ __device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int 
  * into row-contiguous runs of 8 columns through LDS, so each lane finishes
  * 8 outputs and writes them with one 16-byte store. `smem` must be free
  * (all waves past their last LDS read) and hold NW*32*(WTN+8) floats.
- * Every wave of the workgroup must call this (it contains barriers). The
- * store loops are kept rolled: this code runs once per tile, and an
- * unrolled epilogue would not fit the instruction cache. */
+ * Each wave stages through its own region of smem, and the LDS operations
+ * of one wave are performed in program order, so the waves need no
+ * barrier between them here: a wavefront-scope fence keeps the compiler
+ * from moving the staging reads above the writes. The store loops are
+ * kept rolled: this code runs once per tile, and an unrolled epilogue
+ * would not fit the instruction cache. */
 template <int FM, int FN, int WTN, int CK>
 __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&acc)[FM][FN],
 					      char *smem, int wave, int lane, int m0, int n0, int bz)
@@ -188,7 +204,7 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			for (int r = 0; r < 16; ++r)
 				stg[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] =
 					acc[i][j][r];
-		__syncthreads();
+		wave_lds_fence();
 		const int mrow = m0 + i * 32;
 		if (epi) {
 #pragma unroll 1
@@ -205,7 +221,7 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 					finish8<CK, false>(p, cb, mrow + row, n0 + c8, stg + row * PITCH + c8);
 			}
 		}
-		__syncthreads();
+		wave_lds_fence();
 	}
 }
 
