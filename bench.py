@@ -134,6 +134,38 @@ def cpu_baseline(a_bits, w_bits, M, N, K, target_s=10.0):
                       + (f", {model}" if model else "")}
 
 
+def cpu_sdpa(BH, S, D, target_s=4.0):
+    """The reference's f32 SDPA (cpu_kernel_sdpa via oracle/_ref, or the
+    restatement) on the host cores, over a sample of the heads (and, for
+    long sequences, of the queries) of a BH x S x S problem, sized to about
+    target_s seconds; returned as TFLOP/s of 4*S*D flops per (query, key)."""
+    from oracle_bind import Oracle, Ref, have_ref
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    R, kind = (Ref(), "reference") if have_ref() else (Oracle(), "port")
+    k = synth.randn(synth.tensor_seed(7, 1), (1, S, D)) / 4
+    v = synth.randn(synth.tensor_seed(7, 2), (1, S, D))
+    q = synth.randn(synth.tensor_seed(7, 0), (1, S, D)) / 4
+    probe = min(S, 64)
+    t0 = time.perf_counter()
+    R.sdpa(q[:, :probe], k, v, None, threads)
+    per_q = (time.perf_counter() - t0) / probe
+    nq = int(max(probe, min(BH * S, target_s / max(per_q, 1e-9))))
+    heads, rows = (max(1, nq // S), S) if nq >= S else (1, nq)
+    qs = np.ascontiguousarray(np.broadcast_to(q[:, :rows], (heads, rows, D)))
+    ks = np.ascontiguousarray(np.broadcast_to(k, (heads, S, D)))
+    vs = np.ascontiguousarray(np.broadcast_to(v, (heads, S, D)))
+    t0 = time.perf_counter()
+    R.sdpa(qs, ks, vs, None, threads)
+    dt = time.perf_counter() - t0
+    if kind == "reference":
+        R.close()
+    return {"value": round(4.0 * heads * rows * S * D / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": kind,
+            "sample": f"f32 SDPA, {heads} head(s) x {rows} queries x {S} keys, D={D}, "
+                      f"{dt:.2f} s, cpu_kernel_sdpa with a {threads}-thread pool"}
+
+
 def measured_traffic(key):
     """HBM bytes per launch of the headline kernel, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
@@ -401,6 +433,10 @@ def main():
         extra["cfg5_sdpa_fused"] = dict(
             fused, note="one sam3_hip_sdpa launch over BH heads, D=64, no mask; "
                         "4*S^2*D flops per head (Q K^T and P V)")
+        if not args.no_cpu_baseline:
+            log("config 5: reference CPU SDPA (head sample)")
+            extra["cfg5_sdpa_fused"]["cpu_reference"] = {
+                "windowed": cpu_sdpa(1296, 576, D), "global": cpu_sdpa(16, 5184, D)}
         log("  ", extra["cfg5_sdpa_fused"])
 
     cpu = None
