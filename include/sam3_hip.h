@@ -32,7 +32,8 @@ extern "C" {
  * struct sam3_backend_ops (src/backend/backend.h:31-56). graph_eval runs
  * MATMUL nodes (F32, F16, BF16, F32 x Q8_0) on the GPU, fusing
  * TRANSPOSE(W) -> MATMUL -> ADD(bias) -> GELU chains, and runs ADD,
- * GELU, 2-D TRANSPOSE and SDPA on the GPU as well; other ops go to the host
+ * GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE and SLICE on the GPU as well
+ * (RESHAPE is a view: no copy, no transfer); other ops go to the host
  * dispatcher set with sam3_hip_backend_set_host_dispatch, or fail with
  * SAM3_EDTYPE when none is set (as cpu_dispatch_node does for an op with
  * no kernel, src/backend/cpu/cpu_dispatch.c:664-669).
@@ -108,10 +109,35 @@ enum sam3_error sam3_hip_kernel_matmul_q8(const struct sam3_node *node, void *st
  * (the reference reads them as 2-D). */
 enum sam3_error sam3_hip_kernel_sdpa(const struct sam3_node *node, void *stream);
 
+/* The other ops of a ViT block (image_encoder.c:755-916 builds them
+ * through graph_helpers.c:324-520,664-684), on device pointers:
+ *   LAYERNORM over the last dim, eps 1e-5, optional gamma/beta of the
+ *   input's dtype: replaces cpu_kernel_layernorm{,_f16,_bf16}
+ *   (cpu_kernels.h, cpu_layernorm.c:198-254, cpu_layernorm_bf16.c,
+ *   cpu_layernorm_f16.c); mean and variance are summed in another order,
+ *   so f32 results agree to ~1e-6, not bit for bit.
+ *   ROPE on interleaved pairs, x [batch, seq, heads, hd], cos/sin F32
+ *   [seq, hd/2]: replaces cpu_kernel_rope{,_f16,_bf16} (cpu_rope.c:35-108);
+ *   bit-identical.
+ *   SLICE (params axis, start, end): replaces cpu_kernel_slice
+ *   (cpu_slice.c:19-88).
+ *   TRANSPOSE with params as the permutation of up to 4 axes (all zero:
+ *   swap the last two): replaces cpu_kernel_transpose
+ *   (cpu_transpose.c:313-387).
+ *   RESHAPE: a view, output->data = input->data, as cpu_kernel_reshape
+ *   (cpu_reshape.c:19-42). */
+enum sam3_error sam3_hip_kernel_layernorm(const struct sam3_node *node, void *stream);
+enum sam3_error sam3_hip_kernel_rope(const struct sam3_node *node, void *stream);
+enum sam3_error sam3_hip_kernel_slice(const struct sam3_node *node, void *stream);
+enum sam3_error sam3_hip_kernel_transpose(const struct sam3_node *node, void *stream);
+enum sam3_error sam3_hip_kernel_reshape(const struct sam3_node *node);
+
 /* Route one node by op and dtype. Replaces cpu_dispatch_node
  * (src/backend/cpu/cpu_dispatch.c:591-686): same mixed F32 x Q8_0 rule,
  * same SAM3_EDTYPE for mismatched dtypes or an (op, dtype) without a
- * kernel. Runs MATMUL, ADD, GELU, 2-D TRANSPOSE and SDPA. */
+ * kernel. Runs MATMUL, ADD, GELU, TRANSPOSE (up to 4 dims), SDPA,
+ * LAYERNORM, ROPE (F32 cos/sin with any float input, as
+ * cpu_dispatch.c:618-640), SLICE and RESHAPE. */
 enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream);
 
 /* ------------------------------------------------------------------ */

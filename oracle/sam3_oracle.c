@@ -675,3 +675,137 @@ void oracle_sdpa_f32(const float *q, const float *k, const float *v, const float
 	struct sdpa_ctx x = { q, k, v, mask, out, Sq, Sk, D, 1.0f / sqrtf((float)D) };
 	run_rows(sdpa_rows, &x, BH * Sq, n_threads);
 }
+
+/* ------------------------------------------------------------------ */
+/* LayerNorm: cpu_layernorm.c:28-55 (layernorm_row_scalar, the x86      */
+/* build without AVX2), cpu_layernorm_bf16.c:88-115 and                 */
+/* cpu_layernorm_f16.c:99-127 (16-bit in/out, f32 arithmetic). Sums run */
+/* left to right in f32; mean = sum / cols; inv_std =                   */
+/* 1 / sqrtf(var_sum / cols + 1e-5); out = (x - mean) * inv_std, then   */
+/* * gamma, then + beta, each rounded. Rows split across threads.       */
+/* ------------------------------------------------------------------ */
+#define ORACLE_LN_EPS 1e-5f
+
+struct ln_ctx {
+	const void *x, *gamma, *beta;
+	void *out;
+	int cols, kind; /* 0 f32, 1 bf16, 2 f16 */
+};
+
+static float ln_get(const void *p, int kind, size_t i)
+{
+	if (kind == 0)
+		return ((const float *)p)[i];
+	if (kind == 1)
+		return oracle_bf16_to_f32(((const uint16_t *)p)[i]);
+	return oracle_fp16_to_f32(((const uint16_t *)p)[i]);
+}
+
+static void ln_rows(void *p, int r0, int r1)
+{
+	struct ln_ctx *c = p;
+	const int n = c->cols;
+	for (int r = r0; r < r1; r++) {
+		const size_t base = (size_t)r * n;
+		float sum = 0.0f;
+		for (int j = 0; j < n; j++)
+			sum += ln_get(c->x, c->kind, base + j);
+		float mean = sum / (float)n;
+		float var_sum = 0.0f;
+		for (int j = 0; j < n; j++) {
+			float d = ln_get(c->x, c->kind, base + j) - mean;
+			var_sum += d * d;
+		}
+		float inv_std = 1.0f / sqrtf(var_sum / (float)n + ORACLE_LN_EPS);
+		for (int j = 0; j < n; j++) {
+			float val = (ln_get(c->x, c->kind, base + j) - mean) * inv_std;
+			if (c->gamma)
+				val *= ln_get(c->gamma, c->kind, j);
+			if (c->beta)
+				val += ln_get(c->beta, c->kind, j);
+			if (c->kind == 0)
+				((float *)c->out)[base + j] = val;
+			else if (c->kind == 1)
+				((uint16_t *)c->out)[base + j] = oracle_f32_to_bf16(val);
+			else
+				((uint16_t *)c->out)[base + j] = oracle_f32_to_fp16(val);
+		}
+	}
+}
+
+void oracle_layernorm_f32(const float *x, const float *gamma, const float *beta, float *out,
+			  int rows, int cols, int n_threads)
+{
+	struct ln_ctx c = { x, gamma, beta, out, cols, 0 };
+	run_rows(ln_rows, &c, rows, n_threads);
+}
+
+void oracle_layernorm_bf16(const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
+			   uint16_t *out, int rows, int cols, int n_threads)
+{
+	struct ln_ctx c = { x, gamma, beta, out, cols, 1 };
+	run_rows(ln_rows, &c, rows, n_threads);
+}
+
+void oracle_layernorm_f16(const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
+			  uint16_t *out, int rows, int cols, int n_threads)
+{
+	struct ln_ctx c = { x, gamma, beta, out, cols, 2 };
+	run_rows(ln_rows, &c, rows, n_threads);
+}
+
+/* ------------------------------------------------------------------ */
+/* RoPE: cpu_rope.c:88-104 and the 16-bit twins cpu_rope_bf16.c:100-121 */
+/* and cpu_rope_f16.c:100-121. x [batch, seq, heads, hd]; the pair      */
+/* (2d, 2d+1) of every head at position s turns by the angle of         */
+/* cos/sin[s][d]: y0 = x0*c - x1*s, y1 = x0*s + x1*c, each product      */
+/* rounded (no contraction), 16-bit inputs widened and the results      */
+/* rounded once.                                                        */
+/* ------------------------------------------------------------------ */
+static void rope_any(const void *x, const float *cos_t, const float *sin_t, void *y, int batch,
+		     int seq, int heads, int hd, int kind)
+{
+	const int half = hd / 2;
+	for (int b = 0; b < batch; b++)
+		for (int s = 0; s < seq; s++) {
+			const float *cs = cos_t + (size_t)s * half;
+			const float *sn = sin_t + (size_t)s * half;
+			for (int h = 0; h < heads; h++) {
+				const size_t off = (((size_t)b * seq + s) * heads + h) * hd;
+				for (int d = 0; d < half; d++) {
+					float x0 = ln_get(x, kind, off + 2 * d);
+					float x1 = ln_get(x, kind, off + 2 * d + 1);
+					float y0 = x0 * cs[d] - x1 * sn[d];
+					float y1 = x0 * sn[d] + x1 * cs[d];
+					if (kind == 0) {
+						((float *)y)[off + 2 * d] = y0;
+						((float *)y)[off + 2 * d + 1] = y1;
+					} else if (kind == 1) {
+						((uint16_t *)y)[off + 2 * d] = oracle_f32_to_bf16(y0);
+						((uint16_t *)y)[off + 2 * d + 1] = oracle_f32_to_bf16(y1);
+					} else {
+						((uint16_t *)y)[off + 2 * d] = oracle_f32_to_fp16(y0);
+						((uint16_t *)y)[off + 2 * d + 1] = oracle_f32_to_fp16(y1);
+					}
+				}
+			}
+		}
+}
+
+void oracle_rope_f32(const float *x, const float *cos_t, const float *sin_t, float *y,
+		     int batch, int seq, int heads, int hd)
+{
+	rope_any(x, cos_t, sin_t, y, batch, seq, heads, hd, 0);
+}
+
+void oracle_rope_bf16(const uint16_t *x, const float *cos_t, const float *sin_t, uint16_t *y,
+		      int batch, int seq, int heads, int hd)
+{
+	rope_any(x, cos_t, sin_t, y, batch, seq, heads, hd, 1);
+}
+
+void oracle_rope_f16(const uint16_t *x, const float *cos_t, const float *sin_t, uint16_t *y,
+		     int batch, int seq, int heads, int hd)
+{
+	rope_any(x, cos_t, sin_t, y, batch, seq, heads, hd, 2);
+}

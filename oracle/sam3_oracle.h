@@ -87,4 +87,25 @@ void oracle_matmul_bf16_batched(const uint16_t *a, const uint16_t *b,
 void oracle_sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
 		     float *out, int BH, int Sq, int Sk, int D, int n_threads);
 
+/* ---- LayerNorm over the last dim, eps 1e-5 (x86 scalar paths:
+ * src/backend/cpu/kernels/cpu_layernorm.c:28-55, cpu_layernorm_bf16.c:
+ * 88-115, cpu_layernorm_f16.c:99-127). gamma/beta of length cols or NULL,
+ * in the input's dtype. ---- */
+void oracle_layernorm_f32(const float *x, const float *gamma, const float *beta, float *out,
+			  int rows, int cols, int n_threads);
+void oracle_layernorm_bf16(const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
+			   uint16_t *out, int rows, int cols, int n_threads);
+void oracle_layernorm_f16(const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
+			  uint16_t *out, int rows, int cols, int n_threads);
+
+/* ---- RoPE, interleaved pairs (cpu_rope.c:88-104, cpu_rope_bf16.c:100-121,
+ * cpu_rope_f16.c:100-121): x [batch, seq, heads, hd], cos/sin f32
+ * [seq, hd/2]. ---- */
+void oracle_rope_f32(const float *x, const float *cos_t, const float *sin_t, float *y,
+		     int batch, int seq, int heads, int hd);
+void oracle_rope_bf16(const uint16_t *x, const float *cos_t, const float *sin_t, uint16_t *y,
+		      int batch, int seq, int heads, int hd);
+void oracle_rope_f16(const uint16_t *x, const float *cos_t, const float *sin_t, uint16_t *y,
+		     int batch, int seq, int heads, int hd);
+
 #endif /* SAM3_ORACLE_H */

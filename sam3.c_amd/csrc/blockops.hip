@@ -1,0 +1,300 @@
+/*
+ * blockops.hip - the non-matmul ops of a ViT block on gfx950, so that a
+ * block's activations stay in HBM between its matmuls and attention:
+ *
+ *   - LayerNorm over the last dim (src/backend/cpu/kernels/cpu_layernorm.c:
+ *     28-55, 198-254; bf16/f16 twins cpu_layernorm_bf16.c:88-115 and
+ *     cpu_layernorm_f16.c:99-127): one wave per row, the row held in
+ *     registers, mean and variance by wave reductions in f32 (a different
+ *     summation order from the reference's left-to-right loop), then
+ *     (x - mean) * inv_std, * gamma, + beta with one rounding each, as
+ *     there.
+ *   - RoPE on interleaved pairs (cpu_rope.c:88-104, cpu_rope_bf16.c:100-121,
+ *     cpu_rope_f16.c:100-121): one lane per pair, y0 = x0*c - x1*s and
+ *     y1 = x0*s + x1*c with each product rounded (no contraction), which is
+ *     bit-identical to the reference's f32 arithmetic.
+ *   - Permutation of up to 4 axes (cpu_transpose.c:313-387): one lane per
+ *     output element, or per 16/8/4-byte chunk of it when the last axis
+ *     stays last.
+ */
+#include "gemm_common.h"
+
+namespace s3k {
+
+template <int DT>
+__device__ __forceinline__ float bo_ld(const void *p, long long i)
+{
+	if constexpr (DT == S3K_F32)
+		return ((const float *)p)[i];
+	else if constexpr (DT == S3K_BF16)
+		return bf16_to_f32(((const uint16_t *)p)[i]);
+	else
+		return f16_to_f32(((const uint16_t *)p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void bo_st(void *p, long long i, float v)
+{
+	if constexpr (DT == S3K_F32)
+		((float *)p)[i] = v;
+	else if constexpr (DT == S3K_BF16)
+		((uint16_t *)p)[i] = (uint16_t)f32_to_bf16(v);
+	else
+		((uint16_t *)p)[i] = (uint16_t)f32_to_f16(v);
+}
+
+__device__ __forceinline__ float bo_wave_sum(float v)
+{
+#pragma unroll
+	for (int off = 32; off; off >>= 1)
+		v += __shfl_xor(v, off);
+	return v;
+}
+
+/* One wave per row; element j of the row is held by lane j % 64 in slot
+ * j / 64 (EPL slots cover cols <= 64 * EPL). EPL = 0: rows of any length,
+ * re-read from memory in each pass. */
+template <int DT, int EPL>
+__global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *gamma,
+						   const void *beta, void *out, int rows, int cols)
+{
+	const int lane = threadIdx.x & 63;
+	const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (row >= rows)
+		return;
+	const long long base = row * cols;
+	constexpr int N = EPL > 0 ? EPL : 1;
+	float v[N];
+	float sum = 0.0f;
+	if constexpr (EPL > 0) {
+#pragma unroll
+		for (int i = 0; i < EPL; ++i) {
+			const int j = lane + 64 * i;
+			v[i] = j < cols ? bo_ld<DT>(x, base + j) : 0.0f;
+			sum += v[i];
+		}
+	} else {
+		for (int j = lane; j < cols; j += 64)
+			sum += bo_ld<DT>(x, base + j);
+	}
+	const float mean = bo_wave_sum(sum) / (float)cols;
+	float var = 0.0f;
+	if constexpr (EPL > 0) {
+#pragma unroll
+		for (int i = 0; i < EPL; ++i) {
+			const float d = sub_rn(v[i], mean);
+			if (lane + 64 * i < cols)
+				var = fmaf(d, d, var);
+		}
+	} else {
+		for (int j = lane; j < cols; j += 64) {
+			const float d = sub_rn(bo_ld<DT>(x, base + j), mean);
+			var = fmaf(d, d, var);
+		}
+	}
+	const float inv_std = 1.0f / sqrtf(bo_wave_sum(var) / (float)cols + 1e-5f);
+	auto finish = [&](int j, float xj) {
+		float val = mul_rn(sub_rn(xj, mean), inv_std);
+		if (gamma)
+			val = mul_rn(val, bo_ld<DT>(gamma, j));
+		if (beta)
+			val = add_rn(val, bo_ld<DT>(beta, j));
+		bo_st<DT>(out, base + j, val);
+	};
+	if constexpr (EPL > 0) {
+#pragma unroll
+		for (int i = 0; i < EPL; ++i) {
+			const int j = lane + 64 * i;
+			if (j < cols)
+				finish(j, v[i]);
+		}
+	} else {
+		for (int j = lane; j < cols; j += 64)
+			finish(j, bo_ld<DT>(x, base + j));
+	}
+}
+
+/* pair p covers elements 2p, 2p+1 of x; its position s and frequency d
+ * index the [seq, half] tables */
+template <int DT>
+__global__ void __launch_bounds__(256) rope_k(const void *x, const float *cos_t,
+					      const float *sin_t, void *out, long long pairs,
+					      int seq, int heads, int half)
+{
+	const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
+	if (p >= pairs)
+		return;
+	const int d = (int)(p % half);
+	const long long rest = p / half;
+	const int s = (int)((rest / heads) % seq);
+	const float c = cos_t[(long long)s * half + d], sn = sin_t[(long long)s * half + d];
+	const float x0 = bo_ld<DT>(x, 2 * p), x1 = bo_ld<DT>(x, 2 * p + 1);
+	bo_st<DT>(out, 2 * p, sub_rn(mul_rn(x0, c), mul_rn(x1, sn)));
+	bo_st<DT>(out, 2 * p + 1, add_rn(mul_rn(x0, sn), mul_rn(x1, c)));
+}
+
+struct PermArgs {
+	const char *src;
+	char *dst;
+	unsigned od1, od2, od3;          /* output dims 1..3 (dim 0 implied) */
+	long long st0, st1, st2, st3;    /* input stride (elements) of output axis k */
+	long long total;
+};
+
+/* I: index type, 32-bit when the element count allows it */
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) permute_k(PermArgs a)
+{
+	const I stride = (I)gridDim.x * 256, total = (I)a.total;
+	const I od1 = a.od1, od2 = a.od2, od3 = a.od3;
+	for (I i = (I)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+		I t = i;
+		const I o3 = t % od3;
+		t /= od3;
+		const I o2 = t % od2;
+		t /= od2;
+		const I o1 = t % od1;
+		const I o0 = t / od1;
+		const long long src = (long long)o0 * a.st0 + (long long)o1 * a.st1 +
+				      (long long)o2 * a.st2 + (long long)o3 * a.st3;
+		((T *)a.dst)[i] = ((const T *)a.src)[src];
+	}
+}
+
+template <typename T>
+static void launch_perm(const PermArgs &a, dim3 grid, hipStream_t st)
+{
+	if (a.total + (long long)grid.x * 256 < (1LL << 32))
+		hipLaunchKernelGGL((permute_k<T, unsigned>), grid, dim3(256), 0, st, a);
+	else
+		hipLaunchKernelGGL((permute_k<T, long long>), grid, dim3(256), 0, st, a);
+}
+
+template <int DT>
+static void launch_ln(const void *x, const void *g, const void *b, void *o, int rows, int cols,
+		      hipStream_t st)
+{
+	const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+	if (cols <= 256)
+		hipLaunchKernelGGL((layernorm_k<DT, 4>), grid, block, 0, st, x, g, b, o, rows, cols);
+	else if (cols <= 512)
+		hipLaunchKernelGGL((layernorm_k<DT, 8>), grid, block, 0, st, x, g, b, o, rows, cols);
+	else if (cols <= 1024)
+		hipLaunchKernelGGL((layernorm_k<DT, 16>), grid, block, 0, st, x, g, b, o, rows, cols);
+	else if (cols <= 2048)
+		hipLaunchKernelGGL((layernorm_k<DT, 32>), grid, block, 0, st, x, g, b, o, rows, cols);
+	else
+		hipLaunchKernelGGL((layernorm_k<DT, 0>), grid, block, 0, st, x, g, b, o, rows, cols);
+}
+
+} /* namespace s3k */
+
+using namespace s3k;
+
+extern "C" int s3k_layernorm(int kind, const void *x, const void *gamma, const void *beta,
+			     void *out, long long rows, int cols, void *stream)
+{
+	if (rows < 0 || cols <= 0 || rows > 0x7FFFFFFFLL)
+		return (int)hipErrorInvalidValue;
+	if (rows == 0)
+		return (int)hipSuccess;
+	const hipStream_t st = (hipStream_t)stream;
+	if (kind == S3K_F32)
+		launch_ln<S3K_F32>(x, gamma, beta, out, (int)rows, cols, st);
+	else if (kind == S3K_BF16)
+		launch_ln<S3K_BF16>(x, gamma, beta, out, (int)rows, cols, st);
+	else if (kind == S3K_F16)
+		launch_ln<S3K_F16>(x, gamma, beta, out, (int)rows, cols, st);
+	else
+		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t,
+			void *out, int batch, int seq, int heads, int hd, void *stream)
+{
+	if (batch < 0 || seq < 0 || heads < 0 || hd <= 0 || (hd & 1))
+		return (int)hipErrorInvalidValue;
+	const long long pairs = (long long)batch * seq * heads * (hd / 2);
+	if (pairs == 0)
+		return (int)hipSuccess;
+	const hipStream_t st = (hipStream_t)stream;
+	const dim3 grid((unsigned)((pairs + 255) / 256)), block(256);
+	if (kind == S3K_F32)
+		hipLaunchKernelGGL(rope_k<S3K_F32>, grid, block, 0, st, x, cos_t, sin_t, out, pairs,
+				   seq, heads, hd / 2);
+	else if (kind == S3K_BF16)
+		hipLaunchKernelGGL(rope_k<S3K_BF16>, grid, block, 0, st, x, cos_t, sin_t, out, pairs,
+				   seq, heads, hd / 2);
+	else if (kind == S3K_F16)
+		hipLaunchKernelGGL(rope_k<S3K_F16>, grid, block, 0, st, x, cos_t, sin_t, out, pairs,
+				   seq, heads, hd / 2);
+	else
+		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
+}
+
+/* dst = src permuted: output axis k is input axis axes[k]; ndim <= 4,
+ * esize bytes per element. */
+extern "C" int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
+			   const int *axes, void *stream)
+{
+	if (ndim < 1 || ndim > 4 || esize <= 0)
+		return (int)hipErrorInvalidValue;
+	/* pad to 4 axes with leading size-1 axes */
+	long long d[4] = {1, 1, 1, 1};
+	int ax[4] = {0, 1, 2, 3};
+	const int pad = 4 - ndim;
+	int seen = 0;
+	for (int k = 0; k < ndim; ++k) {
+		if (in_dims[k] < 0 || axes[k] < 0 || axes[k] >= ndim || (seen >> axes[k]) & 1)
+			return (int)hipErrorInvalidValue;
+		seen |= 1 << axes[k];
+		d[pad + k] = in_dims[k];
+		ax[pad + k] = pad + axes[k];
+	}
+	long long es = esize;
+	/* the last axis stays last: move it in chunks of up to 16 bytes */
+	if (ax[3] == 3) {
+		long long row = d[3] * es;
+		long long chunk = 1;
+		for (long long c = 16; c > 1; c >>= 1)
+			if (c <= row && row % c == 0 && ((uintptr_t)src % c) == 0 && ((uintptr_t)dst % c) == 0) {
+				chunk = c;
+				break;
+			}
+		if (chunk > 1 && chunk >= es) {
+			d[3] = row / chunk;
+			es = chunk;
+		}
+	}
+	const long long ist[4] = {d[1] * d[2] * d[3], d[2] * d[3], d[3], 1};
+	PermArgs a;
+	a.src = (const char *)src;
+	a.dst = (char *)dst;
+	a.od1 = (unsigned)d[ax[1]];
+	a.od2 = (unsigned)d[ax[2]];
+	a.od3 = (unsigned)d[ax[3]];
+	a.st0 = ist[ax[0]];
+	a.st1 = ist[ax[1]];
+	a.st2 = ist[ax[2]];
+	a.st3 = ist[ax[3]];
+	a.total = d[0] * d[1] * d[2] * d[3];
+	if (a.total == 0)
+		return (int)hipSuccess;
+	if (a.od1 == 0 || a.od2 == 0 || a.od3 == 0)
+		return (int)hipSuccess;
+	const hipStream_t st = (hipStream_t)stream;
+	const long long blocks = (a.total + 255) / 256;
+	const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
+	(void)block;
+	switch (es) {
+	case 1:  launch_perm<uint8_t>(a, grid, st); break;
+	case 2:  launch_perm<uint16_t>(a, grid, st); break;
+	case 4:  launch_perm<uint32_t>(a, grid, st); break;
+	case 8:  launch_perm<uint2>(a, grid, st); break;
+	case 16: launch_perm<uint4>(a, grid, st); break;
+	default: return (int)hipErrorInvalidValue;
+	}
+	return (int)hipGetLastError();
+}

@@ -92,6 +92,17 @@ int s3k_attn_path(int kind, const void *q, const void *k, const void *v, void *o
 		  int BH, int Sq, int Sk, int D);
 int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
 	     const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream);
+/* ViT block ops (blockops.hip). LayerNorm over the last dim of rows x
+ * cols (gamma/beta of the input's kind or NULL, eps 1e-5); RoPE on
+ * interleaved pairs of x [batch, seq, heads, hd] with f32 cos/sin
+ * [seq, hd/2]; permutation of up to 4 axes (output axis k = input axis
+ * axes[k]) of esize-byte elements. */
+int s3k_layernorm(int kind, const void *x, const void *gamma, const void *beta, void *out,
+		  long long rows, int cols, void *stream);
+int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, void *out,
+	     int batch, int seq, int heads, int hd, void *stream);
+int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
+		const int *axes, void *stream);
 /* Whether the MFMA path of g (B Q8_0 [N,K]) runs the direct-to-LDS Q8
  * GEMM: f16 A directly, bf16 A after a cast to f16. */
 int s3k_dlq8_eligible(const struct s3k_gemm *g);

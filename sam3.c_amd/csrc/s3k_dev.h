@@ -33,6 +33,12 @@ __device__ __forceinline__ float add_rn(float a, float b)
 	return a + b;
 }
 
+__device__ __forceinline__ float sub_rn(float a, float b)
+{
+#pragma clang fp contract(off)
+	return a - b;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t b)
 {
 	return __uint_as_float(b << 16);

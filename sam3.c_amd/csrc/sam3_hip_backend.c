@@ -404,7 +404,8 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	return err;
 }
 
-/* ADD / GELU / TRANSPOSE / SDPA on device copies of the node's tensors. */
+/* ADD, GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE, SLICE on device copies of
+ * the node's tensors. */
 static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct sam3_node *n)
 {
 	struct sam3_tensor tin[SAM3_NODE_MAX_INPUTS], tout;
@@ -434,6 +435,12 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 		err = s3h_gelu(&dn, hb->stream);
 	else if (n->op == SAM3_OP_SDPA)
 		err = sam3_hip_kernel_sdpa(&dn, hb->stream);
+	else if (n->op == SAM3_OP_LAYERNORM)
+		err = s3h_layernorm(&dn, hb->stream);
+	else if (n->op == SAM3_OP_ROPE)
+		err = s3h_rope(&dn, hb->stream);
+	else if (n->op == SAM3_OP_SLICE)
+		err = s3h_slice(&dn, hb->stream);
 	else
 		err = s3h_transpose(&dn, hb->stream);
 	if (err == SAM3_OK)
@@ -447,6 +454,8 @@ static int runs_on_gpu(const struct sam3_node *n)
 		return 0;
 	if (n->op == SAM3_OP_SDPA)
 		return s3h_sdpa_node_ok(n);
+	if (n->op == SAM3_OP_ROPE)
+		return s3h_rope_ok(n);
 	const int dt = n->inputs[0]->dtype;
 	for (int k = 1; k < n->n_inputs; k++)
 		if (n->inputs[k] && (int)n->inputs[k]->dtype != dt)
@@ -456,7 +465,11 @@ static int runs_on_gpu(const struct sam3_node *n)
 	case SAM3_OP_GELU:
 		return float_dt(dt);
 	case SAM3_OP_TRANSPOSE:
-		return s3h_dtype_size(dt) != 0 && s3h_transpose_is_swap(n);
+		return s3h_transpose_ok(n);
+	case SAM3_OP_LAYERNORM:
+		return s3h_layernorm_ok(n);
+	case SAM3_OP_SLICE:
+		return s3h_slice_ok(n);
 	default:
 		return 0;
 	}
@@ -531,6 +544,10 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		int used = 1;
 		if (n->op == SAM3_OP_NONE) {
 			err = SAM3_OK;
+		} else if (n->op == SAM3_OP_RESHAPE) {
+			/* a view: consumers find the input's device copy under the
+			 * same host address */
+			err = s3h_reshape(n);
 		} else if (n->op == SAM3_OP_TRANSPOSE && transpose_folds(g, i, &uses)) {
 			folded[i] = 1;
 			hb->stats.fused_nodes++;

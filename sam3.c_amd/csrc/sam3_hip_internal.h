@@ -22,6 +22,16 @@ enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
 int s3h_transpose_is_swap(const struct sam3_node *node);
+/* ViT block ops on device pointers; the _ok forms say whether the node
+ * runs on the GPU (dtypes and shapes), without reporting an error. */
+int s3h_transpose_ok(const struct sam3_node *node);
+int s3h_layernorm_ok(const struct sam3_node *node);
+enum sam3_error s3h_layernorm(const struct sam3_node *node, void *stream);
+int s3h_rope_ok(const struct sam3_node *node);
+enum sam3_error s3h_rope(const struct sam3_node *node, void *stream);
+int s3h_slice_ok(const struct sam3_node *node);
+enum sam3_error s3h_slice(const struct sam3_node *node, void *stream);
+enum sam3_error s3h_reshape(const struct sam3_node *node);
 /* Whether sam3_hip_kernel_sdpa takes this node (dtypes, ranks, head_dim). */
 int s3h_sdpa_node_ok(const struct sam3_node *node);
 

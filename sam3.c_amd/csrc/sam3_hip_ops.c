@@ -584,6 +584,46 @@ int s3h_transpose_is_swap(const struct sam3_node *node)
 	return node->params[nd - 2] == nd - 1 && node->params[nd - 1] == nd - 2;
 }
 
+/* Axes of a TRANSPOSE node as cpu_kernel_transpose reads them
+ * (cpu_transpose.c:330-348): params[0..nd-1]; all zero means the legacy
+ * swap of the last two dims. */
+static void transpose_axes(const struct sam3_node *node, int nd, int *axes)
+{
+	int any = 0;
+	for (int i = 0; i < nd; i++) {
+		axes[i] = node->params[i];
+		if (axes[i])
+			any = 1;
+	}
+	if (!any) {
+		for (int i = 0; i < nd; i++)
+			axes[i] = i;
+		if (nd >= 2) {
+			axes[nd - 2] = nd - 1;
+			axes[nd - 1] = nd - 2;
+		}
+	}
+}
+
+int s3h_transpose_ok(const struct sam3_node *node)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output)
+		return 0;
+	const struct sam3_tensor *in = node->inputs[0];
+	const int nd = in->n_dims;
+	if (nd < 1 || nd > 4 || s3h_dtype_size(in->dtype) == 0 ||
+	    s3h_nelems(node->output) != s3h_nelems(in))
+		return 0;
+	int axes[4], seen = 0;
+	transpose_axes(node, nd, axes);
+	for (int i = 0; i < nd; i++) {
+		if (axes[i] < 0 || axes[i] >= nd || ((seen >> axes[i]) & 1))
+			return 0;
+		seen |= 1 << axes[i];
+	}
+	return 1;
+}
+
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream)
 {
 	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
@@ -591,19 +631,205 @@ enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream)
 		return SAM3_EINVAL;
 	}
 	const struct sam3_tensor *in = node->inputs[0];
-	if (!s3h_transpose_is_swap(node) || s3h_dtype_size(in->dtype) == 0) {
-		s3h_error("transpose: only last-two-dims swaps of element dtypes run on HIP");
+	if (s3h_dtype_size(in->dtype) == 0) {
+		s3h_error("transpose: dtype %d has no element size", in->dtype);
 		return SAM3_EDTYPE;
 	}
-	const int rows = in->dims[in->n_dims - 2], cols = in->dims[in->n_dims - 1];
-	const long long batch = rows && cols ? s3h_nelems(in) / ((long long)rows * cols) : 0;
-	if (s3h_nelems(node->output) != s3h_nelems(in)) {
-		s3h_error("transpose: output size mismatch");
+	if (!s3h_transpose_ok(node)) {
+		s3h_error("transpose: need 1-4 dims, a permutation in params and a same-size output");
 		return SAM3_EINVAL;
 	}
-	return s3h_hip(s3k_transpose2d((int)s3h_dtype_size(in->dtype), in->data,
-				       node->output->data, (int)batch, rows, cols, stream),
+	const int nd = in->n_dims;
+	if (nd >= 2 && s3h_transpose_is_swap(node)) {
+		const int rows = in->dims[nd - 2], cols = in->dims[nd - 1];
+		const long long batch = rows && cols ? s3h_nelems(in) / ((long long)rows * cols) : 0;
+		return s3h_hip(s3k_transpose2d((int)s3h_dtype_size(in->dtype), in->data,
+					       node->output->data, (int)batch, rows, cols, stream),
+			       "transpose");
+	}
+	int axes[4];
+	transpose_axes(node, nd, axes);
+	return s3h_hip(s3k_permute((int)s3h_dtype_size(in->dtype), in->data, node->output->data,
+				   nd, in->dims, axes, stream),
 		       "transpose");
+}
+
+/* LAYERNORM (cpu_layernorm.c:198-254 and its bf16/f16 twins): the last
+ * dim is normalized; gamma and beta (optional) have the input's dtype. */
+int s3h_layernorm_ok(const struct sam3_node *node)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output)
+		return 0;
+	const struct sam3_tensor *in = node->inputs[0];
+	if (!is_float_dtype(in->dtype) || in->n_dims < 1 || (int)node->output->dtype != in->dtype ||
+	    s3h_nelems(node->output) != s3h_nelems(in))
+		return 0;
+	const int cols = in->dims[in->n_dims - 1];
+	if (cols <= 0)
+		return 0;
+	for (int k = 1; k < node->n_inputs && k < 3; k++) {
+		const struct sam3_tensor *t = node->inputs[k];
+		if (t && ((int)t->dtype != in->dtype || s3h_nelems(t) < cols))
+			return 0;
+	}
+	return 1;
+}
+
+enum sam3_error s3h_layernorm(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("layernorm: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *in = node->inputs[0];
+	if (!is_float_dtype(in->dtype)) {
+		s3h_error("layernorm: unsupported dtype %d", in->dtype);
+		return SAM3_EDTYPE;
+	}
+	if (!s3h_layernorm_ok(node)) {
+		s3h_error("layernorm: output, gamma or beta does not match the input");
+		return SAM3_EINVAL;
+	}
+	const int cols = in->dims[in->n_dims - 1];
+	const void *g = node->n_inputs > 1 && node->inputs[1] ? node->inputs[1]->data : NULL;
+	const void *b = node->n_inputs > 2 && node->inputs[2] ? node->inputs[2]->data : NULL;
+	return s3h_hip(s3k_layernorm(in->dtype, in->data, g, b, node->output->data,
+				     s3h_nelems(in) / cols, cols, stream),
+		       "layernorm");
+}
+
+/* ROPE (cpu_rope.c:35-108 and its bf16/f16 twins): x [batch, seq, heads,
+ * hd] (F32, F16 or BF16), cos and sin F32 [seq, hd/2]. */
+int s3h_rope_ok(const struct sam3_node *node)
+{
+	if (node->n_inputs < 3 || !node->inputs[0] || !node->inputs[1] || !node->inputs[2] ||
+	    !node->output)
+		return 0;
+	const struct sam3_tensor *x = node->inputs[0], *c = node->inputs[1], *s = node->inputs[2];
+	if (!is_float_dtype(x->dtype) || x->n_dims != 4 || (x->dims[3] & 1) ||
+	    c->dtype != SAM3_DTYPE_F32 || s->dtype != SAM3_DTYPE_F32 ||
+	    (int)node->output->dtype != x->dtype || s3h_nelems(node->output) != s3h_nelems(x))
+		return 0;
+	const int seq = x->dims[1], half = x->dims[3] / 2;
+	return c->n_dims == 2 && c->dims[0] == seq && c->dims[1] == half && s->n_dims == 2 &&
+	       s->dims[0] == seq && s->dims[1] == half;
+}
+
+enum sam3_error s3h_rope(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 3 || !node->inputs[0] || !node->inputs[1] || !node->inputs[2] ||
+	    !node->output) {
+		s3h_error("rope: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *x = node->inputs[0];
+	if (!is_float_dtype(x->dtype) || node->inputs[1]->dtype != SAM3_DTYPE_F32 ||
+	    node->inputs[2]->dtype != SAM3_DTYPE_F32) {
+		s3h_error("rope: input must be F32/F16/BF16 and cos/sin F32");
+		return SAM3_EDTYPE;
+	}
+	if (!s3h_rope_ok(node)) {
+		s3h_error("rope: need x [batch, seq, heads, hd] (hd even) and cos/sin [seq, hd/2]");
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_rope(x->dtype, x->data, (const float *)node->inputs[1]->data,
+				(const float *)node->inputs[2]->data, node->output->data, x->dims[0],
+				x->dims[1], x->dims[2], x->dims[3], stream),
+		       "rope");
+}
+
+/* SLICE (cpu_slice.c:19-88): params axis, start, end; one strided copy. */
+int s3h_slice_ok(const struct sam3_node *node)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output)
+		return 0;
+	const struct sam3_tensor *in = node->inputs[0];
+	const int axis = node->params[0], start = node->params[1], end = node->params[2];
+	return s3h_dtype_size(in->dtype) != 0 && axis >= 0 && axis < in->n_dims && start >= 0 &&
+	       end <= in->dims[axis] && start < end && node->output->n_dims > axis &&
+	       node->output->dims[axis] == end - start;
+}
+
+enum sam3_error s3h_slice(const struct sam3_node *node, void *stream)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("slice: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *in = node->inputs[0];
+	const size_t es = s3h_dtype_size(in->dtype);
+	if (!es) {
+		s3h_error("slice: dtype %d has no element size", in->dtype);
+		return SAM3_EDTYPE;
+	}
+	if (!s3h_slice_ok(node)) {
+		s3h_error("slice: invalid axis or range [%d, %d)", node->params[1], node->params[2]);
+		return SAM3_EINVAL;
+	}
+	const int axis = node->params[0], start = node->params[1], end = node->params[2];
+	size_t outer = 1, inner = 1;
+	for (int d = 0; d < axis; d++)
+		outer *= (size_t)in->dims[d];
+	for (int d = axis + 1; d < in->n_dims; d++)
+		inner *= (size_t)in->dims[d];
+	const size_t width = (size_t)(end - start) * inner * es;
+	const size_t spitch = (size_t)in->dims[axis] * inner * es;
+	if (!outer || !width)
+		return SAM3_OK;
+	return s3h_hip(hipMemcpy2DAsync(node->output->data, width,
+					(const char *)in->data + (size_t)start * inner * es, spitch,
+					width, outer, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+		       "slice");
+}
+
+/* RESHAPE (cpu_reshape.c:19-42): a view. The output takes the input's
+ * data pointer and row-major strides; nothing is copied. */
+enum sam3_error s3h_reshape(const struct sam3_node *node)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("reshape: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *in = node->inputs[0];
+	struct sam3_tensor *out = node->output;
+	if (s3h_nelems(in) != s3h_nelems(out)) {
+		s3h_error("reshape: element count mismatch %lld != %lld", s3h_nelems(in),
+			  s3h_nelems(out));
+		return SAM3_EINVAL;
+	}
+	out->data = in->data;
+	out->nbytes = in->nbytes;
+	int st = 1;
+	for (int i = out->n_dims - 1; i >= 0; i--) {
+		out->strides[i] = st;
+		st *= out->dims[i];
+	}
+	return SAM3_OK;
+}
+
+enum sam3_error sam3_hip_kernel_layernorm(const struct sam3_node *node, void *stream)
+{
+	return node ? s3h_layernorm(node, stream) : (s3h_error("layernorm: NULL node"), SAM3_EINVAL);
+}
+
+enum sam3_error sam3_hip_kernel_rope(const struct sam3_node *node, void *stream)
+{
+	return node ? s3h_rope(node, stream) : (s3h_error("rope: NULL node"), SAM3_EINVAL);
+}
+
+enum sam3_error sam3_hip_kernel_slice(const struct sam3_node *node, void *stream)
+{
+	return node ? s3h_slice(node, stream) : (s3h_error("slice: NULL node"), SAM3_EINVAL);
+}
+
+enum sam3_error sam3_hip_kernel_transpose(const struct sam3_node *node, void *stream)
+{
+	return node ? s3h_transpose(node, stream) : (s3h_error("transpose: NULL node"), SAM3_EINVAL);
+}
+
+enum sam3_error sam3_hip_kernel_reshape(const struct sam3_node *node)
+{
+	return node ? s3h_reshape(node) : (s3h_error("reshape: NULL node"), SAM3_EINVAL);
 }
 
 /* Shapes as cpu_kernel_sdpa reads them (cpu_sdpa.c:216-288): 4-D
@@ -682,9 +908,15 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 		s3h_error("hip_dispatch: node op=%d has no inputs", node->op);
 		return SAM3_EINVAL;
 	}
-	/* Q, K, V share a dtype and the mask is F32 (checked by the kernel) */
+	/* Q, K, V share a dtype and the mask is F32 (checked by the kernel);
+	 * ROPE takes F32 cos/sin with any float input (cpu_dispatch.c:618-640);
+	 * RESHAPE is a view of any dtype */
 	if (node->op == SAM3_OP_SDPA)
 		return sam3_hip_kernel_sdpa(node, stream);
+	if (node->op == SAM3_OP_ROPE)
+		return s3h_rope(node, stream);
+	if (node->op == SAM3_OP_RESHAPE)
+		return s3h_reshape(node);
 	int dtype = node->inputs[0]->dtype;
 	const int mixed_q8 = node->op == SAM3_OP_MATMUL && node->n_inputs >= 2 &&
 			     node->inputs[1] && node->inputs[1]->dtype == SAM3_DTYPE_Q8_0 &&
@@ -724,8 +956,16 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 			return s3h_gelu(node, stream);
 		break;
 	case SAM3_OP_TRANSPOSE:
-		if (s3h_dtype_size(dtype) && s3h_transpose_is_swap(node))
+		if (s3h_dtype_size(dtype))
 			return s3h_transpose(node, stream);
+		break;
+	case SAM3_OP_LAYERNORM:
+		if (is_float_dtype(dtype))
+			return s3h_layernorm(node, stream);
+		break;
+	case SAM3_OP_SLICE:
+		if (s3h_dtype_size(dtype))
+			return s3h_slice(node, stream);
 		break;
 	default:
 		break;

@@ -31,6 +31,7 @@ F32, F16, BF16, I32, I8, Q8_0 = range(6)
 # enum sam3_op (only the members the matmul path touches are named)
 OP_NONE, OP_MATMUL, OP_ADD, OP_MUL, OP_SOFTMAX, OP_RELU, OP_GELU = range(7)
 OP_LAYERNORM, OP_CONV2D, OP_RESHAPE, OP_TRANSPOSE, OP_CAST = range(7, 12)
+OP_CONCAT, OP_SLICE, OP_EMBED, OP_SIGMOID, OP_UPSAMPLE, OP_ROPE = range(12, 18)
 OP_SDPA = 21
 
 

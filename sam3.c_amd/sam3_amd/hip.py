@@ -32,6 +32,11 @@ SIGNATURES = {
     "sam3_hip_kernel_matmul_bf16": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_q8": (_i, [_vp, _vp]),
     "sam3_hip_kernel_sdpa": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_layernorm": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_rope": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_slice": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_transpose": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_reshape": (_i, [_vp]),
     "sam3_hip_dispatch_node": (_i, [_vp, _vp]),
     "sam3_hip_matmul": (_i, [_i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),

@@ -153,6 +153,18 @@ def main():
     g["sdpa_out"] = R.sdpa(g["sdpa_q"], g["sdpa_k"], g["sdpa_v"], None, threads=3)
     g["sdpa_out_mask"] = R.sdpa(g["sdpa_q"], g["sdpa_k"], g["sdpa_v"], g["sdpa_mask"], threads=3)
 
+    # -- LayerNorm (cpu_layernorm.c, f32, eps 1e-5) over a 96-wide last dim
+    # with gamma and beta, and RoPE (cpu_rope.c, f32) on [2, 9, 3, 16].
+    g["ln_x"] = synth.randn(synth.tensor_seed(72, 0), (37, 96), 3.0, 0.5)
+    g["ln_gamma"] = synth.randn(synth.tensor_seed(72, 1), (96,))
+    g["ln_beta"] = synth.randn(synth.tensor_seed(72, 2), (96,))
+    g["ln_out"] = R.layernorm(g["ln_x"], g["ln_gamma"], g["ln_beta"], "f32")
+    g["rope_x"] = synth.randn(synth.tensor_seed(73, 0), (2, 9, 3, 16))
+    ang = np.outer(np.arange(9), 1.0 / (10000.0 ** (np.arange(8) / 8.0)))
+    g["rope_cos"] = np.cos(ang).astype(np.float32)
+    g["rope_sin"] = np.sin(ang).astype(np.float32)
+    g["rope_out"] = R.rope(g["rope_x"], g["rope_cos"], g["rope_sin"], "f32")
+
     R.close()
     out = HERE / "matmul_golden.npz"
     np.savez_compressed(out, **g)

@@ -63,6 +63,10 @@ class Oracle:
         L.oracle_transpose_f32.argtypes = [_vp, _vp, _i, _i]
         L.oracle_matmul_bf16_batched.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i]
         L.oracle_sdpa_f32.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]
+        for name in ["oracle_layernorm_f32", "oracle_layernorm_bf16", "oracle_layernorm_f16"]:
+            getattr(L, name).argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i]
+        for name in ["oracle_rope_f32", "oracle_rope_bf16", "oracle_rope_f16"]:
+            getattr(L, name).argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i]
 
     # ---- Q8 ----
     def q8_quantize(self, x):
@@ -177,6 +181,37 @@ def _oracle_sdpa(self, q, k, v, mask=None, threads=1):
 
 
 Oracle.sdpa = _oracle_sdpa
+
+_KIND_NP = {"f32": np.float32, "bf16": np.uint16, "f16": np.uint16}
+_KIND_DT = {"f32": abi.F32, "bf16": abi.BF16, "f16": abi.F16}
+
+
+def _oracle_layernorm(self, x, gamma=None, beta=None, kind="f32", threads=1):
+    """x [..., cols] of `kind` (bf16/f16 as uint16 bits); gamma/beta [cols]."""
+    t = _KIND_NP[kind]
+    x = _c(x, t)
+    cols = x.shape[-1]
+    g = _c(gamma, t) if gamma is not None else None
+    b = _c(beta, t) if beta is not None else None
+    out = np.empty_like(x)
+    getattr(self.lib, f"oracle_layernorm_{kind}")(_ptr(x), _ptr(g) if g is not None else None,
+                                                   _ptr(b) if b is not None else None, _ptr(out),
+                                                   x.size // cols, cols, threads)
+    return out
+
+
+def _oracle_rope(self, x, cos_t, sin_t, kind="f32"):
+    """x [batch, seq, heads, hd] of `kind`; cos/sin f32 [seq, hd/2]."""
+    x = _c(x, _KIND_NP[kind])
+    cos_t, sin_t = _c(cos_t, np.float32), _c(sin_t, np.float32)
+    out = np.empty_like(x)
+    getattr(self.lib, f"oracle_rope_{kind}")(_ptr(x), _ptr(cos_t), _ptr(sin_t), _ptr(out),
+                                              *x.shape)
+    return out
+
+
+Oracle.layernorm = _oracle_layernorm
+Oracle.rope = _oracle_rope
 
 
 class Ref:
@@ -326,6 +361,60 @@ def _ref_sdpa(self, q, k, v, mask=None, threads=None):
 
 
 Ref.sdpa = _ref_sdpa
+
+
+def _ref_layernorm(self, x, gamma=None, beta=None, kind="f32", threads=None):
+    """SAM3_OP_LAYERNORM through cpu_dispatch_node (cpu_layernorm*.c)."""
+    t, dt = _KIND_NP[kind], _KIND_DT[kind]
+    x = _c(x, t)
+    ins = [(dt, list(x.shape), x)]
+    for p in (gamma, beta):
+        if p is None:
+            break
+        ins.append((dt, [x.shape[-1]], _c(p, t)))
+    rc, out = self.run("dispatch", abi.OP_LAYERNORM, ins, dt, x.shape, t, threads)
+    assert rc == 0
+    return out
+
+
+def _ref_rope(self, x, cos_t, sin_t, kind="f32"):
+    """SAM3_OP_ROPE through cpu_dispatch_node (cpu_rope*.c)."""
+    t, dt = _KIND_NP[kind], _KIND_DT[kind]
+    x = _c(x, t)
+    ins = [(dt, list(x.shape), x), (abi.F32, list(cos_t.shape), _c(cos_t, np.float32)),
+           (abi.F32, list(sin_t.shape), _c(sin_t, np.float32))]
+    rc, out = self.run("dispatch", abi.OP_ROPE, ins, dt, x.shape, t, None,
+                       params=(x.shape[3], 0, 0, 0))
+    assert rc == 0
+    return out
+
+
+def _ref_slice(self, x, dt, axis, start, end):
+    """SAM3_OP_SLICE (cpu_slice.c:19-88) on a numpy array of sam3 dtype dt."""
+    x = np.ascontiguousarray(x)
+    dims = list(x.shape)
+    dims[axis] = end - start
+    rc, out = self.run("dispatch", abi.OP_SLICE, [(dt, list(x.shape), x)], dt, dims, x.dtype,
+                       None, params=(axis, start, end, 0))
+    assert rc == 0
+    return out
+
+
+def _ref_permute(self, x, dt, axes):
+    """SAM3_OP_TRANSPOSE with explicit axes (cpu_transpose.c:313-387)."""
+    x = np.ascontiguousarray(x)
+    dims = [x.shape[a] for a in axes]
+    params = tuple(axes) + (0,) * (4 - len(axes))
+    rc, out = self.run("dispatch", abi.OP_TRANSPOSE, [(dt, list(x.shape), x)], dt, dims, x.dtype,
+                       None, params=params)
+    assert rc == 0
+    return out
+
+
+Ref.layernorm = _ref_layernorm
+Ref.rope = _ref_rope
+Ref.slice = _ref_slice
+Ref.permute = _ref_permute
 
 
 def have_ref():

@@ -142,10 +142,31 @@ def test_dispatch_routing_errors():
     assert d(C.byref(_node(abi.OP_SOFTMAX, [x], _t(abi.F32, [4, 4]))), None) == abi.EDTYPE
     assert d(C.byref(_node(abi.OP_MATMUL, [_t(abi.I32, [2, 2]), _t(abi.I32, [2, 2])],
                            _t(abi.I32, [2, 2]))), None) == abi.EDTYPE
-    # a transpose with a permutation other than a last-two-dims swap
+    # transposes: params that are not a permutation, and a dtype without an
+    # element size (Q8_0 is blocked)
     t3 = _t(abi.F32, [2, 3, 4])
-    assert d(C.byref(_node(abi.OP_TRANSPOSE, [t3], _t(abi.F32, [3, 2, 4]), (1, 0, 2, 0))),
+    assert d(C.byref(_node(abi.OP_TRANSPOSE, [t3], _t(abi.F32, [3, 3, 2]), (1, 1, 0, 0))),
+             None) == abi.EINVAL
+    assert d(C.byref(_node(abi.OP_TRANSPOSE, [_t(abi.Q8_0, [32, 4])], _t(abi.Q8_0, [4, 32]))),
              None) == abi.EDTYPE
+    # block ops: bad shapes and dtypes are refused before any launch
+    assert d(C.byref(_node(abi.OP_LAYERNORM, [_t(abi.I32, [4, 4])], _t(abi.I32, [4, 4]))),
+             None) == abi.EDTYPE
+    assert d(C.byref(_node(abi.OP_LAYERNORM, [x, _t(abi.F32, [3])], _t(abi.F32, [4, 4]))),
+             None) == abi.EINVAL
+    x4 = _t(abi.F32, [1, 5, 2, 8])
+    assert d(C.byref(_node(abi.OP_ROPE, [x4, _t(abi.F32, [5, 4]), _t(abi.F32, [4, 4])],
+                           _t(abi.F32, [1, 5, 2, 8]))), None) == abi.EINVAL
+    assert d(C.byref(_node(abi.OP_ROPE, [x4, _t(abi.BF16, [5, 4]), _t(abi.BF16, [5, 4])],
+                           _t(abi.F32, [1, 5, 2, 8]))), None) == abi.EDTYPE
+    assert d(C.byref(_node(abi.OP_SLICE, [t3], _t(abi.F32, [2, 2, 4]), (1, 2, 5, 0))),
+             None) == abi.EINVAL
+    # RESHAPE is a view: the output takes the input's data pointer
+    src, dst = _t(abi.F32, [2, 6]), _t(abi.F32, [3, 4])
+    src.data = 0x1000
+    assert d(C.byref(_node(abi.OP_RESHAPE, [src], dst)), None) == abi.OK
+    assert dst.data == 0x1000 and list(dst.strides)[:2] == [4, 1]
+    assert d(C.byref(_node(abi.OP_RESHAPE, [src], _t(abi.F32, [5]))), None) == abi.EINVAL
     # shape errors inside a routed matmul
     assert d(C.byref(_node(abi.OP_MATMUL, [_t(abi.F32, [4, 8]), _t(abi.Q8_0, [9, 4])],
                            _t(abi.F32, [4, 4]))), None) == abi.EINVAL

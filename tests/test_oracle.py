@@ -293,3 +293,69 @@ def test_sdpa_closed_forms(O):
     p = np.exp(s - s.max(axis=2, keepdims=True))
     ref = np.einsum("bqk,bkd->bqd", p / p.sum(axis=2, keepdims=True), v.astype(np.float64))
     assert np.max(np.abs(O.sdpa(q, k, v) - ref)) < 1e-5
+
+
+# ------------------------------------------------------------- LayerNorm
+def _kind_cast(O, x, kind):
+    if kind == "f32":
+        return np.ascontiguousarray(x, np.float32)
+    conv = O.f32_to_bf16 if kind == "bf16" else O.f32_to_fp16
+    return conv(x).reshape(np.shape(x))
+
+
+def test_golden_layernorm(O):
+    out = O.layernorm(GOLD["ln_x"], GOLD["ln_gamma"], GOLD["ln_beta"], "f32", threads=3)
+    assert np.array_equal(bits32(out), bits32(GOLD["ln_out"]))
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("affine", [2, 1, 0])
+def test_ref_layernorm(O, R, kind, affine):
+    x = synth.randn(91, (29, 160), 2.0, -1.0)
+    g, b = synth.randn(92, (160,)), synth.randn(93, (160,))
+    xi, gi, bi = (_kind_cast(O, t, kind) for t in (x, g, b))
+    args = (gi if affine >= 1 else None, bi if affine >= 2 else None)
+    a = O.layernorm(xi, *args, kind=kind, threads=4)
+    r = R.layernorm(xi, *args, kind=kind)
+    assert np.array_equal(a.view(np.uint8), r.view(np.uint8))
+
+
+def test_layernorm_closed_forms(O):
+    """Rows come out with mean 0 and variance var/(var + eps) (float64),
+    a constant row gives exactly beta, and gamma/beta apply per column."""
+    x = synth.randn(94, (16, 256), 3.0, 2.0)
+    y = O.layernorm(x).astype(np.float64)
+    assert np.max(np.abs(y.mean(axis=1))) < 1e-6
+    var = x.astype(np.float64).var(axis=1)
+    assert np.allclose(y.var(axis=1), var / (var + 1e-5), atol=1e-5)
+    const = np.full((3, 64), 7.25, np.float32)
+    beta = synth.randn(95, (64,))
+    out = O.layernorm(const, np.ones(64, np.float32), beta)
+    assert np.array_equal(bits32(out), bits32(np.broadcast_to(beta, (3, 64))))
+
+
+# ------------------------------------------------------------------ RoPE
+def test_golden_rope(O):
+    out = O.rope(GOLD["rope_x"], GOLD["rope_cos"], GOLD["rope_sin"], "f32")
+    assert np.array_equal(bits32(out), bits32(GOLD["rope_out"]))
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
+def test_ref_rope(O, R, kind):
+    x = _kind_cast(O, synth.randn(96, (2, 11, 4, 32)), kind)
+    c, s = synth.randn(97, (11, 16)), synth.randn(98, (11, 16))
+    assert np.array_equal(O.rope(x, c, s, kind).view(np.uint8), R.rope(x, c, s, kind).view(np.uint8))
+
+
+def test_rope_closed_forms(O):
+    """cos 1 / sin 0 is the identity; cos 0 / sin 1 maps (x0, x1) to
+    (-x1, x0) exactly; a rotation keeps each pair's norm (float64)."""
+    x = synth.randn(99, (1, 5, 2, 8))
+    one, zero = np.ones((5, 4), np.float32), np.zeros((5, 4), np.float32)
+    assert np.array_equal(bits32(O.rope(x, one, zero)), bits32(x))
+    y = O.rope(x, zero, one)
+    assert np.array_equal(y[..., 0::2], -x[..., 1::2]) and np.array_equal(y[..., 1::2], x[..., 0::2])
+    ang = synth.randn(100, (5, 4))
+    y = O.rope(x, np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)).astype(np.float64)
+    n0 = np.hypot(x[..., 0::2].astype(np.float64), x[..., 1::2])
+    assert np.allclose(np.hypot(y[..., 0::2], y[..., 1::2]), n0, rtol=1e-6)
