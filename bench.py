@@ -166,6 +166,96 @@ def cpu_sdpa(BH, S, D, target_s=4.0):
                       f"{dt:.2f} s, cpu_kernel_sdpa with a {threads}-thread pool"}
 
 
+def vit_block_flops(npos, e, heads, mlp, seq):
+    """GEMM flops of a ViT-L block (qkv, proj, fc1, fc2) plus attention's
+    4*S^2*D per head over npos/seq windows."""
+    gemm = 2.0 * npos * e * (3 * e + e + 2 * mlp)
+    return gemm + 4.0 * (npos // seq) * heads * seq * seq * (e // heads)
+
+
+def vit_block_graph(grid, window, e, heads, mlp, is_global, wkind, x_dev=None, seed=500):
+    """One ViT-L block as image_encoder.c:755-916 builds it (sam3_amd.graph),
+    f32 activations, weights f32 or Q8_0 (quantized on the device) in the
+    checkpoint layout [out, in]; x on the device when x_dev is given."""
+    from sam3_amd import graph
+    G = graph.Graph()
+    npos = grid * grid
+    if x_dev is not None:
+        x = abi.make_tensor(abi.F32, [npos, e], x_dev, npos * e * 4)
+        G.keep.append(x)
+    else:
+        x = G.tensor(abi.F32, (npos, e), synth.randn(seed, (npos, e)), ephemeral=1)
+
+    def w(i, shape, std, quant=False):
+        v = synth.randn(seed + i, shape, std)
+        if quant and wkind == "q8":
+            return G.tensor(abi.Q8_0, shape, hip.q8_quantize(v))
+        return G.tensor(abi.F32, shape, v)
+    p = {"ln1_w": w(1, (e,), 1.0), "ln1_b": w(2, (e,), 0.1),
+         "qkv_w": w(3, (3 * e, e), 0.03, True), "qkv_b": w(4, (3 * e,), 0.02),
+         "proj_w": w(5, (e, e), 0.03, True), "proj_b": w(6, (e,), 0.02),
+         "ln2_w": w(7, (e,), 1.0), "ln2_b": w(8, (e,), 0.1),
+         "fc1_w": w(9, (mlp, e), 0.03, True), "fc1_b": w(10, (mlp,), 0.02),
+         "fc2_w": w(11, (e, mlp), 0.03, True), "fc2_b": w(12, (e,), 0.02)}
+    c, s_ = graph.rope_tables(grid if is_global else window, e // heads)
+    tc, ts = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s_.shape, s_)
+    out = graph.vit_block(G, x, p, heads, grid, window, is_global, tc, ts)
+    return G, out
+
+
+def vit_block_bench(is_global, wkind, steps=5, warmup=2):
+    """A full ViT-L block (72x72 tokens, e 1024, 16 heads, MLP 4096, window
+    24) through the backend's graph_eval with the block input in HBM and
+    no readback: the latency a sam3.c caller of the vtable sees, weights
+    resident after the first eval."""
+    grid, window, e, heads, mlp = 72, 24, 1024, 16, 4096
+    npos = grid * grid
+    xd = hip.DeviceBuffer.of(synth.randn(500, (npos, e)))
+    G, _ = vit_block_graph(grid, window, e, heads, mlp, is_global, wkind, xd.ptr)
+    G.g.no_readback = True
+    be = hip.Backend(0)
+    try:
+        for _ in range(warmup):
+            hip.check(be.graph_eval(G.g), "graph_eval")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hip.check(be.graph_eval(G.g), "graph_eval")
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        st = be.stats()
+    finally:
+        be.close()
+        xd.free()
+    fl = vit_block_flops(npos, e, heads, mlp, npos if is_global else window * window)
+    return {"ms": round(ms, 3), "tokens_per_s": round(npos / (ms * 1e-3), 1),
+            "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "nodes": G.g.n_nodes,
+            "gpu_nodes": st.gpu_nodes, "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes}
+
+
+def vit_block_cpu(threads=None):
+    """The reference's CPU kernels (cpu_dispatch_node over the same node
+    sequence, oracle/_ref) on one 24x24 window of the block (576 tokens,
+    full width): a bounded sample, reported in tokens/s."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_bind import Ref, have_ref
+    from test_gpu_blockops import reference_eval
+    if not have_ref():
+        return None
+    threads = threads or max(1, min(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1),
+                                    os.cpu_count() or 1))
+    G, _ = vit_block_graph(24, 24, 1024, 16, 4096, False, "f32")
+    R = Ref()
+    t0 = time.perf_counter()
+    rc = reference_eval(R, G.g, R.pool(threads))
+    dt = time.perf_counter() - t0
+    R.close()
+    if rc != 0:
+        return None
+    return {"value": round(576 / dt, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"one 24x24 window (576 tokens) of a windowed ViT-L block, f32 weights, "
+                      f"{dt:.2f} s, cpu_dispatch_node over the same node sequence with a "
+                      f"{threads}-thread pool"}
+
+
 def measured_traffic(key):
     """HBM bytes per launch of the headline kernel, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
@@ -280,8 +370,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
-    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5",
-                    help="comma list of extra sections to run (cfg1..cfg5)")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block",
+                    help="comma list of extra sections to run (cfg1..cfg5, block)")
     args = ap.parse_args()
     only = set(args.only.split(","))
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -438,6 +528,19 @@ def main():
             extra["cfg5_sdpa_fused"]["cpu_reference"] = {
                 "windowed": cpu_sdpa(1296, 576, D), "global": cpu_sdpa(16, 5184, D)}
         log("  ", extra["cfg5_sdpa_fused"])
+
+    if not args.quick and "block" in only:
+        log("ViT-L block through graph_eval (windowed / global; f32 / Q8_0 weights)")
+        blk = {}
+        for name, glob in (("windowed", False), ("global", True)):
+            for wk in ("f32", "q8"):
+                blk[f"{name}_{wk}"] = vit_block_bench(glob, wk)
+                log("  ", name, wk, blk[f"{name}_{wk}"])
+        if not args.no_cpu_baseline:
+            blk["cpu_reference"] = vit_block_cpu()
+        blk["note"] = ("5184 tokens, e 1024, 16 heads, MLP 4096, f32 activations; every node "
+                       "on the GPU; block input in HBM, no readback; wall time of graph_eval")
+        extra["vit_block"] = blk
 
     cpu = None
     if not args.no_cpu_baseline:

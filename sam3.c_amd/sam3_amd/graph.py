@@ -29,7 +29,9 @@ class Graph:
     def tensor(self, dtype, dims, arr=None, ephemeral=0):
         """A tensor header over a host buffer (zeros when arr is None)."""
         if arr is None:
-            arr = np.zeros(int(np.prod(dims)), _NP[dtype])
+            n = int(np.prod(dims))
+            arr = (np.zeros(abi.q8_nbytes(n), np.uint8) if dtype == abi.Q8_0
+                   else np.zeros(n, _NP[dtype]))
         arr = np.ascontiguousarray(arr)
         self.keep.append(arr)
         t = abi.make_tensor(dtype, list(dims), arr.ctypes.data, arr.nbytes)
