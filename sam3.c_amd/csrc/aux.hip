@@ -244,6 +244,50 @@ extern "C" int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream
 	return (int)hipGetLastError();
 }
 
+/* f32 rows [rows, K] (row pitch ld elements) -> bf16 rows [rows, 3K] of
+ * hi = bf16(x) and lo = bf16(x - hi) in the order [hi, lo, hi] (order 0)
+ * or [hi, hi, lo] (order 1): a bf16 GEMM of one against the other over
+ * 3K sums hi*hi + lo*hi + hi*lo. One thread per 8 values of a row. */
+__global__ void __launch_bounds__(256) split3_bf16_k(const float *src, uint16_t *dst, int rows,
+						     int K, long long ld, int order)
+{
+	const int per_row = K / 8;
+	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+	if (t >= (long long)rows * per_row)
+		return;
+	const long long r = t / per_row;
+	const int k0 = (int)(t % per_row) * 8;
+	const float4 a = *(const float4 *)(src + r * ld + k0);
+	const float4 b = *(const float4 *)(src + r * ld + k0 + 4);
+	const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+	uint32_t hi[4], lo[4];
+#pragma unroll
+	for (int i = 0; i < 4; ++i) {
+		hi[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+		lo[i] = pack_bf16x2(x[2 * i] - __uint_as_float(hi[i] << 16),
+				    x[2 * i + 1] - __uint_as_float(hi[i] & 0xFFFF0000u));
+	}
+	const uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+	const uint4 L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+	uint16_t *d = dst + r * 3LL * K + k0;
+	*(uint4 *)d = H;
+	*(uint4 *)(d + K) = order == 0 ? L : H;
+	*(uint4 *)(d + 2LL * K) = order == 0 ? H : L;
+}
+
+extern "C" int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld,
+			       int order, void *stream)
+{
+	if (rows < 0 || K <= 0 || K % 8 || ld < K || ld % 4 || (((uintptr_t)src | (uintptr_t)dst) & 15u))
+		return (int)hipErrorInvalidValue;
+	const long long n = (long long)rows * (K / 8);
+	if (n == 0)
+		return 0;
+	hipLaunchKernelGGL(split3_bf16_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+			   (hipStream_t)stream, src, (uint16_t *)dst, rows, K, ld, order);
+	return (int)hipGetLastError();
+}
+
 extern "C" int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream)
 {
 	if (n <= 0)

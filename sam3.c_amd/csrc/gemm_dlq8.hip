@@ -273,10 +273,14 @@ extern "C" int s3k_dlq8_eligible(const struct s3k_gemm *g)
 		return 0;
 	if (g->a_kind != S3K_F16 && (g->lda != g->K || ((uintptr_t)g->a & 15u)))
 		return 0;
-	/* f32 activations: the register-staged kernel, which converts them in
-	 * its loader, measured faster than a cast pass plus this kernel
-	 * (5184x1024x1024: 39.5 us against 46 us) */
-	if (g->a_kind != S3K_F16 && g->a_kind != S3K_BF16)
+	/* f32 activations too: one cast pass plus this kernel measured faster
+	 * than the register-staged kernel converting in its loader on the
+	 * ViT-L shapes (5184 x {3072, 1024, 4096} x {1024, 4096}: 67 / 37 /
+	 * 90 / 95 us against 102 / 39 / 143 / 120 us). SAM3_HIP_Q8_F32CAST=0
+	 * keeps f32 activations on the register-staged kernel. */
+	const char *env = getenv("SAM3_HIP_Q8_F32CAST");
+	const bool f32_cast = !env || atoi(env) != 0;
+	if (g->a_kind != S3K_F16 && g->a_kind != S3K_BF16 && !(g->a_kind == S3K_F32 && f32_cast))
 		return 0;
 	struct s3k_gemm h = *g;
 	h.a_kind = S3K_F16;

@@ -103,6 +103,10 @@ int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, vo
 	     int batch, int seq, int heads, int hd, void *stream);
 int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
 		const int *axes, void *stream);
+/* f32 rows [rows, K] (pitch ld) -> bf16 [rows, 3K]: [hi, lo, hi] for
+ * order 0, [hi, hi, lo] for order 1 (hi = bf16(x), lo = bf16(x - hi)). */
+int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld, int order,
+		    void *stream);
 /* Whether the MFMA path of g (B Q8_0 [N,K]) runs the direct-to-LDS Q8
  * GEMM: f16 A directly, bf16 A after a cast to f16. */
 int s3k_dlq8_eligible(const struct s3k_gemm *g);

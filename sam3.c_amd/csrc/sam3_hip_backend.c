@@ -111,8 +111,7 @@ static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_te
 	memset(e, 0, sizeof(*e));
 	e->host = t->data;
 	e->nbytes = nbytes;
-	enum sam3_error err = s3h_hip(hipMallocAsync(&e->dev, nbytes ? nbytes : 1, hb->stream),
-				      "graph_eval: device shadow");
+	enum sam3_error err = s3h_scratch_alloc(&e->dev, nbytes, hb->stream);
 	if (err != SAM3_OK)
 		return err;
 	e->host_valid = 1;

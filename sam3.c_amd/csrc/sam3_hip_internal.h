@@ -22,6 +22,10 @@ enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
 int s3h_transpose_is_swap(const struct sam3_node *node);
+/* Stream-ordered device scratch from the default pool, kept mapped
+ * between calls. */
+enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream);
+
 /* ViT block ops on device pointers; the _ok forms say whether the node
  * runs on the GPU (dtypes and shapes), without reporting an error. */
 int s3h_transpose_ok(const struct sam3_node *node);

@@ -50,6 +50,30 @@ enum sam3_error s3h_hip(int e, const char *what)
 	return e == hipErrorOutOfMemory ? SAM3_ENOMEM : SAM3_EBACKEND;
 }
 
+/* Stream-ordered scratch. The device's default memory pool returns
+ * freed blocks to the system at every synchronization unless its release
+ * threshold is raised; scratch of the same size is then mapped again on
+ * the next call. The threshold is raised once per device (a repeated
+ * store from two threads is harmless). */
+#define S3H_MAX_DEVICES 64
+static int s3h_pool_ready[S3H_MAX_DEVICES];
+
+enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
+{
+	int dev = 0;
+	if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < S3H_MAX_DEVICES &&
+	    !s3h_pool_ready[dev]) {
+		hipMemPool_t pool;
+		if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+			uint64_t keep = UINT64_MAX;
+			(void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+		}
+		(void)hipGetLastError();
+		s3h_pool_ready[dev] = 1;
+	}
+	return s3h_hip(hipMallocAsync(p, nbytes ? nbytes : 1, (hipStream_t)stream), "scratch");
+}
+
 /* ------------------------------------------------------------------ */
 /* dtype helpers                                                        */
 /* ------------------------------------------------------------------ */
@@ -143,7 +167,7 @@ static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 	void *w16 = NULL;
 	enum sam3_error err;
 
-	err = s3h_hip(hipMallocAsync(&w16, bytes, (hipStream_t)stream), "matmul_q8 scratch");
+	err = s3h_scratch_alloc(&w16, bytes, stream);
 	if (err != SAM3_OK)
 		return err;
 	int e = nt ? s3k_q8_nk_to_f16_nk(g->b, w16, g->K, g->N, stream)
@@ -174,8 +198,7 @@ static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 {
 	const size_t bytes = (size_t)g->M * g->K * 2;
 	void *a16 = NULL;
-	enum sam3_error err = s3h_hip(hipMallocAsync(&a16, bytes, (hipStream_t)stream),
-				      "matmul_q8 activation scratch");
+	enum sam3_error err = s3h_scratch_alloc(&a16, bytes, stream);
 	if (err != SAM3_OK)
 		return err;
 	err = s3h_hip(s3k_cast_f16(g->a_kind, g->a, a16, (long long)g->M * g->K, stream),
@@ -195,6 +218,58 @@ static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 static int q8_dl_wants_cast(const struct s3k_gemm *g)
 {
 	return g->b_kind == S3K_Q8 && g->a_kind != S3K_F16 && s3k_dlq8_eligible(g);
+}
+
+/* f32 x f32 with W [N,K] on the bf16 MFMA GEMM: A and W are split once
+ * into bf16 hi/lo planes laid out along a tripled k, A' = [Ah | Al | Ah]
+ * and W' = [Wh | Wh | Wl], so that one bf16 GEMM over 3K accumulates
+ * Ah*Wh + Al*Wh + Ah*Wl in f32; the dropped Al*Wl term is below 2^-16 of
+ * each product. */
+static int f32_split_wanted(const struct s3k_gemm *g)
+{
+	const char *env = getenv("SAM3_HIP_F32_SPLIT");
+	if (env && atoi(env) == 0)
+		return 0;
+	return g->a_kind == S3K_F32 && g->b_kind == S3K_F32 && g->c_kind == S3K_F32 &&
+	       (g->flags & S3K_B_NT) && g->batch == 1 && g->K % 8 == 0 && g->lda % 4 == 0 &&
+	       g->ldb % 4 == 0 && !(((uintptr_t)g->a | (uintptr_t)g->b) & 15u) &&
+	       (long long)g->M * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
+	       (long long)g->N * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
+	       (long long)g->M * g->N * g->K >= (1LL << 24);
+}
+
+static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, void *stream)
+{
+	const hipStream_t st = (hipStream_t)stream;
+	const size_t abytes = (size_t)g->M * 3 * g->K * 2, bbytes = (size_t)g->N * 3 * g->K * 2;
+	void *a3 = NULL, *b3 = NULL;
+	enum sam3_error err = s3h_scratch_alloc(&a3, abytes, stream);
+	if (err == SAM3_OK)
+		err = s3h_scratch_alloc(&b3, bbytes, stream);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_split3_bf16((const float *)g->a, a3, g->M, g->K, g->lda, 0, stream),
+			      "matmul f32 split A");
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_split3_bf16((const float *)g->b, b3, g->N, g->K, g->ldb, 1, stream),
+			      "matmul f32 split W");
+	if (err == SAM3_OK) {
+		struct s3k_gemm h = *g;
+		h.a = a3;
+		h.b = b3;
+		h.a_kind = h.b_kind = S3K_BF16;
+		h.K = 3 * g->K;
+		h.lda = h.ldb = 3 * g->K;
+		err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream), "matmul f32 split gemm");
+	}
+	enum sam3_error ferr = SAM3_OK;
+	if (b3)
+		ferr = s3h_hip(hipFreeAsync(b3, st), "matmul f32 split scratch free");
+	if (a3) {
+		enum sam3_error e2 = s3h_hip(hipFreeAsync(a3, st), "matmul f32 split scratch free");
+		if (ferr == SAM3_OK)
+			ferr = e2;
+	}
+	return err != SAM3_OK ? err : ferr;
 }
 
 static int q8_needs_unpack(const struct s3k_gemm *g)
@@ -233,6 +308,8 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	if (path == 0) {
 		if (q8_needs_unpack(&g))
 			return q8_unpacked(&g, stream);
+		if (f32_split_wanted(&g))
+			return f32_split_gemm(&g, stream);
 		if (s3k_gemm_path(&g) == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 			return q8_dl_cast(&g, stream);
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
@@ -243,6 +320,8 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	}
 	if (path == S3K_PATH_MFMA && q8_needs_unpack(&g))
 		return q8_unpacked(&g, stream);
+	if (path == S3K_PATH_MFMA && f32_split_wanted(&g))
+		return f32_split_gemm(&g, stream);
 	if (path == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 		return q8_dl_cast(&g, stream);
 	int e = s3k_gemm_launch_path(&g, path, stream);

@@ -218,7 +218,9 @@ def test_f16_tiled_vs_oracle(M, N, K, nt):
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (100, 72, 36), (257, 130, 512)])
 @pytest.mark.parametrize("nt", [False, True])
-def test_f32_tiled_vs_oracle(M, N, K, nt):
+def test_f32_tiled_vs_oracle(M, N, K, nt, monkeypatch):
+    """The f32 MFMA kernel (v_mfma_f32_32x32x2_f32, exact f32 products)."""
+    monkeypatch.setenv("SAM3_HIP_F32_SPLIT", "0")
     a = rnd(50 + M, (M, K))
     b = rnd(60 + N, (N, K) if nt else (K, N))
     if hip.matmul_path(abi.F32, abi.F32, abi.F32, M, N, K, hip.B_NT if nt else 0) != MFMA:
@@ -227,6 +229,23 @@ def test_f32_tiled_vs_oracle(M, N, K, nt):
                    path=MFMA)
     assert_f32_close(c, ref_linear("f32", a, b, b_nt=nt), rtol=1e-5, floor=1e-5,
                      what=f"f32 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(257, 130, 512), (5184, 1024, 1024), (1000, 3072, 1024),
+                                   (300, 4096, 4096)])
+@pytest.mark.parametrize("epi", [0, 1])
+def test_f32_split_gemm(M, N, K, epi):
+    """f32 x f32 with W [N,K] on the bf16 MFMA GEMM over a tripled k
+    (A' = [Ah|Al|Ah], W' = [Wh|Wh|Wl]): within the f32 bound, and within
+    2e-5 normwise of the reference (each product keeps ~16 bits)."""
+    a, w = rnd(80 + M, (M, K)), rnd(81 + N, (N, K), 0.05)
+    bias = rnd(82, N, 0.3) if epi else None
+    flags = hip.B_NT | ((hip.BIAS | hip.GELU) if epi else 0)
+    c = hip.matmul(a, abi.F32, w, abi.F32, abi.F32, M, N, K, bias=bias, flags=flags, path=MFMA)
+    ref = ref_linear("f32", a, w, bias=bias, gelu=bool(epi), b_nt=True)
+    assert_f32_close(c, ref, what=f"f32 split {M}x{N}x{K}")
+    err = np.abs(c.astype(np.float64) - ref).max() / np.abs(ref).max()
+    assert err <= 2e-5, err
 
 
 @pytest.mark.parametrize("kind", ["bf16", "f16", "f32"])
