@@ -372,6 +372,8 @@ def main():
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
     ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block",
                     help="comma list of extra sections to run (cfg1..cfg5, block)")
+    ap.add_argument("--block", default="windowed_f32,windowed_q8,global_f32,global_q8",
+                    help="block section: comma list of {windowed,global}_{f32,q8}")
     args = ap.parse_args()
     only = set(args.only.split(","))
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -532,8 +534,11 @@ def main():
     if not args.quick and "block" in only:
         log("ViT-L block through graph_eval (windowed / global; f32 / Q8_0 weights)")
         blk = {}
+        want = set(args.block.split(","))
         for name, glob in (("windowed", False), ("global", True)):
             for wk in ("f32", "q8"):
+                if f"{name}_{wk}" not in want:
+                    continue
                 blk[f"{name}_{wk}"] = vit_block_bench(glob, wk)
                 log("  ", name, wk, blk[f"{name}_{wk}"])
         if not args.no_cpu_baseline:
