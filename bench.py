@@ -39,6 +39,7 @@ from sam3_amd import abi, hip, synth  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_PCIE_GBS = 64.0        # host link, PCIe 5.0 x16, one direction
 
 
 def log(*a):
@@ -256,6 +257,78 @@ def vit_block_cpu(threads=None):
                       f"{threads}-thread pool"}
 
 
+def weights_upload_bench(layers=32, e=1024, mlp=4096):
+    """A .sam3 checkpoint of `layers` ViT-L layers (Q8_0 linear weights as
+    in config 3, f32 norms and biases; q/k/v stored separately) written to
+    a temporary file, mmap'd, and its data blob copied to HBM by
+    sam3_hip_backend_map_weights. Beside it: the per-tensor pageable
+    copies graph_eval makes for weights that are not mapped (one hipMemcpy
+    per tensor into a preallocated buffer, so no allocation is timed), and
+    the QKV stacking of every layer (fuse_rows, in HBM)."""
+    import tempfile
+    from sam3_amd import graph
+    from sam3_amd import weights as W
+    one = graph.vit_layer_entries(0, e, mlp, 700, hip.q8_quantize)
+    ents = []
+    for i in range(layers):
+        for name, dt, dims, arr in one:
+            ents.append((name.replace("layers.0.", f"layers.{i}."), dt, dims, arr))
+    fd, path = tempfile.mkstemp(suffix=".sam3")
+    os.close(fd)
+    lib = hip.load()
+    try:
+        W.write(path, ents)
+        wf = W.WeightFile(path)
+        nbytes = wf.data_size
+        be = hip.Backend(0)
+        t0 = time.perf_counter()
+        hip.check(be.map_weights(wf.data_base, nbytes), "map_weights")
+        t_first = time.perf_counter() - t0
+        be.cache_invalidate(wf.data_base, nbytes)
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            hip.check(be.map_weights(wf.data_base, nbytes), "map_weights")
+            ts.append(time.perf_counter() - t0)
+            if len(ts) < 3:
+                be.cache_invalidate(wf.data_base, nbytes)
+        t_map = min(ts)
+        t0 = time.perf_counter()
+        fused = 0
+        for i in range(layers):
+            G = graph.Graph()
+            graph.load_vit_layer(G, wf, i, be)
+            fused += 2
+        t_fuse = time.perf_counter() - t0
+        be.close()
+        dev = hip.DeviceBuffer(nbytes)
+        hip.synchronize()
+        t0 = time.perf_counter()
+        for i in range(wf.n_tensors):
+            d = wf.descs[i]
+            off = int(d["data_offset"])
+            hip.check(lib.sam3_hip_memcpy_h2d(dev.ptr + off, wf.data_base + off,
+                                              int(d["data_size"])), "memcpy_h2d")
+        hip.synchronize()
+        t_tensor = time.perf_counter() - t0
+        dev.free()
+        n_t = wf.n_tensors
+        wf.close()
+    finally:
+        os.remove(path)
+    gbs = nbytes / t_map / 1e9
+    return {"bytes": nbytes, "tensors": n_t, "layers": layers,
+            "map_weights_ms": round(t_map * 1e3, 2), "map_weights_gbs": round(gbs, 2),
+            "first_map_ms": round(t_first * 1e3, 2),
+            "per_tensor_pageable_ms": round(t_tensor * 1e3, 2),
+            "per_tensor_pageable_gbs": round(nbytes / t_tensor / 1e9, 2),
+            "fuse_qkv_ms_per_layer": round(t_fuse * 1e3 / layers, 3),
+            "roofline": {"bound": "pcie", "achieved": round(gbs, 2), "peak": PEAK_PCIE_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_PCIE_GBS, 4)},
+            "note": "file in the page cache; first_map includes the pinned staging "
+                    "allocation and the first touch of the mapping"}
+
+
 def measured_traffic(key):
     """HBM bytes per launch of the headline kernel, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
@@ -370,8 +443,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
-    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block",
-                    help="comma list of extra sections to run (cfg1..cfg5, block)")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,weights",
+                    help="comma list of extra sections to run (cfg1..cfg5, block, weights)")
     ap.add_argument("--block", default="windowed_f32,windowed_q8,global_f32,global_q8",
                     help="block section: comma list of {windowed,global}_{f32,q8}")
     args = ap.parse_args()
@@ -546,6 +619,11 @@ def main():
         blk["note"] = ("5184 tokens, e 1024, 16 heads, MLP 4096, f32 activations; every node "
                        "on the GPU; block input in HBM, no readback; wall time of graph_eval")
         extra["vit_block"] = blk
+
+    if not args.quick and "weights" in only:
+        log("weights: .sam3 blob (32 ViT-L layers, Q8_0 linear weights) to HBM")
+        extra["weights_upload"] = weights_upload_bench()
+        log("  ", extra["weights_upload"])
 
     cpu = None
     if not args.no_cpu_baseline:

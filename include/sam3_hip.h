@@ -72,9 +72,59 @@ struct sam3_hip_eval_stats {
 	int uploads;       /* host -> device copies                            */
 	int cache_hits;    /* inputs found resident from an earlier eval       */
 	int downloads;     /* device -> host copies                            */
+	int mapped_reads;  /* inputs read from a range mapped by map_weights   */
 };
 void sam3_hip_backend_last_stats(struct sam3_backend *be,
 				 struct sam3_hip_eval_stats *out);
+
+/* ------------------------------------------------------------------ */
+/* Weights in HBM                                                       */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Copy a host range of weights into HBM once: in sam3.c, the data blob
+ * of an open weight file, wf->data_base for wf->mapped_size minus the
+ * blob's file offset (src/core/weight.c:303-474, format
+ * docs/weight-format.md:68-98). Tensors made by sam3_weight_to_tensor
+ * (weight.c:534-558) point into that blob, and graph_eval then reads each
+ * input whose bytes lie inside a mapped range from the HBM copy at the
+ * same offset, with no per-tensor upload (the per-tensor shadows that
+ * replace the reference's direct reads of the mmap,
+ * graph_helpers.c:122-145). The 64-byte tensor alignment of the file
+ * carries over to HBM.
+ *
+ * The copy runs through pinned staging buffers on several host threads
+ * and DMA queues; the call returns when the data is in HBM. The range
+ * stays mapped until cache_invalidate touches any byte of it
+ * (backend.h:50-55) or the backend is destroyed; arena_reset leaves it.
+ * A range that overlaps a mapped one, or device memory, is SAM3_EINVAL.
+ * No reference counterpart: the CPU backend reads the mmap directly.
+ */
+enum sam3_error sam3_hip_backend_map_weights(struct sam3_backend *be, const void *host,
+					     size_t nbytes);
+
+/* HBM address of host byte `host` inside a mapped range, else NULL. */
+void *sam3_hip_backend_weight_ptr(struct sam3_backend *be, const void *host);
+
+/*
+ * Stack n_parts tensors of one dtype along dim 0 into a new tensor in HBM
+ * ([d_i, cols] -> [sum d_i, cols], or 1-D [d_i] -> [sum d_i]): the QKV
+ * weight and bias fusion of image_encoder.c:223-254 (fuse_3), also
+ * decoder.c:93-140 and mask_decoder.c:47. fuse_3 declares its output F32
+ * whatever the parts hold, so Q8_0 parts come out as F32-labelled block
+ * bytes. Here the output keeps the parts' dtype: Q8_0 parts, each a whole
+ * number of 32-element blocks, give the Q8_0 tensor of the stacked rows.
+ *
+ * Parts may be host memory, device memory or inside a mapped range (then
+ * the copy stays in HBM). *out is filled: dtype, dims, strides (zero for
+ * Q8_0, as weight.c:551-555), nbytes, and data = a device buffer the
+ * backend owns until it is destroyed. Errors: NULL, rank other than 1-2,
+ * column mismatch, or a Q8_0 part whose element count is not a multiple
+ * of 32 -> SAM3_EINVAL; mixed dtypes -> SAM3_EDTYPE.
+ */
+enum sam3_error sam3_hip_backend_fuse_rows(struct sam3_backend *be,
+					   const struct sam3_tensor *const *parts, int n_parts,
+					   struct sam3_tensor *out);
 
 /* ------------------------------------------------------------------ */
 /* Node-level kernels. Same contract as the reference CPU kernels       */

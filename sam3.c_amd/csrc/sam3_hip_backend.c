@@ -30,6 +30,14 @@
  * Tensors whose data already is device memory are used in place.
  * alloc_tensor hands out pinned host memory (hipHostMalloc), so the
  * copies above run at full PCIe/xGMI rate and asynchronously.
+ *
+ * Mapped weights. sam3_hip_backend_map_weights copies a whole host range
+ * (the data blob of an mmap'd .sam3 file, weight.c:303-474, whose tensors
+ * sit at 64-byte aligned offsets) into one HBM allocation in a single
+ * staged transfer. Any tensor whose data lies inside a mapped range is
+ * then read from that copy at the same offset: no residency entry, no
+ * per-tensor upload. Tensors built on the device (sam3_hip_backend_fuse_rows)
+ * are owned by the backend until it is destroyed.
  */
 #include "sam3_hip.h"
 #include "sam3_hip_internal.h"
@@ -53,12 +61,24 @@ struct s3h_res {
 	unsigned char produced;  /* written by a GPU node in this eval        */
 };
 
+/* A host range copied to HBM once: [host, host + nbytes) -> dev. */
+struct s3h_blob {
+	const char *host;
+	size_t nbytes;
+	char *dev;
+};
+
 struct sam3_hip_backend {
 	struct sam3_backend base; /* must be first (backend.h:59-62) */
 	int device;
 	hipStream_t stream;
 	struct s3h_res *res;
 	int n_res, cap_res;
+	struct s3h_blob *blobs;
+	int n_blobs, cap_blobs;
+	void **owned; /* device buffers made by fuse_rows */
+	int n_owned, cap_owned;
+	struct s3h_stager stager;
 	char *arena;
 	size_t arena_size, arena_off;
 	sam3_hip_host_dispatch_fn host_fn;
@@ -121,6 +141,26 @@ static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_te
 	return SAM3_OK;
 }
 
+/* Device address of [p, p + nbytes) when it lies inside a mapped range. */
+static void *blob_addr(const struct sam3_hip_backend *hb, const void *p, size_t nbytes)
+{
+	const char *c = (const char *)p;
+	for (int i = 0; i < hb->n_blobs; i++) {
+		const struct s3h_blob *b = &hb->blobs[i];
+		if (c >= b->host && c < b->host + b->nbytes && nbytes <= b->nbytes - (size_t)(c - b->host))
+			return b->dev + (c - b->host);
+	}
+	return NULL;
+}
+
+static void blob_drop_at(struct sam3_hip_backend *hb, int i)
+{
+	(void)hipStreamSynchronize(hb->stream);
+	(void)hipFree(hb->blobs[i].dev);
+	hb->blobs[i] = hb->blobs[hb->n_blobs - 1];
+	hb->n_blobs--;
+}
+
 static int is_device_ptr(const void *p)
 {
 	hipPointerAttribute_t attr;
@@ -141,11 +181,17 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		s3h_error("graph_eval: input tensor without data");
 		return SAM3_EINVAL;
 	}
+	size_t nbytes = s3h_tensor_bytes(t);
+	void *mapped = hb->n_blobs ? blob_addr(hb, t->data, nbytes) : NULL;
+	if (mapped) {
+		*out = mapped;
+		hb->stats.mapped_reads++;
+		return SAM3_OK;
+	}
 	if (is_device_ptr(t->data)) {
 		*out = t->data;
 		return SAM3_OK;
 	}
-	size_t nbytes = s3h_tensor_bytes(t);
 	struct s3h_res *e = res_find(hb, t->data);
 	if (e && e->nbytes < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
@@ -615,6 +661,19 @@ static void hip_free(struct sam3_backend *be)
 	free(hb->res);
 	hb->res = NULL;
 	hb->cap_res = 0;
+	while (hb->n_blobs)
+		blob_drop_at(hb, hb->n_blobs - 1);
+	free(hb->blobs);
+	hb->blobs = NULL;
+	hb->cap_blobs = 0;
+	if (hb->stream)
+		(void)hipStreamSynchronize(hb->stream);
+	for (int i = 0; i < hb->n_owned; i++)
+		(void)hipFree(hb->owned[i]);
+	free(hb->owned);
+	hb->owned = NULL;
+	hb->n_owned = hb->cap_owned = 0;
+	s3h_stager_free(&hb->stager);
 	if (hb->stream) {
 		(void)hipStreamSynchronize(hb->stream);
 		(void)hipStreamDestroy(hb->stream);
@@ -687,7 +746,11 @@ static void hip_arena_reset(struct sam3_backend *be)
 static void hip_cache_invalidate(struct sam3_backend *be, const void *start, size_t len)
 {
 	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
-	res_drop_range(hb, (const char *)start, (const char *)start + len);
+	const char *lo = (const char *)start, *hi = lo + len;
+	res_drop_range(hb, lo, hi);
+	for (int i = hb->n_blobs - 1; i >= 0; i--)
+		if (hb->blobs[i].host < hi && hb->blobs[i].host + hb->blobs[i].nbytes > lo)
+			blob_drop_at(hb, i);
 }
 
 static const struct sam3_backend_ops hip_ops = {
@@ -753,4 +816,178 @@ void sam3_hip_backend_last_stats(struct sam3_backend *be, struct sam3_hip_eval_s
 	if (!be || !out)
 		return;
 	*out = ((struct sam3_hip_backend *)be)->stats;
+}
+
+/* ------------------------------------------------------------------ */
+/* Weights in HBM                                                       */
+/* ------------------------------------------------------------------ */
+enum sam3_error sam3_hip_backend_map_weights(struct sam3_backend *be, const void *host,
+					     size_t nbytes)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (!hb || !host || !nbytes) {
+		s3h_error("map_weights: NULL backend or empty range");
+		return SAM3_EINVAL;
+	}
+	const char *lo = (const char *)host, *hi = lo + nbytes;
+	for (int i = 0; i < hb->n_blobs; i++)
+		if (hb->blobs[i].host < hi && hb->blobs[i].host + hb->blobs[i].nbytes > lo) {
+			s3h_error("map_weights: range overlaps a mapped range");
+			return SAM3_EINVAL;
+		}
+	if (is_device_ptr(host)) {
+		s3h_error("map_weights: range is device memory");
+		return SAM3_EINVAL;
+	}
+	enum sam3_error err = s3h_hip(hipSetDevice(hb->device), "map_weights: set device");
+	if (err == SAM3_OK)
+		err = s3h_stager_init(&hb->stager, hb->device);
+	if (err != SAM3_OK)
+		return err;
+	if (hb->n_blobs == hb->cap_blobs) {
+		int cap = hb->cap_blobs ? hb->cap_blobs * 2 : 4;
+		struct s3h_blob *b = realloc(hb->blobs, (size_t)cap * sizeof(*b));
+		if (!b) {
+			s3h_error("map_weights: out of host memory");
+			return SAM3_ENOMEM;
+		}
+		hb->blobs = b;
+		hb->cap_blobs = cap;
+	}
+	char *dev = NULL;
+	err = s3h_hip(hipMalloc((void **)&dev, nbytes), "map_weights: device copy");
+	if (err != SAM3_OK)
+		return err;
+	/* Residency shadows of tensors inside the range become redundant. */
+	res_drop_range(hb, lo, hi);
+	err = s3h_hip(hipStreamSynchronize(hb->stream), "map_weights: sync");
+	if (err == SAM3_OK)
+		err = s3h_stager_copy(&hb->stager, dev, host, nbytes);
+	if (err != SAM3_OK) {
+		(void)hipFree(dev);
+		return err;
+	}
+	hb->blobs[hb->n_blobs++] = (struct s3h_blob){lo, nbytes, dev};
+	return SAM3_OK;
+}
+
+void *sam3_hip_backend_weight_ptr(struct sam3_backend *be, const void *host)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	return hb && host ? blob_addr(hb, host, 1) : NULL;
+}
+
+static enum sam3_error own(struct sam3_hip_backend *hb, void *p)
+{
+	if (hb->n_owned == hb->cap_owned) {
+		int cap = hb->cap_owned ? hb->cap_owned * 2 : 16;
+		void **o = realloc(hb->owned, (size_t)cap * sizeof(*o));
+		if (!o) {
+			s3h_error("fuse_rows: out of host memory");
+			return SAM3_ENOMEM;
+		}
+		hb->owned = o;
+		hb->cap_owned = cap;
+	}
+	hb->owned[hb->n_owned++] = p;
+	return SAM3_OK;
+}
+
+/* Stack parts [d_i, cols] (or [d_i]) of one dtype into one [sum d_i, cols]
+ * tensor in HBM. The replacement of image_encoder.c:223-254 (fuse_3),
+ * which declares its output F32 whatever the parts are, so Q8_0 parts
+ * come out as F32-labelled block bytes. Here the output keeps the parts'
+ * dtype. Q8_0 blocks run along the flat index, so a part whose element
+ * count is a multiple of 32 is a whole number of blocks and the fused
+ * tensor is the byte concatenation; other counts would put one block
+ * across two parts and are rejected. */
+enum sam3_error sam3_hip_backend_fuse_rows(struct sam3_backend *be,
+					   const struct sam3_tensor *const *parts, int n_parts,
+					   struct sam3_tensor *out)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	if (!hb || !parts || !out || n_parts < 1 || n_parts > SAM3_NODE_MAX_INPUTS) {
+		s3h_error("fuse_rows: NULL argument or part count outside [1, %d]",
+			  SAM3_NODE_MAX_INPUTS);
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *p0 = parts[0];
+	if (!p0 || !p0->data || p0->n_dims < 1 || p0->n_dims > 2) {
+		s3h_error("fuse_rows: part 0 must be a 1-D or 2-D tensor with data");
+		return SAM3_EINVAL;
+	}
+	const int dt = p0->dtype, nd = p0->n_dims;
+	if (dt != SAM3_DTYPE_Q8_0 && s3h_dtype_size(dt) == 0) {
+		s3h_error("fuse_rows: dtype %d has no layout", dt);
+		return SAM3_EDTYPE;
+	}
+	long long rows = 0;
+	size_t total = 0;
+	for (int i = 0; i < n_parts; i++) {
+		const struct sam3_tensor *t = parts[i];
+		if (!t || !t->data || t->n_dims != nd || (nd == 2 && t->dims[1] != p0->dims[1]) ||
+		    t->dims[0] <= 0 || (nd == 2 && t->dims[1] <= 0)) {
+			s3h_error("fuse_rows: part %d does not match part 0's rank and columns", i);
+			return SAM3_EINVAL;
+		}
+		if ((int)t->dtype != dt) {
+			s3h_error("fuse_rows: part %d has dtype %d, part 0 has %d", i, t->dtype, dt);
+			return SAM3_EDTYPE;
+		}
+		if (dt == SAM3_DTYPE_Q8_0 && s3h_nelems(t) % 32 != 0) {
+			s3h_error("fuse_rows: Q8_0 part %d has %lld elements, not a whole number "
+				  "of 32-element blocks", i, s3h_nelems(t));
+			return SAM3_EINVAL;
+		}
+		rows += t->dims[0];
+		total += s3h_tensor_bytes(t);
+	}
+	if (rows > INT32_MAX) {
+		s3h_error("fuse_rows: %lld rows", rows);
+		return SAM3_EINVAL;
+	}
+	enum sam3_error err = s3h_hip(hipSetDevice(hb->device), "fuse_rows: set device");
+	char *dev = NULL;
+	if (err == SAM3_OK)
+		err = s3h_hip(hipMalloc((void **)&dev, total), "fuse_rows: device buffer");
+	if (err != SAM3_OK)
+		return err;
+	size_t off = 0;
+	for (int i = 0; i < n_parts && err == SAM3_OK; i++) {
+		const struct sam3_tensor *t = parts[i];
+		const size_t nb = s3h_tensor_bytes(t);
+		const void *src = blob_addr(hb, t->data, nb);
+		hipMemcpyKind kind = hipMemcpyDeviceToDevice;
+		if (!src) {
+			src = t->data;
+			kind = is_device_ptr(src) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+		}
+		err = s3h_hip(hipMemcpyAsync(dev + off, src, nb, kind, hb->stream), "fuse_rows: copy");
+		off += nb;
+	}
+	if (err == SAM3_OK)
+		err = s3h_hip(hipStreamSynchronize(hb->stream), "fuse_rows: sync");
+	if (err == SAM3_OK)
+		err = own(hb, dev);
+	if (err != SAM3_OK) {
+		(void)hipStreamSynchronize(hb->stream);
+		(void)hipFree(dev);
+		return err;
+	}
+	memset(out, 0, sizeof(*out));
+	out->dtype = (enum sam3_dtype)dt;
+	out->n_dims = nd;
+	out->dims[0] = (int)rows;
+	if (nd == 2)
+		out->dims[1] = p0->dims[1];
+	if (dt != SAM3_DTYPE_Q8_0) {
+		int st = 1;
+		for (int d = nd - 1; d >= 0; d--) {
+			out->strides[d] = st;
+			st *= out->dims[d];
+		}
+	}
+	out->data = dev;
+	out->nbytes = total;
+	return SAM3_OK;
 }

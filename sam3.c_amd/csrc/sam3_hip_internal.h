@@ -39,4 +39,27 @@ enum sam3_error s3h_reshape(const struct sam3_node *node);
 /* Whether sam3_hip_kernel_sdpa takes this node (dtypes, ranks, head_dim). */
 int s3h_sdpa_node_ok(const struct sam3_node *node);
 
+/* Bulk host -> device copies through pinned staging buffers (upload.c).
+ * Lanes and chunk size default to S3H_STAGE_LANES x S3H_STAGE_CHUNK_MB;
+ * SAM3_HIP_UPLOAD_LANES / SAM3_HIP_UPLOAD_CHUNK_MB override them. */
+#define S3H_STAGE_MAX_LANES 16
+#define S3H_STAGE_LANES 8
+#define S3H_STAGE_CHUNK_MB 4
+struct s3h_stage_lane {
+	void *stream;   /* hipStream_t */
+	char *buf[2];   /* pinned, chunk bytes each */
+	void *done[2];  /* hipEvent_t: the DMA out of buf[i] has finished */
+};
+struct s3h_stager {
+	int device;
+	int lanes;      /* 0 = not initialised */
+	size_t chunk;
+	struct s3h_stage_lane lane[S3H_STAGE_MAX_LANES];
+};
+enum sam3_error s3h_stager_init(struct s3h_stager *s, int device);
+void s3h_stager_free(struct s3h_stager *s);
+/* Copy nbytes from pageable host memory to dev; returns when the data is
+ * in HBM. */
+enum sam3_error s3h_stager_copy(struct s3h_stager *s, void *dev, const void *host, size_t nbytes);
+
 #endif /* SAM3_HIP_INTERNAL_H */

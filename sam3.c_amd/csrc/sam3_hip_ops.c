@@ -740,7 +740,7 @@ int s3h_layernorm_ok(const struct sam3_node *node)
 	if (node->n_inputs < 1 || !node->inputs[0] || !node->output)
 		return 0;
 	const struct sam3_tensor *in = node->inputs[0];
-	if (!is_float_dtype(in->dtype) || in->n_dims < 1 || (int)node->output->dtype != in->dtype ||
+	if (!is_float_dtype(in->dtype) || in->n_dims < 1 || node->output->dtype != in->dtype ||
 	    s3h_nelems(node->output) != s3h_nelems(in))
 		return 0;
 	const int cols = in->dims[in->n_dims - 1];
@@ -748,7 +748,7 @@ int s3h_layernorm_ok(const struct sam3_node *node)
 		return 0;
 	for (int k = 1; k < node->n_inputs && k < 3; k++) {
 		const struct sam3_tensor *t = node->inputs[k];
-		if (t && ((int)t->dtype != in->dtype || s3h_nelems(t) < cols))
+		if (t && (t->dtype != in->dtype || s3h_nelems(t) < cols))
 			return 0;
 	}
 	return 1;
@@ -787,7 +787,7 @@ int s3h_rope_ok(const struct sam3_node *node)
 	const struct sam3_tensor *x = node->inputs[0], *c = node->inputs[1], *s = node->inputs[2];
 	if (!is_float_dtype(x->dtype) || x->n_dims != 4 || (x->dims[3] & 1) ||
 	    c->dtype != SAM3_DTYPE_F32 || s->dtype != SAM3_DTYPE_F32 ||
-	    (int)node->output->dtype != x->dtype || s3h_nelems(node->output) != s3h_nelems(x))
+	    node->output->dtype != x->dtype || s3h_nelems(node->output) != s3h_nelems(x))
 		return 0;
 	const int seq = x->dims[1], half = x->dims[3] / 2;
 	return c->n_dims == 2 && c->dims[0] == seq && c->dims[1] == half && s->n_dims == 2 &&

@@ -177,6 +177,82 @@ def vit_block(G, x, p, n_heads, grid, window, is_global, cos_t, sin_t):
     return G.add(x, ff)
 
 
+# Block parameter -> checkpoint tensor name, as sam3_vit_load looks them up
+# (image_encoder.c:344-420); q/k/v are stored separately and fused at load.
+VIT_PREFIX = "detector_model.vision_encoder.backbone."
+VIT_NAMES = {
+    "ln1_w": "layers.{}.layer_norm1.weight", "ln1_b": "layers.{}.layer_norm1.bias",
+    "q_w": "layers.{}.attention.q_proj.weight", "k_w": "layers.{}.attention.k_proj.weight",
+    "v_w": "layers.{}.attention.v_proj.weight", "q_b": "layers.{}.attention.q_proj.bias",
+    "k_b": "layers.{}.attention.k_proj.bias", "v_b": "layers.{}.attention.v_proj.bias",
+    "proj_w": "layers.{}.attention.o_proj.weight", "proj_b": "layers.{}.attention.o_proj.bias",
+    "ln2_w": "layers.{}.layer_norm2.weight", "ln2_b": "layers.{}.layer_norm2.bias",
+    "fc1_w": "layers.{}.mlp.fc1.weight", "fc1_b": "layers.{}.mlp.fc1.bias",
+    "fc2_w": "layers.{}.mlp.fc2.weight", "fc2_b": "layers.{}.mlp.fc2.bias",
+}
+_LINEAR = ("q_w", "k_w", "v_w", "proj_w", "fc1_w", "fc2_w")
+
+
+def vit_layer_entries(layer, e, mlp, seed, quantize=None):
+    """Checkpoint entries (name, dtype, dims, array) of one synthetic ViT
+    layer in the file layout: weights [out, in], q/k/v separate. With
+    `quantize` (f32 array -> Q8_0 block bytes) the six linear weights are
+    Q8_0 and everything else stays F32."""
+    from . import synth
+    shapes = {"ln1_w": (e,), "ln1_b": (e,), "q_w": (e, e), "k_w": (e, e), "v_w": (e, e),
+              "q_b": (e,), "k_b": (e,), "v_b": (e,), "proj_w": (e, e), "proj_b": (e,),
+              "ln2_w": (e,), "ln2_b": (e,), "fc1_w": (mlp, e), "fc1_b": (mlp,),
+              "fc2_w": (e, mlp), "fc2_b": (e,)}
+    std = {"ln1_w": 1.0, "ln2_w": 1.0, "ln1_b": 0.1, "ln2_b": 0.1}
+    out = []
+    for j, (key, shape) in enumerate(shapes.items()):
+        v = synth.randn(seed + j, shape, std.get(key, 0.05 if key in _LINEAR else 0.02))
+        name = VIT_PREFIX + VIT_NAMES[key].format(layer)
+        if quantize is not None and key in _LINEAR:
+            out.append((name, abi.Q8_0, list(shape), np.asarray(quantize(v), np.uint8)))
+        else:
+            out.append((name, abi.F32, list(shape), v))
+    return out
+
+
+def load_vit_layer(G, wf, layer, be=None):
+    """The per-layer part of sam3_vit_load (image_encoder.c:344-420) over
+    a `weights.WeightFile`: one tensor per parameter pointing into the
+    mapping, with q/k/v (weights and biases) stacked into qkv_w [3e, e]
+    and qkv_b [3e]. With a backend the stacking is
+    `sam3_hip_backend_fuse_rows` (in HBM, any dtype); without one it is a
+    host byte concatenation that keeps the parts' dtype."""
+    def get(key):
+        i = wf.find(VIT_PREFIX + VIT_NAMES[key].format(layer))
+        if i is None:
+            raise KeyError(VIT_NAMES[key].format(layer))
+        t = wf.to_tensor(i)
+        G.keep.append(t)
+        return t
+
+    def fuse(keys):
+        parts = [get(k) for k in keys]
+        out = abi.Tensor()
+        if be is not None:
+            from . import hip
+            hip.check(be.fuse_rows(parts, out), "fuse_rows")
+        else:
+            raw = np.concatenate([wf.array(wf.find(VIT_PREFIX + VIT_NAMES[k].format(layer)))
+                                  for k in keys])
+            dims = [sum(p.dims[0] for p in parts)] + ([parts[0].dims[1]]
+                                                      if parts[0].n_dims == 2 else [])
+            G.keep.append(raw)
+            out = abi.make_tensor(parts[0].dtype, dims, raw.ctypes.data, raw.nbytes)
+        G.keep.append(out)
+        return out
+
+    p = {k: get(k) for k in ("ln1_w", "ln1_b", "proj_w", "proj_b", "ln2_w", "ln2_b", "fc1_w",
+                             "fc1_b", "fc2_w", "fc2_b")}
+    p["qkv_w"] = fuse(("q_w", "k_w", "v_w"))
+    p["qkv_b"] = fuse(("q_b", "k_b", "v_b"))
+    return p
+
+
 def rope_tables(seq_side, hd, theta=10000.0):
     """2-D axial RoPE tables [seq_side^2, hd/2] (x then y frequencies),
     f32: synthetic stand-ins of the checkpoint's precomputed tables."""

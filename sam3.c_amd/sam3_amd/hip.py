@@ -27,6 +27,9 @@ SIGNATURES = {
     "sam3_hip_backend_set_host_dispatch": (None, [_vp, _vp, _vp]),
     "sam3_hip_backend_stream": (_vp, [_vp]),
     "sam3_hip_backend_last_stats": (None, [_vp, _vp]),
+    "sam3_hip_backend_map_weights": (_i, [_vp, _vp, C.c_size_t]),
+    "sam3_hip_backend_weight_ptr": (_vp, [_vp, _vp]),
+    "sam3_hip_backend_fuse_rows": (_i, [_vp, _vp, _i, _vp]),
     "sam3_hip_kernel_matmul": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_f16": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_bf16": (_i, [_vp, _vp]),
@@ -74,7 +77,8 @@ BIAS, GELU, B_NT = 1, 2, 4
 
 class EvalStats(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("gpu_nodes", "fused_nodes", "host_nodes",
-                                       "uploads", "cache_hits", "downloads")]
+                                       "uploads", "cache_hits", "downloads",
+                                       "mapped_reads")]
 
 
 class HipError(RuntimeError):
@@ -147,6 +151,13 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def download_ptr(ptr, nbytes, dtype=np.uint8):
+    """Copy nbytes at device address ptr into a new host array."""
+    out = np.empty(int(nbytes) // np.dtype(dtype).itemsize, dtype=dtype)
+    check(load().sam3_hip_memcpy_d2h(out.ctypes.data, ptr, out.nbytes), "memcpy_d2h")
+    return out
 
 
 def synchronize():
@@ -315,6 +326,18 @@ class Backend:
     def set_host_dispatch(self, fn):
         self._host_fn = HOST_DISPATCH_FN(fn) if fn else None
         self.lib.sam3_hip_backend_set_host_dispatch(self.be, self._host_fn, None)
+
+    def map_weights(self, host_ptr, nbytes):
+        """sam3_hip_backend_map_weights: copy [host_ptr, +nbytes) to HBM once."""
+        return self.lib.sam3_hip_backend_map_weights(self.be, host_ptr, nbytes)
+
+    def weight_ptr(self, host_ptr):
+        return self.lib.sam3_hip_backend_weight_ptr(self.be, host_ptr)
+
+    def fuse_rows(self, parts, out):
+        """sam3_hip_backend_fuse_rows over a list of abi.Tensor headers."""
+        arr = (C.POINTER(abi.Tensor) * len(parts))(*[C.pointer(t) for t in parts])
+        return self.lib.sam3_hip_backend_fuse_rows(self.be, arr, len(parts), C.byref(out))
 
     def stats(self):
         s = EvalStats()

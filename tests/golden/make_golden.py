@@ -32,9 +32,37 @@ def fp16_bits(ref, x):
     return ref.cast(np.asarray(x, np.float32), abi.F32, abi.F16, np.uint16).reshape(np.shape(x))
 
 
+WEIGHTS_CONFIG = dict(image_size=1008, encoder_dim=1024, decoder_dim=256, n_encoder_layers=32,
+                      n_decoder_layers=2, backbone_type=1, n_fpn_scales=3, variant=2,
+                      text_backbone=1)
+
+
+def weight_fixture_tensors(q8_quantize):
+    """Tensors of weights_golden.sam3: every dtype, ragged sizes (padding
+    between tensors), a 127-byte name, a 140-byte name (the writer keeps
+    127 bytes, weight.c:111-117) and 48 small tensors so lookups probe."""
+    t = [("enc.w", abi.F32, [3, 5], synth.randn(synth.tensor_seed(80, 0), (3, 5))),
+         ("enc.q8", abi.Q8_0, [4, 32], q8_quantize(synth.randn(synth.tensor_seed(80, 1), 128))),
+         ("enc.bf16", abi.BF16, [7], np.arange(7, dtype=np.uint16) * 4099),
+         ("enc.i32", abi.I32, [2, 2, 2], np.arange(8, dtype=np.int32) - 3),
+         ("enc.f16", abi.F16, [1], np.array([0x3C00], np.uint16)),
+         ("enc.i8", abi.I8, [65], (np.arange(65) - 32).astype(np.int8)),
+         ("n" * 127, abi.F32, [2], np.array([1.5, -2.5], np.float32)),
+         ("m" * 140, abi.F32, [1], np.array([7.0], np.float32))]
+    for i in range(48):
+        t.append((f"blk.{i}.w", abi.F32, [i % 5 + 1], np.full(i % 5 + 1, i, np.float32)))
+    return t
+
+
 def main():
     R = Ref()
     g = {}
+
+    # -- .sam3 container written by the reference's sam3_weight_write
+    from oracle_bind import ref_weight_write
+    rc = ref_weight_write(R, HERE / "weights_golden.sam3", weight_fixture_tensors(R.q8_quantize),
+                          WEIGHTS_CONFIG)
+    assert rc == 0, rc
 
     # -- Q8 quantize: random, a zero block, a ragged tail and exact .5 ties
     # (scale 1.0 makes x*inv == x; x86 roundf rounds ties away from zero,

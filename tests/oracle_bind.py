@@ -419,3 +419,108 @@ Ref.permute = _ref_permute
 
 def have_ref():
     return REF_SO.exists()
+
+
+# ---- the reference's .sam3 container (src/core/weight.{h,c}) ----
+
+class _WeightFileC(C.Structure):
+    """struct sam3_weight_file (src/core/weight.h:83-94), x86-64 layout."""
+    _fields_ = [("mapped", _vp), ("mapped_size", C.c_size_t), ("header", _vp), ("tensors", _vp),
+                ("data_base", _vp), ("hash_table", _vp), ("hash_capacity", C.c_uint32),
+                ("prefetch_thread", C.c_ulong), ("prefetch_active", _i),
+                ("text_backbone", C.c_uint32)]
+
+
+class _TensorInfoC(C.Structure):
+    """struct weight_tensor_info (weight.h:180-186)."""
+    _fields_ = [("name", C.c_char_p), ("dtype", _i), ("n_dims", _i), ("dims", _i * 4),
+                ("nbytes", C.c_size_t)]
+
+
+_R_OPEN = C.CFUNCTYPE(_i, _vp, C.c_char_p)
+_R_N = C.CFUNCTYPE(_i, _vp)
+_R_INFO = C.CFUNCTYPE(_i, _vp, _i, C.POINTER(_TensorInfoC))
+_R_READ = C.CFUNCTYPE(_i, _vp, _i, _vp, C.c_size_t)
+_R_CLOSE = C.CFUNCTYPE(None, _vp)
+
+
+class _ReaderOpsC(C.Structure):
+    """struct weight_reader_ops (weight.h:188-196)."""
+    _fields_ = [("open", _R_OPEN), ("n_tensors", _R_N), ("get_tensor_info", _R_INFO),
+                ("read_tensor_data", _R_READ), ("close", _R_CLOSE)]
+
+
+class _ReaderC(C.Structure):
+    _fields_ = [("ops", C.POINTER(_ReaderOpsC)), ("impl", _vp)]
+
+
+class _ModelConfigC(C.Structure):
+    """struct sam3_model_config (include/sam3/sam3_types.h:145-155)."""
+    _fields_ = [(k, _i) for k in ("image_size", "encoder_dim", "decoder_dim", "n_encoder_layers",
+                                  "n_decoder_layers", "backbone_type", "n_fpn_scales", "variant",
+                                  "text_backbone")]
+
+
+def _ref_weight_api(L):
+    L.sam3_weight_write.argtypes = [C.c_char_p, C.POINTER(_ModelConfigC), C.POINTER(_ReaderC)]
+    L.sam3_weight_write.restype = _i
+    L.sam3_weight_open.argtypes = [C.POINTER(_WeightFileC), C.c_char_p]
+    L.sam3_weight_open.restype = _i
+    L.sam3_weight_close.argtypes = [C.POINTER(_WeightFileC)]
+    L.sam3_weight_find.argtypes = [C.POINTER(_WeightFileC), C.c_char_p]
+    L.sam3_weight_find.restype = _vp
+    L.sam3_weight_to_tensor.argtypes = [C.POINTER(_WeightFileC), _vp, C.POINTER(abi.Tensor)]
+    L.sam3_weight_to_tensor.restype = _i
+
+
+def ref_weight_write(ref, path, tensors, config=None):
+    """sam3_weight_write driven by an in-memory weight_reader the way
+    tests/test_weight_q8.c:23-99 builds one: tensors are
+    (name, dtype, dims, numpy array of the bytes)."""
+    _ref_weight_api(ref.lib)
+    arrs = [np.ascontiguousarray(a).reshape(-1).view(np.uint8) for _, _, _, a in tensors]
+    names = [n.encode() for n, _, _, _ in tensors]
+
+    def info(r, idx, out):
+        _, dt, dims, _ = tensors[idx]
+        out.contents.name = names[idx]
+        out.contents.dtype = dt
+        out.contents.n_dims = len(dims)
+        for d in range(4):
+            out.contents.dims[d] = dims[d] if d < len(dims) else 0
+        out.contents.nbytes = arrs[idx].nbytes
+        return 0
+
+    def read(r, idx, dst, size):
+        if size < arrs[idx].nbytes:
+            return abi.EINVAL
+        C.memmove(dst, arrs[idx].ctypes.data, arrs[idx].nbytes)
+        return 0
+
+    cbs = [_R_OPEN(lambda r, p: 0), _R_N(lambda r: len(tensors)), _R_INFO(info),
+           _R_READ(read), _R_CLOSE(lambda r: None)]
+    ops = _ReaderOpsC(*cbs)
+    reader = _ReaderC(C.pointer(ops), None)
+    cfg = _ModelConfigC(**(config or {}))
+    return ref.lib.sam3_weight_write(str(path).encode(), C.byref(cfg), C.byref(reader))
+
+
+class RefWeightFile:
+    """sam3_weight_open / find / to_tensor / close of the reference."""
+
+    def __init__(self, ref, path):
+        _ref_weight_api(ref.lib)
+        self.lib = ref.lib
+        self.wf = _WeightFileC()
+        self.rc = self.lib.sam3_weight_open(C.byref(self.wf), str(path).encode())
+
+    def find(self, name):
+        return self.lib.sam3_weight_find(C.byref(self.wf), name.encode())
+
+    def to_tensor(self, desc):
+        t = abi.Tensor()
+        rc = self.lib.sam3_weight_to_tensor(C.byref(self.wf), desc, C.byref(t))
+        return rc, t
+
+    def close(self):
+        self.lib.sam3_weight_close(C.byref(self.wf))
