@@ -329,6 +329,86 @@ def weights_upload_bench(layers=32, e=1024, mlp=4096):
                     "allocation and the first touch of the mapping"}
 
 
+# name: (x [N,H,W,C], w [OC,KH,KW,C], stride, pad) -- the patch embedding
+# (image_encoder.c:577) and the neck's convs at the 1x and 4x scales
+# (necks.c:345-365)
+CONV_SHAPES = {
+    "patch_embed": ((1, 1008, 1008, 3), (1024, 14, 14, 3), 14, 0),
+    "neck_1x1_72": ((1, 72, 72, 1024), (256, 1, 1, 1024), 1, 0),
+    "neck_3x3_72": ((1, 72, 72, 256), (256, 3, 3, 256), 1, 1),
+    "neck_3x3_288": ((1, 288, 288, 256), (256, 3, 3, 256), 1, 1),
+}
+
+
+def conv_case(lib, stream, timer, kind, xs, ws, stride, pad, steps, warmup):
+    """One CONV2D node (sam3_hip_kernel_conv2d) on device buffers, timed."""
+    dt, npt = {"f32": (abi.F32, np.float32), "bf16": (abi.BF16, np.uint16)}[kind]
+    x = synth.randn(600, xs)
+    w = synth.randn(601, ws, 0.02)
+    if kind == "bf16":
+        x, w = bf16_bits(x), bf16_bits(w)
+    N, H, W, C = xs
+    OC, KH, KW, _ = ws
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    bx, bw = hip.DeviceBuffer.of(x), hip.DeviceBuffer.of(w)
+    by = hip.DeviceBuffer(N * OH * OW * OC * np.dtype(npt).itemsize)
+    tx = abi.make_tensor(dt, list(xs), bx.ptr, x.nbytes)
+    tw = abi.make_tensor(dt, list(ws), bw.ptr, w.nbytes)
+    ty = abi.make_tensor(dt, [N, OH, OW, OC], by.ptr, by.nbytes)
+    node = abi.make_node(abi.OP_CONV2D, [tx, tw], ty, (stride, pad, 1, 0))
+    path = lib.sam3_hip_conv2d_path(hip.C.byref(node))
+
+    def step():
+        hip.check(lib.sam3_hip_kernel_conv2d(hip.C.byref(node), stream), "conv2d")
+
+    ms = timer.run(step, steps, warmup)
+    for b in (bx, bw, by):
+        b.free()
+    M, K = N * OH * OW, KH * KW * C
+    return {"us": round(ms * 1e3, 1), "tflops": round(tflops(M, OC, K, ms), 1),
+            "path": {1: "implicit_gemm", 2: "im2col_gemm", 3: "direct"}.get(path, path)}
+
+
+def cpu_conv(name, threads=None, target_s=3.0):
+    """The reference's f32 conv (cpu_kernel_conv2d via oracle/_ref, or the
+    restatement) on the host cores, on a crop of the input rows sized to a
+    few seconds; TFLOP/s of 2*M*OC*K."""
+    from oracle_bind import Oracle, Ref, have_ref
+    threads = threads or max(1, min(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1),
+                                    os.cpu_count() or 1))
+    xs, ws, stride, pad = CONV_SHAPES[name]
+    N, H, W, C = xs
+    OC, KH, KW, _ = ws
+    # probe on a few rows, then as many rows as fit in about target_s
+    rows = min(H, max(KH, 4 * stride))
+    R0 = Ref() if have_ref() else Oracle()
+    t0 = time.perf_counter()
+    if have_ref():
+        R0.conv2d(synth.randn(602, (N, rows, W, C)), synth.randn(603, ws, 0.02), stride, pad, None,
+                  1, "f32", None, threads)
+        R0.close()
+    else:
+        R0.conv2d(synth.randn(602, (N, rows, W, C)), synth.randn(603, ws, 0.02), stride, pad,
+                  threads=threads)
+    per_row = (time.perf_counter() - t0) / rows
+    rows = int(min(H, max(rows, target_s / max(per_row, 1e-9))))
+    rows -= rows % stride
+    x = synth.randn(602, (N, rows, W, C))
+    w = synth.randn(603, ws, 0.02)
+    R, kind = (Ref(), "reference") if have_ref() else (Oracle(), "port")
+    t0 = time.perf_counter()
+    if kind == "reference":
+        rc, y = R.conv2d(x, w, stride, pad, None, 1, "f32", None, threads)
+        R.close()
+    else:
+        y = R.conv2d(x, w, stride, pad, threads=threads)
+    dt = time.perf_counter() - t0
+    M = y.shape[0] * y.shape[1] * y.shape[2]
+    return {"value": round(2.0 * M * OC * KH * KW * C / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": kind,
+            "sample": f"f32 {name}, {rows} of {H} input rows -> {M} output pixels, {dt:.2f} s"}
+
+
 def measured_traffic(key):
     """HBM bytes per launch of the headline kernel, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
@@ -443,8 +523,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
-    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,weights",
-                    help="comma list of extra sections to run (cfg1..cfg5, block, weights)")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,weights",
+                    help="comma list of extra sections to run (cfg1..cfg5, block, conv, weights)")
     ap.add_argument("--block", default="windowed_f32,windowed_q8,global_f32,global_q8",
                     help="block section: comma list of {windowed,global}_{f32,q8}")
     args = ap.parse_args()
@@ -619,6 +699,20 @@ def main():
         blk["note"] = ("5184 tokens, e 1024, 16 heads, MLP 4096, f32 activations; every node "
                        "on the GPU; block input in HBM, no readback; wall time of graph_eval")
         extra["vit_block"] = blk
+
+    if not args.quick and "conv" in only:
+        log("conv2d: patch embedding and neck convs (NHWC x OHWI)")
+        cv = {}
+        for name, (xs, ws, st, pd) in CONV_SHAPES.items():
+            for kind in ("f32", "bf16"):
+                cv[f"{name}_{kind}"] = conv_case(lib, stream, timer, kind, xs, ws, st, pd,
+                                                 min(K_, 20), min(W_, 3))
+                log("  ", name, kind, cv[f"{name}_{kind}"])
+        if not args.no_cpu_baseline:
+            cv["cpu_reference"] = {n: cpu_conv(n) for n in ("patch_embed", "neck_3x3_72")}
+        cv["note"] = ("one sam3_hip_kernel_conv2d per step, inputs in HBM; 2*M*OC*K flops with "
+                      "M = N*OH*OW, K = KH*KW*C; f32 runs on bf16 hi/lo planes")
+        extra["conv2d"] = cv
 
     if not args.quick and "weights" in only:
         log("weights: .sam3 blob (32 ViT-L layers, Q8_0 linear weights) to HBM")

@@ -32,7 +32,8 @@ extern "C" {
  * struct sam3_backend_ops (src/backend/backend.h:31-56). graph_eval runs
  * MATMUL nodes (F32, F16, BF16, F32 x Q8_0) on the GPU, fusing
  * TRANSPOSE(W) -> MATMUL -> ADD(bias) -> GELU chains, and runs ADD,
- * GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE and SLICE on the GPU as well
+ * GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE, SLICE, CONV2D (with a following
+ * BIAS_ADD and GELU in its epilogue) and BIAS_ADD on the GPU as well
  * (RESHAPE is a view: no copy, no transfer); other ops go to the host
  * dispatcher set with sam3_hip_backend_set_host_dispatch, or fail with
  * SAM3_EDTYPE when none is set (as cpu_dispatch_node does for an op with
@@ -181,6 +182,41 @@ enum sam3_error sam3_hip_kernel_rope(const struct sam3_node *node, void *stream)
 enum sam3_error sam3_hip_kernel_slice(const struct sam3_node *node, void *stream);
 enum sam3_error sam3_hip_kernel_transpose(const struct sam3_node *node, void *stream);
 enum sam3_error sam3_hip_kernel_reshape(const struct sam3_node *node);
+
+/*
+ * CONV2D node kernel: cpu_kernel_conv2d (src/backend/cpu/kernels/
+ * cpu_conv2d.c:296-435) and its twins cpu_kernel_conv2d_f16 / _bf16
+ * (cpu_conv2d_f16.c, cpu_conv2d_bf16.c). Input [N,H,W,C] (NHWC), weight
+ * OHWI [OC,KH,KW,C/groups], output [N,OH,OW,OC] with OH and OW read from
+ * the output; params[0] = stride (<= 0 -> 1), [1] = pad_h, [2] = groups
+ * (<= 0 -> 1), [3] = pad_w (0 -> pad_h). One dtype (F32, F16, BF16) for
+ * input, weight and output, f32 accumulation, one rounding of the output.
+ * Errors as the reference: NULL, non-4-D, channel or output-shape
+ * mismatch -> SAM3_EINVAL; other dtypes or mixed ones -> SAM3_EDTYPE.
+ *
+ * Kernels: groups 1 with C % 64 == 0 runs an implicit GEMM on MFMA (the
+ * column matrix is gathered in the load path, never written); other
+ * groups-1 problems of >= 2^22 multiply-adds write the column matrix
+ * and run the GEMM; the rest (groups, tiny problems) run one output per
+ * thread in the reference's order (bit-exact for F32). F32 tensors run
+ * the GEMMs as bf16 hi/lo splits (~1e-5 normwise; SAM3_HIP_F32_SPLIT=0
+ * keeps them on the direct kernel).
+ */
+enum sam3_error sam3_hip_kernel_conv2d(const struct sam3_node *node, void *stream);
+
+/* The kernel sam3_hip_kernel_conv2d picks (1 implicit GEMM, 2 column
+ * matrix + GEMM, 3 direct; 0 if the node is invalid), and the conv on a
+ * forced path (SAM3_EINVAL when that path cannot run it). No reference
+ * counterpart: for tests and benches. */
+int sam3_hip_conv2d_path(const struct sam3_node *node);
+enum sam3_error sam3_hip_conv2d_on_path(int path, const struct sam3_node *node, void *stream);
+
+/*
+ * BIAS_ADD node kernel: cpu_kernel_bias_add / _bf16
+ * (src/backend/cpu/kernels/cpu_bias_add.c:65-101, :150-190): x [.., C] +
+ * bias [C] over the last dim, F32, BF16 (and F16), one dtype.
+ */
+enum sam3_error sam3_hip_kernel_bias_add(const struct sam3_node *node, void *stream);
 
 /* Route one node by op and dtype. Replaces cpu_dispatch_node
  * (src/backend/cpu/cpu_dispatch.c:591-686): same mixed F32 x Q8_0 rule,

@@ -809,3 +809,98 @@ void oracle_rope_f16(const uint16_t *x, const float *cos_t, const float *sin_t, 
 {
 	rope_any(x, cos_t, sin_t, y, batch, seq, heads, hd, 2);
 }
+
+/* ------------------------------------------------------------------ */
+/* Conv2D, NHWC x OHWI: cpu_conv2d.c:46-88 (im2col_nhwc_f32), :98-128   */
+/* (col x W^T, out[j] zeroed then out[j] += col[k]*w[j][k] for k in     */
+/* order), :296-435 (groups, params); the 16-bit twins                  */
+/* cpu_conv2d_bf16.c:42-80, :179-213 and cpu_conv2d_f16.c (scalar path)  */
+/* accumulate the same products in f32 and round the output once.       */
+/* ------------------------------------------------------------------ */
+struct conv_ctx {
+	const void *x, *w;
+	void *y;
+	int kind; /* 0 f32, 1 bf16, 2 f16 */
+	int N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW;
+};
+
+static void conv_rows(void *p, int r0, int r1)
+{
+	const struct conv_ctx *c = p;
+	const int cpg_in = c->C / c->groups, cpg_out = c->OC / c->groups;
+	const int K = cpg_in * c->KH * c->KW;
+	float *col = malloc((size_t)K * sizeof(float));
+	float *acc = malloc((size_t)cpg_out * sizeof(float));
+	if (!col || !acc) {
+		free(col);
+		free(acc);
+		return;
+	}
+	for (int r = r0; r < r1; r++) { /* r = (n * OH + oh) * OW + ow */
+		const int ow = r % c->OW, oh = (r / c->OW) % c->OH, n = r / (c->OW * c->OH);
+		for (int g = 0; g < c->groups; g++) {
+			/* im2col row: taps (kh, kw), group channels innermost */
+			for (int kh = 0; kh < c->KH; kh++) {
+				const int ih = oh * c->stride + kh - c->ph;
+				for (int kw = 0; kw < c->KW; kw++) {
+					const int iw = ow * c->stride + kw - c->pw;
+					float *d = col + ((size_t)kh * c->KW + kw) * cpg_in;
+					const int in = (unsigned)ih < (unsigned)c->H && (unsigned)iw < (unsigned)c->W;
+					for (int ic = 0; ic < cpg_in; ic++)
+						d[ic] = in ? ln_get(c->x, c->kind,
+								    (((size_t)n * c->H + ih) * c->W + iw) * c->C +
+									    (size_t)g * cpg_in + ic)
+							   : 0.0f;
+				}
+			}
+			const size_t wg = (size_t)g * cpg_out * K;
+			for (int j = 0; j < cpg_out; j++)
+				acc[j] = 0.0f;
+			for (int k = 0; k < K; k++) {
+				const float cik = col[k];
+				for (int j = 0; j < cpg_out; j++)
+					acc[j] += cik * ln_get(c->w, c->kind, wg + (size_t)j * K + k);
+			}
+			const size_t ob = (size_t)r * c->OC + (size_t)g * cpg_out;
+			for (int j = 0; j < cpg_out; j++) {
+				if (c->kind == 0)
+					((float *)c->y)[ob + j] = acc[j];
+				else if (c->kind == 1)
+					((uint16_t *)c->y)[ob + j] = oracle_f32_to_bf16(acc[j]);
+				else
+					((uint16_t *)c->y)[ob + j] = oracle_f32_to_fp16(acc[j]);
+			}
+		}
+	}
+	free(col);
+	free(acc);
+}
+
+static void conv_any(const void *x, const void *w, void *y, int kind, int N, int H, int W, int C,
+		     int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH, int OW,
+		     int n_threads)
+{
+	struct conv_ctx c = { x, w, y, kind, N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW };
+	run_rows(conv_rows, &c, N * OH * OW, n_threads);
+}
+
+void oracle_conv2d_f32(const float *x, const float *w, float *y, int N, int H, int W, int C,
+		       int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH, int OW,
+		       int n_threads)
+{
+	conv_any(x, w, y, 0, N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW, n_threads);
+}
+
+void oracle_conv2d_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N, int H, int W,
+			int C, int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH,
+			int OW, int n_threads)
+{
+	conv_any(x, w, y, 1, N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW, n_threads);
+}
+
+void oracle_conv2d_f16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N, int H, int W,
+		       int C, int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH,
+		       int OW, int n_threads)
+{
+	conv_any(x, w, y, 2, N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW, n_threads);
+}

@@ -108,4 +108,18 @@ void oracle_rope_bf16(const uint16_t *x, const float *cos_t, const float *sin_t,
 void oracle_rope_f16(const uint16_t *x, const float *cos_t, const float *sin_t, uint16_t *y,
 		     int batch, int seq, int heads, int hd);
 
+/* ---- Conv2D NHWC x OHWI -> NHWC (cpu_conv2d.c:46-128, 296-435;
+ * cpu_conv2d_bf16.c, cpu_conv2d_f16.c scalar paths): x [N,H,W,C], w
+ * [OC,KH,KW,C/groups], y [N,OH,OW,OC]; f32 accumulation in im2col order,
+ * 16-bit outputs rounded once. ---- */
+void oracle_conv2d_f32(const float *x, const float *w, float *y, int N, int H, int W, int C,
+		       int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH, int OW,
+		       int n_threads);
+void oracle_conv2d_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N, int H, int W,
+			int C, int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH,
+			int OW, int n_threads);
+void oracle_conv2d_f16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N, int H, int W,
+		       int C, int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH,
+		       int OW, int n_threads);
+
 #endif /* SAM3_ORACLE_H */

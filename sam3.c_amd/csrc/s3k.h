@@ -115,6 +115,32 @@ int s3k_bias_add(int kind, const void *x, const void *bias, void *out,
 int s3k_add_same(int kind, const void *x, const void *y, void *out,
 		 long long n, void *stream);
 int s3k_gelu(int kind, const void *x, void *out, long long n, void *stream);
+/*
+ * NHWC Conv2D (conv.hip): x [N,H,W,C], w OHWI [OC,KH,KW,C/groups],
+ * y [N,OH,OW,OC], one kind for x, w, y (and bias, [OC], with
+ * S3K_EPI_BIAS; S3K_EPI_GELU after it).
+ *   s3k_conv_implicit: groups 1, C % 64 == 0; xa/wb are x and w for
+ *     16-bit kinds, or their bf16 planes for f32 (x: [N*H*W, 3C] =
+ *     [hi|lo|hi], w: [OC, 3K] = [hi|hi|lo], from s3k_split3_bf16);
+ *     pixel_pitch = C or 3C.
+ *   s3k_conv_im2col: the column matrix [M, Kp] (16-bit) or its f32 planes
+ *     [M, 3Kp] for the GEMM, Kp >= KH*KW*C, Kp % 8 == 0 (zero padded);
+ *     s3k_conv_wprep: the weight as [OC, Kp] or planes [OC, 3Kp].
+ *   s3k_conv_direct: any groups; reference accumulation order.
+ */
+struct s3k_conv {
+	const void *x;
+	const void *w;
+	void       *y;
+	const void *bias;
+	int kind, flags;
+	int N, H, W, C, OC, KH, KW, stride, pad_h, pad_w, groups, OH, OW;
+};
+int s3k_conv_implicit(const struct s3k_conv *c, const void *xa, const void *wb, int pixel_pitch,
+		      void *stream);
+int s3k_conv_im2col(const struct s3k_conv *c, void *col, int Kp, void *stream);
+int s3k_conv_wprep(int kind, const void *w, void *out, int OC, int K, int Kp, void *stream);
+int s3k_conv_direct(const struct s3k_conv *c, void *stream);
 /* batch slices of [rows, cols] -> [cols, rows] */
 int s3k_transpose2d(int esize, const void *src, void *dst, int batch, int rows,
 		    int cols, void *stream);

@@ -449,6 +449,61 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	return err;
 }
 
+/* CONV2D at node i, plus a following BIAS_ADD ([OC], used only there)
+ * and GELU folded into the GEMM epilogue when the conv runs as a GEMM. */
+static enum sam3_error run_conv(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+				struct use_map *uses, int *used)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	struct sam3_tensor tx = *n->inputs[0], tw = *n->inputs[1], ty = *n->output;
+	struct sam3_node dn = *n;
+	enum sam3_error err = dev_in(hb, n->inputs[0], &tx.data);
+	if (err == SAM3_OK)
+		err = dev_in(hb, n->inputs[1], &tw.data);
+	if (err != SAM3_OK)
+		return err;
+	dn.inputs[0] = &tx;
+	dn.inputs[1] = &tw;
+	dn.output = &ty;
+	/* the kernel choice looks at the device addresses */
+	const int path = s3h_conv2d_path(&dn);
+	const struct sam3_tensor *out = n->output, *bias = NULL;
+	const long long ny = s3h_nelems(out);
+	int flags = 0, j = i + 1;
+	if (path != S3H_CONV_DIRECT && j < g->n_nodes && g->nodes[j].op == SAM3_OP_BIAS_ADD &&
+	    g->nodes[j].n_inputs == 2 && g->nodes[j].inputs[0] == out && g->nodes[j].inputs[1] &&
+	    g->nodes[j].inputs[1] != out && uses_of(uses, out) == 1 &&
+	    g->nodes[j].inputs[1]->dtype == out->dtype &&
+	    s3h_nelems(g->nodes[j].inputs[1]) == out->dims[3] && g->nodes[j].output &&
+	    s3h_nelems(g->nodes[j].output) == ny) {
+		bias = g->nodes[j].inputs[1];
+		out = g->nodes[j].output;
+		flags |= S3K_EPI_BIAS;
+		j++;
+	}
+	if (path != S3H_CONV_DIRECT && j < g->n_nodes && g->nodes[j].op == SAM3_OP_GELU &&
+	    g->nodes[j].n_inputs >= 1 && g->nodes[j].inputs[0] == out && uses_of(uses, out) == 1 &&
+	    g->nodes[j].output && s3h_nelems(g->nodes[j].output) == ny) {
+		out = g->nodes[j].output;
+		flags |= S3K_EPI_GELU;
+		j++;
+	}
+	void *dbias = NULL;
+	if (bias)
+		err = dev_in(hb, bias, &dbias);
+	if (err == SAM3_OK)
+		err = dev_out(hb, out, &ty.data);
+	if (err != SAM3_OK)
+		return err;
+	err = s3h_conv2d(&dn, dbias, flags, path, hb->stream);
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.fused_nodes += j - i - 1;
+		*used = j - i;
+	}
+	return err;
+}
+
 /* ADD, GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE, SLICE on device copies of
  * the node's tensors. */
 static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct sam3_node *n)
@@ -486,6 +541,8 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 		err = s3h_rope(&dn, hb->stream);
 	else if (n->op == SAM3_OP_SLICE)
 		err = s3h_slice(&dn, hb->stream);
+	else if (n->op == SAM3_OP_BIAS_ADD)
+		err = s3h_bias_add(&dn, hb->stream);
 	else
 		err = s3h_transpose(&dn, hb->stream);
 	if (err == SAM3_OK)
@@ -509,6 +566,8 @@ static int runs_on_gpu(const struct sam3_node *n)
 	case SAM3_OP_ADD:
 	case SAM3_OP_GELU:
 		return float_dt(dt);
+	case SAM3_OP_BIAS_ADD:
+		return s3h_bias_add_ok(n);
 	case SAM3_OP_TRANSPOSE:
 		return s3h_transpose_ok(n);
 	case SAM3_OP_LAYERNORM:
@@ -598,6 +657,8 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 			hb->stats.fused_nodes++;
 		} else if (n->op == SAM3_OP_MATMUL) {
 			err = run_matmul(hb, g, i, folded, &uses, &used);
+		} else if (n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) {
+			err = run_conv(hb, g, i, &uses, &used);
 		} else if (runs_on_gpu(n)) {
 			err = run_elementwise(hb, n);
 		} else {

@@ -39,6 +39,17 @@ enum sam3_error s3h_reshape(const struct sam3_node *node);
 /* Whether sam3_hip_kernel_sdpa takes this node (dtypes, ranks, head_dim). */
 int s3h_sdpa_node_ok(const struct sam3_node *node);
 
+/* CONV2D kernels (conv.hip) and BIAS_ADD. s3h_conv2d runs path 0 (the
+ * best), S3H_CONV_IMPLICIT, _IM2COL or _DIRECT; bias/flags (S3K_EPI_*)
+ * fold a following BIAS_ADD and GELU into the GEMM epilogue (paths 1-2). */
+enum { S3H_CONV_IMPLICIT = 1, S3H_CONV_IM2COL = 2, S3H_CONV_DIRECT = 3 };
+int s3h_conv2d_ok(const struct sam3_node *node);
+int s3h_conv2d_path(const struct sam3_node *node);
+enum sam3_error s3h_conv2d(const struct sam3_node *node, const void *bias, int flags, int path,
+			   void *stream);
+int s3h_bias_add_ok(const struct sam3_node *node);
+enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
+
 /* Bulk host -> device copies through pinned staging buffers (upload.c).
  * Lanes and chunk size default to S3H_STAGE_LANES x S3H_STAGE_CHUNK_MB;
  * SAM3_HIP_UPLOAD_LANES / SAM3_HIP_UPLOAD_CHUNK_MB override them. */

@@ -886,6 +886,272 @@ enum sam3_error s3h_reshape(const struct sam3_node *node)
 	return SAM3_OK;
 }
 
+/* ------------------------------------------------------------------ */
+/* CONV2D and BIAS_ADD                                                  */
+/* ------------------------------------------------------------------ */
+
+/* CONV2D as cpu_kernel_conv2d reads it (cpu_conv2d.c:296-368): input
+ * [N,H,W,C], weight OHWI [OC,KH,KW,C/groups], output [N,OH,OW,OC] with OH,
+ * OW taken from the output; params stride (<= 0 -> 1), pad_h, groups
+ * (<= 0 -> 1), pad_w (0 -> pad_h). Same dtype for input, weight and
+ * output (cpu_dispatch.c:643-655). */
+static enum sam3_error conv_shape(const struct sam3_node *node, struct s3k_conv *c, int quiet)
+{
+#define CONV_FAIL(code, ...)                    \
+	do {                                    \
+		if (!quiet)                     \
+			s3h_error(__VA_ARGS__); \
+		return code;                    \
+	} while (0)
+	if (!node || node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] || !node->output)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: NULL tensor");
+	const struct sam3_tensor *x = node->inputs[0], *w = node->inputs[1], *y = node->output;
+	if (!is_float_dtype(x->dtype) || w->dtype != x->dtype || y->dtype != x->dtype)
+		CONV_FAIL(SAM3_EDTYPE, "conv2d: input, weight and output must share one of F32/F16/BF16 "
+				       "(got %d, %d, %d)", x->dtype, w->dtype, y->dtype);
+	if (x->n_dims != 4 || w->n_dims != 4 || y->n_dims != 4)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: expected 4D tensors");
+	memset(c, 0, sizeof(*c));
+	c->kind = x->dtype;
+	c->x = x->data;
+	c->w = w->data;
+	c->y = y->data;
+	c->N = x->dims[0];
+	c->H = x->dims[1];
+	c->W = x->dims[2];
+	c->C = x->dims[3];
+	c->OC = w->dims[0];
+	c->KH = w->dims[1];
+	c->KW = w->dims[2];
+	c->stride = node->params[0] > 0 ? node->params[0] : 1;
+	c->pad_h = node->params[1];
+	c->groups = node->params[2] > 0 ? node->params[2] : 1;
+	c->pad_w = node->params[3] ? node->params[3] : c->pad_h;
+	c->OH = y->dims[1];
+	c->OW = y->dims[2];
+	if (w->dims[3] * c->groups != c->C)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: channel mismatch %d*%d != %d", w->dims[3], c->groups,
+			  c->C);
+	if (c->C % c->groups || c->OC % c->groups)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: channels not divisible by groups");
+	if (y->dims[0] != c->N || y->dims[3] != c->OC)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: output shape mismatch");
+	if (c->N <= 0 || c->H <= 0 || c->W <= 0 || c->C <= 0 || c->OC <= 0 || c->KH <= 0 ||
+	    c->KW <= 0 || c->OH <= 0 || c->OW <= 0)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: empty dimension");
+	if ((long long)c->N * c->H * c->W * c->C > INT32_MAX ||
+	    (long long)c->N * c->OH * c->OW * c->OC > INT32_MAX ||
+	    (long long)c->OC * c->KH * c->KW * (c->C / c->groups) > INT32_MAX)
+		CONV_FAIL(SAM3_EINVAL, "conv2d: tensor of more than 2^31 elements");
+	return SAM3_OK;
+#undef CONV_FAIL
+}
+
+static int conv_f32_split_allowed(void)
+{
+	const char *env = getenv("SAM3_HIP_F32_SPLIT");
+	return !(env && atoi(env) == 0);
+}
+
+/* Whether the implicit GEMM (1) or the column matrix + GEMM (2) can run
+ * c: groups 1, f32 only with the split allowed, buffer ranges under 2 GiB
+ * (and for 1: C % 64 == 0, 16-byte aligned x and w). */
+static int conv_implicit_ok(const struct s3k_conv *c)
+{
+	const int f32 = c->kind == SAM3_DTYPE_F32;
+	const long long K = (long long)c->KH * c->KW * c->C;
+	const long long pp = f32 ? 3LL * c->C : c->C;
+	return c->groups == 1 && (!f32 || conv_f32_split_allowed()) && c->C % 64 == 0 &&
+	       !(((uintptr_t)c->x | (uintptr_t)c->w) & 15u) &&
+	       (long long)c->N * c->H * c->W * pp * 2 <= 0x7FFFFFF0LL &&
+	       (long long)c->OC * K * (f32 ? 3 : 1) * 2 <= 0x7FFFFFF0LL;
+}
+
+static int conv_im2col_ok(const struct s3k_conv *c)
+{
+	const int f32 = c->kind == SAM3_DTYPE_F32;
+	const long long M = (long long)c->N * c->OH * c->OW;
+	const long long kp = ((long long)c->KH * c->KW * c->C + 7) / 8 * 8 * (f32 ? 3 : 1);
+	return c->groups == 1 && (!f32 || conv_f32_split_allowed()) && M * kp * 2 <= 0x7FFFFFF0LL &&
+	       (long long)c->OC * kp * 2 <= 0x7FFFFFF0LL && !(((uintptr_t)c->y) & 3u);
+}
+
+/* Kernel choice: 1 implicit GEMM, 2 column matrix + GEMM, 3 direct (also
+ * for problems under 2^22 multiply-adds, where a GEMM launch does not pay). */
+static int conv_path_of(const struct s3k_conv *c)
+{
+	const long long M = (long long)c->N * c->OH * c->OW;
+	const long long K = (long long)c->KH * c->KW * c->C;
+	if (M * c->OC * K < (1LL << 22))
+		return S3H_CONV_DIRECT;
+	if (conv_implicit_ok(c))
+		return S3H_CONV_IMPLICIT;
+	return conv_im2col_ok(c) ? S3H_CONV_IM2COL : S3H_CONV_DIRECT;
+}
+
+static enum sam3_error free_scratch(void *p, void *stream, enum sam3_error err)
+{
+	if (!p)
+		return err;
+	enum sam3_error e = s3h_hip(hipFreeAsync(p, (hipStream_t)stream), "conv2d scratch free");
+	return err != SAM3_OK ? err : e;
+}
+
+/* Conv on device pointers; bias ([OC], the conv's dtype) and GELU are
+ * applied in the GEMM epilogue (paths 1 and 2 only). */
+static enum sam3_error conv_run(struct s3k_conv *c, int path, void *stream)
+{
+	const int f32 = c->kind == SAM3_DTYPE_F32;
+	const int K = c->KH * c->KW * c->C;
+	enum sam3_error err = SAM3_OK;
+	if (path == S3H_CONV_DIRECT) {
+		if (c->flags) {
+			s3h_error("conv2d: the direct kernel has no fused epilogue");
+			return SAM3_EINVAL;
+		}
+		return s3h_hip(s3k_conv_direct(c, stream), "conv2d direct");
+	}
+	if (path == S3H_CONV_IMPLICIT) {
+		if (!f32)
+			return s3h_hip(s3k_conv_implicit(c, c->x, c->w, c->C, stream), "conv2d implicit");
+		const long long pix = (long long)c->N * c->H * c->W;
+		void *xp = NULL, *wp = NULL;
+		err = s3h_scratch_alloc(&xp, (size_t)pix * 3 * c->C * 2, stream);
+		if (err == SAM3_OK)
+			err = s3h_scratch_alloc(&wp, (size_t)c->OC * 3 * K * 2, stream);
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_split3_bf16((const float *)c->x, xp, (int)pix, c->C, c->C, 0, stream),
+				      "conv2d split x");
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_split3_bf16((const float *)c->w, wp, c->OC, K, K, 1, stream),
+				      "conv2d split w");
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_conv_implicit(c, xp, wp, 3 * c->C, stream), "conv2d implicit");
+		return free_scratch(xp, stream, free_scratch(wp, stream, err));
+	}
+	/* path 2: column matrix [M, Kp] (or planes [M, 3Kp]) and the NT GEMM */
+	const int Kp = (K + 7) / 8 * 8, segs = f32 ? 3 : 1;
+	const long long M = (long long)c->N * c->OH * c->OW;
+	void *col = NULL, *wq = NULL;
+	err = s3h_scratch_alloc(&col, (size_t)M * Kp * segs * 2, stream);
+	if (err == SAM3_OK)
+		err = s3h_scratch_alloc(&wq, (size_t)c->OC * Kp * segs * 2, stream);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_conv_im2col(c, col, Kp, stream), "conv2d im2col");
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_conv_wprep(c->kind, c->w, wq, c->OC, K, Kp, stream), "conv2d weight");
+	if (err == SAM3_OK) {
+		struct s3k_gemm g;
+		memset(&g, 0, sizeof(g));
+		g.a = col;
+		g.b = wq;
+		g.c = c->y;
+		g.bias = c->bias;
+		g.M = (int)M;
+		g.N = c->OC;
+		g.K = Kp * segs;
+		g.lda = g.ldb = Kp * segs;
+		g.ldc = c->OC;
+		g.batch = 1;
+		g.a_kind = g.b_kind = f32 ? S3K_BF16 : c->kind;
+		g.c_kind = c->kind;
+		g.flags = S3K_B_NT | (c->flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
+		err = s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_MFMA, stream), "conv2d gemm");
+	}
+	return free_scratch(col, stream, free_scratch(wq, stream, err));
+}
+
+int s3h_conv2d_ok(const struct sam3_node *node)
+{
+	struct s3k_conv c;
+	return conv_shape(node, &c, 1) == SAM3_OK;
+}
+
+int s3h_conv2d_path(const struct sam3_node *node)
+{
+	struct s3k_conv c;
+	return conv_shape(node, &c, 1) == SAM3_OK ? conv_path_of(&c) : 0;
+}
+
+enum sam3_error s3h_conv2d(const struct sam3_node *node, const void *bias, int flags, int path,
+			   void *stream)
+{
+	struct s3k_conv c;
+	enum sam3_error err = conv_shape(node, &c, 0);
+	if (err != SAM3_OK)
+		return err;
+	if (path == 0)
+		path = conv_path_of(&c);
+	if (path < S3H_CONV_IMPLICIT || path > S3H_CONV_DIRECT ||
+	    (path == S3H_CONV_IMPLICIT && !conv_implicit_ok(&c)) ||
+	    (path == S3H_CONV_IM2COL && !conv_im2col_ok(&c))) {
+		s3h_error("conv2d: path %d cannot run this problem", path);
+		return SAM3_EINVAL;
+	}
+	c.bias = bias;
+	c.flags = flags & (S3K_EPI_BIAS | S3K_EPI_GELU);
+	if ((c.flags & S3K_EPI_BIAS) && !bias) {
+		s3h_error("conv2d: NULL bias");
+		return SAM3_EINVAL;
+	}
+	return conv_run(&c, path, stream);
+}
+
+enum sam3_error sam3_hip_kernel_conv2d(const struct sam3_node *node, void *stream)
+{
+	return s3h_conv2d(node, NULL, 0, 0, stream);
+}
+
+enum sam3_error sam3_hip_conv2d_on_path(int path, const struct sam3_node *node, void *stream)
+{
+	return s3h_conv2d(node, NULL, 0, path, stream);
+}
+
+int sam3_hip_conv2d_path(const struct sam3_node *node)
+{
+	return s3h_conv2d_path(node);
+}
+
+/* BIAS_ADD (cpu_bias_add.c:65-101, :150-190): x [.., C] + bias [C], F32
+ * and BF16 in the reference; F16 as well here. */
+int s3h_bias_add_ok(const struct sam3_node *node)
+{
+	if (!node || node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] || !node->output)
+		return 0;
+	const struct sam3_tensor *x = node->inputs[0], *b = node->inputs[1];
+	if (!is_float_dtype(x->dtype) || b->dtype != x->dtype || node->output->dtype != x->dtype ||
+	    x->n_dims < 1 || s3h_nelems(node->output) != s3h_nelems(x))
+		return 0;
+	const int C = x->dims[x->n_dims - 1];
+	return C > 0 && s3h_nelems(b) == C;
+}
+
+enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream)
+{
+	if (!node || node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] || !node->output) {
+		s3h_error("bias_add: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *x = node->inputs[0];
+	if (!is_float_dtype(x->dtype) || node->inputs[1]->dtype != x->dtype) {
+		s3h_error("bias_add: x and bias must share one of F32/F16/BF16");
+		return SAM3_EDTYPE;
+	}
+	if (!s3h_bias_add_ok(node)) {
+		s3h_error("bias_add: bias must have the last dim's size, output the input's");
+		return SAM3_EINVAL;
+	}
+	const int C = x->dims[x->n_dims - 1];
+	return s3h_hip(s3k_bias_add(x->dtype, x->data, node->inputs[1]->data, node->output->data,
+				    s3h_nelems(x) / C, C, stream),
+		       "bias_add");
+}
+
+enum sam3_error sam3_hip_kernel_bias_add(const struct sam3_node *node, void *stream)
+{
+	return s3h_bias_add(node, stream);
+}
+
 enum sam3_error sam3_hip_kernel_layernorm(const struct sam3_node *node, void *stream)
 {
 	return node ? s3h_layernorm(node, stream) : (s3h_error("layernorm: NULL node"), SAM3_EINVAL);
@@ -1045,6 +1311,14 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 	case SAM3_OP_SLICE:
 		if (s3h_dtype_size(dtype))
 			return s3h_slice(node, stream);
+		break;
+	case SAM3_OP_CONV2D:
+		if (is_float_dtype(dtype))
+			return s3h_conv2d(node, NULL, 0, 0, stream);
+		break;
+	case SAM3_OP_BIAS_ADD:
+		if (is_float_dtype(dtype))
+			return s3h_bias_add(node, stream);
 		break;
 	default:
 		break;

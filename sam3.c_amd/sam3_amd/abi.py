@@ -32,7 +32,7 @@ F32, F16, BF16, I32, I8, Q8_0 = range(6)
 OP_NONE, OP_MATMUL, OP_ADD, OP_MUL, OP_SOFTMAX, OP_RELU, OP_GELU = range(7)
 OP_LAYERNORM, OP_CONV2D, OP_RESHAPE, OP_TRANSPOSE, OP_CAST = range(7, 12)
 OP_CONCAT, OP_SLICE, OP_EMBED, OP_SIGMOID, OP_UPSAMPLE, OP_ROPE = range(12, 18)
-OP_SDPA = 21
+OP_SILU, OP_CONV_TRANSPOSE2D, OP_MAXPOOL2D, OP_SDPA, OP_BIAS_ADD = range(18, 23)
 
 
 class Tensor(C.Structure):

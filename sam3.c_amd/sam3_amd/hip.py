@@ -35,6 +35,10 @@ SIGNATURES = {
     "sam3_hip_kernel_matmul_bf16": (_i, [_vp, _vp]),
     "sam3_hip_kernel_matmul_q8": (_i, [_vp, _vp]),
     "sam3_hip_kernel_sdpa": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_conv2d": (_i, [_vp, _vp]),
+    "sam3_hip_conv2d_path": (_i, [_vp]),
+    "sam3_hip_conv2d_on_path": (_i, [_i, _vp, _vp]),
+    "sam3_hip_kernel_bias_add": (_i, [_vp, _vp]),
     "sam3_hip_kernel_layernorm": (_i, [_vp, _vp]),
     "sam3_hip_kernel_rope": (_i, [_vp, _vp]),
     "sam3_hip_kernel_slice": (_i, [_vp, _vp]),

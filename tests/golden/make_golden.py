@@ -193,6 +193,27 @@ def main():
     g["rope_sin"] = np.sin(ang).astype(np.float32)
     g["rope_out"] = R.rope(g["rope_x"], g["rope_cos"], g["rope_sin"], "f32")
 
+    # -- Conv2D NHWC x OHWI (cpu_conv2d.c): 3x3 pad 1; stride 2 with 2
+    # groups; the patch embedding's non-overlapping 4x4 stride 4 on C = 3;
+    # asymmetric padding; bf16 and f16 twins of the first case
+    conv_cases = {"p1": ((1, 9, 7, 8), (6, 3, 3, 8), 1, 1, 0, 1),
+                  "s2g2": ((2, 10, 10, 6), (4, 3, 3, 3), 2, 1, 0, 2),
+                  "patch": ((1, 12, 12, 3), (16, 4, 4, 3), 4, 0, 0, 1),
+                  "asym": ((1, 9, 9, 8), (4, 3, 3, 8), 1, 2, 1, 1)}
+    for i, (key, (xs, ws, st, ph, pw, gr)) in enumerate(conv_cases.items()):
+        x = synth.randn(synth.tensor_seed(90 + i, 0), xs)
+        w = synth.randn(synth.tensor_seed(90 + i, 1), ws, 0.2)
+        rc, y = R.conv2d(x, w, st, ph, pw if pw else None, gr)
+        assert rc == 0
+        g[f"conv_{key}_x"], g[f"conv_{key}_w"], g[f"conv_{key}_y"] = x, w, y
+        g[f"conv_{key}_p"] = np.array([st, ph, gr, pw], np.int32)
+    x, w = g["conv_p1_x"], g["conv_p1_w"]
+    for kind, cv in (("bf16", bf16_bits), ("f16", fp16_bits)):
+        xb, wb = cv(R, x), cv(R, w)
+        rc, y = R.conv2d(xb, wb, 1, 1, None, 1, kind)
+        assert rc == 0
+        g[f"conv_p1_{kind}_x"], g[f"conv_p1_{kind}_w"], g[f"conv_p1_{kind}_y"] = xb, wb, y
+
     R.close()
     out = HERE / "matmul_golden.npz"
     np.savez_compressed(out, **g)

@@ -214,6 +214,27 @@ Oracle.layernorm = _oracle_layernorm
 Oracle.rope = _oracle_rope
 
 
+def _oracle_conv2d(self, x, w, stride=1, ph=0, pw=None, groups=1, kind="f32", out_hw=None,
+                   threads=8):
+    """x [N,H,W,C], w [OC,KH,KW,C/groups] (f32 arrays, or uint16 bits for
+    bf16/f16) -> y [N,OH,OW,OC]."""
+    pw = ph if pw is None else pw
+    N, H, W, C = x.shape
+    OC, KH, KW, _ = w.shape
+    OH, OW = out_hw or ((H + 2 * ph - KH) // stride + 1, (W + 2 * pw - KW) // stride + 1)
+    dt = np.float32 if kind == "f32" else np.uint16
+    x, w = _c(x, dt), _c(w, dt)
+    y = np.zeros((N, OH, OW, OC), dt)
+    fn = getattr(self.lib, f"oracle_conv2d_{kind}")
+    fn.argtypes = [_vp, _vp, _vp] + [_i] * 14
+    fn(_ptr(x), _ptr(w), _ptr(y), N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW,
+       threads)
+    return y
+
+
+Oracle.conv2d = _oracle_conv2d
+
+
 class Ref:
     """The reference's own kernels, called through hand-built nodes."""
 
@@ -283,6 +304,36 @@ class Ref:
         else:
             rc = getattr(self.lib, fn)(C.byref(node), self.pool(threads))
         return rc, out
+
+    def conv2d(self, x, w, stride=1, ph=0, pw=None, groups=1, kind="f32", out_hw=None,
+               threads=8):
+        """cpu_dispatch_node on a CONV2D node (cpu_conv2d.c:296-435 and its
+        twins) with a real scratch arena for the column matrix."""
+        N, H, W, Cin = x.shape
+        OC, KH, KW, KIC = w.shape
+        p_w = ph if pw is None else pw
+        OH, OW = out_hw or ((H + 2 * ph - KH) // stride + 1, (W + 2 * p_w - KW) // stride + 1)
+        dt = {"f32": abi.F32, "bf16": abi.BF16, "f16": abi.F16}[kind]
+        npt = np.float32 if kind == "f32" else np.uint16
+        arena = _ArenaC()
+        self.lib.sam3_arena_init.argtypes = [C.POINTER(_ArenaC), C.c_size_t]
+        self.lib.sam3_arena_free.argtypes = [C.POINTER(_ArenaC)]
+        need = OH * OW * KH * KW * KIC * 4 + KH * KW * KIC * OC * 4 + 64 * 8 * OC * 4 + (1 << 20)
+        assert self.lib.sam3_arena_init(C.byref(arena), need) == 0
+        try:
+            keep = []
+            xa, wa = _c(x, npt), _c(w, npt)
+            tx = abi.make_tensor(dt, [N, H, W, Cin], xa.ctypes.data, xa.nbytes)
+            tw = abi.make_tensor(dt, [OC, KH, KW, KIC], wa.ctypes.data, wa.nbytes)
+            y = np.zeros((N, OH, OW, OC), npt)
+            ty = abi.make_tensor(dt, [N, OH, OW, OC], y.ctypes.data, y.nbytes)
+            keep += [xa, wa, tx, tw, ty]
+            node = abi.make_node(abi.OP_CONV2D, [tx, tw], ty,
+                                 (stride, ph, groups, 0 if pw is None else pw))
+            rc = self.lib.cpu_dispatch_node(C.byref(node), C.byref(arena), self.pool(threads))
+        finally:
+            self.lib.sam3_arena_free(C.byref(arena))
+        return rc, y
 
     def matmul_f32(self, a, b, threads=None):
         (M, K), N = a.shape, b.shape[1]
@@ -419,6 +470,11 @@ Ref.permute = _ref_permute
 
 def have_ref():
     return REF_SO.exists()
+
+
+class _ArenaC(C.Structure):
+    """struct sam3_arena (src/core/alloc.h)."""
+    _fields_ = [("base", _vp), ("size", C.c_size_t), ("offset", C.c_size_t), ("skip_data", _i)]
 
 
 # ---- the reference's .sam3 container (src/core/weight.{h,c}) ----

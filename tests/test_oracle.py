@@ -359,3 +359,80 @@ def test_rope_closed_forms(O):
     y = O.rope(x, np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)).astype(np.float64)
     n0 = np.hypot(x[..., 0::2].astype(np.float64), x[..., 1::2])
     assert np.allclose(np.hypot(y[..., 0::2], y[..., 1::2]), n0, rtol=1e-6)
+
+
+# ---- Conv2D (cpu_conv2d.c and its 16-bit twins) ----
+
+CONV_KEYS = ("p1", "s2g2", "patch", "asym")
+
+
+@pytest.mark.parametrize("key", CONV_KEYS)
+def test_golden_conv2d(O, key):
+    x, w, y = GOLD[f"conv_{key}_x"], GOLD[f"conv_{key}_w"], GOLD[f"conv_{key}_y"]
+    st, ph, gr, pw = (int(v) for v in GOLD[f"conv_{key}_p"])
+    got = O.conv2d(x, w, st, ph, pw if pw else None, gr, out_hw=y.shape[1:3], threads=3)
+    assert np.array_equal(bits32(got), bits32(y))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+def test_golden_conv2d_16bit(O, kind):
+    x, w, y = (GOLD[f"conv_p1_{kind}_{t}"] for t in "xwy")
+    assert np.array_equal(O.conv2d(x, w, 1, 1, kind=kind), y)
+
+
+@pytest.mark.parametrize("shape", [((1, 9, 7, 8), (6, 3, 3, 8), 1, 1, 1),
+                                   ((2, 10, 10, 6), (4, 3, 3, 3), 2, 1, 2),
+                                   ((1, 28, 28, 3), (16, 14, 14, 3), 14, 0, 1),
+                                   ((1, 5, 5, 4), (4, 1, 1, 1), 1, 0, 4),
+                                   ((1, 8, 8, 64), (32, 3, 3, 64), 1, 1, 1)],
+                         ids=["p1", "s2g2", "patch14", "depthwise", "c64"])
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
+def test_ref_conv2d(O, R, shape, kind):
+    xs, ws, st, ph, gr = shape
+    x, w = synth.randn(101, xs), synth.randn(102, ws, 0.2)
+    if kind != "f32":
+        cv = O.f32_to_bf16 if kind == "bf16" else O.f32_to_fp16
+        x, w = cv(x).reshape(xs), cv(w).reshape(ws)
+    rc, y = R.conv2d(x, w, st, ph, None, gr, kind)
+    assert rc == 0
+    assert np.array_equal(O.conv2d(x, w, st, ph, groups=gr, kind=kind).view(np.uint8),
+                          y.view(np.uint8))
+
+
+def conv_f64(x, w, stride, ph, pw, groups):
+    """Direct float64 convolution (definition of NHWC x OHWI)."""
+    x, w = x.astype(np.float64), w.astype(np.float64)
+    N, H, W, C = x.shape
+    OC, KH, KW, cg = w.shape
+    OH, OW = (H + 2 * ph - KH) // stride + 1, (W + 2 * pw - KW) // stride + 1
+    xp = np.zeros((N, H + 2 * ph, W + 2 * pw, C))
+    xp[:, ph:ph + H, pw:pw + W] = x
+    og = OC // groups
+    y = np.zeros((N, OH, OW, OC))
+    for oh in range(OH):
+        for ow in range(OW):
+            patch = xp[:, oh * stride:oh * stride + KH, ow * stride:ow * stride + KW]
+            for g in range(groups):
+                pg = patch[..., g * cg:(g + 1) * cg].reshape(N, -1)
+                wg = w[g * og:(g + 1) * og].reshape(og, -1)
+                y[:, oh, ow, g * og:(g + 1) * og] = pg @ wg.T
+    return y
+
+
+def test_conv2d_closed_forms(O):
+    """A centre-tap identity kernel with padding 1 returns x exactly; a
+    1x1 conv is the matmul of the pixels; stride = kernel patchifies; all
+    match a float64 direct convolution within f32 accumulation error."""
+    x = synth.randn(103, (2, 6, 5, 4))
+    eye = np.zeros((4, 3, 3, 4), np.float32)
+    eye[:, 1, 1, :] = np.eye(4, dtype=np.float32)
+    assert np.array_equal(bits32(O.conv2d(x, eye, 1, 1)), bits32(x))
+    w1 = synth.randn(104, (7, 1, 1, 4))
+    y = O.conv2d(x, w1).astype(np.float64)
+    ref = x.reshape(-1, 4).astype(np.float64) @ w1.reshape(7, 4).T.astype(np.float64)
+    assert np.allclose(y.reshape(-1, 7), ref, rtol=1e-5, atol=1e-6)
+    for (xs, ws, st, ph, pw, gr) in [((1, 12, 12, 3), (5, 4, 4, 3), 4, 0, 0, 1),
+                                     ((1, 7, 9, 6), (6, 3, 3, 2), 2, 1, 2, 3)]:
+        xx, ww = synth.randn(105, xs), synth.randn(106, ws)
+        got = O.conv2d(xx, ww, st, ph, pw, gr).astype(np.float64)
+        assert np.allclose(got, conv_f64(xx, ww, st, ph, pw, gr), rtol=1e-5, atol=1e-5)
