@@ -74,6 +74,8 @@ struct sam3_hip_eval_stats {
 	int cache_hits;    /* inputs found resident from an earlier eval       */
 	int downloads;     /* device -> host copies                            */
 	int mapped_reads;  /* inputs read from a range mapped by map_weights   */
+	int prep_hits;     /* weights whose prepared copy (bf16 planes, padded
+			    * rows) was reused instead of recomputed           */
 };
 void sam3_hip_backend_last_stats(struct sam3_backend *be,
 				 struct sam3_hip_eval_stats *out);

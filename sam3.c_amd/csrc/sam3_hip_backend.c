@@ -59,6 +59,14 @@ struct s3h_res {
 	unsigned char host_valid;
 	unsigned char keep;      /* survives the end of this eval            */
 	unsigned char produced;  /* written by a GPU node in this eval        */
+	unsigned char written;   /* written by a GPU node in any eval         */
+};
+
+/* A prepared copy of a constant weight (s3h_prep_*). */
+struct s3h_prep {
+	const char *src;
+	int tag, rows, k;
+	void *dev;
 };
 
 /* A host range copied to HBM once: [host, host + nbytes) -> dev. */
@@ -78,6 +86,8 @@ struct sam3_hip_backend {
 	int n_blobs, cap_blobs;
 	void **owned; /* device buffers made by fuse_rows */
 	int n_owned, cap_owned;
+	struct s3h_prep *prep;
+	int n_prep, cap_prep;
 	struct s3h_stager stager;
 	char *arena;
 	size_t arena_size, arena_off;
@@ -97,8 +107,25 @@ static struct s3h_res *res_find(struct sam3_hip_backend *hb, const void *host)
 	return NULL;
 }
 
+/* The backend whose graph_eval runs on this thread (prepared weights). */
+static _Thread_local struct sam3_hip_backend *s3h_cur;
+
+/* Drop the prepared copies whose source lies in device range [lo, hi). */
+static void prep_drop_range(struct sam3_hip_backend *hb, const char *lo, const char *hi)
+{
+	for (int i = hb->n_prep - 1; i >= 0; i--) {
+		if (hb->prep[i].src < lo || hb->prep[i].src >= hi)
+			continue;
+		(void)hipFreeAsync(hb->prep[i].dev, hb->stream);
+		hb->prep[i] = hb->prep[hb->n_prep - 1];
+		hb->n_prep--;
+	}
+}
+
 static void res_drop_at(struct sam3_hip_backend *hb, int i)
 {
+	if (hb->res[i].dev)
+		prep_drop_range(hb, hb->res[i].dev, (const char *)hb->res[i].dev + hb->res[i].nbytes);
 	if (hb->res[i].dev)
 		(void)hipFreeAsync(hb->res[i].dev, hb->stream);
 	hb->res[i] = hb->res[hb->n_res - 1];
@@ -155,6 +182,7 @@ static void *blob_addr(const struct sam3_hip_backend *hb, const void *p, size_t 
 
 static void blob_drop_at(struct sam3_hip_backend *hb, int i)
 {
+	prep_drop_range(hb, hb->blobs[i].dev, hb->blobs[i].dev + hb->blobs[i].nbytes);
 	(void)hipStreamSynchronize(hb->stream);
 	(void)hipFree(hb->blobs[i].dev);
 	hb->blobs[i] = hb->blobs[hb->n_blobs - 1];
@@ -245,6 +273,7 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 	e->dev_valid = 1;
 	e->host_valid = 0;
 	e->produced = 1;
+	e->written = 1;
 	e->keep = 1;
 	*out = e->dev;
 	return SAM3_OK;
@@ -642,6 +671,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	}
 	for (int i = 0; i < hb->n_res; i++)
 		hb->res[i].produced = 0;
+	s3h_cur = hb;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -679,6 +709,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	enum sam3_error serr = s3h_hip(hipStreamSynchronize(hb->stream), "graph_eval: sync");
 	if (err == SAM3_OK)
 		err = serr;
+	s3h_cur = NULL;
 	for (int i = hb->n_res - 1; i >= 0; i--)
 		if (!hb->res[i].keep)
 			res_drop_at(hb, i);
@@ -734,6 +765,9 @@ static void hip_free(struct sam3_backend *be)
 	free(hb->owned);
 	hb->owned = NULL;
 	hb->n_owned = hb->cap_owned = 0;
+	free(hb->prep);
+	hb->prep = NULL;
+	hb->n_prep = hb->cap_prep = 0;
 	s3h_stager_free(&hb->stager);
 	if (hb->stream) {
 		(void)hipStreamSynchronize(hb->stream);
@@ -1050,5 +1084,64 @@ enum sam3_error sam3_hip_backend_fuse_rows(struct sam3_backend *be,
 	}
 	out->data = dev;
 	out->nbytes = total;
+	return SAM3_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* Prepared weights                                                     */
+/* ------------------------------------------------------------------ */
+void *s3h_prep_find(const void *src, int tag, int rows, int k)
+{
+	struct sam3_hip_backend *hb = s3h_cur;
+	if (!hb)
+		return NULL;
+	for (int i = 0; i < hb->n_prep; i++) {
+		const struct s3h_prep *p = &hb->prep[i];
+		if (p->src == (const char *)src && p->tag == tag && p->rows == rows && p->k == k) {
+			hb->stats.prep_hits++;
+			return p->dev;
+		}
+	}
+	return NULL;
+}
+
+int s3h_prep_cacheable(const void *src, size_t src_bytes)
+{
+	const struct sam3_hip_backend *hb = s3h_cur;
+	const char *c = (const char *)src;
+	if (!hb || !c)
+		return 0;
+	for (int i = 0; i < hb->n_blobs; i++) {
+		const struct s3h_blob *b = &hb->blobs[i];
+		if (c >= b->dev && c < b->dev + b->nbytes && src_bytes <= b->nbytes - (size_t)(c - b->dev))
+			return 1;
+	}
+	for (int i = 0; i < hb->n_res; i++) {
+		const struct s3h_res *e = &hb->res[i];
+		const char *d = (const char *)e->dev;
+		if (d && c >= d && c < d + e->nbytes && src_bytes <= e->nbytes - (size_t)(c - d))
+			return e->keep && !e->written && e->dev_valid;
+	}
+	return 0;
+}
+
+enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev)
+{
+	struct sam3_hip_backend *hb = s3h_cur;
+	if (!hb) {
+		s3h_error("prepared weight: no graph_eval running");
+		return SAM3_EINVAL;
+	}
+	if (hb->n_prep == hb->cap_prep) {
+		int cap = hb->cap_prep ? hb->cap_prep * 2 : 32;
+		struct s3h_prep *p = realloc(hb->prep, (size_t)cap * sizeof(*p));
+		if (!p) {
+			s3h_error("prepared weight: out of host memory");
+			return SAM3_ENOMEM;
+		}
+		hb->prep = p;
+		hb->cap_prep = cap;
+	}
+	hb->prep[hb->n_prep++] = (struct s3h_prep){(const char *)src, tag, rows, k, dev};
 	return SAM3_OK;
 }

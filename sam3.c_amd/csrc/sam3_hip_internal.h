@@ -50,6 +50,20 @@ enum sam3_error s3h_conv2d(const struct sam3_node *node, const void *bias, int f
 int s3h_bias_add_ok(const struct sam3_node *node);
 enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
 
+/* Prepared copies of constant weights (bf16 hi/lo planes, padded rows),
+ * kept by the backend whose graph_eval is running on this thread. A copy
+ * is keyed by the source's device address, the preparation (tag) and its
+ * shape; it is kept only when the source lies in memory the backend knows
+ * to be constant (a mapped weight range, or an uploaded input that no
+ * node writes), and dropped with that memory. Outside graph_eval nothing
+ * is cached. */
+enum { S3H_PREP_SPLIT_W = 1,   /* f32 [rows, k] -> bf16 [rows, 3k] = [hi|hi|lo] */
+       S3H_PREP_PAD_PLANES,    /* f32 [rows, K] -> bf16 [rows, 3k] over k >= K, zero padded */
+       S3H_PREP_PAD16 };       /* 16-bit [rows, K] -> [rows, k], zero padded */
+void *s3h_prep_find(const void *src, int tag, int rows, int k);
+int s3h_prep_cacheable(const void *src, size_t src_bytes);
+enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev);
+
 /* Bulk host -> device copies through pinned staging buffers (upload.c).
  * Lanes and chunk size default to S3H_STAGE_LANES x S3H_STAGE_CHUNK_MB;
  * SAM3_HIP_UPLOAD_LANES / SAM3_HIP_UPLOAD_CHUNK_MB override them. */

@@ -238,20 +238,64 @@ static int f32_split_wanted(const struct s3k_gemm *g)
 	       (long long)g->M * g->N * g->K >= (1LL << 24);
 }
 
+/* A prepared copy of weight w (rows x k source elements of 4 or 2 bytes)
+ * in the layout `tag` with pitch k_out: from the backend's cache when it
+ * holds one, else made by fn into new scratch, which is kept in the cache
+ * when w is a constant weight (*own = 0) or is the caller's to free
+ * (*own = 1). */
+typedef int (*prep_fn)(const void *w, void *out, int rows, int k, int k_out, int kind,
+		       void *stream);
+static enum sam3_error prep_weight(const void *w, size_t w_bytes, int tag, int rows, int k, int k_out,
+				   size_t out_bytes, int kind, prep_fn fn, void *stream, void **out,
+				   int *own)
+{
+	*own = 0;
+	*out = s3h_prep_find(w, tag, rows, k_out);
+	if (*out)
+		return SAM3_OK;
+	enum sam3_error err = s3h_scratch_alloc(out, out_bytes, stream);
+	if (err == SAM3_OK)
+		err = s3h_hip(fn(w, *out, rows, k, k_out, kind, stream), "weight preparation");
+	if (err == SAM3_OK && s3h_prep_cacheable(w, w_bytes)) {
+		err = s3h_prep_store(w, tag, rows, k_out, *out);
+		*own = err != SAM3_OK;
+	} else {
+		*own = 1;
+	}
+	return err;
+}
+
+static int prep_split_w(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
+{
+	(void)k_out;
+	(void)kind;
+	return s3k_split3_bf16((const float *)w, out, rows, k, k, 1, stream);
+}
+
+static int prep_conv_w(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
+{
+	return s3k_conv_wprep(kind, w, out, rows, k, k_out, stream);
+}
+
 static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, void *stream)
 {
 	const hipStream_t st = (hipStream_t)stream;
 	const size_t abytes = (size_t)g->M * 3 * g->K * 2, bbytes = (size_t)g->N * 3 * g->K * 2;
 	void *a3 = NULL, *b3 = NULL;
+	int own_b = 1;
 	enum sam3_error err = s3h_scratch_alloc(&a3, abytes, stream);
-	if (err == SAM3_OK)
-		err = s3h_scratch_alloc(&b3, bbytes, stream);
 	if (err == SAM3_OK)
 		err = s3h_hip(s3k_split3_bf16((const float *)g->a, a3, g->M, g->K, g->lda, 0, stream),
 			      "matmul f32 split A");
-	if (err == SAM3_OK)
-		err = s3h_hip(s3k_split3_bf16((const float *)g->b, b3, g->N, g->K, g->ldb, 1, stream),
-			      "matmul f32 split W");
+	if (err == SAM3_OK && g->ldb == g->K)
+		err = prep_weight(g->b, (size_t)g->N * g->K * 4, S3H_PREP_SPLIT_W, g->N, g->K, g->K,
+				  bbytes, S3K_F32, prep_split_w, stream, &b3, &own_b);
+	else if (err == SAM3_OK) {
+		err = s3h_scratch_alloc(&b3, bbytes, stream);
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_split3_bf16((const float *)g->b, b3, g->N, g->K, g->ldb, 1, stream),
+				      "matmul f32 split W");
+	}
 	if (err == SAM3_OK) {
 		struct s3k_gemm h = *g;
 		h.a = a3;
@@ -262,7 +306,7 @@ static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, void *stream)
 		err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream), "matmul f32 split gemm");
 	}
 	enum sam3_error ferr = SAM3_OK;
-	if (b3)
+	if (b3 && own_b)
 		ferr = s3h_hip(hipFreeAsync(b3, st), "matmul f32 split scratch free");
 	if (a3) {
 		enum sam3_error e2 = s3h_hip(hipFreeAsync(a3, st), "matmul f32 split scratch free");
@@ -1016,30 +1060,30 @@ static enum sam3_error conv_run(struct s3k_conv *c, int path, void *stream)
 			return s3h_hip(s3k_conv_implicit(c, c->x, c->w, c->C, stream), "conv2d implicit");
 		const long long pix = (long long)c->N * c->H * c->W;
 		void *xp = NULL, *wp = NULL;
+		int own_w = 0;
 		err = s3h_scratch_alloc(&xp, (size_t)pix * 3 * c->C * 2, stream);
 		if (err == SAM3_OK)
-			err = s3h_scratch_alloc(&wp, (size_t)c->OC * 3 * K * 2, stream);
+			err = prep_weight(c->w, (size_t)c->OC * K * 4, S3H_PREP_SPLIT_W, c->OC, K, K,
+					  (size_t)c->OC * 3 * K * 2, S3K_F32, prep_split_w, stream, &wp, &own_w);
 		if (err == SAM3_OK)
 			err = s3h_hip(s3k_split3_bf16((const float *)c->x, xp, (int)pix, c->C, c->C, 0, stream),
 				      "conv2d split x");
 		if (err == SAM3_OK)
-			err = s3h_hip(s3k_split3_bf16((const float *)c->w, wp, c->OC, K, K, 1, stream),
-				      "conv2d split w");
-		if (err == SAM3_OK)
 			err = s3h_hip(s3k_conv_implicit(c, xp, wp, 3 * c->C, stream), "conv2d implicit");
-		return free_scratch(xp, stream, free_scratch(wp, stream, err));
+		return free_scratch(xp, stream, free_scratch(own_w ? wp : NULL, stream, err));
 	}
 	/* path 2: column matrix [M, Kp] (or planes [M, 3Kp]) and the NT GEMM */
 	const int Kp = (K + 7) / 8 * 8, segs = f32 ? 3 : 1;
 	const long long M = (long long)c->N * c->OH * c->OW;
 	void *col = NULL, *wq = NULL;
+	int own_w = 0;
 	err = s3h_scratch_alloc(&col, (size_t)M * Kp * segs * 2, stream);
 	if (err == SAM3_OK)
-		err = s3h_scratch_alloc(&wq, (size_t)c->OC * Kp * segs * 2, stream);
+		err = prep_weight(c->w, (size_t)c->OC * K * (f32 ? 4 : 2),
+				  f32 ? S3H_PREP_PAD_PLANES : S3H_PREP_PAD16, c->OC, K, Kp,
+				  (size_t)c->OC * Kp * segs * 2, c->kind, prep_conv_w, stream, &wq, &own_w);
 	if (err == SAM3_OK)
 		err = s3h_hip(s3k_conv_im2col(c, col, Kp, stream), "conv2d im2col");
-	if (err == SAM3_OK)
-		err = s3h_hip(s3k_conv_wprep(c->kind, c->w, wq, c->OC, K, Kp, stream), "conv2d weight");
 	if (err == SAM3_OK) {
 		struct s3k_gemm g;
 		memset(&g, 0, sizeof(g));
@@ -1058,7 +1102,7 @@ static enum sam3_error conv_run(struct s3k_conv *c, int path, void *stream)
 		g.flags = S3K_B_NT | (c->flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
 		err = s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_MFMA, stream), "conv2d gemm");
 	}
-	return free_scratch(col, stream, free_scratch(wq, stream, err));
+	return free_scratch(col, stream, free_scratch(own_w ? wq : NULL, stream, err));
 }
 
 int s3h_conv2d_ok(const struct sam3_node *node)

@@ -191,3 +191,49 @@ def test_fuse_rows_errors():
         assert be.fuse_rows([], out) == abi.EINVAL
     finally:
         be.close()
+
+
+def test_prepared_weights_reused_and_dropped():
+    """The bf16 planes of constant f32 weights are made once per backend:
+    a second eval reuses them (prep_hits) with identical bits, and
+    cache_invalidate of one weight's host range drops its planes, so the
+    next eval uses the new values (equal to a fresh backend's result)."""
+    from test_gpu_blockops import block_weights
+    grid, window, e, heads, mlp = 16, 8, 256, 4, 1024
+
+    def build():
+        G = graph.Graph()
+        x = G.tensor(abi.F32, (grid * grid, e), synth.randn(70, (grid * grid, e)), ephemeral=1)
+        p = block_weights(G, 170, e, mlp)
+        c, s = graph.rope_tables(window, e // heads)
+        tc, ts = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s.shape, s)
+        return G, p, graph.vit_block(G, x, p, heads, grid, window, False, tc, ts)
+
+    G, p, out = build()
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G.g) == abi.OK
+        y1, st1 = out_array(out, (grid * grid, e)), be.stats()
+        assert be.graph_eval(G.g) == abi.OK
+        y2, st2 = out_array(out, (grid * grid, e)), be.stats()
+        w = p["fc2_w"]
+        wa = np.ctypeslib.as_array(C.cast(w.data, C.POINTER(C.c_float)), shape=(e * mlp,))
+        wa *= 2.0
+        be.cache_invalidate(w.data, w.nbytes)
+        assert be.graph_eval(G.g) == abi.OK
+        y3, st3 = out_array(out, (grid * grid, e)), be.stats()
+    finally:
+        be.close()
+    assert st1.prep_hits == 0 and st2.prep_hits == 4 and st3.prep_hits == 3
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    assert not np.array_equal(y2, y3)
+    G4, p4, out4 = build()
+    wa4 = np.ctypeslib.as_array(C.cast(p4["fc2_w"].data, C.POINTER(C.c_float)), shape=(e * mlp,))
+    wa4 *= 2.0
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G4.g) == abi.OK
+        y4 = out_array(out4, (grid * grid, e))
+    finally:
+        be.close()
+    assert np.array_equal(y3.view(np.uint32), y4.view(np.uint32))
