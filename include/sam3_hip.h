@@ -76,6 +76,8 @@ struct sam3_hip_eval_stats {
 	int mapped_reads;  /* inputs read from a range mapped by map_weights   */
 	int prep_hits;     /* weights whose prepared copy (bf16 planes, padded
 			    * rows) was reused instead of recomputed           */
+	int operand_writes; /* LAYERNORM outputs written straight in the form
+			     * their one consuming GEMM reads (not kept)      */
 };
 void sam3_hip_backend_last_stats(struct sam3_backend *be,
 				 struct sam3_hip_eval_stats *out);

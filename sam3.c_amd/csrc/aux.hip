@@ -262,11 +262,8 @@ __global__ void __launch_bounds__(256) split3_bf16_k(const float *src, uint16_t 
 	const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 	uint32_t hi[4], lo[4];
 #pragma unroll
-	for (int i = 0; i < 4; ++i) {
-		hi[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-		lo[i] = pack_bf16x2(x[2 * i] - __uint_as_float(hi[i] << 16),
-				    x[2 * i + 1] - __uint_as_float(hi[i] & 0xFFFF0000u));
-	}
+	for (int i = 0; i < 4; ++i)
+		split_bf16x2(x[2 * i], x[2 * i + 1], hi[i], lo[i]);
 	const uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]);
 	const uint4 L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
 	uint16_t *d = dst + r * 3LL * K + k0;

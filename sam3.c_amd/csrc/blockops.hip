@@ -54,10 +54,11 @@ __device__ __forceinline__ float bo_wave_sum(float v)
 /* One wave per row; element j of the row is held by lane j % 64 in slot
  * j / 64 (EPL slots cover cols <= 64 * EPL). EPL = 0: rows of any length,
  * re-read from memory in each pass. */
-template <int DT, int EPL>
+template <int DT, int EPL, int OUTF>
 __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *gamma,
 						   const void *beta, void *out, int rows, int cols)
 {
+	static_assert(OUTF == S3K_LN_SAME || DT == S3K_F32, "operand formats are made from f32");
 	const int lane = threadIdx.x & 63;
 	const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
 	if (row >= rows)
@@ -99,7 +100,18 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 			val = mul_rn(val, bo_ld<DT>(gamma, j));
 		if (beta)
 			val = add_rn(val, bo_ld<DT>(beta, j));
-		bo_st<DT>(out, base + j, val);
+		if constexpr (OUTF == S3K_LN_SAME) {
+			bo_st<DT>(out, base + j, val);
+		} else if constexpr (OUTF == S3K_LN_PLANES) {
+			uint32_t hi, lo;
+			split_bf16x2(val, 0.0f, hi, lo);
+			uint16_t *d = (uint16_t *)out + row * 3LL * cols + j;
+			d[0] = (uint16_t)hi;
+			d[cols] = (uint16_t)lo;
+			d[2LL * cols] = (uint16_t)hi;
+		} else {
+			((uint16_t *)out)[base + j] = (uint16_t)f32_to_f16(val);
+		}
 	};
 	if constexpr (EPL > 0) {
 #pragma unroll
@@ -111,6 +123,106 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 	} else {
 		for (int j = lane; j < cols; j += 64)
 			finish(j, bo_ld<DT>(x, base + j));
+	}
+}
+
+/* 16 bytes of a row as f32: 4 f32 or 8 bf16/f16 values. */
+template <int DT>
+__device__ __forceinline__ void bo_ld16(const void *p, long long i, float *v)
+{
+	if constexpr (DT == S3K_F32) {
+		const float4 a = *(const float4 *)((const float *)p + i);
+		v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+	} else {
+		const uint4 a = *(const uint4 *)((const uint16_t *)p + i);
+		const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+		for (int e = 0; e < 4; ++e) {
+			v[2 * e] = DT == S3K_BF16 ? bf16_to_f32(w[e] & 0xFFFFu) : f16_to_f32(w[e] & 0xFFFFu);
+			v[2 * e + 1] = DT == S3K_BF16 ? bf16_to_f32(w[e] >> 16) : f16_to_f32(w[e] >> 16);
+		}
+	}
+}
+
+template <int DT>
+__device__ __forceinline__ void bo_st16(void *p, long long i, const float *v)
+{
+	if constexpr (DT == S3K_F32) {
+		*(float4 *)((float *)p + i) = make_float4(v[0], v[1], v[2], v[3]);
+	} else {
+		uint32_t h[8];
+#pragma unroll
+		for (int e = 0; e < 8; ++e)
+			h[e] = DT == S3K_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+		*(uint4 *)((uint16_t *)p + i) = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16),
+							   h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+	}
+}
+
+/* The same LayerNorm with 16-byte accesses: rows of cols = SLOTS * 64 * VEC
+ * elements, lane l holding elements (64 s + l) * VEC .. + VEC - 1 of each
+ * slot s; the sums are taken in the same per-lane-then-wave order. */
+template <int DT, int SLOTS, int OUTF>
+__global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *gamma,
+						   const void *beta, void *out, int rows, int cols)
+{
+	static_assert(OUTF == S3K_LN_SAME || DT == S3K_F32, "operand formats are made from f32");
+	constexpr int VEC = DT == S3K_F32 ? 4 : 8;
+	const int lane = threadIdx.x & 63;
+	const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (row >= rows)
+		return;
+	const long long base = row * cols;
+	float v[SLOTS][VEC];
+	float sum = 0.0f;
+#pragma unroll
+	for (int i = 0; i < SLOTS; ++i) {
+		bo_ld16<DT>(x, base + (long long)(i * 64 + lane) * VEC, v[i]);
+#pragma unroll
+		for (int e = 0; e < VEC; ++e)
+			sum += v[i][e];
+	}
+	const float mean = bo_wave_sum(sum) / (float)cols;
+	float var = 0.0f;
+#pragma unroll
+	for (int i = 0; i < SLOTS; ++i)
+#pragma unroll
+		for (int e = 0; e < VEC; ++e) {
+			const float d = sub_rn(v[i][e], mean);
+			var = fmaf(d, d, var);
+		}
+	const float inv_std = 1.0f / sqrtf(bo_wave_sum(var) / (float)cols + 1e-5f);
+#pragma unroll
+	for (int i = 0; i < SLOTS; ++i) {
+		const int j0 = (i * 64 + lane) * VEC;
+		float g[VEC], b[VEC];
+		if (gamma)
+			bo_ld16<DT>(gamma, j0, g);
+		if (beta)
+			bo_ld16<DT>(beta, j0, b);
+#pragma unroll
+		for (int e = 0; e < VEC; ++e) {
+			float val = mul_rn(sub_rn(v[i][e], mean), inv_std);
+			if (gamma)
+				val = mul_rn(val, g[e]);
+			if (beta)
+				val = add_rn(val, b[e]);
+			v[i][e] = val;
+		}
+		if constexpr (OUTF == S3K_LN_SAME) {
+			bo_st16<DT>(out, base + j0, v[i]);
+		} else if constexpr (OUTF == S3K_LN_PLANES) {
+			uint32_t hi[2], lo[2];
+			split_bf16x2(v[i][0], v[i][1], hi[0], lo[0]);
+			split_bf16x2(v[i][2], v[i][3], hi[1], lo[1]);
+			uint16_t *d = (uint16_t *)out + row * 3LL * cols + j0;
+			*(uint2 *)d = make_uint2(hi[0], hi[1]);
+			*(uint2 *)(d + cols) = make_uint2(lo[0], lo[1]);
+			*(uint2 *)(d + 2LL * cols) = make_uint2(hi[0], hi[1]);
+		} else {
+			*(uint2 *)((uint16_t *)out + base + j0) =
+				make_uint2(pack_f16x2(v[i][0], v[i][1]), pack_f16x2(v[i][2], v[i][3]));
+		}
 	}
 }
 
@@ -170,21 +282,35 @@ static void launch_perm(const PermArgs &a, dim3 grid, hipStream_t st)
 		hipLaunchKernelGGL((permute_k<T, long long>), grid, dim3(256), 0, st, a);
 }
 
-template <int DT>
+template <int DT, int OUTF>
 static void launch_ln(const void *x, const void *g, const void *b, void *o, int rows, int cols,
 		      hipStream_t st)
 {
 	const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+	constexpr int VEC = DT == S3K_F32 ? 4 : 8;
+	const bool vec = cols % (64 * VEC) == 0 && cols / (64 * VEC) <= 8 &&
+			 !(((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)o) & 15u);
+	if (vec) {
+		switch (cols / (64 * VEC)) {
+		case 1: hipLaunchKernelGGL((layernorm_v<DT, 1, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 2: hipLaunchKernelGGL((layernorm_v<DT, 2, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 3: hipLaunchKernelGGL((layernorm_v<DT, 3, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 4: hipLaunchKernelGGL((layernorm_v<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 6: hipLaunchKernelGGL((layernorm_v<DT, 6, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 8: hipLaunchKernelGGL((layernorm_v<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		default: break;
+		}
+	}
 	if (cols <= 256)
-		hipLaunchKernelGGL((layernorm_k<DT, 4>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
 	else if (cols <= 512)
-		hipLaunchKernelGGL((layernorm_k<DT, 8>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
 	else if (cols <= 1024)
-		hipLaunchKernelGGL((layernorm_k<DT, 16>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 16, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
 	else if (cols <= 2048)
-		hipLaunchKernelGGL((layernorm_k<DT, 32>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 32, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
 	else
-		hipLaunchKernelGGL((layernorm_k<DT, 0>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 0, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
 }
 
 } /* namespace s3k */
@@ -200,11 +326,28 @@ extern "C" int s3k_layernorm(int kind, const void *x, const void *gamma, const v
 		return (int)hipSuccess;
 	const hipStream_t st = (hipStream_t)stream;
 	if (kind == S3K_F32)
-		launch_ln<S3K_F32>(x, gamma, beta, out, (int)rows, cols, st);
+		launch_ln<S3K_F32, S3K_LN_SAME>(x, gamma, beta, out, (int)rows, cols, st);
 	else if (kind == S3K_BF16)
-		launch_ln<S3K_BF16>(x, gamma, beta, out, (int)rows, cols, st);
+		launch_ln<S3K_BF16, S3K_LN_SAME>(x, gamma, beta, out, (int)rows, cols, st);
 	else if (kind == S3K_F16)
-		launch_ln<S3K_F16>(x, gamma, beta, out, (int)rows, cols, st);
+		launch_ln<S3K_F16, S3K_LN_SAME>(x, gamma, beta, out, (int)rows, cols, st);
+	else
+		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta,
+				void *out, long long rows, int cols, void *stream)
+{
+	if (rows < 0 || cols <= 0 || rows > 0x7FFFFFFFLL || (fmt == S3K_LN_PLANES && cols % 8))
+		return (int)hipErrorInvalidValue;
+	if (rows == 0)
+		return (int)hipSuccess;
+	const hipStream_t st = (hipStream_t)stream;
+	if (fmt == S3K_LN_PLANES)
+		launch_ln<S3K_F32, S3K_LN_PLANES>(x, gamma, beta, out, (int)rows, cols, st);
+	else if (fmt == S3K_LN_F16)
+		launch_ln<S3K_F32, S3K_LN_F16>(x, gamma, beta, out, (int)rows, cols, st);
 	else
 		return (int)hipErrorInvalidValue;
 	return (int)hipGetLastError();

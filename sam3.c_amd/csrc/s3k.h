@@ -99,6 +99,13 @@ int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
  * axes[k]) of esize-byte elements. */
 int s3k_layernorm(int kind, const void *x, const void *gamma, const void *beta, void *out,
 		  long long rows, int cols, void *stream);
+/* f32 LayerNorm written as the operand a GEMM reads: bf16 planes
+ * [rows, 3*cols] = [hi|lo|hi] (S3K_LN_PLANES, the split f32 GEMM's A) or
+ * f16 [rows, cols] (S3K_LN_F16, the Q8 GEMM's A); the same values as
+ * s3k_layernorm followed by s3k_split3_bf16 / s3k_cast_f16. */
+enum { S3K_LN_SAME = 0, S3K_LN_PLANES = 1, S3K_LN_F16 = 2 };
+int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta, void *out,
+		     long long rows, int cols, void *stream);
 int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, void *out,
 	     int batch, int seq, int heads, int hd, void *stream);
 int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,

@@ -104,6 +104,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 	return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, s3k_bf16x2));
 }
 
+/* Two f32 split into bf16 hi = bf16(x) and lo = bf16(x - hi), each pair
+ * packed lo element first: the operand planes of the split f32 GEMM. */
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo)
+{
+	hi = pack_bf16x2(a, b);
+	lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 /* Pack two f32 as two f16 (RNE) in one dword, lo first. */
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi)
 {

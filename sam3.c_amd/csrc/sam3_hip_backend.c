@@ -60,6 +60,8 @@ struct s3h_res {
 	unsigned char keep;      /* survives the end of this eval            */
 	unsigned char produced;  /* written by a GPU node in this eval        */
 	unsigned char written;   /* written by a GPU node in any eval         */
+	unsigned char fmt;       /* S3H_A_*: the device copy holds a GEMM
+				  * operand form, not the tensor's dtype    */
 };
 
 /* A prepared copy of a constant weight (s3h_prep_*). */
@@ -221,6 +223,11 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		return SAM3_OK;
 	}
 	struct s3h_res *e = res_find(hb, t->data);
+	if (e && e->fmt) {
+		/* a producer wrote the consuming GEMM's operand form */
+		*out = e->dev;
+		return SAM3_OK;
+	}
 	if (e && e->nbytes < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
@@ -275,6 +282,28 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 	e->produced = 1;
 	e->written = 1;
 	e->keep = 1;
+	e->fmt = 0;
+	*out = e->dev;
+	return SAM3_OK;
+}
+
+/* A device buffer of nbytes for output t holding the operand form fmt of
+ * the one GEMM that reads it: never downloaded, dropped after the eval. */
+static enum sam3_error dev_out_fmt(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
+				   size_t nbytes, int fmt, void **out)
+{
+	struct s3h_res *e = res_find(hb, t->data);
+	if (e)
+		res_drop_at(hb, (int)(e - hb->res));
+	enum sam3_error err = res_new(hb, t, nbytes, &e);
+	if (err != SAM3_OK)
+		return err;
+	e->dev_valid = 1;
+	e->host_valid = 0;
+	e->produced = 1;
+	e->written = 1;
+	e->keep = 0;
+	e->fmt = (unsigned char)fmt;
 	*out = e->dev;
 	return SAM3_OK;
 }
@@ -460,6 +489,8 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	}
 
 	void *da, *db, *dc, *dbias = NULL;
+	const struct s3h_res *ae = res_find(hb, a->data);
+	const int a_fmt = ae ? ae->fmt : S3H_A_PLAIN;
 	enum sam3_error err = dev_in(hb, a, &da);
 	if (err == SAM3_OK)
 		err = dev_in(hb, bsrc, &db);
@@ -469,11 +500,104 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_out(hb, out, &dc);
 	if (err != SAM3_OK)
 		return err;
-	err = sam3_hip_matmul(a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags, hb->stream);
+	err = a_fmt ? s3h_matmul_fmt(a_fmt, a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags,
+				     hb->stream)
+		    : sam3_hip_matmul(a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags, hb->stream);
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.fused_nodes += j - i - 1;
 		*used = j - i;
+	}
+	return err;
+}
+
+/* The GEMM operand form an f32 LAYERNORM at node i can be written in:
+ * its output, through RESHAPE views only, must be used once, as the A of
+ * a MATMUL that converts A before its GEMM (s3h_matmul_a_format). The
+ * weight is resolved (and uploaded) here to decide with its device
+ * address. */
+static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			   struct use_map *uses)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->inputs[0]->dtype != SAM3_DTYPE_F32 || !s3h_layernorm_ok(n))
+		return S3H_A_PLAIN;
+	const struct sam3_tensor *t = n->output;
+	int j = i + 1;
+	for (;;) {
+		if (uses_of(uses, t) != 1)
+			return S3H_A_PLAIN;
+		while (j < g->n_nodes) {
+			const struct sam3_node *m = &g->nodes[j];
+			int hit = 0;
+			for (int k = 0; k < m->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++)
+				hit |= m->inputs[k] == t;
+			if (hit)
+				break;
+			j++;
+		}
+		if (j >= g->n_nodes)
+			return S3H_A_PLAIN;
+		if (g->nodes[j].op != SAM3_OP_RESHAPE || g->nodes[j].inputs[0] != t)
+			break;
+		t = g->nodes[j].output;
+		j++;
+	}
+	const struct sam3_node *mm = &g->nodes[j];
+	if (mm->op != SAM3_OP_MATMUL || mm->n_inputs < 2 || mm->inputs[0] != t || !mm->inputs[1] ||
+	    !mm->output)
+		return S3H_A_PLAIN;
+	const struct sam3_tensor *b = mm->inputs[1], *w = NULL;
+	for (int k = i + 1; k < j && !w; k++)
+		if (g->nodes[k].op == SAM3_OP_TRANSPOSE && g->nodes[k].output == b &&
+		    transpose_folds(g, k, uses))
+			w = g->nodes[k].inputs[0];
+	const struct sam3_tensor *bsrc = w ? w : b;
+	if (!bsrc->data || t->n_dims < 1)
+		return S3H_A_PLAIN;
+	const int M = t->n_dims >= 2 ? t->dims[t->n_dims - 2] : 1, K = t->dims[t->n_dims - 1];
+	int N, kb;
+	if (w) {
+		N = w->dims[0];
+		kb = w->dims[1];
+	} else {
+		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
+		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
+	}
+	if (kb != K || s3h_nelems(t) != (long long)M * K || K != n->inputs[0]->dims[n->inputs[0]->n_dims - 1])
+		return S3H_A_PLAIN;
+	void *db = NULL;
+	if (dev_in(hb, bsrc, &db) != SAM3_OK)
+		return S3H_A_PLAIN;
+	static const char aligned_a[16] __attribute__((aligned(16)));
+	return s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, bsrc->dtype, db, SAM3_DTYPE_F32, M, N,
+				   K, w ? SAM3_HIP_B_NT : 0);
+}
+
+/* LAYERNORM written as the operand form fmt of its one consuming GEMM. */
+static enum sam3_error run_layernorm_as(struct sam3_hip_backend *hb, const struct sam3_node *n,
+					int fmt)
+{
+	const struct sam3_tensor *x = n->inputs[0];
+	const int cols = x->dims[x->n_dims - 1];
+	const long long rows = s3h_nelems(x) / cols;
+	void *dx = NULL, *dg = NULL, *db = NULL, *dy = NULL;
+	enum sam3_error err = dev_in(hb, x, &dx);
+	if (err == SAM3_OK && n->n_inputs > 1 && n->inputs[1])
+		err = dev_in(hb, n->inputs[1], &dg);
+	if (err == SAM3_OK && n->n_inputs > 2 && n->inputs[2])
+		err = dev_in(hb, n->inputs[2], &db);
+	if (err == SAM3_OK)
+		err = dev_out_fmt(hb, n->output, (size_t)rows * cols * (fmt == S3H_A_PLANES ? 6 : 2),
+				  fmt, &dy);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_layernorm_to(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
+					       (const float *)dx, (const float *)dg,
+					       (const float *)db, dy, rows, cols, hb->stream),
+			      "layernorm (GEMM operand)");
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.operand_writes++;
 	}
 	return err;
 }
@@ -672,6 +796,9 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	for (int i = 0; i < hb->n_res; i++)
 		hb->res[i].produced = 0;
 	s3h_cur = hb;
+	const char *ln_env = getenv("SAM3_HIP_LN_OPERAND");
+	const int ln_plain = ln_env && atoi(ln_env) == 0;
+	int ln_fmt = S3H_A_PLAIN;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -689,6 +816,9 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 			err = run_matmul(hb, g, i, folded, &uses, &used);
 		} else if (n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) {
 			err = run_conv(hb, g, i, &uses, &used);
+		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain &&
+			   (ln_fmt = ln_operand_form(hb, g, i, &uses)) != S3H_A_PLAIN) {
+			err = run_layernorm_as(hb, n, ln_fmt);
 		} else if (runs_on_gpu(n)) {
 			err = run_elementwise(hb, n);
 		} else {
@@ -702,7 +832,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	if (err == SAM3_OK && !g->no_readback) {
 		for (int i = 0; i < hb->n_res && err == SAM3_OK; i++) {
 			struct s3h_res *e = &hb->res[i];
-			if (e->produced && e->dev_valid && !e->host_valid)
+			if (e->produced && e->dev_valid && !e->host_valid && !e->fmt)
 				err = download(hb, e);
 		}
 	}

@@ -50,6 +50,17 @@ enum sam3_error s3h_conv2d(const struct sam3_node *node, const void *bias, int f
 int s3h_bias_add_ok(const struct sam3_node *node);
 enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
 
+/* The form matmul converts its A operand to before the GEMM, so the node
+ * producing A can write that form directly: S3H_A_PLANES = bf16 [M, 3K]
+ * [hi|lo|hi] (the split f32 GEMM), S3H_A_F16 = f16 [M, K] (the Q8 GEMM
+ * with f32 activations). s3h_matmul_fmt runs the GEMM on A in that form. */
+enum { S3H_A_PLAIN = 0, S3H_A_PLANES = 1, S3H_A_F16 = 2 };
+int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
+			int K, int flags);
+enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, const void *b,
+			       int c_dt, void *c, int M, int N, int K, const void *bias, int flags,
+			       void *stream);
+
 /* Prepared copies of constant weights (bf16 hi/lo planes, padded rows),
  * kept by the backend whose graph_eval is running on this thread. A copy
  * is keyed by the source's device address, the preparation (tag) and its

@@ -277,16 +277,21 @@ static int prep_conv_w(const void *w, void *out, int rows, int k, int k_out, int
 	return s3k_conv_wprep(kind, w, out, rows, k, k_out, stream);
 }
 
-static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, void *stream)
+/* a_planes: A already split by its producer ([M, 3K] = [hi|lo|hi]), or
+ * NULL to split g->a here. */
+static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, const void *a_planes, void *stream)
 {
 	const hipStream_t st = (hipStream_t)stream;
 	const size_t abytes = (size_t)g->M * 3 * g->K * 2, bbytes = (size_t)g->N * 3 * g->K * 2;
 	void *a3 = NULL, *b3 = NULL;
 	int own_b = 1;
-	enum sam3_error err = s3h_scratch_alloc(&a3, abytes, stream);
-	if (err == SAM3_OK)
-		err = s3h_hip(s3k_split3_bf16((const float *)g->a, a3, g->M, g->K, g->lda, 0, stream),
-			      "matmul f32 split A");
+	enum sam3_error err = SAM3_OK;
+	if (!a_planes) {
+		err = s3h_scratch_alloc(&a3, abytes, stream);
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_split3_bf16((const float *)g->a, a3, g->M, g->K, g->lda, 0, stream),
+				      "matmul f32 split A");
+	}
 	if (err == SAM3_OK && g->ldb == g->K)
 		err = prep_weight(g->b, (size_t)g->N * g->K * 4, S3H_PREP_SPLIT_W, g->N, g->K, g->K,
 				  bbytes, S3K_F32, prep_split_w, stream, &b3, &own_b);
@@ -298,7 +303,7 @@ static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, void *stream)
 	}
 	if (err == SAM3_OK) {
 		struct s3k_gemm h = *g;
-		h.a = a3;
+		h.a = a_planes ? a_planes : a3;
 		h.b = b3;
 		h.a_kind = h.b_kind = S3K_BF16;
 		h.K = 3 * g->K;
@@ -353,7 +358,7 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 		if (q8_needs_unpack(&g))
 			return q8_unpacked(&g, stream);
 		if (f32_split_wanted(&g))
-			return f32_split_gemm(&g, stream);
+			return f32_split_gemm(&g, NULL, stream);
 		if (s3k_gemm_path(&g) == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 			return q8_dl_cast(&g, stream);
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
@@ -365,7 +370,7 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	if (path == S3K_PATH_MFMA && q8_needs_unpack(&g))
 		return q8_unpacked(&g, stream);
 	if (path == S3K_PATH_MFMA && f32_split_wanted(&g))
-		return f32_split_gemm(&g, stream);
+		return f32_split_gemm(&g, NULL, stream);
 	if (path == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 		return q8_dl_cast(&g, stream);
 	int e = s3k_gemm_launch_path(&g, path, stream);
@@ -374,6 +379,49 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 		return SAM3_EINVAL;
 	}
 	return s3h_hip(e, "matmul");
+}
+
+int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
+			int K, int flags)
+{
+	if (check_kinds(a_dt, b_dt, c_dt) != SAM3_OK || M <= 0 || N <= 0 || K <= 0 || !a || !b)
+		return S3H_A_PLAIN;
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, c_dt, (void *)a, M, N, K, NULL, flags);
+	if (q8_needs_unpack(&g))
+		return S3H_A_PLAIN;
+	if (f32_split_wanted(&g))
+		return S3H_A_PLANES;
+	if (g.a_kind == S3K_F32 && s3k_gemm_path(&g) == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
+		return S3H_A_F16;
+	return S3H_A_PLAIN;
+}
+
+enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, const void *b,
+			       int c_dt, void *c, int M, int N, int K, const void *bias, int flags,
+			       void *stream)
+{
+	if (a_fmt == S3H_A_PLAIN)
+		return matmul_impl(0, a_dt, a, b_dt, b, c_dt, c, M, N, K, bias, flags, stream);
+	if (M <= 0 || N <= 0 || K <= 0 || !a || !b || !c || ((flags & SAM3_HIP_BIAS) && !bias)) {
+		s3h_error("matmul: bad prepared-operand call M=%d N=%d K=%d", M, N, K);
+		return SAM3_EINVAL;
+	}
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, c_dt, c, M, N, K, bias, flags);
+	if (a_fmt == S3H_A_PLANES) {
+		if (!f32_split_wanted(&g)) {
+			s3h_error("matmul: A given as bf16 planes but the split GEMM cannot run");
+			return SAM3_EINVAL;
+		}
+		return f32_split_gemm(&g, a, stream);
+	}
+	if (a_fmt == S3H_A_F16 && g.a_kind == S3K_F32 && q8_dl_wants_cast(&g)) {
+		g.a_kind = S3K_F16;
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+	}
+	s3h_error("matmul: operand format %d does not fit this GEMM", a_fmt);
+	return SAM3_EINVAL;
 }
 
 enum sam3_error sam3_hip_matmul(int a_dtype, const void *a, int b_dtype, const void *b,

@@ -82,7 +82,7 @@ BIAS, GELU, B_NT = 1, 2, 4
 class EvalStats(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("gpu_nodes", "fused_nodes", "host_nodes",
                                        "uploads", "cache_hits", "downloads",
-                                       "mapped_reads", "prep_hits")]
+                                       "mapped_reads", "prep_hits", "operand_writes")]
 
 
 class HipError(RuntimeError):

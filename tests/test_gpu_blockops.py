@@ -70,7 +70,8 @@ def run_node(fn, op, ins, out, params=(0, 0, 0, 0)):
 
 # ------------------------------------------------------------- LayerNorm
 @pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,cols", [(5184, 1024), (37, 96), (29, 160), (7, 3000), (3, 1), (130, 256)])
+@pytest.mark.parametrize("rows,cols", [(5184, 1024), (37, 96), (29, 160), (7, 3000), (3, 1), (130, 256),
+                                       (64, 1536), (9, 512), (5, 2048), (11, 768)])
 @pytest.mark.parametrize("affine", [2, 0])
 def test_layernorm(kind, rows, cols, affine):
     O, lib = oracle(), hip.load()
@@ -263,3 +264,51 @@ def test_vit_block_graph_all_on_gpu(is_global, e, heads):
     ref = out_array(orf, (grid * grid, e))
     R.close()
     assert_f32_close(got, ref, what=f"vit block e={e} global={is_global}")
+
+
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+@pytest.mark.parametrize("via_reshape", [False, True])
+def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
+    """LAYERNORM -> (RESHAPE ->) linear, as gh_mlp and the global-attention
+    qkv build it: the LN writes the operand its one GEMM reads (bf16
+    hi/lo planes for f32 weights, f16 for Q8_0 weights) instead of its f32
+    output. That is the same arithmetic as LN then split/cast, so the
+    result equals the unfused graph's bit for bit; both match LN + matmul
+    of the oracle."""
+    M, K, N = 1024, 512, 768
+    O = oracle()
+    x = synth.randn(800, (M, K), 2.0, 0.5)
+    gam, bet = synth.randn(801, (K,)), synth.randn(802, (K,), 0.1)
+    w = synth.randn(803, (N, K), 0.05)
+    bias = synth.randn(804, (N,), 0.02)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_LN_OPERAND", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_LN_OPERAND", env)
+        G = graph.Graph()
+        tx = G.tensor(abi.F32, (M, K), x)
+        t = G.layernorm(tx, G.tensor(abi.F32, (K,), gam), G.tensor(abi.F32, (K,), bet))
+        if via_reshape:
+            t = G.reshape(G.reshape(t, [1, M, K]), [M, K])
+        tw = (G.tensor(abi.Q8_0, (N, K), O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, (N, K), w))
+        y = G.linear(t, tw, G.tensor(abi.F32, (N,), bias))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(M, N)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.operand_writes == 1 and st0.operand_writes == 0
+    assert st.host_nodes == 0
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    ln = O.layernorm(x, gam, bet, "f32", threads=8)
+    wd = O.q8_dequantize(O.q8_quantize(w), N * K).reshape(N, K) if wkind == "q8" else w
+    ref = ln.astype(np.float64) @ wd.T.astype(np.float64) + bias
+    assert_f32_close(fused, ref.astype(np.float32), what=f"LN -> linear {wkind}")
