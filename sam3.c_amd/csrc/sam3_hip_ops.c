@@ -190,54 +190,6 @@ static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 	return err != SAM3_OK ? err : ferr;
 }
 
-/* f32/bf16 activations times Q8_0 [N,K] weights on the direct-to-LDS Q8
- * GEMM: the activations are cast to f16 once into stream-ordered scratch
- * (the value the register-staged loader would form), then the GEMM runs
- * on f16 A. */
-static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
-{
-	const size_t bytes = (size_t)g->M * g->K * 2;
-	void *a16 = NULL;
-	enum sam3_error err = s3h_scratch_alloc(&a16, bytes, stream);
-	if (err != SAM3_OK)
-		return err;
-	err = s3h_hip(s3k_cast_f16(g->a_kind, g->a, a16, (long long)g->M * g->K, stream),
-		      "matmul_q8 activation cast");
-	if (err == SAM3_OK) {
-		struct s3k_gemm h = *g;
-		h.a = a16;
-		h.a_kind = S3K_F16;
-		h.lda = g->K;
-		err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
-	}
-	enum sam3_error ferr = s3h_hip(hipFreeAsync(a16, (hipStream_t)stream),
-				       "matmul_q8 activation scratch free");
-	return err != SAM3_OK ? err : ferr;
-}
-
-static int q8_dl_wants_cast(const struct s3k_gemm *g)
-{
-	return g->b_kind == S3K_Q8 && g->a_kind != S3K_F16 && s3k_dlq8_eligible(g);
-}
-
-/* f32 x f32 with W [N,K] on the bf16 MFMA GEMM: A and W are split once
- * into bf16 hi/lo planes laid out along a tripled k, A' = [Ah | Al | Ah]
- * and W' = [Wh | Wh | Wl], so that one bf16 GEMM over 3K accumulates
- * Ah*Wh + Al*Wh + Ah*Wl in f32; the dropped Al*Wl term is below 2^-16 of
- * each product. */
-static int f32_split_wanted(const struct s3k_gemm *g)
-{
-	const char *env = getenv("SAM3_HIP_F32_SPLIT");
-	if (env && atoi(env) == 0)
-		return 0;
-	return g->a_kind == S3K_F32 && g->b_kind == S3K_F32 && g->c_kind == S3K_F32 &&
-	       (g->flags & S3K_B_NT) && g->batch == 1 && g->K % 8 == 0 && g->lda % 4 == 0 &&
-	       g->ldb % 4 == 0 && !(((uintptr_t)g->a | (uintptr_t)g->b) & 15u) &&
-	       (long long)g->M * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
-	       (long long)g->N * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
-	       (long long)g->M * g->N * g->K >= (1LL << 24);
-}
-
 /* A prepared copy of weight w (rows x k source elements of 4 or 2 bytes)
  * in the layout `tag` with pitch k_out: from the backend's cache when it
  * holds one, else made by fn into new scratch, which is kept in the cache
@@ -275,6 +227,97 @@ static int prep_split_w(const void *w, void *out, int rows, int k, int k_out, in
 static int prep_conv_w(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
 {
 	return s3k_conv_wprep(kind, w, out, rows, k, k_out, stream);
+}
+
+static int prep_q8_f16(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
+{
+	(void)k_out;
+	(void)kind;
+	return s3k_q8_nk_to_f16_nk(w, out, k, rows, stream);
+}
+
+/* Q8_0 W [N,K] x f16 A on the MFMA path. Inside graph_eval a constant
+ * weight is expanded once into an f16 [N,K] copy, q*scale formed in f32
+ * and rounded once to f16 (the direct Q8 kernel rounds the scale to f16
+ * and multiplies in f16 at every k-step, one more rounding), and the f16
+ * GEMM runs on it at the dense f16 rate, for 2 bytes per weight of HBM
+ * instead of 1.125. SAM3_HIP_Q8_EXPAND=0, or a call outside graph_eval,
+ * keeps the direct Q8 kernel. */
+static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
+{
+	const char *env = getenv("SAM3_HIP_Q8_EXPAND");
+	const size_t q8_bytes = (size_t)h->N * (h->K / 32) * 36;
+	if ((!env || atoi(env) != 0) && (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1 &&
+	    s3h_prep_cacheable(h->b, q8_bytes)) {
+		void *w16 = NULL;
+		int own = 0;
+		enum sam3_error err = prep_weight(h->b, q8_bytes, S3H_PREP_Q8_F16, h->N, h->K, h->K,
+						  (size_t)h->N * h->K * 2, S3K_Q8, prep_q8_f16, stream,
+						  &w16, &own);
+		if (err == SAM3_OK) {
+			struct s3k_gemm e = *h;
+			e.b = w16;
+			e.b_kind = S3K_F16;
+			e.ldb = h->K;
+			err = s3h_hip(s3k_gemm_launch_path(&e, S3K_PATH_MFMA, stream), "matmul_q8 f16 gemm");
+		}
+		if (own && w16) {
+			enum sam3_error e2 = s3h_hip(hipFreeAsync(w16, (hipStream_t)stream),
+						     "matmul_q8 weight scratch free");
+			if (err == SAM3_OK)
+				err = e2;
+		}
+		return err;
+	}
+	return s3h_hip(s3k_gemm_launch_path(h, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+}
+
+/* f32/bf16 activations times Q8_0 [N,K] weights on the direct-to-LDS Q8
+ * GEMM: the activations are cast to f16 once into stream-ordered scratch
+ * (the value the register-staged loader would form), then the GEMM runs
+ * on f16 A. */
+static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
+{
+	const size_t bytes = (size_t)g->M * g->K * 2;
+	void *a16 = NULL;
+	enum sam3_error err = s3h_scratch_alloc(&a16, bytes, stream);
+	if (err != SAM3_OK)
+		return err;
+	err = s3h_hip(s3k_cast_f16(g->a_kind, g->a, a16, (long long)g->M * g->K, stream),
+		      "matmul_q8 activation cast");
+	if (err == SAM3_OK) {
+		struct s3k_gemm h = *g;
+		h.a = a16;
+		h.a_kind = S3K_F16;
+		h.lda = g->K;
+		err = q8_f16_gemm(&h, stream);
+	}
+	enum sam3_error ferr = s3h_hip(hipFreeAsync(a16, (hipStream_t)stream),
+				       "matmul_q8 activation scratch free");
+	return err != SAM3_OK ? err : ferr;
+}
+
+static int q8_dl_wants_cast(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && g->a_kind != S3K_F16 && s3k_dlq8_eligible(g);
+}
+
+/* f32 x f32 with W [N,K] on the bf16 MFMA GEMM: A and W are split once
+ * into bf16 hi/lo planes laid out along a tripled k, A' = [Ah | Al | Ah]
+ * and W' = [Wh | Wh | Wl], so that one bf16 GEMM over 3K accumulates
+ * Ah*Wh + Al*Wh + Ah*Wl in f32; the dropped Al*Wl term is below 2^-16 of
+ * each product. */
+static int f32_split_wanted(const struct s3k_gemm *g)
+{
+	const char *env = getenv("SAM3_HIP_F32_SPLIT");
+	if (env && atoi(env) == 0)
+		return 0;
+	return g->a_kind == S3K_F32 && g->b_kind == S3K_F32 && g->c_kind == S3K_F32 &&
+	       (g->flags & S3K_B_NT) && g->batch == 1 && g->K % 8 == 0 && g->lda % 4 == 0 &&
+	       g->ldb % 4 == 0 && !(((uintptr_t)g->a | (uintptr_t)g->b) & 15u) &&
+	       (long long)g->M * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
+	       (long long)g->N * 3 * g->K * 2 <= 0x7FFFFFF0LL &&
+	       (long long)g->M * g->N * g->K >= (1LL << 24);
 }
 
 /* a_planes: A already split by its producer ([M, 3K] = [hi|lo|hi]), or
@@ -361,6 +404,8 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 			return f32_split_gemm(&g, NULL, stream);
 		if (s3k_gemm_path(&g) == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 			return q8_dl_cast(&g, stream);
+		if (g.b_kind == S3K_Q8 && g.a_kind == S3K_F16 && s3k_gemm_path(&g) == S3K_PATH_MFMA)
+			return q8_f16_gemm(&g, stream);
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
 	}
 	if (path < S3K_PATH_MFMA || path > S3K_PATH_GENERIC) {
@@ -418,7 +463,7 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 	}
 	if (a_fmt == S3H_A_F16 && g.a_kind == S3K_F32 && q8_dl_wants_cast(&g)) {
 		g.a_kind = S3K_F16;
-		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+		return q8_f16_gemm(&g, stream);
 	}
 	s3h_error("matmul: operand format %d does not fit this GEMM", a_fmt);
 	return SAM3_EINVAL;

@@ -237,3 +237,51 @@ def test_prepared_weights_reused_and_dropped():
     finally:
         be.close()
     assert np.array_equal(y3.view(np.uint32), y4.view(np.uint32))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_q8_weights_expanded_once(monkeypatch, gelu):
+    """Inside graph_eval a constant Q8_0 weight of a large-M GEMM is
+    expanded once to f16 (q*scale in f32, rounded once) and reused by
+    later evals (prep_hits). The f16 GEMM on it and the direct Q8 kernel
+    (SAM3_HIP_Q8_EXPAND=0, which rounds the scale to f16 first) both
+    match the reference's dequantized weights in float64; the expanded
+    path is at least as close."""
+    M, K, N = 2048, 1024, 768
+    O = oracle()
+    x = synth.randn(900, (M, K))
+    wq = O.q8_quantize(synth.randn(901, (N, K), 0.03))
+    bias = synth.randn(902, (N,), 0.02)
+
+    def run(env, evals=2):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_Q8_EXPAND", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_Q8_EXPAND", env)
+        G = graph.Graph()
+        t = G.linear(G.tensor(abi.F32, (M, K), x), G.tensor(abi.Q8_0, (N, K), wq),
+                     G.tensor(abi.F32, (N,), bias))
+        if gelu:
+            t = G.unary(abi.OP_GELU, t)
+        be = hip.Backend(0)
+        stats = []
+        try:
+            for _ in range(evals):
+                assert be.graph_eval(G.g) == abi.OK
+                stats.append(be.stats())
+        finally:
+            be.close()
+        return out_array(t, (M, N)), stats
+
+    y, st = run(None)
+    y0, st0 = run("0")
+    assert st[0].prep_hits == 0 and st[1].prep_hits == 1 and st0[1].prep_hits == 0
+    assert st[1].host_nodes == 0
+    wd = O.q8_dequantize(wq, N * K).reshape(N, K).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T + bias
+    if gelu:
+        ref = O.gelu(ref.astype(np.float32), "f32").astype(np.float64)
+    assert_f32_close(y, np.asarray(ref, np.float32), what=f"Q8 expanded gelu={gelu}")
+    assert_f32_close(y0, np.asarray(ref, np.float32), what=f"Q8 direct gelu={gelu}")
+    e_exp, e_dir = np.abs(y - ref).max(), np.abs(y0 - ref).max()
+    assert e_exp <= 1.05 * e_dir + 1e-6, (e_exp, e_dir)
