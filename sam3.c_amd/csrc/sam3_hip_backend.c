@@ -24,8 +24,10 @@
  *     inputs (weights) keep their shadow across graph_eval calls until
  *     cache_invalidate / arena_reset drops it (tensor.h:31-38,
  *     backend.h:50-55);
- *   - outputs are written to the shadow and copied back to the host when
- *     the eval ends (kept on the device only with g->no_readback);
+ *   - outputs are written to the shadow; when the eval ends the graph's
+ *     final outputs (node outputs no node consumes) are copied back to
+ *     the host, as the reference's GPU backend does, unless
+ *     g->no_readback is set; intermediates stay on the device;
  *   - before a host-dispatched node, its inputs are copied back first.
  * Tensors whose data already is device memory are used in place.
  * alloc_tensor hands out pinned host memory (hipHostMalloc), so the
@@ -62,6 +64,7 @@ struct s3h_res {
 	unsigned char written;   /* written by a GPU node in any eval         */
 	unsigned char fmt;       /* S3H_A_*: the device copy holds a GEMM
 				  * operand form, not the tensor's dtype    */
+	unsigned char fresh;     /* uploaded from the host in this eval      */
 };
 
 /* A prepared copy of a constant weight (s3h_prep_*). */
@@ -237,6 +240,10 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		if (err != SAM3_OK)
 			return err;
 	}
+	/* an ephemeral input is host data the caller may have rewritten since
+	 * the last eval; only a copy a node of this graph wrote is current */
+	if (t->ephemeral && !e->produced && !e->fresh)
+		e->dev_valid = 0;
 	if (!e->dev_valid) {
 		enum sam3_error err = s3h_hip(hipMemcpyAsync(e->dev, e->host, e->nbytes,
 							     hipMemcpyHostToDevice, hb->stream),
@@ -244,6 +251,7 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		if (err != SAM3_OK)
 			return err;
 		e->dev_valid = 1;
+		e->fresh = 1;
 		hb->stats.uploads++;
 	} else if (!e->produced) {
 		hb->stats.cache_hits++;
@@ -794,7 +802,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		return SAM3_ENOMEM;
 	}
 	for (int i = 0; i < hb->n_res; i++)
-		hb->res[i].produced = 0;
+		hb->res[i].produced = hb->res[i].fresh = 0;
 	s3h_cur = hb;
 	const char *ln_env = getenv("SAM3_HIP_LN_OPERAND");
 	const int ln_plain = ln_env && atoi(ln_env) == 0;
@@ -829,17 +837,50 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		i += used;
 	}
 
+	/* Readback of the graph's final outputs: node outputs no node of the
+	 * graph consumes, as the reference's GPU backend does
+	 * (metal_backend.c:1805-1850, 1897-1945). Intermediates stay on the
+	 * device. SAM3_HIP_READBACK=all downloads every produced tensor. */
 	if (err == SAM3_OK && !g->no_readback) {
-		for (int i = 0; i < hb->n_res && err == SAM3_OK; i++) {
-			struct s3h_res *e = &hb->res[i];
-			if (e->produced && e->dev_valid && !e->host_valid && !e->fmt)
-				err = download(hb, e);
+		const char *rb = getenv("SAM3_HIP_READBACK");
+		if (rb && strcmp(rb, "all") == 0) {
+			for (int i = 0; i < hb->n_res && err == SAM3_OK; i++) {
+				struct s3h_res *e = &hb->res[i];
+				if (e->produced && e->dev_valid && !e->host_valid && !e->fmt)
+					err = download(hb, e);
+			}
+		} else {
+			for (int i = 0; i < g->n_nodes && err == SAM3_OK; i++) {
+				const struct sam3_tensor *t = g->nodes[i].output;
+				if (!t || !t->data || uses_of(&uses, t) > 0)
+					continue;
+				struct s3h_res *e = res_find(hb, t->data);
+				if (e && e->produced && e->dev_valid && !e->host_valid && !e->fmt)
+					err = download(hb, e);
+			}
 		}
 	}
 	enum sam3_error serr = s3h_hip(hipStreamSynchronize(hb->stream), "graph_eval: sync");
 	if (err == SAM3_OK)
 		err = serr;
 	s3h_cur = NULL;
+	/* Intermediates leave the device with the eval; final outputs stay
+	 * resident, so a later graph can read them without a copy (the
+	 * reference's GPU backend evicts and keeps the same sets,
+	 * metal_backend.c:1897-1908). A view of an intermediate that is a
+	 * final output keeps the shared copy. */
+	for (int i = 0; i < g->n_nodes; i++) {
+		const struct sam3_tensor *t = g->nodes[i].output;
+		struct s3h_res *e = t && t->data && uses_of(&uses, t) > 0 ? res_find(hb, t->data) : NULL;
+		if (e && e->produced)
+			e->keep = 0;
+	}
+	for (int i = 0; i < g->n_nodes; i++) {
+		const struct sam3_tensor *t = g->nodes[i].output;
+		struct s3h_res *e = t && t->data && uses_of(&uses, t) == 0 ? res_find(hb, t->data) : NULL;
+		if (e && e->produced && !e->fmt)
+			e->keep = 1;
+	}
 	for (int i = hb->n_res - 1; i >= 0; i--)
 		if (!hb->res[i].keep)
 			res_drop_at(hb, i);

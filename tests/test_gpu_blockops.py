@@ -256,6 +256,7 @@ def test_vit_block_graph_all_on_gpu(is_global, e, heads):
         assert be.graph_eval(Gh.g) == abi.OK
         st = be.stats()
         assert st.host_nodes == 0, f"{st.host_nodes} nodes ran on the host"
+        assert st.downloads == 1      # the block output only; intermediates stay
         got = out_array(oh, (grid * grid, e))
     finally:
         be.close()
@@ -312,3 +313,55 @@ def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
     wd = O.q8_dequantize(O.q8_quantize(w), N * K).reshape(N, K) if wkind == "q8" else w
     ref = ln.astype(np.float64) @ wd.T.astype(np.float64) + bias
     assert_f32_close(fused, ref.astype(np.float32), what=f"LN -> linear {wkind}")
+
+
+def test_blocks_chained_across_evals():
+    """The image encoder's block loop (image_encoder.c:736-915): blocks in
+    separate graph_evals, each graph's output the next graph's input. With
+    no_readback on the first graph its output stays on the device and is
+    read there by the second (no upload of x); the result equals one graph
+    of both blocks, and equals it again when the first graph reads back."""
+    grid, window, e, heads, mlp = 8, 4, 128, 2, 512
+    x0 = synth.randn(950, (grid * grid, e))
+    c, s = graph.rope_tables(window, e // heads)
+
+    def two_graphs(no_readback):
+        G1, G2 = graph.Graph(), graph.Graph()
+        x = G1.tensor(abi.F32, (grid * grid, e), x0, ephemeral=1)
+        y1 = graph.vit_block(G1, x, block_weights(G1, 960, e, mlp), heads, grid, window, False,
+                             G1.tensor(abi.F32, c.shape, c), G1.tensor(abi.F32, s.shape, s))
+        G1.g.no_readback = no_readback
+        G2.keep.append(y1)
+        y2 = graph.vit_block(G2, y1, block_weights(G2, 970, e, mlp), heads, grid, window, False,
+                             G2.tensor(abi.F32, c.shape, c), G2.tensor(abi.F32, s.shape, s))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G1.g) == abi.OK
+            st1 = be.stats()
+            assert be.graph_eval(G2.g) == abi.OK
+            st2 = be.stats()
+        finally:
+            be.close()
+        return out_array(y2, (grid * grid, e)), st1, st2
+
+    G = graph.Graph()
+    x = G.tensor(abi.F32, (grid * grid, e), x0, ephemeral=1)
+    y1 = graph.vit_block(G, x, block_weights(G, 960, e, mlp), heads, grid, window, False,
+                         G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s.shape, s))
+    y2 = graph.vit_block(G, y1, block_weights(G, 970, e, mlp), heads, grid, window, False,
+                         G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s.shape, s))
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G.g) == abi.OK
+        st = be.stats()
+        one = out_array(y2, (grid * grid, e))
+    finally:
+        be.close()
+    assert st.downloads == 1
+    assert st.uploads == 27                   # x, 2 x 12 weights, the 2 RoPE tables
+    fwd, st1, st2 = two_graphs(True)
+    assert st1.downloads == 0 and st2.downloads == 1
+    assert st1.uploads == 15 and st2.uploads == 12   # block 2 reads x on the device
+    back, _, _ = two_graphs(False)
+    assert np.array_equal(fwd.view(np.uint32), one.view(np.uint32))
+    assert np.array_equal(back.view(np.uint32), one.view(np.uint32))
