@@ -232,6 +232,68 @@ def vit_block_bench(is_global, wkind, steps=5, warmup=2):
             "gpu_nodes": st.gpu_nodes, "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes}
 
 
+def vit_trunk_bench(wkind, depth=32, per_graph=4, steps=3, warmup=1):
+    """The ViT-L trunk (image_encoder.c:736-915): `depth` blocks, global
+    attention at blocks 7, 15, 23, 31 (image_encoder.c:35), evaluated
+    `per_graph` blocks per graph_eval as the reference's block loop does,
+    each graph's output forwarded on the device to the next graph
+    (no_readback on all but the last). One layer's weights are shared by
+    every block (the time does not depend on their values). Wall time of
+    the whole trunk, block input in HBM."""
+    from sam3_amd import graph
+    grid, window, e, heads, mlp = 72, 24, 1024, 16, 4096
+    npos = grid * grid
+    xd = hip.DeviceBuffer.of(synth.randn(500, (npos, e)))
+    W = graph.Graph()
+
+    def w(i, shape, std, quant=False):
+        v = synth.randn(520 + i, shape, std)
+        if quant and wkind == "q8":
+            return W.tensor(abi.Q8_0, shape, hip.q8_quantize(v))
+        return W.tensor(abi.F32, shape, v)
+    p = {"ln1_w": w(1, (e,), 1.0), "ln1_b": w(2, (e,), 0.1),
+         "qkv_w": w(3, (3 * e, e), 0.03, True), "qkv_b": w(4, (3 * e,), 0.02),
+         "proj_w": w(5, (e, e), 0.03, True), "proj_b": w(6, (e,), 0.02),
+         "ln2_w": w(7, (e,), 1.0), "ln2_b": w(8, (e,), 0.1),
+         "fc1_w": w(9, (mlp, e), 0.03, True), "fc1_b": w(10, (mlp,), 0.02),
+         "fc2_w": w(11, (e, mlp), 0.03, True), "fc2_b": w(12, (e,), 0.02)}
+    tabs = {}
+    for side in (window, grid):
+        c, s_ = graph.rope_tables(side, e // heads)
+        tabs[side] = (W.tensor(abi.F32, c.shape, c), W.tensor(abi.F32, s_.shape, s_))
+    graphs, x = [], abi.make_tensor(abi.F32, [npos, e], xd.ptr, npos * e * 4)
+    W.keep.append(x)
+    for base in range(0, depth, per_graph):
+        G = graph.Graph()
+        G.keep.append(W)
+        for i in range(base, min(depth, base + per_graph)):
+            glob = i in (7, 15, 23, 31)
+            tc, ts = tabs[grid if glob else window]
+            x = graph.vit_block(G, x, p, heads, grid, window, glob, tc, ts)
+        G.g.no_readback = True
+        graphs.append(G)
+    be = hip.Backend(0)
+    try:
+        def run():
+            for G in graphs:
+                hip.check(be.graph_eval(G.g), "graph_eval")
+        for _ in range(warmup):
+            run()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        st = be.stats()
+    finally:
+        be.close()
+        xd.free()
+    fl = 28 * vit_block_flops(npos, e, heads, mlp, window * window) + \
+        4 * vit_block_flops(npos, e, heads, mlp, npos)
+    return {"ms": round(ms, 2), "images_per_s": round(1e3 / ms, 2), "blocks": depth,
+            "graph_evals": len(graphs), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+            "last_eval_host_nodes": st.host_nodes}
+
+
 def vit_block_cpu(threads=None):
     """The reference's CPU kernels (cpu_dispatch_node over the same node
     sequence, oracle/_ref) on one 24x24 window of the block (576 tokens,
@@ -694,6 +756,9 @@ def main():
                     continue
                 blk[f"{name}_{wk}"] = vit_block_bench(glob, wk)
                 log("  ", name, wk, blk[f"{name}_{wk}"])
+        for wk in ("q8", "f32"):
+            blk[f"trunk_32_blocks_{wk}"] = vit_trunk_bench(wk)
+            log("   trunk", wk, blk[f"trunk_32_blocks_{wk}"])
         if not args.no_cpu_baseline:
             blk["cpu_reference"] = vit_block_cpu()
         blk["note"] = ("5184 tokens, e 1024, 16 heads, MLP 4096, f32 activations; every node "

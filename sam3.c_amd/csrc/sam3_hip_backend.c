@@ -296,21 +296,25 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 }
 
 /* A device buffer of nbytes for output t holding the operand form fmt of
- * the one GEMM that reads it: never downloaded, dropped after the eval. */
+ * the one GEMM that reads it: never downloaded, stale after the eval. */
 static enum sam3_error dev_out_fmt(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
 				   size_t nbytes, int fmt, void **out)
 {
 	struct s3h_res *e = res_find(hb, t->data);
-	if (e)
+	if (e && e->nbytes < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
-	enum sam3_error err = res_new(hb, t, nbytes, &e);
-	if (err != SAM3_OK)
-		return err;
+		e = NULL;
+	}
+	if (!e) {
+		enum sam3_error err = res_new(hb, t, nbytes, &e);
+		if (err != SAM3_OK)
+			return err;
+	}
 	e->dev_valid = 1;
 	e->host_valid = 0;
 	e->produced = 1;
 	e->written = 1;
-	e->keep = 0;
+	e->keep = 1;
 	e->fmt = (unsigned char)fmt;
 	*out = e->dev;
 	return SAM3_OK;
@@ -864,22 +868,27 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	if (err == SAM3_OK)
 		err = serr;
 	s3h_cur = NULL;
-	/* Intermediates leave the device with the eval; final outputs stay
-	 * resident, so a later graph can read them without a copy (the
+	/* Intermediates' contents end with the eval; final outputs stay
+	 * resident and valid, so a later graph reads them without a copy (the
 	 * reference's GPU backend evicts and keeps the same sets,
-	 * metal_backend.c:1897-1908). A view of an intermediate that is a
-	 * final output keeps the shared copy. */
+	 * metal_backend.c:1897-1908). An intermediate keeps its allocation
+	 * for the next eval that produces the same host tensor, but is marked
+	 * stale: read as an input later, it is uploaded from the host. A view
+	 * of an intermediate that is a final output keeps the shared copy. */
 	for (int i = 0; i < g->n_nodes; i++) {
 		const struct sam3_tensor *t = g->nodes[i].output;
 		struct s3h_res *e = t && t->data && uses_of(&uses, t) > 0 ? res_find(hb, t->data) : NULL;
-		if (e && e->produced)
-			e->keep = 0;
+		if (e && e->produced) {
+			e->dev_valid = 0;
+			e->fmt = 0;
+			e->keep = 1;
+		}
 	}
 	for (int i = 0; i < g->n_nodes; i++) {
 		const struct sam3_tensor *t = g->nodes[i].output;
 		struct s3h_res *e = t && t->data && uses_of(&uses, t) == 0 ? res_find(hb, t->data) : NULL;
-		if (e && e->produced && !e->fmt)
-			e->keep = 1;
+		if (e && e->produced)
+			e->dev_valid = 1;
 	}
 	for (int i = hb->n_res - 1; i >= 0; i--)
 		if (!hb->res[i].keep)
