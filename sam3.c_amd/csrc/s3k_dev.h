@@ -70,27 +70,29 @@ __device__ __forceinline__ float round_bf16(float f)
 	return bf16_to_f32(f32_to_bf16(f));
 }
 
+/* The same rounding by the hardware conversion (v_cvt_pk_bf16_f32, round
+ * to nearest even) for the epilogue's intermediate roundings; NaN stays a
+ * NaN. Defined after pack_bf16x2. */
+__device__ __forceinline__ float round_bf16_hw(float f);
+
 __device__ __forceinline__ float round_f16(float f)
 {
 	return (float)(_Float16)f;
 }
 
-/* tanh(u) = 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal:
- * a few instructions instead of a library tanhf, relative error near
- * 1e-7 in 1 + tanh(u), which is what GELU uses. */
-__device__ __forceinline__ float tanh_fast(float u)
-{
-	const float e = __builtin_amdgcn_exp2f(fminf(u, 30.0f) * 2.8853900817779268f); /* 2/ln2 */
-	return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-}
-
-/* 0.5*x*(1 + tanh(sqrt(2/pi)*(x + 0.044715*x^3))), the reference's
- * operation order (cpu_gelu.c:30-38) around the tanh. */
+/* The reference's GELU, 0.5*x*(1 + tanh(u)) with
+ * u = 0.7978845608*(x + 0.044715*x^3) (cpu_gelu.c:30-38), evaluated as
+ * x / (1 + exp(-2u)), the same function (0.5*(1 + tanh(u)) is the
+ * logistic of 2u), with the hardware exp2 and reciprocal:
+ * 2u*log2(e) = x*(a + b*x^2), a = 2*0.7978845608*log2(e), b = 0.044715*a.
+ * Five VALU operations and two transcendentals; relative error near 1e-7.
+ * exp2 overflows to +inf for large negative x, giving x * 0 = -0, the
+ * reference's limit; for large positive x it gives x. */
 __device__ __forceinline__ float gelu_tanh(float x)
 {
-	float cube = mul_rn(mul_rn(mul_rn(0.044715f, x), x), x);
-	float inner = mul_rn(0.7978845608f, add_rn(x, cube));
-	return mul_rn(mul_rn(0.5f, x), add_rn(1.0f, tanh_fast(inner)));
+	const float p = fmaf(0.10294324f, x * x, 2.3022082f);
+	const float e = __builtin_amdgcn_exp2f(-(x * p));
+	return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 typedef __bf16 s3k_bf16x2 __attribute__((ext_vector_type(2)));
@@ -110,6 +112,11 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uin
 {
 	hi = pack_bf16x2(a, b);
 	lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
+__device__ __forceinline__ float round_bf16_hw(float f)
+{
+	return __uint_as_float(pack_bf16x2(f, 0.0f) << 16);
 }
 
 /* Pack two f32 as two f16 (RNE) in one dword, lo first. */
@@ -141,11 +148,11 @@ __device__ __forceinline__ float epilogue(float acc, float bias, int flags)
 {
 	float v = acc;
 	if (CK == 2) { /* BF16 */
-		v = round_bf16(v);
+		v = round_bf16_hw(v);
 		if (flags & 1)
-			v = round_bf16(add_rn(v, bias));
+			v = round_bf16_hw(add_rn(v, bias));
 		if (flags & 2)
-			v = round_bf16(gelu_tanh(v));
+			v = round_bf16_hw(gelu_tanh(v));
 	} else if (CK == 1) { /* F16 */
 		v = round_f16(v);
 		if (flags & 1)
