@@ -471,6 +471,72 @@ def cpu_conv(name, threads=None, target_s=3.0):
             "sample": f"f32 {name}, {rows} of {H} input rows -> {M} output pixels, {dt:.2f} s"}
 
 
+def neck_graph(x_dev, dim=1024, d=256, grid=72, seed=640):
+    """The FPN neck of necks.c:30-140 on the trunk's [1, grid, grid, dim]
+    map, all four scales in one graph (f32, synthetic weights, biases on
+    every conv): 4x ConvT(dim->dim/2)+GELU, ConvT(dim/2->dim/4), 1x1, 3x3;
+    2x ConvT(dim->dim/2), 1x1, 3x3; 1x 1x1, 3x3; 0.5x MaxPool 2/2, 1x1, 3x3.
+    Returns the graph, its outputs and its flop count."""
+    from sam3_amd import graph
+    G = graph.Graph()
+    F = abi.F32
+    x = abi.make_tensor(F, [1, grid, grid, dim], x_dev, grid * grid * dim * 4)
+    G.keep.append(x)
+    k = [seed]
+    flops = [0.0]
+
+    def conv(t, oc, ksz, transpose=False, gelu=False):
+        _, h, w, c = (t.dims[i] for i in range(4))
+        k[0] += 2
+        wt = G.tensor(F, (oc, ksz, ksz, c), synth.randn(k[0], (oc, ksz, ksz, c), 0.02))
+        b = G.tensor(F, (oc,), synth.randn(k[0] + 1, (oc,), 0.02))
+        if transpose:
+            oh, ow = h * 2, w * 2
+            t = G.node(abi.OP_CONV_TRANSPOSE2D, [t, wt], G.tensor(F, (1, oh, ow, oc)), (2, 0, 0, 0))
+            flops[0] += 2.0 * h * w * c * oc * ksz * ksz
+        else:
+            oh, ow = h, w
+            t = G.node(abi.OP_CONV2D, [t, wt], G.tensor(F, (1, oh, ow, oc)), (1, ksz // 2, 1, 0))
+            flops[0] += 2.0 * oh * ow * oc * c * ksz * ksz
+        t = G.node(abi.OP_BIAS_ADD, [t, b], G.tensor(F, (1, oh, ow, oc)))
+        if gelu:
+            t = G.node(abi.OP_GELU, [t], G.tensor(F, (1, oh, ow, oc)))
+        return t
+
+    outs = []
+    t = conv(conv(x, dim // 2, 2, True, True), dim // 4, 2, True)
+    outs.append(conv(conv(t, d, 1), d, 3))
+    t = conv(x, dim // 2, 2, True)
+    outs.append(conv(conv(t, d, 1), d, 3))
+    outs.append(conv(conv(x, d, 1), d, 3))
+    t = G.node(abi.OP_MAXPOOL2D, [x], G.tensor(F, (1, grid // 2, grid // 2, dim)), (2, 2, 0, 0))
+    outs.append(conv(conv(t, d, 1), d, 3))
+    return G, outs, flops[0]
+
+
+def neck_bench(steps=10, warmup=2):
+    """The four-scale neck through graph_eval: input map in HBM, outputs
+    kept in HBM (no_readback), f32 weights prepared once."""
+    xd = hip.DeviceBuffer.of(synth.randn(630, (1, 72, 72, 1024)))
+    G, outs, fl = neck_graph(xd.ptr)
+    G.g.no_readback = True
+    be = hip.Backend(0)
+    try:
+        for _ in range(warmup):
+            hip.check(be.graph_eval(G.g), "graph_eval")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hip.check(be.graph_eval(G.g), "graph_eval")
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        st = be.stats()
+    finally:
+        be.close()
+        xd.free()
+    return {"ms": round(ms, 3), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+            "gflop": round(fl / 1e9, 1), "nodes": G.g.n_nodes, "gpu_nodes": st.gpu_nodes,
+            "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes}
+
+
 def measured_traffic(key):
     """HBM bytes per launch of the headline kernel, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json (scaled
@@ -585,8 +651,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
-    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,weights",
-                    help="comma list of extra sections to run (cfg1..cfg5, block, conv, weights)")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,neck,weights",
+                    help="comma list of extra sections to run (cfg1..cfg5, block, conv, neck, "
+                         "weights)")
     ap.add_argument("--block", default="windowed_f32,windowed_q8,global_f32,global_q8",
                     help="block section: comma list of {windowed,global}_{f32,q8}")
     args = ap.parse_args()
@@ -778,6 +845,11 @@ def main():
         cv["note"] = ("one sam3_hip_kernel_conv2d per step, inputs in HBM; 2*M*OC*K flops with "
                       "M = N*OH*OW, K = KH*KW*C; f32 runs on bf16 hi/lo planes")
         extra["conv2d"] = cv
+
+    if not args.quick and "neck" in only:
+        log("FPN neck, four scales, f32 (necks.c)")
+        extra["neck_f32"] = neck_bench()
+        log("  ", extra["neck_f32"])
 
     if not args.quick and "weights" in only:
         log("weights: .sam3 blob (32 ViT-L layers, Q8_0 linear weights) to HBM")

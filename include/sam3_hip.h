@@ -32,8 +32,9 @@ extern "C" {
  * struct sam3_backend_ops (src/backend/backend.h:31-56). graph_eval runs
  * MATMUL nodes (F32, F16, BF16, F32 x Q8_0) on the GPU, fusing
  * TRANSPOSE(W) -> MATMUL -> ADD(bias) -> GELU chains, and runs ADD,
- * GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE, SLICE, CONV2D (with a following
- * BIAS_ADD and GELU in its epilogue) and BIAS_ADD on the GPU as well
+ * GELU, TRANSPOSE, SDPA, LAYERNORM, ROPE, SLICE, CONV2D and
+ * CONV_TRANSPOSE2D (with a following BIAS_ADD and GELU in their
+ * epilogue), MAXPOOL2D and BIAS_ADD on the GPU as well
  * (RESHAPE is a view: no copy, no transfer); other ops go to the host
  * dispatcher set with sam3_hip_backend_set_host_dispatch, or fail with
  * SAM3_EDTYPE when none is set (as cpu_dispatch_node does for an op with
@@ -221,6 +222,37 @@ enum sam3_error sam3_hip_conv2d_on_path(int path, const struct sam3_node *node, 
  * bias [C] over the last dim, F32, BF16 (and F16), one dtype.
  */
 enum sam3_error sam3_hip_kernel_bias_add(const struct sam3_node *node, void *stream);
+
+/*
+ * CONV_TRANSPOSE2D node kernel: cpu_kernel_conv_transpose2d
+ * (src/backend/cpu/kernels/cpu_conv_transpose2d.c:140-217). Input
+ * [N,H,W,C] (NHWC), weight OHWI [OC,KH,KW,C], output [N,OH,OW,OC] with
+ * OH = (H-1)*stride - 2*pad + KH (and OW alike); params[0] = stride
+ * (<= 0 -> 1), [1] = pad. F32 only, as the reference's dtype table
+ * (cpu_dispatch.c:553-555): other dtypes -> SAM3_EDTYPE; channel or
+ * output-shape mismatch -> SAM3_EINVAL. stride = KH = KW with no padding
+ * (the neck's 2x2 upsampling) runs one GEMM over the input pixels and a
+ * pixel-shuffle permute (bf16 hi/lo split GEMM, ~1e-5 normwise); other
+ * shapes run the reference's gather order, bit-exact.
+ */
+enum sam3_error sam3_hip_kernel_conv_transpose2d(const struct sam3_node *node, void *stream);
+
+/* The kernel sam3_hip_kernel_conv_transpose2d picks (1 GEMM, 3 direct; 0
+ * if the node is invalid) and a forced one (SAM3_EINVAL if it cannot run
+ * the node). No reference counterpart: for tests and benches. */
+int sam3_hip_conv_transpose2d_path(const struct sam3_node *node);
+enum sam3_error sam3_hip_conv_transpose2d_on_path(int path, const struct sam3_node *node,
+						  void *stream);
+
+/*
+ * MAXPOOL2D node kernel: cpu_kernel_maxpool2d
+ * (src/backend/cpu/kernels/cpu_maxpool2d.c:113-177). NHWC [N,H,W,C] ->
+ * [N,OH,OW,C], params[0] = kernel (<= 0 -> 2), [1] = stride (<= 0 ->
+ * kernel), OH = (H - kernel)/stride + 1; F32 only. The same scan as the
+ * reference (first tap, then strictly greater ones), bit-exact, NaNs
+ * included.
+ */
+enum sam3_error sam3_hip_kernel_maxpool2d(const struct sam3_node *node, void *stream);
 
 /* Route one node by op and dtype. Replaces cpu_dispatch_node
  * (src/backend/cpu/cpu_dispatch.c:591-686): same mixed F32 x Q8_0 rule,

@@ -904,3 +904,91 @@ void oracle_conv2d_f16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N,
 {
 	conv_any(x, w, y, 2, N, H, W, C, OC, KH, KW, stride, ph, pw, groups, OH, OW, n_threads);
 }
+
+/* ------------------------------------------------------------------ */
+/* ConvTranspose2D, NHWC x OHWI (cpu_conv_transpose2d.c:55-131): per    */
+/* output pixel the channels start at 0; for each tap (kh, kw) whose    */
+/* input pixel ih = (oh + pad - kh) / stride divides exactly and lies   */
+/* inside, out[co] += dot over input channels in order.                 */
+/* ------------------------------------------------------------------ */
+struct convt_ctx {
+	const float *x, *w;
+	float *y;
+	int N, H, W, C, OC, KH, KW, stride, pad, OH, OW;
+};
+
+static void convt_rows(void *p, int r0, int r1)
+{
+	const struct convt_ctx *c = p;
+	const size_t kk = (size_t)c->KH * c->KW * c->C;
+	for (int row = r0; row < r1; row++) { /* row = n * OH + oh */
+		const int n = row / c->OH, oh = row % c->OH;
+		for (int ow = 0; ow < c->OW; ow++) {
+			float *out = c->y + (((size_t)n * c->OH + oh) * c->OW + ow) * c->OC;
+			for (int co = 0; co < c->OC; co++)
+				out[co] = 0.0f;
+			for (int kh = 0; kh < c->KH; kh++) {
+				const int ohf = oh + c->pad - kh;
+				if (ohf < 0 || ohf % c->stride != 0)
+					continue;
+				const int ih = ohf / c->stride;
+				if (ih >= c->H)
+					continue;
+				for (int kw = 0; kw < c->KW; kw++) {
+					const int owf = ow + c->pad - kw;
+					if (owf < 0 || owf % c->stride != 0)
+						continue;
+					const int iw = owf / c->stride;
+					if (iw >= c->W)
+						continue;
+					const float *in = c->x + (((size_t)n * c->H + ih) * c->W + iw) * c->C;
+					for (int co = 0; co < c->OC; co++) {
+						const float *wp = c->w + (size_t)co * kk + ((size_t)kh * c->KW + kw) * c->C;
+						float dot = 0.0f;
+						for (int ci = 0; ci < c->C; ci++)
+							dot += in[ci] * wp[ci];
+						out[co] += dot;
+					}
+				}
+			}
+		}
+	}
+}
+
+void oracle_conv_transpose2d_f32(const float *x, const float *w, float *y, int N, int H, int W,
+				 int C, int OC, int KH, int KW, int stride, int pad, int n_threads)
+{
+	struct convt_ctx c = { x, w, y, N, H, W, C, OC, KH, KW, stride, pad,
+			       (H - 1) * stride - 2 * pad + KH, (W - 1) * stride - 2 * pad + KW };
+	run_rows(convt_rows, &c, N * c.OH, n_threads);
+}
+
+/* ------------------------------------------------------------------ */
+/* MaxPool2D, NHWC (cpu_maxpool2d.c:68-108): start from the window's    */
+/* first tap, then take a tap only when it is greater; taps past the    */
+/* image are skipped. OH = (H - kernel) / stride + 1.                   */
+/* ------------------------------------------------------------------ */
+void oracle_maxpool2d_f32(const float *x, float *y, int N, int H, int W, int C, int kernel,
+			  int stride)
+{
+	const int OH = (H - kernel) / stride + 1, OW = (W - kernel) / stride + 1;
+	for (int n = 0; n < N; n++)
+		for (int oh = 0; oh < OH; oh++)
+			for (int ow = 0; ow < OW; ow++) {
+				float *out = y + (((size_t)n * OH + oh) * OW + ow) * C;
+				const int ih0 = oh * stride, iw0 = ow * stride;
+				const float *first = x + (((size_t)n * H + ih0) * W + iw0) * C;
+				for (int c = 0; c < C; c++)
+					out[c] = first[c];
+				for (int kh = 0; kh < kernel; kh++)
+					for (int kw = 0; kw < kernel; kw++) {
+						const int ih = ih0 + kh, iw = iw0 + kw;
+						if ((kh == 0 && kw == 0) || ih >= H || iw >= W)
+							continue;
+						const float *in = x + (((size_t)n * H + ih) * W + iw) * C;
+						for (int c = 0; c < C; c++)
+							if (in[c] > out[c])
+								out[c] = in[c];
+					}
+			}
+}

@@ -122,4 +122,11 @@ void oracle_conv2d_f16(const uint16_t *x, const uint16_t *w, uint16_t *y, int N,
 		       int C, int OC, int KH, int KW, int stride, int ph, int pw, int groups, int OH,
 		       int OW, int n_threads);
 
+/* ---- ConvTranspose2D NHWC x OHWI (cpu_conv_transpose2d.c:55-131) and
+ * MaxPool2D NHWC (cpu_maxpool2d.c:68-108), f32. ---- */
+void oracle_conv_transpose2d_f32(const float *x, const float *w, float *y, int N, int H, int W,
+				 int C, int OC, int KH, int KW, int stride, int pad, int n_threads);
+void oracle_maxpool2d_f32(const float *x, float *y, int N, int H, int W, int C, int kernel,
+			  int stride);
+
 #endif /* SAM3_ORACLE_H */

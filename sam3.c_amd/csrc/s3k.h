@@ -148,6 +148,14 @@ int s3k_conv_implicit(const struct s3k_conv *c, const void *xa, const void *wb, 
 int s3k_conv_im2col(const struct s3k_conv *c, void *col, int Kp, void *stream);
 int s3k_conv_wprep(int kind, const void *w, void *out, int OC, int K, int Kp, void *stream);
 int s3k_conv_direct(const struct s3k_conv *c, void *stream);
+/* ConvTranspose2D (reference gather order, bit-exact f32) and MaxPool2D,
+ * NHWC f32 (neck.hip); b repeated `times` times. */
+int s3k_conv_transpose_direct(const float *x, const float *w, float *y, int N, int H, int W, int C,
+			      int OC, int KH, int KW, int stride, int pad, int OH, int OW,
+			      void *stream);
+int s3k_maxpool2d(const float *x, float *y, int N, int H, int W, int C, int kernel, int stride,
+		  int OH, int OW, void *stream);
+int s3k_repeat_f32(const float *b, float *out, int n, int times, void *stream);
 /* batch slices of [rows, cols] -> [cols, rows] */
 int s3k_transpose2d(int esize, const void *src, void *dst, int batch, int rows,
 		    int cols, void *stream);

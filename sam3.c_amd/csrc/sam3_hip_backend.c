@@ -72,6 +72,7 @@ struct s3h_prep {
 	const char *src;
 	int tag, rows, k;
 	void *dev;
+	size_t bytes;
 };
 
 /* A host range copied to HBM once: [host, host + nbytes) -> dev. */
@@ -115,15 +116,19 @@ static struct s3h_res *res_find(struct sam3_hip_backend *hb, const void *host)
 /* The backend whose graph_eval runs on this thread (prepared weights). */
 static _Thread_local struct sam3_hip_backend *s3h_cur;
 
-/* Drop the prepared copies whose source lies in device range [lo, hi). */
+/* Drop the prepared copies whose source lies in device range [lo, hi),
+ * and the copies prepared from those in turn. */
 static void prep_drop_range(struct sam3_hip_backend *hb, const char *lo, const char *hi)
 {
-	for (int i = hb->n_prep - 1; i >= 0; i--) {
+	for (int i = hb->n_prep - 1; i >= 0 && i < hb->n_prep; i--) {
 		if (hb->prep[i].src < lo || hb->prep[i].src >= hi)
 			continue;
-		(void)hipFreeAsync(hb->prep[i].dev, hb->stream);
+		const struct s3h_prep p = hb->prep[i];
 		hb->prep[i] = hb->prep[hb->n_prep - 1];
 		hb->n_prep--;
+		prep_drop_range(hb, p.dev, (const char *)p.dev + p.bytes);
+		(void)hipFreeAsync(p.dev, hb->stream);
+		i = hb->n_prep;
 	}
 }
 
@@ -614,11 +619,13 @@ static enum sam3_error run_layernorm_as(struct sam3_hip_backend *hb, const struc
 	return err;
 }
 
-/* CONV2D at node i, plus a following BIAS_ADD ([OC], used only there)
- * and GELU folded into the GEMM epilogue when the conv runs as a GEMM. */
+/* CONV2D or CONV_TRANSPOSE2D at node i, plus a following BIAS_ADD ([OC],
+ * used only there) and GELU folded into the GEMM epilogue when the conv
+ * runs as a GEMM. */
 static enum sam3_error run_conv(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
 				struct use_map *uses, int *used)
 {
+	const int transposed = g->nodes[i].op == SAM3_OP_CONV_TRANSPOSE2D;
 	const struct sam3_node *n = &g->nodes[i];
 	struct sam3_tensor tx = *n->inputs[0], tw = *n->inputs[1], ty = *n->output;
 	struct sam3_node dn = *n;
@@ -631,7 +638,7 @@ static enum sam3_error run_conv(struct sam3_hip_backend *hb, const struct sam3_g
 	dn.inputs[1] = &tw;
 	dn.output = &ty;
 	/* the kernel choice looks at the device addresses */
-	const int path = s3h_conv2d_path(&dn);
+	const int path = transposed ? s3h_conv_transpose2d_path(&dn) : s3h_conv2d_path(&dn);
 	const struct sam3_tensor *out = n->output, *bias = NULL;
 	const long long ny = s3h_nelems(out);
 	int flags = 0, j = i + 1;
@@ -660,7 +667,8 @@ static enum sam3_error run_conv(struct sam3_hip_backend *hb, const struct sam3_g
 		err = dev_out(hb, out, &ty.data);
 	if (err != SAM3_OK)
 		return err;
-	err = s3h_conv2d(&dn, dbias, flags, path, hb->stream);
+	err = transposed ? s3h_conv_transpose2d(&dn, dbias, flags, path, hb->stream)
+			 : s3h_conv2d(&dn, dbias, flags, path, hb->stream);
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.fused_nodes += j - i - 1;
@@ -708,6 +716,8 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 		err = s3h_slice(&dn, hb->stream);
 	else if (n->op == SAM3_OP_BIAS_ADD)
 		err = s3h_bias_add(&dn, hb->stream);
+	else if (n->op == SAM3_OP_MAXPOOL2D)
+		err = s3h_maxpool2d(&dn, hb->stream);
 	else
 		err = s3h_transpose(&dn, hb->stream);
 	if (err == SAM3_OK)
@@ -733,6 +743,8 @@ static int runs_on_gpu(const struct sam3_node *n)
 		return float_dt(dt);
 	case SAM3_OP_BIAS_ADD:
 		return s3h_bias_add_ok(n);
+	case SAM3_OP_MAXPOOL2D:
+		return s3h_maxpool2d_ok(n);
 	case SAM3_OP_TRANSPOSE:
 		return s3h_transpose_ok(n);
 	case SAM3_OP_LAYERNORM:
@@ -826,7 +838,8 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 			hb->stats.fused_nodes++;
 		} else if (n->op == SAM3_OP_MATMUL) {
 			err = run_matmul(hb, g, i, folded, &uses, &used);
-		} else if (n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) {
+		} else if ((n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) ||
+			   (n->op == SAM3_OP_CONV_TRANSPOSE2D && s3h_conv_transpose2d_ok(n))) {
 			err = run_conv(hb, g, i, &uses, &used);
 		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain &&
 			   (ln_fmt = ln_operand_form(hb, g, i, &uses)) != S3H_A_PLAIN) {
@@ -1302,10 +1315,16 @@ int s3h_prep_cacheable(const void *src, size_t src_bytes)
 		if (d && c >= d && c < d + e->nbytes && src_bytes <= e->nbytes - (size_t)(c - d))
 			return e->keep && !e->written && e->dev_valid;
 	}
+	/* a prepared copy is itself constant */
+	for (int i = 0; i < hb->n_prep; i++) {
+		const char *d = (const char *)hb->prep[i].dev;
+		if (c >= d && c < d + hb->prep[i].bytes && src_bytes <= hb->prep[i].bytes - (size_t)(c - d))
+			return 1;
+	}
 	return 0;
 }
 
-enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev)
+enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev, size_t bytes)
 {
 	struct sam3_hip_backend *hb = s3h_cur;
 	if (!hb) {
@@ -1322,6 +1341,6 @@ enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *
 		hb->prep = p;
 		hb->cap_prep = cap;
 	}
-	hb->prep[hb->n_prep++] = (struct s3h_prep){(const char *)src, tag, rows, k, dev};
+	hb->prep[hb->n_prep++] = (struct s3h_prep){(const char *)src, tag, rows, k, dev, bytes};
 	return SAM3_OK;
 }

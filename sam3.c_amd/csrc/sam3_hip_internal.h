@@ -47,6 +47,17 @@ int s3h_conv2d_ok(const struct sam3_node *node);
 int s3h_conv2d_path(const struct sam3_node *node);
 enum sam3_error s3h_conv2d(const struct sam3_node *node, const void *bias, int flags, int path,
 			   void *stream);
+/* CONV_TRANSPOSE2D and MAXPOOL2D (NHWC, F32). s3h_conv_transpose2d runs
+ * path 0 (the best), S3H_CONVT_GEMM (stride = KH = KW, pad 0: one GEMM and
+ * a pixel-shuffle permute; bias/flags fold a BIAS_ADD and GELU) or
+ * S3H_CONVT_DIRECT. */
+enum { S3H_CONVT_GEMM = 1, S3H_CONVT_DIRECT = 3 };
+int s3h_conv_transpose2d_ok(const struct sam3_node *node);
+int s3h_conv_transpose2d_path(const struct sam3_node *node);
+enum sam3_error s3h_conv_transpose2d(const struct sam3_node *node, const void *bias, int flags,
+				     int path, void *stream);
+int s3h_maxpool2d_ok(const struct sam3_node *node);
+enum sam3_error s3h_maxpool2d(const struct sam3_node *node, void *stream);
 int s3h_bias_add_ok(const struct sam3_node *node);
 enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
 
@@ -71,10 +82,11 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 enum { S3H_PREP_SPLIT_W = 1,   /* f32 [rows, k] -> bf16 [rows, 3k] = [hi|hi|lo] */
        S3H_PREP_PAD_PLANES,    /* f32 [rows, K] -> bf16 [rows, 3k] over k >= K, zero padded */
        S3H_PREP_PAD16,         /* 16-bit [rows, K] -> [rows, k], zero padded */
-       S3H_PREP_Q8_F16 };      /* Q8_0 [rows, k] -> f16 [rows, k] (q*scale)   */
+       S3H_PREP_Q8_F16,        /* Q8_0 [rows, k] -> f16 [rows, k] (q*scale)   */
+       S3H_PREP_CONVT_W };     /* OHWI [OC, taps, C] -> [taps*OC, C]           */
 void *s3h_prep_find(const void *src, int tag, int rows, int k);
 int s3h_prep_cacheable(const void *src, size_t src_bytes);
-enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev);
+enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev, size_t bytes);
 
 /* Bulk host -> device copies through pinned staging buffers (upload.c).
  * Lanes and chunk size default to S3H_STAGE_LANES x S3H_STAGE_CHUNK_MB;

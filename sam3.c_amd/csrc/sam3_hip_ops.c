@@ -209,7 +209,7 @@ static enum sam3_error prep_weight(const void *w, size_t w_bytes, int tag, int r
 	if (err == SAM3_OK)
 		err = s3h_hip(fn(w, *out, rows, k, k_out, kind, stream), "weight preparation");
 	if (err == SAM3_OK && s3h_prep_cacheable(w, w_bytes)) {
-		err = s3h_prep_store(w, tag, rows, k_out, *out);
+		err = s3h_prep_store(w, tag, rows, k_out, *out, out_bytes);
 		*own = err != SAM3_OK;
 	} else {
 		*own = 1;
@@ -1289,6 +1289,218 @@ enum sam3_error sam3_hip_kernel_bias_add(const struct sam3_node *node, void *str
 	return s3h_bias_add(node, stream);
 }
 
+/* CONV_TRANSPOSE2D as cpu_kernel_conv_transpose2d reads it
+ * (cpu_conv_transpose2d.c:140-217): x [N,H,W,C], w OHWI [OC,KH,KW,C],
+ * y [N,OH,OW,OC] with OH = (H-1)*stride - 2*pad + KH (the output must
+ * have that shape); params stride (<= 0 -> 1), pad; F32 only
+ * (cpu_dispatch.c:553-555). */
+struct convt_shape {
+	const float *x, *w;
+	float *y;
+	int N, H, W, C, OC, KH, KW, stride, pad, OH, OW;
+};
+
+static enum sam3_error convt_shape(const struct sam3_node *node, struct convt_shape *c, int quiet)
+{
+#define CT_FAIL(code, ...)                      \
+	do {                                    \
+		if (!quiet)                     \
+			s3h_error(__VA_ARGS__); \
+		return code;                    \
+	} while (0)
+	if (!node || node->n_inputs < 2 || !node->inputs[0] || !node->inputs[1] || !node->output)
+		CT_FAIL(SAM3_EINVAL, "conv_transpose2d: NULL tensor");
+	const struct sam3_tensor *x = node->inputs[0], *w = node->inputs[1], *y = node->output;
+	if (x->dtype != SAM3_DTYPE_F32 || w->dtype != SAM3_DTYPE_F32 || y->dtype != SAM3_DTYPE_F32)
+		CT_FAIL(SAM3_EDTYPE, "conv_transpose2d: F32 only (got %d, %d, %d)", x->dtype, w->dtype,
+			y->dtype);
+	if (x->n_dims != 4 || w->n_dims != 4 || y->n_dims != 4)
+		CT_FAIL(SAM3_EINVAL, "conv_transpose2d: expected 4D tensors");
+	memset(c, 0, sizeof(*c));
+	c->x = x->data;
+	c->w = w->data;
+	c->y = y->data;
+	c->N = x->dims[0];
+	c->H = x->dims[1];
+	c->W = x->dims[2];
+	c->C = x->dims[3];
+	c->OC = w->dims[0];
+	c->KH = w->dims[1];
+	c->KW = w->dims[2];
+	c->stride = node->params[0] > 0 ? node->params[0] : 1;
+	c->pad = node->params[1];
+	if (w->dims[3] != c->C)
+		CT_FAIL(SAM3_EINVAL, "conv_transpose2d: channel mismatch %d != %d", w->dims[3], c->C);
+	c->OH = (c->H - 1) * c->stride - 2 * c->pad + c->KH;
+	c->OW = (c->W - 1) * c->stride - 2 * c->pad + c->KW;
+	if (y->dims[0] != c->N || y->dims[1] != c->OH || y->dims[2] != c->OW || y->dims[3] != c->OC)
+		CT_FAIL(SAM3_EINVAL, "conv_transpose2d: output shape mismatch");
+	if (c->N <= 0 || c->H <= 0 || c->W <= 0 || c->C <= 0 || c->OC <= 0 || c->KH <= 0 ||
+	    c->KW <= 0 || c->OH <= 0 || c->OW <= 0 ||
+	    (long long)c->N * c->OH * c->OW * c->OC > INT32_MAX ||
+	    (long long)c->N * c->H * c->W * c->C > INT32_MAX)
+		CT_FAIL(SAM3_EINVAL, "conv_transpose2d: empty or oversized tensor");
+	return SAM3_OK;
+#undef CT_FAIL
+}
+
+static int convt_gemm_ok(const struct convt_shape *c)
+{
+	const long long M = (long long)c->N * c->H * c->W, T = (long long)c->KH * c->KW;
+	return c->stride == c->KH && c->stride == c->KW && c->pad == 0 && c->C % 8 == 0 &&
+	       !(((uintptr_t)c->x | (uintptr_t)c->w | (uintptr_t)c->y) & 15u) &&
+	       M * T * c->OC * 4 <= 0x7FFFFFF0LL && T * c->OC * c->C * 4 <= 0x7FFFFFF0LL;
+}
+
+static int convt_path_of(const struct convt_shape *c)
+{
+	const long long macs = (long long)c->N * c->H * c->W * c->KH * c->KW * c->OC * c->C;
+	return convt_gemm_ok(c) && macs >= (1LL << 22) ? S3H_CONVT_GEMM : S3H_CONVT_DIRECT;
+}
+
+int s3h_conv_transpose2d_ok(const struct sam3_node *node)
+{
+	struct convt_shape c;
+	return convt_shape(node, &c, 1) == SAM3_OK;
+}
+
+int s3h_conv_transpose2d_path(const struct sam3_node *node)
+{
+	struct convt_shape c;
+	return convt_shape(node, &c, 1) == SAM3_OK ? convt_path_of(&c) : 0;
+}
+
+/* OHWI [OC, taps, C] -> [taps * OC, C]: row t*OC + oc is tap t of filter oc */
+static int prep_convt_w(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
+{
+	(void)kind;
+	const int dims[3] = {rows, k_out, k}, axes[3] = {1, 0, 2};
+	return s3k_permute(4, w, out, 3, dims, axes, stream);
+}
+
+enum sam3_error s3h_conv_transpose2d(const struct sam3_node *node, const void *bias, int flags,
+				     int path, void *stream)
+{
+	struct convt_shape c;
+	enum sam3_error err = convt_shape(node, &c, 0);
+	if (err != SAM3_OK)
+		return err;
+	if (path == 0)
+		path = convt_path_of(&c);
+	if (path == S3H_CONVT_DIRECT) {
+		if (flags) {
+			s3h_error("conv_transpose2d: the direct kernel has no fused epilogue");
+			return SAM3_EINVAL;
+		}
+		return s3h_hip(s3k_conv_transpose_direct(c.x, c.w, c.y, c.N, c.H, c.W, c.C, c.OC, c.KH,
+							 c.KW, c.stride, c.pad, c.OH, c.OW, stream),
+			       "conv_transpose2d direct");
+	}
+	if (path != S3H_CONVT_GEMM || !convt_gemm_ok(&c)) {
+		s3h_error("conv_transpose2d: path %d cannot run this problem", path);
+		return SAM3_EINVAL;
+	}
+	if ((flags & S3K_EPI_BIAS) && !bias) {
+		s3h_error("conv_transpose2d: NULL bias");
+		return SAM3_EINVAL;
+	}
+	/* Each input pixel times W' [taps*OC, C] gives its taps' output
+	 * pixels: tmp [N*H*W, taps*OC], then [N*H, W, KH, KW*OC] ->
+	 * [N*H, KH, W, KW*OC] is y. */
+	const int T = c.KH * c.KW, M = c.N * c.H * c.W, NN = T * c.OC;
+	void *wt = NULL, *tmp = NULL, *b4 = NULL;
+	int own_w = 0;
+	err = prep_weight(c.w, (size_t)c.OC * T * c.C * 4, S3H_PREP_CONVT_W, c.OC, c.C, T,
+			  (size_t)NN * c.C * 4, S3K_F32, prep_convt_w, stream, &wt, &own_w);
+	if (err == SAM3_OK)
+		err = s3h_scratch_alloc(&tmp, (size_t)M * NN * 4, stream);
+	if (err == SAM3_OK && (flags & S3K_EPI_BIAS)) {
+		err = s3h_scratch_alloc(&b4, (size_t)NN * 4, stream);
+		if (err == SAM3_OK)
+			err = s3h_hip(s3k_repeat_f32((const float *)bias, b4, c.OC, T, stream),
+				      "conv_transpose2d bias");
+	}
+	if (err == SAM3_OK)
+		err = matmul_impl(0, SAM3_DTYPE_F32, c.x, SAM3_DTYPE_F32, wt, SAM3_DTYPE_F32, tmp, M, NN,
+				  c.C, b4, (flags & (S3K_EPI_BIAS | S3K_EPI_GELU)) | SAM3_HIP_B_NT, stream);
+	if (err == SAM3_OK) {
+		const int dims[4] = {c.N * c.H, c.W, c.KH, c.KW * c.OC}, axes[4] = {0, 2, 1, 3};
+		err = s3h_hip(s3k_permute(4, tmp, c.y, 4, dims, axes, stream), "conv_transpose2d shuffle");
+	}
+	err = free_scratch(b4, stream, err);
+	err = free_scratch(tmp, stream, err);
+	return free_scratch(own_w ? wt : NULL, stream, err);
+}
+
+enum sam3_error sam3_hip_kernel_conv_transpose2d(const struct sam3_node *node, void *stream)
+{
+	return s3h_conv_transpose2d(node, NULL, 0, 0, stream);
+}
+
+enum sam3_error sam3_hip_conv_transpose2d_on_path(int path, const struct sam3_node *node,
+						  void *stream)
+{
+	return s3h_conv_transpose2d(node, NULL, 0, path, stream);
+}
+
+int sam3_hip_conv_transpose2d_path(const struct sam3_node *node)
+{
+	return s3h_conv_transpose2d_path(node);
+}
+
+/* MAXPOOL2D as cpu_kernel_maxpool2d reads it (cpu_maxpool2d.c:113-177):
+ * params kernel (<= 0 -> 2), stride (<= 0 -> kernel); OH = (H - kernel)
+ * / stride + 1; F32 only (cpu_dispatch.c:556-558). */
+static enum sam3_error maxpool_shape(const struct sam3_node *node, int *k, int *st, int quiet)
+{
+	if (!node || node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		if (!quiet)
+			s3h_error("maxpool2d: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *x = node->inputs[0], *y = node->output;
+	if (x->dtype != SAM3_DTYPE_F32 || y->dtype != SAM3_DTYPE_F32) {
+		if (!quiet)
+			s3h_error("maxpool2d: F32 only");
+		return SAM3_EDTYPE;
+	}
+	*k = node->params[0] > 0 ? node->params[0] : 2;
+	*st = node->params[1] > 0 ? node->params[1] : *k;
+	const int OH = x->n_dims == 4 ? (x->dims[1] - *k) / *st + 1 : 0;
+	const int OW = x->n_dims == 4 ? (x->dims[2] - *k) / *st + 1 : 0;
+	if (x->n_dims != 4 || y->n_dims != 4 || x->dims[1] < *k || x->dims[2] < *k ||
+	    y->dims[0] != x->dims[0] || y->dims[1] != OH || y->dims[2] != OW ||
+	    y->dims[3] != x->dims[3]) {
+		if (!quiet)
+			s3h_error("maxpool2d: expected 4D tensors and output [N, OH, OW, C]");
+		return SAM3_EINVAL;
+	}
+	return SAM3_OK;
+}
+
+int s3h_maxpool2d_ok(const struct sam3_node *node)
+{
+	int k, st;
+	return maxpool_shape(node, &k, &st, 1) == SAM3_OK;
+}
+
+enum sam3_error s3h_maxpool2d(const struct sam3_node *node, void *stream)
+{
+	int k, st;
+	enum sam3_error err = maxpool_shape(node, &k, &st, 0);
+	if (err != SAM3_OK)
+		return err;
+	const struct sam3_tensor *x = node->inputs[0], *y = node->output;
+	return s3h_hip(s3k_maxpool2d(x->data, y->data, x->dims[0], x->dims[1], x->dims[2], x->dims[3], k,
+				     st, y->dims[1], y->dims[2], stream),
+		       "maxpool2d");
+}
+
+enum sam3_error sam3_hip_kernel_maxpool2d(const struct sam3_node *node, void *stream)
+{
+	return s3h_maxpool2d(node, stream);
+}
+
 enum sam3_error sam3_hip_kernel_layernorm(const struct sam3_node *node, void *stream)
 {
 	return node ? s3h_layernorm(node, stream) : (s3h_error("layernorm: NULL node"), SAM3_EINVAL);
@@ -1456,6 +1668,14 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 	case SAM3_OP_BIAS_ADD:
 		if (is_float_dtype(dtype))
 			return s3h_bias_add(node, stream);
+		break;
+	case SAM3_OP_CONV_TRANSPOSE2D:
+		if (dtype == SAM3_DTYPE_F32)
+			return s3h_conv_transpose2d(node, NULL, 0, 0, stream);
+		break;
+	case SAM3_OP_MAXPOOL2D:
+		if (dtype == SAM3_DTYPE_F32)
+			return s3h_maxpool2d(node, stream);
 		break;
 	default:
 		break;

@@ -39,6 +39,10 @@ SIGNATURES = {
     "sam3_hip_conv2d_path": (_i, [_vp]),
     "sam3_hip_conv2d_on_path": (_i, [_i, _vp, _vp]),
     "sam3_hip_kernel_bias_add": (_i, [_vp, _vp]),
+    "sam3_hip_kernel_conv_transpose2d": (_i, [_vp, _vp]),
+    "sam3_hip_conv_transpose2d_path": (_i, [_vp]),
+    "sam3_hip_conv_transpose2d_on_path": (_i, [_i, _vp, _vp]),
+    "sam3_hip_kernel_maxpool2d": (_i, [_vp, _vp]),
     "sam3_hip_kernel_layernorm": (_i, [_vp, _vp]),
     "sam3_hip_kernel_rope": (_i, [_vp, _vp]),
     "sam3_hip_kernel_slice": (_i, [_vp, _vp]),

@@ -214,6 +214,25 @@ def main():
         assert rc == 0
         g[f"conv_p1_{kind}_x"], g[f"conv_p1_{kind}_w"], g[f"conv_p1_{kind}_y"] = xb, wb, y
 
+    # -- ConvTranspose2D (the neck's 2x2 stride 2, and an overlapping 3x3
+    # stride 2 pad 1) and MaxPool2D with NaNs in and out of first taps
+    for i, (key, xs, ws, st, pd) in enumerate([("k2", (1, 5, 6, 8), (4, 2, 2, 8), 2, 0),
+                                               ("k3", (2, 4, 4, 3), (5, 3, 3, 3), 2, 1)]):
+        x = synth.randn(synth.tensor_seed(95 + i, 0), xs)
+        w = synth.randn(synth.tensor_seed(95 + i, 1), ws, 0.2)
+        rc, y = R.conv_transpose2d(x, w, st, pd)
+        assert rc == 0
+        g[f"convt_{key}_x"], g[f"convt_{key}_w"], g[f"convt_{key}_y"] = x, w, y
+        g[f"convt_{key}_p"] = np.array([st, pd], np.int32)
+    x = synth.randn(synth.tensor_seed(97, 0), (2, 9, 7, 5))
+    x[0, 0, 0, 0] = np.nan
+    x[1, 2, 3, 1] = np.nan
+    g["maxpool_x"] = x
+    for k, st in ((2, 2), (3, 2)):
+        rc, y = R.maxpool2d(x, k, st)
+        assert rc == 0
+        g[f"maxpool_{k}{st}_y"] = y
+
     R.close()
     out = HERE / "matmul_golden.npz"
     np.savez_compressed(out, **g)

@@ -235,6 +235,34 @@ def _oracle_conv2d(self, x, w, stride=1, ph=0, pw=None, groups=1, kind="f32", ou
 Oracle.conv2d = _oracle_conv2d
 
 
+def _oracle_conv_transpose2d(self, x, w, stride=1, pad=0, threads=8):
+    """x [N,H,W,C], w [OC,KH,KW,C] f32 -> [N,OH,OW,OC]."""
+    N, H, W, C = x.shape
+    OC, KH, KW, _ = w.shape
+    OH, OW = (H - 1) * stride - 2 * pad + KH, (W - 1) * stride - 2 * pad + KW
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    y = np.zeros((N, OH, OW, OC), np.float32)
+    fn = self.lib.oracle_conv_transpose2d_f32
+    fn.argtypes = [_vp, _vp, _vp] + [_i] * 10
+    fn(_ptr(x), _ptr(w), _ptr(y), N, H, W, C, OC, KH, KW, stride, pad, threads)
+    return y
+
+
+def _oracle_maxpool2d(self, x, kernel=2, stride=None):
+    stride = stride or kernel
+    N, H, W, C = x.shape
+    x = _c(x, np.float32)
+    y = np.zeros((N, (H - kernel) // stride + 1, (W - kernel) // stride + 1, C), np.float32)
+    fn = self.lib.oracle_maxpool2d_f32
+    fn.argtypes = [_vp, _vp] + [_i] * 6
+    fn(_ptr(x), _ptr(y), N, H, W, C, kernel, stride)
+    return y
+
+
+Oracle.conv_transpose2d = _oracle_conv_transpose2d
+Oracle.maxpool2d = _oracle_maxpool2d
+
+
 class Ref:
     """The reference's own kernels, called through hand-built nodes."""
 
@@ -333,6 +361,33 @@ class Ref:
             rc = self.lib.cpu_dispatch_node(C.byref(node), C.byref(arena), self.pool(threads))
         finally:
             self.lib.sam3_arena_free(C.byref(arena))
+        return rc, y
+
+    def conv_transpose2d(self, x, w, stride=1, pad=0, threads=8):
+        """cpu_dispatch_node on a CONV_TRANSPOSE2D node (f32)."""
+        N, H, W, Cin = x.shape
+        OC, KH, KW, _ = w.shape
+        OH, OW = (H - 1) * stride - 2 * pad + KH, (W - 1) * stride - 2 * pad + KW
+        xa, wa = _c(x, np.float32), _c(w, np.float32)
+        y = np.zeros((N, OH, OW, OC), np.float32)
+        tx = abi.make_tensor(abi.F32, [N, H, W, Cin], xa.ctypes.data, xa.nbytes)
+        tw = abi.make_tensor(abi.F32, [OC, KH, KW, Cin], wa.ctypes.data, wa.nbytes)
+        ty = abi.make_tensor(abi.F32, [N, OH, OW, OC], y.ctypes.data, y.nbytes)
+        node = abi.make_node(abi.OP_CONV_TRANSPOSE2D, [tx, tw], ty, (stride, pad, 0, 0))
+        scratch = (C.c_char * 64)()
+        rc = self.lib.cpu_dispatch_node(C.byref(node), C.byref(scratch), self.pool(threads))
+        return rc, y
+
+    def maxpool2d(self, x, kernel=2, stride=0):
+        N, H, W, Cin = x.shape
+        k, st = kernel, stride or kernel
+        xa = _c(x, np.float32)
+        y = np.zeros((N, (H - k) // st + 1, (W - k) // st + 1, Cin), np.float32)
+        tx = abi.make_tensor(abi.F32, [N, H, W, Cin], xa.ctypes.data, xa.nbytes)
+        ty = abi.make_tensor(abi.F32, list(y.shape), y.ctypes.data, y.nbytes)
+        node = abi.make_node(abi.OP_MAXPOOL2D, [tx], ty, (kernel, stride, 0, 0))
+        scratch = (C.c_char * 64)()
+        rc = self.lib.cpu_dispatch_node(C.byref(node), C.byref(scratch), self.pool(4))
         return rc, y
 
     def matmul_f32(self, a, b, threads=None):

@@ -189,3 +189,106 @@ def test_neck_conv3x3_full_size():
     got = gpu_conv(x, w, 1, 1, None, 1, "f32", IMPLICIT)
     ref = oracle().conv2d(np.ascontiguousarray(x[:, :7]), w, 1, 1)
     assert_f32_close(got[:, :5], ref[:, :5], what="neck 3x3 rows 0-4")
+
+
+# ---------------------------------------------- ConvTranspose2D and MaxPool2D
+CONVT_GEMM, CONVT_DIRECT = 1, 3
+
+
+def gpu_node(op, ins, out_shape, params):
+    """Run one node kernel on device copies of f32 arrays."""
+    bufs = [hip.DeviceBuffer.of(np.ascontiguousarray(a, np.float32)) for a in ins]
+    by = hip.DeviceBuffer(int(np.prod(out_shape)) * 4)
+    try:
+        ts = [abi.make_tensor(abi.F32, list(a.shape), b.ptr, a.nbytes) for a, b in zip(ins, bufs)]
+        ty = abi.make_tensor(abi.F32, list(out_shape), by.ptr, by.nbytes)
+        node = abi.make_node(op, ts, ty, params)
+        return (node, ts, ty), bufs, by
+    except Exception:
+        for b in bufs + [by]:
+            b.free()
+        raise
+
+
+@pytest.mark.parametrize("shape", [((1, 12, 10, 64), (32, 2, 2, 64), 2, 0, (CONVT_GEMM, CONVT_DIRECT)),
+                                   ((2, 9, 7, 24), (16, 2, 2, 24), 2, 0, (CONVT_GEMM, CONVT_DIRECT)),
+                                   ((1, 5, 6, 8), (4, 3, 3, 8), 2, 1, (CONVT_DIRECT,)),
+                                   ((1, 4, 5, 6), (3, 3, 3, 6), 1, 1, (CONVT_DIRECT,))],
+                         ids=["k2_c64", "k2_ragged", "k3_s2_p1", "k3_s1"])
+def test_conv_transpose2d_vs_oracle(shape):
+    xs, ws, st, pd, paths = shape
+    x, w = synth.randn(400, xs), synth.randn(401, ws, 0.1)
+    ref = oracle().conv_transpose2d(x, w, st, pd)
+    lib = hip.load()
+    for path in paths:
+        (node, ts, ty), bufs, by = gpu_node(abi.OP_CONV_TRANSPOSE2D, [x, w], ref.shape, (st, pd, 0, 0))
+        try:
+            hip.check(lib.sam3_hip_conv_transpose2d_on_path(path, C.byref(node), None), "convT")
+            hip.synchronize()
+            got = by.download(np.float32, ref.shape)
+        finally:
+            for b in bufs + [by]:
+                b.free()
+        if path == CONVT_DIRECT:
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "direct"
+        else:
+            assert_f32_close(got, ref, what="convT gemm")
+
+
+def test_maxpool2d_bit_exact():
+    x = synth.randn(410, (2, 17, 13, 40))
+    x[0, 0, 0, :3] = np.nan
+    x[1, 5, 6, 7] = np.nan
+    lib = hip.load()
+    for k, st in ((2, 2), (3, 2), (2, 1)):
+        ref = oracle().maxpool2d(x, k, st)
+        (node, ts, ty), bufs, by = gpu_node(abi.OP_MAXPOOL2D, [x], ref.shape, (k, st, 0, 0))
+        try:
+            hip.check(lib.sam3_hip_kernel_maxpool2d(C.byref(node), None), "maxpool")
+            hip.synchronize()
+            got = by.download(np.float32, ref.shape)
+        finally:
+            for b in bufs + [by]:
+                b.free()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (k, st)
+
+
+def test_neck_stage_4x_in_graph():
+    """The neck's 4x scale (necks.c:330-365): ConvTranspose2D 2x2 s2
+    (+bias) -> GELU -> ConvTranspose2D 2x2 s2 (+bias) -> Conv2D 1x1
+    (+bias) -> Conv2D 3x3 pad 1 (+bias), on a 12x12x128 map (scaled-down
+    channels), all on the GPU with the bias and GELU folded; against the
+    oracle's kernels in f32."""
+    from sam3_amd import graph
+    O = oracle()
+    x = synth.randn(420, (1, 12, 12, 128))
+    w1, b1 = synth.randn(421, (64, 2, 2, 128), 0.05), synth.randn(422, (64,), 0.1)
+    w2, b2 = synth.randn(423, (32, 2, 2, 64), 0.05), synth.randn(424, (32,), 0.1)
+    w3, b3 = synth.randn(425, (64, 1, 1, 32), 0.1), synth.randn(426, (64,), 0.1)
+    w4, b4 = synth.randn(427, (64, 3, 3, 64), 0.05), synth.randn(428, (64,), 0.1)
+    G = graph.Graph()
+    F = abi.F32
+    t = G.tensor(F, x.shape, x)
+    t = G.node(abi.OP_CONV_TRANSPOSE2D, [t, G.tensor(F, w1.shape, w1)], G.tensor(F, (1, 24, 24, 64)), (2, 0, 0, 0))
+    t = G.node(abi.OP_BIAS_ADD, [t, G.tensor(F, (64,), b1)], G.tensor(F, (1, 24, 24, 64)))
+    t = G.node(abi.OP_GELU, [t], G.tensor(F, (1, 24, 24, 64)))
+    t = G.node(abi.OP_CONV_TRANSPOSE2D, [t, G.tensor(F, w2.shape, w2)], G.tensor(F, (1, 48, 48, 32)), (2, 0, 0, 0))
+    t = G.node(abi.OP_BIAS_ADD, [t, G.tensor(F, (32,), b2)], G.tensor(F, (1, 48, 48, 32)))
+    t = G.node(abi.OP_CONV2D, [t, G.tensor(F, w3.shape, w3)], G.tensor(F, (1, 48, 48, 64)), (1, 0, 1, 0))
+    t = G.node(abi.OP_BIAS_ADD, [t, G.tensor(F, (64,), b3)], G.tensor(F, (1, 48, 48, 64)))
+    t = G.node(abi.OP_CONV2D, [t, G.tensor(F, w4.shape, w4)], G.tensor(F, (1, 48, 48, 64)), (1, 1, 1, 0))
+    t = G.node(abi.OP_BIAS_ADD, [t, G.tensor(F, (64,), b4)], G.tensor(F, (1, 48, 48, 64)))
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G.g) == abi.OK
+        st = be.stats()
+    finally:
+        be.close()
+    assert st.host_nodes == 0 and st.downloads == 1
+    got = np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_float)), shape=(1, 48, 48, 64)).copy()
+    r = O.conv_transpose2d(x, w1, 2, 0)
+    r = O.gelu(O.bias_add(r.reshape(-1, 64), b1, "f32"), "f32").reshape(1, 24, 24, 64)
+    r = O.bias_add(O.conv_transpose2d(r, w2, 2, 0).reshape(-1, 32), b2, "f32").reshape(1, 48, 48, 32)
+    r = O.bias_add(O.conv2d(r, w3, 1, 0).reshape(-1, 64), b3, "f32").reshape(1, 48, 48, 64)
+    r = O.bias_add(O.conv2d(r, w4, 1, 1).reshape(-1, 64), b4, "f32").reshape(1, 48, 48, 64)
+    assert_f32_close(got, r, what="neck 4x stage")

@@ -436,3 +436,54 @@ def test_conv2d_closed_forms(O):
         xx, ww = synth.randn(105, xs), synth.randn(106, ws)
         got = O.conv2d(xx, ww, st, ph, pw, gr).astype(np.float64)
         assert np.allclose(got, conv_f64(xx, ww, st, ph, pw, gr), rtol=1e-5, atol=1e-5)
+
+
+# ---- ConvTranspose2D and MaxPool2D (cpu_conv_transpose2d.c, cpu_maxpool2d.c) ----
+
+@pytest.mark.parametrize("key", ["k2", "k3"])
+def test_golden_conv_transpose2d(O, key):
+    x, w, y = GOLD[f"convt_{key}_x"], GOLD[f"convt_{key}_w"], GOLD[f"convt_{key}_y"]
+    st, pd = (int(v) for v in GOLD[f"convt_{key}_p"])
+    assert np.array_equal(bits32(O.conv_transpose2d(x, w, st, pd, threads=3)), bits32(y))
+
+
+@pytest.mark.parametrize("k,st", [(2, 2), (3, 2)])
+def test_golden_maxpool2d(O, k, st):
+    assert np.array_equal(bits32(O.maxpool2d(GOLD["maxpool_x"], k, st)),
+                          bits32(GOLD[f"maxpool_{k}{st}_y"]))
+
+
+@pytest.mark.parametrize("shape", [((1, 5, 6, 8), (4, 2, 2, 8), 2, 0),
+                                   ((2, 4, 4, 3), (5, 3, 3, 3), 2, 1),
+                                   ((1, 4, 5, 6), (3, 3, 3, 6), 1, 1)])
+def test_ref_conv_transpose2d(O, R, shape):
+    xs, ws, st, pd = shape
+    x, w = synth.randn(110, xs), synth.randn(111, ws, 0.2)
+    rc, y = R.conv_transpose2d(x, w, st, pd)
+    assert rc == 0
+    assert np.array_equal(bits32(O.conv_transpose2d(x, w, st, pd)), bits32(y))
+
+
+def test_conv_transpose2d_closed_forms(O):
+    """stride = kernel, no padding: each output pixel is one input pixel
+    times one tap's [OC, C] slice (float64); an overlapping transposed
+    conv equals the scatter-add definition (float64)."""
+    x, w = synth.randn(112, (1, 3, 4, 5)), synth.randn(113, (6, 2, 2, 5))
+    y = O.conv_transpose2d(x, w, 2, 0).astype(np.float64)
+    ref = np.einsum("nhwc,okjc->nhkwjo", x.astype(np.float64), w.astype(np.float64))
+    assert np.allclose(y, ref.reshape(1, 6, 8, 6), rtol=1e-5, atol=1e-6)
+    x, w = synth.randn(114, (1, 3, 3, 2)), synth.randn(115, (2, 3, 3, 2))
+    st, pd = 2, 1
+    full = np.zeros((1, (3 - 1) * st + 3, (3 - 1) * st + 3, 2))
+    for h in range(3):
+        for ww in range(3):
+            full[0, h * st:h * st + 3, ww * st:ww * st + 3] += np.einsum(
+                "c,okjc->kjo", x[0, h, ww].astype(np.float64), w.astype(np.float64))
+    ref = full[:, pd:full.shape[1] - pd, pd:full.shape[2] - pd]
+    assert np.allclose(O.conv_transpose2d(x, w, st, pd), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_maxpool2d_closed_forms(O):
+    x = synth.randn(116, (2, 8, 6, 3))
+    ref = x.reshape(2, 4, 2, 3, 2, 3).max(axis=(2, 4))
+    assert np.array_equal(O.maxpool2d(x, 2, 2), ref)
