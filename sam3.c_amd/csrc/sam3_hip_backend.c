@@ -127,7 +127,7 @@ static void prep_drop_range(struct sam3_hip_backend *hb, const char *lo, const c
 		hb->prep[i] = hb->prep[hb->n_prep - 1];
 		hb->n_prep--;
 		prep_drop_range(hb, p.dev, (const char *)p.dev + p.bytes);
-		(void)hipFreeAsync(p.dev, hb->stream);
+		(void)s3h_scratch_free(p.dev, hb->stream);
 		i = hb->n_prep;
 	}
 }
@@ -137,7 +137,7 @@ static void res_drop_at(struct sam3_hip_backend *hb, int i)
 	if (hb->res[i].dev)
 		prep_drop_range(hb, hb->res[i].dev, (const char *)hb->res[i].dev + hb->res[i].nbytes);
 	if (hb->res[i].dev)
-		(void)hipFreeAsync(hb->res[i].dev, hb->stream);
+		(void)s3h_scratch_free(hb->res[i].dev, hb->stream);
 	hb->res[i] = hb->res[hb->n_res - 1];
 	hb->n_res--;
 }
@@ -963,6 +963,7 @@ static void hip_free(struct sam3_backend *be)
 	hb->n_prep = hb->cap_prep = 0;
 	s3h_stager_free(&hb->stager);
 	if (hb->stream) {
+		s3h_scratch_release(hb->stream);
 		(void)hipStreamSynchronize(hb->stream);
 		(void)hipStreamDestroy(hb->stream);
 		hb->stream = NULL;

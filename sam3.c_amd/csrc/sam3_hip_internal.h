@@ -22,9 +22,13 @@ enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
 int s3h_transpose_is_swap(const struct sam3_node *node);
-/* Stream-ordered device scratch from the default pool, kept mapped
- * between calls. */
+/* Device scratch reused in stream order: a block given back with
+ * s3h_scratch_free(p, stream) is handed out again only to requests on
+ * that stream. s3h_scratch_release(stream) returns the stream's idle
+ * blocks to the runtime (after synchronizing it). */
 enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream);
+enum sam3_error s3h_scratch_free(void *p, void *stream);
+void s3h_scratch_release(void *stream);
 
 /* ViT block ops on device pointers; the _ok forms say whether the node
  * runs on the GPU (dtypes and shapes), without reporting an error. */

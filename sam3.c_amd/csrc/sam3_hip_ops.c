@@ -19,6 +19,7 @@
 #include "s3k.h"
 
 #include <hip/hip_runtime_api.h>
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -50,28 +51,130 @@ enum sam3_error s3h_hip(int e, const char *what)
 	return e == hipErrorOutOfMemory ? SAM3_ENOMEM : SAM3_EBACKEND;
 }
 
-/* Stream-ordered scratch. The device's default memory pool returns
- * freed blocks to the system at every synchronization unless its release
- * threshold is raised; scratch of the same size is then mapped again on
- * the next call. The threshold is raised once per device (a repeated
- * store from two threads is harmless). */
-#define S3H_MAX_DEVICES 64
-static int s3h_pool_ready[S3H_MAX_DEVICES];
+/* Scratch blocks reused in stream order. A freed block goes back to a
+ * free list tagged with the device and the stream of its last use; a
+ * later request on that same stream may take it at once, because every
+ * kernel that used it was enqueued on that stream before the new user.
+ * Blocks are never handed to another stream. Requests take the smallest
+ * free block that fits and is at most twice the request (or 4 MiB
+ * larger); otherwise a new block is allocated with hipMalloc, after
+ * returning the idle blocks of the device to the runtime if the first
+ * attempt runs out of memory. This replaces stream-ordered
+ * hipMallocAsync / hipFreeAsync pairs, each of which left the GPU idle
+ * for about 5 us between the kernels around it. */
+struct s3h_blk {
+	void *p;
+	size_t n;
+	void *stream;
+	int dev;
+	int busy;
+};
+static struct s3h_blk *s3h_blks;
+static int s3h_nblks, s3h_capblks;
+static pthread_mutex_t s3h_blk_lock = PTHREAD_MUTEX_INITIALIZER;
+
+static size_t scratch_round(size_t n)
+{
+	const size_t g = n > ((size_t)1 << 20) ? ((size_t)1 << 20) : 256;
+	return n ? (n + g - 1) / g * g : g;
+}
+
+/* hipFree every idle block of device dev (all streams when stream_only
+ * is 0, else only those of `stream`), after the work using them is done.
+ * Called with the lock held. */
+static void scratch_trim_locked(int dev, int stream_only, void *stream)
+{
+	int synced = 0;
+	for (int i = s3h_nblks - 1; i >= 0; i--) {
+		struct s3h_blk *b = &s3h_blks[i];
+		if (b->busy || b->dev != dev || (stream_only && b->stream != stream))
+			continue;
+		if (!synced) {
+			if (stream_only)
+				(void)hipStreamSynchronize((hipStream_t)stream);
+			else
+				(void)hipDeviceSynchronize();
+			synced = 1;
+		}
+		(void)hipFree(b->p);
+		s3h_blks[i] = s3h_blks[--s3h_nblks];
+	}
+}
 
 enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
 {
 	int dev = 0;
-	if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < S3H_MAX_DEVICES &&
-	    !s3h_pool_ready[dev]) {
-		hipMemPool_t pool;
-		if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-			uint64_t keep = UINT64_MAX;
-			(void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-		}
-		(void)hipGetLastError();
-		s3h_pool_ready[dev] = 1;
+	(void)hipGetDevice(&dev);
+	const size_t need = scratch_round(nbytes);
+	const size_t most = need * 2 > need + ((size_t)4 << 20) ? need * 2 : need + ((size_t)4 << 20);
+	*p = NULL;
+	pthread_mutex_lock(&s3h_blk_lock);
+	int best = -1;
+	for (int i = 0; i < s3h_nblks; i++) {
+		const struct s3h_blk *b = &s3h_blks[i];
+		if (!b->busy && b->dev == dev && b->stream == stream && b->n >= need && b->n <= most &&
+		    (best < 0 || b->n < s3h_blks[best].n))
+			best = i;
 	}
-	return s3h_hip(hipMallocAsync(p, nbytes ? nbytes : 1, (hipStream_t)stream), "scratch");
+	if (best >= 0) {
+		s3h_blks[best].busy = 1;
+		*p = s3h_blks[best].p;
+		pthread_mutex_unlock(&s3h_blk_lock);
+		return SAM3_OK;
+	}
+	if (s3h_nblks == s3h_capblks) {
+		const int cap = s3h_capblks ? s3h_capblks * 2 : 64;
+		struct s3h_blk *t = realloc(s3h_blks, (size_t)cap * sizeof(*t));
+		if (!t) {
+			pthread_mutex_unlock(&s3h_blk_lock);
+			s3h_error("scratch: out of host memory for the block table");
+			return SAM3_ENOMEM;
+		}
+		s3h_blks = t;
+		s3h_capblks = cap;
+	}
+	void *q = NULL;
+	hipError_t e = hipMalloc(&q, need);
+	if (e == hipErrorOutOfMemory) {
+		(void)hipGetLastError();
+		scratch_trim_locked(dev, 0, NULL);
+		e = hipMalloc(&q, need);
+	}
+	if (e != hipSuccess) {
+		pthread_mutex_unlock(&s3h_blk_lock);
+		return s3h_hip(e, "scratch");
+	}
+	s3h_blks[s3h_nblks++] = (struct s3h_blk){q, need, stream, dev, 1};
+	*p = q;
+	pthread_mutex_unlock(&s3h_blk_lock);
+	return SAM3_OK;
+}
+
+enum sam3_error s3h_scratch_free(void *p, void *stream)
+{
+	if (!p)
+		return SAM3_OK;
+	pthread_mutex_lock(&s3h_blk_lock);
+	for (int i = 0; i < s3h_nblks; i++) {
+		if (s3h_blks[i].p == p) {
+			s3h_blks[i].busy = 0;
+			s3h_blks[i].stream = stream; /* its last use was enqueued here */
+			pthread_mutex_unlock(&s3h_blk_lock);
+			return SAM3_OK;
+		}
+	}
+	pthread_mutex_unlock(&s3h_blk_lock);
+	s3h_error("scratch: free of %p, which is not a scratch block", p);
+	return SAM3_EINVAL;
+}
+
+void s3h_scratch_release(void *stream)
+{
+	int dev = 0;
+	(void)hipGetDevice(&dev);
+	pthread_mutex_lock(&s3h_blk_lock);
+	scratch_trim_locked(dev, 1, stream);
+	pthread_mutex_unlock(&s3h_blk_lock);
 }
 
 /* ------------------------------------------------------------------ */
@@ -185,8 +288,7 @@ static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 			err = s3h_hip(s3k_gemm_launch_path(g, S3K_PATH_GENERIC, stream),
 				      "matmul_q8 generic");
 	}
-	enum sam3_error ferr = s3h_hip(hipFreeAsync(w16, (hipStream_t)stream),
-				       "matmul_q8 scratch free");
+	enum sam3_error ferr = s3h_scratch_free(w16, stream);
 	return err != SAM3_OK ? err : ferr;
 }
 
@@ -241,14 +343,17 @@ static int prep_q8_f16(const void *w, void *out, int rows, int k, int k_out, int
  * and rounded once to f16 (the direct Q8 kernel rounds the scale to f16
  * and multiplies in f16 at every k-step, one more rounding), and the f16
  * GEMM runs on it at the dense f16 rate, for 2 bytes per weight of HBM
- * instead of 1.125. SAM3_HIP_Q8_EXPAND=0, or a call outside graph_eval,
- * keeps the direct Q8 kernel. */
+ * instead of 1.125. Other calls keep the direct Q8 kernel: an expansion
+ * per call measured slower at every M (its two extra passes cost more
+ * than the direct kernel's in-loop dequantization). SAM3_HIP_Q8_EXPAND=0
+ * always keeps the direct kernel, =1 always expands. */
 static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 {
 	const char *env = getenv("SAM3_HIP_Q8_EXPAND");
+	const int mode = env ? atoi(env) : -1;
 	const size_t q8_bytes = (size_t)h->N * (h->K / 32) * 36;
-	if ((!env || atoi(env) != 0) && (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1 &&
-	    s3h_prep_cacheable(h->b, q8_bytes)) {
+	const int layout_ok = (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1;
+	if (layout_ok && mode != 0 && (mode == 1 || s3h_prep_cacheable(h->b, q8_bytes))) {
 		void *w16 = NULL;
 		int own = 0;
 		enum sam3_error err = prep_weight(h->b, q8_bytes, S3H_PREP_Q8_F16, h->N, h->K, h->K,
@@ -262,8 +367,7 @@ static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 			err = s3h_hip(s3k_gemm_launch_path(&e, S3K_PATH_MFMA, stream), "matmul_q8 f16 gemm");
 		}
 		if (own && w16) {
-			enum sam3_error e2 = s3h_hip(hipFreeAsync(w16, (hipStream_t)stream),
-						     "matmul_q8 weight scratch free");
+			enum sam3_error e2 = s3h_scratch_free(w16, stream);
 			if (err == SAM3_OK)
 				err = e2;
 		}
@@ -292,8 +396,7 @@ static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 		h.lda = g->K;
 		err = q8_f16_gemm(&h, stream);
 	}
-	enum sam3_error ferr = s3h_hip(hipFreeAsync(a16, (hipStream_t)stream),
-				       "matmul_q8 activation scratch free");
+	enum sam3_error ferr = s3h_scratch_free(a16, stream);
 	return err != SAM3_OK ? err : ferr;
 }
 
@@ -324,7 +427,6 @@ static int f32_split_wanted(const struct s3k_gemm *g)
  * NULL to split g->a here. */
 static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, const void *a_planes, void *stream)
 {
-	const hipStream_t st = (hipStream_t)stream;
 	const size_t abytes = (size_t)g->M * 3 * g->K * 2, bbytes = (size_t)g->N * 3 * g->K * 2;
 	void *a3 = NULL, *b3 = NULL;
 	int own_b = 1;
@@ -355,9 +457,9 @@ static enum sam3_error f32_split_gemm(const struct s3k_gemm *g, const void *a_pl
 	}
 	enum sam3_error ferr = SAM3_OK;
 	if (b3 && own_b)
-		ferr = s3h_hip(hipFreeAsync(b3, st), "matmul f32 split scratch free");
+		ferr = s3h_scratch_free(b3, stream);
 	if (a3) {
-		enum sam3_error e2 = s3h_hip(hipFreeAsync(a3, st), "matmul f32 split scratch free");
+		enum sam3_error e2 = s3h_scratch_free(a3, stream);
 		if (ferr == SAM3_OK)
 			ferr = e2;
 	}
@@ -1130,7 +1232,7 @@ static enum sam3_error free_scratch(void *p, void *stream, enum sam3_error err)
 {
 	if (!p)
 		return err;
-	enum sam3_error e = s3h_hip(hipFreeAsync(p, (hipStream_t)stream), "conv2d scratch free");
+	enum sam3_error e = s3h_scratch_free(p, stream);
 	return err != SAM3_OK ? err : e;
 }
 
