@@ -102,75 +102,93 @@ __device__ __forceinline__ void wave_lds_fence()
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-/* Store of C[m][n..n+7] from 8 f32 values at v (LDS), output kind CK.
+/* Store of C[m][n..n+W-1] from W f32 values at v (LDS), output kind CK,
+ * W = 4 for f32 C and 8 for 16-bit C (one 16-byte store either way).
  * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
  * points; without it the values are only converted. */
-template <int CK, bool EPI>
-__device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int n, const float *v)
+template <int CK, bool EPI, int W>
+__device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int n, const float *v)
 {
-	const bool full = n + 8 <= p.N;
-	const float4 v0 = *(const float4 *)v, v1 = *(const float4 *)(v + 4);
-	float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-	if (EPI) {
-		float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-		if (p.flags & S3K_EPI_BIAS) {
-			/* n is a multiple of 8 here: 16-byte loads need only an
-			 * aligned bias base */
-			const bool vec = full && (((uintptr_t)p.bias & 15u) == 0) && (n & 7) == 0;
-			if (vec && p.bias_kind != S3K_F32) {
-				/* 8 bf16/f16 values in one 16-byte load */
-				const uint4 w = *(const uint4 *)((const uint16_t *)p.bias + n);
-				const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+	typedef float f4v __attribute__((ext_vector_type(4)));
+	typedef unsigned u4v __attribute__((ext_vector_type(4)));
+	static_assert(W == 4 || W == 8, "4 or 8 outputs per store");
+	const bool full = n + W <= p.N;
+	float x[W];
 #pragma unroll
-				for (int e = 0; e < 4; ++e) {
+	for (int e = 0; e < W; e += 4) {
+		const float4 q = *(const float4 *)(v + e);
+		x[e] = q.x; x[e + 1] = q.y; x[e + 2] = q.z; x[e + 3] = q.w;
+	}
+	if (EPI) {
+		float bv[W];
+#pragma unroll
+		for (int e = 0; e < W; ++e)
+			bv[e] = 0.f;
+		if (p.flags & S3K_EPI_BIAS) {
+			/* n is a multiple of W here: 16-byte (f32) or 8/16-byte
+			 * (16-bit) loads need only an aligned bias base */
+			const bool vec = full && (((uintptr_t)p.bias & 15u) == 0);
+			if (vec && p.bias_kind != S3K_F32) {
+				uint32_t d[W / 2];
+				if constexpr (W == 8) {
+					const uint4 w = *(const uint4 *)((const uint16_t *)p.bias + n);
+					d[0] = w.x; d[1] = w.y; d[2] = w.z; d[3] = w.w;
+				} else {
+					const uint2 w = *(const uint2 *)((const uint16_t *)p.bias + n);
+					d[0] = w.x; d[1] = w.y;
+				}
+#pragma unroll
+				for (int e = 0; e < W / 2; ++e) {
 					bv[2 * e] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] & 0xFFFFu)
 									     : f16_to_f32(d[e] & 0xFFFFu);
 					bv[2 * e + 1] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] >> 16)
 										 : f16_to_f32(d[e] >> 16);
 				}
 			} else if (vec) {
-				const float4 b0 = *(const float4 *)((const float *)p.bias + n);
-				const float4 b1 = *(const float4 *)((const float *)p.bias + n + 4);
-				bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
-				bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+#pragma unroll
+				for (int e = 0; e < W; e += 4) {
+					const float4 b = *(const float4 *)((const float *)p.bias + n + e);
+					bv[e] = b.x; bv[e + 1] = b.y; bv[e + 2] = b.z; bv[e + 3] = b.w;
+				}
 			} else {
 #pragma unroll
-				for (int e = 0; e < 8; ++e)
+				for (int e = 0; e < W; ++e)
 					if (full || n + e < p.N)
 						bv[e] = load_as_f32(p.bias, n + e, p.bias_kind);
 			}
 		}
 #pragma unroll
-		for (int e = 0; e < 8; ++e)
+		for (int e = 0; e < W; ++e)
 			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
 	}
 	const long long o = (long long)m * p.ldc + n;
 	if (CK == S3K_F32) {
 		float *c = (float *)cb + o;
 		if (full && p.vec_ok) {
-			*(float4 *)c = make_float4(x[0], x[1], x[2], x[3]);
-			*(float4 *)(c + 4) = make_float4(x[4], x[5], x[6], x[7]);
+#pragma unroll
+			for (int e = 0; e < W; e += 4)
+				*(f4v *)(c + e) = (f4v){x[e], x[e + 1], x[e + 2], x[e + 3]};
 		} else {
 #pragma unroll
-			for (int e = 0; e < 8; ++e)
+			for (int e = 0; e < W; ++e)
 				if (n + e < p.N)
 					c[e] = x[e];
 		}
 	} else {
-		uint32_t h[8];
+		uint32_t h[W];
 #pragma unroll
-		for (int e = 0; e < 8; e += 2) {
+		for (int e = 0; e < W; e += 2) {
 			const uint32_t w = CK == S3K_BF16 ? pack_bf16x2(x[e], x[e + 1]) : pack_f16x2(x[e], x[e + 1]);
 			h[e] = w & 0xFFFFu;
 			h[e + 1] = w >> 16;
 		}
 		uint16_t *c = (uint16_t *)cb + o;
-		if (full && p.vec_ok) {
-			*(uint4 *)c = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16),
-						 h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+		if (W == 8 && full && p.vec_ok) {
+			*(u4v *)c = (u4v){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4 % W] | (h[5 % W] << 16),
+					  h[6 % W] | (h[7 % W] << 16)};
 		} else {
 #pragma unroll
-			for (int e = 0; e < 8; ++e)
+			for (int e = 0; e < W; ++e)
 				if (n + e < p.N)
 					c[e] = (uint16_t)h[e];
 		}
@@ -179,8 +197,8 @@ __device__ __forceinline__ void finish8(const GemmArgs &p, char *cb, int m, int 
 
 /* Epilogue of a wave tile, one 32-row strip at a time: the MFMA layout
  * (lane holds column l & 31 of rows 8*(r>>2) + 4*(l>>5) + (r&3)) is turned
- * into row-contiguous runs of 8 columns through LDS, so each lane finishes
- * 8 outputs and writes them with one 16-byte store. `smem` must be free
+ * into row-contiguous runs of columns through LDS, so each lane finishes
+ * 4 (f32) or 8 (16-bit) outputs and writes them with one 16-byte store. `smem` must be free
  * (all waves past their last LDS read) and hold NW*32*(WTN+8) floats.
  * Each wave stages through its own region of smem, and the LDS operations
  * of one wave are performed in program order, so the waves need no
@@ -196,6 +214,9 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
 	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU)) != 0;
+	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
+	 * so consecutive lanes write consecutive 16 bytes of a row */
+	constexpr int W = CK == S3K_F32 ? 4 : 8;
 #pragma unroll
 	for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -208,17 +229,17 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 		const int mrow = m0 + i * 32;
 		if (epi) {
 #pragma unroll 1
-			for (int s = lane; s < 32 * WTN / 8; s += 64) {
-				const int row = s / (WTN / 8), c8 = (s % (WTN / 8)) * 8;
-				if (mrow + row < p.M && n0 + c8 < p.N)
-					finish8<CK, true>(p, cb, mrow + row, n0 + c8, stg + row * PITCH + c8);
+			for (int s = lane; s < 32 * WTN / W; s += 64) {
+				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
+				if (mrow + row < p.M && n0 + cw < p.N)
+					finishw<CK, true, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw);
 			}
 		} else {
 #pragma unroll 1
-			for (int s = lane; s < 32 * WTN / 8; s += 64) {
-				const int row = s / (WTN / 8), c8 = (s % (WTN / 8)) * 8;
-				if (mrow + row < p.M && n0 + c8 < p.N)
-					finish8<CK, false>(p, cb, mrow + row, n0 + c8, stg + row * PITCH + c8);
+			for (int s = lane; s < 32 * WTN / W; s += 64) {
+				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
+				if (mrow + row < p.M && n0 + cw < p.N)
+					finishw<CK, false, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw);
 			}
 		}
 		wave_lds_fence();
