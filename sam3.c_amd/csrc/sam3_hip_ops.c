@@ -662,8 +662,32 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 	g.stride_a = stride_a;
 	g.stride_b = stride_w;
 	g.stride_c = stride_c;
-	if (s3k_gemm_path(&g) == S3K_PATH_SKINNY)
+	if (s3k_gemm_path(&g) == S3K_PATH_SKINNY) {
+		/* f32 activations shared by every slice (stride 0): cast them to
+		 * f16 once, the rounding the skinny kernel gives f32 activations
+		 * itself (bit-identical results), so each workgroup moves half
+		 * the activation bytes */
+		if (a_dtype == SAM3_DTYPE_F32 && stride_a == 0 && batch > 1 && M > 1) {
+			void *a16 = NULL;
+			enum sam3_error err = s3h_scratch_alloc(&a16, (size_t)M * K * 2, stream);
+			if (err != SAM3_OK)
+				return err;
+			err = s3h_hip(s3k_cast_f16(S3K_F32, a, a16, (long long)M * K, stream),
+				      "matmul_q8_batched activation cast");
+			if (err == SAM3_OK) {
+				struct s3k_gemm h = g;
+				h.a = a16;
+				h.a_kind = S3K_F16;
+				if (s3k_gemm_path(&h) == S3K_PATH_SKINNY)
+					err = s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8_batched");
+				else
+					err = s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched");
+			}
+			enum sam3_error ferr = s3h_scratch_free(a16, stream);
+			return err != SAM3_OK ? err : ferr;
+		}
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched");
+	}
 	/* one launch per slice on the kernel sam3_hip_matmul picks */
 	const size_t es = s3h_dtype_size(a_dtype);
 	for (int s = 0; s < batch; ++s) {

@@ -485,6 +485,30 @@ def test_q8_batched_stream(shared_a):
         assert_f32_close(c[s], ref, what=f"q8 batched slice {s}")
 
 
+@pytest.mark.parametrize("M", [2, 24, 77])
+def test_q8_batched_shared_f32_cast_once(M):
+    """Shared f32 activations of a batched skinny launch are cast to f16
+    once before the launch; the kernel rounds f32 activations to f16 the
+    same way, so the result has the same bits as passing the activations
+    as f16 (both batched, so the same workgroup shape runs)."""
+    B, N, K = 4, 128, 1024
+    a = rnd(185, (M, K))
+    ws = [q8(rnd(186 + s, (N, K), 0.02)) for s in range(B)]
+    dw = hip.DeviceBuffer.of(np.concatenate(ws))
+    outs = []
+    for dt, host in ((abi.F32, a), (abi.F16, a.astype(np.float16).view(np.uint16))):
+        da, dc = hip.DeviceBuffer.of(np.ascontiguousarray(host)), hip.DeviceBuffer(B * M * N * 4)
+        hip.q8_batched_dev(dt, da.ptr, dw.ptr, dc.ptr, B, M, N, K, 0, ws[0].nbytes, M * N)
+        hip.synchronize()
+        outs.append(dc.download(np.float32, (B, M, N)))
+        da.free()
+        dc.free()
+    dw.free()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for s in range(B):
+        assert_f32_close(outs[0][s], ref_q8(a, ws[s], K, N, nt=True), what=f"slice {s}")
+
+
 def test_q8_batched_falls_back_per_slice():
     """M > 128 is not a skinny problem: one launch per slice, same result."""
     B, M, N, K = 2, 160, 64, 256
