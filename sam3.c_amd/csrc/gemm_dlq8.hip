@@ -242,8 +242,10 @@ bool s3k_dlq8_ok(const struct s3k_gemm *g)
  * Tile choice: 128x128 with 4 waves of 128x32 (one dequantized weight
  * fragment feeds 4 MFMAs) and two workgroups per CU measured fastest on
  * every ViT-L shape (fc1/fc2/qkv/proj at M = 5184), ahead of 256x256 and
- * 256x128 tiles with 8 waves and of 256-row waves. SAM3_HIP_DLQ8_CFG
- * forces another configuration (tests and tuning).
+ * 256x128 tiles with 8 waves and of 256-row waves. M <= 96 (batched
+ * streams of weight copies) takes one tile of 32, 64 or 96 rows, so no
+ * weight tile is read twice. SAM3_HIP_DLQ8_CFG forces another
+ * configuration (tests and tuning).
  */
 int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
@@ -254,7 +256,7 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	const char *e = getenv("SAM3_HIP_DLQ8_CFG");
 	int cfg = e ? atoi(e) : -1;
 	if (cfg < 0)
-		cfg = 2;
+		cfg = g->M <= 32 ? 7 : g->M <= 64 ? 8 : g->M <= 96 ? 9 : 2;
 	switch (cfg) {
 	case 0:  return launch_dlq8_cfg<256, 256, 2, 4, 3, 1>(g, p, st);
 	case 1:  return launch_dlq8_cfg<256, 128, 2, 4, 3, 1>(g, p, st);
@@ -263,6 +265,9 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 4:  return launch_dlq8_cfg<256, 256, 1, 8, 3, 1>(g, p, st);
 	case 5:  return launch_dlq8_cfg<256, 128, 1, 4, 3, 1>(g, p, st);
 	case 6:  return launch_dlq8_cfg<256, 128, 1, 4, 2, 1>(g, p, st);
+	case 7:  return launch_dlq8_cfg<32, 128, 1, 4, 3, 2>(g, p, st);
+	case 8:  return launch_dlq8_cfg<64, 128, 1, 4, 3, 2>(g, p, st);
+	case 9:  return launch_dlq8_cfg<96, 128, 1, 4, 3, 2>(g, p, st);
 	default: return (int)hipErrorInvalidValue;
 	}
 }

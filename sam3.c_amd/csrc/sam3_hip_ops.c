@@ -631,6 +631,13 @@ enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b,
 	return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_batched");
 }
 
+/* Activation rows from which a batched stream of Q8 weights with shared
+ * activations runs on the tiled Q8 GEMM (one tile of all rows per weight
+ * tile, full k per workgroup) instead of the skinny kernel (k split over
+ * a workgroup's waves). SAM3_HIP_Q8_BATCH_PATH=1 forces the skinny
+ * kernel, =2 the GEMM. */
+#define S3H_Q8_BATCH_GEMM_M 8
+
 enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const void *w,
 					   void *c, int batch, int M, int N, int K,
 					   long long stride_a, long long stride_w,
@@ -663,30 +670,38 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 	g.stride_b = stride_w;
 	g.stride_c = stride_c;
 	if (s3k_gemm_path(&g) == S3K_PATH_SKINNY) {
-		/* f32 activations shared by every slice (stride 0): cast them to
+		/* f32 activations shared by every slice (stride 0) are cast to
 		 * f16 once, the rounding the skinny kernel gives f32 activations
 		 * itself (bit-identical results), so each workgroup moves half
 		 * the activation bytes */
+		struct s3k_gemm h = g;
+		void *a16 = NULL;
+		enum sam3_error err = SAM3_OK;
 		if (a_dtype == SAM3_DTYPE_F32 && stride_a == 0 && batch > 1 && M > 1) {
-			void *a16 = NULL;
-			enum sam3_error err = s3h_scratch_alloc(&a16, (size_t)M * K * 2, stream);
+			err = s3h_scratch_alloc(&a16, (size_t)M * K * 2, stream);
 			if (err != SAM3_OK)
 				return err;
 			err = s3h_hip(s3k_cast_f16(S3K_F32, a, a16, (long long)M * K, stream),
 				      "matmul_q8_batched activation cast");
-			if (err == SAM3_OK) {
-				struct s3k_gemm h = g;
-				h.a = a16;
-				h.a_kind = S3K_F16;
-				if (s3k_gemm_path(&h) == S3K_PATH_SKINNY)
-					err = s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8_batched");
-				else
-					err = s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched");
-			}
-			enum sam3_error ferr = s3h_scratch_free(a16, stream);
-			return err != SAM3_OK ? err : ferr;
+			h.a = a16;
+			h.a_kind = S3K_F16;
 		}
-		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched");
+		if (err == SAM3_OK) {
+			const char *pe = getenv("SAM3_HIP_Q8_BATCH_PATH");
+			const int force = pe ? atoi(pe) : 0;
+			const int gemm = h.a_kind == S3K_F16 && batch > 1 &&
+					 (force == 2 || (force != 1 && M >= S3H_Q8_BATCH_GEMM_M)) &&
+					 s3k_dlq8_eligible(&h);
+			err = gemm ? s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream),
+					     "matmul_q8_batched gemm")
+				   : s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8_batched");
+		}
+		if (a16) {
+			enum sam3_error ferr = s3h_scratch_free(a16, stream);
+			if (err == SAM3_OK)
+				err = ferr;
+		}
+		return err;
 	}
 	/* one launch per slice on the kernel sam3_hip_matmul picks */
 	const size_t es = s3h_dtype_size(a_dtype);
