@@ -634,8 +634,10 @@ enum sam3_error sam3_hip_matmul_batched(int dtype, const void *a, const void *b,
 /* Activation rows from which a batched stream of Q8 weights with shared
  * activations runs on the tiled Q8 GEMM (one tile of all rows per weight
  * tile, full k per workgroup) instead of the skinny kernel (k split over
- * a workgroup's waves). SAM3_HIP_Q8_BATCH_PATH=1 forces the skinny
- * kernel, =2 the GEMM. */
+ * a workgroup's waves); K <= 256 takes the GEMM at any M (the skinny
+ * kernel's k split leaves half its waves idle there). Measured on every
+ * config-4 shape. SAM3_HIP_Q8_BATCH_PATH=1 forces the skinny kernel, =2
+ * the GEMM. */
 #define S3H_Q8_BATCH_GEMM_M 8
 
 enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const void *w,
@@ -677,7 +679,7 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 		struct s3k_gemm h = g;
 		void *a16 = NULL;
 		enum sam3_error err = SAM3_OK;
-		if (a_dtype == SAM3_DTYPE_F32 && stride_a == 0 && batch > 1 && M > 1) {
+		if (a_dtype == SAM3_DTYPE_F32 && stride_a == 0 && batch > 1) {
 			err = s3h_scratch_alloc(&a16, (size_t)M * K * 2, stream);
 			if (err != SAM3_OK)
 				return err;
@@ -690,7 +692,8 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 			const char *pe = getenv("SAM3_HIP_Q8_BATCH_PATH");
 			const int force = pe ? atoi(pe) : 0;
 			const int gemm = h.a_kind == S3K_F16 && batch > 1 &&
-					 (force == 2 || (force != 1 && M >= S3H_Q8_BATCH_GEMM_M)) &&
+					 (force == 2 ||
+					  (force != 1 && (M >= S3H_Q8_BATCH_GEMM_M || K <= 256))) &&
 					 s3k_dlq8_eligible(&h);
 			err = gemm ? s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream),
 					     "matmul_q8_batched gemm")

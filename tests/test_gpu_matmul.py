@@ -485,13 +485,13 @@ def test_q8_batched_stream(shared_a):
         assert_f32_close(c[s], ref, what=f"q8 batched slice {s}")
 
 
-@pytest.mark.parametrize("M", [2, 24, 77])
-def test_q8_batched_shared_f32_cast_once(M):
+@pytest.mark.parametrize("M,K", [(1, 256), (2, 1024), (24, 1024), (77, 1024)])
+def test_q8_batched_shared_f32_cast_once(M, K):
     """Shared f32 activations of a batched skinny launch are cast to f16
     once before the launch; the kernel rounds f32 activations to f16 the
     same way, so the result has the same bits as passing the activations
     as f16 (both batched, so the same workgroup shape runs)."""
-    B, N, K = 4, 128, 1024
+    B, N = 4, 128
     a = rnd(185, (M, K))
     ws = [q8(rnd(186 + s, (N, K), 0.02)) for s in range(B)]
     dw = hip.DeviceBuffer.of(np.concatenate(ws))
