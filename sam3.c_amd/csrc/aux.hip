@@ -111,36 +111,58 @@ __global__ void __launch_bounds__(256) q8_dequantize_k(const char *src, float *d
 			dst[e0 + i] = (float)(int)(int8_t)(w >> (8 * i)) * s;
 }
 
-/* f32 or bf16 -> f16 (round to nearest even), 8 values per thread; the
- * f16 staging of activations for the Q8 GEMM. */
-template <bool BF16>
+/* f32 or bf16 -> f16 (round to nearest even); the f16 staging of
+ * activations for the Q8 GEMM. A thread converts U chunks of 8 values,
+ * chunks gridDim*256 apart, and issues all of its loads before the first
+ * conversion, so each wave keeps U 16-byte (bf16) or 2U (f32) loads per
+ * lane in flight instead of one. The n % 8 tail goes to the first lanes
+ * of workgroup 0. */
+template <bool BF16, int U>
 __global__ void __launch_bounds__(256) cast_f16_k(const void *src, uint16_t *dst, long long n)
 {
-	const long long i0 = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
-	if (i0 >= n)
-		return;
-	float x[8];
-	if (i0 + 8 <= n) {
-		if (BF16) {
-			const uint4 v = *(const uint4 *)((const uint16_t *)src + i0);
-			const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+	constexpr int L = BF16 ? 1 : 2; /* 16-byte loads per chunk */
+	const long long chunks = n / 8, stride = (long long)gridDim.x * 256;
+	for (long long c0 = (long long)blockIdx.x * 256 + threadIdx.x; c0 < chunks; c0 += stride * U) {
+		uint4 v[U][L];
 #pragma unroll
-			for (int e = 0; e < 4; ++e) {
-				x[2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
-				x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
+		for (int u = 0; u < U; ++u) {
+			const long long c = c0 + u * stride;
+			if (c < chunks) {
+#pragma unroll
+				for (int l = 0; l < L; ++l)
+					v[u][l] = ((const uint4 *)src)[c * L + l];
 			}
-		} else {
-			const float4 a = *(const float4 *)((const float *)src + i0);
-			const float4 b = *(const float4 *)((const float *)src + i0 + 4);
-			x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-			x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 		}
-		*(uint4 *)(dst + i0) = make_uint4(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]),
-						  pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7]));
-	} else {
-		for (long long i = i0; i < n; ++i)
-			dst[i] = (uint16_t)f32_to_f16(BF16 ? bf16_to_f32(((const uint16_t *)src)[i])
-							  : ((const float *)src)[i]);
+#pragma unroll
+		for (int u = 0; u < U; ++u) {
+			const long long c = c0 + u * stride;
+			if (c >= chunks)
+				break;
+			float x[8];
+			if (BF16) {
+				const uint32_t w[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
+#pragma unroll
+				for (int e = 0; e < 4; ++e) {
+					x[2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
+					x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
+				}
+			} else {
+#pragma unroll
+				for (int l = 0; l < L; ++l) {
+					x[4 * l] = __uint_as_float(v[u][l].x);
+					x[4 * l + 1] = __uint_as_float(v[u][l].y);
+					x[4 * l + 2] = __uint_as_float(v[u][l].z);
+					x[4 * l + 3] = __uint_as_float(v[u][l].w);
+				}
+			}
+			((uint4 *)dst)[c] = make_uint4(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]),
+						       pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7]));
+		}
+	}
+	if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+		const long long i = chunks * 8 + threadIdx.x;
+		dst[i] = (uint16_t)f32_to_f16(BF16 ? bf16_to_f32(((const uint16_t *)src)[i])
+						  : ((const float *)src)[i]);
 	}
 }
 
@@ -291,13 +313,15 @@ extern "C" int s3k_cast_f16(int kind, const void *src, void *dst, long long n, v
 		return 0;
 	if (((uintptr_t)src | (uintptr_t)dst) & 15u)
 		return (int)hipErrorInvalidValue;
-	const dim3 grid((unsigned)((n + 2047) / 2048));
+	/* U chunks of 8 values per thread: 4 for bf16 (64 bytes in flight per
+	 * lane), 2 for f32 (64 bytes) */
+	const long long chunks = n / 8 > 0 ? n / 8 : 1;
 	if (kind == S3K_BF16)
-		hipLaunchKernelGGL(cast_f16_k<true>, grid, dim3(256), 0, (hipStream_t)stream, src,
-				   (uint16_t *)dst, n);
+		hipLaunchKernelGGL((cast_f16_k<true, 4>), dim3((unsigned)((chunks + 1023) / 1024)), dim3(256),
+				   0, (hipStream_t)stream, src, (uint16_t *)dst, n);
 	else if (kind == S3K_F32)
-		hipLaunchKernelGGL(cast_f16_k<false>, grid, dim3(256), 0, (hipStream_t)stream, src,
-				   (uint16_t *)dst, n);
+		hipLaunchKernelGGL((cast_f16_k<false, 2>), dim3((unsigned)((chunks + 511) / 512)), dim3(256),
+				   0, (hipStream_t)stream, src, (uint16_t *)dst, n);
 	else
 		return (int)hipErrorInvalidValue;
 	return (int)hipGetLastError();
