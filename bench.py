@@ -665,8 +665,10 @@ def main():
     ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,neck,weights",
                     help="comma list of extra sections to run (cfg1..cfg5, block, conv, neck, "
                          "weights)")
-    ap.add_argument("--block", default="windowed_f32,windowed_q8,global_f32,global_q8",
-                    help="block section: comma list of {windowed,global}_{f32,q8}")
+    ap.add_argument("--block",
+                    default="windowed_f32,windowed_q8,global_f32,global_q8,trunk_q8,trunk_f32",
+                    help="block section: comma list of {windowed,global}_{f32,q8} and "
+                         "trunk_{q8,f32} (32 blocks)")
     args = ap.parse_args()
     only = set(args.only.split(","))
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -837,6 +839,8 @@ def main():
                 blk[f"{name}_{wk}"] = vit_block_bench(glob, wk)
                 log("  ", name, wk, blk[f"{name}_{wk}"])
         for wk in ("q8", "f32"):
+            if f"trunk_{wk}" not in want:
+                continue
             blk[f"trunk_32_blocks_{wk}"] = vit_trunk_bench(wk)
             log("   trunk", wk, blk[f"trunk_32_blocks_{wk}"])
         if not args.no_cpu_baseline:

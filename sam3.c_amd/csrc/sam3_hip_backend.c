@@ -226,11 +226,14 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		hb->stats.mapped_reads++;
 		return SAM3_OK;
 	}
-	if (is_device_ptr(t->data)) {
+	/* a residency entry exists only for host memory, so the runtime's
+	 * pointer lookup (a few microseconds per call) runs only for
+	 * pointers this backend has not seen */
+	struct s3h_res *e = res_find(hb, t->data);
+	if (!e && is_device_ptr(t->data)) {
 		*out = t->data;
 		return SAM3_OK;
 	}
-	struct s3h_res *e = res_find(hb, t->data);
 	if (e && e->fmt) {
 		/* a producer wrote the consuming GEMM's operand form */
 		*out = e->dev;
@@ -275,12 +278,12 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 		s3h_error("graph_eval: output tensor without data");
 		return SAM3_EINVAL;
 	}
-	if (is_device_ptr(t->data)) {
+	struct s3h_res *e = res_find(hb, t->data);
+	if (!e && is_device_ptr(t->data)) {
 		*out = t->data;
 		return SAM3_OK;
 	}
 	size_t nbytes = s3h_tensor_bytes(t);
-	struct s3h_res *e = res_find(hb, t->data);
 	if (e && e->nbytes < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
