@@ -520,7 +520,8 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.sc = g->stride_c;
 	p.flags = g->flags;
 	p.c_kind = g->c_kind;
-	p.bias_kind = g->c_kind;
+	/* the operand output kinds compute in f32 and take an f32 bias */
+	p.bias_kind = g->c_kind >= S3K_C_F16OP ? S3K_F32 : g->c_kind;
 	p.vec_ok = aligned16(g->c) && g->ldc % 8 == 0 && (g->batch <= 1 || g->stride_c % 8 == 0);
 	p.tiles_m = p.tiles_n = 0;
 	p.a_extent = p.b_extent = 0;
@@ -645,6 +646,8 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 		return (int)hipErrorInvalidValue;
 	if (s3k_dl_ok(g))
 		return s3k_dl_launch(g, p, st);
+	if (g->c_kind >= S3K_C_F16OP) /* only the direct-to-LDS GEMM writes operand forms */
+		return (int)hipErrorInvalidValue;
 	if (s3k_dlq8_ok(g))
 		return s3k_dlq8_launch(g, p, st);
 	if (g->a_kind == S3K_F32 && g->b_kind == S3K_F32) {

@@ -162,7 +162,30 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
 	}
 	const long long o = (long long)m * p.ldc + n;
-	if (CK == S3K_F32) {
+	if constexpr (CK == S3K_C_PLANES) {
+		/* the split of split3_bf16_k: hi = bf16(x), lo = bf16(x - hi) */
+		uint32_t hi[4], lo[4];
+#pragma unroll
+		for (int e = 0; e < 4; ++e)
+			split_bf16x2(x[2 * e], x[2 * e + 1], hi[e], lo[e]);
+		uint16_t *c = (uint16_t *)cb + o;
+		if (W == 8 && full && p.vec_ok) {
+			*(u4v *)c = (u4v){hi[0], hi[1], hi[2], hi[3]};
+			*(u4v *)(c + p.N) = (u4v){lo[0], lo[1], lo[2], lo[3]};
+			*(u4v *)(c + 2LL * p.N) = (u4v){hi[0], hi[1], hi[2], hi[3]};
+		} else {
+#pragma unroll
+			for (int e = 0; e < W; ++e) {
+				if (n + e >= p.N)
+					continue;
+				const uint16_t h = (uint16_t)(e & 1 ? hi[e / 2] >> 16 : hi[e / 2] & 0xFFFFu);
+				const uint16_t l = (uint16_t)(e & 1 ? lo[e / 2] >> 16 : lo[e / 2] & 0xFFFFu);
+				c[e] = h;
+				c[p.N + e] = l;
+				c[2LL * p.N + e] = h;
+			}
+		}
+	} else if (CK == S3K_F32) {
 		float *c = (float *)cb + o;
 		if (full && p.vec_ok) {
 #pragma unroll
@@ -178,6 +201,7 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 		uint32_t h[W];
 #pragma unroll
 		for (int e = 0; e < W; e += 2) {
+			/* S3K_C_F16OP: f16 store of the f32 result (pack_f16x2) */
 			const uint32_t w = CK == S3K_BF16 ? pack_bf16x2(x[e], x[e + 1]) : pack_f16x2(x[e], x[e + 1]);
 			h[e] = w & 0xFFFFu;
 			h[e + 1] = w >> 16;
@@ -213,6 +237,7 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	constexpr int PITCH = WTN + 8; /* floats; 16-B aligned rows, rows 4 apart 32 banks apart */
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
+	static_assert(CK != S3K_C_PLANES || WTN % 8 == 0, "planes are written 8 outputs at a time");
 	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU)) != 0;
 	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
 	 * so consecutive lanes write consecutive 16 bytes of a row */

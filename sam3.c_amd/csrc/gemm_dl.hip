@@ -181,24 +181,43 @@ static void launch_dl_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t
 			   dim3(64 * WGM * WGN), 0, st, p);
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int OCC>
+/* OPK: the configuration is also built for the operand output kinds
+ * (S3K_C_F16OP, S3K_C_PLANES); the others reject them. */
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int OCC, int FAM, bool OPK>
+static int launch_dl_fam(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
+{
+	constexpr int SAME = FAM == FAM_BF16 ? S3K_BF16 : S3K_F16;
+	switch (g->c_kind) {
+	case S3K_F32:
+		launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM, S3K_F32, OCC>(g, p, st);
+		break;
+	case SAME:
+		launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM, SAME, OCC>(g, p, st);
+		break;
+	case S3K_C_F16OP:
+	case S3K_C_PLANES:
+		if constexpr (OPK) {
+			if (g->c_kind == S3K_C_F16OP)
+				launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM, S3K_C_F16OP, OCC>(g, p, st);
+			else
+				launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM, S3K_C_PLANES, OCC>(g, p, st);
+			break;
+		}
+		return (int)hipErrorInvalidValue;
+	default:
+		return (int)hipErrorInvalidValue;
+	}
+	return (int)hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int OCC, bool OPK = false>
 static int launch_dl_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
 	p.tiles_m = (p.M + BM - 1) / BM;
 	p.tiles_n = (p.N + BN - 1) / BN;
-	const bool f32_out = g->c_kind == S3K_F32;
-	if (g->a_kind == S3K_BF16) {
-		if (f32_out)
-			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_BF16, S3K_F32, OCC>(g, p, st);
-		else
-			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_BF16, S3K_BF16, OCC>(g, p, st);
-	} else {
-		if (f32_out)
-			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_F16, S3K_F32, OCC>(g, p, st);
-		else
-			launch_dl_k<BM, BN, BK, WGM, WGN, STAGES, FAM_F16, S3K_F16, OCC>(g, p, st);
-	}
-	return (int)hipGetLastError();
+	if (g->a_kind == S3K_BF16)
+		return launch_dl_fam<BM, BN, BK, WGM, WGN, STAGES, OCC, FAM_BF16, OPK>(g, p, st);
+	return launch_dl_fam<BM, BN, BK, WGM, WGN, STAGES, OCC, FAM_F16, OPK>(g, p, st);
 }
 
 } /* namespace s3k */
@@ -223,6 +242,11 @@ bool s3k_dl_ok(const struct s3k_gemm *g)
 	if ((long long)g->M * g->lda * 2 > 0x7FFFFFF0LL || (long long)g->N * g->ldb * 2 > 0x7FFFFFF0LL)
 		return false;
 	return true;
+}
+
+extern "C" int s3k_dl_eligible(const struct s3k_gemm *g)
+{
+	return s3k_dl_ok(g) ? 1 : 0;
 }
 
 /* Tile shape, from measurements on the ViT-L shapes (bench-like data):
@@ -260,15 +284,15 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	switch (cfg) {
 	case 0:  return launch_dl_cfg<256, 128, 32, 2, 2, 3, 2>(g, p, st);
 	case 1:  return launch_dl_cfg<128, 128, 32, 2, 2, 3, 2>(g, p, st);
-	case 2:  return launch_dl_cfg<64, 64, 32, 2, 2, 3, 2>(g, p, st);
+	case 2:  return launch_dl_cfg<64, 64, 32, 2, 2, 3, 2, true>(g, p, st);
 	case 3:  return launch_dl_cfg<128, 256, 32, 2, 2, 3, 2>(g, p, st);
-	case 4:  return launch_dl_cfg<128, 128, 64, 2, 2, 2, 2>(g, p, st);
+	case 4:  return launch_dl_cfg<128, 128, 64, 2, 2, 2, 2, true>(g, p, st);
 	case 5:  return launch_dl_cfg<256, 256, 32, 2, 2, 4, 1>(g, p, st);
 	case 6:  return launch_dl_cfg<192, 256, 32, 2, 2, 4, 1>(g, p, st);
 	case 7:  return launch_dl_cfg<192, 256, 64, 2, 4, 2, 1>(g, p, st);
 	case 8:  return launch_dl_cfg<256, 256, 32, 2, 4, 3, 1>(g, p, st);
-	case 9:  return launch_dl_cfg<256, 256, 64, 2, 4, 2, 1>(g, p, st);
-	case 10: return launch_dl_cfg<192, 128, 64, 2, 4, 2, 1>(g, p, st);
+	case 9:  return launch_dl_cfg<256, 256, 64, 2, 4, 2, 1, true>(g, p, st);
+	case 10: return launch_dl_cfg<192, 128, 64, 2, 4, 2, 1, true>(g, p, st);
 	case 11: return launch_dl_cfg<256, 128, 64, 2, 4, 2, 1>(g, p, st);
 	case 12: return launch_dl_cfg<128, 256, 64, 2, 4, 2, 1>(g, p, st);
 	case 13: return launch_dl_cfg<256, 256, 32, 2, 4, 4, 1>(g, p, st);

@@ -22,6 +22,11 @@ enum s3k_kind {
 	S3K_F16  = 1,
 	S3K_BF16 = 2,
 	S3K_Q8   = 5,
+	/* output kinds only: f32 epilogue math, then the form the next GEMM
+	 * reads: f16 [M, ldc], or bf16 planes [hi|lo|hi] with row pitch
+	 * ldc = 3N (hi at n, lo at N + n, hi again at 2N + n) */
+	S3K_C_F16OP  = 16,
+	S3K_C_PLANES = 17,
 };
 
 /* Epilogue / layout flags. */
@@ -117,6 +122,8 @@ int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld, 
 /* Whether the MFMA path of g (B Q8_0 [N,K]) runs the direct-to-LDS Q8
  * GEMM: f16 A directly, bf16 A after a cast to f16. */
 int s3k_dlq8_eligible(const struct s3k_gemm *g);
+/* Whether the direct-to-LDS bf16/f16 GEMM takes g (layout and alignment). */
+int s3k_dl_eligible(const struct s3k_gemm *g);
 int s3k_bias_add(int kind, const void *x, const void *bias, void *out,
 		 long long rows, int n, void *stream);
 int s3k_add_same(int kind, const void *x, const void *y, void *out,

@@ -439,6 +439,10 @@ static const struct sam3_tensor *folded_source(const struct sam3_graph *g, int u
 	return NULL;
 }
 
+static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+				 int j, const struct sam3_tensor *t, int row_len,
+				 struct use_map *uses);
+
 /* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
  * Returns the number of nodes consumed in *used. */
 static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3_graph *g,
@@ -516,13 +520,34 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_in(hb, bsrc, &db);
 	if (err == SAM3_OK && bias)
 		err = dev_in(hb, bias, &dbias);
-	if (err == SAM3_OK)
-		err = dev_out(hb, out, &dc);
 	if (err != SAM3_OK)
 		return err;
-	err = a_fmt ? s3h_matmul_fmt(a_fmt, a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags,
-				     hb->stream)
-		    : sam3_hip_matmul(a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags, hb->stream);
+	/* an f32 result read only by the next GEMM, which converts its A
+	 * first: written in that form by this GEMM's epilogue */
+	int o_fmt = S3H_A_PLAIN;
+	const char *o_env = getenv("SAM3_HIP_GEMM_OPERAND");
+	if (c_dt == SAM3_DTYPE_F32 && !(o_env && atoi(o_env) == 0)) {
+		o_fmt = consumer_operand_form(hb, g, i, j, out, N, uses);
+		if (o_fmt != S3H_A_PLAIN &&
+		    !s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, o_fmt))
+			o_fmt = S3H_A_PLAIN;
+	}
+	if (o_fmt != S3H_A_PLAIN) {
+		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
+		if (err == SAM3_OK)
+			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
+						flags, hb->stream);
+		if (err == SAM3_OK)
+			hb->stats.operand_writes++;
+	} else {
+		err = dev_out(hb, out, &dc);
+		if (err != SAM3_OK)
+			return err;
+		err = a_fmt ? s3h_matmul_fmt(a_fmt, a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias,
+					     flags, hb->stream)
+			    : sam3_hip_matmul(a_dt, da, b_dt, db, c_dt, dc, M, N, K, dbias, flags,
+					      hb->stream);
+	}
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.fused_nodes += j - i - 1;
@@ -531,19 +556,17 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	return err;
 }
 
-/* The GEMM operand form an f32 LAYERNORM at node i can be written in:
- * its output, through RESHAPE views only, must be used once, as the A of
- * a MATMUL that converts A before its GEMM (s3h_matmul_a_format). The
+/* The GEMM operand form in which tensor t, produced by node i (or by the
+ * chain of nodes folded into it, the last of them before node j), can be
+ * written: t must be used once, through RESHAPE views only, as the A of a
+ * MATMUL that converts A before its GEMM (s3h_matmul_a_format), with
+ * rows of row_len values (the producer's row length). The consumer's
  * weight is resolved (and uploaded) here to decide with its device
  * address. */
-static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
-			   struct use_map *uses)
+static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+				 int j, const struct sam3_tensor *t, int row_len,
+				 struct use_map *uses)
 {
-	const struct sam3_node *n = &g->nodes[i];
-	if (n->inputs[0]->dtype != SAM3_DTYPE_F32 || !s3h_layernorm_ok(n))
-		return S3H_A_PLAIN;
-	const struct sam3_tensor *t = n->output;
-	int j = i + 1;
 	for (;;) {
 		if (uses_of(uses, t) != 1)
 			return S3H_A_PLAIN;
@@ -584,7 +607,7 @@ static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph 
 		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
 		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
 	}
-	if (kb != K || s3h_nelems(t) != (long long)M * K || K != n->inputs[0]->dims[n->inputs[0]->n_dims - 1])
+	if (kb != K || s3h_nelems(t) != (long long)M * K || K != row_len)
 		return S3H_A_PLAIN;
 	void *db = NULL;
 	if (dev_in(hb, bsrc, &db) != SAM3_OK)
@@ -592,6 +615,17 @@ static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph 
 	static const char aligned_a[16] __attribute__((aligned(16)));
 	return s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, bsrc->dtype, db, SAM3_DTYPE_F32, M, N,
 				   K, w ? SAM3_HIP_B_NT : 0);
+}
+
+/* The form an f32 LAYERNORM at node i writes: its consumer's operand. */
+static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			   struct use_map *uses)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->inputs[0]->dtype != SAM3_DTYPE_F32 || !s3h_layernorm_ok(n))
+		return S3H_A_PLAIN;
+	return consumer_operand_form(hb, g, i, i + 1, n->output,
+				     n->inputs[0]->dims[n->inputs[0]->n_dims - 1], uses);
 }
 
 /* LAYERNORM written as the operand form fmt of its one consuming GEMM. */

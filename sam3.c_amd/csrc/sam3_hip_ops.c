@@ -571,6 +571,67 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 	return SAM3_EINVAL;
 }
 
+/* Whether the GEMM that s3h_matmul_fmt runs for A in form a_fmt can write
+ * its f32 result directly as the operand form out_fmt (S3H_A_PLANES or
+ * S3H_A_F16) of a following GEMM. Only the direct-to-LDS GEMM writes those
+ * forms; f32 weights reach it through the split GEMM (planes), Q8_0
+ * weights through their f16 expansion (f16 A only). b is the weight's
+ * device address; a is used for its alignment only. */
+int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags, int out_fmt)
+{
+	static const char al[16] __attribute__((aligned(16)));
+	if ((out_fmt != S3H_A_PLANES && out_fmt != S3H_A_F16) || M <= 0 || N <= 0 || K <= 0 ||
+	    N % 8 || !a || !b || check_kinds(a_dt, b_dt, SAM3_DTYPE_F32) != SAM3_OK)
+		return 0;
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
+	struct s3k_gemm h = g;
+	h.a = h.b = al;
+	if (b_dt == SAM3_DTYPE_F32) {
+		if ((a_fmt != S3H_A_PLANES && a_fmt != S3H_A_PLAIN) || !f32_split_wanted(&g))
+			return 0;
+		h.a_kind = h.b_kind = S3K_BF16;
+		h.K = 3 * K;
+		h.lda = h.ldb = 3 * K;
+		return s3k_dl_eligible(&h);
+	}
+	if (b_dt != SAM3_DTYPE_Q8_0 || a_fmt != S3H_A_F16 || a_dt != SAM3_DTYPE_F32)
+		return 0;
+	/* the expansion q8_f16_gemm makes */
+	const char *env = getenv("SAM3_HIP_Q8_EXPAND");
+	const int mode = env ? atoi(env) : -1;
+	if (!(g.flags & S3K_B_NT) || K % 32 || mode == 0 ||
+	    (mode != 1 && !s3h_prep_cacheable(b, (size_t)N * (K / 32) * 36)))
+		return 0;
+	h.a_kind = h.b_kind = S3K_F16;
+	h.ldb = K;
+	return s3k_dl_eligible(&h);
+}
+
+/* The GEMM of s3h_matmul_fmt with its f32 result written as out_fmt:
+ * bf16 planes [M, 3N] = [hi|lo|hi] per row, or f16 [M, N], with the
+ * bias and GELU applied in f32 first, the values split3 / the f16 cast
+ * of the f32 output would give. */
+enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
+				  const void *b, void *c, int M, int N, int K, const void *bias,
+				  int flags, void *stream)
+{
+	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) ||
+	    !s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt)) {
+		s3h_error("matmul: cannot write operand form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
+		return SAM3_EINVAL;
+	}
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
+	g.c_kind = out_fmt == S3H_A_PLANES ? S3K_C_PLANES : S3K_C_F16OP;
+	g.ldc = out_fmt == S3H_A_PLANES ? 3 * N : N;
+	if (b_dt == SAM3_DTYPE_F32)
+		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
+	g.a_kind = S3K_F16;
+	return q8_f16_gemm(&g, stream);
+}
+
 enum sam3_error sam3_hip_matmul(int a_dtype, const void *a, int b_dtype, const void *b,
 				int c_dtype, void *c, int M, int N, int K,
 				const void *bias, int flags, void *stream)

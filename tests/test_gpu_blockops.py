@@ -315,6 +315,59 @@ def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
     assert_f32_close(fused, ref.astype(np.float32), what=f"LN -> linear {wkind}")
 
 
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_gemm_written_as_next_gemm_operand(monkeypatch, wkind):
+    """gh_mlp (graph_helpers.c:1258-1276) after a LayerNorm: fc1's result,
+    after its folded bias and GELU, is read only by fc2, which converts
+    its A first (bf16 hi/lo planes for f32 weights, f16 for Q8_0 weights).
+    fc1's epilogue writes that operand directly: the bias and GELU stay in
+    f32 and the split / cast is the one the unfused graph applies to fc1's
+    f32 output, so the result is the same bit for bit; both match the
+    oracle's LN + MLP."""
+    M, E, H = 1024, 256, 1024
+    O = oracle()
+    x = synth.randn(820, (M, E), 2.0, 0.5)
+    gam, bet = synth.randn(821, (E,)), synth.randn(822, (E,), 0.1)
+    w1, b1 = synth.randn(823, (H, E), 0.05), synth.randn(824, (H,), 0.02)
+    w2, b2 = synth.randn(825, (E, H), 0.03), synth.randn(826, (E,), 0.02)
+
+    def wt(G, w):
+        return (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
+                else G.tensor(abi.F32, w.shape, w))
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_GEMM_OPERAND", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_GEMM_OPERAND", env)
+        G = graph.Graph()
+        t = G.layernorm(G.tensor(abi.F32, (M, E), x), G.tensor(abi.F32, (E,), gam),
+                        G.tensor(abi.F32, (E,), bet))
+        y = G.mlp(t, wt(G, w1), G.tensor(abi.F32, (H,), b1), wt(G, w2), G.tensor(abi.F32, (E,), b2))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(M, E)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    # LN2 -> fc1 always; fc1 -> fc2 only when enabled
+    assert st.operand_writes == 2 and st0.operand_writes == 1
+    assert st.host_nodes == 0 and st.downloads == 1
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    ln = O.layernorm(x, gam, bet, "f32", threads=8).astype(np.float64)
+
+    def deq(w):
+        return (O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8"
+                else w).astype(np.float64)
+    h = O.gelu((ln @ deq(w1).T + b1).astype(np.float32), "f32").astype(np.float64)
+    ref = h @ deq(w2).T + b2
+    assert_f32_close(fused, ref.astype(np.float32), what=f"LN -> MLP {wkind}")
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
