@@ -380,6 +380,8 @@ enum sam3_error sam3_hip_memcpy_d2h(void *dst, const void *src, size_t nbytes);
 enum sam3_error sam3_hip_memcpy_d2d(void *dst, const void *src, size_t nbytes);
 enum sam3_error sam3_hip_synchronize(void);
 enum sam3_error sam3_hip_stream_create(void **stream);
+/* Also frees the device scratch the library keeps for this stream (after
+ * the stream's work completes). */
 enum sam3_error sam3_hip_stream_destroy(void *stream);
 enum sam3_error sam3_hip_stream_synchronize(void *stream);
 enum sam3_error sam3_hip_event_create(void **event);

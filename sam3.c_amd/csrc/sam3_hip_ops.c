@@ -1952,6 +1952,10 @@ enum sam3_error sam3_hip_stream_create(void **stream)
 
 enum sam3_error sam3_hip_stream_destroy(void *stream)
 {
+	/* the stream's idle scratch blocks go back to the runtime first: a
+	 * later stream may get the same handle while this one's last kernels
+	 * still run */
+	s3h_scratch_release(stream);
 	return s3h_hip(hipStreamDestroy((hipStream_t)stream), "stream_destroy");
 }
 
