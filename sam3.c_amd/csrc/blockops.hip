@@ -273,6 +273,41 @@ __global__ void __launch_bounds__(256) permute_k(PermArgs a)
 	}
 }
 
+/* f32 permute whose last axis stays last, written as a GEMM operand: the
+ * output, read as rows of K values, becomes bf16 planes [hi|lo|hi] with
+ * row pitch 3K (PLANES) or f16 (else), the split / cast a GEMM applies
+ * to f32 A. One thread per 4 values (one 16-byte source chunk). */
+template <bool PLANES, typename I>
+__global__ void __launch_bounds__(256) permute_op_k(PermArgs a, unsigned K)
+{
+	const I stride = (I)gridDim.x * 256, total = (I)a.total;
+	const I od1 = a.od1, od2 = a.od2, od3 = a.od3;
+	for (I i = (I)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+		I t = i;
+		const I o3 = t % od3;
+		t /= od3;
+		const I o2 = t % od2;
+		t /= od2;
+		const I o1 = t % od1;
+		const I o0 = t / od1;
+		const long long src = (long long)o0 * a.st0 + (long long)o1 * a.st1 +
+				      (long long)o2 * a.st2 + (long long)o3 * a.st3;
+		const float4 v = ((const float4 *)a.src)[src];
+		const long long e = (long long)i * 4;
+		if (PLANES) {
+			uint32_t hi[2], lo[2];
+			split_bf16x2(v.x, v.y, hi[0], lo[0]);
+			split_bf16x2(v.z, v.w, hi[1], lo[1]);
+			uint16_t *d = (uint16_t *)a.dst + (e / K) * 3LL * K + e % K;
+			*(uint2 *)d = make_uint2(hi[0], hi[1]);
+			*(uint2 *)(d + K) = make_uint2(lo[0], lo[1]);
+			*(uint2 *)(d + 2LL * K) = make_uint2(hi[0], hi[1]);
+		} else {
+			*(uint2 *)((uint16_t *)a.dst + e) = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
+		}
+	}
+}
+
 template <typename T>
 static void launch_perm(const PermArgs &a, dim3 grid, hipStream_t st)
 {
@@ -379,6 +414,57 @@ extern "C" int s3k_rope(int kind, const void *x, const float *cos_t, const float
 
 /* dst = src permuted: output axis k is input axis axes[k]; ndim <= 4,
  * esize bytes per element. */
+extern "C" int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
+			      const int *axes, int K, void *stream)
+{
+	if (ndim < 1 || ndim > 4 || K <= 0 || K % 4 || (fmt != S3K_LN_PLANES && fmt != S3K_LN_F16) ||
+	    axes[ndim - 1] != ndim - 1 || in_dims[ndim - 1] % 4 ||
+	    (((uintptr_t)src | (uintptr_t)dst) & 15u))
+		return (int)hipErrorInvalidValue;
+	long long d[4] = {1, 1, 1, 1};
+	int ax[4] = {0, 1, 2, 3};
+	const int pad = 4 - ndim;
+	int seen = 0;
+	for (int k = 0; k < ndim; ++k) {
+		if (in_dims[k] < 0 || axes[k] < 0 || axes[k] >= ndim || (seen >> axes[k]) & 1)
+			return (int)hipErrorInvalidValue;
+		seen |= 1 << axes[k];
+		d[pad + k] = in_dims[k];
+		ax[pad + k] = pad + axes[k];
+	}
+	d[3] /= 4; /* 16-byte chunks of 4 values */
+	const long long ist[4] = {d[1] * d[2] * d[3], d[2] * d[3], d[3], 1};
+	PermArgs a;
+	a.src = (const char *)src;
+	a.dst = (char *)dst;
+	a.od1 = (unsigned)d[ax[1]];
+	a.od2 = (unsigned)d[ax[2]];
+	a.od3 = (unsigned)d[ax[3]];
+	a.st0 = ist[ax[0]];
+	a.st1 = ist[ax[1]];
+	a.st2 = ist[ax[2]];
+	a.st3 = ist[ax[3]];
+	a.total = d[0] * d[1] * d[2] * d[3];
+	if (a.total == 0 || a.od1 == 0 || a.od2 == 0 || a.od3 == 0)
+		return (int)hipSuccess;
+	const long long blocks = (a.total + 255) / 256;
+	const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
+	const hipStream_t st = (hipStream_t)stream;
+	const bool small = a.total * 4 + (long long)grid.x * 256 * 4 < (1LL << 32);
+	if (fmt == S3K_LN_PLANES) {
+		if (small)
+			hipLaunchKernelGGL((permute_op_k<true, unsigned>), grid, block, 0, st, a, (unsigned)K);
+		else
+			hipLaunchKernelGGL((permute_op_k<true, long long>), grid, block, 0, st, a, (unsigned)K);
+	} else {
+		if (small)
+			hipLaunchKernelGGL((permute_op_k<false, unsigned>), grid, block, 0, st, a, (unsigned)K);
+		else
+			hipLaunchKernelGGL((permute_op_k<false, long long>), grid, block, 0, st, a, (unsigned)K);
+	}
+	return (int)hipGetLastError();
+}
+
 extern "C" int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
 			   const int *axes, void *stream)
 {

@@ -115,6 +115,11 @@ int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, vo
 	     int batch, int seq, int heads, int hd, void *stream);
 int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
 		const int *axes, void *stream);
+/* f32 permute (last axis kept, its size % 4 == 0) written as the operand
+ * of a GEMM that reads the output as rows of K values: fmt S3K_LN_PLANES
+ * (bf16 [hi|lo|hi], row pitch 3K) or S3K_LN_F16. */
+int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
+		   const int *axes, int K, void *stream);
 /* f32 rows [rows, K] (pitch ld) -> bf16 [rows, 3K]: [hi, lo, hi] for
  * order 0, [hi, hi, lo] for order 1 (hi = bf16(x), lo = bf16(x - hi)). */
 int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld, int order,

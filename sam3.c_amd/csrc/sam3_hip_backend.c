@@ -441,7 +441,7 @@ static const struct sam3_tensor *folded_source(const struct sam3_graph *g, int u
 
 static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
 				 int j, const struct sam3_tensor *t, int row_len,
-				 struct use_map *uses);
+				 struct use_map *uses, int *k_out);
 
 /* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
  * Returns the number of nodes consumed in *used. */
@@ -527,7 +527,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	int o_fmt = S3H_A_PLAIN;
 	const char *o_env = getenv("SAM3_HIP_GEMM_OPERAND");
 	if (c_dt == SAM3_DTYPE_F32 && !(o_env && atoi(o_env) == 0)) {
-		o_fmt = consumer_operand_form(hb, g, i, j, out, N, uses);
+		o_fmt = consumer_operand_form(hb, g, i, j, out, N, uses, NULL);
 		if (o_fmt != S3H_A_PLAIN &&
 		    !s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, o_fmt))
 			o_fmt = S3H_A_PLAIN;
@@ -565,7 +565,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
  * address. */
 static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
 				 int j, const struct sam3_tensor *t, int row_len,
-				 struct use_map *uses)
+				 struct use_map *uses, int *k_out)
 {
 	for (;;) {
 		if (uses_of(uses, t) != 1)
@@ -607,8 +607,10 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
 		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
 	}
-	if (kb != K || s3h_nelems(t) != (long long)M * K || K != row_len)
+	if (kb != K || s3h_nelems(t) != (long long)M * K || (row_len > 0 && K != row_len))
 		return S3H_A_PLAIN;
+	if (k_out)
+		*k_out = K;
 	void *db = NULL;
 	if (dev_in(hb, bsrc, &db) != SAM3_OK)
 		return S3H_A_PLAIN;
@@ -625,7 +627,42 @@ static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph 
 	if (n->inputs[0]->dtype != SAM3_DTYPE_F32 || !s3h_layernorm_ok(n))
 		return S3H_A_PLAIN;
 	return consumer_operand_form(hb, g, i, i + 1, n->output,
-				     n->inputs[0]->dims[n->inputs[0]->n_dims - 1], uses);
+				     n->inputs[0]->dims[n->inputs[0]->n_dims - 1], uses, NULL);
+}
+
+/* The form an f32 TRANSPOSE at node i that keeps its last axis writes:
+ * its consumer's operand, read as rows of *K values. */
+static int permute_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+				struct use_map *uses, int *K)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->n_inputs < 1 || !n->inputs[0] || !n->output || n->inputs[0]->dtype != SAM3_DTYPE_F32 ||
+	    !s3h_transpose_to_ok(n, 4))
+		return S3H_A_PLAIN;
+	int k = 0;
+	const int f = consumer_operand_form(hb, g, i, i + 1, n->output, 0, uses, &k);
+	if (f == S3H_A_PLAIN || !s3h_transpose_to_ok(n, k))
+		return S3H_A_PLAIN;
+	*K = k;
+	return f;
+}
+
+/* TRANSPOSE written as the operand form fmt of its one consuming GEMM. */
+static enum sam3_error run_permute_as(struct sam3_hip_backend *hb, const struct sam3_node *n,
+				      int fmt, int K)
+{
+	void *dx = NULL, *dy = NULL;
+	enum sam3_error err = dev_in(hb, n->inputs[0], &dx);
+	if (err == SAM3_OK)
+		err = dev_out_fmt(hb, n->output,
+				  (size_t)s3h_nelems(n->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
+	if (err == SAM3_OK)
+		err = s3h_transpose_to(n, dx, dy, fmt, K, hb->stream);
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.operand_writes++;
+	}
+	return err;
 }
 
 /* LAYERNORM written as the operand form fmt of its one consuming GEMM. */
@@ -859,7 +896,9 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	s3h_cur = hb;
 	const char *ln_env = getenv("SAM3_HIP_LN_OPERAND");
 	const int ln_plain = ln_env && atoi(ln_env) == 0;
-	int ln_fmt = S3H_A_PLAIN;
+	const char *perm_env = getenv("SAM3_HIP_PERMUTE_OPERAND");
+	const int perm_plain = perm_env && atoi(perm_env) == 0;
+	int ln_fmt = S3H_A_PLAIN, perm_k = 0;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -881,6 +920,9 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain &&
 			   (ln_fmt = ln_operand_form(hb, g, i, &uses)) != S3H_A_PLAIN) {
 			err = run_layernorm_as(hb, n, ln_fmt);
+		} else if (n->op == SAM3_OP_TRANSPOSE && !perm_plain &&
+			   (ln_fmt = permute_operand_form(hb, g, i, &uses, &perm_k)) != S3H_A_PLAIN) {
+			err = run_permute_as(hb, n, ln_fmt, perm_k);
 		} else if (runs_on_gpu(n)) {
 			err = run_elementwise(hb, n);
 		} else {

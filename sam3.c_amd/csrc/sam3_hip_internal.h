@@ -22,6 +22,11 @@ enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream);
 int s3h_transpose_is_swap(const struct sam3_node *node);
+/* f32 TRANSPOSE keeping its last axis, written as the operand form fmt
+ * (S3H_A_PLANES / S3H_A_F16) of a GEMM reading the output as rows of K. */
+int s3h_transpose_to_ok(const struct sam3_node *node, int K);
+enum sam3_error s3h_transpose_to(const struct sam3_node *node, const void *src, void *dst, int fmt,
+				 int K, void *stream);
 /* Device scratch reused in stream order: a block given back with
  * s3h_scratch_free(p, stream) is handed out again only to requests on
  * that stream. s3h_scratch_release(stream) returns the stream's idle

@@ -1075,6 +1075,35 @@ enum sam3_error s3h_transpose(const struct sam3_node *node, void *stream)
 		       "transpose");
 }
 
+/* An f32 TRANSPOSE that keeps its last axis, with its output read as rows
+ * of K values by a GEMM that converts A first: written in that operand
+ * form (S3H_A_PLANES or S3H_A_F16) by s3h_transpose_to. */
+int s3h_transpose_to_ok(const struct sam3_node *node, int K)
+{
+	if (!s3h_transpose_ok(node) || node->inputs[0]->dtype != SAM3_DTYPE_F32 || K <= 0 || K % 4)
+		return 0;
+	const struct sam3_tensor *in = node->inputs[0];
+	const int nd = in->n_dims;
+	int axes[4];
+	transpose_axes(node, nd, axes);
+	return axes[nd - 1] == nd - 1 && in->dims[nd - 1] % 4 == 0 && s3h_nelems(in) % K == 0;
+}
+
+enum sam3_error s3h_transpose_to(const struct sam3_node *node, const void *src, void *dst, int fmt,
+				 int K, void *stream)
+{
+	if (!s3h_transpose_to_ok(node, K) || (fmt != S3H_A_PLANES && fmt != S3H_A_F16)) {
+		s3h_error("transpose: cannot write GEMM operand form %d (K=%d)", fmt, K);
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *in = node->inputs[0];
+	int axes[4];
+	transpose_axes(node, in->n_dims, axes);
+	return s3h_hip(s3k_permute_to(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
+				      (const float *)src, dst, in->n_dims, in->dims, axes, K, stream),
+		       "transpose (GEMM operand)");
+}
+
 /* LAYERNORM (cpu_layernorm.c:198-254 and its bf16/f16 twins): the last
  * dim is normalized; gamma and beta (optional) have the input's dtype. */
 int s3h_layernorm_ok(const struct sam3_node *node)

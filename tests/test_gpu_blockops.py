@@ -368,6 +368,47 @@ def test_gemm_written_as_next_gemm_operand(monkeypatch, wkind):
     assert_f32_close(fused, ref.astype(np.float32), what=f"LN -> MLP {wkind}")
 
 
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_permute_written_as_gemm_operand(monkeypatch, wkind):
+    """The attention head merge (gh_multihead_attention_rope, [B,H,N,D] ->
+    [B,N,H,D] -> [B*N, H*D] -> out projection): an f32 TRANSPOSE that keeps
+    its last axis and feeds only a GEMM's A writes that GEMM's operand
+    (bf16 planes / f16) while permuting, the same split / cast the GEMM
+    applies otherwise, so the result is the same bit for bit."""
+    B, H, N, D, E = 2, 4, 256, 64, 256
+    O = oracle()
+    x = synth.randn(840, (B, H, N, D))
+    w, bias = synth.randn(841, (E, H * D), 0.05), synth.randn(842, (E,), 0.02)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_PERMUTE_OPERAND", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_PERMUTE_OPERAND", env)
+        G = graph.Graph()
+        t = G.permute(G.tensor(abi.F32, x.shape, x), (0, 2, 1, 3))
+        tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, w.shape, w))
+        y = G.linear(G.reshape(t, [B * N, H * D]), tw, G.tensor(abi.F32, (E,), bias))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(B * N, E)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.operand_writes == 1 and st0.operand_writes == 0
+    assert st.host_nodes == 0 and st.downloads == 1
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    a = x.transpose(0, 2, 1, 3).reshape(B * N, H * D).astype(np.float64)
+    wd = (O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8"
+          else w).astype(np.float64)
+    assert_f32_close(fused, (a @ wd.T + bias).astype(np.float32), what=f"permute -> linear {wkind}")
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
