@@ -647,6 +647,119 @@ static int permute_operand_form(struct sam3_hip_backend *hb, const struct sam3_g
 	return f;
 }
 
+/* gh_multihead_attention_rope's q, k and v preparation
+ * (graph_helpers.c:721-882): SLICE of the fused qkv output's columns ->
+ * RESHAPE [B, S, H, D] -> (ROPE -> RESHAPE ...) -> TRANSPOSE (0, 2, 1, 3).
+ * Every tensor in between is used once, so the chain runs as one kernel
+ * from the qkv rows to the head-split operand (s3k_rope_split). */
+struct qkv_chain {
+	int n, idx[8];
+	const struct sam3_tensor *src, *out, *cos_t, *sin_t;
+	long long col0, pitch;
+	int B, S, H, D;
+};
+
+static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t)
+{
+	for (; j < g->n_nodes; j++) {
+		const struct sam3_node *m = &g->nodes[j];
+		for (int k = 0; k < m->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++)
+			if (m->inputs[k] == t)
+				return j;
+	}
+	return -1;
+}
+
+static int dims_are(const struct sam3_tensor *t, int B, int S, int H, int D)
+{
+	return t && t->n_dims == 4 && t->dims[0] == B && t->dims[1] == S && t->dims[2] == H &&
+	       t->dims[3] == D;
+}
+
+static int match_qkv_chain(const struct sam3_graph *g, int i, struct use_map *uses,
+			   struct qkv_chain *c)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->op != SAM3_OP_SLICE || n->n_inputs < 1 || !n->inputs[0] || !n->output ||
+	    !s3h_slice_ok(n))
+		return 0;
+	const struct sam3_tensor *x = n->inputs[0];
+	const int c0 = n->params[1], c1 = n->params[2];
+	if (x->dtype != SAM3_DTYPE_F32 || x->n_dims != 2 || n->params[0] != 1 || c0 % 4 ||
+	    x->dims[1] % 4 || c1 <= c0 || c1 > x->dims[1])
+		return 0;
+	c->n = 0;
+	c->idx[c->n++] = i;
+	const struct sam3_tensor *t = n->output;
+	int j = i;
+	if (uses_of(uses, t) != 1 || (j = next_reader(g, j + 1, t)) < 0 ||
+	    g->nodes[j].op != SAM3_OP_RESHAPE || !g->nodes[j].output)
+		return 0;
+	c->idx[c->n++] = j;
+	t = g->nodes[j].output;
+	if (t->n_dims != 4)
+		return 0;
+	const int B = t->dims[0], S = t->dims[1], H = t->dims[2], D = t->dims[3];
+	if ((long long)B * S != x->dims[0] || (long long)H * D != c1 - c0 || D % 4)
+		return 0;
+	c->cos_t = c->sin_t = NULL;
+	for (;;) {
+		if (uses_of(uses, t) != 1 || (j = next_reader(g, j + 1, t)) < 0 || c->n >= 8)
+			return 0;
+		const struct sam3_node *m = &g->nodes[j];
+		if (!m->output || m->inputs[0] != t)
+			return 0;
+		if (m->op == SAM3_OP_RESHAPE && s3h_nelems(m->output) == (long long)B * S * H * D) {
+			c->idx[c->n++] = j;
+			t = m->output;
+		} else if (m->op == SAM3_OP_ROPE && !c->cos_t && dims_are(t, B, S, H, D) &&
+			   s3h_rope_ok(m) && m->output->dtype == SAM3_DTYPE_F32) {
+			c->cos_t = m->inputs[1];
+			c->sin_t = m->inputs[2];
+			c->idx[c->n++] = j;
+			t = m->output;
+		} else if (m->op == SAM3_OP_TRANSPOSE && dims_are(t, B, S, H, D) && m->params[0] == 0 &&
+			   m->params[1] == 2 && m->params[2] == 1 && m->params[3] == 3 &&
+			   dims_are(m->output, B, H, S, D) && m->output->dtype == SAM3_DTYPE_F32) {
+			c->idx[c->n++] = j;
+			c->out = m->output;
+			break;
+		} else {
+			return 0;
+		}
+	}
+	c->src = x;
+	c->col0 = c0;
+	c->pitch = x->dims[1];
+	c->B = B;
+	c->S = S;
+	c->H = H;
+	c->D = D;
+	return 1;
+}
+
+static enum sam3_error run_qkv_chain(struct sam3_hip_backend *hb, const struct qkv_chain *c)
+{
+	void *dx = NULL, *dc = NULL, *ds = NULL, *dy = NULL;
+	enum sam3_error err = dev_in(hb, c->src, &dx);
+	if (err == SAM3_OK && c->cos_t)
+		err = dev_in(hb, c->cos_t, &dc);
+	if (err == SAM3_OK && c->sin_t)
+		err = dev_in(hb, c->sin_t, &ds);
+	if (err == SAM3_OK)
+		err = dev_out(hb, c->out, &dy);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_rope_split((const float *)dx, c->pitch, c->col0, (const float *)dc,
+					     (const float *)ds, (float *)dy, c->B, c->S, c->H, c->D,
+					     hb->stream),
+			      "attention operand (slice, rope, head split)");
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.fused_nodes += c->n - 1;
+	}
+	return err;
+}
+
 /* TRANSPOSE written as the operand form fmt of its one consuming GEMM. */
 static enum sam3_error run_permute_as(struct sam3_hip_backend *hb, const struct sam3_node *n,
 				      int fmt, int K)
@@ -885,7 +998,12 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	if (err != SAM3_OK)
 		return err;
 	unsigned char *folded = calloc((size_t)g->n_nodes, 1);
-	if (!folded) {
+	unsigned char *done = calloc((size_t)g->n_nodes, 1);
+	const char *qkv_env = getenv("SAM3_HIP_QKV_CHAIN");
+	const int qkv_plain = qkv_env && atoi(qkv_env) == 0;
+	if (!folded || !done) {
+		free(folded);
+		free(done);
 		free(uses.key);
 		free(uses.count);
 		s3h_error("graph_eval: out of host memory");
@@ -903,8 +1021,13 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
 		int used = 1;
-		if (n->op == SAM3_OP_NONE) {
-			err = SAM3_OK;
+		struct qkv_chain qc;
+		if (n->op == SAM3_OP_NONE || done[i]) {
+			err = SAM3_OK; /* done[i]: run earlier as part of a chain */
+		} else if (n->op == SAM3_OP_SLICE && !qkv_plain && match_qkv_chain(g, i, &uses, &qc)) {
+			err = run_qkv_chain(hb, &qc);
+			for (int k = 1; k < qc.n; k++)
+				done[qc.idx[k]] = 1;
 		} else if (n->op == SAM3_OP_RESHAPE) {
 			/* a view: consumers find the input's device copy under the
 			 * same host address */
@@ -986,6 +1109,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		if (!hb->res[i].keep)
 			res_drop_at(hb, i);
 	free(folded);
+	free(done);
 	free(uses.key);
 	free(uses.count);
 	return err;

@@ -409,6 +409,62 @@ def test_permute_written_as_gemm_operand(monkeypatch, wkind):
     assert_f32_close(fused, (a @ wd.T + bias).astype(np.float32), what=f"permute -> linear {wkind}")
 
 
+def test_qkv_slice_rope_split_chain(monkeypatch):
+    """gh_multihead_attention_rope's q / k / v preparation: SLICE of the
+    fused qkv rows -> RESHAPE [B,S,H,D] -> (ROPE -> RESHAPE -> RESHAPE) ->
+    TRANSPOSE (0,2,1,3) runs as one kernel reading the qkv rows in place
+    (no slice copies, no separate RoPE or permute pass). Same bits as the
+    node-by-node run (SAM3_HIP_QKV_CHAIN=0), and equal to RoPE by the
+    reference's pair formula in float32 (products and sums rounded
+    separately) followed by the head split."""
+    side, H, D = 6, 4, 32
+    B, S, E = 2, side * side, H * D
+    qkv = synth.randn(860, (B * S, 3 * E))
+    c, sn = graph.rope_tables(side, D)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_QKV_CHAIN", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_QKV_CHAIN", env)
+        G = graph.Graph()
+        x = G.tensor(abi.F32, (B * S, 3 * E), qkv)
+        ct, st_ = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, sn.shape, sn)
+        sq, sk, sv = (G.slice(x, 1, i * E, (i + 1) * E) for i in range(3))
+        four = [B, S, H, D]
+        q = G.reshape(G.rope(G.reshape(sq, four), ct, st_), [B * S, E])
+        k = G.reshape(G.rope(G.reshape(sk, four), ct, st_), [B * S, E])
+        outs = [G.permute(G.reshape(t, four), (0, 2, 1, 3)) for t in (q, k, sv)]
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return [np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_float)), shape=(B, H, S, D)).copy()
+                for t in outs], st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st.downloads == 3
+    assert st.gpu_nodes == 3 and st0.gpu_nodes > 3
+    for f, p in zip(fused, plain):
+        assert np.array_equal(f.view(np.uint32), p.view(np.uint32))
+
+    def rope_ref(v):
+        v = v.reshape(B, S, H, D // 2, 2)
+        cc, ss = c[None, :, None, :], sn[None, :, None, :]
+        x0, x1 = v[..., 0], v[..., 1]
+        o0 = (x0 * cc).astype(np.float32) - (x1 * ss).astype(np.float32)
+        o1 = (x0 * ss).astype(np.float32) + (x1 * cc).astype(np.float32)
+        return np.stack([o0, o1], -1).reshape(B, S, H, D)
+
+    parts = [qkv[:, i * E:(i + 1) * E].reshape(B, S, H, D) for i in range(3)]
+    refs = [rope_ref(parts[0]), rope_ref(parts[1]), parts[2]]
+    for f, r in zip(fused, refs):
+        assert np.array_equal(f.view(np.uint32), r.transpose(0, 2, 1, 3).astype(np.float32).view(np.uint32))
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
