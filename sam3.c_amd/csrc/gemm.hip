@@ -504,6 +504,8 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.b = (const char *)g->b;
 	p.c = (char *)g->c;
 	p.bias = (const char *)g->bias;
+	p.res = (const char *)g->res;
+	p.ldr = g->N;
 	p.M = g->M;
 	p.N = g->N;
 	p.K = g->K;
@@ -635,6 +637,9 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 {
 	hipStream_t st = (hipStream_t)stream;
 	GemmArgs p = make_args(g);
+	if ((g->flags & S3K_EPI_RES) && (path != S3K_PATH_MFMA || !g->res || g->batch != 1 ||
+					 g->c_kind == S3K_BF16 || g->c_kind == S3K_F16))
+		return (int)hipErrorInvalidValue; /* only the LDS epilogue adds a residual */
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))
 			return (int)hipErrorInvalidValue;

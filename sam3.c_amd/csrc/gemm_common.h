@@ -16,9 +16,11 @@ struct GemmArgs {
 	const char *b;
 	char       *c;
 	const char *bias;
+	const char *res;              /* S3K_EPI_RES: f32 rows of ldr values */
 	int M, N, K;
 	long long lda_b, ldb_b, ldc;  /* A/B row pitch in bytes, C in elements */
 	long long sa_b, sb_b, sc;     /* batch strides: bytes, bytes, elements */
+	long long ldr;                /* residual row pitch, elements */
 	int flags;
 	int c_kind;
 	int bias_kind;
@@ -160,6 +162,25 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 #pragma unroll
 		for (int e = 0; e < W; ++e)
 			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
+		if (p.flags & S3K_EPI_RES) {
+			/* the residual ADD node that follows, in f32 */
+			const float *r = (const float *)p.res + (long long)m * p.ldr + n;
+			if (full && (((uintptr_t)r & 15u) == 0)) {
+#pragma unroll
+				for (int e = 0; e < W; e += 4) {
+					const float4 q = *(const float4 *)(r + e);
+					x[e] = add_rn(x[e], q.x);
+					x[e + 1] = add_rn(x[e + 1], q.y);
+					x[e + 2] = add_rn(x[e + 2], q.z);
+					x[e + 3] = add_rn(x[e + 3], q.w);
+				}
+			} else {
+#pragma unroll
+				for (int e = 0; e < W; ++e)
+					if (n + e < p.N)
+						x[e] = add_rn(x[e], r[e]);
+			}
+		}
 	}
 	const long long o = (long long)m * p.ldc + n;
 	if constexpr (CK == S3K_C_PLANES) {
@@ -238,7 +259,7 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
 	static_assert(CK != S3K_C_PLANES || WTN % 8 == 0, "planes are written 8 outputs at a time");
-	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU)) != 0;
+	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES)) != 0;
 	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
 	 * so consecutive lanes write consecutive 16 bytes of a row */
 	constexpr int W = CK == S3K_F32 ? 4 : 8;

@@ -33,6 +33,8 @@ enum s3k_kind {
 #define S3K_EPI_BIAS 1  /* out += bias[n] (bias has the output's kind)    */
 #define S3K_EPI_GELU 2  /* out = tanh-GELU(out)                           */
 #define S3K_B_NT     4  /* B stored [N,K] (k contiguous), else [K,N]      */
+#define S3K_EPI_RES  8  /* out += res[m][n] last (res f32 [M,N]; kernels
+			 * with the shared LDS epilogue only)             */
 
 /*
  * One (optionally strided-batched) GEMM: C[M,N] = A[M,K] * B, row-major.
@@ -53,6 +55,7 @@ struct s3k_gemm {
 	int         batch;
 	int         a_kind, b_kind, c_kind;
 	int         flags;
+	const void *res;                          /* S3K_EPI_RES: f32 [M, N] */
 };
 
 /* Which kernel s3k_gemm_launch would pick (for tests and the bench). */

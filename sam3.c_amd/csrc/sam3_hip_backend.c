@@ -512,7 +512,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		j++;
 	}
 
-	void *da, *db, *dc, *dbias = NULL;
+	void *da, *db, *dc, *dbias = NULL, *dres = NULL;
 	const struct s3h_res *ae = res_find(hb, a->data);
 	const int a_fmt = ae ? ae->fmt : S3H_A_PLAIN;
 	enum sam3_error err = dev_in(hb, a, &da);
@@ -522,6 +522,27 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_in(hb, bias, &dbias);
 	if (err != SAM3_OK)
 		return err;
+	/* a residual ADD of an f32 [M, N] tensor computed earlier (the
+	 * block's x + attention / + MLP), folded last into the epilogue */
+	const char *r_env = getenv("SAM3_HIP_RESIDUAL_FOLD");
+	if (c_dt == SAM3_DTYPE_F32 && !(r_env && atoi(r_env) == 0) && j < g->n_nodes &&
+	    g->nodes[j].op == SAM3_OP_ADD && g->nodes[j].n_inputs == 2 && g->nodes[j].output &&
+	    uses_of(uses, out) == 1 &&
+	    s3h_nelems(g->nodes[j].output) == (long long)M * N) {
+		const struct sam3_node *ad = &g->nodes[j];
+		const struct sam3_tensor *r = ad->inputs[0] == out ? ad->inputs[1]
+					      : ad->inputs[1] == out ? ad->inputs[0] : NULL;
+		if (r && r != out && r->data && r->dtype == SAM3_DTYPE_F32 &&
+		    ad->output->dtype == SAM3_DTYPE_F32 && s3h_nelems(r) == (long long)M * N &&
+		    r->data != ad->output->data &&
+		    s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, S3H_A_PLAIN) &&
+		    dev_in(hb, r, &dres) == SAM3_OK) {
+			out = ad->output;
+			j++;
+		} else {
+			dres = NULL;
+		}
+	}
 	/* an f32 result read only by the next GEMM, which converts its A
 	 * first: written in that form by this GEMM's epilogue */
 	int o_fmt = S3H_A_PLAIN;
@@ -536,9 +557,14 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
-						flags, hb->stream);
+						dres, flags, hb->stream);
 		if (err == SAM3_OK)
 			hb->stats.operand_writes++;
+	} else if (dres) {
+		err = dev_out(hb, out, &dc);
+		if (err == SAM3_OK)
+			err = s3h_matmul_fmt_to(a_fmt, S3H_A_PLAIN, a_dt, da, b_dt, db, dc, M, N, K,
+						dbias, dres, flags, hb->stream);
 	} else {
 		err = dev_out(hb, out, &dc);
 		if (err != SAM3_OK)

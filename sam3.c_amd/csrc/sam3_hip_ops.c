@@ -571,18 +571,19 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 	return SAM3_EINVAL;
 }
 
-/* Whether the GEMM that s3h_matmul_fmt runs for A in form a_fmt can write
- * its f32 result directly as the operand form out_fmt (S3H_A_PLANES or
- * S3H_A_F16) of a following GEMM. Only the direct-to-LDS GEMM writes those
- * forms; f32 weights reach it through the split GEMM (planes), Q8_0
- * weights through their f16 expansion (f16 A only). b is the weight's
- * device address; a is used for its alignment only. */
+/* Whether the GEMM that s3h_matmul_fmt runs for A in form a_fmt ends in
+ * the direct-to-LDS GEMM, which can write its f32 result as the operand
+ * form out_fmt (S3H_A_PLANES or S3H_A_F16) of a following GEMM, or as f32
+ * (S3H_A_PLAIN) with a residual added. f32 weights reach it through the
+ * split GEMM, Q8_0 weights through their f16 expansion (f16 A only). b
+ * is the weight's device address; a is used for its alignment only. */
 int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags, int out_fmt)
 {
 	static const char al[16] __attribute__((aligned(16)));
-	if ((out_fmt != S3H_A_PLANES && out_fmt != S3H_A_F16) || M <= 0 || N <= 0 || K <= 0 ||
-	    N % 8 || !a || !b || check_kinds(a_dt, b_dt, SAM3_DTYPE_F32) != SAM3_OK)
+	if ((out_fmt != S3H_A_PLAIN && out_fmt != S3H_A_PLANES && out_fmt != S3H_A_F16) || M <= 0 ||
+	    N <= 0 || K <= 0 || (out_fmt != S3H_A_PLAIN && N % 8) || !a || !b ||
+	    check_kinds(a_dt, b_dt, SAM3_DTYPE_F32) != SAM3_OK)
 		return 0;
 	struct s3k_gemm g;
 	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
@@ -615,17 +616,23 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
  * of the f32 output would give. */
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
-				  int flags, void *stream)
+				  const void *res, int flags, void *stream)
 {
-	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) ||
+	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) || (res && ((uintptr_t)res & 3u)) ||
 	    !s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt)) {
-		s3h_error("matmul: cannot write operand form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
+		s3h_error("matmul: cannot write form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
 		return SAM3_EINVAL;
 	}
 	struct s3k_gemm g;
 	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
-	g.c_kind = out_fmt == S3H_A_PLANES ? S3K_C_PLANES : S3K_C_F16OP;
+	g.c_kind = out_fmt == S3H_A_PLANES ? S3K_C_PLANES
+		 : out_fmt == S3H_A_F16     ? S3K_C_F16OP
+					    : S3K_F32;
 	g.ldc = out_fmt == S3H_A_PLANES ? 3 * N : N;
+	if (res) {
+		g.res = res;
+		g.flags |= S3K_EPI_RES;
+	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
 	g.a_kind = S3K_F16;

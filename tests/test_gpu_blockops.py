@@ -465,6 +465,48 @@ def test_qkv_slice_rope_split_chain(monkeypatch):
         assert np.array_equal(f.view(np.uint32), r.transpose(0, 2, 1, 3).astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_residual_add_folded_into_gemm(monkeypatch, wkind):
+    """x + linear(LN(x)) as the ViT block builds its residuals
+    (image_encoder.c:755-916): the ADD of the earlier f32 tensor is done in
+    the GEMM epilogue after the bias, one f32 rounding as the ADD node
+    does, so the result is the same bit for bit as the unfolded graph."""
+    M, E = 1024, 512
+    O = oracle()
+    x = synth.randn(870, (M, E))
+    gam, bet = synth.randn(871, (E,)), synth.randn(872, (E,), 0.1)
+    w, bias = synth.randn(873, (E, E), 0.04), synth.randn(874, (E,), 0.02)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_RESIDUAL_FOLD", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_RESIDUAL_FOLD", env)
+        G = graph.Graph()
+        tx = G.tensor(abi.F32, (M, E), x)
+        t = G.layernorm(tx, G.tensor(abi.F32, (E,), gam), G.tensor(abi.F32, (E,), bet))
+        tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, w.shape, w))
+        y = G.add(tx, G.linear(t, tw, G.tensor(abi.F32, (E,), bias)))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(M, E)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.fused_nodes == st0.fused_nodes + 1 and st.gpu_nodes == st0.gpu_nodes - 1
+    assert st.host_nodes == 0 and st.downloads == 1
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    ln = O.layernorm(x, gam, bet, "f32", threads=8).astype(np.float64)
+    wd = (O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8"
+          else w).astype(np.float64)
+    assert_f32_close(fused, (x + ln @ wd.T + bias).astype(np.float32), what=f"x + linear {wkind}")
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
