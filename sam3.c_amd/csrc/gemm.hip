@@ -506,6 +506,9 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.bias = (const char *)g->bias;
 	p.res = (const char *)g->res;
 	p.ldr = g->N;
+	p.rm_g = g->rm_g;
+	p.rm_d1 = g->rm_d1;
+	p.rm_d2 = g->rm_d2;
 	p.M = g->M;
 	p.N = g->N;
 	p.K = g->K;
@@ -637,9 +640,12 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 {
 	hipStream_t st = (hipStream_t)stream;
 	GemmArgs p = make_args(g);
-	if ((g->flags & S3K_EPI_RES) && (path != S3K_PATH_MFMA || !g->res || g->batch != 1 ||
-					 g->c_kind == S3K_BF16 || g->c_kind == S3K_F16))
-		return (int)hipErrorInvalidValue; /* only the LDS epilogue adds a residual */
+	if (((g->flags & S3K_EPI_RES) || g->rm_g) &&
+	    (path != S3K_PATH_MFMA || ((g->flags & S3K_EPI_RES) && !g->res) || g->batch != 1 ||
+	     g->c_kind == S3K_BF16 || g->c_kind == S3K_F16 ||
+	     (g->rm_g && (g->rm_d1 <= 0 || g->rm_d2 <= 0 ||
+			  g->M % ((long long)g->rm_g * g->rm_d1 * g->rm_d2)))))
+		return (int)hipErrorInvalidValue; /* only the LDS epilogue adds a residual / maps rows */
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))
 			return (int)hipErrorInvalidValue;

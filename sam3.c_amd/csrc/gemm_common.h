@@ -21,6 +21,7 @@ struct GemmArgs {
 	long long lda_b, ldb_b, ldc;  /* A/B row pitch in bytes, C in elements */
 	long long sa_b, sb_b, sc;     /* batch strides: bytes, bytes, elements */
 	long long ldr;                /* residual row pitch, elements */
+	int rm_g, rm_d1, rm_d2;       /* output row map (s3k_gemm), rm_g 0 = none */
 	int flags;
 	int c_kind;
 	int bias_kind;
@@ -104,6 +105,17 @@ __device__ __forceinline__ void wave_lds_fence()
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+/* Output row of logical row m under the row map (identity when rm_g is 0). */
+__device__ __forceinline__ long long out_row(const GemmArgs &p, int m)
+{
+	if (!p.rm_g)
+		return m;
+	const int gi = m / p.rm_g, w = m - gi * p.rm_g;
+	const int c = gi % p.rm_d2, t = gi / p.rm_d2;
+	const int b = t % p.rm_d1, a = t / p.rm_d1;
+	return ((long long)(a * p.rm_d2 + c) * p.rm_d1 + b) * p.rm_g + w;
+}
+
 /* Store of C[m][n..n+W-1] from W f32 values at v (LDS), output kind CK,
  * W = 4 for f32 C and 8 for 16-bit C (one 16-byte store either way).
  * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
@@ -164,7 +176,7 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
 		if (p.flags & S3K_EPI_RES) {
 			/* the residual ADD node that follows, in f32 */
-			const float *r = (const float *)p.res + (long long)m * p.ldr + n;
+			const float *r = (const float *)p.res + out_row(p, m) * p.ldr + n;
 			if (full && (((uintptr_t)r & 15u) == 0)) {
 #pragma unroll
 				for (int e = 0; e < W; e += 4) {
@@ -182,7 +194,7 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 			}
 		}
 	}
-	const long long o = (long long)m * p.ldc + n;
+	const long long o = out_row(p, m) * p.ldc + n;
 	if constexpr (CK == S3K_C_PLANES) {
 		/* the split of split3_bf16_k: hi = bf16(x), lo = bf16(x - hi) */
 		uint32_t hi[4], lo[4];

@@ -56,6 +56,11 @@ struct s3k_gemm {
 	int         a_kind, b_kind, c_kind;
 	int         flags;
 	const void *res;                          /* S3K_EPI_RES: f32 [M, N] */
+	/* row map (rm_g > 0): C row m is stored (and its residual read) at
+	 * row ((a*rm_d2 + c)*rm_d1 + b)*rm_g + m % rm_g, where
+	 * m / rm_g = (a*rm_d1 + b)*rm_d2 + c: the permute (0,2,1,3) of
+	 * [., rm_d1, rm_d2, rm_g*N] applied to the output */
+	int         rm_g, rm_d1, rm_d2;
 };
 
 /* Which kernel s3k_gemm_launch would pick (for tests and the bench). */

@@ -442,12 +442,13 @@ static const struct sam3_tensor *folded_source(const struct sam3_graph *g, int u
 static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
 				 int j, const struct sam3_tensor *t, int row_len,
 				 struct use_map *uses, int *k_out);
+static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t);
 
 /* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
  * Returns the number of nodes consumed in *used. */
 static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3_graph *g,
-				  int i, const unsigned char *folded, struct use_map *uses,
-				  int *used)
+				  int i, const unsigned char *folded, unsigned char *done,
+				  struct use_map *uses, int *used)
 {
 	const struct sam3_node *n = &g->nodes[i];
 	if (n->n_inputs < 2 || !n->inputs[0] || !n->inputs[1] || !n->output) {
@@ -522,10 +523,70 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_in(hb, bias, &dbias);
 	if (err != SAM3_OK)
 		return err;
+	/* gh_window_unpartition (graph_helpers.c:480-509) right after the
+	 * GEMM: RESHAPE... -> TRANSPOSE (0,2,1,3) of [d0, d1, d2, g*N] ->
+	 * RESHAPE..., every tensor used once, optionally followed by the
+	 * residual ADD: a permutation of whole C rows, done by the epilogue's
+	 * row map (and the ADD with it); the chain's nodes are marked done */
+	int row_map[3] = {0, 0, 0}, chain[10], n_chain = 0;
+	const char *u_env = getenv("SAM3_HIP_UNPARTITION_FOLD");
+	if (c_dt == SAM3_DTYPE_F32 && !(u_env && atoi(u_env) == 0) &&
+	    s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, S3H_A_PLAIN)) {
+		const struct sam3_tensor *t = out;
+		int k = j - 1, ok = 0;
+		for (;;) {
+			if (uses_of(uses, t) != 1 || n_chain >= 8 || (k = next_reader(g, k + 1, t)) < 0)
+				break;
+			const struct sam3_node *m = &g->nodes[k];
+			if (m->inputs[0] != t || !m->output || done[k])
+				break;
+			if (m->op == SAM3_OP_RESHAPE && s3h_nelems(m->output) == (long long)M * N) {
+				chain[n_chain++] = k;
+				t = m->output;
+			} else if (!ok && m->op == SAM3_OP_TRANSPOSE && t->n_dims == 4 &&
+				   m->params[0] == 0 && m->params[1] == 2 && m->params[2] == 1 &&
+				   m->params[3] == 3 && m->output->dtype == SAM3_DTYPE_F32 &&
+				   t->dims[3] % N == 0 && (long long)t->dims[0] * t->dims[1] * t->dims[2] *
+				   t->dims[3] == (long long)M * N) {
+				row_map[0] = t->dims[3] / N;
+				row_map[1] = t->dims[1];
+				row_map[2] = t->dims[2];
+				chain[n_chain++] = k;
+				t = m->output;
+				ok = 1;
+			} else {
+				break;
+			}
+		}
+		/* the residual ADD of the unpartitioned result completes the fold
+		 * (its output, unlike the views before it, has its own buffer) */
+		int fold = 0;
+		if (ok) {
+			const int ka = uses_of(uses, t) == 1 ? next_reader(g, chain[n_chain - 1] + 1, t) : -1;
+			const struct sam3_node *ad = ka >= 0 ? &g->nodes[ka] : NULL;
+			const struct sam3_tensor *r = NULL;
+			if (ad && ad->op == SAM3_OP_ADD && ad->n_inputs == 2 && ad->output && !done[ka])
+				r = ad->inputs[0] == t ? ad->inputs[1] : ad->inputs[1] == t ? ad->inputs[0] : NULL;
+			if (r && r != t && r->data && r->dtype == SAM3_DTYPE_F32 &&
+			    ad->output->dtype == SAM3_DTYPE_F32 && s3h_nelems(r) == (long long)M * N &&
+			    s3h_nelems(ad->output) == (long long)M * N && r->data != ad->output->data &&
+			    dev_in(hb, r, &dres) == SAM3_OK) {
+				chain[n_chain++] = ka;
+				out = ad->output;
+				fold = 1;
+			} else {
+				dres = NULL;
+			}
+		}
+		if (!fold) {
+			n_chain = 0;
+			row_map[0] = 0;
+		}
+	}
 	/* a residual ADD of an f32 [M, N] tensor computed earlier (the
 	 * block's x + attention / + MLP), folded last into the epilogue */
 	const char *r_env = getenv("SAM3_HIP_RESIDUAL_FOLD");
-	if (c_dt == SAM3_DTYPE_F32 && !(r_env && atoi(r_env) == 0) && j < g->n_nodes &&
+	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && !(r_env && atoi(r_env) == 0) && j < g->n_nodes &&
 	    g->nodes[j].op == SAM3_OP_ADD && g->nodes[j].n_inputs == 2 && g->nodes[j].output &&
 	    uses_of(uses, out) == 1 &&
 	    s3h_nelems(g->nodes[j].output) == (long long)M * N) {
@@ -547,7 +608,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	 * first: written in that form by this GEMM's epilogue */
 	int o_fmt = S3H_A_PLAIN;
 	const char *o_env = getenv("SAM3_HIP_GEMM_OPERAND");
-	if (c_dt == SAM3_DTYPE_F32 && !(o_env && atoi(o_env) == 0)) {
+	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && !(o_env && atoi(o_env) == 0)) {
 		o_fmt = consumer_operand_form(hb, g, i, j, out, N, uses, NULL);
 		if (o_fmt != S3H_A_PLAIN &&
 		    !s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, o_fmt))
@@ -557,14 +618,18 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
-						dres, flags, hb->stream);
+						dres, NULL, flags, hb->stream);
 		if (err == SAM3_OK)
 			hb->stats.operand_writes++;
-	} else if (dres) {
+	} else if (dres || row_map[0]) {
 		err = dev_out(hb, out, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, S3H_A_PLAIN, a_dt, da, b_dt, db, dc, M, N, K,
-						dbias, dres, flags, hb->stream);
+						dbias, dres, row_map[0] ? row_map : NULL, flags,
+						hb->stream);
+		if (err == SAM3_OK)
+			for (int k = 0; k < n_chain; k++)
+				done[chain[k]] = 1;
 	} else {
 		err = dev_out(hb, out, &dc);
 		if (err != SAM3_OK)
@@ -576,7 +641,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	}
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
-		hb->stats.fused_nodes += j - i - 1;
+		hb->stats.fused_nodes += j - i - 1 + n_chain;
 		*used = j - i;
 	}
 	return err;
@@ -1062,7 +1127,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 			folded[i] = 1;
 			hb->stats.fused_nodes++;
 		} else if (n->op == SAM3_OP_MATMUL) {
-			err = run_matmul(hb, g, i, folded, &uses, &used);
+			err = run_matmul(hb, g, i, folded, done, &uses, &used);
 		} else if ((n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) ||
 			   (n->op == SAM3_OP_CONV_TRANSPOSE2D && s3h_conv_transpose2d_ok(n))) {
 			err = run_conv(hb, g, i, &uses, &used);

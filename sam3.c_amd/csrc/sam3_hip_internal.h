@@ -83,12 +83,13 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 /* The same GEMM (f32 result) written directly as the operand form out_fmt
  * (S3H_A_PLANES / S3H_A_F16) of the GEMM that reads it next, or as f32
  * (S3H_A_PLAIN), with res (f32 [M, N], or NULL) added last, when
- * s3h_matmul_out_ok says its kernel can. */
+ * s3h_matmul_out_ok says its kernel can. row_map (f32 only; NULL or
+ * {g, d1, d2}) stores C row m permuted as the s3k_gemm row map says. */
 int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags, int out_fmt);
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
-				  const void *res, int flags, void *stream);
+				  const void *res, const int *row_map, int flags, void *stream);
 
 /* Prepared copies of constant weights (bf16 hi/lo planes, padded rows),
  * kept by the backend whose graph_eval is running on this thread. A copy

@@ -616,7 +616,7 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
  * of the f32 output would give. */
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
-				  const void *res, int flags, void *stream)
+				  const void *res, const int *row_map, int flags, void *stream)
 {
 	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) || (res && ((uintptr_t)res & 3u)) ||
 	    !s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt)) {
@@ -632,6 +632,16 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 	if (res) {
 		g.res = res;
 		g.flags |= S3K_EPI_RES;
+	}
+	if (row_map) {
+		if (out_fmt != S3H_A_PLAIN || row_map[0] <= 0 || row_map[1] <= 0 || row_map[2] <= 0 ||
+		    M % ((long long)row_map[0] * row_map[1] * row_map[2])) {
+			s3h_error("matmul: bad output row map");
+			return SAM3_EINVAL;
+		}
+		g.rm_g = row_map[0];
+		g.rm_d1 = row_map[1];
+		g.rm_d2 = row_map[2];
 	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);

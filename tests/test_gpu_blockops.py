@@ -507,6 +507,56 @@ def test_residual_add_folded_into_gemm(monkeypatch, wkind):
     assert_f32_close(fused, (x + ln @ wd.T + bias).astype(np.float32), what=f"x + linear {wkind}")
 
 
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_unpartition_and_residual_folded_into_gemm(monkeypatch, wkind):
+    """The windowed block's output projection: linear on window rows ->
+    gh_window_unpartition (RESHAPE -> TRANSPOSE (0,2,1,3) -> RESHAPE) ->
+    x + that. The epilogue stores each C row at its unpartitioned row and
+    adds x there, so the three nodes and the ADD run inside the GEMM; same
+    bits as the node-by-node run, and equal to the oracle's reference."""
+    grid, ws, E = 24, 8, 256
+    nw = grid // ws
+    M = grid * grid
+    O = oracle()
+    a = synth.randn(880, (M, E))
+    x = synth.randn(881, (M, E))
+    gam, bet = synth.randn(884, (E,)), synth.randn(885, (E,), 0.1)
+    w, bias = synth.randn(882, (E, E), 0.04), synth.randn(883, (E,), 0.02)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_UNPARTITION_FOLD", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_UNPARTITION_FOLD", env)
+        G = graph.Graph()
+        tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, w.shape, w))
+        t = G.layernorm(G.tensor(abi.F32, (M, E), a), G.tensor(abi.F32, (E,), gam),
+                        G.tensor(abi.F32, (E,), bet))
+        aw = G.linear(t, tw, G.tensor(abi.F32, (E,), bias))
+        un = G.window_unpartition(G.reshape(aw, [nw * nw, ws * ws, E]), ws, grid)
+        y = G.add(G.tensor(abi.F32, (M, E), x), un)
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(M, E)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st.downloads == 1
+    assert st.gpu_nodes == 2 and st0.gpu_nodes == 4  # LN + GEMM, or LN, GEMM, permute, ADD
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    wd = (O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8"
+          else w).astype(np.float64)
+    ln = O.layernorm(a, gam, bet, "f32", threads=8).astype(np.float64)
+    lin = ln @ wd.T + bias
+    un_ref = lin.reshape(nw, nw, ws, ws * E).transpose(0, 2, 1, 3).reshape(M, E)
+    assert_f32_close(fused, (x + un_ref).astype(np.float32), what=f"unpartition fold {wkind}")
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
