@@ -54,9 +54,28 @@ __device__ __forceinline__ float bo_wave_sum(float v)
 /* One wave per row; element j of the row is held by lane j % 64 in slot
  * j / 64 (EPL slots cover cols <= 64 * EPL). EPL = 0: rows of any length,
  * re-read from memory in each pass. */
+/* Output row map of a LayerNorm (g 0: identity): row m is stored at
+ * ((a*d2 + c)*d1 + b)*g + m % g, m / g = (a*d1 + b)*d2 + c, i.e. the
+ * permute (0,2,1,3) of [., d1, d2, g*cols] applied to the output (the
+ * ViT window partition written by the LN that precedes it). */
+struct LnMap {
+	int g, d1, d2;
+};
+
+__device__ __forceinline__ long long ln_out_row(const LnMap &rm, long long m)
+{
+	if (!rm.g)
+		return m;
+	const long long gi = m / rm.g, w = m - gi * rm.g;
+	const long long c = gi % rm.d2, t = gi / rm.d2;
+	const long long b = t % rm.d1, a = t / rm.d1;
+	return ((a * rm.d2 + c) * rm.d1 + b) * rm.g + w;
+}
+
 template <int DT, int EPL, int OUTF>
 __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *gamma,
-						   const void *beta, void *out, int rows, int cols)
+						   const void *beta, void *out, int rows, int cols,
+						   LnMap rm)
 {
 	static_assert(OUTF == S3K_LN_SAME || DT == S3K_F32, "operand formats are made from f32");
 	const int lane = threadIdx.x & 63;
@@ -64,6 +83,7 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 	if (row >= rows)
 		return;
 	const long long base = row * cols;
+	const long long orow = ln_out_row(rm, row), obase = orow * cols;
 	constexpr int N = EPL > 0 ? EPL : 1;
 	float v[N];
 	float sum = 0.0f;
@@ -101,16 +121,16 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 		if (beta)
 			val = add_rn(val, bo_ld<DT>(beta, j));
 		if constexpr (OUTF == S3K_LN_SAME) {
-			bo_st<DT>(out, base + j, val);
+			bo_st<DT>(out, obase + j, val);
 		} else if constexpr (OUTF == S3K_LN_PLANES) {
 			uint32_t hi, lo;
 			split_bf16x2(val, 0.0f, hi, lo);
-			uint16_t *d = (uint16_t *)out + row * 3LL * cols + j;
+			uint16_t *d = (uint16_t *)out + orow * 3LL * cols + j;
 			d[0] = (uint16_t)hi;
 			d[cols] = (uint16_t)lo;
 			d[2LL * cols] = (uint16_t)hi;
 		} else {
-			((uint16_t *)out)[base + j] = (uint16_t)f32_to_f16(val);
+			((uint16_t *)out)[obase + j] = (uint16_t)f32_to_f16(val);
 		}
 	};
 	if constexpr (EPL > 0) {
@@ -164,7 +184,8 @@ __device__ __forceinline__ void bo_st16(void *p, long long i, const float *v)
  * slot s; the sums are taken in the same per-lane-then-wave order. */
 template <int DT, int SLOTS, int OUTF>
 __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *gamma,
-						   const void *beta, void *out, int rows, int cols)
+						   const void *beta, void *out, int rows, int cols,
+						   LnMap rm)
 {
 	static_assert(OUTF == S3K_LN_SAME || DT == S3K_F32, "operand formats are made from f32");
 	constexpr int VEC = DT == S3K_F32 ? 4 : 8;
@@ -173,6 +194,7 @@ __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *ga
 	if (row >= rows)
 		return;
 	const long long base = row * cols;
+	const long long orow = ln_out_row(rm, row), obase = orow * cols;
 	float v[SLOTS][VEC];
 	float sum = 0.0f;
 #pragma unroll
@@ -210,17 +232,17 @@ __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *ga
 			v[i][e] = val;
 		}
 		if constexpr (OUTF == S3K_LN_SAME) {
-			bo_st16<DT>(out, base + j0, v[i]);
+			bo_st16<DT>(out, obase + j0, v[i]);
 		} else if constexpr (OUTF == S3K_LN_PLANES) {
 			uint32_t hi[2], lo[2];
 			split_bf16x2(v[i][0], v[i][1], hi[0], lo[0]);
 			split_bf16x2(v[i][2], v[i][3], hi[1], lo[1]);
-			uint16_t *d = (uint16_t *)out + row * 3LL * cols + j0;
+			uint16_t *d = (uint16_t *)out + orow * 3LL * cols + j0;
 			*(uint2 *)d = make_uint2(hi[0], hi[1]);
 			*(uint2 *)(d + cols) = make_uint2(lo[0], lo[1]);
 			*(uint2 *)(d + 2LL * cols) = make_uint2(hi[0], hi[1]);
 		} else {
-			*(uint2 *)((uint16_t *)out + base + j0) =
+			*(uint2 *)((uint16_t *)out + obase + j0) =
 				make_uint2(pack_f16x2(v[i][0], v[i][1]), pack_f16x2(v[i][2], v[i][3]));
 		}
 	}
@@ -355,7 +377,7 @@ static void launch_perm(const PermArgs &a, dim3 grid, hipStream_t st)
 
 template <int DT, int OUTF>
 static void launch_ln(const void *x, const void *g, const void *b, void *o, int rows, int cols,
-		      hipStream_t st)
+		      hipStream_t st, LnMap rm = LnMap{0, 0, 0})
 {
 	const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 	constexpr int VEC = DT == S3K_F32 ? 4 : 8;
@@ -363,25 +385,25 @@ static void launch_ln(const void *x, const void *g, const void *b, void *o, int 
 			 !(((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)o) & 15u);
 	if (vec) {
 		switch (cols / (64 * VEC)) {
-		case 1: hipLaunchKernelGGL((layernorm_v<DT, 1, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
-		case 2: hipLaunchKernelGGL((layernorm_v<DT, 2, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
-		case 3: hipLaunchKernelGGL((layernorm_v<DT, 3, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
-		case 4: hipLaunchKernelGGL((layernorm_v<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
-		case 6: hipLaunchKernelGGL((layernorm_v<DT, 6, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
-		case 8: hipLaunchKernelGGL((layernorm_v<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols); return;
+		case 1: hipLaunchKernelGGL((layernorm_v<DT, 1, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
+		case 2: hipLaunchKernelGGL((layernorm_v<DT, 2, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
+		case 3: hipLaunchKernelGGL((layernorm_v<DT, 3, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
+		case 4: hipLaunchKernelGGL((layernorm_v<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
+		case 6: hipLaunchKernelGGL((layernorm_v<DT, 6, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
+		case 8: hipLaunchKernelGGL((layernorm_v<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm); return;
 		default: break;
 		}
 	}
 	if (cols <= 256)
-		hipLaunchKernelGGL((layernorm_k<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 4, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm);
 	else if (cols <= 512)
-		hipLaunchKernelGGL((layernorm_k<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 8, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm);
 	else if (cols <= 1024)
-		hipLaunchKernelGGL((layernorm_k<DT, 16, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 16, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm);
 	else if (cols <= 2048)
-		hipLaunchKernelGGL((layernorm_k<DT, 32, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 32, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm);
 	else
-		hipLaunchKernelGGL((layernorm_k<DT, 0, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols);
+		hipLaunchKernelGGL((layernorm_k<DT, 0, OUTF>), grid, block, 0, st, x, g, b, o, rows, cols, rm);
 }
 
 } /* namespace s3k */
@@ -407,21 +429,31 @@ extern "C" int s3k_layernorm(int kind, const void *x, const void *gamma, const v
 	return (int)hipGetLastError();
 }
 
-extern "C" int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta,
-				void *out, long long rows, int cols, void *stream)
+extern "C" int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma,
+				    const float *beta, void *out, long long rows, int cols, int rm_g,
+				    int rm_d1, int rm_d2, void *stream)
 {
 	if (rows < 0 || cols <= 0 || rows > 0x7FFFFFFFLL || (fmt == S3K_LN_PLANES && cols % 8))
+		return (int)hipErrorInvalidValue;
+	if (rm_g && (rm_g < 0 || rm_d1 <= 0 || rm_d2 <= 0 || rows % ((long long)rm_g * rm_d1 * rm_d2)))
 		return (int)hipErrorInvalidValue;
 	if (rows == 0)
 		return (int)hipSuccess;
 	const hipStream_t st = (hipStream_t)stream;
+	const LnMap rm{rm_g, rm_d1, rm_d2};
 	if (fmt == S3K_LN_PLANES)
-		launch_ln<S3K_F32, S3K_LN_PLANES>(x, gamma, beta, out, (int)rows, cols, st);
+		launch_ln<S3K_F32, S3K_LN_PLANES>(x, gamma, beta, out, (int)rows, cols, st, rm);
 	else if (fmt == S3K_LN_F16)
-		launch_ln<S3K_F32, S3K_LN_F16>(x, gamma, beta, out, (int)rows, cols, st);
+		launch_ln<S3K_F32, S3K_LN_F16>(x, gamma, beta, out, (int)rows, cols, st, rm);
 	else
 		return (int)hipErrorInvalidValue;
 	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta,
+				void *out, long long rows, int cols, void *stream)
+{
+	return s3k_layernorm_to_map(fmt, x, gamma, beta, out, rows, cols, 0, 0, 0, stream);
 }
 
 extern "C" int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t,

@@ -119,6 +119,11 @@ int s3k_layernorm(int kind, const void *x, const void *gamma, const void *beta, 
 enum { S3K_LN_SAME = 0, S3K_LN_PLANES = 1, S3K_LN_F16 = 2 };
 int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta, void *out,
 		     long long rows, int cols, void *stream);
+/* The same with output row m stored at the row map (rm_g, rm_d1, rm_d2)
+ * of struct s3k_gemm (rm_g 0: identity): the ViT window partition. */
+int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma, const float *beta,
+			 void *out, long long rows, int cols, int rm_g, int rm_d1, int rm_d2,
+			 void *stream);
 int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, void *out,
 	     int batch, int seq, int heads, int hd, void *stream);
 int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,

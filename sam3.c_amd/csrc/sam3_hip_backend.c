@@ -869,6 +869,84 @@ static enum sam3_error run_permute_as(struct sam3_hip_backend *hb, const struct 
 	return err;
 }
 
+/* An f32 LAYERNORM followed by gh_window_partition (graph_helpers.c:
+ * 447-478: RESHAPE -> TRANSPOSE (0,2,1,3) of [d0, d1, d2, g*cols] ->
+ * RESHAPE ...) whose result only a GEMM reads, as its A: the LN writes
+ * that GEMM's operand with its rows already in partition order (a store
+ * row map), under the GEMM's A tensor. Returns the form; rm, the chain's
+ * node indices and that tensor are filled in. */
+static int ln_partition_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			     struct use_map *uses, int rm[3], int *chain, int *n_chain,
+			     const struct sam3_tensor **a_out)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (n->inputs[0]->dtype != SAM3_DTYPE_F32 || !s3h_layernorm_ok(n))
+		return S3H_A_PLAIN;
+	const int cols = n->inputs[0]->dims[n->inputs[0]->n_dims - 1];
+	const long long tot = s3h_nelems(n->inputs[0]);
+	const struct sam3_tensor *t = n->output;
+	int k = i, nc = 0, ok = 0;
+	for (;;) {
+		if (uses_of(uses, t) != 1 || nc >= 8 || (k = next_reader(g, k + 1, t)) < 0)
+			break;
+		const struct sam3_node *m = &g->nodes[k];
+		if (m->inputs[0] != t || !m->output)
+			break;
+		if (m->op == SAM3_OP_RESHAPE && s3h_nelems(m->output) == tot) {
+			chain[nc++] = k;
+			t = m->output;
+		} else if (!ok && m->op == SAM3_OP_TRANSPOSE && t->n_dims == 4 && m->params[0] == 0 &&
+			   m->params[1] == 2 && m->params[2] == 1 && m->params[3] == 3 &&
+			   m->output->dtype == SAM3_DTYPE_F32 && t->dims[3] % cols == 0 &&
+			   s3h_nelems(t) == tot) {
+			rm[0] = t->dims[3] / cols;
+			rm[1] = t->dims[1];
+			rm[2] = t->dims[2];
+			chain[nc++] = k;
+			t = m->output;
+			ok = 1;
+		} else {
+			break;
+		}
+	}
+	if (!ok || !t->data)
+		return S3H_A_PLAIN;
+	const int fmt = consumer_operand_form(hb, g, i, chain[nc - 1] + 1, t, cols, uses, NULL);
+	if (fmt == S3H_A_PLAIN)
+		return S3H_A_PLAIN;
+	*n_chain = nc;
+	*a_out = t;
+	return fmt;
+}
+
+/* LAYERNORM written as that operand, rows in partition order, under t. */
+static enum sam3_error run_layernorm_map(struct sam3_hip_backend *hb, const struct sam3_node *n,
+					 int fmt, const int rm[3], const struct sam3_tensor *t)
+{
+	const struct sam3_tensor *x = n->inputs[0];
+	const int cols = x->dims[x->n_dims - 1];
+	const long long rows = s3h_nelems(x) / cols;
+	void *dx = NULL, *dg = NULL, *db = NULL, *dy = NULL;
+	enum sam3_error err = dev_in(hb, x, &dx);
+	if (err == SAM3_OK && n->n_inputs > 1 && n->inputs[1])
+		err = dev_in(hb, n->inputs[1], &dg);
+	if (err == SAM3_OK && n->n_inputs > 2 && n->inputs[2])
+		err = dev_in(hb, n->inputs[2], &db);
+	if (err == SAM3_OK)
+		err = dev_out_fmt(hb, t, (size_t)rows * cols * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_layernorm_to_map(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
+						   (const float *)dx, (const float *)dg,
+						   (const float *)db, dy, rows, cols, rm[0], rm[1], rm[2],
+						   hb->stream),
+			      "layernorm (GEMM operand, partition order)");
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.operand_writes++;
+	}
+	return err;
+}
+
 /* LAYERNORM written as the operand form fmt of its one consuming GEMM. */
 static enum sam3_error run_layernorm_as(struct sam3_hip_backend *hb, const struct sam3_node *n,
 					int fmt)
@@ -1108,6 +1186,10 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	const char *perm_env = getenv("SAM3_HIP_PERMUTE_OPERAND");
 	const int perm_plain = perm_env && atoi(perm_env) == 0;
 	int ln_fmt = S3H_A_PLAIN, perm_k = 0;
+	const char *part_env = getenv("SAM3_HIP_PARTITION_FOLD");
+	const int part_plain = part_env && atoi(part_env) == 0;
+	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
+	const struct sam3_tensor *lt = NULL;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -1131,6 +1213,15 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		} else if ((n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) ||
 			   (n->op == SAM3_OP_CONV_TRANSPOSE2D && s3h_conv_transpose2d_ok(n))) {
 			err = run_conv(hb, g, i, &uses, &used);
+		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain && !part_plain &&
+			   (ln_fmt = ln_partition_form(hb, g, i, &uses, lrm, lchain, &lnc, &lt)) !=
+				   S3H_A_PLAIN) {
+			err = run_layernorm_map(hb, n, ln_fmt, lrm, lt);
+			if (err == SAM3_OK) {
+				for (int k = 0; k < lnc; k++)
+					done[lchain[k]] = 1;
+				hb->stats.fused_nodes += lnc;
+			}
 		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain &&
 			   (ln_fmt = ln_operand_form(hb, g, i, &uses)) != S3H_A_PLAIN) {
 			err = run_layernorm_as(hb, n, ln_fmt);

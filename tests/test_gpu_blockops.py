@@ -557,6 +557,53 @@ def test_unpartition_and_residual_folded_into_gemm(monkeypatch, wkind):
     assert_f32_close(fused, (x + un_ref).astype(np.float32), what=f"unpartition fold {wkind}")
 
 
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_partition_folded_into_layernorm(monkeypatch, wkind):
+    """The windowed block's LN1 -> gh_window_partition -> qkv linear: the
+    LayerNorm writes the GEMM's operand (bf16 planes / f16) with its rows
+    already in window order, so the partition permute does not run; same
+    bits as the node-by-node run, and equal to the oracle's LN ->
+    partition -> linear."""
+    grid, ws, E, N = 24, 8, 256, 768
+    nw = grid // ws
+    M = grid * grid
+    O = oracle()
+    x = synth.randn(890, (M, E), 2.0, 0.5)
+    gam, bet = synth.randn(891, (E,)), synth.randn(892, (E,), 0.1)
+    w, bias = synth.randn(893, (N, E), 0.04), synth.randn(894, (N,), 0.02)
+
+    def run(env):
+        if env is None:
+            monkeypatch.delenv("SAM3_HIP_PARTITION_FOLD", raising=False)
+        else:
+            monkeypatch.setenv("SAM3_HIP_PARTITION_FOLD", env)
+        G = graph.Graph()
+        t = G.layernorm(G.tensor(abi.F32, (M, E), x), G.tensor(abi.F32, (E,), gam),
+                        G.tensor(abi.F32, (E,), bet))
+        xw = G.window_partition(t, ws, grid)
+        tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, w.shape, w))
+        y = G.linear(G.reshape(xw, [M, E]), tw, G.tensor(abi.F32, (N,), bias))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(M, N)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st.downloads == 1
+    assert st.gpu_nodes == 2 and st0.gpu_nodes == 3  # LN + GEMM, or LN, permute, GEMM
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    ln = O.layernorm(x, gam, bet, "f32", threads=8).astype(np.float64)
+    part = ln.reshape(nw, ws, nw, ws * E).transpose(0, 2, 1, 3).reshape(M, E)
+    wd = (O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8"
+          else w).astype(np.float64)
+    assert_f32_close(fused, (part @ wd.T + bias).astype(np.float32), what=f"LN -> partition {wkind}")
+
+
 def test_blocks_chained_across_evals():
     """The image encoder's block loop (image_encoder.c:736-915): blocks in
     separate graph_evals, each graph's output the next graph's input. With
