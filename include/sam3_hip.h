@@ -392,6 +392,11 @@ enum sam3_error sam3_hip_event_elapsed_ms(float *ms, void *start, void *stop);
 const char *sam3_hip_device_arch(int device);
 /* Message of the last failure on this thread ("" if none). */
 const char *sam3_hip_last_error(void);
+/* Re-read the SAM3_HIP_* environment switches (tile overrides, graph_eval
+ * fold switches). They are parsed once, at first use; call this after
+ * changing the environment, while no other thread launches work. No
+ * reference counterpart (the reference has no such switches). */
+enum sam3_error sam3_hip_reload_settings(void);
 
 #ifdef __cplusplus
 }

@@ -739,9 +739,9 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 	/* waves per workgroup: 4 (128 queries); 6 and 8 for measurements */
 	int nw = 4;
 	if (kind != S3K_F32) {
-		const char *env = getenv("SAM3_HIP_ATTN_NW");
-		if (env && (atoi(env) == 4 || atoi(env) == 6 || atoi(env) == 8))
-			nw = atoi(env);
+		const int env = s3h_settings()->attn_nw;
+		if (env == 4 || env == 6 || env == 8)
+			nw = env;
 	}
 	p.BH = BH;
 	p.nqb = (Sq + 32 * nw - 1) / (32 * nw);

@@ -393,8 +393,7 @@ extern "C" int s3k_conv_implicit(const struct s3k_conv *c, const void *xa, const
 	q.stride = c->stride; q.ph = c->pad_h; q.pw = c->pad_w; q.OH = c->OH; q.OW = c->OW;
 	q.PP = pixel_pitch;
 	hipStream_t st = (hipStream_t)stream;
-	const char *e = getenv("SAM3_HIP_CONV_CFG");
-	int cfg = e ? atoi(e) : -1;
+	int cfg = s3h_settings()->conv_cfg;
 	/* Tiles (measured on the neck shapes): 64x64 when 128x128 tiles would
 	 * not cover the 256 CUs (72x72 maps: 5184 x 256), else the GEMM's
 	 * rule (256x256 for one nearly full round, 192x128 from 192 tiles). */

@@ -268,8 +268,7 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		return (int)hipErrorInvalidValue;
 	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
 	p.b_extent = (unsigned)((long long)g->N * g->ldb * 2);
-	const char *e = getenv("SAM3_HIP_DL_CFG");
-	int cfg = e ? atoi(e) : -1;
+	int cfg = s3h_settings()->dl_cfg;
 	if (cfg < 0) {
 		const long long t9 = dl_tiles(g, 256, 256), t10 = dl_tiles(g, 192, 128);
 		if (t9 >= 224 && t9 <= 256)

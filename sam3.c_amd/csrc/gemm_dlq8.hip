@@ -253,8 +253,7 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		return (int)hipErrorInvalidValue;
 	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
 	p.b_extent = (unsigned)((long long)g->N * (g->K / 32) * 36);
-	const char *e = getenv("SAM3_HIP_DLQ8_CFG");
-	int cfg = e ? atoi(e) : -1;
+	int cfg = s3h_settings()->dlq8_cfg;
 	if (cfg < 0)
 		cfg = g->M <= 32 ? 7 : g->M <= 64 ? 8 : g->M <= 96 ? 9 : 2;
 	switch (cfg) {
@@ -283,8 +282,7 @@ extern "C" int s3k_dlq8_eligible(const struct s3k_gemm *g)
 	 * ViT-L shapes (5184 x {3072, 1024, 4096} x {1024, 4096}: 67 / 37 /
 	 * 90 / 95 us against 102 / 39 / 143 / 120 us). SAM3_HIP_Q8_F32CAST=0
 	 * keeps f32 activations on the register-staged kernel. */
-	const char *env = getenv("SAM3_HIP_Q8_F32CAST");
-	const bool f32_cast = !env || atoi(env) != 0;
+	const bool f32_cast = s3h_settings()->q8_f32cast != 0;
 	if (g->a_kind != S3K_F16 && g->a_kind != S3K_BF16 && !(g->a_kind == S3K_F32 && f32_cast))
 		return 0;
 	struct s3k_gemm h = *g;

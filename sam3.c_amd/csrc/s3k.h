@@ -190,6 +190,28 @@ int s3k_repeat_f32(const float *b, float *out, int n, int times, void *stream);
 int s3k_transpose2d(int esize, const void *src, void *dst, int batch, int rows,
 		    int cols, void *stream);
 
+/*
+ * The library's environment switches, parsed once (settings.c) and
+ * re-read only by sam3_hip_reload_settings(). Tile overrides (-1 / 0 =
+ * automatic choice) exist for measurements and tests; the fold switches
+ * (1 = on) each turn one graph_eval fusion off when set to 0.
+ */
+struct s3h_settings {
+	int dl_cfg, dlq8_cfg, conv_cfg;   /* SAM3_HIP_{DL,DLQ8,CONV}_CFG        */
+	int attn_nw;                      /* SAM3_HIP_ATTN_NW: waves per SDPA wg */
+	int sk_mr, sk_nt;                 /* SAM3_HIP_SK_CFG "mr,nt"             */
+	int q8_expand;                    /* SAM3_HIP_Q8_EXPAND: -1 auto, 0, 1   */
+	int q8_f32cast;                   /* SAM3_HIP_Q8_F32CAST                 */
+	int q8_batch_path;                /* SAM3_HIP_Q8_BATCH_PATH: 0, 1, 2     */
+	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
+	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
+	    permute_operand, partition_fold;
+	int readback_all;                 /* SAM3_HIP_READBACK=all               */
+	int quiet;                        /* SAM3_HIP_QUIET set                  */
+	int arena_mb;                     /* SAM3_HIP_ARENA_MB (0 = default)     */
+};
+const struct s3h_settings *s3h_settings(void);
+
 #ifdef __cplusplus
 }
 #endif

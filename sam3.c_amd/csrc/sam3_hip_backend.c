@@ -55,7 +55,10 @@
 
 struct s3h_res {
 	const char *host;
-	size_t nbytes;
+	size_t nbytes;           /* host bytes of the tensor last bound here:
+				  * every host copy moves exactly this many */
+	size_t cap;              /* bytes of the device allocation (>= the
+				  * tensor, or its GEMM operand form)      */
 	void *dev;
 	unsigned char dev_valid;
 	unsigned char host_valid;
@@ -135,7 +138,7 @@ static void prep_drop_range(struct sam3_hip_backend *hb, const char *lo, const c
 static void res_drop_at(struct sam3_hip_backend *hb, int i)
 {
 	if (hb->res[i].dev)
-		prep_drop_range(hb, hb->res[i].dev, (const char *)hb->res[i].dev + hb->res[i].nbytes);
+		prep_drop_range(hb, hb->res[i].dev, (const char *)hb->res[i].dev + hb->res[i].cap);
 	if (hb->res[i].dev)
 		(void)s3h_scratch_free(hb->res[i].dev, hb->stream);
 	hb->res[i] = hb->res[hb->n_res - 1];
@@ -151,8 +154,9 @@ static void res_drop_range(struct sam3_hip_backend *hb, const char *lo, const ch
 	}
 }
 
+/* A new entry for host tensor t with a device allocation of dev_bytes. */
 static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
-			       size_t nbytes, struct s3h_res **out)
+			       size_t dev_bytes, struct s3h_res **out)
 {
 	if (hb->n_res == hb->cap_res) {
 		int cap = hb->cap_res ? hb->cap_res * 2 : 256;
@@ -167,8 +171,9 @@ static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_te
 	struct s3h_res *e = &hb->res[hb->n_res];
 	memset(e, 0, sizeof(*e));
 	e->host = t->data;
-	e->nbytes = nbytes;
-	enum sam3_error err = s3h_scratch_alloc(&e->dev, nbytes, hb->stream);
+	e->nbytes = s3h_tensor_bytes(t);
+	e->cap = dev_bytes;
+	enum sam3_error err = s3h_scratch_alloc(&e->dev, dev_bytes, hb->stream);
 	if (err != SAM3_OK)
 		return err;
 	e->host_valid = 1;
@@ -239,9 +244,18 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 		*out = e->dev;
 		return SAM3_OK;
 	}
-	if (e && e->nbytes < nbytes) {
+	/* The same host address may now hold a different tensor (sam3.c
+	 * recycles arena memory between graphs without cache_invalidate). A
+	 * tensor larger than the one last bound here is a new tensor: its
+	 * bytes come from the host, into the shadow if it is big enough. A
+	 * smaller one reads the shadow's prefix. */
+	if (e && e->cap < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
+	} else if (e && e->nbytes < nbytes) {
+		e->nbytes = nbytes;
+		e->dev_valid = 0;
+		e->host_valid = 1;
 	}
 	if (!e) {
 		enum sam3_error err = res_new(hb, t, nbytes, &e);
@@ -253,6 +267,7 @@ static enum sam3_error dev_in(struct sam3_hip_backend *hb, const struct sam3_ten
 	if (t->ephemeral && !e->produced && !e->fresh)
 		e->dev_valid = 0;
 	if (!e->dev_valid) {
+		e->nbytes = nbytes;
 		enum sam3_error err = s3h_hip(hipMemcpyAsync(e->dev, e->host, e->nbytes,
 							     hipMemcpyHostToDevice, hb->stream),
 					      "graph_eval: upload");
@@ -284,7 +299,7 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 		return SAM3_OK;
 	}
 	size_t nbytes = s3h_tensor_bytes(t);
-	if (e && e->nbytes < nbytes) {
+	if (e && e->cap < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
 	}
@@ -293,6 +308,7 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 		if (err != SAM3_OK)
 			return err;
 	}
+	e->nbytes = nbytes;
 	e->dev_valid = 1;
 	e->host_valid = 0;
 	e->produced = 1;
@@ -309,7 +325,7 @@ static enum sam3_error dev_out_fmt(struct sam3_hip_backend *hb, const struct sam
 				   size_t nbytes, int fmt, void **out)
 {
 	struct s3h_res *e = res_find(hb, t->data);
-	if (e && e->nbytes < nbytes) {
+	if (e && e->cap < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
 	}
@@ -318,6 +334,7 @@ static enum sam3_error dev_out_fmt(struct sam3_hip_backend *hb, const struct sam
 		if (err != SAM3_OK)
 			return err;
 	}
+	e->nbytes = s3h_tensor_bytes(t);
 	e->dev_valid = 1;
 	e->host_valid = 0;
 	e->produced = 1;
@@ -444,6 +461,18 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 				 struct use_map *uses, int *k_out);
 static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t);
 
+/* Whether a node in [lo, hi) writes tensor r (its header, or its data). */
+static int written_between(const struct sam3_graph *g, int lo, int hi,
+			   const struct sam3_tensor *r)
+{
+	for (int k = lo; k < hi; k++) {
+		const struct sam3_tensor *o = g->nodes[k].output;
+		if (o && (o == r || (o->data && o->data == r->data)))
+			return 1;
+	}
+	return 0;
+}
+
 /* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
  * Returns the number of nodes consumed in *used. */
 static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3_graph *g,
@@ -529,8 +558,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	 * residual ADD: a permutation of whole C rows, done by the epilogue's
 	 * row map (and the ADD with it); the chain's nodes are marked done */
 	int row_map[3] = {0, 0, 0}, chain[10], n_chain = 0;
-	const char *u_env = getenv("SAM3_HIP_UNPARTITION_FOLD");
-	if (c_dt == SAM3_DTYPE_F32 && !(u_env && atoi(u_env) == 0) &&
+	if (c_dt == SAM3_DTYPE_F32 && s3h_settings()->unpartition_fold &&
 	    s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, S3H_A_PLAIN)) {
 		const struct sam3_tensor *t = out;
 		int k = j - 1, ok = 0;
@@ -567,10 +595,12 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 			const struct sam3_tensor *r = NULL;
 			if (ad && ad->op == SAM3_OP_ADD && ad->n_inputs == 2 && ad->output && !done[ka])
 				r = ad->inputs[0] == t ? ad->inputs[1] : ad->inputs[1] == t ? ad->inputs[0] : NULL;
+			/* the epilogue reads r when the GEMM runs, so no node between
+			 * the GEMM and the ADD may write it */
 			if (r && r != t && r->data && r->dtype == SAM3_DTYPE_F32 &&
 			    ad->output->dtype == SAM3_DTYPE_F32 && s3h_nelems(r) == (long long)M * N &&
 			    s3h_nelems(ad->output) == (long long)M * N && r->data != ad->output->data &&
-			    dev_in(hb, r, &dres) == SAM3_OK) {
+			    !written_between(g, i + 1, ka, r) && dev_in(hb, r, &dres) == SAM3_OK) {
 				chain[n_chain++] = ka;
 				out = ad->output;
 				fold = 1;
@@ -585,8 +615,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	}
 	/* a residual ADD of an f32 [M, N] tensor computed earlier (the
 	 * block's x + attention / + MLP), folded last into the epilogue */
-	const char *r_env = getenv("SAM3_HIP_RESIDUAL_FOLD");
-	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && !(r_env && atoi(r_env) == 0) && j < g->n_nodes &&
+	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && s3h_settings()->residual_fold && j < g->n_nodes &&
 	    g->nodes[j].op == SAM3_OP_ADD && g->nodes[j].n_inputs == 2 && g->nodes[j].output &&
 	    uses_of(uses, out) == 1 &&
 	    s3h_nelems(g->nodes[j].output) == (long long)M * N) {
@@ -607,8 +636,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	/* an f32 result read only by the next GEMM, which converts its A
 	 * first: written in that form by this GEMM's epilogue */
 	int o_fmt = S3H_A_PLAIN;
-	const char *o_env = getenv("SAM3_HIP_GEMM_OPERAND");
-	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && !(o_env && atoi(o_env) == 0)) {
+	if (!row_map[0] && c_dt == SAM3_DTYPE_F32 && s3h_settings()->gemm_operand) {
 		o_fmt = consumer_operand_form(hb, g, i, j, out, N, uses, NULL);
 		if (o_fmt != S3H_A_PLAIN &&
 		    !s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, o_fmt))
@@ -1168,8 +1196,8 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		return err;
 	unsigned char *folded = calloc((size_t)g->n_nodes, 1);
 	unsigned char *done = calloc((size_t)g->n_nodes, 1);
-	const char *qkv_env = getenv("SAM3_HIP_QKV_CHAIN");
-	const int qkv_plain = qkv_env && atoi(qkv_env) == 0;
+	const struct s3h_settings *set = s3h_settings();
+	const int qkv_plain = !set->qkv_chain;
 	if (!folded || !done) {
 		free(folded);
 		free(done);
@@ -1181,13 +1209,10 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	for (int i = 0; i < hb->n_res; i++)
 		hb->res[i].produced = hb->res[i].fresh = 0;
 	s3h_cur = hb;
-	const char *ln_env = getenv("SAM3_HIP_LN_OPERAND");
-	const int ln_plain = ln_env && atoi(ln_env) == 0;
-	const char *perm_env = getenv("SAM3_HIP_PERMUTE_OPERAND");
-	const int perm_plain = perm_env && atoi(perm_env) == 0;
+	const int ln_plain = !set->ln_operand;
+	const int perm_plain = !set->permute_operand;
 	int ln_fmt = S3H_A_PLAIN, perm_k = 0;
-	const char *part_env = getenv("SAM3_HIP_PARTITION_FOLD");
-	const int part_plain = part_env && atoi(part_env) == 0;
+	const int part_plain = !set->partition_fold;
 	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
 	const struct sam3_tensor *lt = NULL;
 
@@ -1243,8 +1268,7 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	 * (metal_backend.c:1805-1850, 1897-1945). Intermediates stay on the
 	 * device. SAM3_HIP_READBACK=all downloads every produced tensor. */
 	if (err == SAM3_OK && !g->no_readback) {
-		const char *rb = getenv("SAM3_HIP_READBACK");
-		if (rb && strcmp(rb, "all") == 0) {
+		if (s3h_settings()->readback_all) {
 			for (int i = 0; i < hb->n_res && err == SAM3_OK; i++) {
 				struct s3h_res *e = &hb->res[i];
 				if (e->produced && e->dev_valid && !e->host_valid && !e->fmt)
@@ -1379,8 +1403,8 @@ static enum sam3_error hip_alloc_tensor(struct sam3_backend *be, struct sam3_ten
 		return SAM3_EINVAL;
 	}
 	if (!hb->arena) {
-		const char *env = getenv("SAM3_HIP_ARENA_MB");
-		size_t sz = env ? (size_t)strtoull(env, NULL, 10) << 20 : S3H_ARENA_DEFAULT;
+		const int mb = s3h_settings()->arena_mb;
+		size_t sz = mb > 0 ? (size_t)mb << 20 : S3H_ARENA_DEFAULT;
 		if (!sz)
 			sz = S3H_ARENA_DEFAULT;
 		enum sam3_error err = s3h_hip(hipHostMalloc((void **)&hb->arena, sz,
@@ -1698,7 +1722,7 @@ int s3h_prep_cacheable(const void *src, size_t src_bytes)
 	for (int i = 0; i < hb->n_res; i++) {
 		const struct s3h_res *e = &hb->res[i];
 		const char *d = (const char *)e->dev;
-		if (d && c >= d && c < d + e->nbytes && src_bytes <= e->nbytes - (size_t)(c - d))
+		if (d && c >= d && c < d + e->cap && src_bytes <= e->cap - (size_t)(c - d))
 			return e->keep && !e->written && e->dev_valid;
 	}
 	/* a prepared copy is itself constant */

@@ -34,7 +34,7 @@ void s3h_error(const char *fmt, ...)
 	va_start(ap, fmt);
 	vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
 	va_end(ap);
-	if (!getenv("SAM3_HIP_QUIET"))
+	if (!s3h_settings()->quiet)
 		fprintf(stderr, "[sam3_hip] %s\n", g_last_error);
 }
 
@@ -349,8 +349,7 @@ static int prep_q8_f16(const void *w, void *out, int rows, int k, int k_out, int
  * always keeps the direct kernel, =1 always expands. */
 static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 {
-	const char *env = getenv("SAM3_HIP_Q8_EXPAND");
-	const int mode = env ? atoi(env) : -1;
+	const int mode = s3h_settings()->q8_expand;
 	const size_t q8_bytes = (size_t)h->N * (h->K / 32) * 36;
 	const int layout_ok = (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1;
 	if (layout_ok && mode != 0 && (mode == 1 || s3h_prep_cacheable(h->b, q8_bytes))) {
@@ -412,8 +411,7 @@ static int q8_dl_wants_cast(const struct s3k_gemm *g)
  * each product. */
 static int f32_split_wanted(const struct s3k_gemm *g)
 {
-	const char *env = getenv("SAM3_HIP_F32_SPLIT");
-	if (env && atoi(env) == 0)
+	if (!s3h_settings()->f32_split)
 		return 0;
 	return g->a_kind == S3K_F32 && g->b_kind == S3K_F32 && g->c_kind == S3K_F32 &&
 	       (g->flags & S3K_B_NT) && g->batch == 1 && g->K % 8 == 0 && g->lda % 4 == 0 &&
@@ -600,8 +598,7 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 	if (b_dt != SAM3_DTYPE_Q8_0 || a_fmt != S3H_A_F16 || a_dt != SAM3_DTYPE_F32)
 		return 0;
 	/* the expansion q8_f16_gemm makes */
-	const char *env = getenv("SAM3_HIP_Q8_EXPAND");
-	const int mode = env ? atoi(env) : -1;
+	const int mode = s3h_settings()->q8_expand;
 	if (!(g.flags & S3K_B_NT) || K % 32 || mode == 0 ||
 	    (mode != 1 && !s3h_prep_cacheable(b, (size_t)N * (K / 32) * 36)))
 		return 0;
@@ -767,8 +764,7 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 			h.a_kind = S3K_F16;
 		}
 		if (err == SAM3_OK) {
-			const char *pe = getenv("SAM3_HIP_Q8_BATCH_PATH");
-			const int force = pe ? atoi(pe) : 0;
+			const int force = s3h_settings()->q8_batch_path;
 			const int gemm = h.a_kind == S3K_F16 && batch > 1 &&
 					 (force == 2 ||
 					  (force != 1 && (M >= S3H_Q8_BATCH_GEMM_M || K <= 256))) &&
@@ -1337,8 +1333,7 @@ static enum sam3_error conv_shape(const struct sam3_node *node, struct s3k_conv 
 
 static int conv_f32_split_allowed(void)
 {
-	const char *env = getenv("SAM3_HIP_F32_SPLIT");
-	return !(env && atoi(env) == 0);
+	return s3h_settings()->f32_split;
 }
 
 /* Whether the implicit GEMM (1) or the column matrix + GEMM (2) can run

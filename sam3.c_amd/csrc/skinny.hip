@@ -593,10 +593,9 @@ static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *strea
  */
 static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
 {
-	const char *e = getenv("SAM3_HIP_SK_CFG");
-	if (e) {
-		int mr = 0, nt = 0;
-		if (sscanf(e, "%d,%d", &mr, &nt) == 2 && (nt == 1 || nt == 2 || nt == 4) &&
+	{
+		const int mr = s3h_settings()->sk_mr, nt = s3h_settings()->sk_nt;
+		if ((nt == 1 || nt == 2 || nt == 4) &&
 		    (mr == 1 || mr == 4 || mr == 8 || mr == 16 || mr == 32)) {
 			*mr_out = mr;
 			*nt_out = nt;

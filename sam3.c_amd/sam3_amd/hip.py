@@ -76,6 +76,7 @@ SIGNATURES = {
     "sam3_hip_event_elapsed_ms": (_i, [_P(C.c_float), _vp, _vp]),
     "sam3_hip_device_arch": (C.c_char_p, [_i]),
     "sam3_hip_last_error": (C.c_char_p, []),
+    "sam3_hip_reload_settings": (C.c_int, []),
 }
 
 # kernel paths (sam3_hip_matmul_path)

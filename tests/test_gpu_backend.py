@@ -8,7 +8,8 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from gpu_util import assert_bf16_close, assert_f32_close, oracle, ref_q8, require_gpu
+from gpu_util import (assert_bf16_close, assert_f32_close, oracle, ref_linear, ref_q8,
+                      require_gpu)
 from sam3_amd import abi, hip, synth
 
 pytestmark = pytest.mark.gpu
@@ -208,3 +209,79 @@ def test_alloc_tensor_pinned_arena(be):
     q.dtype, q.n_dims, q.dims[0] = abi.Q8_0, 1, 64
     assert be.alloc_tensor(q) == abi.EINVAL  # no element size (cpu_backend.c:97-101)
     be.arena_reset()
+
+
+def _view(big, nbytes, dtype):
+    """A host tensor buffer at the start of `big` (same address every time)."""
+    return big[:nbytes].view(dtype)
+
+
+def test_reused_host_address_copies_only_the_tensor_bytes(be):
+    """sam3.c recycles arena memory between graphs without cache_invalidate
+    (image_encoder.c:737-738). Eval 1 leaves at host address B a residency
+    entry for fc1's output, written as fc2's bf16-planes operand (6 bytes per
+    element on the device for a 4-byte-per-element host tensor). Eval 2's final
+    output is a smaller f32 tensor at the same B: its readback must write
+    exactly its own bytes, and the next eval's ephemeral input at B must be
+    uploaded with exactly its own bytes."""
+    O = oracle()
+    M, K, N1, N2, N3 = 256, 256, 512, 256, 128
+    big = np.full(M * N1 * 6 + 4096, 0x7F, np.uint8)
+    x = synth.randn(11, (M, K))
+    w1 = synth.randn(12, (N1, K), 0.05)
+    b1 = synth.randn(13, N1, 0.1)
+    w2 = synth.randn(14, (N2, N1), 0.05)
+    w3 = synth.randn(15, (N3, K), 0.05)
+
+    G = GraphBuilder()
+    tx, _ = G.tensor(abi.F32, (M, K), x, ephemeral=1)
+    tw1, _ = G.tensor(abi.F32, (N1, K), w1)
+    tw1t, _ = G.tensor(abi.F32, (K, N1))
+    th, _ = G.tensor(abi.F32, (M, N1))
+    tb1, _ = G.tensor(abi.F32, (N1,), b1)
+    thb, _ = G.tensor(abi.F32, (M, N1))
+    tg = abi.make_tensor(abi.F32, [M, N1], big.ctypes.data, M * N1 * 4)
+    G.keep.append(tg)
+    tw2, _ = G.tensor(abi.F32, (N2, N1), w2)
+    tw2t, _ = G.tensor(abi.F32, (N1, N2))
+    ty, _ = G.tensor(abi.F32, (M, N2))
+    G.node(abi.OP_TRANSPOSE, [tw1], tw1t)
+    G.node(abi.OP_MATMUL, [tx, tw1t], th)
+    G.node(abi.OP_ADD, [th, tb1], thb)
+    G.node(abi.OP_GELU, [thb], tg)
+    G.node(abi.OP_TRANSPOSE, [tw2], tw2t)
+    G.node(abi.OP_MATMUL, [tg, tw2t], ty)
+    assert be.graph_eval(G.g) == abi.OK
+    assert be.stats().operand_writes >= 1, "fc1 did not write fc2's operand form"
+    assert (big[M * N1 * 4:] == 0x7F).all(), "eval 1 wrote past its output"
+
+    big[:] = 0x7F
+    G2 = GraphBuilder()
+    tx2, _ = G2.tensor(abi.F32, (M, K), x, ephemeral=1)
+    tw3, _ = G2.tensor(abi.F32, (N3, K), w3)
+    tw3t, _ = G2.tensor(abi.F32, (K, N3))
+    ty3 = abi.make_tensor(abi.F32, [M, N3], big.ctypes.data, M * N3 * 4)
+    G2.keep.append(ty3)
+    G2.node(abi.OP_TRANSPOSE, [tw3], tw3t)
+    G2.node(abi.OP_MATMUL, [tx2, tw3t], ty3)
+    assert be.graph_eval(G2.g) == abi.OK
+    assert (big[M * N3 * 4:] == 0x7F).all(), "readback wrote past the output tensor"
+    got = _view(big, M * N3 * 4, np.float32).reshape(M, N3).copy()
+    assert_f32_close(got, ref_linear("f32", x, w3, b_nt=True), what="eval 2 output")
+
+    # eval 3: an ephemeral input of fewer bytes at B (the host rewrote it)
+    x4 = synth.randn(16, (M // 2, K // 2))
+    _view(big, x4.nbytes, np.float32)[:] = x4.reshape(-1)
+    w4 = synth.randn(17, (64, K // 2), 0.05)
+    G3 = GraphBuilder()
+    tx4 = abi.make_tensor(abi.F32, [M // 2, K // 2], big.ctypes.data, x4.nbytes)
+    tx4.ephemeral = 1
+    G3.keep.append(tx4)
+    tw4, _ = G3.tensor(abi.F32, (64, K // 2), w4)
+    tw4t, _ = G3.tensor(abi.F32, (K // 2, 64))
+    ty4, _ = G3.tensor(abi.F32, (M // 2, 64))
+    G3.node(abi.OP_TRANSPOSE, [tw4], tw4t)
+    G3.node(abi.OP_MATMUL, [tx4, tw4t], ty4)
+    assert be.graph_eval(G3.g) == abi.OK
+    assert_f32_close(out_array(ty4, np.float32, (M // 2, 64)),
+                     ref_linear("f32", x4, w4, b_nt=True), what="eval 3 output")

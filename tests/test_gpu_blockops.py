@@ -269,7 +269,7 @@ def test_vit_block_graph_all_on_gpu(is_global, e, heads):
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
 @pytest.mark.parametrize("via_reshape", [False, True])
-def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
+def test_layernorm_written_as_gemm_operand(env, wkind, via_reshape):
     """LAYERNORM -> (RESHAPE ->) linear, as gh_mlp and the global-attention
     qkv build it: the LN writes the operand its one GEMM reads (bf16
     hi/lo planes for f32 weights, f16 for Q8_0 weights) instead of its f32
@@ -283,11 +283,11 @@ def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
     w = synth.randn(803, (N, K), 0.05)
     bias = synth.randn(804, (N,), 0.02)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_LN_OPERAND", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_LN_OPERAND")
         else:
-            monkeypatch.setenv("SAM3_HIP_LN_OPERAND", env)
+            env.set("SAM3_HIP_LN_OPERAND", mode)
         G = graph.Graph()
         tx = G.tensor(abi.F32, (M, K), x)
         t = G.layernorm(tx, G.tensor(abi.F32, (K,), gam), G.tensor(abi.F32, (K,), bet))
@@ -316,7 +316,7 @@ def test_layernorm_written_as_gemm_operand(monkeypatch, wkind, via_reshape):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
-def test_gemm_written_as_next_gemm_operand(monkeypatch, wkind):
+def test_gemm_written_as_next_gemm_operand(env, wkind):
     """gh_mlp (graph_helpers.c:1258-1276) after a LayerNorm: fc1's result,
     after its folded bias and GELU, is read only by fc2, which converts
     its A first (bf16 hi/lo planes for f32 weights, f16 for Q8_0 weights).
@@ -335,11 +335,11 @@ def test_gemm_written_as_next_gemm_operand(monkeypatch, wkind):
         return (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
                 else G.tensor(abi.F32, w.shape, w))
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_GEMM_OPERAND", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_GEMM_OPERAND")
         else:
-            monkeypatch.setenv("SAM3_HIP_GEMM_OPERAND", env)
+            env.set("SAM3_HIP_GEMM_OPERAND", mode)
         G = graph.Graph()
         t = G.layernorm(G.tensor(abi.F32, (M, E), x), G.tensor(abi.F32, (E,), gam),
                         G.tensor(abi.F32, (E,), bet))
@@ -369,7 +369,7 @@ def test_gemm_written_as_next_gemm_operand(monkeypatch, wkind):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
-def test_permute_written_as_gemm_operand(monkeypatch, wkind):
+def test_permute_written_as_gemm_operand(env, wkind):
     """The attention head merge (gh_multihead_attention_rope, [B,H,N,D] ->
     [B,N,H,D] -> [B*N, H*D] -> out projection): an f32 TRANSPOSE that keeps
     its last axis and feeds only a GEMM's A writes that GEMM's operand
@@ -380,11 +380,11 @@ def test_permute_written_as_gemm_operand(monkeypatch, wkind):
     x = synth.randn(840, (B, H, N, D))
     w, bias = synth.randn(841, (E, H * D), 0.05), synth.randn(842, (E,), 0.02)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_PERMUTE_OPERAND", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_PERMUTE_OPERAND")
         else:
-            monkeypatch.setenv("SAM3_HIP_PERMUTE_OPERAND", env)
+            env.set("SAM3_HIP_PERMUTE_OPERAND", mode)
         G = graph.Graph()
         t = G.permute(G.tensor(abi.F32, x.shape, x), (0, 2, 1, 3))
         tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
@@ -409,7 +409,7 @@ def test_permute_written_as_gemm_operand(monkeypatch, wkind):
     assert_f32_close(fused, (a @ wd.T + bias).astype(np.float32), what=f"permute -> linear {wkind}")
 
 
-def test_qkv_slice_rope_split_chain(monkeypatch):
+def test_qkv_slice_rope_split_chain(env):
     """gh_multihead_attention_rope's q / k / v preparation: SLICE of the
     fused qkv rows -> RESHAPE [B,S,H,D] -> (ROPE -> RESHAPE -> RESHAPE) ->
     TRANSPOSE (0,2,1,3) runs as one kernel reading the qkv rows in place
@@ -422,11 +422,11 @@ def test_qkv_slice_rope_split_chain(monkeypatch):
     qkv = synth.randn(860, (B * S, 3 * E))
     c, sn = graph.rope_tables(side, D)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_QKV_CHAIN", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_QKV_CHAIN")
         else:
-            monkeypatch.setenv("SAM3_HIP_QKV_CHAIN", env)
+            env.set("SAM3_HIP_QKV_CHAIN", mode)
         G = graph.Graph()
         x = G.tensor(abi.F32, (B * S, 3 * E), qkv)
         ct, st_ = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, sn.shape, sn)
@@ -466,7 +466,7 @@ def test_qkv_slice_rope_split_chain(monkeypatch):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
-def test_residual_add_folded_into_gemm(monkeypatch, wkind):
+def test_residual_add_folded_into_gemm(env, wkind):
     """x + linear(LN(x)) as the ViT block builds its residuals
     (image_encoder.c:755-916): the ADD of the earlier f32 tensor is done in
     the GEMM epilogue after the bias, one f32 rounding as the ADD node
@@ -477,11 +477,11 @@ def test_residual_add_folded_into_gemm(monkeypatch, wkind):
     gam, bet = synth.randn(871, (E,)), synth.randn(872, (E,), 0.1)
     w, bias = synth.randn(873, (E, E), 0.04), synth.randn(874, (E,), 0.02)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_RESIDUAL_FOLD", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_RESIDUAL_FOLD")
         else:
-            monkeypatch.setenv("SAM3_HIP_RESIDUAL_FOLD", env)
+            env.set("SAM3_HIP_RESIDUAL_FOLD", mode)
         G = graph.Graph()
         tx = G.tensor(abi.F32, (M, E), x)
         t = G.layernorm(tx, G.tensor(abi.F32, (E,), gam), G.tensor(abi.F32, (E,), bet))
@@ -508,7 +508,7 @@ def test_residual_add_folded_into_gemm(monkeypatch, wkind):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
-def test_unpartition_and_residual_folded_into_gemm(monkeypatch, wkind):
+def test_unpartition_and_residual_folded_into_gemm(env, wkind):
     """The windowed block's output projection: linear on window rows ->
     gh_window_unpartition (RESHAPE -> TRANSPOSE (0,2,1,3) -> RESHAPE) ->
     x + that. The epilogue stores each C row at its unpartitioned row and
@@ -523,11 +523,11 @@ def test_unpartition_and_residual_folded_into_gemm(monkeypatch, wkind):
     gam, bet = synth.randn(884, (E,)), synth.randn(885, (E,), 0.1)
     w, bias = synth.randn(882, (E, E), 0.04), synth.randn(883, (E,), 0.02)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_UNPARTITION_FOLD", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_UNPARTITION_FOLD")
         else:
-            monkeypatch.setenv("SAM3_HIP_UNPARTITION_FOLD", env)
+            env.set("SAM3_HIP_UNPARTITION_FOLD", mode)
         G = graph.Graph()
         tw = (G.tensor(abi.Q8_0, w.shape, O.q8_quantize(w)) if wkind == "q8"
               else G.tensor(abi.F32, w.shape, w))
@@ -558,7 +558,7 @@ def test_unpartition_and_residual_folded_into_gemm(monkeypatch, wkind):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
-def test_partition_folded_into_layernorm(monkeypatch, wkind):
+def test_partition_folded_into_layernorm(env, wkind):
     """The windowed block's LN1 -> gh_window_partition -> qkv linear: the
     LayerNorm writes the GEMM's operand (bf16 planes / f16) with its rows
     already in window order, so the partition permute does not run; same
@@ -572,11 +572,11 @@ def test_partition_folded_into_layernorm(monkeypatch, wkind):
     gam, bet = synth.randn(891, (E,)), synth.randn(892, (E,), 0.1)
     w, bias = synth.randn(893, (N, E), 0.04), synth.randn(894, (N,), 0.02)
 
-    def run(env):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_PARTITION_FOLD", raising=False)
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_PARTITION_FOLD")
         else:
-            monkeypatch.setenv("SAM3_HIP_PARTITION_FOLD", env)
+            env.set("SAM3_HIP_PARTITION_FOLD", mode)
         G = graph.Graph()
         t = G.layernorm(G.tensor(abi.F32, (M, E), x), G.tensor(abi.F32, (E,), gam),
                         G.tensor(abi.F32, (E,), bet))

@@ -218,9 +218,9 @@ def test_f16_tiled_vs_oracle(M, N, K, nt):
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (100, 72, 36), (257, 130, 512)])
 @pytest.mark.parametrize("nt", [False, True])
-def test_f32_tiled_vs_oracle(M, N, K, nt, monkeypatch):
+def test_f32_tiled_vs_oracle(M, N, K, nt, env):
     """The f32 MFMA kernel (v_mfma_f32_32x32x2_f32, exact f32 products)."""
-    monkeypatch.setenv("SAM3_HIP_F32_SPLIT", "0")
+    env.set("SAM3_HIP_F32_SPLIT", "0")
     a = rnd(50 + M, (M, K))
     b = rnd(60 + N, (N, K) if nt else (K, N))
     if hip.matmul_path(abi.F32, abi.F32, abi.F32, M, N, K, hip.B_NT if nt else 0) != MFMA:
@@ -274,10 +274,10 @@ def test_fused_bias_gelu(kind):
 
 
 @pytest.mark.parametrize("cfg", list(range(13)))
-def test_dl_every_tile_config(monkeypatch, cfg):
+def test_dl_every_tile_config(env, cfg):
     """Each direct-to-LDS tile configuration (forced) on a ragged bf16 NT
     problem with a k tail, bias and GELU, against the oracle."""
-    monkeypatch.setenv("SAM3_HIP_DL_CFG", str(cfg))
+    env.set("SAM3_HIP_DL_CFG", str(cfg))
     O = oracle()
     M, N, K = 300, 520, 200
     a = O.f32_to_bf16(rnd(210, (M, K))).reshape(M, K)
@@ -333,12 +333,12 @@ def test_q8_nt_tiled_bf16_and_f16_activations(M, N, K):
 
 @pytest.mark.parametrize("cfg", list(range(7)))
 @pytest.mark.parametrize("a_dt", [abi.F32, abi.BF16, abi.F16])
-def test_q8_dl_every_config(monkeypatch, cfg, a_dt):
+def test_q8_dl_every_config(env, cfg, a_dt):
     """Direct-to-LDS Q8 GEMM (raw 36-byte blocks in LDS, dequantized per
     fragment) with each tile configuration forced, ragged M and N, bias +
     GELU. bf16 activations go through the f16 cast first; f32 activations
     run the register-staged kernel (the configuration does not apply)."""
-    monkeypatch.setenv("SAM3_HIP_DLQ8_CFG", str(cfg))
+    env.set("SAM3_HIP_DLQ8_CFG", str(cfg))
     O = oracle()
     M, N, K = 300, 200, 576
     a32 = rnd(220, (M, K))
@@ -415,12 +415,12 @@ STREAM_CFGS = [(mr, nt) for mr in (1, 4, 8, 16, 32) for nt in (1, 2, 4)]
 
 @pytest.mark.parametrize("K", [256, 1536])
 @pytest.mark.parametrize("mr,nt", STREAM_CFGS)
-def test_stream_kernel_every_shape(monkeypatch, mr, nt, K):
+def test_stream_kernel_every_shape(env, mr, nt, K):
     """q8_stream (K % 256 == 0) with each workgroup shape forced: M split
     over ceil(M / mr) workgroups, ragged N (not a multiple of 16*nt), one
     8-block chunk (K 256) or three 16-block chunks (K 1536; 8-block chunks
     for mr 32), fused bias + GELU."""
-    monkeypatch.setenv("SAM3_HIP_SK_CFG", f"{mr},{nt}")
+    env.set("SAM3_HIP_SK_CFG", f"{mr},{nt}")
     M, N = 37, 200
     a = rnd(170, (M, K))
     w = q8(rnd(171, (N, K), 0.02))
@@ -434,8 +434,8 @@ def test_stream_kernel_every_shape(monkeypatch, mr, nt, K):
 @pytest.mark.parametrize("K", [768, 1024])
 @pytest.mark.parametrize("a_dt", [abi.BF16, abi.F16])
 @pytest.mark.parametrize("mr,nt", [(1, 1), (8, 2), (32, 4)])
-def test_stream_kernel_16bit_activations(monkeypatch, a_dt, mr, nt, K):
-    monkeypatch.setenv("SAM3_HIP_SK_CFG", f"{mr},{nt}")
+def test_stream_kernel_16bit_activations(env, a_dt, mr, nt, K):
+    env.set("SAM3_HIP_SK_CFG", f"{mr},{nt}")
     O = oracle()
     M, N = 20, 72
     a32 = rnd(175, (M, K))

@@ -240,7 +240,7 @@ def test_prepared_weights_reused_and_dropped():
 
 
 @pytest.mark.parametrize("gelu", [False, True])
-def test_q8_weights_expanded_once(monkeypatch, gelu):
+def test_q8_weights_expanded_once(env, gelu):
     """Inside graph_eval a constant Q8_0 weight of a large-M GEMM is
     expanded once to f16 (q*scale in f32, rounded once) and reused by
     later evals (prep_hits). The f16 GEMM on it and the direct Q8 kernel
@@ -253,11 +253,11 @@ def test_q8_weights_expanded_once(monkeypatch, gelu):
     wq = O.q8_quantize(synth.randn(901, (N, K), 0.03))
     bias = synth.randn(902, (N,), 0.02)
 
-    def run(env, evals=2):
-        if env is None:
-            monkeypatch.delenv("SAM3_HIP_Q8_EXPAND", raising=False)
+    def run(mode, evals=2):
+        if mode is None:
+            env.unset("SAM3_HIP_Q8_EXPAND")
         else:
-            monkeypatch.setenv("SAM3_HIP_Q8_EXPAND", env)
+            env.set("SAM3_HIP_Q8_EXPAND", mode)
         G = graph.Graph()
         t = G.linear(G.tensor(abi.F32, (M, K), x), G.tensor(abi.Q8_0, (N, K), wq),
                      G.tensor(abi.F32, (N,), bias))
