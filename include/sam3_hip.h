@@ -79,6 +79,10 @@ struct sam3_hip_eval_stats {
 			    * rows) was reused instead of recomputed           */
 	int operand_writes; /* LAYERNORM outputs written straight in the form
 			     * their one consuming GEMM reads (not kept)      */
+	int range_reruns;  /* 1 when a fused producer's f16 GEMM operand held
+			    * values outside the f16 range and the graph was
+			    * run again with f32 operands (then the counts
+			    * above are the second run's)                   */
 };
 void sam3_hip_backend_last_stats(struct sam3_backend *be,
 				 struct sam3_hip_eval_stats *out);

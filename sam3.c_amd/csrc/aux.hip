@@ -166,6 +166,108 @@ __global__ void __launch_bounds__(256) cast_f16_k(const void *src, uint16_t *dst
 	}
 }
 
+/* Row-scaled f16 copy of activations (s3k_cast_f16_rows): one wave per
+ * row. The row's largest finite |x| picks a power-of-two factor 2^e
+ * (e = 0 when it lies in [2^-10, 2^15) or is 0, else the e that puts it
+ * in [2^14, 2^15)); the row is stored as f16(x * 2^-e), rs = 2^e. With
+ * VEC the row moves in 16-byte chunks of 8 values, up to CPL chunks per
+ * lane held in registers between the two passes (rows 16-byte aligned,
+ * K % 8 == 0, K <= 512 * CPL); otherwise values are read one at a time,
+ * twice. */
+__device__ __forceinline__ float pow2f(int e)
+{
+	return __uint_as_float((uint32_t)(e + 127) << 23); /* -126 <= e <= 127 */
+}
+
+__device__ __forceinline__ int row_scale_exp(float amax)
+{
+	amax = wave_max_f32(amax);
+	if (amax == 0.0f || (amax >= 0x1p-10f && amax < 0x1p15f))
+		return 0;
+	int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 14;
+	return e < -100 ? -100 : e > 113 ? 113 : e;
+}
+
+__device__ __forceinline__ float finite_abs(float x)
+{
+	const float a = __builtin_fabsf(x);
+	return a <= 3.402823466e38f ? a : 0.0f; /* inf and NaN do not set the scale */
+}
+
+template <bool BF16, bool VEC, int CPL>
+__global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long long lda_b,
+						       long long sa_b, uint16_t *dst, float *rs,
+						       int M, int K)
+{
+	const int lane = threadIdx.x & 63;
+	const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (m >= M)
+		return;
+	const long long row = (long long)blockIdx.y * M + m;
+	const char *x = src + (long long)blockIdx.y * sa_b + (long long)m * lda_b;
+	uint16_t *y = dst + row * K;
+	float amax = 0.0f;
+	if constexpr (VEC) {
+		constexpr int L = BF16 ? 1 : 2;
+		const int chunks = K / 8;
+		uint4 v[CPL][L];
+#pragma unroll
+		for (int u = 0; u < CPL; ++u) {
+			const int c = lane + 64 * u;
+#pragma unroll
+			for (int l = 0; l < L; ++l)
+				v[u][l] = c < chunks ? ((const uint4 *)x)[c * L + l] : make_uint4(0, 0, 0, 0);
+		}
+		float f[CPL][8];
+#pragma unroll
+		for (int u = 0; u < CPL; ++u) {
+			if constexpr (BF16) {
+				const uint32_t w[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
+#pragma unroll
+				for (int e = 0; e < 4; ++e) {
+					f[u][2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
+					f[u][2 * e + 1] = bf16_to_f32(w[e] >> 16);
+				}
+			} else {
+#pragma unroll
+				for (int l = 0; l < 2; ++l) {
+					f[u][4 * l] = __uint_as_float(v[u][l].x);
+					f[u][4 * l + 1] = __uint_as_float(v[u][l].y);
+					f[u][4 * l + 2] = __uint_as_float(v[u][l].z);
+					f[u][4 * l + 3] = __uint_as_float(v[u][l].w);
+				}
+			}
+#pragma unroll
+			for (int e = 0; e < 8; ++e)
+				amax = fmaxf(amax, finite_abs(f[u][e]));
+		}
+		const int ex = row_scale_exp(amax);
+		const float inv = pow2f(-ex);
+#pragma unroll
+		for (int u = 0; u < CPL; ++u) {
+			const int c = lane + 64 * u;
+			if (c < chunks)
+				((uint4 *)y)[c] = make_uint4(pack_f16x2(f[u][0] * inv, f[u][1] * inv),
+							     pack_f16x2(f[u][2] * inv, f[u][3] * inv),
+							     pack_f16x2(f[u][4] * inv, f[u][5] * inv),
+							     pack_f16x2(f[u][6] * inv, f[u][7] * inv));
+		}
+		if (lane == 0)
+			rs[row] = pow2f(ex);
+	} else {
+		for (int k = lane; k < K; k += 64)
+			amax = fmaxf(amax, finite_abs(BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+							: ((const float *)x)[k]));
+		const int ex = row_scale_exp(amax);
+		const float inv = pow2f(-ex);
+		for (int k = lane; k < K; k += 64)
+			y[k] = (uint16_t)f32_to_f16((BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+						     : ((const float *)x)[k]) * inv);
+		if (lane == 0)
+			rs[row] = pow2f(ex);
+	}
+}
+
 template <int KIND>
 __global__ void __launch_bounds__(256) bias_add_k(const void *x, const void *bias, void *out,
 						  long long rows, int n)
@@ -325,6 +427,46 @@ extern "C" int s3k_cast_f16(int kind, const void *src, void *dst, long long n, v
 	else
 		return (int)hipErrorInvalidValue;
 	return (int)hipGetLastError();
+}
+
+template <bool BF16>
+static int cast_rows_launch(const char *src, long long lda_b, long long sa_b, uint16_t *dst,
+			    float *rs, int batch, int M, int K, bool vec, hipStream_t st)
+{
+	const dim3 grid((unsigned)((M + 3) / 4), (unsigned)batch);
+	const int cpl = (K / 8 + 63) / 64;
+	if (!vec || cpl > 8)
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, false, 1>), grid, dim3(256), 0, st, src, lda_b,
+				   sa_b, dst, rs, M, K);
+	else if (cpl <= 2)
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2>), grid, dim3(256), 0, st, src, lda_b,
+				   sa_b, dst, rs, M, K);
+	else if (cpl <= 4)
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 4>), grid, dim3(256), 0, st, src, lda_b,
+				   sa_b, dst, rs, M, K);
+	else
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 8>), grid, dim3(256), 0, st, src, lda_b,
+				   sa_b, dst, rs, M, K);
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_cast_f16_rows(int kind, const void *src, long long lda, long long sa, void *dst,
+				 float *rs, int batch, int M, int K, void *stream)
+{
+	if (batch <= 0 || M <= 0 || K <= 0)
+		return 0;
+	if ((kind != S3K_F32 && kind != S3K_BF16) || !src || !dst || !rs || M > (1 << 30) ||
+	    batch > 65535)
+		return (int)hipErrorInvalidValue;
+	const int es = kind == S3K_F32 ? 4 : 2;
+	const bool vec = K % 8 == 0 && !(((uintptr_t)src | (uintptr_t)dst) & 15u) &&
+			 (lda * es) % 16 == 0 && (sa * es) % 16 == 0;
+	hipStream_t st = (hipStream_t)stream;
+	return kind == S3K_BF16
+		? cast_rows_launch<true>((const char *)src, lda * es, sa * es, (uint16_t *)dst, rs,
+					 batch, M, K, vec, st)
+		: cast_rows_launch<false>((const char *)src, lda * es, sa * es, (uint16_t *)dst, rs,
+					  batch, M, K, vec, st);
 }
 
 extern "C" int s3k_bias_add(int kind, const void *x, const void *bias, void *out,

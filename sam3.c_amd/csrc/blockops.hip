@@ -60,7 +60,24 @@ __device__ __forceinline__ float bo_wave_sum(float v)
  * ViT window partition written by the LN that precedes it). */
 struct LnMap {
 	int g, d1, d2;
+	unsigned *ovf;    /* S3K_LN_F16: range flag, tag stored when a row's  */
+	unsigned tag;     /* largest |y| is >= 2^15 or below 2^-10 (nonzero)  */
 };
+
+/* The f16 operand's range check of one row (rmax: the wave's largest
+ * finite |y|, every lane holding it): a row the f16 copy cannot hold to
+ * f16 precision stores the tag. */
+__device__ __forceinline__ void ln_range_flag(const LnMap &rm, float rmax, int lane)
+{
+	if (rm.ovf && lane == 0 && (rmax >= 32768.0f || (rmax > 0.0f && rmax < 0x1p-10f)))
+		*rm.ovf = rm.tag;
+}
+
+__device__ __forceinline__ float bo_finite_abs(float x)
+{
+	const float a = __builtin_fabsf(x);
+	return a <= 3.402823466e38f ? a : 0.0f;
+}
 
 __device__ __forceinline__ long long ln_out_row(const LnMap &rm, long long m)
 {
@@ -114,12 +131,15 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 		}
 	}
 	const float inv_std = 1.0f / sqrtf(bo_wave_sum(var) / (float)cols + 1e-5f);
+	float ymax = 0.0f;
 	auto finish = [&](int j, float xj) {
 		float val = mul_rn(sub_rn(xj, mean), inv_std);
 		if (gamma)
 			val = mul_rn(val, bo_ld<DT>(gamma, j));
 		if (beta)
 			val = add_rn(val, bo_ld<DT>(beta, j));
+		if constexpr (OUTF == S3K_LN_F16)
+			ymax = fmaxf(ymax, bo_finite_abs(val));
 		if constexpr (OUTF == S3K_LN_SAME) {
 			bo_st<DT>(out, obase + j, val);
 		} else if constexpr (OUTF == S3K_LN_PLANES) {
@@ -144,6 +164,8 @@ __global__ void __launch_bounds__(256) layernorm_k(const void *x, const void *ga
 		for (int j = lane; j < cols; j += 64)
 			finish(j, bo_ld<DT>(x, base + j));
 	}
+	if constexpr (OUTF == S3K_LN_F16)
+		ln_range_flag(rm, wave_max_f32(ymax), lane);
 }
 
 /* 16 bytes of a row as f32: 4 f32 or 8 bf16/f16 values. */
@@ -214,6 +236,7 @@ __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *ga
 			var = fmaf(d, d, var);
 		}
 	const float inv_std = 1.0f / sqrtf(bo_wave_sum(var) / (float)cols + 1e-5f);
+	float ymax = 0.0f;
 #pragma unroll
 	for (int i = 0; i < SLOTS; ++i) {
 		const int j0 = (i * 64 + lane) * VEC;
@@ -230,6 +253,8 @@ __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *ga
 			if (beta)
 				val = add_rn(val, b[e]);
 			v[i][e] = val;
+			if constexpr (OUTF == S3K_LN_F16)
+				ymax = fmaxf(ymax, bo_finite_abs(val));
 		}
 		if constexpr (OUTF == S3K_LN_SAME) {
 			bo_st16<DT>(out, obase + j0, v[i]);
@@ -246,6 +271,8 @@ __global__ void __launch_bounds__(256) layernorm_v(const void *x, const void *ga
 				make_uint2(pack_f16x2(v[i][0], v[i][1]), pack_f16x2(v[i][2], v[i][3]));
 		}
 	}
+	if constexpr (OUTF == S3K_LN_F16)
+		ln_range_flag(rm, wave_max_f32(ymax), lane);
 }
 
 /* pair p covers elements 2p, 2p+1 of x; its position s and frequency d
@@ -309,6 +336,8 @@ struct PermArgs {
 	unsigned od1, od2, od3;          /* output dims 1..3 (dim 0 implied) */
 	long long st0, st1, st2, st3;    /* input stride (elements) of output axis k */
 	long long total;
+	unsigned *ovf;                   /* f16 operand range flag (or NULL) */
+	unsigned tag;
 };
 
 /* I: index type, 32-bit when the element count allows it */
@@ -361,6 +390,17 @@ __global__ void __launch_bounds__(256) permute_op_k(PermArgs a, unsigned K)
 			*(uint2 *)(d + K) = make_uint2(lo[0], lo[1]);
 			*(uint2 *)(d + 2LL * K) = make_uint2(hi[0], hi[1]);
 		} else {
+			/* a value past 2^15, or four nonzero values all below 2^-10:
+			 * the f16 copy would not hold them to f16 precision */
+			const float ax = __builtin_fabsf(v.x), ay = __builtin_fabsf(v.y);
+			const float az = __builtin_fabsf(v.z), aw = __builtin_fabsf(v.w);
+			const float mx = fmaxf(fmaxf(ax, ay), fmaxf(az, aw));
+			const bool big = (ax >= 32768.0f && ax <= 3.402823466e38f) ||
+					 (ay >= 32768.0f && ay <= 3.402823466e38f) ||
+					 (az >= 32768.0f && az <= 3.402823466e38f) ||
+					 (aw >= 32768.0f && aw <= 3.402823466e38f);
+			if (a.ovf && (big || (mx > 0.0f && mx < 0x1p-10f)))
+				*a.ovf = a.tag;
 			*(uint2 *)((uint16_t *)a.dst + e) = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
 		}
 	}
@@ -377,7 +417,7 @@ static void launch_perm(const PermArgs &a, dim3 grid, hipStream_t st)
 
 template <int DT, int OUTF>
 static void launch_ln(const void *x, const void *g, const void *b, void *o, int rows, int cols,
-		      hipStream_t st, LnMap rm = LnMap{0, 0, 0})
+		      hipStream_t st, LnMap rm = LnMap{0, 0, 0, nullptr, 0})
 {
 	const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 	constexpr int VEC = DT == S3K_F32 ? 4 : 8;
@@ -431,7 +471,7 @@ extern "C" int s3k_layernorm(int kind, const void *x, const void *gamma, const v
 
 extern "C" int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma,
 				    const float *beta, void *out, long long rows, int cols, int rm_g,
-				    int rm_d1, int rm_d2, void *stream)
+				    int rm_d1, int rm_d2, unsigned *ovf, unsigned ovf_tag, void *stream)
 {
 	if (rows < 0 || cols <= 0 || rows > 0x7FFFFFFFLL || (fmt == S3K_LN_PLANES && cols % 8))
 		return (int)hipErrorInvalidValue;
@@ -440,7 +480,7 @@ extern "C" int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma,
 	if (rows == 0)
 		return (int)hipSuccess;
 	const hipStream_t st = (hipStream_t)stream;
-	const LnMap rm{rm_g, rm_d1, rm_d2};
+	const LnMap rm{rm_g, rm_d1, rm_d2, fmt == S3K_LN_F16 ? ovf : nullptr, ovf_tag};
 	if (fmt == S3K_LN_PLANES)
 		launch_ln<S3K_F32, S3K_LN_PLANES>(x, gamma, beta, out, (int)rows, cols, st, rm);
 	else if (fmt == S3K_LN_F16)
@@ -451,9 +491,11 @@ extern "C" int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma,
 }
 
 extern "C" int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta,
-				void *out, long long rows, int cols, void *stream)
+				void *out, long long rows, int cols, unsigned *ovf, unsigned ovf_tag,
+				void *stream)
 {
-	return s3k_layernorm_to_map(fmt, x, gamma, beta, out, rows, cols, 0, 0, 0, stream);
+	return s3k_layernorm_to_map(fmt, x, gamma, beta, out, rows, cols, 0, 0, 0, ovf, ovf_tag,
+				    stream);
 }
 
 extern "C" int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t,
@@ -504,7 +546,7 @@ extern "C" int s3k_rope_split(const float *x, long long pitch, long long col0, c
 /* dst = src permuted: output axis k is input axis axes[k]; ndim <= 4,
  * esize bytes per element. */
 extern "C" int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
-			      const int *axes, int K, void *stream)
+			      const int *axes, int K, unsigned *ovf, unsigned ovf_tag, void *stream)
 {
 	if (ndim < 1 || ndim > 4 || K <= 0 || K % 4 || (fmt != S3K_LN_PLANES && fmt != S3K_LN_F16) ||
 	    axes[ndim - 1] != ndim - 1 || in_dims[ndim - 1] % 4 ||
@@ -534,6 +576,8 @@ extern "C" int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, co
 	a.st2 = ist[ax[2]];
 	a.st3 = ist[ax[3]];
 	a.total = d[0] * d[1] * d[2] * d[3];
+	a.ovf = fmt == S3K_LN_F16 ? ovf : nullptr;
+	a.tag = ovf_tag;
 	if (a.total == 0 || a.od1 == 0 || a.od2 == 0 || a.od3 == 0)
 		return (int)hipSuccess;
 	const long long blocks = (a.total + 255) / 256;

@@ -398,6 +398,8 @@ __global__ void __launch_bounds__(256) gemm_generic(GemmArgs p, int a_ld, int b_
 			acc = add_rn(acc, mul_rn(a, load_as_f32(B, bi, BK_)));
 		}
 	}
+	if (p.flags & S3K_EPI_ROWSCALE)
+		acc *= p.rs[(long long)bz * p.rs_sb + m];
 	float bv = 0.0f;
 	if (p.flags & S3K_EPI_BIAS)
 		bv = load_as_f32(p.bias, n, p.bias_kind);
@@ -509,6 +511,10 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.rm_g = g->rm_g;
 	p.rm_d1 = g->rm_d1;
 	p.rm_d2 = g->rm_d2;
+	p.rs = g->rs;
+	p.rs_sb = g->rs_sb;
+	p.ovf = g->ovf;
+	p.ovf_tag = g->ovf_tag;
 	p.M = g->M;
 	p.N = g->N;
 	p.K = g->K;

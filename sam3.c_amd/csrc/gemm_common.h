@@ -22,6 +22,10 @@ struct GemmArgs {
 	long long sa_b, sb_b, sc;     /* batch strides: bytes, bytes, elements */
 	long long ldr;                /* residual row pitch, elements */
 	int rm_g, rm_d1, rm_d2;       /* output row map (s3k_gemm), rm_g 0 = none */
+	const float *rs;              /* S3K_EPI_ROWSCALE factors, rows apart   */
+	long long rs_sb;              /* ... per batch slice                    */
+	unsigned *ovf;                /* S3K_C_F16OP range flag (or NULL)       */
+	unsigned ovf_tag;
 	int flags;
 	int c_kind;
 	int bias_kind;
@@ -120,8 +124,26 @@ __device__ __forceinline__ long long out_row(const GemmArgs &p, int m)
  * W = 4 for f32 C and 8 for 16-bit C (one 16-byte store either way).
  * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
  * points; without it the values are only converted. */
+/* Whether f16 copies of these W values lose more than f16 rounding: an
+ * |x| of 2^15 or more (finite), or nonzero values that all lie below
+ * 2^-10 (a row made only of such runs would round to a few bits). */
+template <int W>
+__device__ __forceinline__ bool f16_out_of_range(const float *x)
+{
+	float mx = 0.0f;
+#pragma unroll
+	for (int e = 0; e < W; ++e) {
+		const float a = __builtin_fabsf(x[e]);
+		if (a >= 32768.0f && a <= 3.402823466e38f)
+			return true;
+		mx = a > mx ? a : mx;
+	}
+	return mx > 0.0f && mx < 0x1p-10f;
+}
+
 template <int CK, bool EPI, int W>
-__device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int n, const float *v)
+__device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int n, const float *v,
+				       int bz)
 {
 	typedef float f4v __attribute__((ext_vector_type(4)));
 	typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -134,6 +156,12 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 		x[e] = q.x; x[e + 1] = q.y; x[e + 2] = q.z; x[e + 3] = q.w;
 	}
 	if (EPI) {
+		if (p.flags & S3K_EPI_ROWSCALE) {
+			const float f = p.rs[(long long)bz * p.rs_sb + m];
+#pragma unroll
+			for (int e = 0; e < W; ++e)
+				x[e] *= f;
+		}
 		float bv[W];
 #pragma unroll
 		for (int e = 0; e < W; ++e)
@@ -231,6 +259,8 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 					c[e] = x[e];
 		}
 	} else {
+		if (CK == S3K_C_F16OP && p.ovf && f16_out_of_range<W>(x))
+			*p.ovf = p.ovf_tag;
 		uint32_t h[W];
 #pragma unroll
 		for (int e = 0; e < W; e += 2) {
@@ -271,7 +301,7 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
 	static_assert(CK != S3K_C_PLANES || WTN % 8 == 0, "planes are written 8 outputs at a time");
-	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES)) != 0;
+	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES | S3K_EPI_ROWSCALE)) != 0;
 	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
 	 * so consecutive lanes write consecutive 16 bytes of a row */
 	constexpr int W = CK == S3K_F32 ? 4 : 8;
@@ -290,14 +320,14 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			for (int s = lane; s < 32 * WTN / W; s += 64) {
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
 				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, true, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw);
+					finishw<CK, true, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw, bz);
 			}
 		} else {
 #pragma unroll 1
 			for (int s = lane; s < 32 * WTN / W; s += 64) {
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
 				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, false, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw);
+					finishw<CK, false, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw, bz);
 			}
 		}
 		wave_lds_fence();

@@ -35,6 +35,10 @@ enum s3k_kind {
 #define S3K_B_NT     4  /* B stored [N,K] (k contiguous), else [K,N]      */
 #define S3K_EPI_RES  8  /* out += res[m][n] last (res f32 [M,N]; kernels
 			 * with the shared LDS epilogue only)             */
+#define S3K_EPI_ROWSCALE 16 /* out = acc * rs[m] first: A holds row m of the
+			     * activations times 1/rs[m] (a power of two,
+			     * s3k_cast_f16_rows), so the f16 copy of rows
+			     * outside the f16 range stays exact           */
 
 /*
  * One (optionally strided-batched) GEMM: C[M,N] = A[M,K] * B, row-major.
@@ -61,6 +65,15 @@ struct s3k_gemm {
 	 * m / rm_g = (a*rm_d1 + b)*rm_d2 + c: the permute (0,2,1,3) of
 	 * [., rm_d1, rm_d2, rm_g*N] applied to the output */
 	int         rm_g, rm_d1, rm_d2;
+	/* S3K_EPI_ROWSCALE: per-row f32 factors, rs[b * rs_sb + m] for
+	 * batch slice b */
+	const float *rs;
+	long long   rs_sb;
+	/* f16 operand output (S3K_C_F16OP): when ovf is set, a value the f16
+	 * copy cannot hold faithfully (|x| >= 2^15, or a run of 8 nonzero
+	 * values all below 2^-10) stores ovf_tag to *ovf */
+	unsigned   *ovf;
+	unsigned    ovf_tag;
 };
 
 /* Which kernel s3k_gemm_launch would pick (for tests and the bench). */
@@ -96,6 +109,18 @@ int s3k_q8_quantize(const void *src, void *dst, int n, void *stream);
 int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream);
 /* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
 int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
+/*
+ * Activations for a GEMM that rounds them to f16, row by row: batch
+ * slices (at element stride sa) of M rows of K values (pitch lda) ->
+ * dense f16 [batch, M, K] and row factors rs [batch, M]. A row whose
+ * largest finite |x| lies in [2^-10, 2^15) (or is 0) is converted as is,
+ * rs = 1; any other row is first multiplied by 2^-e, e chosen so that
+ * its largest |x| lands in [2^14, 2^15), and rs = 2^e. The scaling is
+ * exact, so a GEMM on the copy times rs equals the GEMM on the
+ * activations up to the f16 rounding of in-range values.
+ */
+int s3k_cast_f16_rows(int kind, const void *src, long long lda, long long sa, void *dst,
+		      float *rs, int batch, int M, int K, void *stream);
 /* Fused attention out = softmax(Q K^T / sqrt(D) + mask) V over BH heads:
  * Q and out [BH, Sq, D], K and V [BH, Sk, D], one dtype (S3K_F32, _BF16,
  * _F16); mask f32 [Sq, Sk] or NULL. s3k_attn_path gives the kernel that
@@ -115,24 +140,29 @@ int s3k_layernorm(int kind, const void *x, const void *gamma, const void *beta, 
 /* f32 LayerNorm written as the operand a GEMM reads: bf16 planes
  * [rows, 3*cols] = [hi|lo|hi] (S3K_LN_PLANES, the split f32 GEMM's A) or
  * f16 [rows, cols] (S3K_LN_F16, the Q8 GEMM's A); the same values as
- * s3k_layernorm followed by s3k_split3_bf16 / s3k_cast_f16. */
+ * s3k_layernorm followed by s3k_split3_bf16 / s3k_cast_f16. For the f16
+ * form, ovf (when not NULL) receives ovf_tag if a row's largest |y| lies
+ * outside [2^-10, 2^15) (and is not 0): the f16 copy of that row is not
+ * faithful, and the caller redoes the GEMM on f32 values. */
 enum { S3K_LN_SAME = 0, S3K_LN_PLANES = 1, S3K_LN_F16 = 2 };
 int s3k_layernorm_to(int fmt, const float *x, const float *gamma, const float *beta, void *out,
-		     long long rows, int cols, void *stream);
+		     long long rows, int cols, unsigned *ovf, unsigned ovf_tag, void *stream);
 /* The same with output row m stored at the row map (rm_g, rm_d1, rm_d2)
  * of struct s3k_gemm (rm_g 0: identity): the ViT window partition. */
 int s3k_layernorm_to_map(int fmt, const float *x, const float *gamma, const float *beta,
 			 void *out, long long rows, int cols, int rm_g, int rm_d1, int rm_d2,
-			 void *stream);
+			 unsigned *ovf, unsigned ovf_tag, void *stream);
 int s3k_rope(int kind, const void *x, const float *cos_t, const float *sin_t, void *out,
 	     int batch, int seq, int heads, int hd, void *stream);
 int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_dims,
 		const int *axes, void *stream);
 /* f32 permute (last axis kept, its size % 4 == 0) written as the operand
  * of a GEMM that reads the output as rows of K values: fmt S3K_LN_PLANES
- * (bf16 [hi|lo|hi], row pitch 3K) or S3K_LN_F16. */
+ * (bf16 [hi|lo|hi], row pitch 3K) or S3K_LN_F16 (ovf as for
+ * s3k_layernorm_to, checked per 4 values: one past 2^15, or all nonzero
+ * and below 2^-10). */
 int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
-		   const int *axes, int K, void *stream);
+		   const int *axes, int K, unsigned *ovf, unsigned ovf_tag, void *stream);
 /* Attention operand [B, H, S, D] (f32) from columns col0.. of rows of
  * `pitch` values holding [B*S, H*D] (the q, k or v part of a fused qkv
  * output), with RoPE (tables [S, D/2]) when cos_t/sin_t are given. */

@@ -39,6 +39,15 @@ __device__ __forceinline__ float sub_rn(float a, float b)
 	return a - b;
 }
 
+/* Largest v over the 64 lanes of the wave. */
+__device__ __forceinline__ float wave_max_f32(float v)
+{
+#pragma unroll
+	for (int off = 32; off > 0; off >>= 1)
+		v = fmaxf(v, __shfl_xor(v, off));
+	return v;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t b)
 {
 	return __uint_as_float(b << 16);

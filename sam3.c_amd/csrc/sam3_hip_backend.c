@@ -103,6 +103,13 @@ struct sam3_hip_backend {
 	sam3_hip_host_dispatch_fn host_fn;
 	void *host_ctx;
 	struct sam3_hip_eval_stats stats;
+	/* f16 GEMM operands written by fused producers: a device word the
+	 * writers set to this eval's tag when a value does not fit f16
+	 * (then the eval is redone without f16 operand forms) */
+	unsigned *ovf;
+	unsigned ovf_tag;
+	int f16_writes;
+	int no_f16_ops;
 };
 
 /* ------------------------------------------------------------------ */
@@ -646,15 +653,17 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
-						dres, NULL, flags, hb->stream);
-		if (err == SAM3_OK)
+						dres, NULL, flags, hb->ovf, hb->ovf_tag, hb->stream);
+		if (err == SAM3_OK) {
 			hb->stats.operand_writes++;
+			hb->f16_writes += o_fmt == S3H_A_F16;
+		}
 	} else if (dres || row_map[0]) {
 		err = dev_out(hb, out, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, S3H_A_PLAIN, a_dt, da, b_dt, db, dc, M, N, K,
-						dbias, dres, row_map[0] ? row_map : NULL, flags,
-						hb->stream);
+						dbias, dres, row_map[0] ? row_map : NULL, flags, NULL,
+						0, hb->stream);
 		if (err == SAM3_OK)
 			for (int k = 0; k < n_chain; k++)
 				done[chain[k]] = 1;
@@ -734,8 +743,9 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 	if (dev_in(hb, bsrc, &db) != SAM3_OK)
 		return S3H_A_PLAIN;
 	static const char aligned_a[16] __attribute__((aligned(16)));
-	return s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, bsrc->dtype, db, SAM3_DTYPE_F32, M, N,
-				   K, w ? SAM3_HIP_B_NT : 0);
+	const int f = s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, bsrc->dtype, db, SAM3_DTYPE_F32,
+					  M, N, K, w ? SAM3_HIP_B_NT : 0);
+	return f == S3H_A_F16 && hb->no_f16_ops ? S3H_A_PLAIN : f;
 }
 
 /* The form an f32 LAYERNORM at node i writes: its consumer's operand. */
@@ -889,10 +899,11 @@ static enum sam3_error run_permute_as(struct sam3_hip_backend *hb, const struct 
 		err = dev_out_fmt(hb, n->output,
 				  (size_t)s3h_nelems(n->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
 	if (err == SAM3_OK)
-		err = s3h_transpose_to(n, dx, dy, fmt, K, hb->stream);
+		err = s3h_transpose_to(n, dx, dy, fmt, K, hb->ovf, hb->ovf_tag, hb->stream);
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.operand_writes++;
+		hb->f16_writes += fmt == S3H_A_F16;
 	}
 	return err;
 }
@@ -966,11 +977,12 @@ static enum sam3_error run_layernorm_map(struct sam3_hip_backend *hb, const stru
 		err = s3h_hip(s3k_layernorm_to_map(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
 						   (const float *)dx, (const float *)dg,
 						   (const float *)db, dy, rows, cols, rm[0], rm[1], rm[2],
-						   hb->stream),
+						   hb->ovf, hb->ovf_tag, hb->stream),
 			      "layernorm (GEMM operand, partition order)");
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.operand_writes++;
+		hb->f16_writes += fmt == S3H_A_F16;
 	}
 	return err;
 }
@@ -994,8 +1006,11 @@ static enum sam3_error run_layernorm_as(struct sam3_hip_backend *hb, const struc
 	if (err == SAM3_OK)
 		err = s3h_hip(s3k_layernorm_to(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
 					       (const float *)dx, (const float *)dg,
-					       (const float *)db, dy, rows, cols, hb->stream),
+					       (const float *)db, dy, rows, cols, hb->ovf, hb->ovf_tag,
+					       hb->stream),
 			      "layernorm (GEMM operand)");
+	if (err == SAM3_OK)
+		hb->f16_writes += fmt == S3H_A_F16;
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.operand_writes++;
@@ -1174,41 +1189,15 @@ static enum sam3_error run_host(struct sam3_hip_backend *hb, const struct sam3_n
 	return SAM3_OK;
 }
 
-static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph *g)
+/* The nodes of g in order, as cpu_graph_eval runs them
+ * (cpu_backend.c:134-148), with this backend's folds. */
+static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_graph *g,
+				 struct use_map *uses_p, unsigned char *folded, unsigned char *done)
 {
-	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
-	enum sam3_error err;
-
-	if (!be || !g) {
-		s3h_error("graph_eval: NULL argument");
-		return SAM3_EINVAL;
-	}
-	memset(&hb->stats, 0, sizeof(hb->stats));
-	if (g->n_nodes <= 0)
-		return SAM3_OK;
-	err = s3h_hip(hipSetDevice(hb->device), "graph_eval: set device");
-	if (err != SAM3_OK)
-		return err;
-
-	struct use_map uses;
-	err = build_uses(g, &uses);
-	if (err != SAM3_OK)
-		return err;
-	unsigned char *folded = calloc((size_t)g->n_nodes, 1);
-	unsigned char *done = calloc((size_t)g->n_nodes, 1);
+	enum sam3_error err = SAM3_OK;
+	struct use_map uses = *uses_p;
 	const struct s3h_settings *set = s3h_settings();
 	const int qkv_plain = !set->qkv_chain;
-	if (!folded || !done) {
-		free(folded);
-		free(done);
-		free(uses.key);
-		free(uses.count);
-		s3h_error("graph_eval: out of host memory");
-		return SAM3_ENOMEM;
-	}
-	for (int i = 0; i < hb->n_res; i++)
-		hb->res[i].produced = hb->res[i].fresh = 0;
-	s3h_cur = hb;
 	const int ln_plain = !set->ln_operand;
 	const int perm_plain = !set->permute_operand;
 	int ln_fmt = S3H_A_PLAIN, perm_k = 0;
@@ -1261,6 +1250,71 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 		if (err != SAM3_OK)
 			s3h_error("hip_graph_eval: node %d (op=%d) failed", i, n->op);
 		i += used;
+	}
+
+	return err;
+}
+
+static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph *g)
+{
+	struct sam3_hip_backend *hb = (struct sam3_hip_backend *)be;
+	enum sam3_error err;
+
+	if (!be || !g) {
+		s3h_error("graph_eval: NULL argument");
+		return SAM3_EINVAL;
+	}
+	memset(&hb->stats, 0, sizeof(hb->stats));
+	if (g->n_nodes <= 0)
+		return SAM3_OK;
+	err = s3h_hip(hipSetDevice(hb->device), "graph_eval: set device");
+	if (err != SAM3_OK)
+		return err;
+
+	struct use_map uses;
+	err = build_uses(g, &uses);
+	if (err != SAM3_OK)
+		return err;
+	unsigned char *folded = calloc((size_t)g->n_nodes, 1);
+	unsigned char *done = calloc((size_t)g->n_nodes, 1);
+	if (!folded || !done) {
+		free(folded);
+		free(done);
+		free(uses.key);
+		free(uses.count);
+		s3h_error("graph_eval: out of host memory");
+		return SAM3_ENOMEM;
+	}
+	for (int i = 0; i < hb->n_res; i++)
+		hb->res[i].produced = hb->res[i].fresh = 0;
+	s3h_cur = hb;
+	hb->no_f16_ops = 0;
+	hb->f16_writes = 0;
+	hb->ovf_tag = hb->ovf_tag + 1 ? hb->ovf_tag + 1 : 1;
+	err = run_nodes(hb, g, &uses, folded, done);
+	/* A fused producer that wrote an f16 GEMM operand flags values the
+	 * f16 copy cannot hold (|x| >= 2^15, or runs of tiny values). Then
+	 * the graph runs again without f16 operand forms: the consumers read
+	 * f32 and make their row-scaled f16 copy themselves. The graph's
+	 * inputs are unchanged by the first run (nodes write only their own
+	 * outputs), so the second run starts from the same state. */
+	if (err == SAM3_OK && hb->f16_writes) {
+		unsigned tag = 0;
+		err = s3h_hip(hipMemcpyAsync(&tag, hb->ovf, sizeof(tag), hipMemcpyDeviceToHost,
+					     hb->stream),
+			      "graph_eval: range flag");
+		if (err == SAM3_OK)
+			err = s3h_hip(hipStreamSynchronize(hb->stream), "graph_eval: range flag");
+		if (err == SAM3_OK && tag == hb->ovf_tag) {
+			const struct sam3_hip_eval_stats first = hb->stats;
+			memset(&hb->stats, 0, sizeof(hb->stats));
+			hb->stats.range_reruns = first.range_reruns + 1;
+			memset(folded, 0, (size_t)g->n_nodes);
+			memset(done, 0, (size_t)g->n_nodes);
+			hb->no_f16_ops = 1;
+			err = run_nodes(hb, g, &uses, folded, done);
+			hb->no_f16_ops = 0;
+		}
 	}
 
 	/* Readback of the graph's final outputs: node outputs no node of the
@@ -1341,6 +1395,10 @@ static enum sam3_error hip_init(struct sam3_backend *be)
 	if (err == SAM3_OK)
 		err = s3h_hip(hipStreamCreateWithFlags(&hb->stream, hipStreamNonBlocking),
 			      "hip backend: stream");
+	if (err == SAM3_OK)
+		err = s3h_hip(hipMalloc((void **)&hb->ovf, 256), "hip backend: range flag");
+	if (err == SAM3_OK)
+		err = s3h_hip(hipMemset(hb->ovf, 0, 256), "hip backend: range flag");
 	return err;
 }
 
@@ -1380,6 +1438,10 @@ static void hip_free(struct sam3_backend *be)
 	if (hb->arena) {
 		(void)hipHostFree(hb->arena);
 		hb->arena = NULL;
+	}
+	if (hb->ovf) {
+		(void)hipFree(hb->ovf);
+		hb->ovf = NULL;
 	}
 }
 

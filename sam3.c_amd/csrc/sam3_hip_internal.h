@@ -25,8 +25,11 @@ int s3h_transpose_is_swap(const struct sam3_node *node);
 /* f32 TRANSPOSE keeping its last axis, written as the operand form fmt
  * (S3H_A_PLANES / S3H_A_F16) of a GEMM reading the output as rows of K. */
 int s3h_transpose_to_ok(const struct sam3_node *node, int K);
+/* An f16 form (S3H_A_F16) stores ovf_tag to *ovf (when ovf is set) if
+ * some values do not fit f16 (s3k_permute_to); the same holds for the
+ * f16 output form of s3h_matmul_fmt_to. */
 enum sam3_error s3h_transpose_to(const struct sam3_node *node, const void *src, void *dst, int fmt,
-				 int K, void *stream);
+				 int K, unsigned *ovf, unsigned ovf_tag, void *stream);
 /* Device scratch reused in stream order: a block given back with
  * s3h_scratch_free(p, stream) is handed out again only to requests on
  * that stream. s3h_scratch_release(stream) returns the stream's idle
@@ -89,7 +92,8 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 		      int K, int flags, int out_fmt);
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
-				  const void *res, const int *row_map, int flags, void *stream);
+				  const void *res, const int *row_map, int flags, unsigned *ovf,
+				  unsigned ovf_tag, void *stream);
 
 /* Prepared copies of constant weights (bf16 hi/lo planes, padded rows),
  * kept by the backend whose graph_eval is running on this thread. A copy

@@ -260,6 +260,83 @@ static void fill_gemm(struct s3k_gemm *g, int a_dt, const void *a, int b_dt, con
 	g->flags = flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT);
 }
 
+/* f32 or bf16 activations of a kernel that rounds them to f16 (the Q8
+ * GEMMs and GEMVs, and the f16 GEMM on unpacked Q8 weights): copied row
+ * by row to f16 with a power-of-two factor per row (s3k_cast_f16_rows),
+ * so rows outside the f16 range (|a| >= 2^15, or all below 2^-10) are
+ * scaled into it instead of turning into inf or losing their bits; g
+ * then reads the copy and multiplies row m of its result by rs[m] before
+ * the bias (S3K_EPI_ROWSCALE), which undoes the factor exactly. Slices
+ * sharing their activations (batch stride 0) are copied once. *tmp gets
+ * the scratch block, the caller's to free. */
+static enum sam3_error a_rows_f16(struct s3k_gemm *g, void **tmp, void *stream)
+{
+	const int shared = g->batch > 1 && g->stride_a == 0;
+	const int nb = shared ? 1 : g->batch;
+	const size_t a_bytes = ((size_t)nb * g->M * g->K * 2 + 255) & ~(size_t)255;
+	*tmp = NULL;
+	enum sam3_error err = s3h_scratch_alloc(tmp, a_bytes + (size_t)nb * g->M * 4, stream);
+	if (err != SAM3_OK)
+		return err;
+	float *rs = (float *)((char *)*tmp + a_bytes);
+	err = s3h_hip(s3k_cast_f16_rows(g->a_kind, g->a, g->lda, g->stride_a, *tmp, rs, nb, g->M,
+					g->K, stream),
+		      "matmul activation cast");
+	if (err != SAM3_OK)
+		return err;
+	g->a = *tmp;
+	g->a_kind = S3K_F16;
+	g->lda = g->K;
+	g->stride_a = shared ? 0 : (long long)g->M * g->K;
+	g->rs = rs;
+	g->rs_sb = shared ? 0 : g->M;
+	g->flags |= S3K_EPI_ROWSCALE;
+	return SAM3_OK;
+}
+
+/* Whether kernel path `path` of g rounds f32/bf16 activations to f16. */
+static int rounds_a_to_f16(const struct s3k_gemm *g, int path)
+{
+	if (g->a_kind == S3K_F16 || (path != S3K_PATH_MFMA && path != S3K_PATH_SKINNY))
+		return 0;
+	return g->b_kind == S3K_Q8 || (g->b_kind == S3K_F16 && g->a_kind != S3K_F16);
+}
+
+/* g on kernel path `path`, after the row-scaled f16 copy of its
+ * activations where that path would round them to f16. */
+static enum sam3_error launch_a_safe(const struct s3k_gemm *g, int path, const char *what,
+				     void *stream)
+{
+	if (!rounds_a_to_f16(g, path)) {
+		int e = s3k_gemm_launch_path(g, path, stream);
+		if (e == hipErrorInvalidValue) {
+			s3h_error("%s: path %d cannot run M=%d N=%d K=%d", what, path, g->M, g->N,
+				  g->K);
+			return SAM3_EINVAL;
+		}
+		return s3h_hip(e, what);
+	}
+	struct s3k_gemm h = *g;
+	void *tmp = NULL;
+	enum sam3_error err = a_rows_f16(&h, &tmp, stream);
+	if (err == SAM3_OK) {
+		int e = s3k_gemm_launch_path(&h, path, stream);
+		if (e == hipErrorInvalidValue) {
+			s3h_error("%s: path %d cannot run M=%d N=%d K=%d", what, path, g->M, g->N,
+				  g->K);
+			err = SAM3_EINVAL;
+		} else {
+			err = s3h_hip(e, what);
+		}
+	}
+	if (tmp) {
+		enum sam3_error ferr = s3h_scratch_free(tmp, stream);
+		if (err == SAM3_OK)
+			err = ferr;
+	}
+	return err;
+}
+
 /* Q8 layouts the tiled kernels cannot stream (blocks over the [K,N] flat
  * index, or [N,K] rows that split blocks): unpack to f16 [N,K] in
  * stream-ordered scratch and run the f16 NT GEMM on it. */
@@ -283,7 +360,7 @@ static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 		h.ldb = g->K;
 		h.flags |= S3K_B_NT;
 		if (h.a_kind == S3K_F16 || s3k_gemm_path(&h) == S3K_PATH_MFMA)
-			err = s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8 gemm");
+			err = launch_a_safe(&h, s3k_gemm_path(&h), "matmul_q8 gemm", stream);
 		else
 			err = s3h_hip(s3k_gemm_launch_path(g, S3K_PATH_GENERIC, stream),
 				      "matmul_q8 generic");
@@ -376,27 +453,21 @@ static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 }
 
 /* f32/bf16 activations times Q8_0 [N,K] weights on the direct-to-LDS Q8
- * GEMM: the activations are cast to f16 once into stream-ordered scratch
- * (the value the register-staged loader would form), then the GEMM runs
- * on f16 A. */
+ * GEMM (or the f16 GEMM on expanded weights): the activations are copied
+ * to f16 once, row-scaled (a_rows_f16), then the GEMM runs on f16 A. */
 static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 {
-	const size_t bytes = (size_t)g->M * g->K * 2;
-	void *a16 = NULL;
-	enum sam3_error err = s3h_scratch_alloc(&a16, bytes, stream);
-	if (err != SAM3_OK)
-		return err;
-	err = s3h_hip(s3k_cast_f16(g->a_kind, g->a, a16, (long long)g->M * g->K, stream),
-		      "matmul_q8 activation cast");
-	if (err == SAM3_OK) {
-		struct s3k_gemm h = *g;
-		h.a = a16;
-		h.a_kind = S3K_F16;
-		h.lda = g->K;
+	struct s3k_gemm h = *g;
+	void *tmp = NULL;
+	enum sam3_error err = a_rows_f16(&h, &tmp, stream);
+	if (err == SAM3_OK)
 		err = q8_f16_gemm(&h, stream);
+	if (tmp) {
+		enum sam3_error ferr = s3h_scratch_free(tmp, stream);
+		if (err == SAM3_OK)
+			err = ferr;
 	}
-	enum sam3_error ferr = s3h_scratch_free(a16, stream);
-	return err != SAM3_OK ? err : ferr;
+	return err;
 }
 
 static int q8_dl_wants_cast(const struct s3k_gemm *g)
@@ -506,7 +577,12 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 			return q8_dl_cast(&g, stream);
 		if (g.b_kind == S3K_Q8 && g.a_kind == S3K_F16 && s3k_gemm_path(&g) == S3K_PATH_MFMA)
 			return q8_f16_gemm(&g, stream);
-		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul");
+		const int p0 = s3k_gemm_path(&g);
+		if (p0 == S3K_PATH_NONE) {
+			s3h_error("matmul: no kernel for M=%d N=%d K=%d", M, N, K);
+			return SAM3_EINVAL;
+		}
+		return launch_a_safe(&g, p0, "matmul", stream);
 	}
 	if (path < S3K_PATH_MFMA || path > S3K_PATH_GENERIC) {
 		s3h_error("matmul: unknown path %d", path);
@@ -518,12 +594,7 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 		return f32_split_gemm(&g, NULL, stream);
 	if (path == S3K_PATH_MFMA && q8_dl_wants_cast(&g))
 		return q8_dl_cast(&g, stream);
-	int e = s3k_gemm_launch_path(&g, path, stream);
-	if (e == hipErrorInvalidValue) {
-		s3h_error("matmul: path %d cannot run M=%d N=%d K=%d", path, M, N, K);
-		return SAM3_EINVAL;
-	}
-	return s3h_hip(e, "matmul");
+	return launch_a_safe(&g, path, "matmul", stream);
 }
 
 int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
@@ -613,7 +684,8 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
  * of the f32 output would give. */
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
-				  const void *res, const int *row_map, int flags, void *stream)
+				  const void *res, const int *row_map, int flags, unsigned *ovf,
+				  unsigned ovf_tag, void *stream)
 {
 	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) || (res && ((uintptr_t)res & 3u)) ||
 	    !s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt)) {
@@ -626,6 +698,10 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 		 : out_fmt == S3H_A_F16     ? S3K_C_F16OP
 					    : S3K_F32;
 	g.ldc = out_fmt == S3H_A_PLANES ? 3 * N : N;
+	if (out_fmt == S3H_A_F16) {
+		g.ovf = ovf;
+		g.ovf_tag = ovf_tag;
+	}
 	if (res) {
 		g.res = res;
 		g.flags |= S3K_EPI_RES;
@@ -747,22 +823,14 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 	g.stride_b = stride_w;
 	g.stride_c = stride_c;
 	if (s3k_gemm_path(&g) == S3K_PATH_SKINNY) {
-		/* f32 activations shared by every slice (stride 0) are cast to
-		 * f16 once, the rounding the skinny kernel gives f32 activations
-		 * itself (bit-identical results), so each workgroup moves half
-		 * the activation bytes */
+		/* f32/bf16 activations are copied to f16 once, row-scaled
+		 * (a_rows_f16; slices sharing them, at stride 0, share the copy),
+		 * so each workgroup moves half the activation bytes */
 		struct s3k_gemm h = g;
 		void *a16 = NULL;
 		enum sam3_error err = SAM3_OK;
-		if (a_dtype == SAM3_DTYPE_F32 && stride_a == 0 && batch > 1) {
-			err = s3h_scratch_alloc(&a16, (size_t)M * K * 2, stream);
-			if (err != SAM3_OK)
-				return err;
-			err = s3h_hip(s3k_cast_f16(S3K_F32, a, a16, (long long)M * K, stream),
-				      "matmul_q8_batched activation cast");
-			h.a = a16;
-			h.a_kind = S3K_F16;
-		}
+		if (a_dtype != SAM3_DTYPE_F16)
+			err = a_rows_f16(&h, &a16, stream);
 		if (err == SAM3_OK) {
 			const int force = s3h_settings()->q8_batch_path;
 			const int gemm = h.a_kind == S3K_F16 && batch > 1 &&
@@ -1103,7 +1171,7 @@ int s3h_transpose_to_ok(const struct sam3_node *node, int K)
 }
 
 enum sam3_error s3h_transpose_to(const struct sam3_node *node, const void *src, void *dst, int fmt,
-				 int K, void *stream)
+				 int K, unsigned *ovf, unsigned ovf_tag, void *stream)
 {
 	if (!s3h_transpose_to_ok(node, K) || (fmt != S3H_A_PLANES && fmt != S3H_A_F16)) {
 		s3h_error("transpose: cannot write GEMM operand form %d (K=%d)", fmt, K);
@@ -1113,7 +1181,8 @@ enum sam3_error s3h_transpose_to(const struct sam3_node *node, const void *src, 
 	int axes[4];
 	transpose_axes(node, in->n_dims, axes);
 	return s3h_hip(s3k_permute_to(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
-				      (const float *)src, dst, in->n_dims, in->dims, axes, K, stream),
+				      (const float *)src, dst, in->n_dims, in->dims, axes, K, ovf, ovf_tag,
+				      stream),
 		       "transpose (GEMM operand)");
 }
 

@@ -57,6 +57,7 @@ struct SkinnyArgs {
 	int M, N, K;
 	long long lda, ldc;   /* elements */
 	int a_kind, c_kind, flags;
+	const float *rs;      /* S3K_EPI_ROWSCALE row factors */
 };
 
 /* Two int8 (selected by SEL from w ^ 0x80808080) -> exact f16 pair. */
@@ -169,6 +170,8 @@ __global__ void __launch_bounds__(WV * 64) q8_skinny(SkinnyArgs p)
 		const int n = n0 + t * 16 + (ln & 15);
 		if (m >= p.M || n >= p.N)
 			continue;
+		if (p.flags & S3K_EPI_ROWSCALE)
+			s *= p.rs[m];
 		float bv = 0.0f;
 		if (p.flags & S3K_EPI_BIAS)
 			bv = load_as_f32(p.bias, n, p.c_kind);
@@ -201,6 +204,8 @@ struct StreamArgs {
 	int flags;
 	int groups;                /* weight-row groups: ceil(N / NR)         */
 	int zsplit;                /* activation-row groups: ceil(M / MR)     */
+	const float *rs;           /* S3K_EPI_ROWSCALE row factors ...        */
+	long long rs_sb;           /* ... and their batch stride              */
 };
 
 template <int AK, int MR, int NT, int KC>
@@ -430,6 +435,8 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		const int n = n0 + t * 16 + (ln & 15);
 		if (m >= Mz || n >= p.N)
 			continue;
+		if (p.flags & S3K_EPI_ROWSCALE)
+			s *= p.rs[blockIdx.y * p.rs_sb + m0 + m];
 		const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
 		cb[(long long)(m0 + m) * p.ldc + n] = epilogue<0>(s, bv, p.flags);
 	}
@@ -545,6 +552,8 @@ static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 	p.flags = g->flags;
 	p.groups = (g->N + 16 * NT - 1) / (16 * NT);
 	p.zsplit = (g->M + MR - 1) / MR;
+	p.rs = g->rs;
+	p.rs_sb = g->rs_sb;
 	dim3 grid(p.groups * p.zsplit, g->batch);
 	hipLaunchKernelGGL((q8_stream<AK, MR, NT, KC>), grid,
 			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), 0, (hipStream_t)stream, p);
@@ -685,6 +694,7 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 	p.a_kind = g->a_kind;
 	p.c_kind = g->c_kind;
 	p.flags = g->flags;
+	p.rs = g->rs;
 	hipStream_t st = (hipStream_t)stream;
 	switch (g->a_kind) {
 	case S3K_F32:  return launch_mt<S3K_F32>(p, st);

@@ -87,7 +87,8 @@ BIAS, GELU, B_NT = 1, 2, 4
 class EvalStats(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("gpu_nodes", "fused_nodes", "host_nodes",
                                        "uploads", "cache_hits", "downloads",
-                                       "mapped_reads", "prep_hits", "operand_writes")]
+                                       "mapped_reads", "prep_hits", "operand_writes",
+                                       "range_reruns")]
 
 
 class HipError(RuntimeError):
