@@ -319,6 +319,24 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 					   long long stride_c, const void *bias, int flags,
 					   void *stream);
 
+/*
+ * sam3_hip_matmul for Q8_0 weights that allocates nothing: C[M,N] (F32) =
+ * A[M,K] * W^T (+bias) (GELU), W[N,K] Q8_0 blocks along k (K % 32 == 0),
+ * A F32, F16 or BF16, bias F32 [N]. The same kernels run as in
+ * sam3_hip_matmul (same bits). The f16 copy of f32/bf16 activations goes
+ * to a fixed scratch array of 48 MiB that the library keeps on each
+ * device until the process ends; a problem needing more (M * K * 2 bytes
+ * plus 4 per row) fails with SAM3_EINVAL before any launch. No hipMalloc,
+ * hipFree or other allocation happens. Calls that overlap on one device
+ * (from two threads or on two streams) share the array and race.
+ * No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops).
+ * flags: SAM3_HIP_BIAS | SAM3_HIP_GELU (W is always [N,K]).
+ */
+enum sam3_error sam3_hip_matmul_q8_noalloc(int a_dtype, const void *a, const void *w, void *c,
+					   int M, int N, int K, const void *bias, int flags,
+					   void *stream);
+
 /* Which kernel sam3_hip_matmul would launch for this problem:
  * 1 = tiled MFMA, 2 = skinny (small-M Q8), 3 = generic, 0 = none. */
 int sam3_hip_matmul_path(int a_dtype, int b_dtype, int c_dtype,

@@ -242,6 +242,12 @@ struct s3h_settings {
 };
 const struct s3h_settings *s3h_settings(void);
 
+/* The fixed device scratch of sam3_hip_matmul_q8_noalloc (noalloc.hip):
+ * the current device's copy of a file-scope __device__ array, found with
+ * hipGetSymbolAddress on a device's first call and kept per device.
+ * *bytes is its size. Returns a hipError_t value. */
+int s3k_noalloc_scratch(void **ptr, size_t *bytes);
+
 #ifdef __cplusplus
 }
 #endif

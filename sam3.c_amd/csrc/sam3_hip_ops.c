@@ -269,22 +269,27 @@ static void fill_gemm(struct s3k_gemm *g, int a_dt, const void *a, int b_dt, con
  * the bias (S3K_EPI_ROWSCALE), which undoes the factor exactly. Slices
  * sharing their activations (batch stride 0) are copied once. *tmp gets
  * the scratch block, the caller's to free. */
-static enum sam3_error a_rows_f16(struct s3k_gemm *g, void **tmp, void *stream)
+static size_t a_rows_f16_bytes(const struct s3k_gemm *g, size_t *a_bytes)
+{
+	const int nb = g->batch > 1 && g->stride_a == 0 ? 1 : g->batch;
+	*a_bytes = ((size_t)nb * g->M * g->K * 2 + 255) & ~(size_t)255;
+	return *a_bytes + (size_t)nb * g->M * 4;
+}
+
+/* The copy into buf (a_rows_f16_bytes of g, 16-byte aligned). */
+static enum sam3_error a_rows_f16_into(struct s3k_gemm *g, void *buf, void *stream)
 {
 	const int shared = g->batch > 1 && g->stride_a == 0;
 	const int nb = shared ? 1 : g->batch;
-	const size_t a_bytes = ((size_t)nb * g->M * g->K * 2 + 255) & ~(size_t)255;
-	*tmp = NULL;
-	enum sam3_error err = s3h_scratch_alloc(tmp, a_bytes + (size_t)nb * g->M * 4, stream);
+	size_t a_bytes;
+	(void)a_rows_f16_bytes(g, &a_bytes);
+	float *rs = (float *)((char *)buf + a_bytes);
+	enum sam3_error err = s3h_hip(s3k_cast_f16_rows(g->a_kind, g->a, g->lda, g->stride_a, buf, rs,
+							nb, g->M, g->K, stream),
+				      "matmul activation cast");
 	if (err != SAM3_OK)
 		return err;
-	float *rs = (float *)((char *)*tmp + a_bytes);
-	err = s3h_hip(s3k_cast_f16_rows(g->a_kind, g->a, g->lda, g->stride_a, *tmp, rs, nb, g->M,
-					g->K, stream),
-		      "matmul activation cast");
-	if (err != SAM3_OK)
-		return err;
-	g->a = *tmp;
+	g->a = buf;
 	g->a_kind = S3K_F16;
 	g->lda = g->K;
 	g->stride_a = shared ? 0 : (long long)g->M * g->K;
@@ -292,6 +297,16 @@ static enum sam3_error a_rows_f16(struct s3k_gemm *g, void **tmp, void *stream)
 	g->rs_sb = shared ? 0 : g->M;
 	g->flags |= S3K_EPI_ROWSCALE;
 	return SAM3_OK;
+}
+
+static enum sam3_error a_rows_f16(struct s3k_gemm *g, void **tmp, void *stream)
+{
+	size_t a_bytes;
+	*tmp = NULL;
+	enum sam3_error err = s3h_scratch_alloc(tmp, a_rows_f16_bytes(g, &a_bytes), stream);
+	if (err != SAM3_OK)
+		return err;
+	return a_rows_f16_into(g, *tmp, stream);
 }
 
 /* Whether kernel path `path` of g rounds f32/bf16 activations to f16. */
@@ -859,6 +874,65 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 			return err;
 	}
 	return SAM3_OK;
+}
+
+/* sam3_hip_matmul for Q8_0 weights [N,K] without any allocation: the
+ * row-scaled f16 copy of the activations that the MFMA and GEMV kernels
+ * read goes to the library's fixed per-device scratch array
+ * (s3k_noalloc_scratch), and the Q8_0 weights are read in place (never
+ * expanded). The same kernels as sam3_hip_matmul run, in the same order,
+ * so the results have the same bits. Calls that overlap on one device
+ * (two threads, or two streams) share the array and race. */
+enum sam3_error sam3_hip_matmul_q8_noalloc(int a_dtype, const void *a, const void *w, void *c,
+					   int M, int N, int K, const void *bias, int flags,
+					   void *stream)
+{
+	if (M < 0 || N < 0 || K < 0) {
+		s3h_error("matmul_q8_noalloc: negative size M=%d N=%d K=%d", M, N, K);
+		return SAM3_EINVAL;
+	}
+	if (M == 0 || N == 0)
+		return SAM3_OK;
+	if (!a || !w || !c || ((flags & SAM3_HIP_BIAS) && !bias)) {
+		s3h_error("matmul_q8_noalloc: NULL pointer");
+		return SAM3_EINVAL;
+	}
+	if (!is_float_dtype(a_dtype)) {
+		s3h_error("matmul_q8_noalloc: unsupported activation dtype %d", a_dtype);
+		return SAM3_EDTYPE;
+	}
+	if (K % 32) {
+		s3h_error("matmul_q8_noalloc: K=%d is not a multiple of 32 (W must be whole Q8_0 "
+			  "blocks per row)", K);
+		return SAM3_EINVAL;
+	}
+	flags = (flags & (SAM3_HIP_BIAS | SAM3_HIP_GELU)) | SAM3_HIP_B_NT;
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dtype, a, SAM3_DTYPE_Q8_0, w, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
+	const int path = s3k_gemm_path(&g);
+	if (path == S3K_PATH_NONE) {
+		s3h_error("matmul_q8_noalloc: no kernel for M=%d N=%d K=%d", M, N, K);
+		return SAM3_EINVAL;
+	}
+	if (!rounds_a_to_f16(&g, path))
+		return s3h_hip(s3k_gemm_launch_path(&g, path, stream), "matmul_q8_noalloc");
+	size_t a_bytes, cap = 0;
+	const size_t need = a_rows_f16_bytes(&g, &a_bytes);
+	void *buf = NULL;
+	enum sam3_error err = s3h_hip(s3k_noalloc_scratch(&buf, &cap), "matmul_q8_noalloc: scratch");
+	if (err != SAM3_OK)
+		return err;
+	if (need > cap) {
+		s3h_error("matmul_q8_noalloc: M=%d K=%d needs %zu bytes of scratch for the f16 "
+			  "activations, more than the %zu the library holds per device", M, K, need,
+			  cap);
+		return SAM3_EINVAL;
+	}
+	struct s3k_gemm h = g;
+	err = a_rows_f16_into(&h, buf, stream);
+	if (err != SAM3_OK)
+		return err;
+	return s3h_hip(s3k_gemm_launch_path(&h, path, stream), "matmul_q8_noalloc");
 }
 
 /* ------------------------------------------------------------------ */

@@ -53,6 +53,7 @@ SIGNATURES = {
     "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),
     "sam3_hip_matmul_q8_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll,
                                         _vp, _i, _vp]),
+    "sam3_hip_matmul_q8_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_sdpa": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "sam3_hip_sdpa_on_path": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "sam3_hip_q8_quantize": (_i, [_vp, _vp, _i, _vp]),
