@@ -192,6 +192,19 @@ enum sam3_error sam3_hip_kernel_slice(const struct sam3_node *node, void *stream
 enum sam3_error sam3_hip_kernel_transpose(const struct sam3_node *node, void *stream);
 enum sam3_error sam3_hip_kernel_reshape(const struct sam3_node *node);
 
+/* CAST between F32, F16 and BF16: replaces cpu_kernel_cast
+ * (src/backend/cpu/kernels/cpu_cast.c:162-215; the fp16/bf16 converters
+ * of src/core/half.h:58-210). params[0] = target dtype, which must be the
+ * output's (else SAM3_EINVAL); the same dtype is a copy; other pairs are
+ * SAM3_EDTYPE. Bit-exact with half.h, NaN payloads included. */
+enum sam3_error sam3_hip_kernel_cast(const struct sam3_node *node, void *stream);
+/* The same on a forced conversion path: 1 = integer arithmetic (what
+ * sam3_hip_kernel_cast runs), 2 = the hardware conversion instructions
+ * the GEMM epilogues round with (v_cvt_pk_bf16_f32, v_cvt_f16_f32,
+ * v_cvt_f32_f16). No reference counterpart: it exists to check those
+ * instructions against half.h. */
+enum sam3_error sam3_hip_cast_on_path(int path, const struct sam3_node *node, void *stream);
+
 /*
  * CONV2D node kernel: cpu_kernel_conv2d (src/backend/cpu/kernels/
  * cpu_conv2d.c:296-435) and its twins cpu_kernel_conv2d_f16 / _bf16

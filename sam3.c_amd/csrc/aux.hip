@@ -268,6 +268,34 @@ __global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long lon
 	}
 }
 
+/* CAST between f32, f16 and bf16 (cpu_cast.c:26-145): one element per
+ * thread and step. HW = false converts by integer arithmetic, bit-exact
+ * with half.h; HW = true uses the conversion instructions the GEMM
+ * epilogues use (v_cvt_pk_bf16_f32, v_cvt_f16_f32, v_cvt_f32_f16). */
+template <int SRC, int DST, bool HW>
+__global__ void __launch_bounds__(256) cast_k(const void *src, void *dst, long long n)
+{
+	const long long stride = (long long)gridDim.x * 256;
+	for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+		float v;
+		if constexpr (SRC == S3K_F32) {
+			v = ((const float *)src)[i];
+		} else {
+			const uint32_t h = ((const uint16_t *)src)[i];
+			if constexpr (SRC == S3K_BF16)
+				v = bf16_to_f32(h);
+			else
+				v = HW ? f16_to_f32(h) : f16_to_f32_sw(h);
+		}
+		if constexpr (DST == S3K_F32)
+			((float *)dst)[i] = v;
+		else if constexpr (DST == S3K_BF16)
+			((uint16_t *)dst)[i] = (uint16_t)(HW ? pack_bf16x2(v, 0.0f) & 0xFFFFu : f32_to_bf16(v));
+		else
+			((uint16_t *)dst)[i] = (uint16_t)(HW ? f32_to_f16(v) : f32_to_f16_sw(v));
+	}
+}
+
 template <int KIND>
 __global__ void __launch_bounds__(256) bias_add_k(const void *x, const void *bias, void *out,
 						  long long rows, int n)
@@ -467,6 +495,35 @@ extern "C" int s3k_cast_f16_rows(int kind, const void *src, long long lda, long 
 					 batch, M, K, vec, st)
 		: cast_rows_launch<false>((const char *)src, lda * es, sa * es, (uint16_t *)dst, rs,
 					  batch, M, K, vec, st);
+}
+
+template <int SRC, int DST>
+static void cast_launch(const void *src, void *dst, long long n, bool hw, hipStream_t st)
+{
+	const long long blocks = (n + 255) / 256;
+	const dim3 grid((unsigned)(blocks < 16384 ? blocks : 16384));
+	if (hw)
+		hipLaunchKernelGGL((cast_k<SRC, DST, true>), grid, dim3(256), 0, st, src, dst, n);
+	else
+		hipLaunchKernelGGL((cast_k<SRC, DST, false>), grid, dim3(256), 0, st, src, dst, n);
+}
+
+extern "C" int s3k_cast(int src_kind, int dst_kind, const void *src, void *dst, long long n, int hw,
+			void *stream)
+{
+	if (n <= 0)
+		return 0;
+	const hipStream_t st = (hipStream_t)stream;
+	switch (src_kind * 8 + dst_kind) {
+	case S3K_F32 * 8 + S3K_F16:  cast_launch<S3K_F32, S3K_F16>(src, dst, n, hw, st); break;
+	case S3K_F32 * 8 + S3K_BF16: cast_launch<S3K_F32, S3K_BF16>(src, dst, n, hw, st); break;
+	case S3K_F16 * 8 + S3K_F32:  cast_launch<S3K_F16, S3K_F32>(src, dst, n, hw, st); break;
+	case S3K_F16 * 8 + S3K_BF16: cast_launch<S3K_F16, S3K_BF16>(src, dst, n, hw, st); break;
+	case S3K_BF16 * 8 + S3K_F32: cast_launch<S3K_BF16, S3K_F32>(src, dst, n, hw, st); break;
+	case S3K_BF16 * 8 + S3K_F16: cast_launch<S3K_BF16, S3K_F16>(src, dst, n, hw, st); break;
+	default: return (int)hipErrorInvalidValue;
+	}
+	return (int)hipGetLastError();
 }
 
 extern "C" int s3k_bias_add(int kind, const void *x, const void *bias, void *out,

@@ -107,6 +107,11 @@ int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N,
 /* Q8_0 quantize / dequantize of n f32 values (blocks over the flat index). */
 int s3k_q8_quantize(const void *src, void *dst, int n, void *stream);
 int s3k_q8_dequantize(const void *src, void *dst, int n, void *stream);
+/* n values of kind src_kind -> dst_kind (F32, F16, BF16; kinds differ):
+ * hw 0 by integer arithmetic, bit-exact with sam3.c's half.h; hw 1 by
+ * the hardware conversions the GEMM epilogues use. */
+int s3k_cast(int src_kind, int dst_kind, const void *src, void *dst, long long n, int hw,
+	     void *stream);
 /* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
 int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
 /*

@@ -74,6 +74,56 @@ __device__ __forceinline__ uint32_t f32_to_f16(float f)
 	return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+/* IEEE binary16 <-> binary32 by integer arithmetic, bit-exact with
+ * sam3.c's scalar converters (src/core/half.h:58-161): RNE (for f16
+ * subnormals after the reference's truncating pre-shift); f32 NaN -> f16
+ * keeps the top mantissa bits and sets bit 0;
+ * f16 NaN -> f32 keeps the payload as is (no quieting). The hardware
+ * conversions (f32_to_f16 / f16_to_f32 above) agree on every finite
+ * value and infinity; NaN payloads may differ. */
+__device__ __forceinline__ uint32_t f32_to_f16_sw(float f)
+{
+	const uint32_t u = __float_as_uint(f);
+	const uint32_t sign = (u >> 16) & 0x8000u;
+	const uint32_t e8 = (u >> 23) & 0xFFu;
+	uint32_t m = u & 0x7FFFFFu;
+	if (e8 == 0xFFu)
+		return sign | 0x7C00u | (m ? (m >> 13) | 1u : 0u);
+	const int e = (int)e8 - 112; /* f16 biased exponent */
+	if (e >= 31)
+		return sign | 0x7C00u;
+	if (e <= 0) {
+		if (e < -10)
+			return sign;
+		/* subnormal: the mantissa with its leading one is first shifted
+		 * down by 1 - e (those bits are dropped, as the reference does),
+		 * then rounded to nearest even on its low 13 bits */
+		m = (m | 0x800000u) >> (1 - e);
+	}
+	const uint32_t rest = m & 0x1FFFu;
+	uint32_t q = m >> 13;
+	if (rest > 0x1000u || (rest == 0x1000u && (q & 1u)))
+		++q;
+	/* a carry out of the mantissa moves into the exponent (and from the
+	 * largest finite value to infinity) by itself */
+	return sign | (e > 0 ? (((uint32_t)e << 10) + q) : q);
+}
+
+__device__ __forceinline__ float f16_to_f32_sw(uint32_t h)
+{
+	const uint32_t sign = (h & 0x8000u) << 16;
+	const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+	if (e == 0x1Fu)
+		return __uint_as_float(sign | 0x7F800000u | (m << 13));
+	if (e)
+		return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+	if (!m)
+		return __uint_as_float(sign);
+	/* subnormal: m * 2^-24, normalized by the leading one's position */
+	const int lz = __builtin_clz(m) - 21; /* shifts that bring its top bit to bit 10 */
+	return __uint_as_float(sign | ((uint32_t)(113 - lz) << 23) | (((m << lz) & 0x3FFu) << 13));
+}
+
 __device__ __forceinline__ float round_bf16(float f)
 {
 	return bf16_to_f32(f32_to_bf16(f));

@@ -1117,6 +1117,8 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 		err = s3h_bias_add(&dn, hb->stream);
 	else if (n->op == SAM3_OP_MAXPOOL2D)
 		err = s3h_maxpool2d(&dn, hb->stream);
+	else if (n->op == SAM3_OP_CAST)
+		err = sam3_hip_kernel_cast(&dn, hb->stream);
 	else
 		err = s3h_transpose(&dn, hb->stream);
 	if (err == SAM3_OK)
@@ -1150,6 +1152,8 @@ static int runs_on_gpu(const struct sam3_node *n)
 		return s3h_layernorm_ok(n);
 	case SAM3_OP_SLICE:
 		return s3h_slice_ok(n);
+	case SAM3_OP_CAST:
+		return s3h_cast_ok(n);
 	default:
 		return 0;
 	}

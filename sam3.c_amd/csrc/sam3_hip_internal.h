@@ -46,6 +46,7 @@ enum sam3_error s3h_layernorm(const struct sam3_node *node, void *stream);
 int s3h_rope_ok(const struct sam3_node *node);
 enum sam3_error s3h_rope(const struct sam3_node *node, void *stream);
 int s3h_slice_ok(const struct sam3_node *node);
+int s3h_cast_ok(const struct sam3_node *node);
 enum sam3_error s3h_slice(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_reshape(const struct sam3_node *node);
 /* Whether sam3_hip_kernel_sdpa takes this node (dtypes, ranks, head_dim). */

@@ -1139,6 +1139,67 @@ enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream)
 				node->output->data, n, stream), "gelu");
 }
 
+/* CAST (cpu_kernel_cast, cpu_cast.c:162-215): params[0] is the target
+ * dtype and must be the output's; the same dtype is a copy; f32, f16 and
+ * bf16 convert into each other. hw 0 converts bit-exactly as half.h
+ * does; hw 1 with the hardware conversion instructions. */
+int s3h_cast_ok(const struct sam3_node *node)
+{
+	if (node->n_inputs < 1 || !node->inputs[0] || !node->output)
+		return 0;
+	const int src = node->inputs[0]->dtype, dst = node->params[0];
+	return dst == (int)node->output->dtype && is_float_dtype(src) && is_float_dtype(dst) &&
+	       s3h_nelems(node->output) == s3h_nelems(node->inputs[0]);
+}
+
+static enum sam3_error cast_run(const struct sam3_node *node, int hw, void *stream)
+{
+	if (!node || node->n_inputs < 1 || !node->inputs[0] || !node->output) {
+		s3h_error("cast: NULL tensor");
+		return SAM3_EINVAL;
+	}
+	const int src = node->inputs[0]->dtype, dst = node->params[0];
+	if (dst != (int)node->output->dtype) {
+		s3h_error("cast: output dtype %d != params[0] %d", node->output->dtype, dst);
+		return SAM3_EINVAL;
+	}
+	const long long n = s3h_nelems(node->inputs[0]);
+	if (s3h_nelems(node->output) != n) {
+		s3h_error("cast: output has %lld elements, input %lld", s3h_nelems(node->output), n);
+		return SAM3_EINVAL;
+	}
+	if (n > 0 && (!node->inputs[0]->data || !node->output->data)) {
+		s3h_error("cast: tensor without data");
+		return SAM3_EINVAL;
+	}
+	if (src == dst)
+		return n > 0 ? s3h_hip(hipMemcpyAsync(node->output->data, node->inputs[0]->data,
+						      (size_t)n * s3h_dtype_size(src),
+						      hipMemcpyDeviceToDevice, (hipStream_t)stream),
+				       "cast (copy)")
+			     : SAM3_OK;
+	if (!is_float_dtype(src) || !is_float_dtype(dst)) {
+		s3h_error("cast: unsupported %d -> %d", src, dst);
+		return SAM3_EDTYPE;
+	}
+	return s3h_hip(s3k_cast(src, dst, node->inputs[0]->data, node->output->data, n, hw, stream),
+		       "cast");
+}
+
+enum sam3_error sam3_hip_kernel_cast(const struct sam3_node *node, void *stream)
+{
+	return cast_run(node, 0, stream);
+}
+
+enum sam3_error sam3_hip_cast_on_path(int path, const struct sam3_node *node, void *stream)
+{
+	if (path != 1 && path != 2) {
+		s3h_error("cast: unknown path %d", path);
+		return SAM3_EINVAL;
+	}
+	return cast_run(node, path == 2, stream);
+}
+
 /* TRANSPOSE of the last two dims (params all zero, or the permutation
  * that swaps the last two axes; cpu_transpose.c:330-348). Other
  * permutations are not run here. */
@@ -2021,6 +2082,10 @@ enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *strea
 		return SAM3_EDTYPE;
 	}
 	switch (node->op) {
+	case SAM3_OP_CAST:
+		if (is_float_dtype(dtype))
+			return sam3_hip_kernel_cast(node, stream);
+		break;
 	case SAM3_OP_MATMUL:
 		switch (dtype) {
 		case SAM3_DTYPE_F32:  return sam3_hip_kernel_matmul(node, stream);

@@ -48,6 +48,8 @@ SIGNATURES = {
     "sam3_hip_kernel_slice": (_i, [_vp, _vp]),
     "sam3_hip_kernel_transpose": (_i, [_vp, _vp]),
     "sam3_hip_kernel_reshape": (_i, [_vp]),
+    "sam3_hip_kernel_cast": (_i, [_vp, _vp]),
+    "sam3_hip_cast_on_path": (_i, [_i, _vp, _vp]),
     "sam3_hip_dispatch_node": (_i, [_vp, _vp]),
     "sam3_hip_matmul": (_i, [_i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i, _vp]),
     "sam3_hip_matmul_batched": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _ll, _ll, _ll, _i, _vp]),
