@@ -654,3 +654,79 @@ def test_blocks_chained_across_evals():
     back, _, _ = two_graphs(False)
     assert np.array_equal(fwd.view(np.uint32), one.view(np.uint32))
     assert np.array_equal(back.view(np.uint32), one.view(np.uint32))
+
+
+def _block_full(wkind, seed, deq_ref=False):
+    """The windowed ViT-L block at its production shape (grid 72, window
+    24, e 1024, 16 heads, MLP 4096), f32 or Q8_0 linear weights (the
+    reference graph gets the dequantized Q8_0 weights in f32: its own Q8
+    path through gh_linear's transpose is a no-op, cpu_transpose.c:
+    355-366)."""
+    O = oracle()
+    grid, window, e, heads, mlp = 72, 24, 1024, 16, 4096
+    G = graph.Graph()
+    x = G.tensor(abi.F32, (grid * grid, e), synth.randn(seed, (grid * grid, e)), ephemeral=1)
+    p = {}
+    shapes = {"ln1_w": ((e,), 1.0), "ln1_b": ((e,), 0.1), "qkv_w": ((3 * e, e), 0.05),
+              "qkv_b": ((3 * e,), 0.02), "proj_w": ((e, e), 0.05), "proj_b": ((e,), 0.02),
+              "ln2_w": ((e,), 1.0), "ln2_b": ((e,), 0.1), "fc1_w": ((mlp, e), 0.05),
+              "fc1_b": ((mlp,), 0.02), "fc2_w": ((e, mlp), 0.05), "fc2_b": ((e,), 0.02)}
+    for i, (name, (shape, std)) in enumerate(shapes.items()):
+        w = synth.randn(seed + 100 + i, shape, std)
+        if len(shape) == 2 and wkind == "q8":
+            blocks = O.q8_quantize(w)
+            if deq_ref:
+                p[name] = G.tensor(abi.F32, shape, O.q8_dequantize(blocks, w.size).reshape(shape))
+            else:
+                p[name] = G.tensor(abi.Q8_0, shape, blocks)
+        else:
+            p[name] = G.tensor(abi.F32, shape, w)
+    c, s = graph.rope_tables(window, e // heads)
+    tc, ts = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s.shape, s)
+    out = graph.vit_block(G, x, p, heads, grid, window, False, tc, ts)
+    return G, out
+
+
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_vit_block_full_size_windowed(env, wkind):
+    """The production windowed block (5184 tokens, the SLOTS = 4 LayerNorm
+    and the g = 24 row maps): the default run is bit-identical to the run
+    with the partition and unpartition folds off, and matches the
+    reference's CPU kernels run over the same graph."""
+    from oracle_bind import Ref, have_ref
+    if not have_ref():
+        pytest.skip("oracle/_ref not built")
+    M, e = 72 * 72, 1024
+
+    def gpu_run(fold):
+        for name in ("SAM3_HIP_PARTITION_FOLD", "SAM3_HIP_UNPARTITION_FOLD"):
+            if fold:
+                env.unset(name)
+            else:
+                env.set(name, "0")
+        G, out = _block_full(wkind, 470)
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+            assert st.host_nodes == 0
+            return out_array(out, (M, e)), st
+        finally:
+            be.close()
+
+    y, st = gpu_run(True)
+    y0, st0 = gpu_run(False)
+    assert st.gpu_nodes < st0.gpu_nodes, "the folds did not apply"
+    assert np.array_equal(y.view(np.uint32), y0.view(np.uint32))
+    Gr, orf = _block_full(wkind, 470, deq_ref=True)
+    R = Ref()
+    assert reference_eval(R, Gr.g, R.pool(0)) == 0
+    ref = out_array(orf, (M, e))
+    R.close()
+    # Q8_0: each of the block's five chained GEMMs (qkv, proj, fc1, fc2 and
+    # the attention it feeds) rounds its activations and q*scale to f16,
+    # about 3e-4 normwise each; the block output keeps the 1e-3 normwise
+    # bound and cosine, with an elementwise floor of 1.5e-2 * rms(ref)
+    # (2e-3 for the f32 weights)
+    assert_f32_close(y, ref, floor=1.5e-2 if wkind == "q8" else 2e-3,
+                     what=f"full-size windowed block {wkind}")
