@@ -173,6 +173,220 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
 	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
+/*
+ * gemm_dlp: the same GEMM for K % 64 == 0 with a software pipeline that
+ * keeps the matrix cores fed across k-steps (BK 64, two LDS stages).
+ *   - LDS holds [A stage 0 | A stage 1 | B stage 0 | B stage 1], so every
+ *     fragment read is one of eight per-lane base registers plus an
+ *     immediate (the swizzle of fragment i is that of fragment 0 with the
+ *     chunk's bit 2 flipped when i is odd).
+ *   - Sub-steps 0-2 of a k-step read the next sub-step's fragments while
+ *     their MFMAs issue. Before sub-step 3 a wave waits for its own LDS
+ *     reads and for the next stage's DMA, and the workgroup meets at the
+ *     barrier; the MFMAs issued before it keep the matrix pipe busy. Then
+ *     sub-step 3's MFMAs issue together with the next stage's first
+ *     fragment reads and the DMA of k-step kt + 2 into the stage every
+ *     wave has just finished reading (INTER: one read or DMA after each
+ *     MFMA; else grouped after them).
+ *   - The steady-state loop has no branches: the last two k-steps are
+ *     peeled.
+ * Same per-element accumulation order as gemm_dl, so the same bits.
+ */
+typedef unsigned lds_u4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const lds_u4v lds_cu4;
+
+__device__ __forceinline__ uint4 lds_rd16(unsigned base, unsigned off)
+{
+	const lds_u4v v = *(lds_cu4 *)(size_t)(base + off);
+	return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
+{
+	constexpr int NW = WGM * WGN, BK = 64, CPR = 8;
+	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2; /* one stage */
+	constexpr int B_BASE = 2 * A_BYTES, LDS_BYTES = 2 * (A_BYTES + B_BYTES);
+	static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "loads split evenly over waves");
+	constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW, LOADS = A_PER + B_PER;
+	constexpr int WTM = BM / WGM, WTN = BN / WGN;
+	constexpr int FM = WTM / 32, FN = WTN / 32, NMF = FM * FN, NRD = FM + FN;
+	static_assert(A_BYTES + (FM - 1) * 4096 < 65536 && B_BYTES + (FN - 1) * 4096 < 65536,
+		      "fragment offsets fit the LDS instruction's immediate");
+	static_assert(NW * 32 * (WTN + 8) * 4 <= LDS_BYTES, "epilogue staging fits");
+	__shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
+
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+	const int bz = blockIdx.y;
+	const unsigned lds0 = lds_addr_of(smem);
+	int tm, tn;
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+
+	/* per-lane source of DMA instruction t (A rows first, then B); rows
+	 * past M / N read zeros */
+	unsigned off[LOADS];
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t) {
+		const bool isa = t < A_PER;
+		const int s = ((isa ? t : t - A_PER) * NW + wave) * 64 + lane;
+		const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+		const int g = (isa ? tm * BM : tn * BN) + row;
+		off[t] = g < (isa ? p.M : p.N) ? (unsigned)(g * (isa ? p.lda_b : p.ldb_b) + c * 16)
+					       : S3K_OOB;
+	}
+	auto dma = [&](int kt, int t, int stg) {
+		if (t < A_PER)
+			dma16s(lds0 + (unsigned)(stg * A_BYTES + (t * NW + wave) * 1024), ra, off[t],
+			       (unsigned)(kt * BK * 2));
+		else
+			dma16s(lds0 + (unsigned)(B_BASE + stg * B_BYTES + ((t - A_PER) * NW + wave) * 1024),
+			       rb, off[t], (unsigned)(kt * BK * 2));
+	};
+
+	unsigned abase[4], bbase[4];
+	{
+		const int l32 = lane & 31, h = lane >> 5, r0 = wm0 + l32, r1 = wn0 + l32;
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks) {
+			abase[ks] = lds0 + (unsigned)((r0 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r0))) << 4);
+			bbase[ks] = lds0 + B_BASE +
+				    (unsigned)((r1 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r1))) << 4);
+		}
+	}
+
+	s3k_f32x16 acc[FM][FN];
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+
+	uint4 af[2][FM], bf[2][FN];
+	/* read r of a sub-step: the FM A fragments, then the FN B fragments */
+	auto frag = [&](int buf, int stg, int ks, int r) {
+		if (r < FM)
+			af[buf][r] = lds_rd16(abase[ks ^ (2 * (r & 1))], (unsigned)(stg * A_BYTES + r * 4096));
+		else
+			bf[buf][r - FM] = lds_rd16(bbase[ks ^ (2 * ((r - FM) & 1))],
+						   (unsigned)(stg * B_BYTES + (r - FM) * 4096));
+	};
+
+	/* k-step kt from stage stg; next: a k-step follows; dmak: issue the
+	 * DMA of k-step kt + 2 into stg */
+	auto step = [&](int stg, int kt, bool next, bool dmak) {
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks) {
+			const int cur = ks & 1, nxt = cur ^ 1;
+			if (ks == 3) {
+				__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): own reads done */
+				if (next) {
+					wait_vm<0>();
+					wg_barrier();
+				}
+			}
+			__builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+			for (int m = 0; m < NMF; ++m) {
+				mfma_chunk<FAM>(acc[m / FN][m % FN], af[cur][m / FN], bf[cur][m % FN]);
+				if (INTER) {
+					if (ks < 3) {
+						if (m < NRD)
+							frag(nxt, stg, ks + 1, m);
+					} else {
+						if (next && m < NRD)
+							frag(0, stg ^ 1, 0, m);
+						if (dmak && m < LOADS)
+							dma(kt + 2, m, stg);
+					}
+					__builtin_amdgcn_sched_barrier(0);
+				}
+			}
+			const int r0 = INTER ? NMF : 0;
+#pragma unroll
+			for (int r = r0; r < NRD; ++r) {
+				if (ks < 3)
+					frag(nxt, stg, ks + 1, r);
+				else if (next)
+					frag(0, stg ^ 1, 0, r);
+			}
+			if (ks == 3 && dmak) {
+#pragma unroll
+				for (int t = r0; t < LOADS; ++t)
+					dma(kt + 2, t, stg);
+			}
+		}
+	};
+
+	const int nk = p.K / BK;
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t)
+		dma(0, t, 0);
+	if (nk > 1) {
+#pragma unroll
+		for (int t = 0; t < LOADS; ++t)
+			dma(1, t, 1);
+		wait_vm<LOADS>();
+	} else {
+		wait_vm<0>();
+	}
+	wg_barrier();
+#pragma unroll
+	for (int r = 0; r < NRD; ++r)
+		frag(0, 0, 0, r);
+	int kt = 0;
+	for (; kt + 2 < nk; ++kt)
+		step(kt & 1, kt, true, true);
+	if (kt + 1 < nk) {
+		step(kt & 1, kt, true, false);
+		++kt;
+	}
+	step(kt & 1, kt, false, false);
+
+	__syncthreads();
+	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+}
+
+template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER>
+static void launch_dlp_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
+{
+	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	hipLaunchKernelGGL((gemm_dlp<BM, BN, WGM, WGN, FAM, CK, INTER>), grid, dim3(64 * WGM * WGN),
+			   0, st, p);
+}
+
+template <int BM, int BN, int WGM, int WGN, bool INTER, int FAM>
+static int launch_dlp_fam(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
+{
+	constexpr int SAME = FAM == FAM_BF16 ? S3K_BF16 : S3K_F16;
+	switch (g->c_kind) {
+	case S3K_F32:      launch_dlp_k<BM, BN, WGM, WGN, FAM, S3K_F32, INTER>(g, p, st); break;
+	case SAME:         launch_dlp_k<BM, BN, WGM, WGN, FAM, SAME, INTER>(g, p, st); break;
+	case S3K_C_F16OP:  launch_dlp_k<BM, BN, WGM, WGN, FAM, S3K_C_F16OP, INTER>(g, p, st); break;
+	case S3K_C_PLANES: launch_dlp_k<BM, BN, WGM, WGN, FAM, S3K_C_PLANES, INTER>(g, p, st); break;
+	default:           return (int)hipErrorInvalidValue;
+	}
+	return (int)hipGetLastError();
+}
+
+/* the pipelined kernel needs whole 64-k steps */
+template <int BM, int BN, int WGM, int WGN, bool INTER>
+static int launch_dlp_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	if (g->K % 64)
+		return (int)hipErrorInvalidValue;
+	p.tiles_m = (p.M + BM - 1) / BM;
+	p.tiles_n = (p.N + BN - 1) / BN;
+	if (g->a_kind == S3K_BF16)
+		return launch_dlp_fam<BM, BN, WGM, WGN, INTER, FAM_BF16>(g, p, st);
+	return launch_dlp_fam<BM, BN, WGM, WGN, INTER, FAM_F16>(g, p, st);
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int FAM, int CK, int OCC>
 static void launch_dl_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
 {
@@ -249,11 +463,17 @@ extern "C" int s3k_dl_eligible(const struct s3k_gemm *g)
 	return s3k_dl_ok(g) ? 1 : 0;
 }
 
-/* Tile shape, from measurements on the ViT-L shapes (bench-like data):
- *   - 256x256 (cfg 9, 8 waves, one workgroup per CU) when the problem is
- *     one nearly full round of 224..256 such tiles (qkv 5184x3072, 4096^2);
- *   - 192x128 (cfg 10, 8 waves, two workgroups per CU) when that gives
- *     at least 192 tiles (fc1, fc2, proj, batched attention);
+/* Tile shape, from measurements on the ViT-L shapes (bench data, one
+ * process, interleaved repetitions). With K % 64 == 0 the pipelined
+ * kernel (gemm_dlp) runs; it was 1-9 % faster than gemm_dl on every
+ * shape:
+ *   - 256x256 (cfg 20 / 9, 8 waves) when the problem is one nearly full
+ *     round of 224..256 such tiles (qkv 5184x3072: 32.1 against 33.3 us;
+ *     4096^3: 1266 against 1201 TFLOP/s);
+ *   - 192x256 (cfg 23, 8 waves) from 384 such tiles (fc1: 45.5 against
+ *     49.7 us for 192x128);
+ *   - 192x128 (cfg 24 / 10, 8 waves) when that gives at least 192 tiles
+ *     (fc2, proj, batched attention);
  *   - 128x128 (cfg 4, 4 waves) for mid-size problems, 64x64 (cfg 2) for
  *     small ones.
  * SAM3_HIP_DL_CFG forces a configuration (tuning and tests). */
@@ -271,10 +491,13 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	int cfg = s3h_settings()->dl_cfg;
 	if (cfg < 0) {
 		const long long t9 = dl_tiles(g, 256, 256), t10 = dl_tiles(g, 192, 128);
+		const bool pipe = g->K % 64 == 0;
 		if (t9 >= 224 && t9 <= 256)
-			cfg = 9;
+			cfg = pipe ? 20 : 9;
+		else if (pipe && dl_tiles(g, 192, 256) >= 384)
+			cfg = 23;
 		else if (t10 >= 192)
-			cfg = 10;
+			cfg = pipe ? 24 : 10;
 		else if (dl_tiles(g, 128, 128) >= 64)
 			cfg = 4;
 		else
@@ -295,6 +518,13 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 11: return launch_dl_cfg<256, 128, 64, 2, 4, 2, 1>(g, p, st);
 	case 12: return launch_dl_cfg<128, 256, 64, 2, 4, 2, 1>(g, p, st);
 	case 13: return launch_dl_cfg<256, 256, 32, 2, 4, 4, 1>(g, p, st);
+	case 20: return launch_dlp_cfg<256, 256, 2, 4, false>(g, p, st);
+	case 21: return launch_dlp_cfg<256, 256, 2, 4, true>(g, p, st);
+	case 22: return launch_dlp_cfg<192, 256, 2, 4, true>(g, p, st);
+	case 23: return launch_dlp_cfg<192, 256, 2, 4, false>(g, p, st);
+	case 24: return launch_dlp_cfg<192, 128, 2, 4, true>(g, p, st);
+	case 25: return launch_dlp_cfg<256, 192, 4, 2, true>(g, p, st);
+	case 26: return launch_dlp_cfg<128, 128, 2, 2, true>(g, p, st);
 	default: return (int)hipErrorInvalidValue;
 	}
 }

@@ -273,7 +273,7 @@ def test_fused_bias_gelu(kind):
          "f16": lambda g, r: assert_f16_close(g, r, what=f"fused {kind} {flags}")}[kind](c, ref)
 
 
-@pytest.mark.parametrize("cfg", list(range(13)))
+@pytest.mark.parametrize("cfg", list(range(14)))
 def test_dl_every_tile_config(env, cfg):
     """Each direct-to-LDS tile configuration (forced) on a ragged bf16 NT
     problem with a k tail, bias and GELU, against the oracle."""
@@ -288,6 +288,36 @@ def test_dl_every_tile_config(env, cfg):
                    flags=hip.B_NT | hip.BIAS | hip.GELU)
     ref = ref_linear("bf16", a, w, bias=bias, gelu=True, b_nt=True)
     assert_bf16_close(c, ref, what=f"dl cfg {cfg}")
+
+
+@pytest.mark.parametrize("cfg", [20, 21, 22, 23, 24, 25, 26])
+@pytest.mark.parametrize("K", [64, 128, 320])
+def test_dl_pipelined_every_tile_config(env, cfg, K):
+    """The pipelined direct-to-LDS kernel (K % 64 == 0: one, two and five
+    k-steps, so the peeled last steps and the steady-state loop both run)
+    on ragged M and N with bias and GELU, against the oracle, and with the
+    same bits as gemm_dl (same accumulation order)."""
+    O = oracle()
+    M, N = 300, 520
+    a = O.f32_to_bf16(rnd(213, (M, K))).reshape(M, K)
+    w = O.f32_to_bf16(rnd(214, (N, K), 0.05)).reshape(N, K)
+    bias = O.f32_to_bf16(rnd(215, N, 0.1))
+    flags = hip.B_NT | hip.BIAS | hip.GELU
+    env.set("SAM3_HIP_DL_CFG", str(cfg))
+    c = hip.matmul(a, abi.BF16, w, abi.BF16, abi.BF16, M, N, K, bias=bias, flags=flags)
+    assert_bf16_close(c, ref_linear("bf16", a, w, bias=bias, gelu=True, b_nt=True),
+                      what=f"dlp cfg {cfg} K={K}")
+    env.set("SAM3_HIP_DL_CFG", "4")
+    c4 = hip.matmul(a, abi.BF16, w, abi.BF16, abi.BF16, M, N, K, bias=bias, flags=flags)
+    assert np.array_equal(c, c4)
+    # f16 operands with an f32 output through the same kernels
+    env.set("SAM3_HIP_DL_CFG", str(cfg))
+    a16 = O.f32_to_fp16(rnd(216, (M, K))).reshape(M, K)
+    w16 = O.f32_to_fp16(rnd(217, (N, K), 0.05)).reshape(N, K)
+    c32 = hip.matmul(a16, abi.F16, w16, abi.F16, abi.F32, M, N, K, flags=hip.B_NT)
+    ref = (O.fp16_to_f32(a16).reshape(M, K).astype(np.float64) @
+           O.fp16_to_f32(w16).reshape(N, K).astype(np.float64).T)
+    assert_f32_close(c32, ref.astype(np.float32), what=f"dlp cfg {cfg} f16 K={K}")
 
 
 def test_bf16_output_f32():
