@@ -20,8 +20,41 @@
 
 namespace s3k {
 
-/* One thread per 2 outputs of f16 [N,K]; element (n,k) reads block
- * lin/32 of the flat Q8 array, lin = k*N+n (KN) or n*K+k (NK). */
+/* Q8_0 [N,K] blocks along k (K % 32 == 0, every row whole blocks) ->
+ * f16 [N,K]: one thread per block, its 36 bytes read as nine dwords and
+ * its 32 outputs (q * scale formed in f32, rounded once) stored as four
+ * 16-byte writes. */
+__global__ void __launch_bounds__(256) q8_expand_nk_k(const char *blk, uint16_t *out,
+						      long long nblk)
+{
+	const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+	if (b >= nblk)
+		return;
+	const uint32_t *w = (const uint32_t *)(blk + b * 36);
+	const float s = __uint_as_float(w[0]);
+	uint32_t q[8];
+#pragma unroll
+	for (int i = 0; i < 8; ++i)
+		q[i] = w[1 + i];
+	uint4 *o = (uint4 *)(out + b * 32);
+#pragma unroll
+	for (int c = 0; c < 4; ++c) {
+		uint32_t h[4];
+#pragma unroll
+		for (int e = 0; e < 4; ++e) {
+			const uint32_t d = q[2 * c + e / 2];
+			const int sh = 16 * (e & 1);
+			const float q0 = (float)(int)(int8_t)(d >> sh);
+			const float q1 = (float)(int)(int8_t)(d >> (sh + 8));
+			h[e] = f32_to_f16(q0 * s) | (f32_to_f16(q1 * s) << 16);
+		}
+		o[c] = make_uint4(h[0], h[1], h[2], h[3]);
+	}
+}
+
+/* One thread per output of f16 [N,K]; element (n,k) reads block lin/32
+ * of the flat Q8 array, lin = k*N+n (KN) or n*K+k (NK, rows that split
+ * blocks). */
 template <bool KN>
 __global__ void __launch_bounds__(256) q8_to_f16_nk(const char *blk, uint16_t *out, int K, int N)
 {
@@ -194,77 +227,94 @@ __device__ __forceinline__ float finite_abs(float x)
 	return a <= 3.402823466e38f ? a : 0.0f; /* inf and NaN do not set the scale */
 }
 
-template <bool BF16, bool VEC, int CPL>
+template <bool BF16, bool VEC, int CPL, int RPW>
 __global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long long lda_b,
 						       long long sa_b, uint16_t *dst, float *rs,
 						       int M, int K)
 {
 	const int lane = threadIdx.x & 63;
-	const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-	if (m >= M)
+	const int m0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+	if (m0 >= M)
 		return;
-	const long long row = (long long)blockIdx.y * M + m;
-	const char *x = src + (long long)blockIdx.y * sa_b + (long long)m * lda_b;
-	uint16_t *y = dst + row * K;
-	float amax = 0.0f;
+	const char *xb = src + (long long)blockIdx.y * sa_b;
 	if constexpr (VEC) {
 		constexpr int L = BF16 ? 1 : 2;
 		const int chunks = K / 8;
-		uint4 v[CPL][L];
+		/* every load of the wave's rows first (RPW * CPL * L per lane) */
+		uint4 v[RPW][CPL][L];
 #pragma unroll
-		for (int u = 0; u < CPL; ++u) {
-			const int c = lane + 64 * u;
+		for (int r = 0; r < RPW; ++r) {
+			const uint4 *x = (const uint4 *)(xb + (long long)(m0 + r) * lda_b);
 #pragma unroll
-			for (int l = 0; l < L; ++l)
-				v[u][l] = c < chunks ? ((const uint4 *)x)[c * L + l] : make_uint4(0, 0, 0, 0);
-		}
-		float f[CPL][8];
+			for (int u = 0; u < CPL; ++u) {
+				const int c = lane + 64 * u;
 #pragma unroll
-		for (int u = 0; u < CPL; ++u) {
-			if constexpr (BF16) {
-				const uint32_t w[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
-#pragma unroll
-				for (int e = 0; e < 4; ++e) {
-					f[u][2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
-					f[u][2 * e + 1] = bf16_to_f32(w[e] >> 16);
-				}
-			} else {
-#pragma unroll
-				for (int l = 0; l < 2; ++l) {
-					f[u][4 * l] = __uint_as_float(v[u][l].x);
-					f[u][4 * l + 1] = __uint_as_float(v[u][l].y);
-					f[u][4 * l + 2] = __uint_as_float(v[u][l].z);
-					f[u][4 * l + 3] = __uint_as_float(v[u][l].w);
-				}
+				for (int l = 0; l < L; ++l)
+					v[r][u][l] = (m0 + r < M && c < chunks) ? x[c * L + l]
+										 : make_uint4(0, 0, 0, 0);
 			}
-#pragma unroll
-			for (int e = 0; e < 8; ++e)
-				amax = fmaxf(amax, finite_abs(f[u][e]));
 		}
-		const int ex = row_scale_exp(amax);
-		const float inv = pow2f(-ex);
 #pragma unroll
-		for (int u = 0; u < CPL; ++u) {
-			const int c = lane + 64 * u;
-			if (c < chunks)
-				((uint4 *)y)[c] = make_uint4(pack_f16x2(f[u][0] * inv, f[u][1] * inv),
-							     pack_f16x2(f[u][2] * inv, f[u][3] * inv),
-							     pack_f16x2(f[u][4] * inv, f[u][5] * inv),
-							     pack_f16x2(f[u][6] * inv, f[u][7] * inv));
+		for (int r = 0; r < RPW; ++r) {
+			if (m0 + r >= M)
+				break;
+			float f[CPL][8];
+			float amax = 0.0f;
+#pragma unroll
+			for (int u = 0; u < CPL; ++u) {
+				if constexpr (BF16) {
+					const uint32_t w[4] = {v[r][u][0].x, v[r][u][0].y, v[r][u][0].z, v[r][u][0].w};
+#pragma unroll
+					for (int e = 0; e < 4; ++e) {
+						f[u][2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
+						f[u][2 * e + 1] = bf16_to_f32(w[e] >> 16);
+					}
+				} else {
+#pragma unroll
+					for (int l = 0; l < 2; ++l) {
+						f[u][4 * l] = __uint_as_float(v[r][u][l].x);
+						f[u][4 * l + 1] = __uint_as_float(v[r][u][l].y);
+						f[u][4 * l + 2] = __uint_as_float(v[r][u][l].z);
+						f[u][4 * l + 3] = __uint_as_float(v[r][u][l].w);
+					}
+				}
+#pragma unroll
+				for (int e = 0; e < 8; ++e)
+					amax = fmaxf(amax, finite_abs(f[u][e]));
+			}
+			const int ex = row_scale_exp(amax);
+			const float inv = pow2f(-ex);
+			const long long row = (long long)blockIdx.y * M + m0 + r;
+			uint16_t *y = dst + row * K;
+#pragma unroll
+			for (int u = 0; u < CPL; ++u) {
+				const int c = lane + 64 * u;
+				if (c < chunks)
+					((uint4 *)y)[c] = make_uint4(pack_f16x2(f[u][0] * inv, f[u][1] * inv),
+								     pack_f16x2(f[u][2] * inv, f[u][3] * inv),
+								     pack_f16x2(f[u][4] * inv, f[u][5] * inv),
+								     pack_f16x2(f[u][6] * inv, f[u][7] * inv));
+			}
+			if (lane == 0)
+				rs[row] = pow2f(ex);
 		}
-		if (lane == 0)
-			rs[row] = pow2f(ex);
 	} else {
-		for (int k = lane; k < K; k += 64)
-			amax = fmaxf(amax, finite_abs(BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
-							: ((const float *)x)[k]));
-		const int ex = row_scale_exp(amax);
-		const float inv = pow2f(-ex);
-		for (int k = lane; k < K; k += 64)
-			y[k] = (uint16_t)f32_to_f16((BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
-						     : ((const float *)x)[k]) * inv);
-		if (lane == 0)
-			rs[row] = pow2f(ex);
+		for (int r = 0; r < RPW && m0 + r < M; ++r) {
+			const char *x = xb + (long long)(m0 + r) * lda_b;
+			float amax = 0.0f;
+			for (int k = lane; k < K; k += 64)
+				amax = fmaxf(amax, finite_abs(BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+								: ((const float *)x)[k]));
+			const int ex = row_scale_exp(amax);
+			const float inv = pow2f(-ex);
+			const long long row = (long long)blockIdx.y * M + m0 + r;
+			uint16_t *y = dst + row * K;
+			for (int k = lane; k < K; k += 64)
+				y[k] = (uint16_t)f32_to_f16((BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+							     : ((const float *)x)[k]) * inv);
+			if (lane == 0)
+				rs[row] = pow2f(ex);
+		}
 	}
 }
 
@@ -371,8 +421,14 @@ extern "C" int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N, 
 	const long long tot = (long long)K * N;
 	if (tot <= 0)
 		return 0;
-	hipLaunchKernelGGL(q8_to_f16_nk<false>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
-			   (const char *)blocks, (uint16_t *)out, K, N);
+	if (K % 32 == 0 && !((uintptr_t)blocks & 3u) && !((uintptr_t)out & 15u)) {
+		const long long nblk = tot / 32;
+		hipLaunchKernelGGL(q8_expand_nk_k, grid1(nblk), dim3(256), 0, (hipStream_t)stream,
+				   (const char *)blocks, (uint16_t *)out, nblk);
+	} else {
+		hipLaunchKernelGGL(q8_to_f16_nk<false>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
+				   (const char *)blocks, (uint16_t *)out, K, N);
+	}
 	return (int)hipGetLastError();
 }
 
@@ -411,17 +467,20 @@ __global__ void __launch_bounds__(256) split3_bf16_k(const float *src, uint16_t 
 	const int k0 = (int)(t % per_row) * 8;
 	const float4 a = *(const float4 *)(src + r * ld + k0);
 	const float4 b = *(const float4 *)(src + r * ld + k0 + 4);
-	const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-	uint32_t hi[4], lo[4];
-#pragma unroll
-	for (int i = 0; i < 4; ++i)
-		split_bf16x2(x[2 * i], x[2 * i + 1], hi[i], lo[i]);
-	const uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-	const uint4 L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+	uint4 H, L;
+	split_bf16x2(a.x, a.y, H.x, L.x);
+	split_bf16x2(a.z, a.w, H.y, L.y);
+	split_bf16x2(b.x, b.y, H.z, L.z);
+	split_bf16x2(b.z, b.w, H.w, L.w);
 	uint16_t *d = dst + r * 3LL * K + k0;
 	*(uint4 *)d = H;
-	*(uint4 *)(d + K) = order == 0 ? L : H;
-	*(uint4 *)(d + 2LL * K) = order == 0 ? H : L;
+	if (order == 0) {
+		*(uint4 *)(d + K) = L;
+		*(uint4 *)(d + 2LL * K) = H;
+	} else {
+		*(uint4 *)(d + K) = H;
+		*(uint4 *)(d + 2LL * K) = L;
+	}
 }
 
 extern "C" int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld,
@@ -457,24 +516,30 @@ extern "C" int s3k_cast_f16(int kind, const void *src, void *dst, long long n, v
 	return (int)hipGetLastError();
 }
 
+/* Rows per wave: enough loads in flight per lane (RPW * CPL * L) to
+ * cover HBM latency, without leaving the chip half empty on small M. */
 template <bool BF16>
 static int cast_rows_launch(const char *src, long long lda_b, long long sa_b, uint16_t *dst,
 			    float *rs, int batch, int M, int K, bool vec, hipStream_t st)
 {
-	const dim3 grid((unsigned)((M + 3) / 4), (unsigned)batch);
 	const int cpl = (K / 8 + 63) / 64;
+	const int rpw = (!vec || cpl > 2 || (long long)M * batch < 4096) ? 1 : 4;
+	const dim3 grid((unsigned)((M + 4 * rpw - 1) / (4 * rpw)), (unsigned)batch);
 	if (!vec || cpl > 8)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, false, 1>), grid, dim3(256), 0, st, src, lda_b,
-				   sa_b, dst, rs, M, K);
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, false, 1, 1>), grid, dim3(256), 0, st, src,
+				   lda_b, sa_b, dst, rs, M, K);
+	else if (cpl <= 2 && rpw == 4)
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2, 4>), grid, dim3(256), 0, st, src,
+				   lda_b, sa_b, dst, rs, M, K);
 	else if (cpl <= 2)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2>), grid, dim3(256), 0, st, src, lda_b,
-				   sa_b, dst, rs, M, K);
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2, 1>), grid, dim3(256), 0, st, src,
+				   lda_b, sa_b, dst, rs, M, K);
 	else if (cpl <= 4)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 4>), grid, dim3(256), 0, st, src, lda_b,
-				   sa_b, dst, rs, M, K);
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 4, 1>), grid, dim3(256), 0, st, src,
+				   lda_b, sa_b, dst, rs, M, K);
 	else
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 8>), grid, dim3(256), 0, st, src, lda_b,
-				   sa_b, dst, rs, M, K);
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 8, 1>), grid, dim3(256), 0, st, src,
+				   lda_b, sa_b, dst, rs, M, K);
 	return (int)hipGetLastError();
 }
 

@@ -141,9 +141,83 @@ __device__ __forceinline__ bool f16_out_of_range(const float *x)
 	return mx > 0.0f && mx < 0x1p-10f;
 }
 
+/* The global inputs of one output chunk's epilogue (C[m][n..n+W-1]):
+ * bias and residual, each when its flag is set. */
+template <int W>
+struct EpiIn {
+	float b[W];
+	float f;
+	float r[W];
+};
+
+template <int W>
+__device__ __forceinline__ void epi_bias(const GemmArgs &p, int n, float *bv)
+{
+	const bool full = n + W <= p.N;
+#pragma unroll
+	for (int e = 0; e < W; ++e)
+		bv[e] = 0.f;
+	/* n is a multiple of W here: 16-byte (f32) or 8/16-byte (16-bit)
+	 * loads need only an aligned bias base */
+	const bool vec = full && (((uintptr_t)p.bias & 15u) == 0);
+	if (vec && p.bias_kind != S3K_F32) {
+		uint32_t d[W / 2];
+		if constexpr (W == 8) {
+			const uint4 w = *(const uint4 *)((const uint16_t *)p.bias + n);
+			d[0] = w.x; d[1] = w.y; d[2] = w.z; d[3] = w.w;
+		} else {
+			const uint2 w = *(const uint2 *)((const uint16_t *)p.bias + n);
+			d[0] = w.x; d[1] = w.y;
+		}
+#pragma unroll
+		for (int e = 0; e < W / 2; ++e) {
+			bv[2 * e] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] & 0xFFFFu)
+							     : f16_to_f32(d[e] & 0xFFFFu);
+			bv[2 * e + 1] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] >> 16)
+								 : f16_to_f32(d[e] >> 16);
+		}
+	} else if (vec) {
+#pragma unroll
+		for (int e = 0; e < W; e += 4) {
+			const float4 b = *(const float4 *)((const float *)p.bias + n + e);
+			bv[e] = b.x; bv[e + 1] = b.y; bv[e + 2] = b.z; bv[e + 3] = b.w;
+		}
+	} else {
+#pragma unroll
+		for (int e = 0; e < W; ++e)
+			if (n + e < p.N)
+				bv[e] = load_as_f32(p.bias, n + e, p.bias_kind);
+	}
+}
+
+/* Loads of chunk (m, n); the bias only when fetch_bias (else the caller
+ * filled it from registers it loaded once). */
+template <int W>
+__device__ __forceinline__ void epi_fetch(const GemmArgs &p, int m, int n, int bz, bool fetch_bias,
+					  EpiIn<W> &e)
+{
+	if (fetch_bias && (p.flags & S3K_EPI_BIAS))
+		epi_bias<W>(p, n, e.b);
+	if (p.flags & S3K_EPI_RES) {
+		/* the residual ADD node that follows, in f32 */
+		const float *r = (const float *)p.res + out_row(p, m) * p.ldr + n;
+		if (n + W <= p.N && (((uintptr_t)r & 15u) == 0)) {
+#pragma unroll
+			for (int q = 0; q < W; q += 4) {
+				const float4 v = *(const float4 *)(r + q);
+				e.r[q] = v.x; e.r[q + 1] = v.y; e.r[q + 2] = v.z; e.r[q + 3] = v.w;
+			}
+		} else {
+#pragma unroll
+			for (int q = 0; q < W; ++q)
+				e.r[q] = n + q < p.N ? r[q] : 0.0f;
+		}
+	}
+}
+
 template <int CK, bool EPI, int W>
-__device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int n, const float *v,
-				       int bz)
+__device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, int m, int n,
+				       const float *v, const EpiIn<W> &ein)
 {
 	typedef float f4v __attribute__((ext_vector_type(4)));
 	typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -156,70 +230,13 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, char *cb, int m, int 
 		x[e] = q.x; x[e + 1] = q.y; x[e + 2] = q.z; x[e + 3] = q.w;
 	}
 	if (EPI) {
-		if (p.flags & S3K_EPI_ROWSCALE) {
-			const float f = p.rs[(long long)bz * p.rs_sb + m];
+#pragma unroll
+		for (int e = 0; e < W; ++e)
+			x[e] = epilogue<CK>(x[e], ein.b[e], flags);
+		if (flags & S3K_EPI_RES) {
 #pragma unroll
 			for (int e = 0; e < W; ++e)
-				x[e] *= f;
-		}
-		float bv[W];
-#pragma unroll
-		for (int e = 0; e < W; ++e)
-			bv[e] = 0.f;
-		if (p.flags & S3K_EPI_BIAS) {
-			/* n is a multiple of W here: 16-byte (f32) or 8/16-byte
-			 * (16-bit) loads need only an aligned bias base */
-			const bool vec = full && (((uintptr_t)p.bias & 15u) == 0);
-			if (vec && p.bias_kind != S3K_F32) {
-				uint32_t d[W / 2];
-				if constexpr (W == 8) {
-					const uint4 w = *(const uint4 *)((const uint16_t *)p.bias + n);
-					d[0] = w.x; d[1] = w.y; d[2] = w.z; d[3] = w.w;
-				} else {
-					const uint2 w = *(const uint2 *)((const uint16_t *)p.bias + n);
-					d[0] = w.x; d[1] = w.y;
-				}
-#pragma unroll
-				for (int e = 0; e < W / 2; ++e) {
-					bv[2 * e] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] & 0xFFFFu)
-									     : f16_to_f32(d[e] & 0xFFFFu);
-					bv[2 * e + 1] = p.bias_kind == S3K_BF16 ? bf16_to_f32(d[e] >> 16)
-										 : f16_to_f32(d[e] >> 16);
-				}
-			} else if (vec) {
-#pragma unroll
-				for (int e = 0; e < W; e += 4) {
-					const float4 b = *(const float4 *)((const float *)p.bias + n + e);
-					bv[e] = b.x; bv[e + 1] = b.y; bv[e + 2] = b.z; bv[e + 3] = b.w;
-				}
-			} else {
-#pragma unroll
-				for (int e = 0; e < W; ++e)
-					if (full || n + e < p.N)
-						bv[e] = load_as_f32(p.bias, n + e, p.bias_kind);
-			}
-		}
-#pragma unroll
-		for (int e = 0; e < W; ++e)
-			x[e] = epilogue<CK>(x[e], bv[e], p.flags);
-		if (p.flags & S3K_EPI_RES) {
-			/* the residual ADD node that follows, in f32 */
-			const float *r = (const float *)p.res + out_row(p, m) * p.ldr + n;
-			if (full && (((uintptr_t)r & 15u) == 0)) {
-#pragma unroll
-				for (int e = 0; e < W; e += 4) {
-					const float4 q = *(const float4 *)(r + e);
-					x[e] = add_rn(x[e], q.x);
-					x[e + 1] = add_rn(x[e + 1], q.y);
-					x[e + 2] = add_rn(x[e + 2], q.z);
-					x[e + 3] = add_rn(x[e + 3], q.w);
-				}
-			} else {
-#pragma unroll
-				for (int e = 0; e < W; ++e)
-					if (n + e < p.N)
-						x[e] = add_rn(x[e], r[e]);
-			}
+				x[e] = add_rn(x[e], ein.r[e]);
 		}
 	}
 	const long long o = out_row(p, m) * p.ldc + n;
@@ -301,10 +318,51 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
 	static_assert(CK != S3K_C_PLANES || WTN % 8 == 0, "planes are written 8 outputs at a time");
-	const bool epi = (p.flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES | S3K_EPI_ROWSCALE)) != 0;
 	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
 	 * so consecutive lanes write consecutive 16 bytes of a row */
 	constexpr int W = CK == S3K_F32 ? 4 : 8;
+	/* when WTN / W divides 64, a lane keeps the same W columns for every
+	 * row it finishes: their bias is loaded once per tile */
+	constexpr bool FIXED = 64 % (WTN / W) == 0;
+	/* Global loads inside the store loops would be expensive: vmcnt counts
+	 * stores as well as loads, so the wait for a load issued after a store
+	 * also waits for that store. So the row factors are applied to the
+	 * accumulators and the bias is loaded before the first store; only the
+	 * residual (S3K_EPI_RES) is loaded inside a store loop. */
+	if (p.flags & S3K_EPI_ROWSCALE) {
+		/* lane l holds rows 8t + 4(l >> 5) + q (q < 4) of each 32-row strip */
+#pragma unroll
+		for (int i = 0; i < FM; ++i)
+#pragma unroll
+			for (int t = 0; t < 4; ++t) {
+				const int r0 = m0 + i * 32 + 8 * t + 4 * (lane >> 5);
+				const float *rp = p.rs + (long long)bz * p.rs_sb + r0;
+				float f[4];
+#pragma unroll
+				for (int q = 0; q < 4; ++q)
+					f[q] = r0 + q < p.M ? rp[q] : 1.0f;
+#pragma unroll
+				for (int j = 0; j < FN; ++j)
+#pragma unroll
+					for (int q = 0; q < 4; ++q)
+						acc[i][j][4 * t + q] *= f[q];
+			}
+	}
+	const int flags = p.flags & ~S3K_EPI_ROWSCALE;
+	const bool heavy = (flags & S3K_EPI_RES) || (!FIXED && (flags & S3K_EPI_BIAS));
+	const bool light = !heavy && (flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
+	EpiIn<W> ein;
+#pragma unroll
+	for (int q = 0; q < W; ++q) {
+		ein.b[q] = 0.f;
+		ein.r[q] = 0.f;
+	}
+	ein.f = 1.0f;
+	if (FIXED && (flags & S3K_EPI_BIAS)) {
+		const int cw = (lane % (WTN / W)) * W;
+		if (n0 + cw < p.N)
+			epi_bias<W>(p, n0 + cw, ein.b);
+	}
 #pragma unroll
 	for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -315,19 +373,32 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 					acc[i][j][r];
 		wave_lds_fence();
 		const int mrow = m0 + i * 32;
-		if (epi) {
+		if (heavy) {
+#pragma unroll 1
+			for (int s = lane; s < 32 * WTN / W; s += 64) {
+				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
+				if (mrow + row < p.M && n0 + cw < p.N) {
+					EpiIn<W> e = ein;
+					epi_fetch<W>(p, mrow + row, n0 + cw, bz, !FIXED, e);
+					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw,
+							     stg + row * PITCH + cw, e);
+				}
+			}
+		} else if (light) {
 #pragma unroll 1
 			for (int s = lane; s < 32 * WTN / W; s += 64) {
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
 				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, true, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw, bz);
+					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw,
+							     stg + row * PITCH + cw, ein);
 			}
 		} else {
 #pragma unroll 1
 			for (int s = lane; s < 32 * WTN / W; s += 64) {
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
 				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, false, W>(p, cb, mrow + row, n0 + cw, stg + row * PITCH + cw, bz);
+					finishw<CK, false, W>(p, flags, cb, mrow + row, n0 + cw,
+							      stg + row * PITCH + cw, ein);
 			}
 		}
 		wave_lds_fence();

@@ -509,7 +509,6 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 2:  return launch_dl_cfg<64, 64, 32, 2, 2, 3, 2, true>(g, p, st);
 	case 3:  return launch_dl_cfg<128, 256, 32, 2, 2, 3, 2>(g, p, st);
 	case 4:  return launch_dl_cfg<128, 128, 64, 2, 2, 2, 2, true>(g, p, st);
-	case 5:  return launch_dl_cfg<256, 256, 32, 2, 2, 4, 1>(g, p, st);
 	case 6:  return launch_dl_cfg<192, 256, 32, 2, 2, 4, 1>(g, p, st);
 	case 7:  return launch_dl_cfg<192, 256, 64, 2, 4, 2, 1>(g, p, st);
 	case 8:  return launch_dl_cfg<256, 256, 32, 2, 4, 3, 1>(g, p, st);

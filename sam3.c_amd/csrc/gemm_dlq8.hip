@@ -261,7 +261,6 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 1:  return launch_dlq8_cfg<256, 128, 2, 4, 3, 1>(g, p, st);
 	case 2:  return launch_dlq8_cfg<128, 128, 1, 4, 3, 2>(g, p, st);
 	case 3:  return launch_dlq8_cfg<128, 256, 1, 8, 3, 1>(g, p, st);
-	case 4:  return launch_dlq8_cfg<256, 256, 1, 8, 3, 1>(g, p, st);
 	case 5:  return launch_dlq8_cfg<256, 128, 1, 4, 3, 1>(g, p, st);
 	case 6:  return launch_dlq8_cfg<256, 128, 1, 4, 2, 1>(g, p, st);
 	case 7:  return launch_dlq8_cfg<32, 128, 1, 4, 3, 2>(g, p, st);
