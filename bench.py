@@ -19,6 +19,10 @@ reported under "extra":
 `roofline` is for the headline kernel; `cpu_baseline` times the reference
 CPU bf16 kernel (oracle/_ref, compiled from the reference's own sources)
 on the GPU box's host cores over a bounded row sample of the same GEMM.
+"q8" is the same kind of record for the Q8_0 path on config 3's fc1
+layer (bf16 activations x Q8_0 W[4096,1024], f32 out): its own value,
+roofline (f16 MFMA peak, with the f16 GEMM timed on its own as the
+dominant kernel) and the reference's Q8_0 CPU kernel as cpu_baseline.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -559,6 +563,110 @@ def measured_traffic(key):
         return None
 
 
+def q8_host_f16(wq, N, K):
+    """f16 bits of q * scale (f32 product, rounded once) for Q8_0 blocks
+    [N, K/32] x 36 bytes: the weight the per-call expansion hands the f16
+    GEMM (bench plumbing, to time that GEMM on its own)."""
+    blk = wq.reshape(N * K // 32, 36)
+    scale = blk[:, :4].copy().view(np.float32)
+    q = blk[:, 4:].view(np.int8).astype(np.float32)
+    return (q * scale).reshape(N, K).astype(np.float16).view(np.uint16)
+
+
+def q8_cpu_baseline(a32, N, K, target_s=10.0):
+    """The reference's Q8_0 kernel (cpu_kernel_matmul_q8 via oracle/_ref: f32
+    activations, Q8_0 weight [K,N] per its contract, f32 out) on all allowed
+    host cores, on a row sample of the Q8 fc1 GEMM sized to ~target_s s."""
+    from oracle_bind import Oracle, Ref, have_ref
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    wkn = hip.q8_quantize(synth.randn(synth.tensor_seed(7, 1), (K, N), 0.02))
+    if have_ref():
+        R, kind = Ref(), "reference"
+    else:
+        R, kind = Oracle(), "port"
+    fn = lambda a: R.matmul_q8(a, wkn, K, N, threads)  # noqa: E731
+    M = a32.shape[0]
+    probe = max(threads, 32)
+    t0 = time.perf_counter()
+    fn(a32[:probe])
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(min(M, max(probe, target_s / max(per_row, 1e-9))))
+    rows -= rows % threads if rows > threads else 0
+    t0 = time.perf_counter()
+    fn(a32[:rows])
+    dt = time.perf_counter() - t0
+    if kind == "reference":
+        R.close()
+    return {"value": round(tflops(rows, N, K, dt * 1e3), 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": kind,
+            "sample": f"Q8_0 matmul rows 0..{rows - 1} of {M} (x {N}x{K}), one call, {dt:.2f} s, "
+                      f"cpu_kernel_matmul_q8 (f32 activations, W [K,N]) with a "
+                      f"{threads}-thread pool"}
+
+
+def q8_record(stream, timer, a_bf, w32, steps, warmup, with_cpu):
+    """The Q8 line: BASELINE configs[2]'s fc1 layer GEMM, C[5184,4096] f32 =
+    A[5184,1024] bf16 x W[4096,1024] Q8_0, one sam3_hip_matmul per step
+    (row-scaled f16 copy of A, per-call f16 expansion of W, f16 MFMA GEMM).
+    The dominant kernel, the f16 GEMM, is also timed on its own: the same
+    kernel over f16 copies made beforehand."""
+    M, K = a_bf.shape
+    N = w32.shape[0]
+    wq = hip.q8_quantize(w32)
+    ms = gemm_case(stream, timer, abi.BF16, a_bf, abi.Q8_0, wq, abi.F32, M, N, K, hip.B_NT,
+                   steps, warmup)
+    value = tflops(M, N, K, ms)
+    a16 = f16_bits((a_bf.astype(np.uint32) << 16).view(np.float32))
+    w16 = q8_host_f16(wq, N, K)
+    ms_g = gemm_case(stream, timer, abi.F16, a16, abi.F16, w16, abi.F32, M, N, K, hip.B_NT,
+                     steps, warmup)
+    g = tflops(M, N, K, ms_g)
+    rec = {
+        "metric": "TFLOP/s, bf16 activations x Q8_0 weights 5184x1024x4096 (ViT-L fc1), "
+                  "f32 out",
+        "value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 5),
+        "steps": steps, "warmup": warmup, "dtype": "f16 MFMA (bf16 A and Q8_0 W rounded to f16 "
+                                                     "once), f32 accumulate",
+        "config": {"workload": "BASELINE configs[2] fc1: C[5184,4096] f32 = A[5184,1024] bf16 x "
+                               "W[4096,1024]^T Q8_0 (36-byte blocks along K), one "
+                               "sam3_hip_matmul per step", "M": M, "N": N, "K": K},
+        "roofline": {"bound": "mfma", "achieved": round(value, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(value / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("q8_fc1_f16_gemm_5184x4096x1024"),
+                     "dominant_kernel": {
+                         "kernel": "f16 GEMM on the expanded weight (f32 out)",
+                         "us": round(ms_g * 1e3, 2), "tflops": round(g, 2),
+                         "frac": round(g / PEAK_BF16_TFLOPS, 4)},
+                     "other_kernels_us": round((ms - ms_g) * 1e3, 2)},
+    }
+    if with_cpu:
+        log("cpu baseline (reference Q8_0 kernel, row sample)")
+        rec["cpu_baseline"] = q8_cpu_baseline(synth.randn(synth.tensor_seed(7, 0), (M, K)), N, K)
+    return rec
+
+
+def traffic_calibration(stream, n=64 << 20, reps=5):
+    """Known-traffic launches for the FETCH_SIZE / WRITE_SIZE scale: the
+    CAST node kernel f32 -> bf16 (cast_k) over n elements reads 4n bytes
+    and writes 2n bytes once each, no reuse (256 MiB and 128 MiB here)."""
+    import ctypes as C
+    lib = hip.load()
+    src, dst = hip.DeviceBuffer(4 * n), hip.DeviceBuffer(2 * n)
+    ti = abi.make_tensor(abi.F32, [n], src.ptr, 4 * n)
+    to = abi.make_tensor(abi.BF16, [n], dst.ptr, 2 * n)
+    nd = abi.Node()
+    nd.op, nd.n_inputs = abi.OP_CAST, 1
+    nd.inputs[0] = C.pointer(ti)
+    nd.output = C.pointer(to)
+    nd.params[0] = abi.BF16
+    for _ in range(reps):
+        hip.check(lib.sam3_hip_cast_on_path(2, C.byref(nd), stream), "calibration cast")
+    hip.check(lib.sam3_hip_stream_synchronize(stream), "sync")
+    src.free(); dst.free()  # noqa: E702
+    return {"kernel": "cast_k<f32,bf16,hw>", "read_bytes": 4 * n, "write_bytes": 2 * n}
+
+
 class HipGraph:
     """Stream capture into a HIP graph, through the HIP runtime our library
     already loaded (bench plumbing: replaying a captured sequence of
@@ -660,6 +768,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only, no extra configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-q8", action="store_true", help="leave out the Q8 line (\"q8\" key)")
+    ap.add_argument("--calibrate-traffic", action="store_true",
+                    help="also run the known-traffic cast launches that scale rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
     ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,neck,weights",
@@ -702,7 +814,16 @@ def main():
     value = tflops(M, N, K, ms)
     log(f"  {ms * 1e3:.1f} us/step  {value:.1f} TFLOP/s")
 
+    q8 = None
+    if not args.no_q8:
+        log("Q8 line: bf16 x Q8_0 fc1", M, N, K)
+        q8 = q8_record(stream, timer, a_bf, w32, K_, W_, not args.no_cpu_baseline)
+        log(f"  {q8['ms_per_step'] * 1e3:.1f} us/step  {q8['value']:.1f} TFLOP/s; f16 GEMM "
+            f"{q8['roofline']['dominant_kernel']['us']:.1f} us")
+
     extra = {}
+    if args.calibrate_traffic:
+        extra["traffic_calibration"] = traffic_calibration(stream)
     steps2, warm2 = max(10, K_ // 4), max(3, W_ // 2)
     if not args.quick and "cfg2" in only:
         bias = bf16_bits(synth.randn(synth.tensor_seed(2, 2), N, 0.01))
@@ -734,10 +855,6 @@ def main():
         extra["cfg1_q8_f32act_5184x1024x1024"] = {
             "us": round(ms1 * 1e3, 2), "tflops": round(tflops(5184, 1024, 1024, ms1), 2),
             "gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)}
-        wq_fc1 = O.q8_quantize(w32)
-        msq = gemm_case(stream, timer, abi.BF16, a_bf, abi.Q8_0, wq_fc1, abi.F32, M, N, K,
-                        hip.B_NT, steps2, warm2)
-        extra["q8_bf16act_fc1_5184x1024x4096_tflops"] = round(tflops(M, N, K, msq), 2)
 
     if not args.quick and "cfg3" in only:
         log("config 3: 32 layers, distinct Q8 weights")
@@ -899,6 +1016,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(value / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("bf16_fc1_5184x4096x1024")},
         "cpu_baseline": cpu,
+        "q8": q8,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

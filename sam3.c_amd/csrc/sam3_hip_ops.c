@@ -430,21 +430,26 @@ static int prep_q8_f16(const void *w, void *out, int rows, int k, int k_out, int
 	return s3k_q8_nk_to_f16_nk(w, out, k, rows, stream);
 }
 
-/* Q8_0 W [N,K] x f16 A on the MFMA path. Inside graph_eval a constant
- * weight is expanded once into an f16 [N,K] copy, q*scale formed in f32
- * and rounded once to f16 (the direct Q8 kernel rounds the scale to f16
- * and multiplies in f16 at every k-step, one more rounding), and the f16
- * GEMM runs on it at the dense f16 rate, for 2 bytes per weight of HBM
- * instead of 1.125. Other calls keep the direct Q8 kernel: an expansion
- * per call measured slower at every M (its two extra passes cost more
- * than the direct kernel's in-loop dequantization). SAM3_HIP_Q8_EXPAND=0
- * always keeps the direct kernel, =1 always expands. */
+/* Q8_0 W [N,K] x f16 A on the MFMA path. The weight is expanded into an
+ * f16 [N,K] copy, q*scale formed in f32 and rounded once to f16 (the
+ * direct Q8 kernel rounds the scale to f16 and multiplies in f16 at every
+ * k-step, one more rounding), and the f16 GEMM runs on it at the dense
+ * f16 rate. Inside graph_eval a constant weight is expanded once and
+ * kept. Other calls expand per call from M = 3072 on, where the f16 GEMM
+ * gains more than the expansion pass costs (kernel times, bf16 A, f32
+ * out: fc1 N=4096 K=1024 at M = 3072 46.8 us expanded against 55.1 us
+ * direct, at M = 5184 69 against 85; at M = 2048 37.0 direct against
+ * 42.5), and keep the direct kernel below, which reads 1.125 bytes per
+ * weight and needs no scratch. SAM3_HIP_Q8_EXPAND=0 always keeps the
+ * direct kernel, =1 always expands. */
+#define S3H_Q8_EXPAND_MIN_M 3072
 static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 {
 	const int mode = s3h_settings()->q8_expand;
 	const size_t q8_bytes = (size_t)h->N * (h->K / 32) * 36;
 	const int layout_ok = (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1;
-	if (layout_ok && mode != 0 && (mode == 1 || s3h_prep_cacheable(h->b, q8_bytes))) {
+	if (layout_ok && mode != 0 &&
+	    (mode == 1 || h->M >= S3H_Q8_EXPAND_MIN_M || s3h_prep_cacheable(h->b, q8_bytes))) {
 		void *w16 = NULL;
 		int own = 0;
 		enum sam3_error err = prep_weight(h->b, q8_bytes, S3H_PREP_Q8_F16, h->N, h->K, h->K,
@@ -686,7 +691,8 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 	/* the expansion q8_f16_gemm makes */
 	const int mode = s3h_settings()->q8_expand;
 	if (!(g.flags & S3K_B_NT) || K % 32 || mode == 0 ||
-	    (mode != 1 && !s3h_prep_cacheable(b, (size_t)N * (K / 32) * 36)))
+	    (mode != 1 && M < S3H_Q8_EXPAND_MIN_M &&
+	     !s3h_prep_cacheable(b, (size_t)N * (K / 32) * 36)))
 		return 0;
 	h.a_kind = h.b_kind = S3K_F16;
 	h.ldb = K;
