@@ -117,12 +117,14 @@ __device__ __forceinline__ void at_split8(const float4 &x, const float4 &y, uint
 	at_split2(y.z, y.w, hi.w, lo.w);
 }
 
-/* workgroups per CU the registers are budgeted for: four (16 waves) for
- * the 16-bit kernel without a mask */
+/* workgroups per CU the registers are budgeted for, chosen so that no
+ * variant spills: three (12 waves, 168 VGPRs) for the 16-bit kernel
+ * without a mask, two for f32 or a mask, one for f32 with a mask (its
+ * mask tile, score halves and hi/lo operand planes need 256+ VGPRs) */
 template <int DT, int NW, bool MASK>
 constexpr int at_minb()
 {
-	return NW != 4 ? 1 : (DT == S3K_F32 || MASK) ? 2 : 4;
+	return NW != 4 ? 1 : (DT == S3K_F32 && MASK) ? 1 : (DT == S3K_F32 || MASK) ? 2 : 3;
 }
 
 template <int N>
