@@ -309,6 +309,74 @@ def vit_trunk_bench(wkind, depth=32, per_graph=4, steps=3, warmup=1):
             "last_eval_host_nodes": st.host_nodes}
 
 
+def text_encoder_bench(seqs=(1, 8, 32, 77), layers=24, per_graph=4, steps=3, warmup=1):
+    """BASELINE config 4's shapes as a dependent chain: the text encoder's
+    24 layers (text_encoder.c:559-660: width 1024, 16 heads, MLP 4096,
+    causal mask) with distinct Q8_0 linear weights per layer (254 MB, as
+    much as the MALL holds), evaluated 4 layers per graph_eval as the
+    reference's block loop does, x forwarded on the device between evals,
+    for seq in `seqs`. Reports the wall time of all 24 layers and the
+    weight bytes streamed per second."""
+    from sam3_amd import graph
+    w_, heads, mlp = 1024, 16, 4096
+    shapes = {"qkv_w": (3 * w_, w_), "proj_w": (w_, w_), "fc1_w": (mlp, w_), "fc2_w": (w_, mlp)}
+    base = {k: hip.q8_quantize(synth.randn(900 + i, sh, 0.02)) for i, (k, sh) in enumerate(shapes.items())}
+    W = graph.Graph()
+    params = []
+    wbytes = 0
+    for li in range(layers):
+        p = {}
+        for k, sh in shapes.items():
+            blk = base[k].copy()
+            blk[4::36] ^= np.uint8(li)  # distinct bytes per layer (a q value of each block)
+            p[k] = W.tensor(abi.Q8_0, sh, blk)
+            wbytes += blk.nbytes
+        for k, n in (("qkv_b", 3 * w_), ("proj_b", w_), ("fc1_b", mlp), ("fc2_b", w_)):
+            p[k] = W.tensor(abi.F32, (n,), synth.randn(950 + li, (n,), 0.02))
+        for k in ("ln1", "ln2"):
+            p[k + "_w"] = W.tensor(abi.F32, (w_,), synth.randn(960 + li, (w_,), 1.0))
+            p[k + "_b"] = W.tensor(abi.F32, (w_,), synth.randn(970 + li, (w_,), 0.1))
+        params.append(p)
+    out = {}
+    for seq in seqs:
+        xd = hip.DeviceBuffer.of(synth.randn(980 + seq, (seq, w_)))
+        mask = W.tensor(abi.F32, (seq, seq), graph.causal_mask(seq))
+        graphs, x = [], abi.make_tensor(abi.F32, [seq, w_], xd.ptr, seq * w_ * 4)
+        W.keep.append(x)
+        for b0 in range(0, layers, per_graph):
+            G = graph.Graph()
+            G.keep.append(W)
+            for li in range(b0, min(layers, b0 + per_graph)):
+                x = graph.text_layer(G, x, params[li], heads, mask)
+            G.g.no_readback = True
+            graphs.append(G)
+        be = hip.Backend(0)
+        try:
+            def run():
+                for G in graphs:
+                    hip.check(be.graph_eval(G.g), "graph_eval")
+            for _ in range(warmup):
+                run()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                run()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+            st = be.stats()
+        finally:
+            be.close()
+            xd.free()
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        out[f"seq{seq}"] = {"ms": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
+                            "weights_gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                            "kernels_per_eval": st.gpu_nodes - st.fused_nodes,
+                            "nodes_per_eval": graphs[0].g.n_nodes}
+        log(f"  seq {seq}: {out[f'seq{seq}']}")
+    out["note"] = (f"{layers} layers, {per_graph} per graph_eval, Q8_0 weights "
+                   f"{wbytes / 1e6:.0f} MB distinct per layer, f32 activations; weights_gbs = "
+                   "weight bytes / wall time of all layers")
+    return out
+
+
 def vit_block_cpu(threads=None):
     """The reference's CPU kernels (cpu_dispatch_node over the same node
     sequence, oracle/_ref) on one 24x24 window of the block (576 tokens,
@@ -774,9 +842,9 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-graph", action="store_true",
                     help="config 4: issue the per-copy launches directly, not from a HIP graph")
-    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,block,conv,neck,weights",
-                    help="comma list of extra sections to run (cfg1..cfg5, block, conv, neck, "
-                         "weights)")
+    ap.add_argument("--only", default="cfg1,cfg2,cfg3,cfg4,cfg5,textenc,block,conv,neck,weights",
+                    help="comma list of extra sections to run (cfg1..cfg5, textenc, block, conv, "
+                         "neck, weights)")
     ap.add_argument("--block",
                     default="windowed_f32,windowed_q8,global_f32,global_q8,trunk_q8,trunk_f32",
                     help="block section: comma list of {windowed,global}_{f32,q8} and "
@@ -965,6 +1033,10 @@ def main():
         blk["note"] = ("5184 tokens, e 1024, 16 heads, MLP 4096, f32 activations; every node "
                        "on the GPU; block input in HBM, no readback; wall time of graph_eval")
         extra["vit_block"] = blk
+
+    if not args.quick and "textenc" in only:
+        log("text encoder: 24 dependent layers, Q8_0 weights, seq 1/8/32/77")
+        extra["text_encoder_chain"] = text_encoder_bench()
 
     if not args.quick and "conv" in only:
         log("conv2d: patch embedding and neck convs (NHWC x OHWI)")

@@ -294,40 +294,52 @@ __global__ void __launch_bounds__(256) rope_k(const void *x, const float *cos_t,
 	bo_st<DT>(out, 2 * p + 1, add_rn(mul_rn(x0, sn), mul_rn(x1, c)));
 }
 
-/* One head-split operand of attention straight from the fused qkv
- * projection: x holds rows of `pitch` f32 values and the slice starts at
- * column col0; element (b, s, h, d) of the [B, S, H, D] view is
- * x[(b*S + s)*pitch + col0 + h*D + d]. The output is [B, H, S, D]
- * (permute 0,2,1,3). With tables, RoPE is applied on the way exactly as
+/* Head-split operands of attention straight from the fused qkv
+ * projection: x holds rows of `pitch` f32 values; element (b, s, h, d)
+ * of the [B, S, H, D] view of operand y is
+ * x[(b*S + s)*pitch + col0[y] + h*D + d]. The output is [B, H, S, D]
+ * (permute 0,2,1,3). With RoPE it is applied on the way exactly as
  * rope_k does it (pair (d, d+1), cos/sin [S, D/2], products and sums
- * rounded separately). Four values per thread. */
-template <bool ROPE>
-__global__ void __launch_bounds__(256) rope_split_k(const float *x, long long pitch, long long col0,
-						    const float *cos_t, const float *sin_t, float *out,
-						    int B, int S, int H, int D)
+ * rounded separately). Four values per thread. Up to three operands
+ * from the same qkv rows in one launch (blockIdx.y picks the operand):
+ * out[y] takes columns col0[y] onward, with RoPE when bit y of rope_mask
+ * is set. */
+struct Split3Args {
+	const float *x;
+	long long pitch;
+	long long col0[3];
+	float *out[3];
+	const float *cos_t, *sin_t;
+	int rope_mask;
+	int B, S, H, D;
+};
+
+__global__ void __launch_bounds__(256) rope_split3_k(Split3Args a)
 {
+	const int y = blockIdx.y;
 	const long long q = (long long)blockIdx.x * 256 + threadIdx.x;
-	const int D4 = D / 4;
-	if (q >= (long long)B * S * H * D4)
+	const int D4 = a.D / 4;
+	if (q >= (long long)a.B * a.S * a.H * D4)
 		return;
 	const int d = (int)(q % D4) * 4;
 	long long r = q / D4;
-	const int h = (int)(r % H);
-	r /= H;
-	const int s = (int)(r % S);
-	const int b = (int)(r / S);
-	float4 v = *(const float4 *)(x + ((long long)b * S + s) * pitch + col0 + (long long)h * D + d);
-	if (ROPE) {
-		const int half = D / 2;
+	const int h = (int)(r % a.H);
+	r /= a.H;
+	const int s = (int)(r % a.S);
+	const int b = (int)(r / a.S);
+	float4 v = *(const float4 *)(a.x + ((long long)b * a.S + s) * a.pitch + a.col0[y] +
+				     (long long)h * a.D + d);
+	if ((a.rope_mask >> y) & 1) {
+		const int half = a.D / 2;
 		const long long t = (long long)s * half + d / 2;
-		const float c0 = cos_t[t], s0 = sin_t[t], c1 = cos_t[t + 1], s1 = sin_t[t + 1];
+		const float c0 = a.cos_t[t], s0 = a.sin_t[t], c1 = a.cos_t[t + 1], s1 = a.sin_t[t + 1];
 		const float4 u = v;
 		v.x = sub_rn(mul_rn(u.x, c0), mul_rn(u.y, s0));
 		v.y = add_rn(mul_rn(u.x, s0), mul_rn(u.y, c0));
 		v.z = sub_rn(mul_rn(u.z, c1), mul_rn(u.w, s1));
 		v.w = add_rn(mul_rn(u.z, s1), mul_rn(u.w, c1));
 	}
-	*(float4 *)(out + (((long long)b * H + h) * S + s) * D + d) = v;
+	*(float4 *)(a.out[y] + (((long long)b * a.H + h) * a.S + s) * a.D + d) = v;
 }
 
 struct PermArgs {
@@ -522,24 +534,36 @@ extern "C" int s3k_rope(int kind, const void *x, const float *cos_t, const float
 	return (int)hipGetLastError();
 }
 
-extern "C" int s3k_rope_split(const float *x, long long pitch, long long col0, const float *cos_t,
-			      const float *sin_t, float *out, int B, int S, int H, int D,
-			      void *stream)
+extern "C" int s3k_rope_split3(const float *x, long long pitch, const long long *col0,
+			       const float *cos_t, const float *sin_t, int rope_mask, float *const *out,
+			       int n_out, int B, int S, int H, int D, void *stream)
 {
-	if (B < 0 || S < 0 || H < 0 || D <= 0 || D % 4 || pitch % 4 || col0 % 4 ||
-	    col0 + (long long)H * D > pitch || (!cos_t) != (!sin_t) ||
-	    (((uintptr_t)x | (uintptr_t)out) & 15u))
+	if (n_out < 1 || n_out > 3 || B < 0 || S < 0 || H < 0 || D <= 0 || D % 4 || pitch % 4 ||
+	    (rope_mask && (!cos_t || !sin_t)) || (rope_mask >> n_out) || (((uintptr_t)x) & 15u))
 		return (int)hipErrorInvalidValue;
+	Split3Args a;
+	a.x = x;
+	a.pitch = pitch;
+	for (int y = 0; y < 3; ++y) {
+		const int k = y < n_out ? y : 0;
+		if (col0[k] % 4 || col0[k] < 0 || col0[k] + (long long)H * D > pitch || !out[k] ||
+		    ((uintptr_t)out[k] & 15u))
+			return (int)hipErrorInvalidValue;
+		a.col0[y] = col0[k];
+		a.out[y] = out[k];
+	}
+	a.cos_t = cos_t;
+	a.sin_t = sin_t;
+	a.rope_mask = rope_mask;
+	a.B = B;
+	a.S = S;
+	a.H = H;
+	a.D = D;
 	const long long n = (long long)B * S * H * (D / 4);
 	if (n == 0)
 		return (int)hipSuccess;
-	const dim3 grid((unsigned)((n + 255) / 256)), block(256);
-	if (cos_t)
-		hipLaunchKernelGGL(rope_split_k<true>, grid, block, 0, (hipStream_t)stream, x, pitch, col0,
-				   cos_t, sin_t, out, B, S, H, D);
-	else
-		hipLaunchKernelGGL(rope_split_k<false>, grid, block, 0, (hipStream_t)stream, x, pitch, col0,
-				   cos_t, sin_t, out, B, S, H, D);
+	hipLaunchKernelGGL(rope_split3_k, dim3((unsigned)((n + 255) / 256), (unsigned)n_out), dim3(256),
+			   0, (hipStream_t)stream, a);
 	return (int)hipGetLastError();
 }
 

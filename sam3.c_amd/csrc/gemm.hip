@@ -646,12 +646,16 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 {
 	hipStream_t st = (hipStream_t)stream;
 	GemmArgs p = make_args(g);
+	/* the LDS epilogue adds a residual and maps rows; the skinny kernels
+	 * add a residual (f32 output, batch 1) */
 	if (((g->flags & S3K_EPI_RES) || g->rm_g) &&
-	    (path != S3K_PATH_MFMA || ((g->flags & S3K_EPI_RES) && !g->res) || g->batch != 1 ||
+	    ((path != S3K_PATH_MFMA && !(path == S3K_PATH_SKINNY && !g->rm_g)) ||
+	     ((g->flags & S3K_EPI_RES) && !g->res) || g->batch != 1 ||
 	     g->c_kind == S3K_BF16 || g->c_kind == S3K_F16 ||
+	     (path == S3K_PATH_SKINNY && (g->c_kind != S3K_F32 || g->ldc != g->N)) ||
 	     (g->rm_g && (g->rm_d1 <= 0 || g->rm_d2 <= 0 ||
 			  g->M % ((long long)g->rm_g * g->rm_d1 * g->rm_d2)))))
-		return (int)hipErrorInvalidValue; /* only the LDS epilogue adds a residual / maps rows */
+		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))
 			return (int)hipErrorInvalidValue;

@@ -168,11 +168,13 @@ int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_d
  * and below 2^-10). */
 int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
 		   const int *axes, int K, unsigned *ovf, unsigned ovf_tag, void *stream);
-/* Attention operand [B, H, S, D] (f32) from columns col0.. of rows of
- * `pitch` values holding [B*S, H*D] (the q, k or v part of a fused qkv
- * output), with RoPE (tables [S, D/2]) when cos_t/sin_t are given. */
-int s3k_rope_split(const float *x, long long pitch, long long col0, const float *cos_t,
-		   const float *sin_t, float *out, int B, int S, int H, int D, void *stream);
+/* Attention operands [B, H, S, D] (f32), up to three (n_out) in one
+ * launch: out[y] from columns col0[y].. of rows of `pitch` values holding
+ * [B*S, H*D] (the q, k or v part of a fused qkv output), with RoPE
+ * (tables [S, D/2]) where bit y of rope_mask is set. */
+int s3k_rope_split3(const float *x, long long pitch, const long long *col0, const float *cos_t,
+		    const float *sin_t, int rope_mask, float *const *out, int n_out, int B, int S,
+		    int H, int D, void *stream);
 /* f32 rows [rows, K] (pitch ld) -> bf16 [rows, 3K]: [hi, lo, hi] for
  * order 0, [hi, hi, lo] for order 1 (hi = bf16(x), lo = bf16(x - hi)). */
 int s3k_split3_bf16(const float *src, void *dst, int rows, int K, long long ld, int order,

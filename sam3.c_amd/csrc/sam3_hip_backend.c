@@ -91,6 +91,11 @@ struct sam3_hip_backend {
 	hipStream_t stream;
 	struct s3h_res *res;
 	int n_res, cap_res;
+	/* open-addressing index host address -> res slot + 1 (0 empty),
+	 * rebuilt after drops (which move entries) */
+	int *res_ix;
+	size_t res_ix_cap;
+	int res_ix_dirty;
 	struct s3h_blob *blobs;
 	int n_blobs, cap_blobs;
 	void **owned; /* device buffers made by fuse_rows */
@@ -115,11 +120,62 @@ struct sam3_hip_backend {
 /* ------------------------------------------------------------------ */
 /* Residency table                                                      */
 /* ------------------------------------------------------------------ */
+static size_t res_hash(const void *p)
+{
+	uint64_t x = (uint64_t)(uintptr_t)p;
+	x ^= x >> 33;
+	x *= 0xff51afd7ed558ccdULL;
+	x ^= x >> 33;
+	return (size_t)x;
+}
+
+static void res_ix_put(struct sam3_hip_backend *hb, int slot)
+{
+	size_t k = res_hash(hb->res[slot].host) & (hb->res_ix_cap - 1);
+	while (hb->res_ix[k])
+		k = (k + 1) & (hb->res_ix_cap - 1);
+	hb->res_ix[k] = slot + 1;
+}
+
+/* (Re)build the index for the current table, at most half full. Returns
+ * 0 when out of host memory (lookups then scan the table). */
+static int res_ix_rebuild(struct sam3_hip_backend *hb)
+{
+	size_t cap = 64;
+	while (cap < 4 * (size_t)hb->n_res)
+		cap <<= 1;
+	if (cap != hb->res_ix_cap) {
+		int *ix = realloc(hb->res_ix, cap * sizeof(*ix));
+		if (!ix)
+			return 0;
+		hb->res_ix = ix;
+		hb->res_ix_cap = cap;
+	}
+	memset(hb->res_ix, 0, hb->res_ix_cap * sizeof(*hb->res_ix));
+	for (int i = 0; i < hb->n_res; i++)
+		res_ix_put(hb, i);
+	hb->res_ix_dirty = 0;
+	return 1;
+}
+
+/* The entry for host address `host`. Graphs of several layers hold
+ * hundreds of entries and look them up several times per node: a hash
+ * index, not a scan. Host addresses are unique in the table. */
 static struct s3h_res *res_find(struct sam3_hip_backend *hb, const void *host)
 {
-	for (int i = 0; i < hb->n_res; i++)
-		if (hb->res[i].host == host)
-			return &hb->res[i];
+	if ((hb->res_ix_dirty || 2 * (size_t)hb->n_res >= hb->res_ix_cap) && !res_ix_rebuild(hb)) {
+		for (int i = 0; i < hb->n_res; i++)
+			if (hb->res[i].host == host)
+				return &hb->res[i];
+		return NULL;
+	}
+	size_t k = res_hash(host) & (hb->res_ix_cap - 1);
+	while (hb->res_ix[k]) {
+		struct s3h_res *e = &hb->res[hb->res_ix[k] - 1];
+		if (e->host == host)
+			return e;
+		k = (k + 1) & (hb->res_ix_cap - 1);
+	}
 	return NULL;
 }
 
@@ -150,6 +206,7 @@ static void res_drop_at(struct sam3_hip_backend *hb, int i)
 		(void)s3h_scratch_free(hb->res[i].dev, hb->stream);
 	hb->res[i] = hb->res[hb->n_res - 1];
 	hb->n_res--;
+	hb->res_ix_dirty = 1;
 }
 
 static void res_drop_range(struct sam3_hip_backend *hb, const char *lo, const char *hi)
@@ -186,6 +243,10 @@ static enum sam3_error res_new(struct sam3_hip_backend *hb, const struct sam3_te
 	e->host_valid = 1;
 	e->keep = !t->ephemeral;
 	hb->n_res++;
+	if (!hb->res_ix_dirty && 2 * (size_t)hb->n_res < hb->res_ix_cap)
+		res_ix_put(hb, hb->n_res - 1);
+	else
+		hb->res_ix_dirty = 1;
 	*out = e;
 	return SAM3_OK;
 }
@@ -632,8 +693,8 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		if (r && r != out && r->data && r->dtype == SAM3_DTYPE_F32 &&
 		    ad->output->dtype == SAM3_DTYPE_F32 && s3h_nelems(r) == (long long)M * N &&
 		    r->data != ad->output->data &&
-		    s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, S3H_A_PLAIN) &&
-		    dev_in(hb, r, &dres) == SAM3_OK) {
+		    s3h_matmul_res_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags) &&
+		    !written_between(g, i + 1, j, r) && dev_in(hb, r, &dres) == SAM3_OK) {
 			out = ad->output;
 			j++;
 		} else {
@@ -780,7 +841,8 @@ static int permute_operand_form(struct sam3_hip_backend *hb, const struct sam3_g
  * (graph_helpers.c:721-882): SLICE of the fused qkv output's columns ->
  * RESHAPE [B, S, H, D] -> (ROPE -> RESHAPE ...) -> TRANSPOSE (0, 2, 1, 3).
  * Every tensor in between is used once, so the chain runs as one kernel
- * from the qkv rows to the head-split operand (s3k_rope_split). */
+ * from the qkv rows to the head-split operand (s3k_rope_split3, which
+ * takes the q, k and v chains of one qkv output in one launch). */
 struct qkv_chain {
 	int n, idx[8];
 	const struct sam3_tensor *src, *out, *cos_t, *sin_t;
@@ -867,26 +929,72 @@ static int match_qkv_chain(const struct sam3_graph *g, int i, struct use_map *us
 	return 1;
 }
 
-static enum sam3_error run_qkv_chain(struct sam3_hip_backend *hb, const struct qkv_chain *c)
+/* The chain c0 at node c0->idx[0] and the next (up to two) chains that
+ * slice the same qkv rows with the same head split (k and v after q), as
+ * one launch of s3k_rope_split3. A later chain joins only if no node
+ * before it writes the rows or the RoPE tables it reads, and the RoPE
+ * chains share one pair of tables. */
+static enum sam3_error run_qkv_chains(struct sam3_hip_backend *hb, const struct sam3_graph *g,
+				      const struct qkv_chain *c0, struct use_map *uses,
+				      unsigned char *done)
 {
-	void *dx = NULL, *dc = NULL, *ds = NULL, *dy = NULL;
-	enum sam3_error err = dev_in(hb, c->src, &dx);
-	if (err == SAM3_OK && c->cos_t)
-		err = dev_in(hb, c->cos_t, &dc);
-	if (err == SAM3_OK && c->sin_t)
-		err = dev_in(hb, c->sin_t, &ds);
-	if (err == SAM3_OK)
-		err = dev_out(hb, c->out, &dy);
-	if (err == SAM3_OK)
-		err = s3h_hip(s3k_rope_split((const float *)dx, c->pitch, c->col0, (const float *)dc,
-					     (const float *)ds, (float *)dy, c->B, c->S, c->H, c->D,
-					     hb->stream),
-			      "attention operand (slice, rope, head split)");
-	if (err == SAM3_OK) {
-		hb->stats.gpu_nodes++;
-		hb->stats.fused_nodes += c->n - 1;
+	struct qkv_chain cs[3];
+	int n = 1;
+	cs[0] = *c0;
+	const struct sam3_tensor *ct = c0->cos_t, *st = c0->sin_t;
+	const int i = c0->idx[0];
+	for (int j = i + 1; j < g->n_nodes && n < 3; j++) {
+		const struct sam3_node *m = &g->nodes[j];
+		if (done[j] || m->op != SAM3_OP_SLICE || m->n_inputs < 1 || m->inputs[0] != c0->src)
+			continue;
+		struct qkv_chain c;
+		if (!match_qkv_chain(g, j, uses, &c) || c.B != c0->B || c.S != c0->S || c.H != c0->H ||
+		    c.D != c0->D || c.pitch != c0->pitch)
+			break;
+		if (c.cos_t && ct && (c.cos_t != ct || c.sin_t != st))
+			break;
+		if (written_between(g, i + 1, j, c0->src) ||
+		    (c.cos_t && (written_between(g, i + 1, j, c.cos_t) ||
+				 written_between(g, i + 1, j, c.sin_t))))
+			break;
+		if (c.cos_t) {
+			ct = c.cos_t;
+			st = c.sin_t;
+		}
+		cs[n++] = c;
 	}
-	return err;
+	void *dx = NULL, *dc = NULL, *ds = NULL;
+	float *outs[3] = {NULL, NULL, NULL};
+	long long cols[3] = {0, 0, 0};
+	int rope_mask = 0;
+	enum sam3_error err = dev_in(hb, c0->src, &dx);
+	if (err == SAM3_OK && ct)
+		err = dev_in(hb, ct, &dc);
+	if (err == SAM3_OK && st)
+		err = dev_in(hb, st, &ds);
+	for (int k = 0; k < n && err == SAM3_OK; k++) {
+		void *dy = NULL;
+		err = dev_out(hb, cs[k].out, &dy);
+		outs[k] = (float *)dy;
+		cols[k] = cs[k].col0;
+		rope_mask |= (cs[k].cos_t != NULL) << k;
+	}
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_rope_split3((const float *)dx, c0->pitch, cols, (const float *)dc,
+					      (const float *)ds, rope_mask, outs, n, c0->B, c0->S,
+					      c0->H, c0->D, hb->stream),
+			      "attention operands (slice, rope, head split)");
+	if (err != SAM3_OK)
+		return err;
+	int fused = -1;
+	for (int k = 0; k < n; k++) {
+		for (int t = k ? 0 : 1; t < cs[k].n; t++)
+			done[cs[k].idx[t]] = 1;
+		fused += cs[k].n;
+	}
+	hb->stats.gpu_nodes++;
+	hb->stats.fused_nodes += fused;
+	return SAM3_OK;
 }
 
 /* TRANSPOSE written as the operand form fmt of its one consuming GEMM. */
@@ -1216,9 +1324,7 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 		if (n->op == SAM3_OP_NONE || done[i]) {
 			err = SAM3_OK; /* done[i]: run earlier as part of a chain */
 		} else if (n->op == SAM3_OP_SLICE && !qkv_plain && match_qkv_chain(g, i, &uses, &qc)) {
-			err = run_qkv_chain(hb, &qc);
-			for (int k = 1; k < qc.n; k++)
-				done[qc.idx[k]] = 1;
+			err = run_qkv_chains(hb, g, &qc, &uses, done);
 		} else if (n->op == SAM3_OP_RESHAPE) {
 			/* a view: consumers find the input's device copy under the
 			 * same host address */
@@ -1417,6 +1523,9 @@ static void hip_free(struct sam3_backend *be)
 	free(hb->res);
 	hb->res = NULL;
 	hb->cap_res = 0;
+	free(hb->res_ix);
+	hb->res_ix = NULL;
+	hb->res_ix_cap = 0;
 	while (hb->n_blobs)
 		blob_drop_at(hb, hb->n_blobs - 1);
 	free(hb->blobs);

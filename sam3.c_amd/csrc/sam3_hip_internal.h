@@ -91,6 +91,11 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
  * {g, d1, d2}) stores C row m permuted as the s3k_gemm row map says. */
 int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags, int out_fmt);
+/* Whether s3h_matmul_fmt_to can add an f32 [M, N] residual to the f32
+ * result (S3H_A_PLAIN, no row map): the direct-to-LDS GEMM, or a skinny
+ * Q8_0 GEMM. */
+int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags);
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
 				  const void *res, const int *row_map, int flags, unsigned *ovf,

@@ -71,7 +71,85 @@ struct s3h_blk {
 };
 static struct s3h_blk *s3h_blks;
 static int s3h_nblks, s3h_capblks;
+/* The idle blocks (indices into s3h_blks), which is all a request scans,
+ * and an open-addressing index block address -> slot + 1 for frees: a
+ * backend keeps hundreds of blocks busy (its resident weights), so
+ * neither may walk the whole table. The index is rebuilt after the table
+ * changes order (a trim). */
+static int *s3h_idle, s3h_nidle, s3h_capidle;
+static int *s3h_bix;
+static size_t s3h_bix_cap;
+static int s3h_bix_dirty;
 static pthread_mutex_t s3h_blk_lock = PTHREAD_MUTEX_INITIALIZER;
+
+static size_t blk_hash(const void *p)
+{
+	uint64_t x = (uint64_t)(uintptr_t)p;
+	x ^= x >> 33;
+	x *= 0xff51afd7ed558ccdULL;
+	x ^= x >> 33;
+	return (size_t)x;
+}
+
+static void bix_put(int slot)
+{
+	size_t k = blk_hash(s3h_blks[slot].p) & (s3h_bix_cap - 1);
+	while (s3h_bix[k])
+		k = (k + 1) & (s3h_bix_cap - 1);
+	s3h_bix[k] = slot + 1;
+}
+
+static int bix_rebuild(void)
+{
+	size_t cap = 64;
+	while (cap < 4 * (size_t)s3h_nblks)
+		cap <<= 1;
+	if (cap != s3h_bix_cap) {
+		int *ix = realloc(s3h_bix, cap * sizeof(*ix));
+		if (!ix)
+			return 0;
+		s3h_bix = ix;
+		s3h_bix_cap = cap;
+	}
+	memset(s3h_bix, 0, s3h_bix_cap * sizeof(*s3h_bix));
+	for (int i = 0; i < s3h_nblks; i++)
+		bix_put(i);
+	s3h_bix_dirty = 0;
+	return 1;
+}
+
+/* Slot of block p, or -1. Called with the lock held. */
+static int blk_slot(const void *p)
+{
+	if ((s3h_bix_dirty || 2 * (size_t)s3h_nblks >= s3h_bix_cap) && !bix_rebuild()) {
+		for (int i = 0; i < s3h_nblks; i++)
+			if (s3h_blks[i].p == p)
+				return i;
+		return -1;
+	}
+	size_t k = blk_hash(p) & (s3h_bix_cap - 1);
+	while (s3h_bix[k]) {
+		const int i = s3h_bix[k] - 1;
+		if (s3h_blks[i].p == p)
+			return i;
+		k = (k + 1) & (s3h_bix_cap - 1);
+	}
+	return -1;
+}
+
+static int idle_push(int slot)
+{
+	if (s3h_nidle == s3h_capidle) {
+		const int cap = s3h_capidle ? 2 * s3h_capidle : 64;
+		int *t = realloc(s3h_idle, (size_t)cap * sizeof(*t));
+		if (!t)
+			return 0;
+		s3h_idle = t;
+		s3h_capidle = cap;
+	}
+	s3h_idle[s3h_nidle++] = slot;
+	return 1;
+}
 
 static size_t scratch_round(size_t n)
 {
@@ -99,6 +177,12 @@ static void scratch_trim_locked(int dev, int stream_only, void *stream)
 		(void)hipFree(b->p);
 		s3h_blks[i] = s3h_blks[--s3h_nblks];
 	}
+	/* slots moved: rebuild the idle list and the address index */
+	s3h_nidle = 0;
+	for (int i = 0; i < s3h_nblks; i++)
+		if (!s3h_blks[i].busy)
+			(void)idle_push(i); /* the list only shrank: no allocation */
+	s3h_bix_dirty = 1;
 }
 
 enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
@@ -110,15 +194,17 @@ enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
 	*p = NULL;
 	pthread_mutex_lock(&s3h_blk_lock);
 	int best = -1;
-	for (int i = 0; i < s3h_nblks; i++) {
-		const struct s3h_blk *b = &s3h_blks[i];
-		if (!b->busy && b->dev == dev && b->stream == stream && b->n >= need && b->n <= most &&
-		    (best < 0 || b->n < s3h_blks[best].n))
-			best = i;
+	for (int j = 0; j < s3h_nidle; j++) {
+		const struct s3h_blk *b = &s3h_blks[s3h_idle[j]];
+		if (b->dev == dev && b->stream == stream && b->n >= need && b->n <= most &&
+		    (best < 0 || b->n < s3h_blks[s3h_idle[best]].n))
+			best = j;
 	}
 	if (best >= 0) {
-		s3h_blks[best].busy = 1;
-		*p = s3h_blks[best].p;
+		const int slot = s3h_idle[best];
+		s3h_idle[best] = s3h_idle[--s3h_nidle];
+		s3h_blks[slot].busy = 1;
+		*p = s3h_blks[slot].p;
 		pthread_mutex_unlock(&s3h_blk_lock);
 		return SAM3_OK;
 	}
@@ -133,6 +219,18 @@ enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
 		s3h_blks = t;
 		s3h_capblks = cap;
 	}
+	/* room in the idle list for this block's later free */
+	if (s3h_capidle < s3h_nblks + 1) {
+		const int cap = 2 * (s3h_nblks + 1);
+		int *t = realloc(s3h_idle, (size_t)cap * sizeof(*t));
+		if (!t) {
+			pthread_mutex_unlock(&s3h_blk_lock);
+			s3h_error("scratch: out of host memory for the idle list");
+			return SAM3_ENOMEM;
+		}
+		s3h_idle = t;
+		s3h_capidle = cap;
+	}
 	void *q = NULL;
 	hipError_t e = hipMalloc(&q, need);
 	if (e == hipErrorOutOfMemory) {
@@ -145,6 +243,10 @@ enum sam3_error s3h_scratch_alloc(void **p, size_t nbytes, void *stream)
 		return s3h_hip(e, "scratch");
 	}
 	s3h_blks[s3h_nblks++] = (struct s3h_blk){q, need, stream, dev, 1};
+	if (!s3h_bix_dirty && 2 * (size_t)s3h_nblks < s3h_bix_cap)
+		bix_put(s3h_nblks - 1);
+	else
+		s3h_bix_dirty = 1;
 	*p = q;
 	pthread_mutex_unlock(&s3h_blk_lock);
 	return SAM3_OK;
@@ -155,13 +257,15 @@ enum sam3_error s3h_scratch_free(void *p, void *stream)
 	if (!p)
 		return SAM3_OK;
 	pthread_mutex_lock(&s3h_blk_lock);
-	for (int i = 0; i < s3h_nblks; i++) {
-		if (s3h_blks[i].p == p) {
+	const int i = blk_slot(p);
+	if (i >= 0) {
+		if (s3h_blks[i].busy) {
 			s3h_blks[i].busy = 0;
 			s3h_blks[i].stream = stream; /* its last use was enqueued here */
-			pthread_mutex_unlock(&s3h_blk_lock);
-			return SAM3_OK;
+			(void)idle_push(i); /* room was reserved when the block was made */
 		}
+		pthread_mutex_unlock(&s3h_blk_lock);
+		return SAM3_OK;
 	}
 	pthread_mutex_unlock(&s3h_blk_lock);
 	s3h_error("scratch: free of %p, which is not a scratch block", p);
@@ -617,6 +721,22 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
 	return launch_a_safe(&g, path, "matmul", stream);
 }
 
+/* f32 activations times Q8_0 weights on the skinny kernels, which would
+ * first copy A to f16 rows (launch_a_safe): A given already as f16 (an
+ * operand a producer wrote) is read as it is. Producers are not asked to
+ * write this form (s3h_matmul_a_format): their range flag makes
+ * graph_eval wait for the GPU at its end, which costs a skinny chain more
+ * than the row copy it saves. */
+static int skinny_takes_f16(const struct s3k_gemm *g)
+{
+	if (g->a_kind != S3K_F32 || g->b_kind != S3K_Q8 || g->batch != 1 ||
+	    s3k_gemm_path(g) != S3K_PATH_SKINNY)
+		return 0;
+	struct s3k_gemm h = *g;
+	h.a_kind = S3K_F16;
+	return s3k_gemm_path(&h) == S3K_PATH_SKINNY && rounds_a_to_f16(g, S3K_PATH_SKINNY);
+}
+
 int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
 			int K, int flags)
 {
@@ -651,6 +771,10 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 			return SAM3_EINVAL;
 		}
 		return f32_split_gemm(&g, a, stream);
+	}
+	if (a_fmt == S3H_A_F16 && skinny_takes_f16(&g)) {
+		g.a_kind = S3K_F16;
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream), "matmul skinny");
 	}
 	if (a_fmt == S3H_A_F16 && g.a_kind == S3K_F32 && q8_dl_wants_cast(&g)) {
 		g.a_kind = S3K_F16;
@@ -688,6 +812,8 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 	}
 	if (b_dt != SAM3_DTYPE_Q8_0 || a_fmt != S3H_A_F16 || a_dt != SAM3_DTYPE_F32)
 		return 0;
+	if (s3k_gemm_path(&h) == S3K_PATH_SKINNY)
+		return 0; /* few rows: the Q8_0 blocks streamed, not an f16 copy */
 	/* the expansion q8_f16_gemm makes */
 	const int mode = s3h_settings()->q8_expand;
 	if (!(g.flags & S3K_B_NT) || K % 32 || mode == 0 ||
@@ -699,6 +825,36 @@ int s3h_matmul_out_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 	return s3k_dl_eligible(&h);
 }
 
+/* A skinny Q8_0 GEMM (f32 out, batch 1) that adds a residual in its
+ * epilogue: A f16 written by its producer (S3H_A_F16), or f32 (copied to
+ * f16 rows first). */
+static int skinny_res_fits(int a_fmt, const struct s3k_gemm *g)
+{
+	if (g->b_kind != S3K_Q8 || g->c_kind != S3K_F32 || g->batch != 1 || g->ldc != g->N ||
+	    g->a_kind != S3K_F32)
+		return 0;
+	if (a_fmt == S3H_A_F16)
+		return skinny_takes_f16(g);
+	return a_fmt == S3H_A_PLAIN && s3k_gemm_path(g) == S3K_PATH_SKINNY;
+}
+
+/* Whether s3h_matmul_fmt_to can add an f32 [M, N] residual to this GEMM's
+ * f32 result in its epilogue (no row map). */
+int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags)
+{
+	if (s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN))
+		return 1;
+	if (M <= 0 || N <= 0 || K <= 0 || !a || !b ||
+	    check_kinds(a_dt, b_dt, SAM3_DTYPE_F32) != SAM3_OK)
+		return 0;
+	static const char al[16] __attribute__((aligned(16)));
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
+	g.a = al;
+	return skinny_res_fits(a_fmt, &g);
+}
+
 /* The GEMM of s3h_matmul_fmt with its f32 result written as out_fmt:
  * bf16 planes [M, 3N] = [hi|lo|hi] per row, or f16 [M, N], with the
  * bias and GELU applied in f32 first, the values split3 / the f16 cast
@@ -708,8 +864,10 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 				  const void *res, const int *row_map, int flags, unsigned *ovf,
 				  unsigned ovf_tag, void *stream)
 {
-	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) || (res && ((uintptr_t)res & 3u)) ||
-	    !s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt)) {
+	const int fits = out_fmt == S3H_A_PLAIN && !row_map
+				 ? s3h_matmul_res_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags)
+				 : s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, out_fmt);
+	if (!c || ((flags & SAM3_HIP_BIAS) && !bias) || (res && ((uintptr_t)res & 3u)) || !fits) {
 		s3h_error("matmul: cannot write form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
 		return SAM3_EINVAL;
 	}
@@ -739,6 +897,14 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
+	if (out_fmt == S3H_A_PLAIN && !row_map && skinny_res_fits(a_fmt, &g)) {
+		if (a_fmt == S3H_A_F16) {
+			g.a_kind = S3K_F16;
+			return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
+				       "matmul skinny");
+		}
+		return launch_a_safe(&g, S3K_PATH_SKINNY, "matmul skinny", stream);
+	}
 	g.a_kind = S3K_F16;
 	return q8_f16_gemm(&g, stream);
 }

@@ -58,6 +58,7 @@ struct SkinnyArgs {
 	long long lda, ldc;   /* elements */
 	int a_kind, c_kind, flags;
 	const float *rs;      /* S3K_EPI_ROWSCALE row factors */
+	const float *res;     /* S3K_EPI_RES: f32 [M, N], pitch N, added last */
 };
 
 /* Two int8 (selected by SEL from w ^ 0x80808080) -> exact f16 pair. */
@@ -182,6 +183,8 @@ __global__ void __launch_bounds__(WV * 64) q8_skinny(SkinnyArgs p)
 			o = epilogue<1>(s, bv, p.flags);
 		else
 			o = epilogue<0>(s, bv, p.flags);
+		if (p.flags & S3K_EPI_RES)
+			o += p.res[(long long)m * p.N + n];
 		store_from_f32(p.c, (long long)m * p.ldc + n, p.c_kind, o);
 	}
 }
@@ -206,6 +209,7 @@ struct StreamArgs {
 	int zsplit;                /* activation-row groups: ceil(M / MR)     */
 	const float *rs;           /* S3K_EPI_ROWSCALE row factors ...        */
 	long long rs_sb;           /* ... and their batch stride              */
+	const float *res;          /* S3K_EPI_RES: f32 [M, N], pitch N (batch 1) */
 };
 
 template <int AK, int MR, int NT, int KC>
@@ -438,7 +442,10 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		if (p.flags & S3K_EPI_ROWSCALE)
 			s *= p.rs[blockIdx.y * p.rs_sb + m0 + m];
 		const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
-		cb[(long long)(m0 + m) * p.ldc + n] = epilogue<0>(s, bv, p.flags);
+		float o = epilogue<0>(s, bv, p.flags);
+		if (p.flags & S3K_EPI_RES)
+			o += p.res[(long long)(m0 + m) * p.N + n];
+		cb[(long long)(m0 + m) * p.ldc + n] = o;
 	}
 }
 
@@ -554,6 +561,7 @@ static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 	p.zsplit = (g->M + MR - 1) / MR;
 	p.rs = g->rs;
 	p.rs_sb = g->rs_sb;
+	p.res = (const float *)g->res;
 	dim3 grid(p.groups * p.zsplit, g->batch);
 	hipLaunchKernelGGL((q8_stream<AK, MR, NT, KC>), grid,
 			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), 0, (hipStream_t)stream, p);
@@ -695,6 +703,7 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 	p.c_kind = g->c_kind;
 	p.flags = g->flags;
 	p.rs = g->rs;
+	p.res = (const float *)g->res;
 	hipStream_t st = (hipStream_t)stream;
 	switch (g->a_kind) {
 	case S3K_F32:  return launch_mt<S3K_F32>(p, st);

@@ -138,19 +138,22 @@ class Graph:
         t = self.permute(self.reshape(x, [nw, nw, ws, ws * e]), (0, 2, 1, 3))
         return self.reshape(t, [grid * grid, e])
 
-    def mha_rope(self, x, qkv_w, qkv_b, out_w, out_b, n_heads, cos_t, sin_t, grid_w, scale):
+    def mha_rope(self, x, qkv_w, qkv_b, out_w, out_b, n_heads, cos_t, sin_t, grid_w, scale,
+                 mask=None):
         """gh_multihead_attention_rope (:721-882) with q = k = v = x
-        [batch, seq, d_model]."""
+        [batch, seq, d_model]; no RoPE when cos_t / sin_t are None
+        (:774), an additive [seq, seq] mask when given (:842-843)."""
         batch, seq, d = x.dims[0], x.dims[1], x.dims[2]
         hd = d // n_heads
         flat = [batch * seq, d]
         qkv = self.linear(self.reshape(x, flat), qkv_w, qkv_b)
         sq, sk, sv = (self.slice(qkv, 1, i * d, (i + 1) * d) for i in range(3))
         four = [batch, seq, n_heads, hd]
-        sq = self.reshape(self.rope(self.reshape(sq, four), cos_t, sin_t, grid_w, scale), flat)
-        sk = self.reshape(self.rope(self.reshape(sk, four), cos_t, sin_t, grid_w, scale), flat)
+        if cos_t is not None and sin_t is not None:
+            sq = self.reshape(self.rope(self.reshape(sq, four), cos_t, sin_t, grid_w, scale), flat)
+            sk = self.reshape(self.rope(self.reshape(sk, four), cos_t, sin_t, grid_w, scale), flat)
         q4, k4, v4 = (self.permute(self.reshape(t, four), (0, 2, 1, 3)) for t in (sq, sk, sv))
-        attn = self.permute(self.sdpa(q4, k4, v4, None, hd), (0, 2, 1, 3))
+        attn = self.permute(self.sdpa(q4, k4, v4, mask, hd), (0, 2, 1, 3))
         return self.linear(self.reshape(attn, flat), out_w, out_b)
 
 
@@ -175,6 +178,28 @@ def vit_block(G, x, p, n_heads, grid, window, is_global, cos_t, sin_t):
     ff = G.mlp(G.layernorm(x, p["ln2_w"], p["ln2_b"]), p["fc1_w"], p["fc1_b"], p["fc2_w"],
                p["fc2_b"])
     return G.add(x, ff)
+
+
+def text_layer(G, x, p, n_heads, mask):
+    """One text-encoder layer as text_encoder.c:588-652 builds it, on x
+    [seq, width]: LN -> MHA (fused QKV, causal mask, no RoPE) -> + x ->
+    LN -> MLP (GELU) -> + x. p: dict of weight tensors ln1_w, ln1_b,
+    qkv_w, qkv_b, proj_w, proj_b, ln2_w, ln2_b, fc1_w, fc1_b, fc2_w, fc2_b."""
+    seq, w = x.dims[0], x.dims[1]
+    xn = G.reshape(G.layernorm(x, p["ln1_w"], p["ln1_b"]), [1, seq, w])
+    attn = G.mha_rope(xn, p["qkv_w"], p["qkv_b"], p["proj_w"], p["proj_b"], n_heads,
+                      None, None, 0, 0.0, mask)
+    x = G.add(x, attn)
+    ff = G.mlp(G.layernorm(x, p["ln2_w"], p["ln2_b"]), p["fc1_w"], p["fc1_b"], p["fc2_w"],
+               p["fc2_b"])
+    return G.add(x, ff)
+
+
+def causal_mask(seq):
+    """The text encoder's additive causal mask (text_encoder.c:552-557):
+    -1e9 above the diagonal, 0 elsewhere."""
+    c = np.arange(seq)
+    return np.where(c[None, :] > c[:, None], np.float32(-1e9), np.float32(0.0)).astype(np.float32)
 
 
 # Block parameter -> checkpoint tensor name, as sam3_vit_load looks them up

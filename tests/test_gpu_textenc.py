@@ -1,0 +1,136 @@
+"""The text encoder's layer chain (text_encoder.c:559-660) through the HIP
+backend's graph_eval: LN -> MHA with the fused QKV weight and the causal
+mask -> + x -> LN -> MLP -> + x, several layers per graph_eval, for the
+token counts of BASELINE config 4 (seq 1, 8, 32, 77), with Q8_0 or f32
+linear weights at the production width (1024, 16 heads, MLP 4096).
+
+Every node must run on the GPU. The output is compared with the
+reference's own cpu_dispatch_node loop over the same graph (oracle/_ref);
+for Q8_0 weights the reference graph gets the dequantized weights in f32
+(its Q8 linear path is the same arithmetic on them, cpu_matmul_q8.c:
+124-131). Bounds: f32 weights 1e-3 normwise with a 2e-3 * rms elementwise
+floor; Q8_0 weights the same with a 1.5e-2 * rms floor (each of a
+layer's four GEMMs rounds activations and q*scale to f16, about 3e-4
+normwise each).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import assert_f32_close, oracle, require_gpu
+from sam3_amd import abi, graph, hip, synth
+from test_gpu_blockops import out_array, reference_eval
+
+pytestmark = pytest.mark.gpu
+
+W, HEADS, MLP = 1024, 16, 4096
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    require_gpu()
+
+
+def build(seq, n_layers, wkind, seed, deq_ref=False):
+    O = oracle()
+    G = graph.Graph()
+    x = G.tensor(abi.F32, (seq, W), synth.randn(seed, (seq, W)), ephemeral=1)
+    mask = G.tensor(abi.F32, (seq, seq), graph.causal_mask(seq))
+    shapes = {"ln1_w": ((W,), 1.0), "ln1_b": ((W,), 0.1), "qkv_w": ((3 * W, W), 0.03),
+              "qkv_b": ((3 * W,), 0.02), "proj_w": ((W, W), 0.03), "proj_b": ((W,), 0.02),
+              "ln2_w": ((W,), 1.0), "ln2_b": ((W,), 0.1), "fc1_w": ((MLP, W), 0.03),
+              "fc1_b": ((MLP,), 0.02), "fc2_w": ((W, MLP), 0.03), "fc2_b": ((W,), 0.02)}
+    for li in range(n_layers):
+        p = {}
+        for i, (name, (shape, std)) in enumerate(shapes.items()):
+            w = synth.randn(seed + 100 * (li + 1) + i, shape, std)
+            if len(shape) == 2 and wkind == "q8":
+                blocks = O.q8_quantize(w)
+                p[name] = (G.tensor(abi.F32, shape, O.q8_dequantize(blocks, w.size).reshape(shape))
+                           if deq_ref else G.tensor(abi.Q8_0, shape, blocks))
+            else:
+                p[name] = G.tensor(abi.F32, shape, w)
+        x = graph.text_layer(G, x, p, HEADS, mask)
+    return G, x
+
+
+def test_causal_mask_matches_the_reference_rule():
+    m = graph.causal_mask(5)
+    assert m[0, 0] == 0 and m[0, 1] == np.float32(-1e9) and m[4, 0] == 0 and m[3, 4] < 0
+    assert (np.triu(m, 1) == np.float32(-1e9))[np.triu_indices(5, 1)].all()
+    assert (np.tril(m) == 0).all()
+
+
+@pytest.mark.parametrize("seq", [1, 8, 32, 77])
+@pytest.mark.parametrize("wkind", ["q8", "f32"])
+def test_text_layers_graph_all_on_gpu(seq, wkind):
+    from oracle_bind import Ref, have_ref
+    if not have_ref():
+        pytest.skip("oracle/_ref not built")
+    n_layers = 2
+    G, out = build(seq, n_layers, wkind, 1300 + seq)
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G.g) == abi.OK
+        st = be.stats()
+        assert st.host_nodes == 0, f"{st.host_nodes} nodes ran on the host"
+        got = out_array(out, (seq, W))
+    finally:
+        be.close()
+    Gr, orf = build(seq, n_layers, wkind, 1300 + seq, deq_ref=True)
+    R = Ref()
+    assert reference_eval(R, Gr.g, R.pool(8)) == 0
+    ref = out_array(orf, (seq, W))
+    R.close()
+    assert_f32_close(got, ref, floor=1.5e-2 if wkind == "q8" else 2e-3,
+                     what=f"text layers seq {seq} {wkind}")
+
+
+def test_text_chain_forwarded_between_evals_matches_one_eval():
+    """Four layers as two graph_evals of two, the first's output left in HBM
+    and wrapped as the second's input (the reference's batched block loop,
+    text_encoder.c:559-575), equal bit for bit to the four layers in one
+    eval."""
+    seq = 77
+    G1, out1 = build(seq, 4, "q8", 1400)
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G1.g) == abi.OK
+        one = out_array(out1, (seq, W))
+    finally:
+        be.close()
+    O = oracle()
+    xd = hip.DeviceBuffer.of(synth.randn(1400, (seq, W)))
+    mask_h = graph.causal_mask(seq)
+    shapes = {"ln1_w": ((W,), 1.0), "ln1_b": ((W,), 0.1), "qkv_w": ((3 * W, W), 0.03),
+              "qkv_b": ((3 * W,), 0.02), "proj_w": ((W, W), 0.03), "proj_b": ((W,), 0.02),
+              "ln2_w": ((W,), 1.0), "ln2_b": ((W,), 0.1), "fc1_w": ((MLP, W), 0.03),
+              "fc1_b": ((MLP,), 0.02), "fc2_w": ((W, MLP), 0.03), "fc2_b": ((W,), 0.02)}
+    Wg = graph.Graph()
+    params = []
+    for li in range(4):
+        p = {}
+        for i, (name, (shape, std)) in enumerate(shapes.items()):
+            w = synth.randn(1400 + 100 * (li + 1) + i, shape, std)
+            p[name] = (Wg.tensor(abi.Q8_0, shape, O.q8_quantize(w)) if len(shape) == 2
+                       else Wg.tensor(abi.F32, shape, w))
+        params.append(p)
+    mask = Wg.tensor(abi.F32, (seq, seq), mask_h)
+    x = abi.make_tensor(abi.F32, [seq, W], xd.ptr, seq * W * 4)
+    Wg.keep.append(x)
+    graphs = []
+    for b0 in (0, 2):
+        G = graph.Graph()
+        G.keep.append(Wg)
+        for li in (b0, b0 + 1):
+            x = graph.text_layer(G, x, params[li], HEADS, mask)
+        G.g.no_readback = b0 == 0
+        graphs.append(G)
+    be = hip.Backend(0)
+    try:
+        for G in graphs:
+            assert be.graph_eval(G.g) == abi.OK
+        two = out_array(x, (seq, W))
+    finally:
+        be.close()
+        xd.free()
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
