@@ -204,26 +204,6 @@ __global__ void __launch_bounds__(256) cast_f16_k(const void *src, uint16_t *dst
  * lane held in registers between the two passes (rows 16-byte aligned,
  * K % 8 == 0, K <= 512 * CPL); otherwise values are read one at a time,
  * twice. */
-__device__ __forceinline__ float pow2f(int e)
-{
-	return __uint_as_float((uint32_t)(e + 127) << 23); /* -126 <= e <= 127 */
-}
-
-__device__ __forceinline__ int row_scale_exp(float amax)
-{
-	amax = wave_max_f32(amax);
-	if (amax == 0.0f || (amax >= 0x1p-10f && amax < 0x1p15f))
-		return 0;
-	int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 14;
-	return e < -100 ? -100 : e > 113 ? 113 : e;
-}
-
-__device__ __forceinline__ float finite_abs(float x)
-{
-	const float a = __builtin_fabsf(x);
-	return a <= 3.402823466e38f ? a : 0.0f; /* inf and NaN do not set the scale */
-}
-
 template <bool BF16, bool VEC, int CPL, int RPW>
 __global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long long lda_b,
 						       long long sa_b, uint16_t *dst, float *rs,

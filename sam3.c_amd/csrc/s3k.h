@@ -168,6 +168,10 @@ int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_d
  * and below 2^-10). */
 int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
 		   const int *axes, int K, unsigned *ovf, unsigned ovf_tag, void *stream);
+/* Whether the skinny launch of g rounds its f32 / bf16 activations to f16
+ * with per-row power-of-two factors inside the kernel (no row-scaled f16
+ * copy needed first). */
+int s3k_skinny_scales_rows(const struct s3k_gemm *g);
 /* Attention operands [B, H, S, D] (f32), up to three (n_out) in one
  * launch: out[y] from columns col0[y].. of rows of `pitch` values holding
  * [B*S, H*D] (the q, k or v part of a fused qkv output), with RoPE

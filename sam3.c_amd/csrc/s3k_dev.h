@@ -48,6 +48,38 @@ __device__ __forceinline__ float wave_max_f32(float v)
 	return v;
 }
 
+/* 2^e as a float, -126 <= e <= 127 */
+__device__ __forceinline__ float pow2f(int e)
+{
+	return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+/* |x| for the row scale; inf and NaN count as 0 (they do not set it) */
+__device__ __forceinline__ float finite_abs(float x)
+{
+	const float a = __builtin_fabsf(x);
+	return a <= 3.402823466e38f ? a : 0.0f;
+}
+
+/* The exponent e of the power-of-two factor of an f16 copy of a row
+ * whose largest finite |value| is amax (already reduced over the row):
+ * 0 when amax lies in [2^-10, 2^15) or is 0, else the e that puts amax
+ * in [2^14, 2^15), clamped to [-100, 113]. The row is stored as
+ * f16(x * 2^-e) and the product scaled back by 2^e. */
+__device__ __forceinline__ int scale_exp_of(float amax)
+{
+	if (amax == 0.0f || (amax >= 0x1p-10f && amax < 0x1p15f))
+		return 0;
+	int e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 14;
+	return e < -100 ? -100 : e > 113 ? 113 : e;
+}
+
+/* scale_exp_of the largest amax over the wave */
+__device__ __forceinline__ int row_scale_exp(float amax)
+{
+	return scale_exp_of(wave_max_f32(amax));
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t b)
 {
 	return __uint_as_float(b << 16);

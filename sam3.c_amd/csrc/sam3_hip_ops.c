@@ -418,6 +418,8 @@ static int rounds_a_to_f16(const struct s3k_gemm *g, int path)
 {
 	if (g->a_kind == S3K_F16 || (path != S3K_PATH_MFMA && path != S3K_PATH_SKINNY))
 		return 0;
+	if (path == S3K_PATH_SKINNY && s3k_skinny_scales_rows(g))
+		return 0; /* q8_stream scales the rows itself */
 	return g->b_kind == S3K_Q8 || (g->b_kind == S3K_F16 && g->a_kind != S3K_F16);
 }
 

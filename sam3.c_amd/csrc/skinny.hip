@@ -247,7 +247,13 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 {
 	using C = StreamCfg<AK, MR, NT, KC>;
 	constexpr int WV = C::WV;
+	/* f32 / bf16 activations are rounded to f16 at the fragment read: each
+	 * row first gets its power-of-two factor (scale_exp_of, as the
+	 * row-scaled f16 copy uses), 2^-e applied before the rounding and 2^e
+	 * in the epilogue */
+	constexpr bool SCALE = AK != S3K_F16;
 	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+	__shared__ float rsc[SCALE ? 2 * MR : 1];
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 	const int g16 = lane >> 4, l16 = lane & 15;
 
@@ -327,6 +333,50 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		if (s < nch)
 			issue(s);
 
+	/* row factors while the first chunks arrive: TPR lanes of one wave
+	 * per row (every row's loads in flight at once), 4 values per load,
+	 * K a multiple of 256 */
+	float inv[C::MT];
+	if constexpr (SCALE) {
+		constexpr int TPR = MR >= 16 ? 1024 / MR < 64 ? 1024 / MR : 64 : 64;
+		constexpr int RPW = 64 / TPR;                    /* rows per wave */
+		const int m = wave * RPW + lane / TPR, c = lane % TPR;
+		float amax = 0.0f;
+		if (m < Mz) {
+			const char *row = abase + (long long)m * p.lda_b;
+#pragma unroll 8
+			for (int k = c * 4; k < p.K; k += TPR * 4) {
+				float v[4];
+				if constexpr (AK == S3K_F32) {
+					const float4 x = *(const float4 *)(row + (long long)k * 4);
+					v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+				} else {
+					const uint2 x = *(const uint2 *)(row + (long long)k * 2);
+					v[0] = bf16_to_f32(x.x & 0xFFFFu), v[1] = bf16_to_f32(x.x >> 16);
+					v[2] = bf16_to_f32(x.y & 0xFFFFu), v[3] = bf16_to_f32(x.y >> 16);
+				}
+#pragma unroll
+				for (int e = 0; e < 4; ++e)
+					amax = fmaxf(amax, finite_abs(v[e]));
+			}
+		}
+#pragma unroll
+		for (int off = TPR / 2; off > 0; off >>= 1)
+			amax = fmaxf(amax, __shfl_xor(amax, off));
+		if (c == 0 && m < MR && wave * RPW < MR) {
+			const int ex = scale_exp_of(amax);
+			rsc[m] = pow2f(-ex);
+			rsc[MR + m] = pow2f(ex);
+		}
+		__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): the factors are in LDS */
+		wg_barrier();
+#pragma unroll
+		for (int mt = 0; mt < C::MT; ++mt) {
+			const int m = mt * 16 + l16;
+			inv[mt] = m < MR ? rsc[m] : 1.0f;
+		}
+	}
+
 	for (int ch = 0; ch < nch; ++ch) {
 		/* this wave's loads of chunk ch done (younger chunks may fly) */
 		if (ch + C::ST - 2 < nch)
@@ -358,22 +408,25 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 						const int q0 = kb * 8 + 2 * g16;
 						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
 						const uint4 y = *(const uint4 *)(row + (((q0 + 1) ^ (m & 15)) << 4));
+						const float s = inv[mt];
 						af[u][mt] = make_uint4(
-							pack_f16x2(__uint_as_float(x.x), __uint_as_float(x.y)),
-							pack_f16x2(__uint_as_float(x.z), __uint_as_float(x.w)),
-							pack_f16x2(__uint_as_float(y.x), __uint_as_float(y.y)),
-							pack_f16x2(__uint_as_float(y.z), __uint_as_float(y.w)));
+							pack_f16x2(__uint_as_float(x.x) * s, __uint_as_float(x.y) * s),
+							pack_f16x2(__uint_as_float(x.z) * s, __uint_as_float(x.w) * s),
+							pack_f16x2(__uint_as_float(y.x) * s, __uint_as_float(y.y) * s),
+							pack_f16x2(__uint_as_float(y.z) * s, __uint_as_float(y.w) * s));
 					} else {
 						const int q0 = kb * 4 + g16;
 						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
-						if constexpr (AK == S3K_BF16)
+						if constexpr (AK == S3K_BF16) {
+							const float s = inv[mt];
 							af[u][mt] = make_uint4(
-								pack_f16x2(bf16_to_f32(x.x & 0xFFFF), bf16_to_f32(x.x >> 16)),
-								pack_f16x2(bf16_to_f32(x.y & 0xFFFF), bf16_to_f32(x.y >> 16)),
-								pack_f16x2(bf16_to_f32(x.z & 0xFFFF), bf16_to_f32(x.z >> 16)),
-								pack_f16x2(bf16_to_f32(x.w & 0xFFFF), bf16_to_f32(x.w >> 16)));
-						else
+								pack_f16x2(bf16_to_f32(x.x & 0xFFFF) * s, bf16_to_f32(x.x >> 16) * s),
+								pack_f16x2(bf16_to_f32(x.y & 0xFFFF) * s, bf16_to_f32(x.y >> 16) * s),
+								pack_f16x2(bf16_to_f32(x.z & 0xFFFF) * s, bf16_to_f32(x.z >> 16) * s),
+								pack_f16x2(bf16_to_f32(x.w & 0xFFFF) * s, bf16_to_f32(x.w >> 16) * s));
+						} else {
 							af[u][mt] = x;
+						}
 					}
 				}
 			}
@@ -439,6 +492,8 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		const int n = n0 + t * 16 + (ln & 15);
 		if (m >= Mz || n >= p.N)
 			continue;
+		if constexpr (SCALE)
+			s *= rsc[MR + m];
 		if (p.flags & S3K_EPI_ROWSCALE)
 			s *= p.rs[blockIdx.y * p.rs_sb + m0 + m];
 		const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
@@ -468,6 +523,15 @@ static bool stream_ok(const struct s3k_gemm *g)
 	if (g->batch > 1 && (g->stride_b % 16 || (g->stride_a * es) % 16))
 		return false;
 	return true;
+}
+
+/* Whether the skinny launch of g rounds f32 / bf16 activations to f16
+ * with per-row power-of-two factors itself (q8_stream), so that no
+ * row-scaled f16 copy is needed before it. */
+extern "C" int s3k_skinny_scales_rows(const struct s3k_gemm *g)
+{
+	return (g->a_kind == S3K_F32 || g->a_kind == S3K_BF16) && stream_ok(g) &&
+	       !(g->flags & S3K_EPI_ROWSCALE);
 }
 
 extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
