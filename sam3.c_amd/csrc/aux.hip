@@ -34,12 +34,8 @@ __device__ __forceinline__ uint32_t q8_pair_to_f16(uint32_t d, int sh, float s)
 	       (f32_to_f16((float)(int)(int8_t)(d >> (sh + 8)) * s) << 16);
 }
 
-__global__ void __launch_bounds__(256) q8_expand_nk_k(const char *blk, uint16_t *out,
-						      long long nchunk)
+__device__ __forceinline__ void expand_chunk(const char *blk, uint16_t *out, long long t)
 {
-	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-	if (t >= nchunk)
-		return;
 	const char *b = blk + (t >> 2) * 36;
 	const int part = (int)(t & 3);
 	const float s = *(const float *)b;
@@ -47,6 +43,14 @@ __global__ void __launch_bounds__(256) q8_expand_nk_k(const char *blk, uint16_t 
 	const uint32_t d1 = *(const uint32_t *)(b + 8 + 8 * part);
 	((uint4 *)out)[t] = make_uint4(q8_pair_to_f16(d0, 0, s), q8_pair_to_f16(d0, 16, s),
 				       q8_pair_to_f16(d1, 0, s), q8_pair_to_f16(d1, 16, s));
+}
+
+__global__ void __launch_bounds__(256) q8_expand_nk_k(const char *blk, uint16_t *out,
+						      long long nchunk)
+{
+	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+	if (t < nchunk)
+		expand_chunk(blk, out, t);
 }
 
 /* One thread per output of f16 [N,K]; element (n,k) reads block lin/32
@@ -204,94 +208,114 @@ __global__ void __launch_bounds__(256) cast_f16_k(const void *src, uint16_t *dst
  * lane held in registers between the two passes (rows 16-byte aligned,
  * K % 8 == 0, K <= 512 * CPL); otherwise values are read one at a time,
  * twice. */
-template <bool BF16, bool VEC, int CPL, int RPW>
+/* One row of K values (16-byte chunks of 8, up to CPL per lane) to f16
+ * with its row factor, by one wave: every load first, then the row's
+ * largest |value|, then the stores. */
+template <bool BF16, int CPL>
+__device__ __forceinline__ void cast_row_vec(const char *xrow, uint16_t *y, float *rsp, int K,
+					     int lane)
+{
+	constexpr int L = BF16 ? 1 : 2;
+	const int chunks = K / 8;
+	const uint4 *x = (const uint4 *)xrow;
+	uint4 v[CPL][L];
+#pragma unroll
+	for (int u = 0; u < CPL; ++u) {
+		const int c = lane + 64 * u;
+#pragma unroll
+		for (int l = 0; l < L; ++l)
+			v[u][l] = c < chunks ? x[c * L + l] : make_uint4(0, 0, 0, 0);
+	}
+	float f[CPL][8];
+	float amax = 0.0f;
+#pragma unroll
+	for (int u = 0; u < CPL; ++u) {
+		if constexpr (BF16) {
+			const uint32_t w[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
+#pragma unroll
+			for (int e = 0; e < 4; ++e) {
+				f[u][2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
+				f[u][2 * e + 1] = bf16_to_f32(w[e] >> 16);
+			}
+		} else {
+#pragma unroll
+			for (int l = 0; l < 2; ++l) {
+				f[u][4 * l] = __uint_as_float(v[u][l].x);
+				f[u][4 * l + 1] = __uint_as_float(v[u][l].y);
+				f[u][4 * l + 2] = __uint_as_float(v[u][l].z);
+				f[u][4 * l + 3] = __uint_as_float(v[u][l].w);
+			}
+		}
+#pragma unroll
+		for (int e = 0; e < 8; ++e)
+			amax = fmaxf(amax, finite_abs(f[u][e]));
+	}
+	const int ex = row_scale_exp(amax);
+	const float inv = pow2f(-ex);
+#pragma unroll
+	for (int u = 0; u < CPL; ++u) {
+		const int c = lane + 64 * u;
+		if (c < chunks)
+			((uint4 *)y)[c] = make_uint4(pack_f16x2(f[u][0] * inv, f[u][1] * inv),
+						     pack_f16x2(f[u][2] * inv, f[u][3] * inv),
+						     pack_f16x2(f[u][4] * inv, f[u][5] * inv),
+						     pack_f16x2(f[u][6] * inv, f[u][7] * inv));
+	}
+	if (lane == 0)
+		*rsp = pow2f(ex);
+}
+
+/* One row per wave, four rows per workgroup. With VEC the row moves in
+ * 16-byte chunks (cast_row_vec); otherwise values are read one at a
+ * time, twice. */
+template <bool BF16, bool VEC, int CPL>
 __global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long long lda_b,
 						       long long sa_b, uint16_t *dst, float *rs,
 						       int M, int K)
 {
 	const int lane = threadIdx.x & 63;
-	const int m0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
-	if (m0 >= M)
+	const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (m >= M)
 		return;
-	const char *xb = src + (long long)blockIdx.y * sa_b;
+	const char *x = src + (long long)blockIdx.y * sa_b + (long long)m * lda_b;
+	const long long row = (long long)blockIdx.y * M + m;
+	uint16_t *y = dst + row * K;
 	if constexpr (VEC) {
-		constexpr int L = BF16 ? 1 : 2;
-		const int chunks = K / 8;
-		/* every load of the wave's rows first (RPW * CPL * L per lane) */
-		uint4 v[RPW][CPL][L];
-#pragma unroll
-		for (int r = 0; r < RPW; ++r) {
-			const uint4 *x = (const uint4 *)(xb + (long long)(m0 + r) * lda_b);
-#pragma unroll
-			for (int u = 0; u < CPL; ++u) {
-				const int c = lane + 64 * u;
-#pragma unroll
-				for (int l = 0; l < L; ++l)
-					v[r][u][l] = (m0 + r < M && c < chunks) ? x[c * L + l]
-										 : make_uint4(0, 0, 0, 0);
-			}
-		}
-#pragma unroll
-		for (int r = 0; r < RPW; ++r) {
-			if (m0 + r >= M)
-				break;
-			float f[CPL][8];
-			float amax = 0.0f;
-#pragma unroll
-			for (int u = 0; u < CPL; ++u) {
-				if constexpr (BF16) {
-					const uint32_t w[4] = {v[r][u][0].x, v[r][u][0].y, v[r][u][0].z, v[r][u][0].w};
-#pragma unroll
-					for (int e = 0; e < 4; ++e) {
-						f[u][2 * e] = bf16_to_f32(w[e] & 0xFFFFu);
-						f[u][2 * e + 1] = bf16_to_f32(w[e] >> 16);
-					}
-				} else {
-#pragma unroll
-					for (int l = 0; l < 2; ++l) {
-						f[u][4 * l] = __uint_as_float(v[r][u][l].x);
-						f[u][4 * l + 1] = __uint_as_float(v[r][u][l].y);
-						f[u][4 * l + 2] = __uint_as_float(v[r][u][l].z);
-						f[u][4 * l + 3] = __uint_as_float(v[r][u][l].w);
-					}
-				}
-#pragma unroll
-				for (int e = 0; e < 8; ++e)
-					amax = fmaxf(amax, finite_abs(f[u][e]));
-			}
-			const int ex = row_scale_exp(amax);
-			const float inv = pow2f(-ex);
-			const long long row = (long long)blockIdx.y * M + m0 + r;
-			uint16_t *y = dst + row * K;
-#pragma unroll
-			for (int u = 0; u < CPL; ++u) {
-				const int c = lane + 64 * u;
-				if (c < chunks)
-					((uint4 *)y)[c] = make_uint4(pack_f16x2(f[u][0] * inv, f[u][1] * inv),
-								     pack_f16x2(f[u][2] * inv, f[u][3] * inv),
-								     pack_f16x2(f[u][4] * inv, f[u][5] * inv),
-								     pack_f16x2(f[u][6] * inv, f[u][7] * inv));
-			}
-			if (lane == 0)
-				rs[row] = pow2f(ex);
-		}
+		cast_row_vec<BF16, CPL>(x, y, rs + row, K, lane);
 	} else {
-		for (int r = 0; r < RPW && m0 + r < M; ++r) {
-			const char *x = xb + (long long)(m0 + r) * lda_b;
-			float amax = 0.0f;
-			for (int k = lane; k < K; k += 64)
-				amax = fmaxf(amax, finite_abs(BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
-								: ((const float *)x)[k]));
-			const int ex = row_scale_exp(amax);
-			const float inv = pow2f(-ex);
-			const long long row = (long long)blockIdx.y * M + m0 + r;
-			uint16_t *y = dst + row * K;
-			for (int k = lane; k < K; k += 64)
-				y[k] = (uint16_t)f32_to_f16((BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
-							     : ((const float *)x)[k]) * inv);
-			if (lane == 0)
-				rs[row] = pow2f(ex);
-		}
+		float amax = 0.0f;
+		for (int k = lane; k < K; k += 64)
+			amax = fmaxf(amax, finite_abs(BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+							: ((const float *)x)[k]));
+		const int ex = row_scale_exp(amax);
+		const float inv = pow2f(-ex);
+		for (int k = lane; k < K; k += 64)
+			y[k] = (uint16_t)f32_to_f16((BF16 ? bf16_to_f32(((const uint16_t *)x)[k])
+						     : ((const float *)x)[k]) * inv);
+		if (lane == 0)
+			rs[row] = pow2f(ex);
+	}
+}
+
+/* The row cast of A and the expansion of a Q8_0 weight in one launch:
+ * workgroups [0, row_wgs) cast four rows each, the rest expand 256
+ * output chunks each. The two are independent and short, so one launch
+ * lets them overlap instead of paying two dispatch ramps. */
+template <bool BF16, int CPL>
+__global__ void __launch_bounds__(256) cast_expand_k(const char *src, long long lda_b,
+						     uint16_t *dst, float *rs, int M, int K,
+						     const char *blk, uint16_t *wout, long long nchunk,
+						     int row_wgs)
+{
+	if ((int)blockIdx.x < row_wgs) {
+		const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+		if (m < M)
+			cast_row_vec<BF16, CPL>(src + (long long)m * lda_b, dst + (long long)m * K, rs + m,
+						K, threadIdx.x & 63);
+	} else {
+		const long long t = (long long)(blockIdx.x - row_wgs) * 256 + threadIdx.x;
+		if (t < nchunk)
+			expand_chunk(blk, wout, t);
 	}
 }
 
@@ -504,18 +528,64 @@ static int cast_rows_launch(const char *src, long long lda_b, long long sa_b, ui
 	const int cpl = (K / 8 + 63) / 64;
 	const dim3 grid((unsigned)((M + 3) / 4), (unsigned)batch);
 	if (!vec || cpl > 8)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, false, 1, 1>), grid, dim3(256), 0, st, src,
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, false, 1>), grid, dim3(256), 0, st, src,
 				   lda_b, sa_b, dst, rs, M, K);
 	else if (cpl <= 2)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2, 1>), grid, dim3(256), 0, st, src,
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 2>), grid, dim3(256), 0, st, src,
 				   lda_b, sa_b, dst, rs, M, K);
 	else if (cpl <= 4)
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 4, 1>), grid, dim3(256), 0, st, src,
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 4>), grid, dim3(256), 0, st, src,
 				   lda_b, sa_b, dst, rs, M, K);
 	else
-		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 8, 1>), grid, dim3(256), 0, st, src,
+		hipLaunchKernelGGL((cast_f16_rows_k<BF16, true, 8>), grid, dim3(256), 0, st, src,
 				   lda_b, sa_b, dst, rs, M, K);
 	return (int)hipGetLastError();
+}
+
+template <bool BF16>
+static int cast_expand_launch(const char *src, long long lda_b, uint16_t *dst, float *rs, int M,
+			      int K, const char *blk, uint16_t *wout, long long nchunk,
+			      hipStream_t st)
+{
+	const int cpl = (K / 8 + 63) / 64;
+	const int row_wgs = (M + 3) / 4;
+	const long long wgs = row_wgs + (nchunk + 255) / 256;
+	const dim3 grid((unsigned)wgs);
+	if (cpl <= 2)
+		hipLaunchKernelGGL((cast_expand_k<BF16, 2>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
+				   M, K, blk, wout, nchunk, row_wgs);
+	else if (cpl <= 4)
+		hipLaunchKernelGGL((cast_expand_k<BF16, 4>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
+				   M, K, blk, wout, nchunk, row_wgs);
+	else
+		hipLaunchKernelGGL((cast_expand_k<BF16, 8>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
+				   M, K, blk, wout, nchunk, row_wgs);
+	return (int)hipGetLastError();
+}
+
+/* A (f32 or bf16 [M, K], pitch lda elements) to row-scaled f16 rows plus
+ * factors (as s3k_cast_f16_rows, one batch), and W (Q8_0 [N, K]) to f16
+ * [N, K] (as s3k_q8_nk_to_f16_nk), in one launch. hipErrorInvalidValue
+ * when the shapes or alignments do not allow it (K % 32, K > 4096,
+ * 16-byte rows): the caller then uses the two separate launches. */
+extern "C" int s3k_cast_rows_expand(int kind, const void *src, long long lda, void *dst, float *rs,
+				    int M, int K, const void *wblk, void *wout, int N, void *stream)
+{
+	const int es = kind == S3K_F32 ? 4 : 2;
+	if ((kind != S3K_F32 && kind != S3K_BF16) || M <= 0 || N <= 0 || K <= 0 || K % 32 ||
+	    K > 4096 || M > (1 << 28) || (lda * es) % 16 || lda < K ||
+	    (((uintptr_t)src | (uintptr_t)dst | (uintptr_t)wout) & 15u) || ((uintptr_t)wblk & 3u) ||
+	    !rs)
+		return (int)hipErrorInvalidValue;
+	const long long nchunk = (long long)N * K / 8;
+	if ((M + 3) / 4 + (nchunk + 255) / 256 > 0x7FFFFFFFLL)
+		return (int)hipErrorInvalidValue;
+	hipStream_t st = (hipStream_t)stream;
+	return kind == S3K_BF16
+		? cast_expand_launch<true>((const char *)src, lda * es, (uint16_t *)dst, rs, M, K,
+					   (const char *)wblk, (uint16_t *)wout, nchunk, st)
+		: cast_expand_launch<false>((const char *)src, lda * es, (uint16_t *)dst, rs, M, K,
+					    (const char *)wblk, (uint16_t *)wout, nchunk, st);
 }
 
 extern "C" int s3k_cast_f16_rows(int kind, const void *src, long long lda, long long sa, void *dst,

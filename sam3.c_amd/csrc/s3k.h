@@ -114,6 +114,11 @@ int s3k_cast(int src_kind, int dst_kind, const void *src, void *dst, long long n
 	     void *stream);
 /* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
 int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
+/* s3k_cast_f16_rows (one batch) and s3k_q8_nk_to_f16_nk of an [N, K]
+ * weight in one launch; hipErrorInvalidValue when K % 32, K > 4096 or an
+ * alignment rules it out (then run the two separately). */
+int s3k_cast_rows_expand(int kind, const void *src, long long lda, void *dst, float *rs, int M,
+			 int K, const void *wblk, void *wout, int N, void *stream);
 /*
  * Activations for a GEMM that rounds them to f16, row by row: batch
  * slices (at element stride sa) of M rows of K values (pitch lda) ->

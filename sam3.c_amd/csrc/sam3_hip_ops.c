@@ -578,12 +578,61 @@ static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 	return s3h_hip(s3k_gemm_launch_path(h, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
 }
 
+/* Whether q8_f16_gemm of h expands the weight for this call alone (not a
+ * cached constant weight). */
+static int q8_expands_per_call(const struct s3k_gemm *h)
+{
+	const int mode = s3h_settings()->q8_expand;
+	const size_t q8_bytes = (size_t)h->N * (h->K / 32) * 36;
+	return (h->flags & S3K_B_NT) && h->K % 32 == 0 && h->batch == 1 && mode != 0 &&
+	       (mode == 1 || h->M >= S3H_Q8_EXPAND_MIN_M) && !s3h_prep_cacheable(h->b, q8_bytes) &&
+	       !s3h_prep_find(h->b, S3H_PREP_Q8_F16, h->N, h->K);
+}
+
 /* f32/bf16 activations times Q8_0 [N,K] weights on the direct-to-LDS Q8
  * GEMM (or the f16 GEMM on expanded weights): the activations are copied
- * to f16 once, row-scaled (a_rows_f16), then the GEMM runs on f16 A. */
+ * to f16 once, row-scaled (a_rows_f16), then the GEMM runs on f16 A.
+ * When the weight is expanded for this call only, the copy and the
+ * expansion are one launch (s3k_cast_rows_expand). */
 static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 {
 	struct s3k_gemm h = *g;
+	if (q8_expands_per_call(&h) && h.batch == 1) {
+		size_t a_bytes;
+		const size_t abuf = a_rows_f16_bytes(&h, &a_bytes);
+		const size_t wbytes = (size_t)h.N * h.K * 2;
+		void *buf = NULL;
+		enum sam3_error err = s3h_scratch_alloc(&buf, a_bytes + ((abuf - a_bytes + 255) & ~(size_t)255) + wbytes, stream);
+		if (err != SAM3_OK)
+			return err;
+		float *rs = (float *)((char *)buf + a_bytes);
+		uint16_t *w16 = (uint16_t *)((char *)buf + a_bytes +
+					     ((abuf - a_bytes + 255) & ~(size_t)255));
+		const int e = s3k_cast_rows_expand(h.a_kind, h.a, h.lda, buf, rs, h.M, h.K, h.b, w16, h.N,
+						   stream);
+		if (e == (int)hipSuccess) {
+			h.a = buf;
+			h.a_kind = S3K_F16;
+			h.lda = h.K;
+			h.stride_a = 0;
+			h.rs = rs;
+			h.rs_sb = 0;
+			h.flags |= S3K_EPI_ROWSCALE;
+			h.b = w16;
+			h.b_kind = S3K_F16;
+			h.ldb = h.K;
+			err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream),
+				      "matmul_q8 f16 gemm");
+			enum sam3_error ferr = s3h_scratch_free(buf, stream);
+			return err != SAM3_OK ? err : ferr;
+		}
+		(void)hipGetLastError();
+		err = s3h_scratch_free(buf, stream);
+		if (err != SAM3_OK)
+			return err;
+		if (e != (int)hipErrorInvalidValue)
+			return s3h_hip(e, "matmul_q8 cast + expand");
+	}
 	void *tmp = NULL;
 	enum sam3_error err = a_rows_f16(&h, &tmp, stream);
 	if (err == SAM3_OK)

@@ -53,6 +53,7 @@ def assert_rows_close(got, ref, rtol=1e-3, what=""):
     (77, 96, 256, hip.PATH_SKINNY),       # not a multiple of 256: q8_skinny
     (300, 1024, 512, hip.PATH_MFMA),      # direct-to-LDS Q8 GEMM
     (300, 96, 256, hip.PATH_MFMA),        # K % 64 != 0: register-staged GEMM
+    (3072, 1024, 256, hip.PATH_MFMA),     # per-call expansion: cast + expand in one launch
 ])
 def test_f32_activations_wide_range_nt(M, K, N, want):
     O = oracle()
