@@ -54,12 +54,15 @@ constexpr int AT_VT_PITCH = AT_BKV * 2 + 8;          /* bytes per V^T row */
 constexpr int AT_K_BYTES = AT_BKV * AT_D * 2;        /* 8 KiB per plane */
 constexpr int AT_VT_BYTES = AT_D * AT_VT_PITCH;      /* 8.5 KiB per plane */
 
-template <int DT, int NW>
+/* VD: V tiles by direct-to-LDS loads, row-major [key][d], read as the
+ * V^T operand with transposing LDS reads (16-bit inputs); else staged
+ * through registers into a V^T tile */
+template <int DT, int NW, bool VD = false>
 struct AtCfg {
 	static constexpr bool SPLIT = DT == S3K_F32;
 	static constexpr int NPL = SPLIT ? 2 : 1;        /* bf16 planes */
 	static constexpr int KS = NPL * AT_K_BYTES;      /* one K slot */
-	static constexpr int VS = NPL * AT_VT_BYTES;     /* one V^T slot */
+	static constexpr int VS = VD ? AT_K_BYTES : NPL * AT_VT_BYTES; /* one V slot */
 	static constexpr int LDS = 2 * KS + 2 * VS;      /* two of each */
 	static constexpr int FAM = DT == S3K_F16 ? FAM_F16 : FAM_BF16;
 	static constexpr int BQ = 32 * NW;                /* queries per workgroup */
@@ -87,6 +90,28 @@ __device__ __forceinline__ float at_sum2(uint32_t w, float acc)
 		const s3k_bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 		return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s3k_bf16x2, w), one, acc, false);
 	}
+}
+
+/* Chunk swizzle of a direct-to-LDS V tile row: it depends on the key's
+ * low four bits only, so the transposed reads of the four 16-key chunks
+ * of a tile differ by a constant offset. */
+__device__ __forceinline__ int at_vswz(int key)
+{
+	const int r = key & 15;
+	return (r ^ (r >> 3)) & 7;
+}
+
+typedef short at_v4i16 __attribute__((ext_vector_type(4)));
+
+/* ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
+ * element i % 4 of the 8 bytes addressed by lanes i / 4, 4 + i / 4,
+ * 8 + i / 4 and 12 + i / 4 (measured on gfx950). */
+__device__ __forceinline__ uint2 at_read_tr(const char *smem, unsigned off)
+{
+	const at_v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+		(__attribute__((address_space(3))) at_v4i16 *)((__attribute__((address_space(3))) char *)
+								       smem + off));
+	return __builtin_bit_cast(uint2, r);
 }
 
 /* x combined with the value of lane ^ 32 (v_permlane32_swap) */
@@ -121,7 +146,7 @@ __device__ __forceinline__ void at_split8(const float4 &x, const float4 &y, uint
  * variant spills: three (12 waves, 168 VGPRs) for the 16-bit kernel
  * without a mask, two for f32 or a mask, one for f32 with a mask (its
  * mask tile, score halves and hi/lo operand planes need 256+ VGPRs) */
-template <int DT, int NW, bool MASK>
+template <int DT, int NW, bool MASK, bool VD = false>
 constexpr int at_minb()
 {
 	return NW != 4 ? 1 : (DT == S3K_F32 && MASK) ? 1 : (DT == S3K_F32 || MASK) ? 2 : 3;
@@ -140,10 +165,11 @@ struct at_int {
  * then below 2^15, inside the f16 range. */
 constexpr float AT_PSUM_MAX = 32768.0f;
 
-template <int DT, int NW, bool MASK>
-__global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(AttnArgs p)
+template <int DT, int NW, bool MASK, bool VD>
+__global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK, VD>())) attn_fwd(AttnArgs p)
 {
-	using C = AtCfg<DT, NW>;
+	using C = AtCfg<DT, NW, VD>;
+	static_assert(!VD || !C::SPLIT, "V by direct-to-LDS loads for 16-bit inputs");
 	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -239,6 +265,31 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(A
 		}
 	};
 
+	/* 16-bit V tile (VD): like K, 8 direct-to-LDS instructions, slot s of
+	 * instruction j holding key row s/8, chunk (s%8) ^ at_vswz(row) */
+	const s3k_i32x4 rv = buf_rsrc(p.v + head * p.hk * ES, kv_bytes);
+	unsigned v_off[VD ? C::KJ : 1];
+	if constexpr (VD) {
+#pragma unroll
+		for (int t = 0; t < C::KJ; ++t) {
+			const int s = (wave + t * NW) * 64 + lane;
+			const int row = s / 8, c = (s % 8) ^ at_vswz(row);
+			v_off[t] = (unsigned)(row * AT_D * 2 + c * 16);
+		}
+	}
+	auto issue_v = [&](int kt, unsigned slot) {
+		const int rows_left = p.Sk - kt * AT_BKV;
+#pragma unroll
+		for (int t = 0; t < C::KJ; ++t) {
+			const int j = wave + t * NW;
+			if (j < 8) {
+				const int row = (j * 64 + lane) / 8;
+				const unsigned o = row < rows_left ? v_off[t] : S3K_OOB;
+				dma16s(lds0 + slot + j * 1024, rv, o, (unsigned)kt * TILE_BYTES);
+			}
+		}
+	};
+
 	/* staging through registers (threads 0..255): f32 K row t/4, d
 	 * 16*(t%4)..+15; V keys 4*(t/16)..+3, d 4*(t%16)..+3 */
 	const int kr0 = (threadIdx.x & 255) >> 2, kd0 = 16 * (threadIdx.x & 3);
@@ -318,6 +369,23 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(A
 			ka[c][mb] = lds0 + (unsigned)((row * 8 + ((2 * c + h) ^ lds_swz<8>(row))) << 4);
 		}
 	const unsigned va = lds0 + (unsigned)(l32 * AT_VT_PITCH + 8 * h);
+	/* VD: the V^T operand of O^T += V^T P^T for row d = 32 md + l32 and keys
+	 * 16 cc + 4h + {0..3} (lo) / {8..11} (hi) by transposed reads: lane q of
+	 * a 16-lane group G addresses key 4 (G >> 1) + q / 4 (+ 8 for hi), d
+	 * 32 md + 16 (G & 1) + 4 (q % 4); chunk cc adds 16 rows (2 KiB) */
+	unsigned vtr[2][2];
+	if constexpr (VD) {
+		const int G = lane >> 4, q = lane & 15;
+#pragma unroll
+		for (int md = 0; md < 2; ++md)
+#pragma unroll
+			for (int hl = 0; hl < 2; ++hl) {
+				const int key = 4 * (G >> 1) + (q >> 2) + 8 * hl;
+				const int d = 32 * md + 16 * (G & 1) + 4 * (q & 3);
+				vtr[md][hl] = (unsigned)(key * AT_D * 2 +
+							 (((d >> 3) ^ at_vswz(key)) << 4) + ((d >> 2) & 1) * 8);
+			}
+	}
 
 	const float *mrow = MASK ? p.mask + (long long)(q < p.Sq ? q : p.Sq - 1) * p.Sk : nullptr;
 
@@ -347,7 +415,9 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(A
 		if (more) {
 			if constexpr (!C::SPLIT)
 				issue_k(kt + 1, KNEXT);
-			if (stager)
+			if constexpr (VD)
+				issue_v(kt + 1, VNEXT);
+			else if (stager)
 				load_kv(kt + 1);
 		}
 
@@ -473,8 +543,14 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(A
 					const char *vrow = smem + (va - lds0) + VSLOT + md * 32 * AT_VT_PITCH;
 #pragma unroll
 					for (int cc = 2 * mb; cc < 2 * mb + 2; ++cc) {
-						const uint2 lo = *(const uint2 *)(vrow + 32 * cc);
-						const uint2 hi = *(const uint2 *)(vrow + 32 * cc + 16);
+						uint2 lo, hi;
+						if constexpr (VD) {
+							lo = at_read_tr(smem, VSLOT + cc * 2048 + vtr[md][0]);
+							hi = at_read_tr(smem, VSLOT + cc * 2048 + vtr[md][1]);
+						} else {
+							lo = *(const uint2 *)(vrow + 32 * cc);
+							hi = *(const uint2 *)(vrow + 32 * cc + 16);
+						}
 						const uint4 vh = make_uint4(lo.x, lo.y, hi.x, hi.y);
 						if constexpr (C::SPLIT) {
 							const uint2 llo = *(const uint2 *)(vrow + AT_VT_BYTES + 32 * cc);
@@ -499,14 +575,18 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK>())) attn_fwd(A
 			pv_half(1);
 		}
 
-		if (more && stager)
-			store_kv(KNEXT, VNEXT);
+		if constexpr (!VD) {
+			if (more && stager)
+				store_kv(KNEXT, VNEXT);
+		}
 	};
 
 	/* prologue: tile 0 into slot 0 */
 	if constexpr (!C::SPLIT)
 		issue_k(0, 0);
-	if (stager) {
+	if constexpr (VD) {
+		issue_v(0, 2 * C::KS);
+	} else if (stager) {
 		load_kv(0);
 		store_kv(0, 2 * C::KS);
 	}
@@ -749,29 +829,34 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 	p.nqb = (Sq + 32 * nw - 1) / (32 * nw);
 	const dim3 grid((unsigned)((long long)p.nqb * BH));
 	const dim3 block(64 * nw);
-#define S3K_ATTN_GO(DT_, NW_)                                                               \
+#define S3K_ATTN_GO(DT_, NW_, VD_)                                                          \
 	do {                                                                                 \
 		if (mask)                                                                    \
-			hipLaunchKernelGGL((attn_fwd<DT_, NW_, true>), grid, block, 0, st, p);   \
+			hipLaunchKernelGGL((attn_fwd<DT_, NW_, true, VD_>), grid, block, 0, st, p);  \
 		else                                                                         \
-			hipLaunchKernelGGL((attn_fwd<DT_, NW_, false>), grid, block, 0, st, p);  \
+			hipLaunchKernelGGL((attn_fwd<DT_, NW_, false, VD_>), grid, block, 0, st, p); \
 	} while (0)
+	const bool vd = s3h_settings()->attn_vdma != 0;
 	if (kind == S3K_F32)
-		S3K_ATTN_GO(S3K_F32, 4);
+		S3K_ATTN_GO(S3K_F32, 4, false);
 	else if (kind == S3K_BF16) {
-		if (nw == 4)
-			S3K_ATTN_GO(S3K_BF16, 4);
+		if (nw == 4 && vd)
+			S3K_ATTN_GO(S3K_BF16, 4, true);
+		else if (nw == 4)
+			S3K_ATTN_GO(S3K_BF16, 4, false);
 		else if (nw == 6)
-			S3K_ATTN_GO(S3K_BF16, 6);
+			S3K_ATTN_GO(S3K_BF16, 6, false);
 		else
-			S3K_ATTN_GO(S3K_BF16, 8);
+			S3K_ATTN_GO(S3K_BF16, 8, false);
 	} else {
-		if (nw == 4)
-			S3K_ATTN_GO(S3K_F16, 4);
+		if (nw == 4 && vd)
+			S3K_ATTN_GO(S3K_F16, 4, true);
+		else if (nw == 4)
+			S3K_ATTN_GO(S3K_F16, 4, false);
 		else if (nw == 6)
-			S3K_ATTN_GO(S3K_F16, 6);
+			S3K_ATTN_GO(S3K_F16, 6, false);
 		else
-			S3K_ATTN_GO(S3K_F16, 8);
+			S3K_ATTN_GO(S3K_F16, 8, false);
 	}
 #undef S3K_ATTN_GO
 	return (int)hipGetLastError();

@@ -245,6 +245,9 @@ int s3k_transpose2d(int esize, const void *src, void *dst, int batch, int rows,
 struct s3h_settings {
 	int dl_cfg, dlq8_cfg, conv_cfg;   /* SAM3_HIP_{DL,DLQ8,CONV}_CFG        */
 	int attn_nw;                      /* SAM3_HIP_ATTN_NW: waves per SDPA wg */
+	int attn_vdma;                    /* SAM3_HIP_ATTN_VDMA: 16-bit SDPA V tiles by
+					   * direct-to-LDS loads (1, default) or
+					   * through registers (0) */
 	int sk_mr, sk_nt;                 /* SAM3_HIP_SK_CFG "mr,nt"             */
 	int q8_expand;                    /* SAM3_HIP_Q8_EXPAND: -1 auto, 0, 1   */
 	int q8_f32cast;                   /* SAM3_HIP_Q8_F32CAST                 */

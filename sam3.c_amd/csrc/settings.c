@@ -40,6 +40,7 @@ static void parse(struct s3h_settings *s)
 	s->dlq8_cfg = env_int("SAM3_HIP_DLQ8_CFG", -1);
 	s->conv_cfg = env_int("SAM3_HIP_CONV_CFG", -1);
 	s->attn_nw = env_int("SAM3_HIP_ATTN_NW", 4);
+	s->attn_vdma = env_int("SAM3_HIP_ATTN_VDMA", 1);
 	s->sk_mr = s->sk_nt = 0;
 	const char *sk = getenv("SAM3_HIP_SK_CFG");
 	if (sk && sscanf(sk, "%d,%d", &s->sk_mr, &s->sk_nt) != 2)

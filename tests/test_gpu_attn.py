@@ -126,6 +126,30 @@ def test_sdpa_mask(dt, Sk):
     check(dt, got, ref, f"sdpa mask {DT_ID[dt]} Sk={Sk}")
 
 
+@pytest.mark.parametrize("dt", [abi.BF16, abi.F16], ids=lambda d: DT_ID[d])
+@pytest.mark.parametrize("BH,Sq,Sk,masked", [(3, 150, 70, True), (2, 129, 65, False),
+                                             (8, 576, 576, False), (1, 200, 1000, True),
+                                             (2, 256, 5184, False), (2, 1, 1, False)])
+def test_sdpa_v_tiles_by_dma_same_bits(env, dt, BH, Sq, Sk, masked):
+    """16-bit V tiles by direct-to-LDS loads read with ds_read_b64_tr_b16
+    (the default) give the same MFMA operands as V staged through
+    registers into a transposed tile (SAM3_HIP_ATTN_VDMA=0): the same bits,
+    ragged key tails and masks included."""
+    q, k, v = inputs(980 + Sq + Sk, BH, Sq, Sk, 64)
+    mask = None
+    if masked:
+        mask = synth.randn(990 + Sk, (Sq, Sk), 2.0)
+        mask[::5, ::3] = -np.inf
+    qd, _ = to_dtype(q, dt)
+    kd, _ = to_dtype(k, dt)
+    vd, _ = to_dtype(v, dt)
+    env.unset("SAM3_HIP_ATTN_VDMA")
+    dma = hip.sdpa(qd, kd, vd, mask, dtype=dt, path=MFMA)
+    env.set("SAM3_HIP_ATTN_VDMA", 0)
+    staged = hip.sdpa(qd, kd, vd, mask, dtype=dt, path=MFMA)
+    assert np.array_equal(np.asarray(dma).view(np.uint16), np.asarray(staged).view(np.uint16))
+
+
 @pytest.mark.parametrize("dt", DTS, ids=lambda d: DT_ID[d])
 def test_sdpa_sharp_softmax(dt):
     """Scores with a spread of ~100 (q scaled by 12): the running max and
