@@ -247,13 +247,13 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 {
 	using C = StreamCfg<AK, MR, NT, KC>;
 	constexpr int WV = C::WV;
-	/* f32 / bf16 activations are rounded to f16 at the fragment read: each
-	 * row first gets its power-of-two factor (scale_exp_of, as the
-	 * row-scaled f16 copy uses), 2^-e applied before the rounding and 2^e
-	 * in the epilogue */
+	/* f32 / bf16 activations are rounded to f16 at the fragment read with
+	 * a power-of-two factor per row (scale_exp_of, as the row-scaled f16
+	 * copy uses): 2^-e before the rounding, 2^e in the epilogue */
 	constexpr bool SCALE = AK != S3K_F16;
 	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
 	__shared__ float rsc[SCALE ? 2 * MR : 1];
+	__shared__ float rmx[SCALE ? C::WV * MR : 1];
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 	const int g16 = lane >> 4, l16 = lane & 15;
 
@@ -321,147 +321,163 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 	};
 
 	s3k_f32x4 acc[NT][C::MT];
-#pragma unroll
-	for (int t = 0; t < NT; ++t)
-#pragma unroll
-		for (int mt = 0; mt < C::MT; ++mt)
-			acc[t][mt] = (s3k_f32x4){0.f, 0.f, 0.f, 0.f};
-
 	const int nch = p.K / (KC * 32);
-#pragma unroll
-	for (int s = 0; s < C::ST - 1; ++s)
-		if (s < nch)
-			issue(s);
 
-	/* row factors while the first chunks arrive: TPR lanes of one wave
-	 * per row (every row's loads in flight at once), 4 values per load,
-	 * K a multiple of 256 */
-	float inv[C::MT];
-	if constexpr (SCALE) {
-		constexpr int TPR = MR >= 16 ? 1024 / MR < 64 ? 1024 / MR : 64 : 64;
-		constexpr int RPW = 64 / TPR;                    /* rows per wave */
-		const int m = wave * RPW + lane / TPR, c = lane % TPR;
-		float amax = 0.0f;
-		if (m < Mz) {
-			const char *row = abase + (long long)m * p.lda_b;
-#pragma unroll 8
-			for (int k = c * 4; k < p.K; k += TPR * 4) {
-				float v[4];
-				if constexpr (AK == S3K_F32) {
-					const float4 x = *(const float4 *)(row + (long long)k * 4);
-					v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
-				} else {
-					const uint2 x = *(const uint2 *)(row + (long long)k * 2);
-					v[0] = bf16_to_f32(x.x & 0xFFFFu), v[1] = bf16_to_f32(x.x >> 16);
-					v[2] = bf16_to_f32(x.y & 0xFFFFu), v[3] = bf16_to_f32(x.y >> 16);
-				}
+	/* f32 / bf16 rows are rounded with factor 1 first while each lane
+	 * tracks the largest |value| of its rows; rows that need another
+	 * factor (rare) make the workgroup run the pass again with the factors */
+	float inv[C::MT], amx[C::MT];
 #pragma unroll
-				for (int e = 0; e < 4; ++e)
-					amax = fmaxf(amax, finite_abs(v[e]));
-			}
-		}
-#pragma unroll
-		for (int off = TPR / 2; off > 0; off >>= 1)
-			amax = fmaxf(amax, __shfl_xor(amax, off));
-		if (c == 0 && m < MR && wave * RPW < MR) {
-			const int ex = scale_exp_of(amax);
-			rsc[m] = pow2f(-ex);
-			rsc[MR + m] = pow2f(ex);
-		}
-		__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): the factors are in LDS */
-		wg_barrier();
-#pragma unroll
-		for (int mt = 0; mt < C::MT; ++mt) {
-			const int m = mt * 16 + l16;
-			inv[mt] = m < MR ? rsc[m] : 1.0f;
-		}
-	}
+	for (int mt = 0; mt < C::MT; ++mt)
+		inv[mt] = 1.0f, amx[mt] = 0.0f;
 
-	for (int ch = 0; ch < nch; ++ch) {
-		/* this wave's loads of chunk ch done (younger chunks may fly) */
-		if (ch + C::ST - 2 < nch)
-			wait_vm<(C::ST - 2) * C::NPW>();
-		else
-			wait_vm<0>();
-		wg_barrier();
-		if (ch + C::ST - 1 < nch)
-			issue(ch + C::ST - 1);
+	auto pass = [&](bool track) {
+#pragma unroll
+		for (int t = 0; t < NT; ++t)
+#pragma unroll
+			for (int mt = 0; mt < C::MT; ++mt)
+				acc[t][mt] = (s3k_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+		for (int s = 0; s < C::ST - 1; ++s)
+			if (s < nch)
+				issue(s);
 
-		if (C::CW < WV && wave >= C::CW)
-			continue;
-		const char *Ws = smem + (ch % C::ST) * C::SB;
-		const char *As = Ws + C::SW;
-		/* operands of this wave's U k-blocks first, then all MFMAs, then
-		 * the scale FMAs: independent chains instead of one per block */
-		uint4 af[C::U][C::MT], wf[C::U][NT];
-		float sc[C::U][NT];
+		for (int ch = 0; ch < nch; ++ch) {
+			/* this wave's loads of chunk ch done (younger chunks may fly) */
+			if (ch + C::ST - 2 < nch)
+				wait_vm<(C::ST - 2) * C::NPW>();
+			else
+				wait_vm<0>();
+			wg_barrier();
+			if (ch + C::ST - 1 < nch)
+				issue(ch + C::ST - 1);
+
+			if (C::CW < WV && wave >= C::CW)
+				continue;
+			const char *Ws = smem + (ch % C::ST) * C::SB;
+			const char *As = Ws + C::SW;
+			/* operands of this wave's U k-blocks first, then all MFMAs,
+			 * then the scale FMAs: independent chains instead of one per
+			 * block */
+			uint4 af[C::U][C::MT], wf[C::U][NT];
+			float sc[C::U][NT];
 #pragma unroll
-		for (int u = 0; u < C::U; ++u) {
-			const int kb = u * C::CW + wave;
+			for (int u = 0; u < C::U; ++u) {
+				const int kb = u * C::CW + wave;
 #pragma unroll
-			for (int mt = 0; mt < C::MT; ++mt) {
-				const int m = mt * 16 + l16;
-				af[u][mt] = make_uint4(0, 0, 0, 0);
-				if (m < MR) {
-					const char *row = As + m * (C::GAR * 16);
-					if constexpr (AK == S3K_F32) {
-						const int q0 = kb * 8 + 2 * g16;
-						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
-						const uint4 y = *(const uint4 *)(row + (((q0 + 1) ^ (m & 15)) << 4));
-						const float s = inv[mt];
-						af[u][mt] = make_uint4(
-							pack_f16x2(__uint_as_float(x.x) * s, __uint_as_float(x.y) * s),
-							pack_f16x2(__uint_as_float(x.z) * s, __uint_as_float(x.w) * s),
-							pack_f16x2(__uint_as_float(y.x) * s, __uint_as_float(y.y) * s),
-							pack_f16x2(__uint_as_float(y.z) * s, __uint_as_float(y.w) * s));
-					} else {
-						const int q0 = kb * 4 + g16;
-						const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
-						if constexpr (AK == S3K_BF16) {
-							const float s = inv[mt];
-							af[u][mt] = make_uint4(
-								pack_f16x2(bf16_to_f32(x.x & 0xFFFF) * s, bf16_to_f32(x.x >> 16) * s),
-								pack_f16x2(bf16_to_f32(x.y & 0xFFFF) * s, bf16_to_f32(x.y >> 16) * s),
-								pack_f16x2(bf16_to_f32(x.z & 0xFFFF) * s, bf16_to_f32(x.z >> 16) * s),
-								pack_f16x2(bf16_to_f32(x.w & 0xFFFF) * s, bf16_to_f32(x.w >> 16) * s));
+				for (int mt = 0; mt < C::MT; ++mt) {
+					const int m = mt * 16 + l16;
+					af[u][mt] = make_uint4(0, 0, 0, 0);
+					if (m < MR) {
+						const char *row = As + m * (C::GAR * 16);
+						float v[8];
+						if constexpr (AK == S3K_F32) {
+							const int q0 = kb * 8 + 2 * g16;
+							const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
+							const uint4 y = *(const uint4 *)(row + (((q0 + 1) ^ (m & 15)) << 4));
+							v[0] = __uint_as_float(x.x), v[1] = __uint_as_float(x.y);
+							v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
+							v[4] = __uint_as_float(y.x), v[5] = __uint_as_float(y.y);
+							v[6] = __uint_as_float(y.z), v[7] = __uint_as_float(y.w);
+						} else if constexpr (AK == S3K_BF16) {
+							const int q0 = kb * 4 + g16;
+							const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
+							v[0] = bf16_to_f32(x.x & 0xFFFF), v[1] = bf16_to_f32(x.x >> 16);
+							v[2] = bf16_to_f32(x.y & 0xFFFF), v[3] = bf16_to_f32(x.y >> 16);
+							v[4] = bf16_to_f32(x.z & 0xFFFF), v[5] = bf16_to_f32(x.z >> 16);
+							v[6] = bf16_to_f32(x.w & 0xFFFF), v[7] = bf16_to_f32(x.w >> 16);
 						} else {
-							af[u][mt] = x;
+							const int q0 = kb * 4 + g16;
+							af[u][mt] = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
+						}
+						if constexpr (SCALE) {
+							if (track) {
+#pragma unroll
+								for (int e = 0; e < 8; ++e)
+									amx[mt] = fmaxf(amx[mt], finite_abs(v[e]));
+							}
+							const float f = inv[mt];
+							af[u][mt] = make_uint4(pack_f16x2(v[0] * f, v[1] * f),
+									       pack_f16x2(v[2] * f, v[3] * f),
+									       pack_f16x2(v[4] * f, v[5] * f),
+									       pack_f16x2(v[6] * f, v[7] * f));
 						}
 					}
 				}
-			}
 #pragma unroll
-			for (int t = 0; t < NT; ++t) {
-				const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
-				sc[u][t] = *(const float *)blk;
-				const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16) ^ 0x80808080u;
-				const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16) ^ 0x80808080u;
-				wf[u][t].x = q8pair_to_f16(w0, 0x04010400u);
-				wf[u][t].y = q8pair_to_f16(w0, 0x04030402u);
-				wf[u][t].z = q8pair_to_f16(w1, 0x04010400u);
-				wf[u][t].w = q8pair_to_f16(w1, 0x04030402u);
+				for (int t = 0; t < NT; ++t) {
+					const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
+					sc[u][t] = *(const float *)blk;
+					const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16) ^ 0x80808080u;
+					const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16) ^ 0x80808080u;
+					wf[u][t].x = q8pair_to_f16(w0, 0x04010400u);
+					wf[u][t].y = q8pair_to_f16(w0, 0x04030402u);
+					wf[u][t].z = q8pair_to_f16(w1, 0x04010400u);
+					wf[u][t].w = q8pair_to_f16(w1, 0x04030402u);
+				}
 			}
+			s3k_f32x4 part[C::U][NT][C::MT];
+#pragma unroll
+			for (int u = 0; u < C::U; ++u)
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int mt = 0; mt < C::MT; ++mt)
+						part[u][t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+							__builtin_bit_cast(s3k_f16x8, af[u][mt]),
+							__builtin_bit_cast(s3k_f16x8, wf[u][t]),
+							(s3k_f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+			for (int u = 0; u < C::U; ++u)
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+						for (int j = 0; j < 4; ++j)
+							acc[t][mt][j] += part[u][t][mt][j] * sc[u][t];
 		}
-		s3k_f32x4 part[C::U][NT][C::MT];
+		wait_vm<0>();
+		wg_barrier();
+	};
+
+	pass(SCALE);
+	if constexpr (SCALE) {
+		/* each row's largest |value|: over the 4 lanes of a wave that hold
+		 * it (g16), then over the waves through LDS; rsc = 2^-e, 2^e */
 #pragma unroll
-		for (int u = 0; u < C::U; ++u)
+		for (int mt = 0; mt < C::MT; ++mt) {
+			float a = amx[mt];
+			a = fmaxf(a, __shfl_xor(a, 16));
+			a = fmaxf(a, __shfl_xor(a, 32));
+			const int m = mt * 16 + l16;
+			if (g16 == 0 && m < MR)
+				rmx[wave * MR + m] = a;
+		}
+		__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+		wg_barrier();
+		if (threadIdx.x < MR) {
+			float a = 0.0f;
+			for (int w = 0; w < C::CW; ++w)
+				a = fmaxf(a, rmx[w * MR + threadIdx.x]);
+			const int ex = threadIdx.x < Mz ? scale_exp_of(a) : 0;
+			rsc[threadIdx.x] = pow2f(-ex);
+			rsc[MR + threadIdx.x] = pow2f(ex);
+			rmx[threadIdx.x] = ex != 0 ? 1.0f : 0.0f; /* rows 0..MR-1 of wave 0 are read */
+		}
+		__builtin_amdgcn_s_waitcnt(0xC07F);
+		wg_barrier();
+		bool again = false;
+		for (int m = 0; m < MR; ++m)
+			again |= rmx[m] != 0.0f;
+		if (again) {
 #pragma unroll
-			for (int t = 0; t < NT; ++t)
-#pragma unroll
-				for (int mt = 0; mt < C::MT; ++mt)
-					part[u][t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-						__builtin_bit_cast(s3k_f16x8, af[u][mt]),
-						__builtin_bit_cast(s3k_f16x8, wf[u][t]),
-						(s3k_f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-		for (int u = 0; u < C::U; ++u)
-#pragma unroll
-			for (int t = 0; t < NT; ++t)
-#pragma unroll
-				for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-					for (int j = 0; j < 4; ++j)
-						acc[t][mt][j] += part[u][t][mt][j] * sc[u][t];
+			for (int mt = 0; mt < C::MT; ++mt) {
+				const int m = mt * 16 + l16;
+				inv[mt] = m < MR ? rsc[m] : 1.0f;
+			}
+			pass(false);
+		}
 	}
 
 	/* Cross-wave reduction in a fixed order, then bias/GELU and store. */

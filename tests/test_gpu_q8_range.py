@@ -92,11 +92,14 @@ def test_f32_activations_wide_range_bias_gelu():
         assert np.abs(g[row] - r[row]).max() <= 1e-3 * s, row
 
 
-def test_bf16_activations_near_1e30():
+@pytest.mark.parametrize("M", [512, 77, 8], ids=["mfma", "skinny77", "skinny8"])
+def test_bf16_activations_near_1e30(M):
     """Config 3's dtype pairing (bf16 activations x Q8_0) with activations
-    far outside f16, as bf16 carries the f32 exponent range."""
+    far outside f16, as bf16 carries the f32 exponent range; on the MFMA
+    GEMM (M = 512) and the streaming skinny kernel (M = 77, 8), which
+    rounds bf16 to f16 itself."""
     O = oracle()
-    M, K, N = 512, 1024, 512
+    K, N = 1024, 512
     a32 = wide_rows(330, M, K)
     a = O.f32_to_bf16(a32).reshape(M, K)
     w = O.q8_quantize(synth.randn(331, (N, K), 0.02))
