@@ -469,7 +469,9 @@ extern "C" int s3k_dl_eligible(const struct s3k_gemm *g)
  * shape:
  *   - 256x256 (cfg 20 / 9, 8 waves) when the problem is one nearly full
  *     round of 224..256 such tiles (qkv 5184x3072: 32.1 against 33.3 us;
- *     4096^3: 1266 against 1201 TFLOP/s);
+ *     4096^3: 1266 against 1201 TFLOP/s), and (K % 64 == 0) from 160
+ *     such tiles when 192x256 tiles would spill into a second round
+ *     (4096x3072x1024: 29.2 against 37.1 us for 192x128);
  *   - 192x256 (cfg 23, 8 waves) from 384 such tiles (fc1: 45.5 against
  *     49.7 us for 192x128);
  *   - 192x128 (cfg 24 / 10, 8 waves) when that gives at least 192 tiles
@@ -494,6 +496,8 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		const bool pipe = g->K % 64 == 0;
 		if (t9 >= 224 && t9 <= 256)
 			cfg = pipe ? 20 : 9;
+		else if (pipe && t9 >= 160 && t9 <= 256 && dl_tiles(g, 192, 256) > 256)
+			cfg = 20;
 		else if (pipe && dl_tiles(g, 192, 256) >= 384)
 			cfg = 23;
 		else if (t10 >= 192)
