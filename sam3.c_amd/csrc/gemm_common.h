@@ -217,7 +217,7 @@ __device__ __forceinline__ void epi_fetch(const GemmArgs &p, int m, int n, int b
 
 template <int CK, bool EPI, int W>
 __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, int m, int n,
-				       const float *v, const EpiIn<W> &ein)
+				       const float (&xv)[W], const EpiIn<W> &ein)
 {
 	typedef float f4v __attribute__((ext_vector_type(4)));
 	typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -225,10 +225,8 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, 
 	const bool full = n + W <= p.N;
 	float x[W];
 #pragma unroll
-	for (int e = 0; e < W; e += 4) {
-		const float4 q = *(const float4 *)(v + e);
-		x[e] = q.x; x[e + 1] = q.y; x[e + 2] = q.z; x[e + 3] = q.w;
-	}
+	for (int e = 0; e < W; ++e)
+		x[e] = xv[e];
 	if (EPI) {
 #pragma unroll
 		for (int e = 0; e < W; ++e)
@@ -299,28 +297,43 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, 
 	}
 }
 
-/* Epilogue of a wave tile, one 32-row strip at a time: the MFMA layout
- * (lane holds column l & 31 of rows 8*(r>>2) + 4*(l>>5) + (r&3)) is turned
- * into row-contiguous runs of columns through LDS, so each lane finishes
- * 4 (f32) or 8 (16-bit) outputs and writes them with one 16-byte store. `smem` must be free
- * (all waves past their last LDS read) and hold NW*32*(WTN+8) floats.
- * Each wave stages through its own region of smem, and the LDS operations
- * of one wave are performed in program order, so the waves need no
- * barrier between them here: a wavefront-scope fence keeps the compiler
- * from moving the staging reads above the writes. The store loops are
- * kept rolled: this code runs once per tile, and an unrolled epilogue
- * would not fit the instruction cache. */
-template <int FM, int FN, int WTN, int CK>
+/* Epilogue of a wave tile, one 32-row strip at a time: the MFMA layout is
+ * turned into row-contiguous runs of columns through LDS, so each lane
+ * finishes 4 (f32) or 8 (16-bit) outputs and writes them with one 16-byte
+ * store. Two accumulator layouts:
+ *   - TR false (C = A W^T, A as the MFMA's first operand): lane l holds
+ *     column l & 31 of rows 8*(r>>2) + 4*(l>>5) + (r&3), staged with one
+ *     4-byte LDS write per value;
+ *   - TR true (the operands swapped, the MFMA forms C^T): lane l holds row
+ *     l & 31 and columns 8*(r>>2) + 4*(l>>5) + (r&3), four consecutive
+ *     columns per 16-byte LDS write (a quarter of the write instructions).
+ *     The swap does not change any product or the order of the sums.
+ * `smem` must be free (all waves past their last LDS read) and hold
+ * NW*32*(WTN+8) floats. Each wave stages through its own region of smem,
+ * and the LDS operations of one wave are performed in program order, so
+ * the waves need no barrier between them here: a wavefront-scope fence
+ * keeps the compiler from moving the staging reads above the writes.
+ * Without a residual (or a per-row bias) a wave reads all of a strip's
+ * staged values and then issues its stores, so the LDS latency is paid
+ * once per strip; the residual loop is kept rolled (it loads inside the
+ * loop, and unrolled it would not fit the instruction cache), and each of
+ * its iterations reads the next iteration's staged values first. */
+template <int FM, int FN, int WTN, int CK, bool TR = false>
 __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&acc)[FM][FN],
 					      char *smem, int wave, int lane, int m0, int n0, int bz)
 {
-	constexpr int PITCH = WTN + 8; /* floats; 16-B aligned rows, rows 4 apart 32 banks apart */
+	/* floats per staged row, 16-byte aligned: rows 4 apart land 32 banks
+	 * apart for the 4-byte writes, and 16 consecutive rows on distinct
+	 * banks for the 16-byte ones */
+	constexpr int PITCH = TR ? WTN + 4 : WTN + 8;
 	float *stg = (float *)smem + wave * 32 * PITCH;
 	char *cb = p.c + (long long)bz * p.sc * (CK == S3K_F32 ? 4 : 2);
 	static_assert(CK != S3K_C_PLANES || WTN % 8 == 0, "planes are written 8 outputs at a time");
 	/* one 16-byte store per lane and unit: 4 f32 or 8 16-bit outputs,
 	 * so consecutive lanes write consecutive 16 bytes of a row */
 	constexpr int W = CK == S3K_F32 ? 4 : 8;
+	constexpr int UNITS = 32 * WTN / W; /* per strip, a multiple of 64 */
+	static_assert(UNITS % 64 == 0, "whole store rounds per strip");
 	/* when WTN / W divides 64, a lane keeps the same W columns for every
 	 * row it finishes: their bias is loaded once per tile */
 	constexpr bool FIXED = 64 % (WTN / W) == 0;
@@ -330,27 +343,46 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	 * accumulators and the bias is loaded before the first store; only the
 	 * residual (S3K_EPI_RES) is loaded inside a store loop. */
 	if (p.flags & S3K_EPI_ROWSCALE) {
-		/* lane l holds rows 8t + 4(l >> 5) + q (q < 4) of each 32-row strip */
+		if constexpr (TR) {
+			/* lane l holds row l & 31 of each 32-row strip */
 #pragma unroll
-		for (int i = 0; i < FM; ++i)
-#pragma unroll
-			for (int t = 0; t < 4; ++t) {
-				const int r0 = m0 + i * 32 + 8 * t + 4 * (lane >> 5);
-				const float *rp = p.rs + (long long)bz * p.rs_sb + r0;
-				float f[4];
-#pragma unroll
-				for (int q = 0; q < 4; ++q)
-					f[q] = r0 + q < p.M ? rp[q] : 1.0f;
+			for (int i = 0; i < FM; ++i) {
+				const int r = m0 + i * 32 + (lane & 31);
+				const float f = r < p.M ? p.rs[(long long)bz * p.rs_sb + r] : 1.0f;
 #pragma unroll
 				for (int j = 0; j < FN; ++j)
 #pragma unroll
-					for (int q = 0; q < 4; ++q)
-						acc[i][j][4 * t + q] *= f[q];
+					for (int q = 0; q < 16; ++q)
+						acc[i][j][q] *= f;
 			}
+		} else {
+			/* lane l holds rows 8t + 4(l >> 5) + q (q < 4) of each strip */
+#pragma unroll
+			for (int i = 0; i < FM; ++i)
+#pragma unroll
+				for (int t = 0; t < 4; ++t) {
+					const int r0 = m0 + i * 32 + 8 * t + 4 * (lane >> 5);
+					const float *rp = p.rs + (long long)bz * p.rs_sb + r0;
+					float f[4];
+#pragma unroll
+					for (int q = 0; q < 4; ++q)
+						f[q] = r0 + q < p.M ? rp[q] : 1.0f;
+#pragma unroll
+					for (int j = 0; j < FN; ++j)
+#pragma unroll
+						for (int q = 0; q < 4; ++q)
+							acc[i][j][4 * t + q] *= f[q];
+				}
+		}
 	}
 	const int flags = p.flags & ~S3K_EPI_ROWSCALE;
 	const bool heavy = (flags & S3K_EPI_RES) || (!FIXED && (flags & S3K_EPI_BIAS));
 	const bool light = !heavy && (flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
+	/* the common case, one rounding of the sum and plain rows: a store
+	 * path without per-element flag tests, row maps or partial vectors */
+	constexpr bool PLAIN_CK = CK == S3K_F32 || CK == S3K_BF16 || CK == S3K_F16;
+	const bool fast = PLAIN_CK && !(flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES)) && !p.rm_g &&
+			  p.vec_ok && n0 + WTN <= p.N;
 	EpiIn<W> ein;
 #pragma unroll
 	for (int q = 0; q < W; ++q) {
@@ -363,42 +395,118 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 		if (n0 + cw < p.N)
 			epi_bias<W>(p, n0 + cw, ein.b);
 	}
+	/* staged values of unit s: row s / (WTN / W), columns cw.. cw + W - 1 */
+	auto staged = [&](int s, float (&x)[W]) {
+		const float *v = stg + (s / (WTN / W)) * PITCH + (s % (WTN / W)) * W;
 #pragma unroll
+		for (int e = 0; e < W; e += 4) {
+			const float4 q = *(const float4 *)(v + e);
+			x[e] = q.x; x[e + 1] = q.y; x[e + 2] = q.z; x[e + 3] = q.w;
+		}
+	};
+	/* stage strip i's accumulators (the wave's own LDS region) */
+	auto stage = [&](const s3k_f32x16 (&a)[FN]) {
+		if constexpr (TR) {
+			const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+			for (int j = 0; j < FN; ++j)
+#pragma unroll
+				for (int t = 0; t < 4; ++t)
+					*(float4 *)(stg + l32 * PITCH + 32 * j + 8 * t + 4 * h) =
+						make_float4(a[j][4 * t], a[j][4 * t + 1], a[j][4 * t + 2], a[j][4 * t + 3]);
+		} else {
+#pragma unroll
+			for (int j = 0; j < FN; ++j)
+#pragma unroll
+				for (int r = 0; r < 16; ++r)
+					stg[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] =
+						a[j][r];
+		}
+	};
+	if (fast) {
+		/* unrolled over the strips: little code per strip, and the
+		 * compiler may start a strip's stores under the MFMAs still
+		 * finishing the other strips */
+		constexpr int IT = UNITS / 64;
+#pragma unroll
+		for (int i = 0; i < FM; ++i) {
+			stage(acc[i]);
+			wave_lds_fence();
+			float v[IT][W];
+#pragma unroll
+			for (int it = 0; it < IT; ++it)
+				staged(lane + 64 * it, v[it]);
+#pragma unroll
+			for (int it = 0; it < IT; ++it) {
+				const int s = lane + 64 * it;
+				const int m = m0 + i * 32 + s / (WTN / W), n = n0 + (s % (WTN / W)) * W;
+				if (m < p.M) {
+					const long long o = (long long)m * p.ldc + n;
+					if constexpr (CK == S3K_F32) {
+						*(float4 *)((float *)cb + o) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+					} else {
+						uint32_t w[4];
+#pragma unroll
+						for (int e = 0; e < 4; ++e)
+							w[e] = CK == S3K_BF16 ? pack_bf16x2(v[it][2 * e], v[it][2 * e + 1])
+									      : pack_f16x2(v[it][2 * e], v[it][2 * e + 1]);
+						*(uint4 *)((uint16_t *)cb + o) = make_uint4(w[0], w[1], w[2], w[3]);
+					}
+				}
+			}
+			wave_lds_fence();
+		}
+		return;
+	}
+	/* The strip loop is rolled so that the store code exists once; the
+	 * staging of strip i picks acc[i] by a wave-uniform branch (the
+	 * accumulators stay in registers). */
+#pragma unroll 1
 	for (int i = 0; i < FM; ++i) {
 #pragma unroll
-		for (int j = 0; j < FN; ++j)
-#pragma unroll
-			for (int r = 0; r < 16; ++r)
-				stg[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] =
-					acc[i][j][r];
+		for (int ii = 0; ii < FM; ++ii)
+			if (ii == i)
+				stage(acc[ii]);
 		wave_lds_fence();
 		const int mrow = m0 + i * 32;
+		float cur[W];
+		staged(lane, cur);
 		if (heavy) {
 #pragma unroll 1
-			for (int s = lane; s < 32 * WTN / W; s += 64) {
+			for (int s = lane; s < UNITS; s += 64) {
+				float nxt[W];
+				if (s + 64 < UNITS)
+					staged(s + 64, nxt);
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
 				if (mrow + row < p.M && n0 + cw < p.N) {
 					EpiIn<W> e = ein;
 					epi_fetch<W>(p, mrow + row, n0 + cw, bz, !FIXED, e);
-					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw,
-							     stg + row * PITCH + cw, e);
+					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, cur, e);
 				}
-			}
-		} else if (light) {
-#pragma unroll 1
-			for (int s = lane; s < 32 * WTN / W; s += 64) {
-				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
-				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw,
-							     stg + row * PITCH + cw, ein);
+#pragma unroll
+				for (int e = 0; e < W; ++e)
+					cur[e] = nxt[e];
 			}
 		} else {
-#pragma unroll 1
-			for (int s = lane; s < 32 * WTN / W; s += 64) {
+			/* all of the strip's staged values first, then the stores */
+			constexpr int IT = UNITS / 64;
+			float v[IT][W];
+#pragma unroll
+			for (int e = 0; e < W; ++e)
+				v[0][e] = cur[e];
+#pragma unroll
+			for (int it = 1; it < IT; ++it)
+				staged(lane + 64 * it, v[it]);
+#pragma unroll
+			for (int it = 0; it < IT; ++it) {
+				const int s = lane + 64 * it;
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
-				if (mrow + row < p.M && n0 + cw < p.N)
-					finishw<CK, false, W>(p, flags, cb, mrow + row, n0 + cw,
-							      stg + row * PITCH + cw, ein);
+				if (mrow + row < p.M && n0 + cw < p.N) {
+					if (light)
+						finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
+					else
+						finishw<CK, false, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
+				}
 			}
 		}
 		wave_lds_fence();

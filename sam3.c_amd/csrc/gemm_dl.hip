@@ -20,8 +20,11 @@
  *     flight while step kt is multiplied. Completion is tracked with an
  *     explicit s_waitcnt vmcnt(loads of the younger stages) followed by
  *     s_barrier; HIP's __syncthreads would wait for every load.
- *   - MFMA v_mfma_f32_32x32x16_{bf16,f16}, wave tile (BM/WGM) x (BN/WGN).
- *   - Epilogue through LDS with 16-byte stores (gemm_common.h).
+ *   - MFMA v_mfma_f32_32x32x16_{bf16,f16}, wave tile (BM/WGM) x (BN/WGN),
+ *     with W as the first operand: the MFMA forms C^T, so a lane holds
+ *     four consecutive columns of one row (same products and sums as A W^T).
+ *   - Epilogue through LDS with 16-byte stores (gemm_common.h); the
+ *     transposed accumulators are staged with 16-byte LDS writes.
  */
 #include "gemm_common.h"
 #include "lds_dma.h"
@@ -164,13 +167,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
 			for (int i = 0; i < FM; ++i)
 #pragma unroll
 				for (int j = 0; j < FN; ++j)
-					mfma_chunk<FAM>(acc[i][j], af[cur][i], bfr[cur][j]);
+					mfma_chunk<FAM>(acc[i][j], bfr[cur][j], af[cur][i]);
 			__builtin_amdgcn_s_setprio(0);
 		}
 	}
 
 	__syncthreads();
-	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+	write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
 /*
@@ -293,7 +296,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 			__builtin_amdgcn_sched_barrier(0);
 #pragma unroll
 			for (int m = 0; m < NMF; ++m) {
-				mfma_chunk<FAM>(acc[m / FN][m % FN], af[cur][m / FN], bf[cur][m % FN]);
+				mfma_chunk<FAM>(acc[m / FN][m % FN], bf[cur][m % FN], af[cur][m / FN]);
 				if (INTER) {
 					if (ks < 3) {
 						if (m < NRD)
@@ -349,7 +352,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 	step(kt & 1, kt, false, false);
 
 	__syncthreads();
-	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+	write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
 template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER>
