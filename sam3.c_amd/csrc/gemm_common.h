@@ -297,6 +297,11 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, 
 	}
 }
 
+template <bool B>
+struct epi_b {
+	static constexpr bool value = B;
+};
+
 /* Epilogue of a wave tile, one 32-row strip at a time: the MFMA layout is
  * turned into row-contiguous runs of columns through LDS, so each lane
  * finishes 4 (f32) or 8 (16-bit) outputs and writes them with one 16-byte
@@ -378,11 +383,12 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	const int flags = p.flags & ~S3K_EPI_ROWSCALE;
 	const bool heavy = (flags & S3K_EPI_RES) || (!FIXED && (flags & S3K_EPI_BIAS));
 	const bool light = !heavy && (flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
-	/* the common case, one rounding of the sum and plain rows: a store
-	 * path without per-element flag tests, row maps or partial vectors */
+	/* the common cases (plain rows, whole 16-byte vectors, no residual,
+	 * a bias loaded once per tile): a store path whose flag tests are
+	 * made once per tile instead of once per element */
 	constexpr bool PLAIN_CK = CK == S3K_F32 || CK == S3K_BF16 || CK == S3K_F16;
-	const bool fast = PLAIN_CK && !(flags & (S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_RES)) && !p.rm_g &&
-			  p.vec_ok && n0 + WTN <= p.N;
+	const bool fast = PLAIN_CK && !(flags & S3K_EPI_RES) && (FIXED || !(flags & S3K_EPI_BIAS)) &&
+			  !p.rm_g && p.vec_ok && n0 + WTN <= p.N;
 	EpiIn<W> ein;
 #pragma unroll
 	for (int q = 0; q < W; ++q) {
@@ -423,10 +429,11 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 						a[j][r];
 		}
 	};
-	if (fast) {
-		/* unrolled over the strips: little code per strip, and the
-		 * compiler may start a strip's stores under the MFMAs still
-		 * finishing the other strips */
+	/* the strips unrolled (little code per strip, and the compiler may
+	 * start a strip's stores under the MFMAs still finishing the others);
+	 * EB / EG: bias / GELU with epilogue<CK>'s rounding points */
+	auto fast_strips = [&](auto eb_t, auto eg_t) {
+		constexpr bool EB = decltype(eb_t)::value, EG = decltype(eg_t)::value;
 		constexpr int IT = UNITS / 64;
 #pragma unroll
 		for (int i = 0; i < FM; ++i) {
@@ -440,6 +447,12 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			for (int it = 0; it < IT; ++it) {
 				const int s = lane + 64 * it;
 				const int m = m0 + i * 32 + s / (WTN / W), n = n0 + (s % (WTN / W)) * W;
+				if constexpr (EB || EG) {
+#pragma unroll
+					for (int e = 0; e < W; ++e)
+						v[it][e] = epilogue<CK>(v[it][e], ein.b[e], (EB ? S3K_EPI_BIAS : 0) |
+												(EG ? S3K_EPI_GELU : 0));
+				}
 				if (m < p.M) {
 					const long long o = (long long)m * p.ldc + n;
 					if constexpr (CK == S3K_F32) {
@@ -456,6 +469,17 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			}
 			wave_lds_fence();
 		}
+	};
+	if (fast) {
+		const bool eb = flags & S3K_EPI_BIAS, eg = flags & S3K_EPI_GELU;
+		if (!eb && !eg)
+			fast_strips(epi_b<false>{}, epi_b<false>{});
+		else if (eb && eg)
+			fast_strips(epi_b<true>{}, epi_b<true>{});
+		else if (eb)
+			fast_strips(epi_b<true>{}, epi_b<false>{});
+		else
+			fast_strips(epi_b<false>{}, epi_b<true>{});
 		return;
 	}
 	/* The strip loop is rolled so that the store code exists once; the
