@@ -186,13 +186,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) conv_dl(ConvArgs q)
 			for (int i = 0; i < FM; ++i)
 #pragma unroll
 				for (int j = 0; j < FN; ++j)
-					mfma_chunk<FAM>(acc[i][j], af[cur][i], bfr[cur][j]);
+					/* the weights first: the MFMA forms C^T (the
+					 * transposed layout the epilogue stages) */
+					mfma_chunk<FAM>(acc[i][j], bfr[cur][j], af[cur][i]);
 			__builtin_amdgcn_s_setprio(0);
 		}
 	}
 
 	__syncthreads();
-	write_tile_ck<FM, FN, WTN, CK>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, 0);
+	write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, 0);
 }
 
 /* Element k of row m of the column matrix (cpu_conv2d.c:46-88): k runs

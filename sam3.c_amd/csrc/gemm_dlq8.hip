@@ -19,7 +19,9 @@
  *     block scale rounded to f16, so the MFMA sees q*scale in f16, as the
  *     register-staged Q8 loader produces it;
  *   - v_mfma_f32_32x32x16_f16, f32 accumulate; each wave covers 128 rows
- *     of A so one dequantized B fragment serves 4 MFMAs.
+ *     of A so one dequantized B fragment serves 4 MFMAs. The B fragment
+ *     is the MFMA's first operand (the MFMA forms C^T; the epilogue stages
+ *     the transposed layout).
  * The ring, the waits and the epilogue follow gemm_dl.hip.
  */
 #include "gemm_common.h"
@@ -196,12 +198,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 			for (int i = 0; i < FM; ++i)
 #pragma unroll
 				for (int j = 0; j < FN; ++j)
-					mfma_chunk<FAM_F16>(acc[i][j], af[cur][i], bfr[ks][j]);
+					mfma_chunk<FAM_F16>(acc[i][j], bfr[ks][j], af[cur][i]);
 		}
 	}
 
 	__syncthreads();
-	write_tile_ck<FM, FN, WTN, S3K_F32>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+	write_tile_ck<FM, FN, WTN, S3K_F32, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
 template <int BM, int BN, int WGM, int WGN, int STAGES, int OCC>
