@@ -368,11 +368,11 @@ def text_encoder_bench(seqs=(1, 8, 32, 77), layers=24, per_graph=4, steps=3, war
         gbs = wbytes / (ms * 1e-3) / 1e9
         out[f"seq{seq}"] = {"ms": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
                             "weights_gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                            "kernels_per_eval": st.gpu_nodes - st.fused_nodes,
+                            "gpu_nodes_per_eval": st.gpu_nodes, "fused_nodes_per_eval": st.fused_nodes,
                             "nodes_per_eval": graphs[0].g.n_nodes}
         log(f"  seq {seq}: {out[f'seq{seq}']}")
     out["note"] = (f"{layers} layers, {per_graph} per graph_eval, Q8_0 weights "
-                   f"{wbytes / 1e6:.0f} MB distinct per layer, f32 activations; weights_gbs = "
+                   f"{wbytes / 1e6:.0f} MB in all (distinct per layer), f32 activations; weights_gbs = "
                    "weight bytes / wall time of all layers")
     return out
 
