@@ -536,7 +536,40 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.vec_ok = aligned16(g->c) && g->ldc % 8 == 0 && (g->batch <= 1 || g->stride_c % 8 == 0);
 	p.tiles_m = p.tiles_n = 0;
 	p.a_extent = p.b_extent = 0;
+	for (int y = 0; y < 3; ++y)
+		p.qkv_out[y] = g->qkv_out[y];
+	p.qkv_cos = g->qkv_cos;
+	p.qkv_sin = g->qkv_sin;
+	p.qkv_S = g->qkv_S;
+	p.qkv_H = g->qkv_H;
+	p.qkv_dsh = g->qkv_D > 0 ? __builtin_ctz((unsigned)g->qkv_D) : 0;
+	p.qkv_rope = g->qkv_rope;
 	return p;
+}
+
+/* What the S3K_EPI_QKV epilogue assumes (struct s3k_gemm): the
+ * pipelined direct-to-LDS kernel (whole 64-k steps) with f32 output, one
+ * batch slice, no residual, row map or GELU, and the operand geometry
+ * below. */
+static bool qkv_ok(const struct s3k_gemm *g)
+{
+	const int D = g->qkv_D, H = g->qkv_H, S = g->qkv_S;
+	if (g->c_kind != S3K_F32 || g->batch != 1 || (g->flags & (S3K_EPI_RES | S3K_EPI_GELU)) ||
+	    g->rm_g || g->K % 64 || D < 4 || (D & (D - 1)) || H <= 0 || S < 32 || g->M % S ||
+	    (long long)H * D > (1 << 28) || (long long)S * D > 0x7FFFFFFFLL)
+		return false;
+	const int E = H * D, n_out = g->N / E;
+	if (g->N % E || n_out < 1 || n_out > 3 || g->qkv_rope < 0 || (g->qkv_rope >> n_out))
+		return false;
+	for (int y = 0; y < n_out; ++y)
+		if (!g->qkv_out[y] || ((uintptr_t)g->qkv_out[y] & 15u))
+			return false;
+	if (g->qkv_rope && (!g->qkv_cos || !g->qkv_sin ||
+			    (((uintptr_t)g->qkv_cos | (uintptr_t)g->qkv_sin) & 7u)))
+		return false;
+	if ((g->flags & S3K_EPI_BIAS) && (!g->bias || ((uintptr_t)g->bias & 15u)))
+		return false;
+	return s3k_dl_ok(g);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int FAM, int CK, class LA, class LB>
@@ -655,6 +688,8 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	     (path == S3K_PATH_SKINNY && (g->c_kind != S3K_F32 || g->ldc != g->N)) ||
 	     (g->rm_g && (g->rm_d1 <= 0 || g->rm_d2 <= 0 ||
 			  g->M % ((long long)g->rm_g * g->rm_d1 * g->rm_d2)))))
+		return (int)hipErrorInvalidValue;
+	if ((g->flags & S3K_EPI_QKV) && (path != S3K_PATH_MFMA || !mfma_ok(g) || !qkv_ok(g)))
 		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))

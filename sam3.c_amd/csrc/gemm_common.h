@@ -32,6 +32,10 @@ struct GemmArgs {
 	int vec_ok;   /* rows of C (and the base) allow 16-byte stores */
 	int tiles_m, tiles_n;
 	unsigned a_extent, b_extent; /* bytes of one batch slice (buffer range) */
+	/* S3K_EPI_QKV (struct s3k_gemm): head size 1 << qkv_dsh */
+	float *qkv_out[3];
+	const float *qkv_cos, *qkv_sin;
+	int qkv_S, qkv_H, qkv_dsh, qkv_rope;
 };
 
 enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };
@@ -322,8 +326,10 @@ struct epi_b {
  * staged values and then issues its stores, so the LDS latency is paid
  * once per strip; the residual loop is kept rolled (it loads inside the
  * loop, and unrolled it would not fit the instruction cache), and each of
- * its iterations reads the next iteration's staged values first. */
-template <int FM, int FN, int WTN, int CK, bool TR = false>
+ * its iterations reads the next iteration's staged values first.
+ * QKV_OK (TR, f32 output): the S3K_EPI_QKV epilogue only, a kernel of
+ * its own (the other paths' registers would not leave room for it). */
+template <int FM, int FN, int WTN, int CK, bool TR = false, bool QKV_OK = false>
 __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&acc)[FM][FN],
 					      char *smem, int wave, int lane, int m0, int n0, int bz)
 {
@@ -470,6 +476,96 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			wave_lds_fence();
 		}
 	};
+	/* S3K_EPI_QKV: the strips go out through LDS as in the fast path;
+	 * each lane finishes four consecutive columns of a row (bias, then
+	 * RoPE: the pairs (d, d + 1) and (d + 2, d + 3) never leave the lane)
+	 * and writes them to one run of a head-split row. A row's 16 or 32
+	 * lanes read one contiguous run of each table row, so a table load
+	 * touches as many cache lines as a store does. The tables of strip
+	 * i + 1 are loaded before strip i's stores: a load issued after a
+	 * store would wait for that store too. */
+	if constexpr (QKV_OK) {
+		static_assert(TR && CK == S3K_F32 && FIXED, "QKV stores: transposed f32 tiles");
+		{
+			const int S = p.qkv_S, dsh = p.qkv_dsh, D = 1 << dsh, E = p.qkv_H << dsh;
+			const bool eb = flags & S3K_EPI_BIAS;
+			/* unit u of a strip: row u / LPR, columns (u % LPR) * 4 + [0, 4) */
+			constexpr int LPR = WTN / W, RPI = 64 / LPR, IT = UNITS / 64;
+			const int n = n0 + (lane % LPR) * W;
+			const bool nok = n < p.N;
+			const int y = (n >= E) + (n >= 2 * E), r = n - y * E;
+			float *ob = nok ? (y == 0 ? p.qkv_out[0] : y == 1 ? p.qkv_out[1] : p.qkv_out[2]) +
+						  (long long)(r >> dsh) * S * D + (r & (D - 1))
+					: nullptr;
+			const long long hsd = (long long)p.qkv_H * S * D;
+			const bool rope = nok && ((p.qkv_rope >> y) & 1);
+			/* this lane's rows: m1 + RPI*k for k = 0, 1, ... over the strips;
+			 * (b, sr): the next row to store, st: the next row whose
+			 * tables are loaded (RPI <= S, so one wrap at a time) */
+			const int m1 = m0 + lane / LPR;
+			int b = m1 / S, sr = m1 - b * S, st = sr;
+			const unsigned tbytes = (unsigned)S * (unsigned)D * 2u;
+			const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+				(void *)p.qkv_cos, (short)0, (int)tbytes, 0x00020000);
+			const __amdgpu_buffer_rsrc_t rsn = __builtin_amdgcn_make_buffer_rsrc(
+				(void *)p.qkv_sin, (short)0, (int)tbytes, 0x00020000);
+			/* byte offset of the lane's first pair in a table row; every
+			 * offset stays inside the tables (s < S, d + 3 < D) */
+			const unsigned dp = (unsigned)(n & (D - 1)) * 2u;
+			float2 tc[2][IT], ts[2][IT];
+			auto load_tables = [&](float2 (&c)[IT], float2 (&sn)[IT]) {
+#pragma unroll
+				for (int it = 0; it < IT; ++it) {
+					const unsigned off = (unsigned)st * (unsigned)D * 2u + dp;
+					c[it] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rc, off, 0, 0));
+					sn[it] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rsn, off, 0, 0));
+					st += RPI;
+					if (st >= S)
+						st -= S;
+				}
+			};
+			if (p.qkv_rope)
+				load_tables(tc[0], ts[0]);
+#pragma unroll
+			for (int i = 0; i < FM; ++i) {
+				if (p.qkv_rope && i + 1 < FM)
+					load_tables(tc[(i + 1) & 1], ts[(i + 1) & 1]);
+				stage(acc[i]);
+				wave_lds_fence();
+				float v[IT][W];
+#pragma unroll
+				for (int it = 0; it < IT; ++it)
+					staged(lane + 64 * it, v[it]);
+#pragma unroll
+				for (int it = 0; it < IT; ++it) {
+					float x[4] = {v[it][0], v[it][1], v[it][2], v[it][3]};
+					if (eb) {
+#pragma unroll
+						for (int q = 0; q < 4; ++q)
+							x[q] = add_rn(x[q], ein.b[q]);
+					}
+					if (rope) {
+						const float2 cc = tc[i & 1][it], ss = ts[i & 1][it];
+						const float u0 = x[0], u1 = x[1], u2 = x[2], u3 = x[3];
+						x[0] = sub_rn(mul_rn(u0, cc.x), mul_rn(u1, ss.x));
+						x[1] = add_rn(mul_rn(u0, ss.x), mul_rn(u1, cc.x));
+						x[2] = sub_rn(mul_rn(u2, cc.y), mul_rn(u3, ss.y));
+						x[3] = add_rn(mul_rn(u2, ss.y), mul_rn(u3, cc.y));
+					}
+					const int m = m1 + 32 * i + RPI * it;
+					if (m < p.M && nok)
+						*(float4 *)(ob + b * hsd + (long long)sr * D) = make_float4(x[0], x[1], x[2], x[3]);
+					sr += RPI;
+					if (sr >= S) {
+						sr -= S;
+						++b;
+					}
+				}
+				wave_lds_fence();
+			}
+			return;
+		}
+	}
 	if (fast) {
 		const bool eb = flags & S3K_EPI_BIAS, eg = flags & S3K_EPI_GELU;
 		if (!eb && !eg)

@@ -37,6 +37,14 @@ __device__ __forceinline__ int dl_off(int row, int c)
 	return (row * CPR + (c ^ lds_swz<CPR>(row))) << 4;
 }
 
+/* The S3K_EPI_QKV epilogue needs f32 output and wave tiles whose width
+ * in 4-column units divides 64 (each lane keeps its columns for the
+ * whole tile); it is built for the pipelined kernel only. */
+__host__ __device__ constexpr bool qkv_tiles(int ck, int wtn)
+{
+	return ck == S3K_F32 && 64 % (wtn / 4) == 0;
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int FAM, int CK, int OCC>
 __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
 {
@@ -204,7 +212,8 @@ __device__ __forceinline__ uint4 lds_rd16(unsigned base, unsigned off)
 	return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER>
+/* QKV: the S3K_EPI_QKV epilogue (f32 output), instead of C */
+template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER, bool QKV = false>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 {
 	constexpr int NW = WGM * WGN, BK = 64, CPR = 8;
@@ -352,21 +361,31 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 	step(kt & 1, kt, false, false);
 
 	__syncthreads();
-	write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+	write_tile_ck<FM, FN, WTN, CK, true, QKV>(p, acc, smem, wave, lane, tm * BM + wm0,
+						 tn * BN + wn0, bz);
 }
 
-template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER>
+template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER, bool QKV = false>
 static void launch_dlp_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
 {
 	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
-	hipLaunchKernelGGL((gemm_dlp<BM, BN, WGM, WGN, FAM, CK, INTER>), grid, dim3(64 * WGM * WGN),
-			   0, st, p);
+	hipLaunchKernelGGL((gemm_dlp<BM, BN, WGM, WGN, FAM, CK, INTER, QKV>), grid,
+			   dim3(64 * WGM * WGN), 0, st, p);
 }
 
 template <int BM, int BN, int WGM, int WGN, bool INTER, int FAM>
 static int launch_dlp_fam(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
 {
 	constexpr int SAME = FAM == FAM_BF16 ? S3K_BF16 : S3K_F16;
+	if (g->flags & S3K_EPI_QKV) {
+		if constexpr (qkv_tiles(S3K_F32, BN / WGN)) {
+			if (g->c_kind != S3K_F32)
+				return (int)hipErrorInvalidValue;
+			launch_dlp_k<BM, BN, WGM, WGN, FAM, S3K_F32, INTER, true>(g, p, st);
+			return (int)hipGetLastError();
+		}
+		return (int)hipErrorInvalidValue;
+	}
 	switch (g->c_kind) {
 	case S3K_F32:      launch_dlp_k<BM, BN, WGM, WGN, FAM, S3K_F32, INTER>(g, p, st); break;
 	case SAME:         launch_dlp_k<BM, BN, WGM, WGN, FAM, SAME, INTER>(g, p, st); break;
@@ -430,6 +449,8 @@ static int launch_dl_fam(const struct s3k_gemm *g, const GemmArgs &p, hipStream_
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int OCC, bool OPK = false>
 static int launch_dl_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
+	if (g->flags & S3K_EPI_QKV) /* the pipelined kernels only */
+		return (int)hipErrorInvalidValue;
 	p.tiles_m = (p.M + BM - 1) / BM;
 	p.tiles_n = (p.N + BN - 1) / BN;
 	if (g->a_kind == S3K_BF16)
@@ -510,6 +531,11 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		else
 			cfg = 2;
 	}
+	/* the S3K_EPI_QKV epilogue exists for the pipelined kernel with wave
+	 * tiles of 64 columns or 128: the small problems take its 128x128
+	 * tile */
+	if ((g->flags & S3K_EPI_QKV) && (cfg < 20 || cfg == 25))
+		cfg = 26;
 	switch (cfg) {
 	case 0:  return launch_dl_cfg<256, 128, 32, 2, 2, 3, 2>(g, p, st);
 	case 1:  return launch_dl_cfg<128, 128, 32, 2, 2, 3, 2>(g, p, st);

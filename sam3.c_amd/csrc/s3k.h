@@ -39,6 +39,9 @@ enum s3k_kind {
 			     * activations times 1/rs[m] (a power of two,
 			     * s3k_cast_f16_rows), so the f16 copy of rows
 			     * outside the f16 range stays exact           */
+#define S3K_EPI_QKV 32  /* f32 out, batch 1, direct-to-LDS GEMM only: the
+			 * result is stored as the head-split attention
+			 * operands (struct s3k_gemm, qkv_*) instead of C */
 
 /*
  * One (optionally strided-batched) GEMM: C[M,N] = A[M,K] * B, row-major.
@@ -74,6 +77,17 @@ struct s3k_gemm {
 	 * values all below 2^-10) stores ovf_tag to *ovf */
 	unsigned   *ovf;
 	unsigned    ovf_tag;
+	/* S3K_EPI_QKV: with E = qkv_H * qkv_D, output column n of row m is
+	 * element (b, s, h, d) = (m / qkv_S, m % qkv_S, (n % E) / qkv_D,
+	 * n % qkv_D) of operand y = n / E and is stored at qkv_out[y] +
+	 * ((b * qkv_H + h) * qkv_S + s) * qkv_D + d: the [B, H, S, D] head
+	 * split. When bit y of qkv_rope is set, RoPE is applied to operand y
+	 * after the bias: pairs (d, d + 1), cos / sin tables [qkv_S, qkv_D/2],
+	 * products and sums rounded separately. qkv_D is a power of two
+	 * >= 4, qkv_S >= 32, N = E, 2E or 3E, M a multiple of qkv_S. */
+	float       *qkv_out[3];
+	const float *qkv_cos, *qkv_sin;
+	int          qkv_S, qkv_H, qkv_D, qkv_rope;
 };
 
 /* Which kernel s3k_gemm_launch would pick (for tests and the bench). */
@@ -254,7 +268,7 @@ struct s3h_settings {
 	int q8_batch_path;                /* SAM3_HIP_Q8_BATCH_PATH: 0, 1, 2     */
 	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
 	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
-	    permute_operand, partition_fold;
+	    permute_operand, partition_fold, qkv_fold;
 	int readback_all;                 /* SAM3_HIP_READBACK=all               */
 	int quiet;                        /* SAM3_HIP_QUIET set                  */
 	int arena_mb;                     /* SAM3_HIP_ARENA_MB (0 = default)     */

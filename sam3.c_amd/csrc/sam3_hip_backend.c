@@ -529,6 +529,22 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 				 struct use_map *uses, int *k_out);
 static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t);
 
+/* gh_multihead_attention_rope's q, k and v preparation
+ * (graph_helpers.c:721-882): SLICE of the fused qkv output's columns ->
+ * RESHAPE [B, S, H, D] -> (ROPE -> RESHAPE ...) -> TRANSPOSE (0, 2, 1, 3).
+ * Every tensor in between is used once, so the chain runs as one kernel
+ * from the qkv rows to the head-split operand (s3k_rope_split3, which
+ * takes the q, k and v chains of one qkv output in one launch), or is
+ * stored that way by the qkv GEMM's epilogue (qkv_epilogue_chains). */
+struct qkv_chain {
+	int n, idx[8];
+	const struct sam3_tensor *src, *out, *cos_t, *sin_t;
+	long long col0, pitch;
+	int B, S, H, D;
+};
+static int match_qkv_chain(const struct sam3_graph *g, int i, struct use_map *uses,
+			   struct qkv_chain *c);
+
 /* Whether a node in [lo, hi) writes tensor r (its header, or its data). */
 static int written_between(const struct sam3_graph *g, int lo, int hi,
 			   const struct sam3_tensor *r)
@@ -539,6 +555,77 @@ static int written_between(const struct sam3_graph *g, int lo, int hi,
 			return 1;
 	}
 	return 0;
+}
+
+static int in_chains(const struct qkv_chain *cs, int n, int k)
+{
+	for (int c = 0; c < n; c++)
+		for (int t = 0; t < cs[c].n; t++)
+			if (cs[c].idx[t] == k)
+				return 1;
+	return 0;
+}
+
+static int same_data(const struct sam3_tensor *a, const struct sam3_tensor *b)
+{
+	return a && b && (a == b || (a->data && a->data == b->data));
+}
+
+/* The q/k/v chains (match_qkv_chain) that are the only readers of the
+ * f32 result `out` [M, N] of the GEMM at node i, whose folded nodes end
+ * before node j: chain y takes columns [y*E, (y+1)*E), E = H*D, n*E = N,
+ * the RoPE chains share one pair of tables, and storing the chains'
+ * outputs at node i changes nothing that another node before them reads
+ * or writes (no such node touches an output's buffer or writes a table).
+ * Returns the number of chains in cs, 0 when they do not fit. */
+static int qkv_epilogue_chains(const struct sam3_graph *g, int i, int j,
+			       const struct sam3_tensor *out, int M, int N, struct use_map *uses,
+			       const unsigned char *done, struct qkv_chain *cs)
+{
+	const struct s3h_settings *set = s3h_settings();
+	if (!set->qkv_fold || !set->qkv_chain)
+		return 0;
+	const int nu = uses_of(uses, out);
+	if (nu < 1 || nu > 3)
+		return 0;
+	const struct sam3_tensor *ct = NULL, *st = NULL;
+	int n = 0, k = j - 1, last = j - 1;
+	while (n < nu) {
+		k = next_reader(g, k + 1, out);
+		if (k < 0 || done[k] || !match_qkv_chain(g, k, uses, &cs[n]) || cs[n].src != out)
+			return 0;
+		const struct qkv_chain *c = &cs[n];
+		if (c->pitch != N || (long long)c->B * c->S != M ||
+		    c->col0 != (long long)n * c->H * c->D ||
+		    (n && (c->S != cs[0].S || c->H != cs[0].H || c->D != cs[0].D)))
+			return 0;
+		if (c->cos_t) {
+			if (ct && (c->cos_t != ct || c->sin_t != st))
+				return 0;
+			ct = c->cos_t;
+			st = c->sin_t;
+		}
+		for (int t = 0; t < c->n; t++)
+			last = c->idx[t] > last ? c->idx[t] : last;
+		n++;
+	}
+	if ((long long)n * cs[0].H * cs[0].D != N)
+		return 0;
+	for (int m = i + 1; m <= last; m++) {
+		if (m < j || in_chains(cs, n, m))
+			continue;
+		const struct sam3_node *o = &g->nodes[m];
+		if (ct && (same_data(o->output, ct) || same_data(o->output, st)))
+			return 0;
+		for (int c = 0; c < n; c++) {
+			if (same_data(o->output, cs[c].out))
+				return 0;
+			for (int q = 0; q < o->n_inputs && q < SAM3_NODE_MAX_INPUTS; q++)
+				if (same_data(o->inputs[q], cs[c].out))
+					return 0;
+		}
+	}
+	return n;
 }
 
 /* MATMUL at node i, plus the ADD(bias)/GELU nodes folded into it.
@@ -710,7 +797,58 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		    !s3h_matmul_out_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, o_fmt))
 			o_fmt = S3H_A_PLAIN;
 	}
-	if (o_fmt != S3H_A_PLAIN) {
+	/* an f32 result read only by the q/k/v chains of attention: stored
+	 * by the epilogue as their head-split outputs (RoPE applied) */
+	struct qkv_chain qcs[3];
+	int n_qkv = 0;
+	struct s3h_qkv qkv;
+	memset(&qkv, 0, sizeof(qkv));
+	if (o_fmt == S3H_A_PLAIN && !dres && !row_map[0] && c_dt == SAM3_DTYPE_F32 &&
+	    (n_qkv = qkv_epilogue_chains(g, i, j, out, M, N, uses, done, qcs)) > 0) {
+		static const float al[4] __attribute__((aligned(16)));
+		qkv.S = qcs[0].S;
+		qkv.H = qcs[0].H;
+		qkv.D = qcs[0].D;
+		for (int y = 0; y < n_qkv; y++) {
+			qkv.out[y] = (float *)al;
+			qkv.rope |= (qcs[y].cos_t != NULL) << y;
+			if (qcs[y].cos_t) {
+				qkv.cos_t = al;
+				qkv.sin_t = al;
+			}
+		}
+		if (!s3h_matmul_qkv_ok(a_fmt, a_dt, da, b_dt, db, M, N, K, flags, &qkv) ||
+		    (bias && ((uintptr_t)dbias & 15u)))
+			n_qkv = 0;
+	}
+	if (n_qkv) {
+		const struct sam3_tensor *ct = NULL, *st = NULL;
+		for (int y = 0; y < n_qkv && err == SAM3_OK; y++) {
+			void *dy = NULL;
+			err = dev_out(hb, qcs[y].out, &dy);
+			qkv.out[y] = (float *)dy;
+			if (qcs[y].cos_t) {
+				ct = qcs[y].cos_t;
+				st = qcs[y].sin_t;
+			}
+		}
+		void *dct = NULL, *dst = NULL;
+		if (err == SAM3_OK && ct)
+			err = dev_in(hb, ct, &dct);
+		if (err == SAM3_OK && st)
+			err = dev_in(hb, st, &dst);
+		qkv.cos_t = (const float *)dct;
+		qkv.sin_t = (const float *)dst;
+		if (err == SAM3_OK)
+			err = s3h_matmul_qkv(a_fmt, a_dt, da, b_dt, db, M, N, K, dbias, flags, &qkv,
+					     hb->stream);
+		if (err == SAM3_OK)
+			for (int y = 0; y < n_qkv; y++) {
+				for (int t = 0; t < qcs[y].n; t++)
+					done[qcs[y].idx[t]] = 1;
+				n_chain += qcs[y].n;
+			}
+	} else if (o_fmt != S3H_A_PLAIN) {
 		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
@@ -838,17 +976,7 @@ static int permute_operand_form(struct sam3_hip_backend *hb, const struct sam3_g
 }
 
 /* gh_multihead_attention_rope's q, k and v preparation
- * (graph_helpers.c:721-882): SLICE of the fused qkv output's columns ->
- * RESHAPE [B, S, H, D] -> (ROPE -> RESHAPE ...) -> TRANSPOSE (0, 2, 1, 3).
- * Every tensor in between is used once, so the chain runs as one kernel
- * from the qkv rows to the head-split operand (s3k_rope_split3, which
- * takes the q, k and v chains of one qkv output in one launch). */
-struct qkv_chain {
-	int n, idx[8];
-	const struct sam3_tensor *src, *out, *cos_t, *sin_t;
-	long long col0, pitch;
-	int B, S, H, D;
-};
+ * (graph_helpers.c:721-882): match_qkv_chain below. */
 
 static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t)
 {

@@ -100,6 +100,21 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 				  const void *b, void *c, int M, int N, int K, const void *bias,
 				  const void *res, const int *row_map, int flags, unsigned *ovf,
 				  unsigned ovf_tag, void *stream);
+/* The attention operands of a fused qkv projection: the f32 result
+ * [B*S, n_out*H*D] stored as n_out head-split tensors out[y] [B, H, S, D]
+ * (columns y*H*D onward), RoPE (cos / sin [S, D/2]) applied to operand y
+ * after the bias when bit y of rope is set (S3K_EPI_QKV). */
+struct s3h_qkv {
+	float *out[3];
+	const float *cos_t, *sin_t;
+	int S, H, D, rope;
+};
+/* Whether s3h_matmul_qkv can run this GEMM (s3h_matmul_fmt's, f32 out). */
+int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags, const struct s3h_qkv *q);
+enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M,
+			       int N, int K, const void *bias, int flags, const struct s3h_qkv *q,
+			       void *stream);
 
 /* Prepared copies of constant weights (bf16 hi/lo planes, padded rows),
  * kept by the backend whose graph_eval is running on this thread. A copy

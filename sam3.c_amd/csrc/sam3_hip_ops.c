@@ -960,6 +960,58 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 	return q8_f16_gemm(&g, stream);
 }
 
+static void fill_qkv(struct s3k_gemm *g, const struct s3h_qkv *q)
+{
+	for (int y = 0; y < 3; y++)
+		g->qkv_out[y] = q->out[y];
+	g->qkv_cos = q->cos_t;
+	g->qkv_sin = q->sin_t;
+	g->qkv_S = q->S;
+	g->qkv_H = q->H;
+	g->qkv_D = q->D;
+	g->qkv_rope = q->rope;
+	g->flags |= S3K_EPI_QKV;
+}
+
+/* The kernel's conditions (s3k_gemm_launch_path) on the GEMM that
+ * s3h_matmul_fmt_to would run, here for the operand geometry; the GEMM
+ * itself must reach the direct-to-LDS kernel (s3h_matmul_out_ok). */
+int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags, const struct s3h_qkv *q)
+{
+	if (!q || (flags & SAM3_HIP_GELU) || K % 64 || q->D < 4 || (q->D & (q->D - 1)) || q->H <= 0 ||
+	    q->S < 32 || M % q->S || (long long)q->H * q->D > (1 << 28) ||
+	    (long long)q->S * q->D > 0x7FFFFFFFLL || N % (q->H * q->D))
+		return 0;
+	const int n_out = N / (q->H * q->D);
+	if (n_out < 1 || n_out > 3 || q->rope < 0 || (q->rope >> n_out) ||
+	    (q->rope && (!q->cos_t || !q->sin_t ||
+			 (((uintptr_t)q->cos_t | (uintptr_t)q->sin_t) & 7u))))
+		return 0;
+	for (int y = 0; y < n_out; y++)
+		if (!q->out[y] || ((uintptr_t)q->out[y] & 15u))
+			return 0;
+	return s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN);
+}
+
+enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M,
+			       int N, int K, const void *bias, int flags, const struct s3h_qkv *q,
+			       void *stream)
+{
+	if (((flags & SAM3_HIP_BIAS) && (!bias || ((uintptr_t)bias & 15u))) ||
+	    !s3h_matmul_qkv_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, q)) {
+		s3h_error("matmul: cannot store the attention operands (M=%d N=%d K=%d)", M, N, K);
+		return SAM3_EINVAL;
+	}
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, q->out[0], M, N, K, bias, flags);
+	fill_qkv(&g, q);
+	if (b_dt == SAM3_DTYPE_F32)
+		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
+	g.a_kind = S3K_F16;
+	return q8_f16_gemm(&g, stream);
+}
+
 enum sam3_error sam3_hip_matmul(int a_dtype, const void *a, int b_dtype, const void *b,
 				int c_dtype, void *c, int M, int N, int K,
 				const void *bias, int flags, void *stream)

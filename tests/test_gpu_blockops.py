@@ -466,6 +466,85 @@ def test_qkv_slice_rope_split_chain(env):
         assert np.array_equal(f.view(np.uint32), r.transpose(0, 2, 1, 3).astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("cfg", [None, "20", "24", "2"], ids=["auto", "dlp256", "dlp192x128", "dl64"])
+@pytest.mark.parametrize("geom", [(3, 8, 4, 64), (2, 12, 5, 32)], ids=["s64h4d64", "s144h5d32"])
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_qkv_projection_stores_attention_operands(env, wkind, geom, cfg):
+    """gh_multihead_attention_rope after its LayerNorm (graph_helpers.c:
+    721-882): LN -> linear qkv (+ bias) -> the q / k / v chains (SLICE ->
+    RESHAPE -> ROPE -> ... -> TRANSPOSE 0,2,1,3). The qkv GEMM's epilogue
+    stores the three head-split operands itself, RoPE applied to q and k
+    after the bias, so the qkv rows are never written and the chain
+    kernel does not run. Same bits as the chain kernel on the GEMM's f32
+    result (SAM3_HIP_QKV_FOLD=0) on every tile shape (SAM3_HIP_DL_CFG;
+    the non-pipelined "2" is replaced by the pipelined 128x128 tile), and
+    equal to LN + matmul + RoPE of the oracle within f32 tolerance.
+    Shapes: partial M and N tiles, and a head size of 32."""
+    B, side, H, D = geom
+    S, E, Ein = side * side, H * D, 256
+    M = B * S
+    O = oracle()
+    x = synth.randn(870, (M, Ein), 2.0, 0.5)
+    gam, bet = synth.randn(871, (Ein,)), synth.randn(872, (Ein,), 0.1)
+    w = synth.randn(873, (3 * E, Ein), 0.05)
+    bias = synth.randn(874, (3 * E,), 0.02)
+    c, sn = graph.rope_tables(side, D)
+    if cfg is None:
+        env.unset("SAM3_HIP_DL_CFG")
+    else:
+        env.set("SAM3_HIP_DL_CFG", cfg)
+
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_QKV_FOLD")
+        else:
+            env.set("SAM3_HIP_QKV_FOLD", mode)
+        G = graph.Graph()
+        tx = G.tensor(abi.F32, (M, Ein), x)
+        t = G.layernorm(tx, G.tensor(abi.F32, (Ein,), gam), G.tensor(abi.F32, (Ein,), bet))
+        tw = (G.tensor(abi.Q8_0, (3 * E, Ein), O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, (3 * E, Ein), w))
+        qkv = G.linear(t, tw, G.tensor(abi.F32, (3 * E,), bias))
+        ct, st_ = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, sn.shape, sn)
+        sq, sk, sv = (G.slice(qkv, 1, i * E, (i + 1) * E) for i in range(3))
+        four = [B, S, H, D]
+        q = G.reshape(G.rope(G.reshape(sq, four), ct, st_), [M, E])
+        k = G.reshape(G.rope(G.reshape(sk, four), ct, st_), [M, E])
+        outs = [G.permute(G.reshape(t, four), (0, 2, 1, 3)) for t in (q, k, sv)]
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return [np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_float)), shape=(B, H, S, D)).copy()
+                for t in outs], st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st0.host_nodes == 0
+    assert st.gpu_nodes == st0.gpu_nodes - 1, (st.gpu_nodes, st0.gpu_nodes)
+    for f, p in zip(fused, plain):
+        assert np.array_equal(f.view(np.uint32), p.view(np.uint32))
+
+    ln = O.layernorm(x, gam, bet, "f32", threads=8)
+    wd = O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8" else w
+    y = (ln.astype(np.float64) @ wd.T.astype(np.float64) + bias).astype(np.float32)
+
+    def rope_ref(v):
+        v = v.reshape(B, S, H, D // 2, 2)
+        cc, ss = c[None, :, None, :], sn[None, :, None, :]
+        x0, x1 = v[..., 0], v[..., 1]
+        o0 = (x0 * cc).astype(np.float32) - (x1 * ss).astype(np.float32)
+        o1 = (x0 * ss).astype(np.float32) + (x1 * cc).astype(np.float32)
+        return np.stack([o0, o1], -1).reshape(B, S, H, D)
+
+    parts = [y[:, i * E:(i + 1) * E].reshape(B, S, H, D) for i in range(3)]
+    refs = [rope_ref(parts[0]), rope_ref(parts[1]), parts[2]]
+    for f, r, name in zip(fused, refs, "qkv"):
+        assert_f32_close(f, r.transpose(0, 2, 1, 3), what=f"qkv epilogue {name} {wkind} {geom}")
+
+
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
 def test_residual_add_folded_into_gemm(env, wkind):
     """x + linear(LN(x)) as the ViT block builds its residuals
