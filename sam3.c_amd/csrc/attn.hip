@@ -47,7 +47,19 @@ struct AttnArgs {
 	long long hq, hk;       /* per-head strides, elements */
 	int BH, nqb;            /* heads, query blocks per head */
 	int mask_vec;           /* mask rows 16-byte aligned: float4 loads */
+	int oh;                 /* > 0: output head-merged (at_out_row)      */
 };
+
+/* Element offset of output row q of head hh: [BH, Sq, D] rows, or with
+ * oh > 0 heads merged, hh = b*oh + h stored as row b*Sq + q, columns
+ * h*D.. of [B*Sq, oh*D] (the permute (0,2,1,3) of [B, oh, Sq, D]). */
+__device__ __forceinline__ long long at_out_row(int oh, long long hh, int Sq, int q, int D)
+{
+	if (oh <= 0)
+		return (hh * Sq + q) * (long long)D;
+	const long long b = hh / oh, h = hh - b * oh;
+	return ((b * Sq + q) * oh + h) * (long long)D;
+}
 
 constexpr int AT_D = 64, AT_BKV = 64;
 constexpr int AT_VT_PITCH = AT_BKV * 2 + 8;          /* bytes per V^T row */
@@ -608,11 +620,12 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK, VD>())) attn_f
 				const int d0 = 32 * md + 8 * g + 4 * h;
 				const float x0 = o[md][4 * g] * inv, x1 = o[md][4 * g + 1] * inv;
 				const float x2 = o[md][4 * g + 2] * inv, x3 = o[md][4 * g + 3] * inv;
+				const long long orow = at_out_row(p.oh, head, p.Sq, q, AT_D);
 				if constexpr (C::SPLIT) {
-					float *O = (float *)p.out + head * p.hq + (long long)q * AT_D;
+					float *O = (float *)p.out + orow;
 					*(float4 *)(O + d0) = make_float4(x0, x1, x2, x3);
 				} else {
-					uint16_t *O = (uint16_t *)p.out + head * p.hq + (long long)q * AT_D;
+					uint16_t *O = (uint16_t *)p.out + orow;
 					*(uint2 *)(O + d0) = make_uint2(at_pack2<DT>(x0, x1), at_pack2<DT>(x2, x3));
 				}
 			}
@@ -628,6 +641,7 @@ struct AttnGArgs {
 	char *out;
 	int BH, Sq, Sk, D;
 	float scale;
+	int oh;                 /* > 0: output head-merged (at_out_row) */
 };
 
 template <int DT>
@@ -728,7 +742,7 @@ __global__ void __launch_bounds__(256) attn_generic(AttnGArgs p)
 		for (int i = 0; i < NACC; ++i) {
 			const int d = lane + 64 * i;
 			if (d < p.D)
-				at_st<DT>(p.out, row * p.D + d, acc[i] * inv);
+				at_st<DT>(p.out, at_out_row(p.oh, head, p.Sq, qi, p.D) + d, acc[i] * inv);
 		}
 	}
 }
@@ -775,12 +789,14 @@ extern "C" int s3k_attn_path(int kind, const void *q, const void *k, const void 
 	return 0;
 }
 
-extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
-			const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream)
+extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
+			      const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
+			      void *stream)
 {
 	const int best = s3k_attn_path(kind, q, k, v, out, BH, Sq, Sk, D);
 	if (!best || (path == S3K_ATTN_MFMA && best != S3K_ATTN_MFMA) ||
-	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC))
+	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC) || oh < 0 ||
+	    (oh > 0 && BH % oh))
 		return (int)hipErrorInvalidValue;
 	if ((long long)BH * Sq == 0)
 		return (int)hipSuccess;
@@ -798,6 +814,7 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 		g.Sq = Sq;
 		g.Sk = Sk;
 		g.D = D;
+		g.oh = oh;
 		g.scale = 1.0f / sqrtf((float)D);
 		if (kind == S3K_F32)
 			launch_generic<S3K_F32>(g, st);
@@ -826,6 +843,7 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 			nw = env;
 	}
 	p.BH = BH;
+	p.oh = oh;
 	p.nqb = (Sq + 32 * nw - 1) / (32 * nw);
 	const dim3 grid((unsigned)((long long)p.nqb * BH));
 	const dim3 block(64 * nw);
@@ -860,4 +878,10 @@ extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const 
 	}
 #undef S3K_ATTN_GO
 	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
+			const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream)
+{
+	return s3k_attn_heads(path, kind, q, k, v, mask, out, BH, Sq, Sk, D, 0, stream);
 }

@@ -547,16 +547,19 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	return p;
 }
 
-/* What the S3K_EPI_QKV epilogue assumes (struct s3k_gemm): the
- * pipelined direct-to-LDS kernel (whole 64-k steps) with f32 output, one
- * batch slice, no residual, row map or GELU, and the operand geometry
- * below. */
-static bool qkv_ok(const struct s3k_gemm *g)
+/* What the S3K_EPI_QKV epilogue assumes (struct s3k_gemm) on `path`:
+ * f32 output, one batch slice, no residual, row map or GELU, the operand
+ * geometry below, and either the pipelined direct-to-LDS kernel (whole
+ * 64-k steps, sequences of at least 32 rows) or the streaming skinny
+ * kernel (no RoPE; its own checks in s3k_skinny_launch). */
+static bool qkv_ok(const struct s3k_gemm *g, int path)
 {
 	const int D = g->qkv_D, H = g->qkv_H, S = g->qkv_S;
+	const bool sk = path == S3K_PATH_SKINNY;
 	if (g->c_kind != S3K_F32 || g->batch != 1 || (g->flags & (S3K_EPI_RES | S3K_EPI_GELU)) ||
-	    g->rm_g || g->K % 64 || D < 4 || (D & (D - 1)) || H <= 0 || S < 32 || g->M % S ||
-	    (long long)H * D > (1 << 28) || (long long)S * D > 0x7FFFFFFFLL)
+	    g->rm_g || (!sk && g->K % 64) || D < 4 || (D & (D - 1)) || H <= 0 || S < (sk ? 1 : 32) ||
+	    g->M % S || (sk && g->qkv_rope) || (long long)H * D > (1 << 28) ||
+	    (long long)S * D > 0x7FFFFFFFLL)
 		return false;
 	const int E = H * D, n_out = g->N / E;
 	if (g->N % E || n_out < 1 || n_out > 3 || g->qkv_rope < 0 || (g->qkv_rope >> n_out))
@@ -569,7 +572,7 @@ static bool qkv_ok(const struct s3k_gemm *g)
 		return false;
 	if ((g->flags & S3K_EPI_BIAS) && (!g->bias || ((uintptr_t)g->bias & 15u)))
 		return false;
-	return s3k_dl_ok(g);
+	return sk ? s3k_skinny_ok(g) != 0 : s3k_dl_ok(g);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int FAM, int CK, class LA, class LB>
@@ -689,7 +692,9 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	     (g->rm_g && (g->rm_d1 <= 0 || g->rm_d2 <= 0 ||
 			  g->M % ((long long)g->rm_g * g->rm_d1 * g->rm_d2)))))
 		return (int)hipErrorInvalidValue;
-	if ((g->flags & S3K_EPI_QKV) && (path != S3K_PATH_MFMA || !mfma_ok(g) || !qkv_ok(g)))
+	if ((g->flags & S3K_EPI_QKV) &&
+	    ((path != S3K_PATH_MFMA && path != S3K_PATH_SKINNY) ||
+	     (path == S3K_PATH_MFMA && !mfma_ok(g)) || !qkv_ok(g, path)))
 		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))

@@ -154,6 +154,13 @@ int s3k_attn_path(int kind, const void *q, const void *k, const void *v, void *o
 		  int BH, int Sq, int Sk, int D);
 int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
 	     const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream);
+/* s3k_attn with the heads merged in the output (oh > 0 heads per batch
+ * item, oh | BH): head b*oh + h, query q is stored at row b*Sq + q,
+ * columns h*D.., of [BH/oh * Sq, oh*D], the permute (0,2,1,3) of
+ * [BH/oh, oh, Sq, D]. oh = 0 is s3k_attn. */
+int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
+		   const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
+		   void *stream);
 /* ViT block ops (blockops.hip). LayerNorm over the last dim of rows x
  * cols (gamma/beta of the input's kind or NULL, eps 1e-5); RoPE on
  * interleaved pairs of x [batch, seq, heads, hd] with f32 cos/sin
@@ -268,7 +275,7 @@ struct s3h_settings {
 	int q8_batch_path;                /* SAM3_HIP_Q8_BATCH_PATH: 0, 1, 2     */
 	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
 	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
-	    permute_operand, partition_fold, qkv_fold;
+	    permute_operand, partition_fold, qkv_fold, sdpa_merge;
 	int readback_all;                 /* SAM3_HIP_READBACK=all               */
 	int quiet;                        /* SAM3_HIP_QUIET set                  */
 	int arena_mb;                     /* SAM3_HIP_ARENA_MB (0 = default)     */

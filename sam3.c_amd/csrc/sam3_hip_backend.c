@@ -1362,6 +1362,73 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 	return err;
 }
 
+/* gh_multihead_attention_rope's head merge (graph_helpers.c:721-882):
+ * an SDPA node whose one reader is TRANSPOSE (0,2,1,3) of its
+ * [B, H, Sq, D] output, when that transpose is not written as a GEMM's
+ * operand: the attention kernel stores the merged rows itself. Returns
+ * the transpose's node index, or -1. Storing the transpose's output at
+ * node i must change nothing another node before it reads or writes. */
+static int sdpa_merge_target(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			     struct use_map *uses, const unsigned char *done)
+{
+	const struct s3h_settings *set = s3h_settings();
+	const struct sam3_node *n = &g->nodes[i];
+	if (!set->sdpa_merge || n->op != SAM3_OP_SDPA || !n->output || !s3h_sdpa_node_ok(n))
+		return -1;
+	const struct sam3_tensor *o = n->output, *q = n->inputs[0];
+	if (q->n_dims != 4 || o->n_dims != 4 || !dims_are(o, q->dims[0], q->dims[1], q->dims[2],
+							   n->params[0]) ||
+	    uses_of(uses, o) != 1)
+		return -1;
+	const int j = next_reader(g, i + 1, o);
+	if (j < 0 || done[j])
+		return -1;
+	const struct sam3_node *t = &g->nodes[j];
+	if (t->op != SAM3_OP_TRANSPOSE || t->n_inputs < 1 || t->inputs[0] != o || !t->output ||
+	    t->params[0] != 0 || t->params[1] != 2 || t->params[2] != 1 || t->params[3] != 3 ||
+	    t->output->dtype != o->dtype ||
+	    !dims_are(t->output, o->dims[0], o->dims[2], o->dims[1], o->dims[3]))
+		return -1;
+	int k = 0;
+	if (set->permute_operand && permute_operand_form(hb, g, j, uses, &k) != S3H_A_PLAIN)
+		return -1;
+	for (int m = i + 1; m < j; m++) {
+		const struct sam3_node *x = &g->nodes[m];
+		if (same_data(x->output, t->output))
+			return -1;
+		for (int r = 0; r < x->n_inputs && r < SAM3_NODE_MAX_INPUTS; r++)
+			if (same_data(x->inputs[r], t->output))
+				return -1;
+	}
+	return j;
+}
+
+static enum sam3_error run_sdpa_merged(struct sam3_hip_backend *hb, const struct sam3_node *n,
+				       const struct sam3_node *t)
+{
+	struct sam3_tensor tin[SAM3_NODE_MAX_INPUTS];
+	struct sam3_node dn = *n;
+	enum sam3_error err = SAM3_OK;
+	for (int k = 0; k < n->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++) {
+		if (!n->inputs[k])
+			continue;
+		tin[k] = *n->inputs[k];
+		err = dev_in(hb, n->inputs[k], &tin[k].data);
+		if (err != SAM3_OK)
+			return err;
+		dn.inputs[k] = &tin[k];
+	}
+	void *dy = NULL;
+	err = dev_out(hb, t->output, &dy);
+	if (err == SAM3_OK)
+		err = s3h_sdpa_merged(&dn, dy, hb->stream);
+	if (err == SAM3_OK) {
+		hb->stats.gpu_nodes++;
+		hb->stats.fused_nodes++;
+	}
+	return err;
+}
+
 static int runs_on_gpu(const struct sam3_node *n)
 {
 	if (n->n_inputs < 1 || !n->inputs[0])
@@ -1440,7 +1507,7 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 	const int qkv_plain = !set->qkv_chain;
 	const int ln_plain = !set->ln_operand;
 	const int perm_plain = !set->permute_operand;
-	int ln_fmt = S3H_A_PLAIN, perm_k = 0;
+	int ln_fmt = S3H_A_PLAIN, perm_k = 0, merge_j = -1;
 	const int part_plain = !set->partition_fold;
 	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
 	const struct sam3_tensor *lt = NULL;
@@ -1480,6 +1547,11 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 		} else if (n->op == SAM3_OP_TRANSPOSE && !perm_plain &&
 			   (ln_fmt = permute_operand_form(hb, g, i, &uses, &perm_k)) != S3H_A_PLAIN) {
 			err = run_permute_as(hb, n, ln_fmt, perm_k);
+		} else if (n->op == SAM3_OP_SDPA &&
+			   (merge_j = sdpa_merge_target(hb, g, i, &uses, done)) >= 0) {
+			err = run_sdpa_merged(hb, n, &g->nodes[merge_j]);
+			if (err == SAM3_OK)
+				done[merge_j] = 1;
 		} else if (runs_on_gpu(n)) {
 			err = run_elementwise(hb, n);
 		} else {

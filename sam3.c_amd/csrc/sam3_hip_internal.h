@@ -17,6 +17,10 @@ size_t s3h_dtype_size(int dtype);
 long long s3h_nelems(const struct sam3_tensor *t);
 size_t s3h_tensor_bytes(const struct sam3_tensor *t);
 
+/* SDPA node on device tensors with its output stored head-merged
+ * ([B, Sq, H, D], the TRANSPOSE (0,2,1,3) of the node's output). */
+enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, void *stream);
+
 /* Device-pointer elementwise nodes used by the dispatcher and graph_eval. */
 enum sam3_error s3h_add(const struct sam3_node *node, void *stream);
 enum sam3_error s3h_gelu(const struct sam3_node *node, void *stream);

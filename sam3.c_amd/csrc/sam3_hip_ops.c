@@ -973,14 +973,32 @@ static void fill_qkv(struct s3k_gemm *g, const struct s3h_qkv *q)
 	g->flags |= S3K_EPI_QKV;
 }
 
+/* A Q8_0 GEMM on the streaming skinny kernel that takes the head-split
+ * stores (no RoPE): f32 activations read as they are (the kernel scales
+ * rows into the f16 range itself) or an f16 operand a producer wrote. */
+static int qkv_skinny(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
+		      int K, int flags)
+{
+	if (b_dt != SAM3_DTYPE_Q8_0 || a_dt != SAM3_DTYPE_F32 || !(flags & SAM3_HIP_B_NT))
+		return 0;
+	static const char al[16] __attribute__((aligned(16)));
+	struct s3k_gemm g;
+	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
+	if (a_fmt == S3H_A_F16)
+		return skinny_takes_f16(&g);
+	return a_fmt == S3H_A_PLAIN && s3k_gemm_path(&g) == S3K_PATH_SKINNY &&
+	       !rounds_a_to_f16(&g, S3K_PATH_SKINNY);
+}
+
 /* The kernel's conditions (s3k_gemm_launch_path) on the GEMM that
  * s3h_matmul_fmt_to would run, here for the operand geometry; the GEMM
- * itself must reach the direct-to-LDS kernel (s3h_matmul_out_ok). */
+ * itself must reach the direct-to-LDS kernel (s3h_matmul_out_ok) or,
+ * without RoPE, the streaming skinny kernel. */
 int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags, const struct s3h_qkv *q)
 {
-	if (!q || (flags & SAM3_HIP_GELU) || K % 64 || q->D < 4 || (q->D & (q->D - 1)) || q->H <= 0 ||
-	    q->S < 32 || M % q->S || (long long)q->H * q->D > (1 << 28) ||
+	if (!q || (flags & SAM3_HIP_GELU) || q->D < 4 || (q->D & (q->D - 1)) || q->H <= 0 ||
+	    q->S < 1 || M % q->S || (long long)q->H * q->D > (1 << 28) ||
 	    (long long)q->S * q->D > 0x7FFFFFFFLL || N % (q->H * q->D))
 		return 0;
 	const int n_out = N / (q->H * q->D);
@@ -991,7 +1009,10 @@ int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 	for (int y = 0; y < n_out; y++)
 		if (!q->out[y] || ((uintptr_t)q->out[y] & 15u))
 			return 0;
-	return s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN);
+	if (!q->rope && qkv_skinny(a_fmt, a_dt, a, b_dt, b, M, N, K, flags))
+		return 1;
+	return K % 64 == 0 && q->S >= 32 &&
+	       s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN);
 }
 
 enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M,
@@ -1006,6 +1027,12 @@ enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, con
 	struct s3k_gemm g;
 	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, q->out[0], M, N, K, bias, flags);
 	fill_qkv(&g, q);
+	if (!q->rope && qkv_skinny(a_fmt, a_dt, a, b_dt, b, M, N, K, flags)) {
+		if (a_fmt == S3H_A_F16)
+			g.a_kind = S3K_F16;
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
+			       "matmul skinny (attention operands)");
+	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
 	g.a_kind = S3K_F16;
@@ -2313,6 +2340,33 @@ enum sam3_error sam3_hip_kernel_sdpa(const struct sam3_node *node, void *stream)
 	return sam3_hip_sdpa(node->inputs[0]->dtype, node->inputs[0]->data, node->inputs[1]->data,
 			     node->inputs[2]->data, M ? (const float *)M->data : NULL,
 			     node->output->data, BH, Sq, Sk, D, stream);
+}
+
+/* The SDPA node (4-D [B, H, Sq, D]) with its output stored head-merged
+ * at `out`: [B, Sq, H, D], what TRANSPOSE (0,2,1,3) of its output
+ * gives. Inputs read from the node's tensors' data (device addresses). */
+enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, void *stream)
+{
+	int BH, Sq, Sk, D;
+	enum sam3_error err = sdpa_shape(node, &BH, &Sq, &Sk, &D, 0);
+	if (err != SAM3_OK)
+		return err;
+	const struct sam3_tensor *Q = node->inputs[0];
+	if (Q->n_dims != 4 || !out) {
+		s3h_error("sdpa: head-merged output needs 4-D tensors");
+		return SAM3_EINVAL;
+	}
+	const struct sam3_tensor *M = node->n_inputs > 3 ? node->inputs[3] : NULL;
+	const int dt = Q->dtype;
+	if (!s3k_attn_path(dt, Q->data, node->inputs[1]->data, node->inputs[2]->data, out, BH, Sq,
+			   Sk, D)) {
+		s3h_error("sdpa: no kernel for D=%d", D);
+		return SAM3_EINVAL;
+	}
+	return s3h_hip(s3k_attn_heads(0, dt, Q->data, node->inputs[1]->data, node->inputs[2]->data,
+				      M ? (const float *)M->data : NULL, out, BH, Sq, Sk, D,
+				      Q->dims[1], stream),
+		       "sdpa (heads merged)");
 }
 
 enum sam3_error sam3_hip_dispatch_node(const struct sam3_node *node, void *stream)

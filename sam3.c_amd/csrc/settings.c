@@ -57,6 +57,7 @@ static void parse(struct s3h_settings *s)
 	s->permute_operand = env_on("SAM3_HIP_PERMUTE_OPERAND");
 	s->partition_fold = env_on("SAM3_HIP_PARTITION_FOLD");
 	s->qkv_fold = env_on("SAM3_HIP_QKV_FOLD");
+	s->sdpa_merge = env_on("SAM3_HIP_SDPA_MERGE");
 	const char *rb = getenv("SAM3_HIP_READBACK");
 	s->readback_all = rb && rb[0] == 'a' && rb[1] == 'l' && rb[2] == 'l' && !rb[3];
 	s->quiet = getenv("SAM3_HIP_QUIET") != NULL;

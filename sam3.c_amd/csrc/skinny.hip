@@ -210,6 +210,9 @@ struct StreamArgs {
 	const float *rs;           /* S3K_EPI_ROWSCALE row factors ...        */
 	long long rs_sb;           /* ... and their batch stride              */
 	const float *res;          /* S3K_EPI_RES: f32 [M, N], pitch N (batch 1) */
+	/* S3K_EPI_QKV without RoPE (struct s3k_gemm): the head-split stores */
+	float *qkv_out[3];
+	int qkv_S, qkv_H, qkv_dsh;
 };
 
 template <int AK, int MR, int NT, int KC>
@@ -516,7 +519,16 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		float o = epilogue<0>(s, bv, p.flags);
 		if (p.flags & S3K_EPI_RES)
 			o += p.res[(long long)(m0 + m) * p.N + n];
-		cb[(long long)(m0 + m) * p.ldc + n] = o;
+		if (p.flags & S3K_EPI_QKV) {
+			/* column n: operand y, head h, element d; row: (b, s) */
+			const int D = 1 << p.qkv_dsh, E = p.qkv_H << p.qkv_dsh;
+			const int y = (n >= E) + (n >= 2 * E), r = n - y * E;
+			const int mm = m0 + m, b = mm / p.qkv_S, sq = mm - b * p.qkv_S;
+			float *oy = y == 0 ? p.qkv_out[0] : y == 1 ? p.qkv_out[1] : p.qkv_out[2];
+			oy[(((long long)b * p.qkv_H + (r >> p.qkv_dsh)) * p.qkv_S + sq) * D + (r & (D - 1))] = o;
+		} else {
+			cb[(long long)(m0 + m) * p.ldc + n] = o;
+		}
 	}
 }
 
@@ -642,6 +654,11 @@ static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 	p.rs = g->rs;
 	p.rs_sb = g->rs_sb;
 	p.res = (const float *)g->res;
+	for (int y = 0; y < 3; ++y)
+		p.qkv_out[y] = g->qkv_out[y];
+	p.qkv_S = g->qkv_S;
+	p.qkv_H = g->qkv_H;
+	p.qkv_dsh = g->qkv_D > 0 ? __builtin_ctz((unsigned)g->qkv_D) : 0;
 	dim3 grid(p.groups * p.zsplit, g->batch);
 	hipLaunchKernelGGL((q8_stream<AK, MR, NT, KC>), grid,
 			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), 0, (hipStream_t)stream, p);
@@ -749,6 +766,9 @@ static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
 
 extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 {
+	/* the head-split stores (no RoPE) exist in q8_stream only */
+	if ((g->flags & S3K_EPI_QKV) && (!stream_ok(g) || g->batch != 1 || g->qkv_rope))
+		return (int)hipErrorInvalidValue;
 	if (stream_ok(g)) {
 		int mr, nt;
 		stream_pick(g, &mr, &nt);

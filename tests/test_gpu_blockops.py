@@ -545,6 +545,101 @@ def test_qkv_projection_stores_attention_operands(env, wkind, geom, cfg):
         assert_f32_close(f, r.transpose(0, 2, 1, 3), what=f"qkv epilogue {name} {wkind} {geom}")
 
 
+@pytest.mark.parametrize("S", [1, 8, 77])
+def test_skinny_qkv_stores_attention_operands(env, S):
+    """The text encoder's attention operands (text_encoder.c:588-652, no
+    RoPE): x -> linear qkv (Q8_0, + bias) on the streaming skinny kernel ->
+    SLICE -> RESHAPE -> TRANSPOSE (0,2,1,3) for q, k and v. The skinny
+    GEMM's epilogue stores the head-split operands itself: same bits as
+    the chain kernel on its f32 result (SAM3_HIP_QKV_FOLD=0), and the
+    oracle's Q8 matmul within f32 tolerance."""
+    H, D, Ein = 16, 64, 1024
+    E = H * D
+    O = oracle()
+    x = synth.randn(880 + S, (S, Ein))
+    w = synth.randn(881, (3 * E, Ein), 0.02)
+    bias = synth.randn(882, (3 * E,), 0.02)
+    wq = O.q8_quantize(w)
+
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_QKV_FOLD")
+        else:
+            env.set("SAM3_HIP_QKV_FOLD", mode)
+        G = graph.Graph()
+        tx = G.tensor(abi.F32, (S, Ein), x)
+        qkv = G.linear(tx, G.tensor(abi.Q8_0, (3 * E, Ein), wq), G.tensor(abi.F32, (3 * E,), bias))
+        four = [1, S, H, D]
+        outs = [G.permute(G.reshape(G.slice(qkv, 1, i * E, (i + 1) * E), four), (0, 2, 1, 3))
+                for i in range(3)]
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return [np.ctypeslib.as_array(C.cast(t.data, C.POINTER(C.c_float)), shape=(1, H, S, D)).copy()
+                for t in outs], st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st0.host_nodes == 0
+    assert st.gpu_nodes == 1 and st0.gpu_nodes == 2, (st.gpu_nodes, st0.gpu_nodes)
+    for f, p in zip(fused, plain):
+        assert np.array_equal(f.view(np.uint32), p.view(np.uint32))
+    wd = O.q8_dequantize(wq, w.size).reshape(w.shape)
+    y = (x.astype(np.float64) @ wd.T.astype(np.float64) + bias).astype(np.float32)
+    for i, (f, name) in enumerate(zip(fused, "qkv")):
+        ref = y[:, i * E:(i + 1) * E].reshape(1, S, H, D).transpose(0, 2, 1, 3)
+        assert_f32_close(f, ref, what=f"skinny qkv epilogue {name} S={S}")
+
+
+@pytest.mark.parametrize("dt", [abi.F32, abi.BF16, abi.F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("B,H,S", [(1, 16, 1), (1, 16, 77), (2, 3, 300)])
+def test_sdpa_stores_heads_merged(env, dt, B, H, S):
+    """SDPA -> TRANSPOSE (0,2,1,3), the head merge of
+    gh_multihead_attention_rope when no GEMM takes the result as its
+    operand (the text encoder's skinny output projection): the attention
+    kernel stores the merged rows itself, one launch instead of two.
+    Same bits as the SDPA node followed by the permute kernel
+    (SAM3_HIP_SDPA_MERGE=0), masked, on the MFMA kernel (D = 64) and the
+    any-D kernel (D = 32)."""
+    def to_dtype(x):
+        if dt == abi.F32:
+            return np.ascontiguousarray(x, np.float32)
+        if dt == abi.F16:
+            return np.ascontiguousarray(x, np.float32).astype(np.float16).view(np.uint16)
+        return oracle().f32_to_bf16(x).reshape(x.shape)
+
+    for D in (64, 32):
+        q, k, v = (synth.randn(890 + i, (B, H, S, D)) for i in range(3))
+        c = np.arange(S)
+        mask = np.where(c[None, :] > c[:, None], np.float32(-1e9), np.float32(0)).astype(np.float32)
+        nbytes = B * S * H * D * (4 if dt == abi.F32 else 2)
+
+        def run(mode):
+            if mode is None:
+                env.unset("SAM3_HIP_SDPA_MERGE")
+            else:
+                env.set("SAM3_HIP_SDPA_MERGE", mode)
+            G = graph.Graph()
+            tq, tk, tv = (G.tensor(dt, x.shape, to_dtype(x)) for x in (q, k, v))
+            o = G.permute(G.sdpa(tq, tk, tv, G.tensor(abi.F32, mask.shape, mask)), (0, 2, 1, 3))
+            be = hip.Backend(0)
+            try:
+                assert be.graph_eval(G.g) == abi.OK
+                st = be.stats()
+            finally:
+                be.close()
+            got = np.ctypeslib.as_array(C.cast(o.data, C.POINTER(C.c_uint8)), shape=(nbytes,)).copy()
+            return got, st
+
+        fused, st = run(None)
+        plain, st0 = run("0")
+        assert st.gpu_nodes == 1 and st0.gpu_nodes == 2, (D, st.gpu_nodes, st0.gpu_nodes)
+        assert np.array_equal(fused, plain), D
+
+
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
 def test_residual_add_folded_into_gemm(env, wkind):
     """x + linear(LN(x)) as the ViT block builds its residuals
