@@ -467,7 +467,8 @@ def test_qkv_slice_rope_split_chain(env):
 
 
 @pytest.mark.parametrize("cfg", [None, "20", "24", "2"], ids=["auto", "dlp256", "dlp192x128", "dl64"])
-@pytest.mark.parametrize("geom", [(3, 8, 4, 64), (2, 12, 5, 32)], ids=["s64h4d64", "s144h5d32"])
+@pytest.mark.parametrize("geom", [(3, 8, 4, 64), (2, 12, 5, 32), (2, 8, 2, 128)],
+                         ids=["s64h4d64", "s144h5d32", "s64h2d128"])
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
 def test_qkv_projection_stores_attention_operands(env, wkind, geom, cfg):
     """gh_multihead_attention_rope after its LayerNorm (graph_helpers.c:
@@ -479,7 +480,8 @@ def test_qkv_projection_stores_attention_operands(env, wkind, geom, cfg):
     result (SAM3_HIP_QKV_FOLD=0) on every tile shape (SAM3_HIP_DL_CFG;
     the non-pipelined "2" is replaced by the pipelined 128x128 tile), and
     equal to LN + matmul + RoPE of the oracle within f32 tolerance.
-    Shapes: partial M and N tiles, and a head size of 32."""
+    Shapes: partial M and N tiles, head sizes of 32 (a wave's columns
+    span two heads) and 128 (half a head)."""
     B, side, H, D = geom
     S, E, Ein = side * side, H * D, 256
     M = B * S
