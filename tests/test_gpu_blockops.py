@@ -467,7 +467,7 @@ def test_qkv_slice_rope_split_chain(env):
 
 
 @pytest.mark.parametrize("cfg", [None, "20", "24", "2"], ids=["auto", "dlp256", "dlp192x128", "dl64"])
-@pytest.mark.parametrize("geom", [(3, 8, 4, 64), (2, 12, 5, 32), (2, 8, 2, 128)],
+@pytest.mark.parametrize("geom", [(3, 8, 4, 64), (2, 12, 5, 32), (3, 8, 2, 128)],
                          ids=["s64h4d64", "s144h5d32", "s64h2d128"])
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
 def test_qkv_projection_stores_attention_operands(env, wkind, geom, cfg):
