@@ -48,6 +48,11 @@ struct AttnArgs {
 	int BH, nqb;            /* heads, query blocks per head */
 	int mask_vec;           /* mask rows 16-byte aligned: float4 loads */
 	int oh;                 /* > 0: output head-merged (at_out_row)      */
+	int ofmt;               /* merged f32 rows written as a GEMM operand:
+				 * 0 f32, 1 bf16 planes [hi|lo|hi] (row pitch
+				 * 3*oh*D), 2 f16 with the range flag        */
+	unsigned *ovf;          /* ofmt 2: range flag (or NULL) and its tag  */
+	unsigned ovf_tag;
 };
 
 /* Element offset of output row q of head hh: [BH, Sq, D] rows, or with
@@ -622,8 +627,36 @@ __global__ void __launch_bounds__(64 * NW, (at_minb<DT, NW, MASK, VD>())) attn_f
 				const float x2 = o[md][4 * g + 2] * inv, x3 = o[md][4 * g + 3] * inv;
 				const long long orow = at_out_row(p.oh, head, p.Sq, q, AT_D);
 				if constexpr (C::SPLIT) {
-					float *O = (float *)p.out + orow;
-					*(float4 *)(O + d0) = make_float4(x0, x1, x2, x3);
+					if (p.ofmt == 1) {
+						/* the merged row r = orow / K as bf16 planes,
+						 * the split of split3 / the permute kernel */
+						const long long K = (long long)p.oh * AT_D, r = orow / K;
+						uint16_t *dp = (uint16_t *)p.out + r * 3 * K + (orow - r * K) + d0;
+						uint32_t hi[2], lo[2];
+						split_bf16x2(x0, x1, hi[0], lo[0]);
+						split_bf16x2(x2, x3, hi[1], lo[1]);
+						*(uint2 *)dp = make_uint2(hi[0], hi[1]);
+						*(uint2 *)(dp + K) = make_uint2(lo[0], lo[1]);
+						*(uint2 *)(dp + 2 * K) = make_uint2(hi[0], hi[1]);
+					} else if (p.ofmt == 2) {
+						/* f16, flagged as the permute kernel flags it: a
+						 * value past 2^15, or four nonzero values all
+						 * below 2^-10 */
+						const float ax = __builtin_fabsf(x0), ay = __builtin_fabsf(x1);
+						const float az = __builtin_fabsf(x2), aw = __builtin_fabsf(x3);
+						const float mx = fmaxf(fmaxf(ax, ay), fmaxf(az, aw));
+						const bool big = (ax >= 32768.0f && ax <= 3.402823466e38f) ||
+								 (ay >= 32768.0f && ay <= 3.402823466e38f) ||
+								 (az >= 32768.0f && az <= 3.402823466e38f) ||
+								 (aw >= 32768.0f && aw <= 3.402823466e38f);
+						if (p.ovf && (big || (mx > 0.0f && mx < 0x1p-10f)))
+							*p.ovf = p.ovf_tag;
+						*(uint2 *)((uint16_t *)p.out + orow + d0) =
+							make_uint2(pack_f16x2(x0, x1), pack_f16x2(x2, x3));
+					} else {
+						float *O = (float *)p.out + orow;
+						*(float4 *)(O + d0) = make_float4(x0, x1, x2, x3);
+					}
 				} else {
 					uint16_t *O = (uint16_t *)p.out + orow;
 					*(uint2 *)(O + d0) = make_uint2(at_pack2<DT>(x0, x1), at_pack2<DT>(x2, x3));
@@ -791,12 +824,13 @@ extern "C" int s3k_attn_path(int kind, const void *q, const void *k, const void 
 
 extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
 			      const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
-			      void *stream)
+			      int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream)
 {
 	const int best = s3k_attn_path(kind, q, k, v, out, BH, Sq, Sk, D);
 	if (!best || (path == S3K_ATTN_MFMA && best != S3K_ATTN_MFMA) ||
 	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC) || oh < 0 ||
-	    (oh > 0 && BH % oh))
+	    (oh > 0 && BH % oh) || ofmt < 0 || ofmt > 2 ||
+	    (ofmt && (oh <= 0 || kind != S3K_F32 || best != S3K_ATTN_MFMA || path == S3K_ATTN_GENERIC)))
 		return (int)hipErrorInvalidValue;
 	if ((long long)BH * Sq == 0)
 		return (int)hipSuccess;
@@ -844,6 +878,9 @@ extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, 
 	}
 	p.BH = BH;
 	p.oh = oh;
+	p.ofmt = ofmt;
+	p.ovf = ovf;
+	p.ovf_tag = ovf_tag;
 	p.nqb = (Sq + 32 * nw - 1) / (32 * nw);
 	const dim3 grid((unsigned)((long long)p.nqb * BH));
 	const dim3 block(64 * nw);
@@ -883,5 +920,5 @@ extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, 
 extern "C" int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
 			const float *mask, void *out, int BH, int Sq, int Sk, int D, void *stream)
 {
-	return s3k_attn_heads(path, kind, q, k, v, mask, out, BH, Sq, Sk, D, 0, stream);
+	return s3k_attn_heads(path, kind, q, k, v, mask, out, BH, Sq, Sk, D, 0, 0, nullptr, 0, stream);
 }

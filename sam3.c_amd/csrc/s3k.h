@@ -157,10 +157,13 @@ int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
 /* s3k_attn with the heads merged in the output (oh > 0 heads per batch
  * item, oh | BH): head b*oh + h, query q is stored at row b*Sq + q,
  * columns h*D.., of [BH/oh * Sq, oh*D], the permute (0,2,1,3) of
- * [BH/oh, oh, Sq, D]. oh = 0 is s3k_attn. */
+ * [BH/oh, oh, Sq, D]. oh = 0 is s3k_attn. ofmt (f32 on the MFMA kernel
+ * only): 0 f32 rows, S3K_LN_PLANES bf16 planes [hi|lo|hi] with row pitch
+ * 3*oh*D, S3K_LN_F16 f16 rows storing ovf_tag to *ovf (when set) as
+ * s3k_permute_to does: the merged rows as a GEMM's operand. */
 int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
 		   const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
-		   void *stream);
+		   int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream);
 /* ViT block ops (blockops.hip). LayerNorm over the last dim of rows x
  * cols (gamma/beta of the input's kind or NULL, eps 1e-5); RoPE on
  * interleaved pairs of x [batch, seq, heads, hd] with f32 cos/sin

@@ -1364,12 +1364,13 @@ static enum sam3_error run_elementwise(struct sam3_hip_backend *hb, const struct
 
 /* gh_multihead_attention_rope's head merge (graph_helpers.c:721-882):
  * an SDPA node whose one reader is TRANSPOSE (0,2,1,3) of its
- * [B, H, Sq, D] output, when that transpose is not written as a GEMM's
- * operand: the attention kernel stores the merged rows itself. Returns
+ * [B, H, Sq, D] output: the attention kernel stores the merged rows
+ * itself, as f32 or, when a GEMM reads them as its A (rows of H*D), in
+ * that GEMM's operand form (*fmt; f32 SDPA with head size 64). Returns
  * the transpose's node index, or -1. Storing the transpose's output at
  * node i must change nothing another node before it reads or writes. */
 static int sdpa_merge_target(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
-			     struct use_map *uses, const unsigned char *done)
+			     struct use_map *uses, const unsigned char *done, int *fmt)
 {
 	const struct s3h_settings *set = s3h_settings();
 	const struct sam3_node *n = &g->nodes[i];
@@ -1390,7 +1391,9 @@ static int sdpa_merge_target(struct sam3_hip_backend *hb, const struct sam3_grap
 	    !dims_are(t->output, o->dims[0], o->dims[2], o->dims[1], o->dims[3]))
 		return -1;
 	int k = 0;
-	if (set->permute_operand && permute_operand_form(hb, g, j, uses, &k) != S3H_A_PLAIN)
+	*fmt = set->permute_operand ? permute_operand_form(hb, g, j, uses, &k) : S3H_A_PLAIN;
+	if (*fmt != S3H_A_PLAIN &&
+	    (o->dtype != SAM3_DTYPE_F32 || n->params[0] != 64 || k != o->dims[1] * o->dims[3]))
 		return -1;
 	for (int m = i + 1; m < j; m++) {
 		const struct sam3_node *x = &g->nodes[m];
@@ -1404,7 +1407,7 @@ static int sdpa_merge_target(struct sam3_hip_backend *hb, const struct sam3_grap
 }
 
 static enum sam3_error run_sdpa_merged(struct sam3_hip_backend *hb, const struct sam3_node *n,
-				       const struct sam3_node *t)
+				       const struct sam3_node *t, int fmt)
 {
 	struct sam3_tensor tin[SAM3_NODE_MAX_INPUTS];
 	struct sam3_node dn = *n;
@@ -1418,13 +1421,39 @@ static enum sam3_error run_sdpa_merged(struct sam3_hip_backend *hb, const struct
 			return err;
 		dn.inputs[k] = &tin[k];
 	}
+	if (fmt != S3H_A_PLAIN) {
+		int BH = 0, Sq = 0, Sk = 0;
+		const struct sam3_tensor *q = dn.inputs[0];
+		if (q->n_dims == 4) {
+			BH = q->dims[0] * q->dims[1];
+			Sq = q->dims[2];
+			Sk = dn.inputs[1]->dims[2];
+		}
+		/* the operand forms are written by the MFMA kernel only: any
+		 * other case runs the two nodes as they are */
+		if (s3k_attn_path(q->dtype, q->data, dn.inputs[1]->data, dn.inputs[2]->data, q->data, BH,
+				  Sq, Sk, n->params[0]) != S3K_ATTN_MFMA) {
+			err = run_elementwise(hb, n);
+			if (err == SAM3_OK)
+				err = run_permute_as(hb, t, fmt, q->dims[1] * n->params[0]);
+			return err;
+		}
+	}
 	void *dy = NULL;
-	err = dev_out(hb, t->output, &dy);
+	if (fmt == S3H_A_PLAIN)
+		err = dev_out(hb, t->output, &dy);
+	else
+		err = dev_out_fmt(hb, t->output,
+				  (size_t)s3h_nelems(t->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
 	if (err == SAM3_OK)
-		err = s3h_sdpa_merged(&dn, dy, hb->stream);
+		err = s3h_sdpa_merged(&dn, dy, fmt, hb->ovf, hb->ovf_tag, hb->stream);
 	if (err == SAM3_OK) {
 		hb->stats.gpu_nodes++;
 		hb->stats.fused_nodes++;
+		if (fmt != S3H_A_PLAIN) {
+			hb->stats.operand_writes++;
+			hb->f16_writes += fmt == S3H_A_F16;
+		}
 	}
 	return err;
 }
@@ -1507,7 +1536,7 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 	const int qkv_plain = !set->qkv_chain;
 	const int ln_plain = !set->ln_operand;
 	const int perm_plain = !set->permute_operand;
-	int ln_fmt = S3H_A_PLAIN, perm_k = 0, merge_j = -1;
+	int ln_fmt = S3H_A_PLAIN, perm_k = 0, merge_j = -1, merge_fmt = S3H_A_PLAIN;
 	const int part_plain = !set->partition_fold;
 	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
 	const struct sam3_tensor *lt = NULL;
@@ -1548,8 +1577,8 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 			   (ln_fmt = permute_operand_form(hb, g, i, &uses, &perm_k)) != S3H_A_PLAIN) {
 			err = run_permute_as(hb, n, ln_fmt, perm_k);
 		} else if (n->op == SAM3_OP_SDPA &&
-			   (merge_j = sdpa_merge_target(hb, g, i, &uses, done)) >= 0) {
-			err = run_sdpa_merged(hb, n, &g->nodes[merge_j]);
+			   (merge_j = sdpa_merge_target(hb, g, i, &uses, done, &merge_fmt)) >= 0) {
+			err = run_sdpa_merged(hb, n, &g->nodes[merge_j], merge_fmt);
 			if (err == SAM3_OK)
 				done[merge_j] = 1;
 		} else if (runs_on_gpu(n)) {

@@ -18,8 +18,11 @@ long long s3h_nelems(const struct sam3_tensor *t);
 size_t s3h_tensor_bytes(const struct sam3_tensor *t);
 
 /* SDPA node on device tensors with its output stored head-merged
- * ([B, Sq, H, D], the TRANSPOSE (0,2,1,3) of the node's output). */
-enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, void *stream);
+ * ([B, Sq, H, D], the TRANSPOSE (0,2,1,3) of the node's output), as f32
+ * or as the operand form fmt (S3H_A_PLANES / S3H_A_F16, f32 SDPA with
+ * head size 64) of a GEMM reading rows of H*D. */
+enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, int fmt, unsigned *ovf,
+				unsigned ovf_tag, void *stream);
 
 /* Device-pointer elementwise nodes used by the dispatcher and graph_eval. */
 enum sam3_error s3h_add(const struct sam3_node *node, void *stream);

@@ -2344,8 +2344,11 @@ enum sam3_error sam3_hip_kernel_sdpa(const struct sam3_node *node, void *stream)
 
 /* The SDPA node (4-D [B, H, Sq, D]) with its output stored head-merged
  * at `out`: [B, Sq, H, D], what TRANSPOSE (0,2,1,3) of its output
- * gives. Inputs read from the node's tensors' data (device addresses). */
-enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, void *stream)
+ * gives, as f32 (S3H_A_PLAIN) or as the operand form fmt of a GEMM
+ * reading rows of H*D (f32 SDPA on the MFMA kernel). Inputs read from
+ * the node's tensors' data (device addresses). */
+enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, int fmt, unsigned *ovf,
+				unsigned ovf_tag, void *stream)
 {
 	int BH, Sq, Sk, D;
 	enum sam3_error err = sdpa_shape(node, &BH, &Sq, &Sk, &D, 0);
@@ -2363,9 +2366,14 @@ enum sam3_error s3h_sdpa_merged(const struct sam3_node *node, void *out, void *s
 		s3h_error("sdpa: no kernel for D=%d", D);
 		return SAM3_EINVAL;
 	}
+	const int ofmt = fmt == S3H_A_PLANES ? S3K_LN_PLANES : fmt == S3H_A_F16 ? S3K_LN_F16 : 0;
+	if (fmt != S3H_A_PLAIN && !ofmt) {
+		s3h_error("sdpa: unknown output form %d", fmt);
+		return SAM3_EINVAL;
+	}
 	return s3h_hip(s3k_attn_heads(0, dt, Q->data, node->inputs[1]->data, node->inputs[2]->data,
 				      M ? (const float *)M->data : NULL, out, BH, Sq, Sk, D,
-				      Q->dims[1], stream),
+				      Q->dims[1], ofmt, ovf, ovf_tag, stream),
 		       "sdpa (heads merged)");
 }
 

@@ -643,6 +643,54 @@ def test_sdpa_stores_heads_merged(env, dt, B, H, S):
 
 
 @pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_sdpa_stores_heads_merged_gemm_operand(env, wkind):
+    """gh_multihead_attention_rope's SDPA -> TRANSPOSE (0,2,1,3) ->
+    RESHAPE -> output projection (the ViT block's path): the attention
+    kernel stores the merged rows directly as the projection's operand
+    (bf16 planes for f32 weights, f16 for Q8_0 weights) instead of f32
+    rows that a permute kernel then converts: one launch fewer, the same
+    bits as that permute (SAM3_HIP_SDPA_MERGE=0), and the oracle's
+    attention + matmul within f32 tolerance."""
+    B, H, S, D, N = 4, 4, 64, 64, 512
+    E = H * D
+    O = oracle()
+    q, k, v = (synth.randn(895 + i, (B, H, S, D)) for i in range(3))
+    w = synth.randn(898, (N, E), 0.05)
+    bias = synth.randn(899, (N,), 0.02)
+
+    def run(mode):
+        if mode is None:
+            env.unset("SAM3_HIP_SDPA_MERGE")
+        else:
+            env.set("SAM3_HIP_SDPA_MERGE", mode)
+        G = graph.Graph()
+        tq, tk, tv = (G.tensor(abi.F32, x.shape, x) for x in (q, k, v))
+        a = G.reshape(G.permute(G.sdpa(tq, tk, tv), (0, 2, 1, 3)), [B * S, E])
+        tw = (G.tensor(abi.Q8_0, (N, E), O.q8_quantize(w)) if wkind == "q8"
+              else G.tensor(abi.F32, (N, E), w))
+        y = G.linear(a, tw, G.tensor(abi.F32, (N,), bias))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        return np.ctypeslib.as_array(C.cast(y.data, C.POINTER(C.c_float)), shape=(B * S, N)).copy(), st
+
+    fused, st = run(None)
+    plain, st0 = run("0")
+    assert st.host_nodes == 0 and st0.host_nodes == 0
+    assert st.gpu_nodes == st0.gpu_nodes - 1, (st.gpu_nodes, st0.gpu_nodes)
+    assert st.operand_writes == st0.operand_writes == 1
+    assert np.array_equal(fused.view(np.uint32), plain.view(np.uint32))
+    att = O.sdpa(q.reshape(B * H, S, D), k.reshape(B * H, S, D), v.reshape(B * H, S, D), None, 8)
+    a = att.reshape(B, H, S, D).transpose(0, 2, 1, 3).reshape(B * S, E).astype(np.float64)
+    wd = O.q8_dequantize(O.q8_quantize(w), w.size).reshape(w.shape) if wkind == "q8" else w
+    assert_f32_close(fused, (a @ wd.T.astype(np.float64) + bias).astype(np.float32),
+                     what=f"sdpa -> merged operand -> linear {wkind}")
+
+
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
 def test_residual_add_folded_into_gemm(env, wkind):
     """x + linear(LN(x)) as the ViT block builds its residuals
     (image_encoder.c:755-916): the ADD of the earlier f32 tensor is done in
