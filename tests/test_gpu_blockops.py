@@ -881,9 +881,9 @@ def test_blocks_chained_across_evals():
     assert np.array_equal(back.view(np.uint32), one.view(np.uint32))
 
 
-def _block_full(wkind, seed, deq_ref=False):
-    """The windowed ViT-L block at its production shape (grid 72, window
-    24, e 1024, 16 heads, MLP 4096), f32 or Q8_0 linear weights (the
+def _block_full(wkind, seed, deq_ref=False, is_global=False):
+    """The windowed (or global) ViT-L block at its production shape (grid
+    72, window 24, e 1024, 16 heads, MLP 4096), f32 or Q8_0 linear weights (the
     reference graph gets the dequantized Q8_0 weights in f32: its own Q8
     path through gh_linear's transpose is a no-op, cpu_transpose.c:
     355-366)."""
@@ -906,9 +906,9 @@ def _block_full(wkind, seed, deq_ref=False):
                 p[name] = G.tensor(abi.Q8_0, shape, blocks)
         else:
             p[name] = G.tensor(abi.F32, shape, w)
-    c, s = graph.rope_tables(window, e // heads)
+    c, s = graph.rope_tables(grid if is_global else window, e // heads)
     tc, ts = G.tensor(abi.F32, c.shape, c), G.tensor(abi.F32, s.shape, s)
-    out = graph.vit_block(G, x, p, heads, grid, window, False, tc, ts)
+    out = graph.vit_block(G, x, p, heads, grid, window, is_global, tc, ts)
     return G, out
 
 
@@ -916,15 +916,17 @@ def _block_full(wkind, seed, deq_ref=False):
 def test_vit_block_full_size_windowed(env, wkind):
     """The production windowed block (5184 tokens, the SLOTS = 4 LayerNorm
     and the g = 24 row maps): the default run is bit-identical to the run
-    with the partition and unpartition folds off, and matches the
-    reference's CPU kernels run over the same graph."""
+    with the partition, unpartition, qkv-epilogue and head-merge folds
+    off, and matches the reference's CPU kernels run over the same
+    graph."""
     from oracle_bind import Ref, have_ref
     if not have_ref():
         pytest.skip("oracle/_ref not built")
     M, e = 72 * 72, 1024
 
     def gpu_run(fold):
-        for name in ("SAM3_HIP_PARTITION_FOLD", "SAM3_HIP_UNPARTITION_FOLD"):
+        for name in ("SAM3_HIP_PARTITION_FOLD", "SAM3_HIP_UNPARTITION_FOLD",
+                     "SAM3_HIP_QKV_FOLD", "SAM3_HIP_SDPA_MERGE"):
             if fold:
                 env.unset(name)
             else:
@@ -955,3 +957,44 @@ def test_vit_block_full_size_windowed(env, wkind):
     # (2e-3 for the f32 weights)
     assert_f32_close(y, ref, floor=1.5e-2 if wkind == "q8" else 2e-3,
                      what=f"full-size windowed block {wkind}")
+
+
+@pytest.mark.parametrize("wkind", ["f32", "q8"])
+def test_vit_block_full_size_global(env, wkind):
+    """The production global block (5184 tokens in one sequence: the qkv
+    epilogue's RoPE over 5184 positions, attention over 5184 keys storing
+    the projection's operand): bit-identical to the run with the
+    qkv-epilogue, head-merge and residual folds off, and matching the
+    reference's CPU kernels run over the same graph."""
+    from oracle_bind import Ref, have_ref
+    if not have_ref():
+        pytest.skip("oracle/_ref not built")
+    M, e = 72 * 72, 1024
+
+    def gpu_run(fold):
+        for name in ("SAM3_HIP_QKV_FOLD", "SAM3_HIP_SDPA_MERGE", "SAM3_HIP_RESIDUAL_FOLD"):
+            if fold:
+                env.unset(name)
+            else:
+                env.set(name, "0")
+        G, out = _block_full(wkind, 480, is_global=True)
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+            assert st.host_nodes == 0
+            return out_array(out, (M, e)), st
+        finally:
+            be.close()
+
+    y, st = gpu_run(True)
+    y0, st0 = gpu_run(False)
+    assert st.gpu_nodes == 7 and st0.gpu_nodes > st.gpu_nodes, (st.gpu_nodes, st0.gpu_nodes)
+    assert np.array_equal(y.view(np.uint32), y0.view(np.uint32))
+    Gr, orf = _block_full(wkind, 480, deq_ref=True, is_global=True)
+    R = Ref()
+    assert reference_eval(R, Gr.g, R.pool(0)) == 0
+    ref = out_array(orf, (M, e))
+    R.close()
+    assert_f32_close(y, ref, floor=1.5e-2 if wkind == "q8" else 2e-3,
+                     what=f"full-size global block {wkind}")
