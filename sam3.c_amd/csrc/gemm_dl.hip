@@ -365,6 +365,175 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 						 tn * BN + wn0, bz);
 }
 
+/* One k-step GEMMs (K = 64: the attention scores Q K^T, batched over
+ * windows and heads). With a single k-step a workgroup loads, multiplies
+ * once and stores, and the next workgroup on the CU starts only after
+ * that: the output stores, most of the bytes, do not overlap anything.
+ * Here workgroups are persistent: each walks the tiles (all batch slices
+ * together) gridDim.x apart, and after the MFMAs of tile i it issues the
+ * direct-to-LDS loads of tile i + 1 into the other panel buffer and only
+ * then the stores of tile i, so that waiting for those loads does not
+ * wait for the stores (vmcnt counts both, in order). 192x192 tiles of
+ * four 96x96 wave tiles; M and N multiples of 192, whole tiles only, so
+ * every lane issues the same number of stores (the epilogue's fast
+ * path) and the wait counts below are exact. Same MFMA sequence per
+ * output as gemm_dl / gemm_dlp, so the same bits. */
+constexpr int DLK_B = 192, DLK_WT = 96, DLK_NW = 4;
+
+template <int FAM, int CK>
+__global__ void __launch_bounds__(64 * DLK_NW, 1) gemm_dlk(GemmArgs p, int total)
+{
+	constexpr int BM = DLK_B, BN = DLK_B, NW = DLK_NW, BK = 64, CPR = 8;
+	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2, STAGE = A_BYTES + B_BYTES;
+	constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW, LOADS = A_PER + B_PER;
+	constexpr int WTM = DLK_WT, WTN = DLK_WT, FM = WTM / 32, FN = WTN / 32;
+	constexpr int W = CK == S3K_F32 ? 4 : 8;
+	constexpr int STORES = FM * (32 * WTN / W) / 64;   /* per lane and tile */
+	static_assert((32 * WTN / W) % 64 == 0, "whole store rounds");
+	static_assert(LOADS + STORES < 64, "vmcnt range");
+	constexpr int STG = NW * 32 * (WTN + 4) * 4;      /* epilogue staging (transposed tiles) */
+	__shared__ __attribute__((aligned(1024))) char smem[2 * STAGE + STG];
+
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int wm0 = (wave / 2) * WTM, wn0 = (wave % 2) * WTN;
+	const unsigned lds0 = lds_addr_of(smem);
+	const int per_slice = p.tiles_m * p.tiles_n;
+
+	/* per-lane chunk of DMA instruction t within a panel (rows past M / N
+	 * never occur: whole tiles) */
+	unsigned rowoff_a[A_PER], rowoff_b[B_PER];
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t) {
+		const bool isa = t < A_PER;
+		const int s = ((isa ? t : t - A_PER) * NW + wave) * 64 + lane;
+		const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+		if (isa)
+			rowoff_a[t] = (unsigned)(row * p.lda_b + c * 16);
+		else
+			rowoff_b[t - A_PER] = (unsigned)(row * p.ldb_b + c * 16);
+	}
+	/* tile -> (slice, tm, tn) and its panels' loads into buffer b */
+	auto coords = [&](int t, int &bz, int &tm, int &tn) {
+		bz = t / per_slice;
+		tile_of(t - bz * per_slice, p.tiles_m, p.tiles_n, tm, tn);
+	};
+	auto load_tile = [&](int t, int b) {
+		int bz, tm, tn;
+		coords(t, bz, tm, tn);
+		const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+		const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+		const unsigned oa = (unsigned)(tm * BM * p.lda_b), ob = (unsigned)(tn * BN * p.ldb_b);
+#pragma unroll
+		for (int u = 0; u < A_PER; ++u)
+			dma16s(lds0 + (unsigned)(b * STAGE + (u * NW + wave) * 1024), ra, rowoff_a[u], oa);
+#pragma unroll
+		for (int u = 0; u < B_PER; ++u)
+			dma16s(lds0 + (unsigned)(b * STAGE + A_BYTES + (u * NW + wave) * 1024), rb,
+			       rowoff_b[u], ob);
+	};
+
+	unsigned abase[4], bbase[4];
+	{
+		const int l32 = lane & 31, h = lane >> 5, r0 = wm0 + l32, r1 = wn0 + l32;
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks) {
+			abase[ks] = lds0 + (unsigned)((r0 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r0))) << 4);
+			bbase[ks] = lds0 + A_BYTES +
+				    (unsigned)((r1 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r1))) << 4);
+		}
+	}
+
+	int t = blockIdx.x;
+	if (t >= total)
+		return;
+	load_tile(t, 0);
+	for (int i = 0; t < total; ++i, t += gridDim.x) {
+		const int b = i & 1;
+		/* this tile's panels: issued before the previous tile's stores */
+		if (i == 0)
+			wait_vm<0>();
+		else
+			wait_vm<STORES>();
+		wg_barrier();
+		s3k_f32x16 acc[FM][FN];
+#pragma unroll
+		for (int x = 0; x < FM; ++x)
+#pragma unroll
+			for (int y = 0; y < FN; ++y)
+#pragma unroll
+				for (int r = 0; r < 16; ++r)
+					acc[x][y][r] = 0.0f;
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks) {
+			uint4 af[FM], bf[FN];
+			/* block x starts 32x rows further down: an odd x flips bit 2
+			 * of the row's chunk permutation, i.e. k-substep ks ^ 2 */
+#pragma unroll
+			for (int x = 0; x < FM; ++x)
+				af[x] = lds_rd16(abase[ks ^ (2 * (x & 1))], (unsigned)(b * STAGE + x * 4096));
+#pragma unroll
+			for (int y = 0; y < FN; ++y)
+				bf[y] = lds_rd16(bbase[ks ^ (2 * (y & 1))], (unsigned)(b * STAGE + y * 4096));
+			__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+#pragma unroll
+			for (int x = 0; x < FM; ++x)
+#pragma unroll
+				for (int y = 0; y < FN; ++y)
+					mfma_chunk<FAM>(acc[x][y], bf[y], af[x]);
+		}
+		/* every wave is done with buffer b ^ 1 (read in the previous
+		 * tile) and with its own fragment reads of b */
+		wg_barrier();
+		const int tn2 = t + (int)gridDim.x;
+		if (tn2 < total)
+			load_tile(tn2, b ^ 1);
+		int bz, tm, tn;
+		coords(t, bz, tm, tn);
+		write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem + 2 * STAGE, wave, lane, tm * BM + wm0,
+						      tn * BN + wn0, bz);
+	}
+}
+
+/* gemm_dlk's conditions: K = 64, M and N multiples of 192, plain f32 or
+ * same-kind 16-bit output with 16-byte rows, no epilogue flags, enough
+ * tiles to keep every CU busy. */
+static bool dlk_ok(const struct s3k_gemm *g)
+{
+	return g->K == 64 && g->M % DLK_B == 0 && g->N % DLK_B == 0 &&
+	       (g->flags & ~S3K_B_NT) == 0 && !g->rm_g && !g->res &&
+	       (g->c_kind == S3K_F32 || g->c_kind == g->a_kind) && g->ldc % 8 == 0 &&
+	       !((uintptr_t)g->c & 15u) && (g->batch <= 1 || g->stride_c % 8 == 0) &&
+	       (long long)(g->M / DLK_B) * (g->N / DLK_B) * g->batch >= 1024 &&
+	       (long long)(g->M / DLK_B) * (g->N / DLK_B) * g->batch < (1LL << 31);
+}
+
+template <int FAM>
+static int launch_dlk(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	p.tiles_m = g->M / DLK_B;
+	p.tiles_n = g->N / DLK_B;
+	const int total = p.tiles_m * p.tiles_n * g->batch;
+	static int cu_count[64];
+	int dev = 0, cus = 256;
+	if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+		if (!cu_count[dev] &&
+		    hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev) !=
+			    hipSuccess)
+			cu_count[dev] = 0;
+		if (cu_count[dev] > 0)
+			cus = cu_count[dev];
+	}
+	const dim3 grid((unsigned)(total < cus ? total : cus));
+	if (g->c_kind == S3K_F32)
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F32>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+	else if (FAM == FAM_BF16)
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_BF16>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+	else
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F16>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+	return (int)hipGetLastError();
+}
+
 template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER, bool QKV = false>
 static void launch_dlp_k(const struct s3k_gemm *g, const GemmArgs &p, hipStream_t st)
 {
@@ -536,6 +705,10 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	 * tile */
 	if ((g->flags & S3K_EPI_QKV) && (cfg < 20 || cfg == 25))
 		cfg = 26;
+	if ((s3h_settings()->dl_cfg < 0 || cfg == 30) && dlk_ok(g))
+		return g->a_kind == S3K_BF16 ? launch_dlk<FAM_BF16>(g, p, st) : launch_dlk<FAM_F16>(g, p, st);
+	if (cfg == 30)
+		cfg = 2;
 	switch (cfg) {
 	case 0:  return launch_dl_cfg<256, 128, 32, 2, 2, 3, 2>(g, p, st);
 	case 1:  return launch_dl_cfg<128, 128, 32, 2, 2, 3, 2>(g, p, st);

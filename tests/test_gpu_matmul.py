@@ -606,6 +606,37 @@ def test_batched_attention_matmuls(B, S, D):
     assert_bf16_close(o, O.matmul_bf16_batched(p, v, b_nt=False, threads=8), what="PV")
 
 
+@pytest.mark.parametrize("dt", [abi.BF16, abi.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("B,S", [(1296, 576), (16, 5184), (300, 384)])
+def test_batched_scores_persistent_kernel(env, dt, B, S):
+    """Q K^T with K = 64 over many slices (the ViT's windowed and global
+    attention scores) runs the persistent one-k-step kernel: the same bits
+    as the per-tile kernel (SAM3_HIP_DL_CFG=24), and a sample of slices
+    against the oracle."""
+    O = oracle()
+    D = 64
+    q = rnd(175, (B, S, D)) / 8
+    k = rnd(176, (B, S, D)) / 8
+    if dt == abi.BF16:
+        q, k = (O.f32_to_bf16(x).reshape(x.shape) for x in (q, k))
+    else:
+        q, k = q.astype(np.float16), k.astype(np.float16)
+    env.unset("SAM3_HIP_DL_CFG")
+    got = hip.batched(dt, q, k, B, S, S, D, b_nt=True)
+    env.set("SAM3_HIP_DL_CFG", 24)
+    ref_tile = hip.batched(dt, q, k, B, S, S, D, b_nt=True)
+    env.unset("SAM3_HIP_DL_CFG")
+    assert np.array_equal(got.view(np.uint16), ref_tile.view(np.uint16))
+    pick = np.unique(np.array([0, B // 2, B - 1]))
+    if dt == abi.BF16:
+        ref = O.matmul_bf16_batched(q[pick], k[pick], b_nt=True, threads=8)
+        assert_bf16_close(got[pick], ref, what=f"QK^T {B}x{S}")
+    else:
+        qf, kf = q[pick].astype(np.float64), k[pick].astype(np.float64)
+        ref = np.einsum("bsd,btd->bst", qf, kf).astype(np.float16)
+        assert_f16_close(got[pick].view(np.uint16), ref.view(np.uint16), what=f"QK^T f16 {B}x{S}")
+
+
 # -------------------------------------------- full-size shapes, row sample
 def _row_sample(M, n=48, seed=7):
     rng = np.random.default_rng(seed)
