@@ -378,15 +378,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
  * every lane issues the same number of stores (the epilogue's fast
  * path) and the wait counts below are exact. Same MFMA sequence per
  * output as gemm_dl / gemm_dlp, so the same bits. */
-constexpr int DLK_B = 192, DLK_WT = 96, DLK_NW = 4;
+constexpr int DLK_B = 192;
 
-template <int FAM, int CK>
-__global__ void __launch_bounds__(64 * DLK_NW, 1) gemm_dlk(GemmArgs p, int total)
+template <int FAM, int CK, int WGN>
+__global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
 {
-	constexpr int BM = DLK_B, BN = DLK_B, NW = DLK_NW, BK = 64, CPR = 8;
+	constexpr int BM = DLK_B, BN = DLK_B, NW = 2 * WGN, BK = 64, CPR = 8;
 	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2, STAGE = A_BYTES + B_BYTES;
 	constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW, LOADS = A_PER + B_PER;
-	constexpr int WTM = DLK_WT, WTN = DLK_WT, FM = WTM / 32, FN = WTN / 32;
+	constexpr int WTM = BM / 2, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
 	constexpr int W = CK == S3K_F32 ? 4 : 8;
 	constexpr int STORES = FM * (32 * WTN / W) / 64;   /* per lane and tile */
 	static_assert((32 * WTN / W) % 64 == 0, "whole store rounds");
@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(64 * DLK_NW, 1) gemm_dlk(GemmArgs p, int total
 
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-	const int wm0 = (wave / 2) * WTM, wn0 = (wave % 2) * WTN;
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
 	const unsigned lds0 = lds_addr_of(smem);
 	const int per_slice = p.tiles_m * p.tiles_n;
 
@@ -508,7 +508,7 @@ static bool dlk_ok(const struct s3k_gemm *g)
 	       (long long)(g->M / DLK_B) * (g->N / DLK_B) * g->batch < (1LL << 31);
 }
 
-template <int FAM>
+template <int FAM, int WGN>
 static int launch_dlk(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
 	p.tiles_m = g->M / DLK_B;
@@ -525,12 +525,13 @@ static int launch_dlk(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 			cus = cu_count[dev];
 	}
 	const dim3 grid((unsigned)(total < cus ? total : cus));
+	const dim3 block(128 * WGN);
 	if (g->c_kind == S3K_F32)
-		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F32>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F32, WGN>), grid, block, 0, st, p, total);
 	else if (FAM == FAM_BF16)
-		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_BF16>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_BF16, WGN>), grid, block, 0, st, p, total);
 	else
-		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F16>), grid, dim3(64 * DLK_NW), 0, st, p, total);
+		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F16, WGN>), grid, block, 0, st, p, total);
 	return (int)hipGetLastError();
 }
 
@@ -671,6 +672,10 @@ extern "C" int s3k_dl_eligible(const struct s3k_gemm *g)
  *     (fc2, proj, batched attention);
  *   - 128x128 (cfg 4, 4 waves) for mid-size problems, 64x64 (cfg 2) for
  *     small ones.
+ *   - K = 64 with M, N multiples of 192 and at least 1024 such tiles
+ *     (attention scores over many slices): the persistent gemm_dlk,
+ *     six waves (cfg 30; cfg 31 the four-wave form, as fast within the
+ *     run-to-run spread).
  * SAM3_HIP_DL_CFG forces a configuration (tuning and tests). */
 static long long dl_tiles(const struct s3k_gemm *g, int bm, int bn)
 {
@@ -706,8 +711,12 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	if ((g->flags & S3K_EPI_QKV) && (cfg < 20 || cfg == 25))
 		cfg = 26;
 	if ((s3h_settings()->dl_cfg < 0 || cfg == 30) && dlk_ok(g))
-		return g->a_kind == S3K_BF16 ? launch_dlk<FAM_BF16>(g, p, st) : launch_dlk<FAM_F16>(g, p, st);
-	if (cfg == 30)
+		return g->a_kind == S3K_BF16 ? launch_dlk<FAM_BF16, 3>(g, p, st)
+					     : launch_dlk<FAM_F16, 3>(g, p, st);
+	if (cfg == 31 && dlk_ok(g))
+		return g->a_kind == S3K_BF16 ? launch_dlk<FAM_BF16, 2>(g, p, st)
+					     : launch_dlk<FAM_F16, 2>(g, p, st);
+	if (cfg == 30 || cfg == 31)
 		cfg = 2;
 	switch (cfg) {
 	case 0:  return launch_dl_cfg<256, 128, 32, 2, 2, 3, 2>(g, p, st);
