@@ -651,6 +651,9 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, s3k_f32x16 (&acc)[
 /* Direct-to-LDS bf16/f16 NT GEMM (gemm_dl.hip). */
 bool s3k_dl_ok(const struct s3k_gemm *g);
 int s3k_dl_launch(const struct s3k_gemm *g, s3k::GemmArgs p, hipStream_t st);
+/* Direct-to-LDS GEMM with B stored [K, N], N <= 128 (gemm_dl.hip). */
+bool s3k_dlt_ok(const struct s3k_gemm *g);
+int s3k_dlt_launch(const struct s3k_gemm *g, s3k::GemmArgs p, hipStream_t st);
 
 /* Direct-to-LDS f16 x Q8_0 NT GEMM, f32 out (gemm_dlq8.hip). */
 bool s3k_dlq8_ok(const struct s3k_gemm *g);

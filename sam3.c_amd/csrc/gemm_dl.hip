@@ -495,6 +495,138 @@ __global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
 	}
 }
 
+/* B stored [K, N] (n contiguous: the attention's P V, whose V is
+ * [keys, head dim]) with a narrow N: both panels arrive in LDS by
+ * direct-to-LDS loads as they lie in memory, and the B fragments (eight
+ * consecutive k of one n per lane, as the MFMA's first operand) are read
+ * with ds_read_b64_tr_b16, which hands lane i of each 16-lane group
+ * element i % 4 of the 8 bytes addressed by lanes i / 4 + 4q, q = 0..3:
+ * with lane j of the group addressing row k0 + j / 4, columns
+ * n0 + 4 (j % 4).., lane i receives rows k0..k0 + 3 of column n0 + i.
+ * Two such reads give the lane's eight k. 192x64 tiles of four 96x32
+ * wave tiles, k-steps of 64 double-buffered; M a multiple of 192, N of
+ * 64, K of 64. Same MFMA sequence per output as the other kernels. */
+typedef short dlt_v4i16 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 dlt_read_tr(unsigned addr)
+{
+	const dlt_v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+		(__attribute__((address_space(3))) dlt_v4i16 *)(size_t)addr);
+	return __builtin_bit_cast(uint2, r);
+}
+
+template <int FAM, int CK>
+__global__ void __launch_bounds__(256, 2) gemm_dlt(GemmArgs p)
+{
+	constexpr int BM = 192, BN = 64, BK = 64, NW = 4, CPR = 8;
+	constexpr int WTM = 96, WTN = 32, FM = WTM / 32, FN = WTN / 32;
+	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2, STAGE = A_BYTES + B_BYTES;
+	constexpr int A_PER = BM * CPR / 64 / NW, B_PER = BK * (BN * 2 / 16) / 64 / NW;
+	constexpr int LOADS = A_PER + B_PER, LDS_BYTES = 2 * STAGE;
+	static_assert(NW * 32 * (WTN + 8) * 4 <= LDS_BYTES, "epilogue staging fits");
+	__shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
+
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int wm0 = (wave / 2) * WTM, wn0 = (wave % 2) * WTN;
+	const int bz = blockIdx.y;
+	const unsigned lds0 = lds_addr_of(smem);
+	int tm, tn;
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+
+	/* A: rows of 8 swizzled 16-byte chunks; B: k rows of BN n, 8 chunks,
+	 * in memory order */
+	unsigned off[LOADS];
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t) {
+		if (t < A_PER) {
+			const int s = (t * NW + wave) * 64 + lane;
+			const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+			off[t] = (unsigned)((tm * BM + row) * p.lda_b + c * 16);
+		} else {
+			const int s = ((t - A_PER) * NW + wave) * 64 + lane;
+			const int kr = s / 8, c = s % 8;
+			off[t] = (unsigned)(kr * p.ldb_b + tn * BN * 2 + c * 16);
+		}
+	}
+	auto dma = [&](int kt, int stg) {
+#pragma unroll
+		for (int t = 0; t < LOADS; ++t) {
+			if (t < A_PER)
+				dma16s(lds0 + (unsigned)(stg * STAGE + (t * NW + wave) * 1024), ra, off[t],
+				       (unsigned)(kt * BK * 2));
+			else
+				dma16s(lds0 + (unsigned)(stg * STAGE + A_BYTES + ((t - A_PER) * NW + wave) * 1024),
+				       rb, off[t], (unsigned)(kt * BK * p.ldb_b));
+		}
+	};
+
+	unsigned abase[4];
+	{
+		const int l32 = lane & 31, h = lane >> 5, r0 = wm0 + l32;
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks)
+			abase[ks] = lds0 + (unsigned)((r0 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r0))) << 4);
+	}
+	/* B fragment read r (k 4r..4r+3 of the lane's eight) of k-substep ks:
+	 * lane j of its group addresses row 16ks + 8(l >> 5) + 4r + j / 4,
+	 * columns wn0 + 16((l >> 4) & 1) + 4(j % 4).. */
+	const int j16 = lane & 15;
+	const unsigned btr = lds0 + A_BYTES +
+			     (unsigned)((8 * (lane >> 5) + (j16 >> 2)) * (BN * 2) +
+					(wn0 + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3)) * 2);
+
+	s3k_f32x16 acc[FM][FN];
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+
+	const int nk = p.K / BK;
+	dma(0, 0);
+	if (nk > 1)
+		dma(1, 1);
+	for (int kt = 0; kt < nk; ++kt) {
+		const int stg = kt & 1;
+		/* this stage's loads; the next stage's may stay in flight */
+		if (kt + 1 < nk)
+			wait_vm<LOADS>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks) {
+			uint4 af[FM], bf[FN];
+#pragma unroll
+			for (int i = 0; i < FM; ++i)
+				af[i] = lds_rd16(abase[ks ^ (2 * (i & 1))], (unsigned)(stg * STAGE + i * 4096));
+#pragma unroll
+			for (int j = 0; j < FN; ++j) {
+				const unsigned a0 = btr + (unsigned)(stg * STAGE + ks * 16 * (BN * 2) + j * 64);
+				const uint2 lo = dlt_read_tr(a0), hi = dlt_read_tr(a0 + 4 * (BN * 2));
+				bf[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+			}
+			__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+#pragma unroll
+			for (int i = 0; i < FM; ++i)
+#pragma unroll
+				for (int j = 0; j < FN; ++j)
+					mfma_chunk<FAM>(acc[i][j], bf[j], af[i]);
+		}
+		/* every wave is done with this stage before it is refilled */
+		wg_barrier();
+		if (kt + 2 < nk)
+			dma(kt + 2, stg);
+	}
+	__syncthreads();
+	write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
+}
+
 /* gemm_dlk's conditions: K = 64, M and N multiples of 192, plain f32 or
  * same-kind 16-bit output with 16-byte rows, no epilogue flags, enough
  * tiles to keep every CU busy. */
@@ -634,6 +766,54 @@ using namespace s3k;
 
 /* bf16 x bf16 or f16 x f16, B as [N,K], 16-byte aligned rows, each batch
  * slice within a 2 GiB buffer range. */
+/* gemm_dlt's conditions: B [K, N] 16-bit like A, M a multiple of 192,
+ * N of 64 and at most 128, K of 64, 16-byte rows, enough tiles. */
+bool s3k_dlt_ok(const struct s3k_gemm *g)
+{
+	if ((g->flags & S3K_B_NT) || g->a_kind != g->b_kind ||
+	    (g->a_kind != S3K_BF16 && g->a_kind != S3K_F16) || g->rm_g)
+		return false;
+	if (g->M <= 0 || g->M % 192 || g->N % 64 || g->N > 128 || g->K <= 0 || g->K % 64 ||
+	    g->batch <= 0)
+		return false;
+	if (((uintptr_t)g->a | (uintptr_t)g->b) & 15u || (g->lda * 2LL) % 16 || (g->ldb * 2LL) % 16)
+		return false;
+	if (g->batch > 1 && ((g->stride_a * 2) % 16 || (g->stride_b * 2) % 16))
+		return false;
+	if ((long long)g->M * g->lda * 2 > 0x7FFFFFF0LL || (long long)g->K * g->ldb * 2 > 0x7FFFFFF0LL)
+		return false;
+	return (long long)(g->M / 192) * (g->N / 64) * g->batch >= 256;
+}
+
+int s3k_dlt_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	if (!s3k_dlt_ok(g))
+		return (int)hipErrorInvalidValue;
+	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
+	p.b_extent = (unsigned)((long long)g->K * g->ldb * 2);
+	p.tiles_m = g->M / 192;
+	p.tiles_n = g->N / 64;
+	const dim3 grid(p.tiles_m * p.tiles_n, g->batch), block(256);
+#define S3K_DLT(FAM_, CK_) hipLaunchKernelGGL((gemm_dlt<FAM_, CK_>), grid, block, 0, st, p)
+	if (g->a_kind == S3K_BF16) {
+		if (g->c_kind == S3K_F32)
+			S3K_DLT(FAM_BF16, S3K_F32);
+		else if (g->c_kind == S3K_BF16)
+			S3K_DLT(FAM_BF16, S3K_BF16);
+		else
+			return (int)hipErrorInvalidValue;
+	} else {
+		if (g->c_kind == S3K_F32)
+			S3K_DLT(FAM_F16, S3K_F32);
+		else if (g->c_kind == S3K_F16)
+			S3K_DLT(FAM_F16, S3K_F16);
+		else
+			return (int)hipErrorInvalidValue;
+	}
+#undef S3K_DLT
+	return (int)hipGetLastError();
+}
+
 bool s3k_dl_ok(const struct s3k_gemm *g)
 {
 	if (!(g->flags & S3K_B_NT) || g->a_kind != g->b_kind ||
@@ -669,7 +849,8 @@ extern "C" int s3k_dl_eligible(const struct s3k_gemm *g)
  *   - 192x256 (cfg 23, 8 waves) from 384 such tiles (fc1: 45.5 against
  *     49.7 us for 192x128);
  *   - 192x128 (cfg 24 / 10, 8 waves) when that gives at least 192 tiles
- *     (fc2, proj, batched attention);
+ *     (fc2, proj, batched attention), and first of all for N <= 128 (P V
+ *     as an NT product: 200 against 303 us for 192x256);
  *   - 128x128 (cfg 4, 4 waves) for mid-size problems, 64x64 (cfg 2) for
  *     small ones.
  *   - K = 64 with M, N multiples of 192 and at least 1024 such tiles
@@ -692,7 +873,9 @@ int s3k_dl_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	if (cfg < 0) {
 		const long long t9 = dl_tiles(g, 256, 256), t10 = dl_tiles(g, 192, 128);
 		const bool pipe = g->K % 64 == 0;
-		if (t9 >= 224 && t9 <= 256)
+		if (pipe && g->N <= 128 && t10 >= 192)
+			cfg = 24; /* narrow N: wider tiles would only compute padding */
+		else if (t9 >= 224 && t9 <= 256)
 			cfg = pipe ? 20 : 9;
 		else if (pipe && t9 >= 160 && t9 <= 256 && dl_tiles(g, 192, 256) > 256)
 			cfg = 20;

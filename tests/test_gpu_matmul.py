@@ -637,6 +637,36 @@ def test_batched_scores_persistent_kernel(env, dt, B, S):
         assert_f16_close(got[pick].view(np.uint16), ref.view(np.uint16), what=f"QK^T f16 {B}x{S}")
 
 
+@pytest.mark.parametrize("dt", [abi.BF16, abi.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("B,S,D", [(120, 576, 64), (16, 5184, 64), (90, 384, 128)])
+def test_batched_pv_transposing_reads(env, dt, B, S, D):
+    """P V with V stored [keys, head dim] (B as [K, N], N <= 128) over many
+    slices runs the direct-to-LDS kernel that reads V's fragments with
+    transposing LDS reads: the same bits as the register-staged [K, N]
+    kernel (taken when SAM3_HIP_DL_CFG is set), and a sample of slices
+    against the oracle."""
+    O = oracle()
+    pm = rnd(185, (B, S, S)) / 8
+    v = rnd(186, (B, S, D)) / 8
+    if dt == abi.BF16:
+        pm, v = (O.f32_to_bf16(x).reshape(x.shape) for x in (pm, v))
+    else:
+        pm, v = pm.astype(np.float16), v.astype(np.float16)
+    env.unset("SAM3_HIP_DL_CFG")
+    got = hip.batched(dt, pm, v, B, S, D, S, b_nt=False)
+    env.set("SAM3_HIP_DL_CFG", 2)
+    staged = hip.batched(dt, pm, v, B, S, D, S, b_nt=False)
+    env.unset("SAM3_HIP_DL_CFG")
+    assert np.array_equal(got.view(np.uint16), staged.view(np.uint16))
+    pick = np.unique(np.array([0, B // 2, B - 1]))
+    if dt == abi.BF16:
+        ref = O.matmul_bf16_batched(pm[pick], v[pick], b_nt=False, threads=8)
+        assert_bf16_close(got[pick], ref, what=f"PV {B}x{S}x{D}")
+    else:
+        ref = np.matmul(pm[pick].astype(np.float64), v[pick].astype(np.float64)).astype(np.float16)
+        assert_f16_close(got[pick].view(np.uint16), ref.view(np.uint16), what=f"PV f16 {B}x{S}x{D}")
+
+
 # -------------------------------------------- full-size shapes, row sample
 def _row_sample(M, n=48, seed=7):
     rng = np.random.default_rng(seed)
