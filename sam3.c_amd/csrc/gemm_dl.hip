@@ -503,9 +503,11 @@ __global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
  * element i % 4 of the 8 bytes addressed by lanes i / 4 + 4q, q = 0..3:
  * with lane j of the group addressing row k0 + j / 4, columns
  * n0 + 4 (j % 4).., lane i receives rows k0..k0 + 3 of column n0 + i.
- * Two such reads give the lane's eight k. 192x64 tiles of four 96x32
- * wave tiles, k-steps of 64 double-buffered; M a multiple of 192, N of
- * 64, K of 64. Same MFMA sequence per output as the other kernels. */
+ * Two such reads give the lane's eight k. BMxBN tiles of WGM x WGN wave
+ * tiles, k-steps of 64 double-buffered (192x64 for N <= 128, 192x256
+ * for wide N); K a multiple of 64; rows past M read zeros and columns
+ * past N are never stored. Same MFMA sequence per output as the other
+ * kernels. */
 typedef short dlt_v4i16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint2 dlt_read_tr(unsigned addr)
@@ -515,20 +517,21 @@ __device__ __forceinline__ uint2 dlt_read_tr(unsigned addr)
 	return __builtin_bit_cast(uint2, r);
 }
 
-template <int FAM, int CK>
-__global__ void __launch_bounds__(256, 2) gemm_dlt(GemmArgs p)
+template <int BM, int BN, int WGM, int WGN, int OCC, int FAM, int CK>
+__global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 {
-	constexpr int BM = 192, BN = 64, BK = 64, NW = 4, CPR = 8;
-	constexpr int WTM = 96, WTN = 32, FM = WTM / 32, FN = WTN / 32;
+	constexpr int BK = 64, NW = WGM * WGN, CPR = 8, BCH = BN / 8; /* B: 16-byte chunks per k row */
+	constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 32, FN = WTN / 32;
 	constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2, STAGE = A_BYTES + B_BYTES;
-	constexpr int A_PER = BM * CPR / 64 / NW, B_PER = BK * (BN * 2 / 16) / 64 / NW;
+	constexpr int A_PER = BM * CPR / 64 / NW, B_PER = BK * BCH / 64 / NW;
+	static_assert(BM * CPR % (64 * NW) == 0 && BK * BCH % (64 * NW) == 0, "loads split evenly");
 	constexpr int LOADS = A_PER + B_PER, LDS_BYTES = 2 * STAGE;
 	static_assert(NW * 32 * (WTN + 8) * 4 <= LDS_BYTES, "epilogue staging fits");
 	__shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
 
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-	const int wm0 = (wave / 2) * WTM, wn0 = (wave % 2) * WTN;
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
 	const int bz = blockIdx.y;
 	const unsigned lds0 = lds_addr_of(smem);
 	int tm, tn;
@@ -536,18 +539,19 @@ __global__ void __launch_bounds__(256, 2) gemm_dlt(GemmArgs p)
 	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
 	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
 
-	/* A: rows of 8 swizzled 16-byte chunks; B: k rows of BN n, 8 chunks,
-	 * in memory order */
+	/* A: rows of 8 swizzled 16-byte chunks (rows past M read zeros); B:
+	 * k rows of BN n in BCH chunks, in memory order */
 	unsigned off[LOADS];
 #pragma unroll
 	for (int t = 0; t < LOADS; ++t) {
 		if (t < A_PER) {
 			const int s = (t * NW + wave) * 64 + lane;
 			const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
-			off[t] = (unsigned)((tm * BM + row) * p.lda_b + c * 16);
+			off[t] = tm * BM + row < p.M ? (unsigned)((tm * BM + row) * p.lda_b + c * 16)
+						    : S3K_OOB;
 		} else {
 			const int s = ((t - A_PER) * NW + wave) * 64 + lane;
-			const int kr = s / 8, c = s % 8;
+			const int kr = s / BCH, c = s % BCH;
 			off[t] = (unsigned)(kr * p.ldb_b + tn * BN * 2 + c * 16);
 		}
 	}
@@ -766,14 +770,19 @@ using namespace s3k;
 
 /* bf16 x bf16 or f16 x f16, B as [N,K], 16-byte aligned rows, each batch
  * slice within a 2 GiB buffer range. */
-/* gemm_dlt's conditions: B [K, N] 16-bit like A, M a multiple of 192,
- * N of 64 and at most 128, K of 64, 16-byte rows, enough tiles. */
+/* gemm_dlt's conditions: B [K, N] 16-bit like A, K a multiple of 64, N
+ * of 64 (at most 128) or of 256, 16-byte rows, enough tiles. */
+static bool dlt_narrow(const struct s3k_gemm *g)
+{
+	return g->N % 64 == 0 && g->N <= 128;
+}
+
 bool s3k_dlt_ok(const struct s3k_gemm *g)
 {
 	if ((g->flags & S3K_B_NT) || g->a_kind != g->b_kind ||
 	    (g->a_kind != S3K_BF16 && g->a_kind != S3K_F16) || g->rm_g)
 		return false;
-	if (g->M <= 0 || g->M % 192 || g->N % 64 || g->N > 128 || g->K <= 0 || g->K % 64 ||
+	if (g->M <= 0 || (!dlt_narrow(g) && g->N % 256) || g->N <= 0 || g->K <= 0 || g->K % 64 ||
 	    g->batch <= 0)
 		return false;
 	if (((uintptr_t)g->a | (uintptr_t)g->b) & 15u || (g->lda * 2LL) % 16 || (g->ldb * 2LL) % 16)
@@ -782,7 +791,7 @@ bool s3k_dlt_ok(const struct s3k_gemm *g)
 		return false;
 	if ((long long)g->M * g->lda * 2 > 0x7FFFFFF0LL || (long long)g->K * g->ldb * 2 > 0x7FFFFFF0LL)
 		return false;
-	return (long long)(g->M / 192) * (g->N / 64) * g->batch >= 256;
+	return (long long)((g->M + 191) / 192) * (g->N / (dlt_narrow(g) ? 64 : 256)) * g->batch >= 256;
 }
 
 int s3k_dlt_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
@@ -791,25 +800,31 @@ int s3k_dlt_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		return (int)hipErrorInvalidValue;
 	p.a_extent = (unsigned)((long long)g->M * g->lda * 2);
 	p.b_extent = (unsigned)((long long)g->K * g->ldb * 2);
-	p.tiles_m = g->M / 192;
-	p.tiles_n = g->N / 64;
-	const dim3 grid(p.tiles_m * p.tiles_n, g->batch), block(256);
-#define S3K_DLT(FAM_, CK_) hipLaunchKernelGGL((gemm_dlt<FAM_, CK_>), grid, block, 0, st, p)
-	if (g->a_kind == S3K_BF16) {
-		if (g->c_kind == S3K_F32)
-			S3K_DLT(FAM_BF16, S3K_F32);
-		else if (g->c_kind == S3K_BF16)
-			S3K_DLT(FAM_BF16, S3K_BF16);
-		else
-			return (int)hipErrorInvalidValue;
-	} else {
-		if (g->c_kind == S3K_F32)
-			S3K_DLT(FAM_F16, S3K_F32);
-		else if (g->c_kind == S3K_F16)
-			S3K_DLT(FAM_F16, S3K_F16);
-		else
-			return (int)hipErrorInvalidValue;
-	}
+	const bool narrow = dlt_narrow(g);
+	p.tiles_m = (g->M + 191) / 192;
+	p.tiles_n = g->N / (narrow ? 64 : 256);
+	const dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	if (!(g->c_kind == S3K_F32 || g->c_kind == g->a_kind))
+		return (int)hipErrorInvalidValue;
+#define S3K_DLT(BN_, WGN_, OCC_, FAM_, CK_)                                                  \
+	hipLaunchKernelGGL((gemm_dlt<192, BN_, 2, WGN_, OCC_, FAM_, CK_>), grid, dim3(128 * WGN_), \
+			   0, st, p)
+#define S3K_DLT_K(FAM_, CKS_)                                      \
+	do {                                                       \
+		if (narrow && g->c_kind == S3K_F32)                \
+			S3K_DLT(64, 2, 2, FAM_, S3K_F32);          \
+		else if (narrow)                                   \
+			S3K_DLT(64, 2, 2, FAM_, CKS_);             \
+		else if (g->c_kind == S3K_F32)                     \
+			S3K_DLT(256, 4, 1, FAM_, S3K_F32);         \
+		else                                               \
+			S3K_DLT(256, 4, 1, FAM_, CKS_);            \
+	} while (0)
+	if (g->a_kind == S3K_BF16)
+		S3K_DLT_K(FAM_BF16, S3K_BF16);
+	else
+		S3K_DLT_K(FAM_F16, S3K_F16);
+#undef S3K_DLT_K
 #undef S3K_DLT
 	return (int)hipGetLastError();
 }

@@ -667,6 +667,45 @@ def test_batched_pv_transposing_reads(env, dt, B, S, D):
         assert_f16_close(got[pick].view(np.uint16), ref.view(np.uint16), what=f"PV f16 {B}x{S}x{D}")
 
 
+@pytest.mark.parametrize("dt,ct,M,N,K", [
+    (abi.BF16, abi.BF16, 5184, 4096, 1024),
+    (abi.BF16, abi.F32, 5000, 2560, 320),
+    (abi.F16, abi.F16, 5000, 2560, 320),
+    (abi.F16, abi.F32, 1000, 16384, 128),
+], ids=["fc1-bf16", "ragged-bf16-f32", "ragged-f16", "wide-f16-f32"])
+def test_wide_kn_weight_transposing_reads(env, dt, ct, M, N, K):
+    """A 16-bit product with W stored [K, N] and N a multiple of 256 runs
+    the 192x256 direct-to-LDS tile that reads W's fragments with
+    transposing LDS reads (rows past M, when M is not a multiple of 192,
+    read zeros and are not stored): the same bits as the register-staged
+    [K, N] kernel (taken when SAM3_HIP_DL_CFG is set), and a row sample
+    against the oracle."""
+    O = oracle()
+    a = rnd(187, (M, K))
+    w = rnd(188, (K, N), 0.05)
+    if dt == abi.BF16:
+        a, w = (O.f32_to_bf16(x).reshape(x.shape) for x in (a, w))
+        dec = bf16_to_f32
+    else:
+        a, w = a.astype(np.float16), w.astype(np.float16)
+        dec = lambda x: x.astype(np.float32)
+    env.unset("SAM3_HIP_DL_CFG")
+    got = hip.matmul(a, dt, w, dt, ct, M, N, K, path=MFMA)
+    env.set("SAM3_HIP_DL_CFG", 2)
+    staged = hip.matmul(a, dt, w, dt, ct, M, N, K, path=MFMA)
+    env.unset("SAM3_HIP_DL_CFG")
+    assert np.array_equal(got.view(np.uint8), staged.view(np.uint8))
+    rows = _row_sample(M, n=24)
+    if ct == abi.F32:
+        ref = O.matmul_f32(dec(a[rows]), dec(w), 8)
+        assert_f32_close(got[rows], ref, what=f"[K,N] {M}x{N}x{K} f32 out")
+    elif dt == abi.BF16:
+        assert_bf16_close(got[rows], ref_linear("bf16", a[rows], w), what=f"[K,N] {M}x{N}x{K}")
+    else:
+        assert_f16_close(got[rows].view(np.uint16), ref_linear("f16", a[rows].view(np.uint16), w.view(np.uint16)),
+                         what=f"[K,N] f16 {M}x{N}x{K}")
+
+
 # -------------------------------------------- full-size shapes, row sample
 def _row_sample(M, n=48, seed=7):
     rng = np.random.default_rng(seed)
