@@ -510,6 +510,16 @@ __global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
  * kernels. */
 typedef short dlt_v4i16 __attribute__((ext_vector_type(4)));
 
+/* B's 16-byte chunks sit XOR-swizzled by k row so that the eight rows
+ * one transposing read touches (row bits 0, 1 and 3) fall in different
+ * banks; bits 2, 4 and 5 leave the swizzle unchanged, so the read's k
+ * offsets stay immediates. */
+template <int BCH>
+__device__ __forceinline__ int dlt_bswz(int row)
+{
+	return BCH >= 32 ? 4 * ((row & 3) | ((row >> 1) & 4)) : 4 * ((row >> 1) & 1);
+}
+
 __device__ __forceinline__ uint2 dlt_read_tr(unsigned addr)
 {
 	const dlt_v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -551,7 +561,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 						    : S3K_OOB;
 		} else {
 			const int s = ((t - A_PER) * NW + wave) * 64 + lane;
-			const int kr = s / BCH, c = s % BCH;
+			const int kr = s / BCH, c = (s % BCH) ^ dlt_bswz<BCH>(kr);
 			off[t] = (unsigned)(kr * p.ldb_b + tn * BN * 2 + c * 16);
 		}
 	}
@@ -576,11 +586,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 	}
 	/* B fragment read r (k 4r..4r+3 of the lane's eight) of k-substep ks:
 	 * lane j of its group addresses row 16ks + 8(l >> 5) + 4r + j / 4,
-	 * columns wn0 + 16((l >> 4) & 1) + 4(j % 4).. */
+	 * columns wn0 + 32 (fragment) + 16((l >> 4) & 1) + 4(j % 4).., at
+	 * their chunk's swizzled place */
 	const int j16 = lane & 15;
-	const unsigned btr = lds0 + A_BYTES +
-			     (unsigned)((8 * (lane >> 5) + (j16 >> 2)) * (BN * 2) +
-					(wn0 + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3)) * 2);
+	const int brow = 8 * (lane >> 5) + (j16 >> 2), bsw = dlt_bswz<BCH>(brow);
+	unsigned btr[FN];
+#pragma unroll
+	for (int j = 0; j < FN; ++j) {
+		const int n = wn0 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+		btr[j] = lds0 + A_BYTES + (unsigned)(brow * (BN * 2) + (((n >> 3) ^ bsw) << 4) + (n & 7) * 2);
+	}
 
 	s3k_f32x16 acc[FM][FN];
 #pragma unroll
@@ -611,7 +626,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 				af[i] = lds_rd16(abase[ks ^ (2 * (i & 1))], (unsigned)(stg * STAGE + i * 4096));
 #pragma unroll
 			for (int j = 0; j < FN; ++j) {
-				const unsigned a0 = btr + (unsigned)(stg * STAGE + ks * 16 * (BN * 2) + j * 64);
+				const unsigned a0 = btr[j] + (unsigned)(stg * STAGE + ks * 16 * (BN * 2));
 				const uint2 lo = dlt_read_tr(a0), hi = dlt_read_tr(a0 + 4 * (BN * 2));
 				bf[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
 			}
