@@ -707,7 +707,8 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 		return (int)hipErrorInvalidValue;
 	if (s3k_dl_ok(g))
 		return s3k_dl_launch(g, p, st);
-	/* B stored [K, N] with a narrow N (the attention's P V) */
+	/* B stored [K, N]: the attention's P V (narrow N) and weights kept
+	 * [K, N] (N a multiple of 256) */
 	if (s3k_dlt_ok(g) && !(g->flags & S3K_EPI_QKV) && s3h_settings()->dl_cfg < 0 &&
 	    (g->c_kind == S3K_F32 || g->c_kind == g->a_kind))
 		return s3k_dlt_launch(g, p, st);
