@@ -4,8 +4,10 @@
  *   - Q8_0 -> f16 unpacking for Q8 layouts the tiled GEMM does not read
  *     directly: B[K,N] with blocks over the flat index k*N+n (the
  *     reference kernel contract, cpu_matmul_q8.c:29-35) and W[N,K] with
- *     K % 32 != 0 (blocks straddle rows). Output is f16 [N,K], value
- *     q*scale rounded once to f16 (src/core/quant.c:134-165 gives q*scale).
+ *     K % 32 != 0 (blocks straddle rows), and the expansion of W[N,K]
+ *     for the f16 GEMM. Output is f16 [N,K], value q*scale times the
+ *     weight row's power-of-two factor, rounded once to f16
+ *     (src/core/quant.c:134-165 gives q*scale), and the factors.
  *   - Q8_0 quantize / dequantize of flat f32 arrays on the device
  *     (src/core/quant.c:67-165), bit-exact with the reference's x86 build;
  *   - bias add over the last dim, same-shape add, tanh-GELU and 2-D
@@ -21,43 +23,128 @@
 namespace s3k {
 
 /* Q8_0 [N,K] blocks along k (K % 32 == 0, every row whole blocks) ->
- * f16 [N,K]: one thread per 16-byte output chunk (8 values, a quarter of
- * a block), which reads the block scale and its two dwords of q; the
- * outputs are q * scale formed in f32 and rounded once. A wave's stores
- * are one contiguous KiB, and its loads span 16 blocks (576 bytes).
- * Measured 3.3 us for 4096 x 1024 against 4.9 us for one thread per
- * block (nine dword loads at a 36-byte lane stride, four strided
- * stores). */
+ * f16 [N,K] with the weight-row factors of s3k_q8_wfactors: one wave per
+ * row, CPL 16-byte output chunks (8 values, a quarter of a block) per
+ * lane. Every lane first loads its chunks' block scales and q dwords;
+ * the row's largest |scale| over those (every block is some lane's)
+ * gives the factor 2^e, stored to cs[n]; then the outputs
+ * f16(q * (scale * 2^-e)), q * scale' formed in f32 and rounded once. At
+ * e = 0 these are the plain q * scale. A wave's stores are one
+ * contiguous KiB per round. */
 __device__ __forceinline__ uint32_t q8_pair_to_f16(uint32_t d, int sh, float s)
 {
 	return f32_to_f16((float)(int)(int8_t)(d >> sh) * s) |
 	       (f32_to_f16((float)(int)(int8_t)(d >> (sh + 8)) * s) << 16);
 }
 
-__device__ __forceinline__ void expand_chunk(const char *blk, uint16_t *out, long long t)
+template <int CPL>
+__device__ __forceinline__ void expand_row(const char *blk, uint16_t *out, float *cs, int K, int n,
+					   int lane)
 {
-	const char *b = blk + (t >> 2) * 36;
-	const int part = (int)(t & 3);
-	const float s = *(const float *)b;
-	const uint32_t d0 = *(const uint32_t *)(b + 4 + 8 * part);
-	const uint32_t d1 = *(const uint32_t *)(b + 8 + 8 * part);
-	((uint4 *)out)[t] = make_uint4(q8_pair_to_f16(d0, 0, s), q8_pair_to_f16(d0, 16, s),
-				       q8_pair_to_f16(d1, 0, s), q8_pair_to_f16(d1, 16, s));
+	const int chunks = K / 8;
+	const char *row = blk + (long long)n * (K / 32) * 36;
+	float s[CPL];
+	uint32_t d0[CPL], d1[CPL];
+	float m = 0.0f;
+#pragma unroll
+	for (int u = 0; u < CPL; ++u) {
+		const int c = lane + 64 * u;
+		s[u] = 0.0f;
+		d0[u] = d1[u] = 0u;
+		if (c < chunks) {
+			const char *b = row + (c >> 2) * 36;
+			s[u] = *(const float *)b;
+			d0[u] = *(const uint32_t *)(b + 4 + 8 * (c & 3));
+			d1[u] = *(const uint32_t *)(b + 8 + 8 * (c & 3));
+			m = fmaxf(m, finite_abs(s[u]));
+		}
+	}
+	const int e = wscale_exp_of(127.0f * wave_max_f32(m));
+	if (lane == 0)
+		cs[n] = pow2f(e);
+	const float inv = pow2f(-e);
+	uint4 *o = (uint4 *)(out + (long long)n * K);
+#pragma unroll
+	for (int u = 0; u < CPL; ++u) {
+		const int c = lane + 64 * u;
+		const float sc = s[u] * inv;
+		if (c < chunks)
+			o[c] = make_uint4(q8_pair_to_f16(d0[u], 0, sc), q8_pair_to_f16(d0[u], 16, sc),
+					  q8_pair_to_f16(d1[u], 0, sc), q8_pair_to_f16(d1[u], 16, sc));
+	}
 }
 
-__global__ void __launch_bounds__(256) q8_expand_nk_k(const char *blk, uint16_t *out,
-						      long long nchunk)
+/* four rows per workgroup (K <= 512 * CPL) */
+template <int CPL>
+__global__ void __launch_bounds__(256) q8_expand_rows_k(const char *blk, uint16_t *out, float *cs,
+							int K, int N)
 {
-	const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-	if (t < nchunk)
-		expand_chunk(blk, out, t);
+	const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (n < N)
+		expand_row<CPL>(blk, out, cs, K, n, threadIdx.x & 63);
+}
+
+/* The factors alone (s3k_q8_wfactors). [N,K] over the flat index (slices
+ * sb bytes apart): one wave per row n. Rows of whole blocks (K % 32 ==
+ * 0) take 127 * their largest |scale|; a row that shares blocks with its
+ * neighbours (another row's values may have set a block's scale) takes
+ * the largest |q| * |scale| over its own elements. */
+__global__ void __launch_bounds__(256) q8_wfac_nk_k(const char *blk, float *cs, int K, int N,
+						    long long sb)
+{
+	const int lane = threadIdx.x & 63;
+	const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (n >= N)
+		return;
+	const char *b = blk + (long long)blockIdx.y * sb;
+	float m = 0.0f;
+	if (K % 32 == 0) {
+		const long long b0 = (long long)n * (K / 32);
+		for (int i = lane; i < K / 32; i += 64)
+			m = fmaxf(m, finite_abs(*(const float *)(b + (b0 + i) * 36)));
+		m *= 127.0f;
+	} else {
+		for (int k = lane; k < K; k += 64) {
+			const long long lin = (long long)n * K + k;
+			const char *bk = b + (lin >> 5) * 36;
+			const float q = (float)__builtin_abs((int)(int8_t)bk[4 + (lin & 31)]);
+			m = fmaxf(m, finite_abs(*(const float *)bk) * q);
+		}
+	}
+	m = wave_max_f32(m);
+	if (lane == 0)
+		cs[(long long)blockIdx.y * N + n] = pow2f(wscale_exp_of(m));
+}
+
+/* [K,N] with blocks over k*N+n (a block spans 32 columns): column n
+ * takes the largest |q| * |scale| over its own elements; 64 columns per
+ * workgroup, its four waves splitting k. */
+__global__ void __launch_bounds__(256) q8_wfac_kn_k(const char *blk, float *cs, int K, int N)
+{
+	__shared__ float part[4][64];
+	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+	const int n = blockIdx.x * 64 + lane;
+	float m = 0.0f;
+	if (n < N)
+		for (int k = w; k < K; k += 4) {
+			const long long lin = (long long)k * N + n;
+			const char *bk = blk + (lin >> 5) * 36;
+			const float q = (float)__builtin_abs((int)(int8_t)bk[4 + (lin & 31)]);
+			m = fmaxf(m, finite_abs(*(const float *)bk) * q);
+		}
+	part[w][lane] = m;
+	__syncthreads();
+	if (w == 0 && n < N)
+		cs[n] = pow2f(wscale_exp_of(fmaxf(fmaxf(part[0][lane], part[1][lane]),
+						  fmaxf(part[2][lane], part[3][lane]))));
 }
 
 /* One thread per output of f16 [N,K]; element (n,k) reads block lin/32
  * of the flat Q8 array, lin = k*N+n (KN) or n*K+k (NK, rows that split
- * blocks). */
+ * blocks), and is stored as f16(q * (scale / cs[n])). */
 template <bool KN>
-__global__ void __launch_bounds__(256) q8_to_f16_nk(const char *blk, uint16_t *out, int K, int N)
+__global__ void __launch_bounds__(256) q8_to_f16_nk(const char *blk, uint16_t *out,
+						    const float *cs, int K, int N)
 {
 	const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
 	const long long tot = (long long)N * K;
@@ -66,7 +153,7 @@ __global__ void __launch_bounds__(256) q8_to_f16_nk(const char *blk, uint16_t *o
 	const int n = (int)(i / K), k = (int)(i % K);
 	const long long lin = KN ? (long long)k * N + n : i;
 	const char *b = blk + (lin >> 5) * 36;
-	const float s = *(const float *)b;
+	const float s = *(const float *)b * inv_pow2(cs[n]);
 	const float q = (float)(int)(int8_t)b[4 + (lin & 31)];
 	out[i] = (uint16_t)f32_to_f16(q * s);
 }
@@ -298,13 +385,14 @@ __global__ void __launch_bounds__(256) cast_f16_rows_k(const char *src, long lon
 }
 
 /* The row cast of A and the expansion of a Q8_0 weight in one launch:
- * workgroups [0, row_wgs) cast four rows each, the rest expand 256
- * output chunks each. The two are independent and short, so one launch
- * lets them overlap instead of paying two dispatch ramps. */
+ * workgroups [0, row_wgs) cast four rows of A each, the rest expand four
+ * weight rows each (expand_row, with their factors). The two are
+ * independent and short, so one launch lets them overlap instead of
+ * paying two dispatch ramps. */
 template <bool BF16, int CPL>
 __global__ void __launch_bounds__(256) cast_expand_k(const char *src, long long lda_b,
 						     uint16_t *dst, float *rs, int M, int K,
-						     const char *blk, uint16_t *wout, long long nchunk,
+						     const char *blk, uint16_t *wout, float *cs, int N,
 						     int row_wgs)
 {
 	if ((int)blockIdx.x < row_wgs) {
@@ -313,9 +401,9 @@ __global__ void __launch_bounds__(256) cast_expand_k(const char *src, long long 
 			cast_row_vec<BF16, CPL>(src + (long long)m * lda_b, dst + (long long)m * K, rs + m,
 						K, threadIdx.x & 63);
 	} else {
-		const long long t = (long long)(blockIdx.x - row_wgs) * 256 + threadIdx.x;
-		if (t < nchunk)
-			expand_chunk(blk, wout, t);
+		const int n = (blockIdx.x - row_wgs) * 4 + (threadIdx.x >> 6);
+		if (n < N)
+			expand_row<CPL>(blk, wout, cs, K, n, threadIdx.x & 63);
 	}
 }
 
@@ -407,29 +495,62 @@ static dim3 grid1(long long n)
 	return dim3((unsigned)((n + 255) / 256));
 }
 
-extern "C" int s3k_q8_kn_to_f16_nk(const void *blocks, void *out, int K, int N, void *stream)
+extern "C" int s3k_q8_wfactors(const void *blocks, float *cs, int K, int N, int nt, int batch,
+			       long long stride_b, void *stream)
 {
-	const long long tot = (long long)K * N;
-	if (tot <= 0)
-		return 0;
-	hipLaunchKernelGGL(q8_to_f16_nk<true>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
-			   (const char *)blocks, (uint16_t *)out, K, N);
+	if (K <= 0 || N <= 0 || batch <= 0 || !cs || ((uintptr_t)blocks & 3u) || (!nt && batch != 1) ||
+	    batch > 65535)
+		return (int)hipErrorInvalidValue;
+	if (nt)
+		hipLaunchKernelGGL(q8_wfac_nk_k, dim3((unsigned)((N + 3) / 4), (unsigned)batch),
+				   dim3(256), 0, (hipStream_t)stream, (const char *)blocks, cs, K, N,
+				   stride_b);
+	else
+		hipLaunchKernelGGL(q8_wfac_kn_k, dim3((unsigned)((N + 63) / 64)), dim3(256), 0,
+				   (hipStream_t)stream, (const char *)blocks, cs, K, N);
 	return (int)hipGetLastError();
 }
 
-extern "C" int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N, void *stream)
+extern "C" int s3k_q8_kn_to_f16_nk(const void *blocks, void *out, const float *cs, int K, int N,
+				   void *stream)
 {
 	const long long tot = (long long)K * N;
 	if (tot <= 0)
 		return 0;
-	if (K % 32 == 0 && !((uintptr_t)blocks & 3u) && !((uintptr_t)out & 15u)) {
-		const long long nchunk = tot / 8;
-		hipLaunchKernelGGL(q8_expand_nk_k, grid1(nchunk), dim3(256), 0, (hipStream_t)stream,
-				   (const char *)blocks, (uint16_t *)out, nchunk);
-	} else {
-		hipLaunchKernelGGL(q8_to_f16_nk<false>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
-				   (const char *)blocks, (uint16_t *)out, K, N);
+	if (!cs)
+		return (int)hipErrorInvalidValue;
+	hipLaunchKernelGGL(q8_to_f16_nk<true>, grid1(tot), dim3(256), 0, (hipStream_t)stream,
+			   (const char *)blocks, (uint16_t *)out, cs, K, N);
+	return (int)hipGetLastError();
+}
+
+extern "C" int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, float *cs, int K, int N,
+				   void *stream)
+{
+	const long long tot = (long long)K * N;
+	if (tot <= 0)
+		return 0;
+	if (!cs)
+		return (int)hipErrorInvalidValue;
+	hipStream_t st = (hipStream_t)stream;
+	if (K % 32 == 0 && K <= 4096 && !((uintptr_t)blocks & 3u) && !((uintptr_t)out & 15u)) {
+		const int cpl = (K / 8 + 63) / 64;
+		const dim3 grid((unsigned)((N + 3) / 4));
+		const char *b = (const char *)blocks;
+		uint16_t *o = (uint16_t *)out;
+		if (cpl <= 2)
+			hipLaunchKernelGGL(q8_expand_rows_k<2>, grid, dim3(256), 0, st, b, o, cs, K, N);
+		else if (cpl <= 4)
+			hipLaunchKernelGGL(q8_expand_rows_k<4>, grid, dim3(256), 0, st, b, o, cs, K, N);
+		else
+			hipLaunchKernelGGL(q8_expand_rows_k<8>, grid, dim3(256), 0, st, b, o, cs, K, N);
+		return (int)hipGetLastError();
 	}
+	const int e = s3k_q8_wfactors(blocks, cs, K, N, 1, 1, 0, stream);
+	if (e)
+		return e;
+	hipLaunchKernelGGL(q8_to_f16_nk<false>, grid1(tot), dim3(256), 0, st, (const char *)blocks,
+			   (uint16_t *)out, cs, K, N);
 	return (int)hipGetLastError();
 }
 
@@ -544,48 +665,45 @@ static int cast_rows_launch(const char *src, long long lda_b, long long sa_b, ui
 
 template <bool BF16>
 static int cast_expand_launch(const char *src, long long lda_b, uint16_t *dst, float *rs, int M,
-			      int K, const char *blk, uint16_t *wout, long long nchunk,
-			      hipStream_t st)
+			      int K, const char *blk, uint16_t *wout, float *cs, int N, hipStream_t st)
 {
 	const int cpl = (K / 8 + 63) / 64;
 	const int row_wgs = (M + 3) / 4;
-	const long long wgs = row_wgs + (nchunk + 255) / 256;
-	const dim3 grid((unsigned)wgs);
+	const dim3 grid((unsigned)(row_wgs + (N + 3) / 4));
 	if (cpl <= 2)
 		hipLaunchKernelGGL((cast_expand_k<BF16, 2>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
-				   M, K, blk, wout, nchunk, row_wgs);
+				   M, K, blk, wout, cs, N, row_wgs);
 	else if (cpl <= 4)
 		hipLaunchKernelGGL((cast_expand_k<BF16, 4>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
-				   M, K, blk, wout, nchunk, row_wgs);
+				   M, K, blk, wout, cs, N, row_wgs);
 	else
 		hipLaunchKernelGGL((cast_expand_k<BF16, 8>), grid, dim3(256), 0, st, src, lda_b, dst, rs,
-				   M, K, blk, wout, nchunk, row_wgs);
+				   M, K, blk, wout, cs, N, row_wgs);
 	return (int)hipGetLastError();
 }
 
 /* A (f32 or bf16 [M, K], pitch lda elements) to row-scaled f16 rows plus
  * factors (as s3k_cast_f16_rows, one batch), and W (Q8_0 [N, K]) to f16
- * [N, K] (as s3k_q8_nk_to_f16_nk), in one launch. hipErrorInvalidValue
- * when the shapes or alignments do not allow it (K % 32, K > 4096,
- * 16-byte rows): the caller then uses the two separate launches. */
+ * [N, K] with its factors cs (as s3k_q8_nk_to_f16_nk), in one launch.
+ * hipErrorInvalidValue when the shapes or alignments do not allow it
+ * (K % 32, K > 4096, 16-byte rows): the caller then uses the two
+ * separate launches. */
 extern "C" int s3k_cast_rows_expand(int kind, const void *src, long long lda, void *dst, float *rs,
-				    int M, int K, const void *wblk, void *wout, int N, void *stream)
+				    int M, int K, const void *wblk, void *wout, float *cs, int N,
+				    void *stream)
 {
 	const int es = kind == S3K_F32 ? 4 : 2;
 	if ((kind != S3K_F32 && kind != S3K_BF16) || M <= 0 || N <= 0 || K <= 0 || K % 32 ||
-	    K > 4096 || M > (1 << 28) || (lda * es) % 16 || lda < K ||
+	    K > 4096 || M > (1 << 28) || N > (1 << 28) || (lda * es) % 16 || lda < K ||
 	    (((uintptr_t)src | (uintptr_t)dst | (uintptr_t)wout) & 15u) || ((uintptr_t)wblk & 3u) ||
-	    !rs)
-		return (int)hipErrorInvalidValue;
-	const long long nchunk = (long long)N * K / 8;
-	if ((M + 3) / 4 + (nchunk + 255) / 256 > 0x7FFFFFFFLL)
+	    !rs || !cs)
 		return (int)hipErrorInvalidValue;
 	hipStream_t st = (hipStream_t)stream;
 	return kind == S3K_BF16
 		? cast_expand_launch<true>((const char *)src, lda * es, (uint16_t *)dst, rs, M, K,
-					   (const char *)wblk, (uint16_t *)wout, nchunk, st)
+					   (const char *)wblk, (uint16_t *)wout, cs, N, st)
 		: cast_expand_launch<false>((const char *)src, lda * es, (uint16_t *)dst, rs, M, K,
-					    (const char *)wblk, (uint16_t *)wout, nchunk, st);
+					    (const char *)wblk, (uint16_t *)wout, cs, N, st);
 }
 
 extern "C" int s3k_cast_f16_rows(int kind, const void *src, long long lda, long long sa, void *dst,

@@ -235,7 +235,9 @@ struct LoadQ8NT {
 	static constexpr int TOT = R * BPR;
 	static constexpr int NB = (TOT + NT - 1) / NT;
 	uint32_t v[NB][9];
+	float inv[NB];
 	const char *src;
+	const float *cs;
 	long long rowbytes;
 	int rows, kbt, tid;
 
@@ -246,6 +248,8 @@ struct LoadQ8NT {
 		rows = p.N - row0;
 		kbt = p.K / 32;
 		tid = t;
+		/* weight row r's values go to f16 as q * scale / cs[r] */
+		cs = (p.flags & S3K_EPI_COLSCALE) ? p.cs + bz * p.cs_sb + row0 : nullptr;
 	}
 	__device__ void load(int kc0)
 	{
@@ -260,6 +264,7 @@ struct LoadQ8NT {
 			const uint32_t *g = (const uint32_t *)(src + r * rowbytes +
 							      (long long)(kb0 + j) * 36);
 			bool ok = kb0 + j < kbt;
+			inv[i] = cs ? inv_pow2(cs[r]) : 1.0f;
 #pragma unroll
 			for (int d = 0; d < 9; ++d)
 				v[i][d] = ok ? g[d] : 0u;
@@ -273,7 +278,7 @@ struct LoadQ8NT {
 			if (TOT % NT != 0 && q >= TOT)
 				continue;
 			int row = q / BPR, j = q % BPR;
-			float s = __uint_as_float(v[i][0]);
+			float s = __uint_as_float(v[i][0]) * inv[i];
 #pragma unroll
 			for (int cc = 0; cc < 4; ++cc) {
 				uint2 lo = dequant4_f16(v[i][1 + 2 * cc], s);
@@ -513,6 +518,8 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.rm_d2 = g->rm_d2;
 	p.rs = g->rs;
 	p.rs_sb = g->rs_sb;
+	p.cs = g->cs;
+	p.cs_sb = g->cs_sb;
 	p.ovf = g->ovf;
 	p.ovf_tag = g->ovf_tag;
 	p.M = g->M;
@@ -695,6 +702,12 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	if ((g->flags & S3K_EPI_QKV) &&
 	    ((path != S3K_PATH_MFMA && path != S3K_PATH_SKINNY) ||
 	     (path == S3K_PATH_MFMA && !mfma_ok(g)) || !qkv_ok(g, path)))
+		return (int)hipErrorInvalidValue;
+	/* the weight-row factors: every MFMA GEMM rounding q*scale to f16
+	 * applies them (S3K_EPI_COLSCALE), and only the MFMA epilogue takes
+	 * them (the skinny and generic kernels keep q*scale in f32) */
+	if ((g->flags & S3K_EPI_COLSCALE) ? (path != S3K_PATH_MFMA || !g->cs)
+					  : (path == S3K_PATH_MFMA && g->b_kind == S3K_Q8))
 		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))

@@ -24,6 +24,8 @@ struct GemmArgs {
 	int rm_g, rm_d1, rm_d2;       /* output row map (s3k_gemm), rm_g 0 = none */
 	const float *rs;              /* S3K_EPI_ROWSCALE factors, rows apart   */
 	long long rs_sb;              /* ... per batch slice                    */
+	const float *cs;              /* S3K_EPI_COLSCALE factors, columns apart */
+	long long cs_sb;              /* ... per batch slice                    */
 	unsigned *ovf;                /* S3K_C_F16OP range flag (or NULL)       */
 	unsigned ovf_tag;
 	int flags;
@@ -386,7 +388,42 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 				}
 		}
 	}
-	const int flags = p.flags & ~S3K_EPI_ROWSCALE;
+	if (p.flags & S3K_EPI_COLSCALE) {
+		/* the weight-row factors of a Q8_0 weight, per output column */
+		const float *cp = p.cs + (long long)bz * p.cs_sb;
+		if constexpr (TR) {
+			/* lane l holds columns 8t + 4(l >> 5) + q (q < 4) of each
+			 * 32-column block */
+#pragma unroll
+			for (int j = 0; j < FN; ++j)
+#pragma unroll
+				for (int t = 0; t < 4; ++t) {
+					const int c0 = n0 + j * 32 + 8 * t + 4 * (lane >> 5);
+					float f[4];
+#pragma unroll
+					for (int q = 0; q < 4; ++q)
+						f[q] = c0 + q < p.N ? cp[c0 + q] : 1.0f;
+#pragma unroll
+					for (int i = 0; i < FM; ++i)
+#pragma unroll
+						for (int q = 0; q < 4; ++q)
+							acc[i][j][4 * t + q] *= f[q];
+				}
+		} else {
+			/* lane l holds column l & 31 of each 32-column block */
+#pragma unroll
+			for (int j = 0; j < FN; ++j) {
+				const int c = n0 + j * 32 + (lane & 31);
+				const float f = c < p.N ? cp[c] : 1.0f;
+#pragma unroll
+				for (int i = 0; i < FM; ++i)
+#pragma unroll
+					for (int q = 0; q < 16; ++q)
+						acc[i][j][q] *= f;
+			}
+		}
+	}
+	const int flags = p.flags & ~(S3K_EPI_ROWSCALE | S3K_EPI_COLSCALE);
 	const bool heavy = (flags & S3K_EPI_RES) || (!FIXED && (flags & S3K_EPI_BIAS));
 	const bool light = !heavy && (flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
 	/* the common cases (plain rows, whole 16-byte vectors, no residual,

@@ -16,8 +16,9 @@
  *     turns the 8 int8 into exact f16 integers with one byte permute and
  *     one packed subtract per pair (bytes biased by 128 under the f16
  *     exponent of 1024, then 1152 subtracted) and multiplies them by the
- *     block scale rounded to f16, so the MFMA sees q*scale in f16, as the
- *     register-staged Q8 loader produces it;
+ *     block scale divided by the weight row's factor (S3K_EPI_COLSCALE,
+ *     a power of two that keeps the row's largest scale an f16 normal)
+ *     and rounded to f16; the epilogue multiplies the factor back;
  *   - v_mfma_f32_32x32x16_f16, f32 accumulate; each wave covers 128 rows
  *     of A so one dequantized B fragment serves 4 MFMAs. The B fragment
  *     is the MFMA's first operand (the MFMA forms C^T; the epilogue stages
@@ -121,9 +122,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 		qo[ks] = b + (b >= 64 ? 8 : 0);
 	}
 	int brow[FN];
+	/* weight row n's block scales are divided by its factor cs[n] (a
+	 * power of two, so exactly) before their rounding to f16 */
+	float binv[FN];
 #pragma unroll
-	for (int j = 0; j < FN; ++j)
+	for (int j = 0; j < FN; ++j) {
 		brow[j] = (wn0 + j * 32 + (lane & 31)) * (PW * 16);
+		const int n = tn * BN + wn0 + j * 32 + (lane & 31);
+		binv[j] = (p.flags & S3K_EPI_COLSCALE) && n < p.N
+				  ? inv_pow2(p.cs[(long long)bz * p.cs_sb + n]) : 1.0f;
+	}
 
 	s3k_f32x16 acc[FM][FN];
 #pragma unroll
@@ -163,7 +171,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 			q8h2_t s2[2];
 #pragma unroll
 			for (int blk = 0; blk < 2; ++blk) {
-				const _Float16 sh = (_Float16)*(const float *)(row + 36 * blk);
+				const _Float16 sh = (_Float16)(*(const float *)(row + 36 * blk) * binv[j]);
 				s2[blk] = (q8h2_t){sh, sh};
 			}
 #pragma unroll

@@ -42,6 +42,15 @@ enum s3k_kind {
 #define S3K_EPI_QKV 32  /* f32 out, batch 1, direct-to-LDS GEMM only: the
 			 * result is stored as the head-split attention
 			 * operands (struct s3k_gemm, qkv_*) instead of C */
+#define S3K_EPI_COLSCALE 64 /* out = acc * cs[n] first (with the row factor):
+			     * the weight-row factors of a Q8_0 weight
+			     * (s3k_q8_wfactors). Kernels that round q*scale
+			     * to f16 form f16(q * scale / cs[n]); on an f16
+			     * copy of the weight made that way
+			     * (s3k_q8_nk_to_f16_nk) only the epilogue
+			     * multiply remains. The MFMA path requires it
+			     * for Q8_0 weights; the skinny and generic
+			     * kernels (q exact, scale in f32) reject it. */
 
 /*
  * One (optionally strided-batched) GEMM: C[M,N] = A[M,K] * B, row-major.
@@ -72,6 +81,10 @@ struct s3k_gemm {
 	 * batch slice b */
 	const float *rs;
 	long long   rs_sb;
+	/* S3K_EPI_COLSCALE: per-column (weight-row) f32 factors, powers of
+	 * two, cs[b * cs_sb + n] for batch slice b */
+	const float *cs;
+	long long   cs_sb;
 	/* f16 operand output (S3K_C_F16OP): when ovf is set, a value the f16
 	 * copy cannot hold faithfully (|x| >= 2^15, or a run of 8 nonzero
 	 * values all below 2^-10) stores ovf_tag to *ovf */
@@ -106,14 +119,32 @@ int s3k_gemm_launch(const struct s3k_gemm *g, void *stream);
 int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *stream);
 
 /*
- * Q8 [K,N] with blocks over the flat index k*N+n (the reference kernel
- * contract) -> f16 W^T[N,K] (q*scale rounded to f16), so the Q8 NN case
- * runs on the f16 NT GEMM. Any K, N.
+ * Weight-row factors of Q8_0 weights for kernels that round q*scale to
+ * f16 (struct s3k_gemm, S3K_EPI_COLSCALE): for output column n, with
+ * m the largest |q*scale| over the elements of weight row n (for a row
+ * of whole blocks, 127 * its largest |block scale|: the same for blocks
+ * of the quantizer, an upper bound otherwise), cs[n] = 2^e, e = 0 when m
+ * lies in [2^-6, 2^15) or is 0, else the e that brings m into
+ * [2^14, 2^15). The f16 values f16(q*scale*2^-e) then keep 11 bits, and
+ * the f32 epilogue multiplies by 2^e, exactly. Batch slices of an [N,K]
+ * weight (nt 1, blocks over the flat index n*K+k, any K) lie stride_b
+ * bytes apart, cs[b*N + n]; nt 0 is one [K,N] weight with blocks over
+ * k*N+n (the reference kernel contract), batch 1.
  */
-int s3k_q8_kn_to_f16_nk(const void *blocks, void *out, int K, int N,
+int s3k_q8_wfactors(const void *blocks, float *cs, int K, int N, int nt, int batch,
+		    long long stride_b, void *stream);
+/*
+ * Q8 [K,N] with blocks over the flat index k*N+n (the reference kernel
+ * contract) -> f16 W^T[N,K], q*scale/cs[n] rounded to f16 (cs from
+ * s3k_q8_wfactors with nt 0), so the Q8 NN case runs on the f16 NT GEMM
+ * with S3K_EPI_COLSCALE. Any K, N.
+ */
+int s3k_q8_kn_to_f16_nk(const void *blocks, void *out, const float *cs, int K, int N,
 			void *stream);
-/* Q8 [N,K] with blocks over the flat index n*K+k (any K) -> f16 [N,K]. */
-int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, int K, int N,
+/* Q8 [N,K] with blocks over the flat index n*K+k (any K) -> f16 [N,K],
+ * q*scale/cs[n] rounded to f16; the factors cs[N] are computed here and
+ * stored (s3k_q8_wfactors' rule). */
+int s3k_q8_nk_to_f16_nk(const void *blocks, void *out, float *cs, int K, int N,
 			void *stream);
 
 /* Elementwise ops the fused graph paths fall back to when they cannot
@@ -129,10 +160,11 @@ int s3k_cast(int src_kind, int dst_kind, const void *src, void *dst, long long n
 /* n f32 or bf16 values -> f16 (RNE); 16-byte aligned pointers. */
 int s3k_cast_f16(int kind, const void *src, void *dst, long long n, void *stream);
 /* s3k_cast_f16_rows (one batch) and s3k_q8_nk_to_f16_nk of an [N, K]
- * weight in one launch; hipErrorInvalidValue when K % 32, K > 4096 or an
- * alignment rules it out (then run the two separately). */
+ * weight (with its factors cs[N]) in one launch; hipErrorInvalidValue
+ * when K % 32, K > 4096 or an alignment rules it out (then run the two
+ * separately). */
 int s3k_cast_rows_expand(int kind, const void *src, long long lda, void *dst, float *rs, int M,
-			 int K, const void *wblk, void *wout, int N, void *stream);
+			 int K, const void *wblk, void *wout, float *cs, int N, void *stream);
 /*
  * Activations for a GEMM that rounds them to f16, row by row: batch
  * slices (at element stride sa) of M rows of K values (pitch lda) ->

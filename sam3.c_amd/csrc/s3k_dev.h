@@ -74,6 +74,28 @@ __device__ __forceinline__ int scale_exp_of(float amax)
 	return e < -100 ? -100 : e > 113 ? 113 : e;
 }
 
+/* The exponent e of the weight-row factor 2^e of a Q8_0 weight row
+ * whose values |q*scale| are at most m (inf and NaN counted as 0): 0
+ * when m lies in [2^-6, 2^15) or is 0, else the e that brings m into
+ * [2^14, 2^15), clamped to [-100, 113]. For a row of whole blocks m is
+ * 127 * its largest |scale|, so at e = 0 that scale, at least 2^-6 / 127,
+ * is an f16 normal (2^-14 and up), and so is every nonzero q times it.
+ * The row's weights go to f16 as f16(q * scale * 2^-e); output column n
+ * is multiplied by 2^e in the f32 epilogue. */
+__device__ __forceinline__ int wscale_exp_of(float m)
+{
+	if (!(m > 0.0f) || m > 3.402823466e38f || (m >= 0x1p-6f && m < 0x1p15f))
+		return 0;
+	int e = (int)((__float_as_uint(m) >> 23) & 0xFFu) - 127 - 14;
+	return e < -100 ? -100 : e > 113 ? 113 : e;
+}
+
+/* 1 / f for f = 2^e, -126 <= e <= 126 (exact) */
+__device__ __forceinline__ float inv_pow2(float f)
+{
+	return __uint_as_float((254u - ((__float_as_uint(f) >> 23) & 0xFFu)) << 23);
+}
+
 /* scale_exp_of the largest amax over the wave */
 __device__ __forceinline__ int row_scale_exp(float amax)
 {

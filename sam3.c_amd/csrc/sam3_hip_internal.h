@@ -133,8 +133,10 @@ enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, con
 enum { S3H_PREP_SPLIT_W = 1,   /* f32 [rows, k] -> bf16 [rows, 3k] = [hi|hi|lo] */
        S3H_PREP_PAD_PLANES,    /* f32 [rows, K] -> bf16 [rows, 3k] over k >= K, zero padded */
        S3H_PREP_PAD16,         /* 16-bit [rows, K] -> [rows, k], zero padded */
-       S3H_PREP_Q8_F16,        /* Q8_0 [rows, k] -> f16 [rows, k] (q*scale)   */
-       S3H_PREP_CONVT_W };     /* OHWI [OC, taps, C] -> [taps*OC, C]           */
+       S3H_PREP_Q8_F16,        /* Q8_0 [rows, k] -> f16 [rows, k] (q*scale
+				* over the row factor), then the factors f32 [rows] */
+       S3H_PREP_CONVT_W,       /* OHWI [OC, taps, C] -> [taps*OC, C]           */
+       S3H_PREP_Q8_CS };       /* Q8_0 [rows, k] -> weight-row factors f32 [rows] */
 void *s3h_prep_find(const void *src, int tag, int rows, int k);
 int s3h_prep_cacheable(const void *src, size_t src_bytes);
 enum sam3_error s3h_prep_store(const void *src, int tag, int rows, int k, void *dev, size_t bytes);

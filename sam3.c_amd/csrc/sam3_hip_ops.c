@@ -425,9 +425,26 @@ static int rounds_a_to_f16(const struct s3k_gemm *g, int path)
 
 /* g on kernel path `path`, after the row-scaled f16 copy of its
  * activations where that path would round them to f16. */
+static enum sam3_error q8_colscale(struct s3k_gemm *g, void **own, void *stream);
+
 static enum sam3_error launch_a_safe(const struct s3k_gemm *g, int path, const char *what,
 				     void *stream)
 {
+	if (g->b_kind == S3K_Q8 && path == S3K_PATH_MFMA && !(g->flags & S3K_EPI_COLSCALE)) {
+		/* the MFMA kernels round q*scale to f16: with the weight-row
+		 * factors */
+		struct s3k_gemm h = *g;
+		void *own = NULL;
+		enum sam3_error err = q8_colscale(&h, &own, stream);
+		if (err == SAM3_OK)
+			err = launch_a_safe(&h, path, what, stream);
+		if (own) {
+			enum sam3_error ferr = s3h_scratch_free(own, stream);
+			if (err == SAM3_OK)
+				err = ferr;
+		}
+		return err;
+	}
 	if (!rounds_a_to_f16(g, path)) {
 		int e = s3k_gemm_launch_path(g, path, stream);
 		if (e == hipErrorInvalidValue) {
@@ -459,32 +476,41 @@ static enum sam3_error launch_a_safe(const struct s3k_gemm *g, int path, const c
 }
 
 /* Q8 layouts the tiled kernels cannot stream (blocks over the [K,N] flat
- * index, or [N,K] rows that split blocks): unpack to f16 [N,K] in
- * stream-ordered scratch and run the f16 NT GEMM on it. */
+ * index, or [N,K] rows that split blocks): unpacked, with the weight-row
+ * factors, to f16 [N,K] in stream-ordered scratch, and the f16 NT GEMM
+ * runs on it with the factors in its epilogue (S3K_EPI_COLSCALE). When
+ * the f16 problem would not reach the MFMA GEMM, the generic kernel runs
+ * on the Q8_0 blocks instead. */
 static enum sam3_error q8_unpacked(struct s3k_gemm *g, void *stream)
 {
 	const int nt = g->flags & S3K_B_NT;
 	const size_t bytes = (size_t)g->N * g->K * 2;
+	struct s3k_gemm h = *g;
+	h.b_kind = S3K_F16;
+	h.ldb = g->K;
+	h.flags |= S3K_B_NT;
+	if (s3k_gemm_path(&h) != S3K_PATH_MFMA)
+		return s3h_hip(s3k_gemm_launch_path(g, S3K_PATH_GENERIC, stream), "matmul_q8 generic");
 	void *w16 = NULL;
-	enum sam3_error err;
-
-	err = s3h_scratch_alloc(&w16, bytes, stream);
+	enum sam3_error err = s3h_scratch_alloc(&w16, bytes + (size_t)g->N * 4, stream);
 	if (err != SAM3_OK)
 		return err;
-	int e = nt ? s3k_q8_nk_to_f16_nk(g->b, w16, g->K, g->N, stream)
-		   : s3k_q8_kn_to_f16_nk(g->b, w16, g->K, g->N, stream);
+	float *cs = (float *)((char *)w16 + bytes);
+	int e = 0;
+	if (nt) {
+		e = s3k_q8_nk_to_f16_nk(g->b, w16, cs, g->K, g->N, stream);
+	} else {
+		e = s3k_q8_wfactors(g->b, cs, g->K, g->N, 0, 1, 0, stream);
+		if (!e)
+			e = s3k_q8_kn_to_f16_nk(g->b, w16, cs, g->K, g->N, stream);
+	}
 	err = s3h_hip(e, "matmul_q8 unpack");
 	if (err == SAM3_OK) {
-		struct s3k_gemm h = *g;
 		h.b = w16;
-		h.b_kind = S3K_F16;
-		h.ldb = g->K;
-		h.flags |= S3K_B_NT;
-		if (h.a_kind == S3K_F16 || s3k_gemm_path(&h) == S3K_PATH_MFMA)
-			err = launch_a_safe(&h, s3k_gemm_path(&h), "matmul_q8 gemm", stream);
-		else
-			err = s3h_hip(s3k_gemm_launch_path(g, S3K_PATH_GENERIC, stream),
-				      "matmul_q8 generic");
+		h.cs = cs;
+		h.cs_sb = 0;
+		h.flags |= S3K_EPI_COLSCALE;
+		err = launch_a_safe(&h, S3K_PATH_MFMA, "matmul_q8 gemm", stream);
 	}
 	enum sam3_error ferr = s3h_scratch_free(w16, stream);
 	return err != SAM3_OK ? err : ferr;
@@ -529,11 +555,60 @@ static int prep_conv_w(const void *w, void *out, int rows, int k, int k_out, int
 	return s3k_conv_wprep(kind, w, out, rows, k, k_out, stream);
 }
 
+/* f16 [rows, k] followed by the weight-row factors f32 [rows] */
 static int prep_q8_f16(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
 {
 	(void)k_out;
 	(void)kind;
-	return s3k_q8_nk_to_f16_nk(w, out, k, rows, stream);
+	return s3k_q8_nk_to_f16_nk(w, out, (float *)((char *)out + (size_t)rows * k * 2), k, rows,
+				   stream);
+}
+
+static int prep_q8_cs(const void *w, void *out, int rows, int k, int k_out, int kind, void *stream)
+{
+	(void)k_out;
+	(void)kind;
+	return s3k_q8_wfactors(w, (float *)out, k, rows, 1, 1, 0, stream);
+}
+
+/* The weight-row factors (S3K_EPI_COLSCALE, s3k_q8_wfactors) of g's
+ * Q8_0 [N,K] weight for an MFMA kernel that rounds q*scale to f16: from
+ * the backend's prepared-weight cache when the weight is constant (made
+ * once there), else computed into scratch that *own returns for the
+ * caller to free. A batch of distinct weights (stride_b != 0) gets the
+ * factors of every slice, cs_sb = N apart. */
+static enum sam3_error q8_colscale(struct s3k_gemm *g, void **own, void *stream)
+{
+	*own = NULL;
+	if (!(g->flags & S3K_B_NT)) {
+		s3h_error("matmul_q8: the MFMA kernels read Q8_0 weights as [N, K] only");
+		return SAM3_EINVAL;
+	}
+	const int nb = g->batch > 1 && g->stride_b != 0 ? g->batch : 1;
+	void *cs = NULL;
+	enum sam3_error err;
+	if (nb == 1) {
+		const size_t q8_bytes = ((size_t)g->N * g->K + 31) / 32 * 36;
+		int mine = 0;
+		err = prep_weight(g->b, q8_bytes, S3H_PREP_Q8_CS, g->N, g->K, g->K, (size_t)g->N * 4,
+				  S3K_Q8, prep_q8_cs, stream, &cs, &mine);
+		if (mine)
+			*own = cs;
+	} else {
+		err = s3h_scratch_alloc(&cs, (size_t)nb * g->N * 4, stream);
+		if (err == SAM3_OK) {
+			*own = cs;
+			err = s3h_hip(s3k_q8_wfactors(g->b, (float *)cs, g->K, g->N, 1, nb, g->stride_b,
+						      stream),
+				      "matmul_q8 weight factors");
+		}
+	}
+	if (err != SAM3_OK)
+		return err;
+	g->cs = (const float *)cs;
+	g->cs_sb = nb > 1 ? g->N : 0;
+	g->flags |= S3K_EPI_COLSCALE;
+	return SAM3_OK;
 }
 
 /* Q8_0 W [N,K] x f16 A on the MFMA path. The weight is expanded into an
@@ -558,14 +633,18 @@ static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 	    (mode == 1 || h->M >= S3H_Q8_EXPAND_MIN_M || s3h_prep_cacheable(h->b, q8_bytes))) {
 		void *w16 = NULL;
 		int own = 0;
+		const size_t wbytes = (size_t)h->N * h->K * 2;
 		enum sam3_error err = prep_weight(h->b, q8_bytes, S3H_PREP_Q8_F16, h->N, h->K, h->K,
-						  (size_t)h->N * h->K * 2, S3K_Q8, prep_q8_f16, stream,
-						  &w16, &own);
+						  wbytes + (size_t)h->N * 4, S3K_Q8, prep_q8_f16,
+						  stream, &w16, &own);
 		if (err == SAM3_OK) {
 			struct s3k_gemm e = *h;
 			e.b = w16;
 			e.b_kind = S3K_F16;
 			e.ldb = h->K;
+			e.cs = (const float *)((const char *)w16 + wbytes);
+			e.cs_sb = 0;
+			e.flags |= S3K_EPI_COLSCALE;
 			err = s3h_hip(s3k_gemm_launch_path(&e, S3K_PATH_MFMA, stream), "matmul_q8 f16 gemm");
 		}
 		if (own && w16) {
@@ -575,7 +654,17 @@ static enum sam3_error q8_f16_gemm(const struct s3k_gemm *h, void *stream)
 		}
 		return err;
 	}
-	return s3h_hip(s3k_gemm_launch_path(h, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+	struct s3k_gemm e = *h;
+	void *own = NULL;
+	enum sam3_error err = q8_colscale(&e, &own, stream);
+	if (err == SAM3_OK)
+		err = s3h_hip(s3k_gemm_launch_path(&e, S3K_PATH_MFMA, stream), "matmul_q8 gemm");
+	if (own) {
+		enum sam3_error e2 = s3h_scratch_free(own, stream);
+		if (err == SAM3_OK)
+			err = e2;
+	}
+	return err;
 }
 
 /* Whether q8_f16_gemm of h expands the weight for this call alone (not a
@@ -602,14 +691,17 @@ static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 		const size_t abuf = a_rows_f16_bytes(&h, &a_bytes);
 		const size_t wbytes = (size_t)h.N * h.K * 2;
 		void *buf = NULL;
-		enum sam3_error err = s3h_scratch_alloc(&buf, a_bytes + ((abuf - a_bytes + 255) & ~(size_t)255) + wbytes, stream);
+		enum sam3_error err = s3h_scratch_alloc(
+			&buf, a_bytes + ((abuf - a_bytes + 255) & ~(size_t)255) + wbytes + (size_t)h.N * 4,
+			stream);
 		if (err != SAM3_OK)
 			return err;
 		float *rs = (float *)((char *)buf + a_bytes);
 		uint16_t *w16 = (uint16_t *)((char *)buf + a_bytes +
 					     ((abuf - a_bytes + 255) & ~(size_t)255));
-		const int e = s3k_cast_rows_expand(h.a_kind, h.a, h.lda, buf, rs, h.M, h.K, h.b, w16, h.N,
-						   stream);
+		float *cs = (float *)((char *)w16 + wbytes);
+		const int e = s3k_cast_rows_expand(h.a_kind, h.a, h.lda, buf, rs, h.M, h.K, h.b, w16, cs,
+						   h.N, stream);
 		if (e == (int)hipSuccess) {
 			h.a = buf;
 			h.a_kind = S3K_F16;
@@ -621,6 +713,9 @@ static enum sam3_error q8_dl_cast(struct s3k_gemm *g, void *stream)
 			h.b = w16;
 			h.b_kind = S3K_F16;
 			h.ldb = h.K;
+			h.cs = cs;
+			h.cs_sb = 0;
+			h.flags |= S3K_EPI_COLSCALE;
 			err = s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream),
 				      "matmul_q8 f16 gemm");
 			enum sam3_error ferr = s3h_scratch_free(buf, stream);
@@ -1154,8 +1249,8 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 					 (force == 2 ||
 					  (force != 1 && (M >= S3H_Q8_BATCH_GEMM_M || K <= 256))) &&
 					 s3k_dlq8_eligible(&h);
-			err = gemm ? s3h_hip(s3k_gemm_launch_path(&h, S3K_PATH_MFMA, stream),
-					     "matmul_q8_batched gemm")
+			/* the GEMM with the weight-row factors of every slice */
+			err = gemm ? launch_a_safe(&h, S3K_PATH_MFMA, "matmul_q8_batched gemm", stream)
 				   : s3h_hip(s3k_gemm_launch(&h, stream), "matmul_q8_batched");
 		}
 		if (a16) {
@@ -1180,10 +1275,14 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 
 /* sam3_hip_matmul for Q8_0 weights [N,K] without any allocation: the
  * row-scaled f16 copy of the activations that the MFMA and GEMV kernels
- * read goes to the library's fixed per-device scratch array
- * (s3k_noalloc_scratch), and the Q8_0 weights are read in place (never
- * expanded). The same kernels as sam3_hip_matmul run, in the same order,
- * so the results have the same bits. Calls that overlap on one device
+ * read, and the weight-row factors of the MFMA kernels, go to the
+ * library's fixed per-device scratch array (s3k_noalloc_scratch), and
+ * the Q8_0 weights are read in place (never expanded). With the
+ * expansion off (SAM3_HIP_Q8_EXPAND=0) sam3_hip_matmul runs the same
+ * kernels on the same values, so the results have the same bits; at the
+ * default setting sam3_hip_matmul expands large weights to f16 (one
+ * rounding of q*scale instead of the scale's and the product's) and the
+ * two agree within the f32 tolerance. Calls that overlap on one device
  * (two threads, or two streams) share the array and race. */
 enum sam3_error sam3_hip_matmul_q8_noalloc(int a_dtype, const void *a, const void *w, void *c,
 					   int M, int N, int K, const void *bias, int flags,
@@ -1216,24 +1315,39 @@ enum sam3_error sam3_hip_matmul_q8_noalloc(int a_dtype, const void *a, const voi
 		s3h_error("matmul_q8_noalloc: no kernel for M=%d N=%d K=%d", M, N, K);
 		return SAM3_EINVAL;
 	}
-	if (!rounds_a_to_f16(&g, path))
+	const int cast = rounds_a_to_f16(&g, path), fac = path == S3K_PATH_MFMA;
+	if (!cast && !fac)
 		return s3h_hip(s3k_gemm_launch_path(&g, path, stream), "matmul_q8_noalloc");
-	size_t a_bytes, cap = 0;
-	const size_t need = a_rows_f16_bytes(&g, &a_bytes);
+	/* [f16 activations, row factors | weight-row factors] */
+	size_t a_bytes = 0, cap = 0;
+	const size_t abuf = cast ? (a_rows_f16_bytes(&g, &a_bytes) + 255) & ~(size_t)255 : 0;
+	const size_t need = abuf + (fac ? (size_t)N * 4 : 0);
 	void *buf = NULL;
 	enum sam3_error err = s3h_hip(s3k_noalloc_scratch(&buf, &cap), "matmul_q8_noalloc: scratch");
 	if (err != SAM3_OK)
 		return err;
 	if (need > cap) {
-		s3h_error("matmul_q8_noalloc: M=%d K=%d needs %zu bytes of scratch for the f16 "
-			  "activations, more than the %zu the library holds per device", M, K, need,
-			  cap);
+		s3h_error("matmul_q8_noalloc: M=%d N=%d K=%d needs %zu bytes of scratch for the f16 "
+			  "activations and weight factors, more than the %zu the library holds per "
+			  "device", M, N, K, need, cap);
 		return SAM3_EINVAL;
 	}
 	struct s3k_gemm h = g;
-	err = a_rows_f16_into(&h, buf, stream);
-	if (err != SAM3_OK)
-		return err;
+	if (cast) {
+		err = a_rows_f16_into(&h, buf, stream);
+		if (err != SAM3_OK)
+			return err;
+	}
+	if (fac) {
+		float *cs = (float *)((char *)buf + abuf);
+		err = s3h_hip(s3k_q8_wfactors(w, cs, K, N, 1, 1, 0, stream),
+			      "matmul_q8_noalloc weight factors");
+		if (err != SAM3_OK)
+			return err;
+		h.cs = cs;
+		h.cs_sb = 0;
+		h.flags |= S3K_EPI_COLSCALE;
+	}
 	return s3h_hip(s3k_gemm_launch_path(&h, path, stream), "matmul_q8_noalloc");
 }
 
