@@ -927,11 +927,19 @@ def main():
     if not args.quick and "cfg3" in only:
         log("config 3: 32 layers, distinct Q8 weights")
         shapes = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
-        wbase = {s: O.q8_quantize(synth.randn(synth.tensor_seed(3, i), s, 0.02))
-                 for i, s in enumerate(shapes)}
-        layers = [[hip.DeviceBuffer.of(wbase[s]) for s in shapes] for _ in range(32)]
+        # distinct seeded weights for every layer, quantized on the device
+        layers, wbytes, wlast = [], 0, None
+        for L in range(32):
+            bufs = []
+            for i, s in enumerate(shapes):
+                wq = O.q8_quantize(synth.randn(synth.tensor_seed(3, 100 + 4 * L + i), s, 0.02))
+                bufs.append(hip.DeviceBuffer.of(wq))
+                wbytes += wq.nbytes
+                wlast = wq
+            layers.append(bufs)
+        a4_bits = bf16_bits(synth.randn(synth.tensor_seed(3, 10), (M, 4096)))
         act1 = hip.DeviceBuffer.of(bf16_bits(synth.randn(synth.tensor_seed(3, 9), (M, 1024))))
-        act4 = hip.DeviceBuffer.of(bf16_bits(synth.randn(synth.tensor_seed(3, 10), (M, 4096))))
+        act4 = hip.DeviceBuffer.of(a4_bits)
         out = hip.DeviceBuffer(M * 4096 * 4)
 
         def encoder():
@@ -942,9 +950,20 @@ def main():
 
         ms3 = timer.run(encoder, 3, 1)
         flops3 = 32 * sum(2.0 * M * n_ * k_ for n_, k_ in shapes)
+        # the stream's last GEMM (layer 31's fc2) left its whole output:
+        # against float64 on the dequantized weight (outside the timing)
+        hip.check(lib.sam3_hip_stream_synchronize(stream), "sync")
+        n_, k_ = shapes[-1]
+        got = out.download(np.float32, (M, n_)).astype(np.float64)
+        wd = hip.q8_dequantize(wlast, n_ * k_).reshape(n_, k_).astype(np.float64)
+        a4 = (a4_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        ref = a4 @ wd.T
+        err3 = float(np.abs(got - ref).max() / np.abs(ref).max())
         extra["cfg3_q8_32layers"] = {"ms": round(ms3, 3),
                                      "tflops": round(flops3 / (ms3 * 1e-3) / 1e12, 2),
-                                     "weights_mb": round(32 * sum(w.nbytes for w in wbase.values()) / 1e6, 1)}
+                                     "weights_mb": round(wbytes / 1e6, 1),
+                                     "last_output_normwise_err_vs_f64": float(f"{err3:.3g}")}
+        del got, ref, a4, wd
         for L in layers:
             for b in L:
                 b.free()
