@@ -149,6 +149,13 @@ class Oracle:
         self.lib.oracle_transpose_u16(_ptr(x), _ptr(out), R, Cc)
         return out
 
+    def transpose_f32(self, x):
+        R, Cc = x.shape
+        x = _c(x, np.float32)
+        out = np.empty((Cc, R), dtype=np.float32)
+        self.lib.oracle_transpose_f32(_ptr(x), _ptr(out), R, Cc)
+        return out
+
     # ---- epilogues ----
     def bias_add(self, x, bias, kind):
         x = np.ascontiguousarray(x)

@@ -38,6 +38,39 @@ def bits32(x):
     return np.ascontiguousarray(x, np.float32).view(np.uint32)
 
 
+# ------------------------------------------------------------- transpose
+TR_SHAPES = [(1, 1), (1, 7), (7, 1), (13, 37), (64, 96), (129, 257)]
+
+
+@pytest.mark.parametrize("R_,C_", TR_SHAPES)
+def test_transpose_is_numpy_transpose(O, R_, C_):
+    """oracle_transpose_u16 / _f32 (cpu_transpose.c:355-366's 2-D swap)
+    move every element bit for bit to [c][r]: arbitrary bit patterns
+    (NaN payloads included) against numpy's .T."""
+    rng = np.random.default_rng(R_ * 1000 + C_)
+    x16 = rng.integers(0, 1 << 16, (R_, C_), dtype=np.uint32).astype(np.uint16)
+    assert np.array_equal(O.transpose_u16(x16), x16.T)
+    x32 = rng.integers(0, 1 << 32, (R_, C_), dtype=np.uint64).astype(np.uint32)
+    got = O.transpose_f32(x32.view(np.float32))
+    assert np.array_equal(got.view(np.uint32), x32.T)
+
+
+@pytest.mark.parametrize("R_,C_", TR_SHAPES)
+def test_transpose_matches_reference_kernel(O, R, R_, C_):
+    """The same against the reference's own cpu_kernel_transpose on a 2-D
+    TRANSPOSE node (its default last-two-axes swap), 16-bit and f32."""
+    rng = np.random.default_rng(R_ * 7 + C_)
+    x16 = rng.integers(0, 1 << 16, (R_, C_), dtype=np.uint32).astype(np.uint16)
+    rc, ref = R.run("cpu_kernel_transpose", abi.OP_TRANSPOSE, [(abi.BF16, [R_, C_], x16)],
+                    abi.BF16, (C_, R_), np.uint16, threads=3)
+    assert rc == 0 and np.array_equal(O.transpose_u16(x16), ref)
+    x32 = rng.integers(0, 1 << 32, (R_, C_), dtype=np.uint64).astype(np.uint32).view(np.float32)
+    rc, ref = R.run("cpu_kernel_transpose", abi.OP_TRANSPOSE, [(abi.F32, [R_, C_], x32)],
+                    abi.F32, (C_, R_), np.float32, threads=3)
+    assert rc == 0
+    assert np.array_equal(O.transpose_f32(x32).view(np.uint32), ref.view(np.uint32))
+
+
 # ---------------------------------------------------------------- golden
 def test_golden_q8_quantize(O):
     qx = GOLD["quant_x"]
