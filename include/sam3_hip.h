@@ -335,11 +335,15 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 /*
  * sam3_hip_matmul for Q8_0 weights that allocates nothing: C[M,N] (F32) =
  * A[M,K] * W^T (+bias) (GELU), W[N,K] Q8_0 blocks along k (K % 32 == 0),
- * A F32, F16 or BF16, bias F32 [N]. The same kernels run as in
- * sam3_hip_matmul (same bits). The f16 copy of f32/bf16 activations goes
- * to a fixed scratch array of 48 MiB that the library keeps on each
- * device until the process ends; a problem needing more (M * K * 2 bytes
- * plus 4 per row) fails with SAM3_EINVAL before any launch. No hipMalloc,
+ * A F32, F16 or BF16, bias F32 [N]. It runs the kernels of
+ * sam3_hip_matmul with per-call weight expansion off (SAM3_HIP_Q8_EXPAND=0):
+ * the same bits as that setting; at the default setting sam3_hip_matmul
+ * expands large weights to f16 first, and the two agree within the f32
+ * tolerance. The f16 copy of f32/bf16 activations and the weight-row
+ * factors of the MFMA kernels go to a fixed scratch array of 48 MiB that
+ * the library keeps on each device until the process ends; a problem
+ * needing more (M * K * 2 bytes plus 4 per row, rounded up to 256, plus
+ * 4 * N) fails with SAM3_EINVAL before any launch. No hipMalloc,
  * hipFree or other allocation happens. Calls that overlap on one device
  * (from two threads or on two streams) share the array and race.
  * No counterpart in the reference: it is for callers that cannot

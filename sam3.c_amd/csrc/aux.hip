@@ -139,6 +139,24 @@ __global__ void __launch_bounds__(256) q8_wfac_kn_k(const char *blk, float *cs, 
 						  fmaxf(part[2][lane], part[3][lane]))));
 }
 
+/* Row tags of f16 operand writers (s3k_rowflag_check): one thread per
+ * row, over up to 32 tag arrays (blockIdx.y). */
+struct RowFlagSet {
+	unsigned *f[32];
+	int rows[32];
+};
+
+__global__ void __launch_bounds__(256) rowflag_check_k(RowFlagSet s, unsigned tag, unsigned *ovf)
+{
+	const int y = blockIdx.y;
+	const long long m = (long long)blockIdx.x * 256 + threadIdx.x;
+	if (m >= s.rows[y])
+		return;
+	const unsigned *f = s.f[y] + 2 * m;
+	if (f[1] == tag && f[0] != tag)
+		*ovf = tag;
+}
+
 /* One thread per output of f16 [N,K]; element (n,k) reads block lin/32
  * of the flat Q8 array, lin = k*N+n (KN) or n*K+k (NK, rows that split
  * blocks), and is stored as f16(q * (scale / cs[n])). */
@@ -493,6 +511,29 @@ using namespace s3k;
 static dim3 grid1(long long n)
 {
 	return dim3((unsigned)((n + 255) / 256));
+}
+
+extern "C" int s3k_rowflag_check(int n, unsigned *const *flags, const int *rows, unsigned tag,
+				 unsigned *ovf, void *stream)
+{
+	if (n <= 0)
+		return 0;
+	if (n > 32 || !ovf)
+		return (int)hipErrorInvalidValue;
+	RowFlagSet s = {};
+	int most = 0;
+	for (int i = 0; i < n; ++i) {
+		if (!flags[i] || rows[i] < 0)
+			return (int)hipErrorInvalidValue;
+		s.f[i] = flags[i];
+		s.rows[i] = rows[i];
+		most = rows[i] > most ? rows[i] : most;
+	}
+	if (most == 0)
+		return 0;
+	hipLaunchKernelGGL(rowflag_check_k, dim3((unsigned)((most + 255) / 256), (unsigned)n),
+			   dim3(256), 0, (hipStream_t)stream, s, tag, ovf);
+	return (int)hipGetLastError();
 }
 
 extern "C" int s3k_q8_wfactors(const void *blocks, float *cs, int K, int N, int nt, int batch,

@@ -522,6 +522,7 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 	p.cs_sb = g->cs_sb;
 	p.ovf = g->ovf;
 	p.ovf_tag = g->ovf_tag;
+	p.rowf = g->rowf;
 	p.M = g->M;
 	p.N = g->N;
 	p.K = g->K;

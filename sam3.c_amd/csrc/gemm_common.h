@@ -28,6 +28,7 @@ struct GemmArgs {
 	long long cs_sb;              /* ... per batch slice                    */
 	unsigned *ovf;                /* S3K_C_F16OP range flag (or NULL)       */
 	unsigned ovf_tag;
+	unsigned *rowf;               /* S3K_C_F16OP per-row tags (s3k_gemm)    */
 	int flags;
 	int c_kind;
 	int bias_kind;
@@ -130,21 +131,45 @@ __device__ __forceinline__ long long out_row(const GemmArgs &p, int m)
  * W = 4 for f32 C and 8 for 16-bit C (one 16-byte store either way).
  * EPI adds the bias and/or GELU (p.flags) with the reference's rounding
  * points; without it the values are only converted. */
-/* Whether f16 copies of these W values lose more than f16 rounding: an
- * |x| of 2^15 or more (finite), or nonzero values that all lie below
- * 2^-10 (a row made only of such runs would round to a few bits). */
+/* The f16 operand output's range checks. f16 copies lose more than f16
+ * rounding where |x| >= 2^15 (finite): f16_big, checked per value and
+ * flagged at once. A row whose nonzero values all lie below 2^-10 would
+ * round to a few bits too, but whether a row is such depends on all of
+ * it, which spans several workgroups: each writer reports the largest
+ * |x| of its part of a row (f16_row_tags). */
 template <int W>
-__device__ __forceinline__ bool f16_out_of_range(const float *x)
+__device__ __forceinline__ bool f16_big(const float *x)
 {
-	float mx = 0.0f;
+	bool big = false;
 #pragma unroll
 	for (int e = 0; e < W; ++e) {
 		const float a = __builtin_fabsf(x[e]);
-		if (a >= 32768.0f && a <= 3.402823466e38f)
-			return true;
-		mx = a > mx ? a : mx;
+		big |= a >= 32768.0f && a <= 3.402823466e38f;
 	}
-	return mx > 0.0f && mx < 0x1p-10f;
+	return big;
+}
+
+template <int W>
+__device__ __forceinline__ float f16_part_max(const float *x)
+{
+	float mx = 0.0f;
+#pragma unroll
+	for (int e = 0; e < W; ++e)
+		mx = fmaxf(mx, finite_abs(x[e]));
+	return mx;
+}
+
+/* Row m's tags (p.rowf, two words per row, the eval's tag p.ovf_tag):
+ * word 2m when a part of the row holds a value of |x| >= 2^-10, word
+ * 2m + 1 when a part holds nonzero values only below it. A row tagged
+ * in the second word and not in the first is tiny throughout
+ * (s3k_rowflag_check). Plain stores of the same value, in any order. */
+__device__ __forceinline__ void f16_row_tag(const GemmArgs &p, long long m, float mx)
+{
+	if (mx >= 0x1p-10f)
+		p.rowf[2 * m] = p.ovf_tag;
+	else if (mx > 0.0f)
+		p.rowf[2 * m + 1] = p.ovf_tag;
 }
 
 /* The global inputs of one output chunk's epilogue (C[m][n..n+W-1]):
@@ -221,9 +246,10 @@ __device__ __forceinline__ void epi_fetch(const GemmArgs &p, int m, int n, int b
 	}
 }
 
+/* Returns the largest finite |value| stored (S3K_C_F16OP; 0 otherwise). */
 template <int CK, bool EPI, int W>
-__device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, int m, int n,
-				       const float (&xv)[W], const EpiIn<W> &ein)
+__device__ __forceinline__ float finishw(const GemmArgs &p, int flags, char *cb, int m, int n,
+					const float (&xv)[W], const EpiIn<W> &ein)
 {
 	typedef float f4v __attribute__((ext_vector_type(4)));
 	typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -280,7 +306,7 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, 
 					c[e] = x[e];
 		}
 	} else {
-		if (CK == S3K_C_F16OP && p.ovf && f16_out_of_range<W>(x))
+		if (CK == S3K_C_F16OP && p.ovf && f16_big<W>(x))
 			*p.ovf = p.ovf_tag;
 		uint32_t h[W];
 #pragma unroll
@@ -301,6 +327,7 @@ __device__ __forceinline__ void finishw(const GemmArgs &p, int flags, char *cb, 
 					c[e] = (uint16_t)h[e];
 		}
 	}
+	return CK == S3K_C_F16OP ? f16_part_max<W>(x) : 0.0f;
 }
 
 template <bool B>
@@ -428,7 +455,10 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 	const bool light = !heavy && (flags & (S3K_EPI_BIAS | S3K_EPI_GELU));
 	/* the common cases (plain rows, whole 16-byte vectors, no residual,
 	 * a bias loaded once per tile): a store path whose flag tests are
-	 * made once per tile instead of once per element */
+	 * made once per tile instead of once per element. gemm_dlk's vmcnt
+	 * arithmetic relies on this path issuing exactly FM * UNITS / 64
+	 * stores per lane and no load for whole tiles (dlk_ok admits only
+	 * problems that take it). */
 	constexpr bool PLAIN_CK = CK == S3K_F32 || CK == S3K_BF16 || CK == S3K_F16;
 	const bool fast = PLAIN_CK && !(flags & S3K_EPI_RES) && (FIXED || !(flags & S3K_EPI_BIAS)) &&
 			  !p.rm_g && p.vec_ok && n0 + WTN <= p.N;
@@ -615,6 +645,23 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			fast_strips(epi_b<false>{}, epi_b<true>{});
 		return;
 	}
+	/* S3K_C_F16OP: the largest |value| of this wave's part of each row
+	 * (the WTN / W lanes holding the row's units in one round, when they
+	 * divide the round; else each unit on its own) as row tags. Every lane
+	 * calls it, so the shuffles see the whole wave. */
+	auto row_tags = [&](float mx, int row) {
+		constexpr int L = WTN / W;
+		if constexpr (FIXED) {
+#pragma unroll
+			for (int off = 1; off < L; off <<= 1)
+				mx = fmaxf(mx, __shfl_xor(mx, off));
+			if ((lane & (L - 1)) == 0 && row < p.M)
+				f16_row_tag(p, row, mx);
+		} else {
+			if (row < p.M)
+				f16_row_tag(p, row, mx);
+		}
+	};
 	/* The strip loop is rolled so that the store code exists once; the
 	 * staging of strip i picks acc[i] by a wave-uniform branch (the
 	 * accumulators stay in registers). */
@@ -635,11 +682,14 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 				if (s + 64 < UNITS)
 					staged(s + 64, nxt);
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
+				float mx = 0.0f;
 				if (mrow + row < p.M && n0 + cw < p.N) {
 					EpiIn<W> e = ein;
 					epi_fetch<W>(p, mrow + row, n0 + cw, bz, !FIXED, e);
-					finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, cur, e);
+					mx = finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, cur, e);
 				}
+				if (CK == S3K_C_F16OP && p.rowf)
+					row_tags(mx, mrow + row);
 #pragma unroll
 				for (int e = 0; e < W; ++e)
 					cur[e] = nxt[e];
@@ -658,12 +708,15 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 			for (int it = 0; it < IT; ++it) {
 				const int s = lane + 64 * it;
 				const int row = s / (WTN / W), cw = (s % (WTN / W)) * W;
+				float mx = 0.0f;
 				if (mrow + row < p.M && n0 + cw < p.N) {
 					if (light)
-						finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
+						mx = finishw<CK, true, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
 					else
-						finishw<CK, false, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
+						mx = finishw<CK, false, W>(p, flags, cb, mrow + row, n0 + cw, v[it], ein);
 				}
+				if (CK == S3K_C_F16OP && p.rowf)
+					row_tags(mx, mrow + row);
 			}
 		}
 		wave_lds_fence();

@@ -648,7 +648,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 
 /* gemm_dlk's conditions: K = 64, M and N multiples of 192, plain f32 or
  * same-kind 16-bit output with 16-byte rows, no epilogue flags, enough
- * tiles to keep every CU busy. */
+ * tiles to keep every CU busy. Its wait_vm<STORES> counts on every tile
+ * taking write_tile_ck's fast path with whole tiles: exactly STORES
+ * 16-byte stores per lane and no loads. The conditions here are the fast
+ * path's (p.vec_ok: 16-byte aligned C, ldc and stride_c multiples of 8;
+ * no bias, residual, row or column factors, row map or QKV stores; N a
+ * multiple of the wave tile); a change to either must keep them equal. */
 static bool dlk_ok(const struct s3k_gemm *g)
 {
 	return g->K == 64 && g->M % DLK_B == 0 && g->N % DLK_B == 0 &&

@@ -86,10 +86,15 @@ struct s3k_gemm {
 	const float *cs;
 	long long   cs_sb;
 	/* f16 operand output (S3K_C_F16OP): when ovf is set, a value the f16
-	 * copy cannot hold faithfully (|x| >= 2^15, or a run of 8 nonzero
-	 * values all below 2^-10) stores ovf_tag to *ovf */
+	 * copy cannot hold (|x| >= 2^15, finite) stores ovf_tag to *ovf; when
+	 * rowf is set, output row m's parts store ovf_tag to rowf[2m] if they
+	 * hold a value of |x| >= 2^-10 and to rowf[2m + 1] if their nonzero
+	 * values all lie below it, so that s3k_rowflag_check finds the rows
+	 * whose nonzero values are all below 2^-10 (their f16 copy would keep
+	 * only a few bits) */
 	unsigned   *ovf;
 	unsigned    ovf_tag;
+	unsigned   *rowf;
 	/* S3K_EPI_QKV: with E = qkv_H * qkv_D, output column n of row m is
 	 * element (b, s, h, d) = (m / qkv_S, m % qkv_S, (n % E) / qkv_D,
 	 * n % qkv_D) of operand y = n / E and is stored at qkv_out[y] +
@@ -229,6 +234,12 @@ int s3k_permute(int esize, const void *src, void *dst, int ndim, const int *in_d
  * and below 2^-10). */
 int s3k_permute_to(int fmt, const float *src, void *dst, int ndim, const int *in_dims,
 		   const int *axes, int K, unsigned *ovf, unsigned ovf_tag, void *stream);
+/* Stores tag to *ovf when some row of the n row-tag arrays flags[i]
+ * (2 * rows[i] words each, as struct s3k_gemm's rowf) holds tag in its
+ * second word and not in its first: a row whose nonzero values are all
+ * below 2^-10. n <= 32 per call. */
+int s3k_rowflag_check(int n, unsigned *const *flags, const int *rows, unsigned tag, unsigned *ovf,
+		      void *stream);
 /* Whether the skinny launch of g rounds its f32 / bf16 activations to f16
  * with per-row power-of-two factors inside the kernel (no row-scaled f16
  * copy needed first). */

@@ -115,6 +115,11 @@ struct sam3_hip_backend {
 	unsigned ovf_tag;
 	int f16_writes;
 	int no_f16_ops;
+	/* the row tags of this eval's GEMM-written f16 operands (struct
+	 * s3k_gemm rowf), checked together before the flag is read */
+	unsigned *rowf[32];
+	int rowf_rows[32];
+	int n_rowf;
 };
 
 /* ------------------------------------------------------------------ */
@@ -389,14 +394,32 @@ static enum sam3_error dev_out(struct sam3_hip_backend *hb, const struct sam3_te
 
 /* A device buffer of nbytes for output t holding the operand form fmt of
  * the one GEMM that reads it: never downloaded, stale after the eval. */
+/* The row tags collected so far: rows whose nonzero values were all
+ * below 2^-10 set the range flag (s3k_rowflag_check). */
+static enum sam3_error rowf_flush(struct sam3_hip_backend *hb)
+{
+	enum sam3_error err = SAM3_OK;
+	if (hb->n_rowf)
+		err = s3h_hip(s3k_rowflag_check(hb->n_rowf, hb->rowf, hb->rowf_rows, hb->ovf_tag,
+						hb->ovf, hb->stream),
+			      "graph_eval: row tag check");
+	hb->n_rowf = 0;
+	return err;
+}
+
+/* *same (when not NULL): the allocation held this operand form before
+ * (not new, not another form), so words past the data keep their
+ * contents from earlier evals of this form. */
 static enum sam3_error dev_out_fmt(struct sam3_hip_backend *hb, const struct sam3_tensor *t,
-				   size_t nbytes, int fmt, void **out)
+				   size_t nbytes, int fmt, void **out, int *same)
 {
 	struct s3h_res *e = res_find(hb, t->data);
 	if (e && e->cap < nbytes) {
 		res_drop_at(hb, (int)(e - hb->res));
 		e = NULL;
 	}
+	if (same)
+		*same = e && e->fmt == fmt;
 	if (!e) {
 		enum sam3_error err = res_new(hb, t, nbytes, &e);
 		if (err != SAM3_OK)
@@ -849,20 +872,40 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 				n_chain += qcs[y].n;
 			}
 	} else if (o_fmt != S3H_A_PLAIN) {
-		err = dev_out_fmt(hb, out, (size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2), o_fmt, &dc);
+		/* an f16 operand carries its row tags (two words per row) after
+		 * the data: zeroed when the allocation is new to this form, then
+		 * stamped with each eval's own tag */
+		const size_t dbytes = ((size_t)M * N * (o_fmt == S3H_A_PLANES ? 6 : 2) + 15) & ~(size_t)15;
+		const int f16 = o_fmt == S3H_A_F16;
+		int same = 0;
+		unsigned *rowf = NULL;
+		err = dev_out_fmt(hb, out, dbytes + (f16 ? (size_t)M * 8 : 0), o_fmt, &dc, &same);
+		if (err == SAM3_OK && f16) {
+			rowf = (unsigned *)((char *)dc + dbytes);
+			if (!same)
+				err = s3h_hip(hipMemsetAsync(rowf, 0, (size_t)M * 8, hb->stream),
+					      "graph_eval: row tags");
+			if (err == SAM3_OK && hb->n_rowf == 32)
+				err = rowf_flush(hb);
+		}
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, o_fmt, a_dt, da, b_dt, db, dc, M, N, K, dbias,
-						dres, NULL, flags, hb->ovf, hb->ovf_tag, hb->stream);
+						dres, NULL, flags, hb->ovf, hb->ovf_tag, rowf,
+						hb->stream);
 		if (err == SAM3_OK) {
 			hb->stats.operand_writes++;
-			hb->f16_writes += o_fmt == S3H_A_F16;
+			hb->f16_writes += f16;
+			if (f16) {
+				hb->rowf[hb->n_rowf] = rowf;
+				hb->rowf_rows[hb->n_rowf++] = M;
+			}
 		}
 	} else if (dres || row_map[0]) {
 		err = dev_out(hb, out, &dc);
 		if (err == SAM3_OK)
 			err = s3h_matmul_fmt_to(a_fmt, S3H_A_PLAIN, a_dt, da, b_dt, db, dc, M, N, K,
 						dbias, dres, row_map[0] ? row_map : NULL, flags, NULL,
-						0, hb->stream);
+						0, NULL, hb->stream);
 		if (err == SAM3_OK)
 			for (int k = 0; k < n_chain; k++)
 				done[chain[k]] = 1;
@@ -1133,7 +1176,8 @@ static enum sam3_error run_permute_as(struct sam3_hip_backend *hb, const struct 
 	enum sam3_error err = dev_in(hb, n->inputs[0], &dx);
 	if (err == SAM3_OK)
 		err = dev_out_fmt(hb, n->output,
-				  (size_t)s3h_nelems(n->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
+				  (size_t)s3h_nelems(n->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy,
+				  NULL);
 	if (err == SAM3_OK)
 		err = s3h_transpose_to(n, dx, dy, fmt, K, hb->ovf, hb->ovf_tag, hb->stream);
 	if (err == SAM3_OK) {
@@ -1208,7 +1252,8 @@ static enum sam3_error run_layernorm_map(struct sam3_hip_backend *hb, const stru
 	if (err == SAM3_OK && n->n_inputs > 2 && n->inputs[2])
 		err = dev_in(hb, n->inputs[2], &db);
 	if (err == SAM3_OK)
-		err = dev_out_fmt(hb, t, (size_t)rows * cols * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
+		err = dev_out_fmt(hb, t, (size_t)rows * cols * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy,
+				  NULL);
 	if (err == SAM3_OK)
 		err = s3h_hip(s3k_layernorm_to_map(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
 						   (const float *)dx, (const float *)dg,
@@ -1238,7 +1283,7 @@ static enum sam3_error run_layernorm_as(struct sam3_hip_backend *hb, const struc
 		err = dev_in(hb, n->inputs[2], &db);
 	if (err == SAM3_OK)
 		err = dev_out_fmt(hb, n->output, (size_t)rows * cols * (fmt == S3H_A_PLANES ? 6 : 2),
-				  fmt, &dy);
+				  fmt, &dy, NULL);
 	if (err == SAM3_OK)
 		err = s3h_hip(s3k_layernorm_to(fmt == S3H_A_PLANES ? S3K_LN_PLANES : S3K_LN_F16,
 					       (const float *)dx, (const float *)dg,
@@ -1444,7 +1489,8 @@ static enum sam3_error run_sdpa_merged(struct sam3_hip_backend *hb, const struct
 		err = dev_out(hb, t->output, &dy);
 	else
 		err = dev_out_fmt(hb, t->output,
-				  (size_t)s3h_nelems(t->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy);
+				  (size_t)s3h_nelems(t->output) * (fmt == S3H_A_PLANES ? 6 : 2), fmt, &dy,
+				  NULL);
 	if (err == SAM3_OK)
 		err = s3h_sdpa_merged(&dn, dy, fmt, hb->ovf, hb->ovf_tag, hb->stream);
 	if (err == SAM3_OK) {
@@ -1629,10 +1675,16 @@ static enum sam3_error hip_graph_eval(struct sam3_backend *be, struct sam3_graph
 	s3h_cur = hb;
 	hb->no_f16_ops = 0;
 	hb->f16_writes = 0;
+	hb->n_rowf = 0;
 	hb->ovf_tag = hb->ovf_tag + 1 ? hb->ovf_tag + 1 : 1;
 	err = run_nodes(hb, g, &uses, folded, done);
+	if (err == SAM3_OK)
+		err = rowf_flush(hb);
+	hb->n_rowf = 0;
 	/* A fused producer that wrote an f16 GEMM operand flags values the
-	 * f16 copy cannot hold (|x| >= 2^15, or runs of tiny values). Then
+	 * f16 copy cannot hold (|x| >= 2^15, or rows of tiny values: per row
+	 * for LayerNorm and the GEMM epilogue, per four values for the
+	 * permute and the attention kernel's merged heads). Then
 	 * the graph runs again without f16 operand forms: the consumers read
 	 * f32 and make their row-scaled f16 copy themselves. The graph's
 	 * inputs are unchanged by the first run (nodes write only their own

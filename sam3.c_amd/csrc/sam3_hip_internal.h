@@ -106,7 +106,7 @@ int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
 				  const void *res, const int *row_map, int flags, unsigned *ovf,
-				  unsigned ovf_tag, void *stream);
+				  unsigned ovf_tag, unsigned *rowf, void *stream);
 /* The attention operands of a fused qkv projection: the f32 result
  * [B*S, n_out*H*D] stored as n_out head-split tensors out[y] [B, H, S, D]
  * (columns y*H*D onward), RoPE (cos / sin [S, D/2]) applied to operand y

@@ -1008,7 +1008,7 @@ int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *a, int b_dt,
 				  const void *b, void *c, int M, int N, int K, const void *bias,
 				  const void *res, const int *row_map, int flags, unsigned *ovf,
-				  unsigned ovf_tag, void *stream)
+				  unsigned ovf_tag, unsigned *rowf, void *stream)
 {
 	const int fits = out_fmt == S3H_A_PLAIN && !row_map
 				 ? s3h_matmul_res_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags)
@@ -1026,6 +1026,7 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 	if (out_fmt == S3H_A_F16) {
 		g.ovf = ovf;
 		g.ovf_tag = ovf_tag;
+		g.rowf = ovf ? rowf : NULL;
 	}
 	if (res) {
 		g.res = res;

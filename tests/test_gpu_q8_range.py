@@ -213,3 +213,48 @@ def test_graph_gemm_operand_out_of_range_reruns():
     y, ref, st = run(b1_big)
     assert st.range_reruns == 1, "the f16 operand overflow was not caught"
     assert_rows_close(y, ref, what="fc1 bias 1e5")
+
+
+def test_graph_gemm_operand_tiny_parts_of_rows_do_not_rerun():
+    """fc1 + GELU writing fc2's f16 operand (gh_mlp with Q8_0 weights):
+    strongly negative pre-activations give GELU outputs of ~1e-9. When
+    such runs are only parts of a row (every other group of 8 columns
+    here), the row's f16 copy keeps its bits where they matter, so the
+    eval is not redone (the GEMM epilogue tags rows, and only a row whose
+    nonzero values are all below 2^-10 sets the flag). When whole rows
+    are that small (every column), the eval is redone on f32. Both match
+    the oracle."""
+    O = oracle()
+    M, K, H, N = 512, 256, 1024, 256
+    x = synth.randn(370, (M, K))
+    gamma, beta = synth.randn(375, (K,)), synth.randn(376, (K,), 0.1)
+    w1 = O.q8_quantize(synth.randn(371, (H, K), 0.05))
+    w2 = O.q8_quantize(synth.randn(372, (N, H), 0.02))
+    b2 = synth.randn(374, (N,), 0.02)
+    ln = O.layernorm(x, gamma, beta)
+
+    def run(b1):
+        G = graph.Graph()
+        t = G.layernorm(G.tensor(abi.F32, (M, K), x), G.tensor(abi.F32, (K,), gamma),
+                        G.tensor(abi.F32, (K,), beta))
+        y = G.mlp(t, G.tensor(abi.Q8_0, (H, K), w1), G.tensor(abi.F32, (H,), b1),
+                  G.tensor(abi.Q8_0, (N, H), w2), G.tensor(abi.F32, (N,), b2))
+        be = hip.Backend(0)
+        try:
+            assert be.graph_eval(G.g) == abi.OK
+            st = be.stats()
+        finally:
+            be.close()
+        h_ref = ref_q8(ln, w1, K, H, nt=True, bias=b1, gelu=True)
+        return _out(y, (M, N)), ref_q8(h_ref, w2, H, N, nt=True, bias=b2), st
+
+    b1 = synth.randn(373, (H,), 0.1)
+    half = b1.copy()
+    half[(np.arange(H) // 8) % 2 == 0] = np.float32(-6.0)
+    y, ref, st = run(half)
+    assert st.operand_writes >= 2
+    assert st.range_reruns == 0, "tiny parts of rows made the eval run again"
+    assert_rows_close(y, ref, what="half the columns tiny")
+    y, ref, st = run(np.full(H, -6.0, np.float32))
+    assert st.range_reruns == 1, "rows of only tiny values were not caught"
+    assert_rows_close(y, ref, what="whole rows tiny")

@@ -94,3 +94,80 @@ def test_noalloc_rejects_oversize_before_launch():
     # K not whole Q8_0 blocks
     assert lib.sam3_hip_matmul_q8_noalloc(abi.F32, da.ptr, dw.ptr, dc.ptr, 4, 4, 48, None, 0,
                                           None) == abi.EINVAL
+
+
+class _Graph:
+    """Stream capture into a HIP graph through the HIP runtime the library
+    loaded (hipStreamBeginCapture / EndCapture / GraphInstantiate)."""
+
+    def __init__(self, stream, record):
+        import ctypes as C
+        self.rt = rt = C.CDLL("libamdhip64.so.7")
+        vp = C.c_void_p
+        rt.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        rt.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+        rt.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, vp, C.c_size_t]
+        rt.hipGraphLaunch.argtypes = [vp, vp]
+        rt.hipGraphExecDestroy.argtypes = [vp]
+        rt.hipGraphDestroy.argtypes = [vp]
+        self.stream, self.graph, self.exec = stream, C.c_void_p(), C.c_void_p()
+        assert rt.hipStreamBeginCapture(stream, 2) == 0
+        try:
+            record()
+        finally:
+            assert rt.hipStreamEndCapture(stream, C.byref(self.graph)) == 0
+        assert rt.hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0) == 0
+
+    def launch(self):
+        assert self.rt.hipGraphLaunch(self.exec, self.stream) == 0
+
+    def close(self):
+        self.rt.hipGraphExecDestroy(self.exec)
+        self.rt.hipGraphDestroy(self.graph)
+
+
+@pytest.mark.parametrize("M", [300, 77], ids=["mfma", "skinny"])
+def test_noalloc_captured_in_a_hip_graph(M):
+    """The entry point's callers run it under HIP graph capture: after one
+    eager call (which looks the scratch array up), the call is captured on
+    a stream and the graph replayed three times, with eager calls of
+    another problem in between that overwrite the shared array. Every
+    replay must give the eager call's bits."""
+    import ctypes as C
+    O = oracle()
+    lib = hip.load()
+    N, K = 512, 1024
+    a = synth.randn(620 + M, (M, K))
+    w = O.q8_quantize(synth.randn(621, (N, K), 0.02))
+    bias = synth.randn(622, N, 0.01)
+    da, dw, db = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(w), hip.DeviceBuffer.of(bias)
+    c_eager, c_graph = hip.DeviceBuffer(M * N * 4), hip.DeviceBuffer(M * N * 4)
+    flags = hip.BIAS | hip.GELU
+    hip.check(lib.sam3_hip_matmul_q8_noalloc(abi.F32, da.ptr, dw.ptr, c_eager.ptr, M, N, K, db.ptr,
+                                             flags, None), "eager")
+    hip.synchronize()
+    want = c_eager.download(np.float32, (M, N))
+    # other work sharing the array between replays
+    a2 = synth.randn(623, (64, K)) * np.float32(1e5)
+    da2, dc2 = hip.DeviceBuffer.of(a2), hip.DeviceBuffer(64 * N * 4)
+    sp = C.c_void_p()
+    hip.check(lib.sam3_hip_stream_create(C.byref(sp)), "stream")
+    g = _Graph(sp.value, lambda: hip.check(
+        lib.sam3_hip_matmul_q8_noalloc(abi.F32, da.ptr, dw.ptr, c_graph.ptr, M, N, K, db.ptr,
+                                       flags, sp.value), "captured"))
+    try:
+        for rep in range(3):
+            hip.check(lib.sam3_hip_matmul_q8_noalloc(abi.F32, da2.ptr, dw.ptr, dc2.ptr, 64, N, K,
+                                                     None, 0, None), "between")
+            hip.synchronize()
+            hip.check(lib.sam3_hip_memcpy_h2d(c_graph.ptr, np.zeros(M * N, np.float32).ctypes.data,
+                                              M * N * 4), "clear")
+            g.launch()
+            hip.check(lib.sam3_hip_stream_synchronize(sp.value), "replay")
+            got = c_graph.download(np.float32, (M, N))
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+    finally:
+        g.close()
+        hip.check(lib.sam3_hip_stream_destroy(sp.value), "stream")
+    assert_f32_close(want, ref_q8(a, w, K, N, nt=True, bias=bias, gelu=True),
+                     what="noalloc bias gelu")
