@@ -492,8 +492,6 @@ static bool mfma_ok(const struct s3k_gemm *g)
 	return true;
 }
 
-extern "C" int s3k_skinny_ok(const struct s3k_gemm *g);
-
 extern "C" int s3k_gemm_path(const struct s3k_gemm *g)
 {
 	if (g->M <= 0 || g->N <= 0 || g->K < 0 || g->batch <= 0)
@@ -709,6 +707,9 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	 * them (the skinny and generic kernels keep q*scale in f32) */
 	if ((g->flags & S3K_EPI_COLSCALE) ? (path != S3K_PATH_MFMA || !g->cs)
 					  : (path == S3K_PATH_MFMA && g->b_kind == S3K_Q8))
+		return (int)hipErrorInvalidValue;
+	/* a LayerNorm's input rows as A: the streaming skinny kernel only */
+	if ((g->flags & S3K_A_LN) && path != S3K_PATH_SKINNY)
 		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))

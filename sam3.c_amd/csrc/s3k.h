@@ -42,6 +42,10 @@ enum s3k_kind {
 #define S3K_EPI_QKV 32  /* f32 out, batch 1, direct-to-LDS GEMM only: the
 			 * result is stored as the head-split attention
 			 * operands (struct s3k_gemm, qkv_*) instead of C */
+#define S3K_A_LN    128 /* A holds a LayerNorm's f32 input rows: the kernel
+			  * normalizes each row (eps 1e-5, gamma ln_g, beta
+			  * ln_b, either NULL) with the LayerNorm kernel's
+			  * arithmetic before use (q8_stream only) */
 #define S3K_EPI_COLSCALE 64 /* out = acc * cs[n] first (with the row factor):
 			     * the weight-row factors of a Q8_0 weight
 			     * (s3k_q8_wfactors). Kernels that round q*scale
@@ -85,6 +89,8 @@ struct s3k_gemm {
 	 * two, cs[b * cs_sb + n] for batch slice b */
 	const float *cs;
 	long long   cs_sb;
+	/* S3K_A_LN: LayerNorm gamma and beta, f32 [K], 16-byte aligned */
+	const float *ln_g, *ln_b;
 	/* f16 operand output (S3K_C_F16OP): when ovf is set, a value the f16
 	 * copy cannot hold (|x| >= 2^15, finite) stores ovf_tag to *ovf; when
 	 * rowf is set, output row m's parts store ovf_tag to rowf[2m] if they
@@ -244,6 +250,9 @@ int s3k_rowflag_check(int n, unsigned *const *flags, const int *rows, unsigned t
  * with per-row power-of-two factors inside the kernel (no row-scaled f16
  * copy needed first). */
 int s3k_skinny_scales_rows(const struct s3k_gemm *g);
+/* Whether the skinny kernels take g as it is (shape, kinds, alignment,
+ * and for S3K_A_LN the streaming kernel's conditions). */
+int s3k_skinny_ok(const struct s3k_gemm *g);
 /* Attention operands [B, H, S, D] (f32), up to three (n_out) in one
  * launch: out[y] from columns col0[y].. of rows of `pitch` values holding
  * [B*S, H*D] (the q, k or v part of a fused qkv output), with RoPE
@@ -321,7 +330,7 @@ struct s3h_settings {
 	int q8_batch_path;                /* SAM3_HIP_Q8_BATCH_PATH: 0, 1, 2     */
 	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
 	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
-	    permute_operand, partition_fold, qkv_fold, sdpa_merge;
+	    permute_operand, partition_fold, qkv_fold, sdpa_merge, ln_gemv_fold;
 	int readback_all;                 /* SAM3_HIP_READBACK=all               */
 	int quiet;                        /* SAM3_HIP_QUIET set                  */
 	int arena_mb;                     /* SAM3_HIP_ARENA_MB (0 = default)     */

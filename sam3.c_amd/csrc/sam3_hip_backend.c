@@ -68,6 +68,9 @@ struct s3h_res {
 	unsigned char fmt;       /* S3H_A_*: the device copy holds a GEMM
 				  * operand form, not the tensor's dtype    */
 	unsigned char fresh;     /* uploaded from the host in this eval      */
+	const void *ln[3];       /* fmt S3H_A_LN: the LayerNorm's input,
+				  * gamma and beta on the device (the
+				  * consuming GEMM normalizes as it reads) */
 };
 
 /* A prepared copy of a constant weight (s3h_prep_*). */
@@ -723,7 +726,16 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	void *da, *db, *dc, *dbias = NULL, *dres = NULL;
 	const struct s3h_res *ae = res_find(hb, a->data);
 	const int a_fmt = ae ? ae->fmt : S3H_A_PLAIN;
+	struct s3h_ln_in ln_a = {NULL, NULL, NULL};
 	enum sam3_error err = dev_in(hb, a, &da);
+	if (err == SAM3_OK && a_fmt == S3H_A_LN) {
+		/* A is a LayerNorm's output that did not run: the GEMM reads
+		 * the LN's input and normalizes it (ln_gemv_form) */
+		ln_a.x = ae->ln[0];
+		ln_a.gamma = ae->ln[1];
+		ln_a.beta = ae->ln[2];
+		da = &ln_a;
+	}
 	if (err == SAM3_OK)
 		err = dev_in(hb, bsrc, &db);
 	if (err == SAM3_OK && bias)
@@ -926,6 +938,70 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	return err;
 }
 
+/* The MATMUL that reads tensor t, produced by node i (or by the chain of
+ * nodes folded into it, the last of them before node j), as its A: t
+ * used once, through RESHAPE views only. Fills r (the MATMUL's index, its
+ * A view, the weight tensor it uses - the source of a folded TRANSPOSE
+ * when its B is one, then nt = 1 - and the GEMM's M, N, K). */
+struct gemm_reader {
+	int j, nt, M, N, K;
+	const struct sam3_tensor *a, *w;
+};
+static int find_gemm_reader(const struct sam3_graph *g, int i, int j, const struct sam3_tensor *t,
+			    struct use_map *uses, struct gemm_reader *r)
+{
+	for (;;) {
+		if (uses_of(uses, t) != 1)
+			return 0;
+		while (j < g->n_nodes) {
+			const struct sam3_node *m = &g->nodes[j];
+			int hit = 0;
+			for (int k = 0; k < m->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++)
+				hit |= m->inputs[k] == t;
+			if (hit)
+				break;
+			j++;
+		}
+		if (j >= g->n_nodes)
+			return 0;
+		if (g->nodes[j].op != SAM3_OP_RESHAPE || g->nodes[j].inputs[0] != t)
+			break;
+		t = g->nodes[j].output;
+		j++;
+	}
+	const struct sam3_node *mm = &g->nodes[j];
+	if (mm->op != SAM3_OP_MATMUL || mm->n_inputs < 2 || mm->inputs[0] != t || !mm->inputs[1] ||
+	    !mm->output)
+		return 0;
+	const struct sam3_tensor *b = mm->inputs[1], *w = NULL;
+	for (int k = i + 1; k < j && !w; k++)
+		if (g->nodes[k].op == SAM3_OP_TRANSPOSE && g->nodes[k].output == b &&
+		    transpose_folds(g, k, uses))
+			w = g->nodes[k].inputs[0];
+	const struct sam3_tensor *bsrc = w ? w : b;
+	if (!bsrc->data || t->n_dims < 1)
+		return 0;
+	const int M = t->n_dims >= 2 ? t->dims[t->n_dims - 2] : 1, K = t->dims[t->n_dims - 1];
+	int N, kb;
+	if (w) {
+		N = w->dims[0];
+		kb = w->dims[1];
+	} else {
+		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
+		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
+	}
+	if (kb != K || s3h_nelems(t) != (long long)M * K)
+		return 0;
+	r->j = j;
+	r->a = t;
+	r->w = bsrc;
+	r->nt = w != NULL;
+	r->M = M;
+	r->N = N;
+	r->K = K;
+	return 1;
+}
+
 /* The GEMM operand form in which tensor t, produced by node i (or by the
  * chain of nodes folded into it, the last of them before node j), can be
  * written: t must be used once, through RESHAPE views only, as the A of a
@@ -937,56 +1013,17 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 				 int j, const struct sam3_tensor *t, int row_len,
 				 struct use_map *uses, int *k_out)
 {
-	for (;;) {
-		if (uses_of(uses, t) != 1)
-			return S3H_A_PLAIN;
-		while (j < g->n_nodes) {
-			const struct sam3_node *m = &g->nodes[j];
-			int hit = 0;
-			for (int k = 0; k < m->n_inputs && k < SAM3_NODE_MAX_INPUTS; k++)
-				hit |= m->inputs[k] == t;
-			if (hit)
-				break;
-			j++;
-		}
-		if (j >= g->n_nodes)
-			return S3H_A_PLAIN;
-		if (g->nodes[j].op != SAM3_OP_RESHAPE || g->nodes[j].inputs[0] != t)
-			break;
-		t = g->nodes[j].output;
-		j++;
-	}
-	const struct sam3_node *mm = &g->nodes[j];
-	if (mm->op != SAM3_OP_MATMUL || mm->n_inputs < 2 || mm->inputs[0] != t || !mm->inputs[1] ||
-	    !mm->output)
-		return S3H_A_PLAIN;
-	const struct sam3_tensor *b = mm->inputs[1], *w = NULL;
-	for (int k = i + 1; k < j && !w; k++)
-		if (g->nodes[k].op == SAM3_OP_TRANSPOSE && g->nodes[k].output == b &&
-		    transpose_folds(g, k, uses))
-			w = g->nodes[k].inputs[0];
-	const struct sam3_tensor *bsrc = w ? w : b;
-	if (!bsrc->data || t->n_dims < 1)
-		return S3H_A_PLAIN;
-	const int M = t->n_dims >= 2 ? t->dims[t->n_dims - 2] : 1, K = t->dims[t->n_dims - 1];
-	int N, kb;
-	if (w) {
-		N = w->dims[0];
-		kb = w->dims[1];
-	} else {
-		kb = b->n_dims >= 2 ? b->dims[b->n_dims - 2] : b->dims[0];
-		N = b->n_dims >= 2 ? b->dims[b->n_dims - 1] : 1;
-	}
-	if (kb != K || s3h_nelems(t) != (long long)M * K || (row_len > 0 && K != row_len))
+	struct gemm_reader r;
+	if (!find_gemm_reader(g, i, j, t, uses, &r) || (row_len > 0 && r.K != row_len))
 		return S3H_A_PLAIN;
 	if (k_out)
-		*k_out = K;
+		*k_out = r.K;
 	void *db = NULL;
-	if (dev_in(hb, bsrc, &db) != SAM3_OK)
+	if (dev_in(hb, r.w, &db) != SAM3_OK)
 		return S3H_A_PLAIN;
 	static const char aligned_a[16] __attribute__((aligned(16)));
-	const int f = s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, bsrc->dtype, db, SAM3_DTYPE_F32,
-					  M, N, K, w ? SAM3_HIP_B_NT : 0);
+	const int f = s3h_matmul_a_format(SAM3_DTYPE_F32, aligned_a, r.w->dtype, db, SAM3_DTYPE_F32,
+					  r.M, r.N, r.K, r.nt ? SAM3_HIP_B_NT : 0);
 	return f == S3H_A_F16 && hb->no_f16_ops ? S3H_A_PLAIN : f;
 }
 
@@ -999,6 +1036,75 @@ static int ln_operand_form(struct sam3_hip_backend *hb, const struct sam3_graph 
 		return S3H_A_PLAIN;
 	return consumer_operand_form(hb, g, i, i + 1, n->output,
 				     n->inputs[0]->dims[n->inputs[0]->n_dims - 1], uses, NULL);
+}
+
+/* Whether a node after node i writes tensor r's data. */
+static int written_after(const struct sam3_graph *g, int i, const struct sam3_tensor *r)
+{
+	if (!r)
+		return 0;
+	for (int k = i + 1; k < g->n_nodes; k++) {
+		const struct sam3_tensor *o = g->nodes[k].output;
+		if (o && (o == r || (o->data && o->data == r->data)))
+			return 1;
+	}
+	return 0;
+}
+
+/* An f32 LAYERNORM at node i whose output only a Q8_0 GEMM on the
+ * streaming skinny kernel reads (through RESHAPE views): the LN does not
+ * run; the GEMM normalizes its rows as it reads the LN's input
+ * (S3H_A_LN, the same arithmetic, so the same bits). No later node may
+ * write the LN's input, gamma or beta, which the GEMM reads when it runs.
+ * Fills ln with their device addresses. */
+static int ln_gemv_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			struct use_map *uses, struct s3h_ln_in *ln)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (!s3h_settings()->ln_gemv_fold || n->inputs[0]->dtype != SAM3_DTYPE_F32 ||
+	    !s3h_layernorm_ok(n))
+		return 0;
+	const struct sam3_tensor *x = n->inputs[0];
+	const struct sam3_tensor *gm = n->n_inputs > 1 ? n->inputs[1] : NULL;
+	const struct sam3_tensor *bt = n->n_inputs > 2 ? n->inputs[2] : NULL;
+	struct gemm_reader r;
+	if (!find_gemm_reader(g, i, i + 1, n->output, uses, &r) || !r.nt ||
+	    r.w->dtype != SAM3_DTYPE_Q8_0 || r.K != x->dims[x->n_dims - 1] ||
+	    (long long)r.M * r.K != s3h_nelems(x) || !x->data || written_after(g, i, x) ||
+	    written_after(g, i, gm) || written_after(g, i, bt))
+		return 0;
+	const struct s3h_res *xe = res_find(hb, x->data);
+	if (xe && xe->fmt)
+		return 0;
+	void *dx = NULL, *dg = NULL, *dbt = NULL, *dw = NULL;
+	if (dev_in(hb, x, &dx) != SAM3_OK || (gm && dev_in(hb, gm, &dg) != SAM3_OK) ||
+	    (bt && dev_in(hb, bt, &dbt) != SAM3_OK) || dev_in(hb, r.w, &dw) != SAM3_OK)
+		return 0;
+	ln->x = dx;
+	ln->gamma = dg;
+	ln->beta = dbt;
+	return s3h_matmul_ln_ok(r.w->dtype, dw, r.M, r.N, r.K, SAM3_HIP_B_NT, ln);
+}
+
+/* LAYERNORM left to its consuming GEMM: the output's residency entry
+ * holds the form S3H_A_LN and the device addresses in ln. */
+static enum sam3_error run_layernorm_gemv(struct sam3_hip_backend *hb, const struct sam3_node *n,
+					  const struct s3h_ln_in *ln)
+{
+	void *dy = NULL;
+	enum sam3_error err = dev_out_fmt(hb, n->output, 256, S3H_A_LN, &dy, NULL);
+	if (err != SAM3_OK)
+		return err;
+	struct s3h_res *e = res_find(hb, n->output->data);
+	if (!e) {
+		s3h_error("graph_eval: LayerNorm output not resident");
+		return SAM3_EBACKEND;
+	}
+	e->ln[0] = ln->x;
+	e->ln[1] = ln->gamma;
+	e->ln[2] = ln->beta;
+	hb->stats.fused_nodes++;
+	return SAM3_OK;
 }
 
 /* The form an f32 TRANSPOSE at node i that keeps its last axis writes:
@@ -1586,6 +1692,7 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 	const int part_plain = !set->partition_fold;
 	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
 	const struct sam3_tensor *lt = NULL;
+	struct s3h_ln_in lng;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -1607,6 +1714,8 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 		} else if ((n->op == SAM3_OP_CONV2D && s3h_conv2d_ok(n)) ||
 			   (n->op == SAM3_OP_CONV_TRANSPOSE2D && s3h_conv_transpose2d_ok(n))) {
 			err = run_conv(hb, g, i, &uses, &used);
+		} else if (n->op == SAM3_OP_LAYERNORM && ln_gemv_form(hb, g, i, &uses, &lng)) {
+			err = run_layernorm_gemv(hb, n, &lng);
 		} else if (n->op == SAM3_OP_LAYERNORM && !ln_plain && !part_plain &&
 			   (ln_fmt = ln_partition_form(hb, g, i, &uses, lrm, lchain, &lnc, &lt)) !=
 				   S3H_A_PLAIN) {

@@ -85,7 +85,19 @@ enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
  * producing A can write that form directly: S3H_A_PLANES = bf16 [M, 3K]
  * [hi|lo|hi] (the split f32 GEMM), S3H_A_F16 = f16 [M, K] (the Q8 GEMM
  * with f32 activations). s3h_matmul_fmt runs the GEMM on A in that form. */
-enum { S3H_A_PLAIN = 0, S3H_A_PLANES = 1, S3H_A_F16 = 2 };
+enum { S3H_A_PLAIN = 0, S3H_A_PLANES = 1, S3H_A_F16 = 2, S3H_A_LN = 3 };
+/* S3H_A_LN: A is the output of a LayerNorm that did not run; the skinny
+ * Q8_0 GEMM normalizes its input rows itself (S3K_A_LN). With this form
+ * the `a` argument of the s3h_matmul_* functions points to this host
+ * struct of device pointers (gamma, beta may be NULL). */
+struct s3h_ln_in {
+	const float *x, *gamma, *beta;
+};
+/* Whether a Q8_0 GEMM (b on the device) can read A as the LayerNorm
+ * input ln (f32 [M, K] rows): the streaming skinny kernel with
+ * S3K_A_LN, the normalization bit-identical to the LayerNorm kernel's. */
+int s3h_matmul_ln_ok(int b_dt, const void *b, int M, int N, int K, int flags,
+		     const struct s3h_ln_in *ln);
 int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
 			int K, int flags);
 enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, const void *b,

@@ -873,6 +873,37 @@ static enum sam3_error matmul_impl(int path, int a_dt, const void *a, int b_dt, 
  * write this form (s3h_matmul_a_format): their range flag makes
  * graph_eval wait for the GPU at its end, which costs a skinny chain more
  * than the row copy it saves. */
+/* g reads A as the LayerNorm input ln (S3K_A_LN). */
+static void use_ln_input(struct s3k_gemm *g, const struct s3h_ln_in *ln)
+{
+	g->a = ln->x;
+	g->a_kind = S3K_F32;
+	g->lda = g->K;
+	g->flags |= S3K_A_LN;
+	g->ln_g = ln->gamma;
+	g->ln_b = ln->beta;
+}
+
+/* The skinny launch takes g with its A as a LayerNorm's input. */
+static int skinny_takes_ln(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && g->batch == 1 && s3k_gemm_path(g) == S3K_PATH_SKINNY &&
+	       s3k_skinny_ok(g);
+}
+
+int s3h_matmul_ln_ok(int b_dt, const void *b, int M, int N, int K, int flags,
+		     const struct s3h_ln_in *ln)
+{
+	if (b_dt != SAM3_DTYPE_Q8_0 || !(flags & SAM3_HIP_B_NT) || !ln || !ln->x || !b || M <= 0 ||
+	    N <= 0 || K <= 0 || !s3h_settings()->ln_gemv_fold)
+		return 0;
+	struct s3k_gemm g;
+	fill_gemm(&g, SAM3_DTYPE_F32, ln->x, b_dt, b, SAM3_DTYPE_F32, (void *)ln->x, M, N, K, NULL,
+		  flags);
+	use_ln_input(&g, ln);
+	return skinny_takes_ln(&g);
+}
+
 static int skinny_takes_f16(const struct s3k_gemm *g)
 {
 	if (g->a_kind != S3K_F32 || g->b_kind != S3K_Q8 || g->batch != 1 ||
@@ -917,6 +948,14 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 			return SAM3_EINVAL;
 		}
 		return f32_split_gemm(&g, a, stream);
+	}
+	if (a_fmt == S3H_A_LN) {
+		use_ln_input(&g, (const struct s3h_ln_in *)a);
+		if (!skinny_takes_ln(&g)) {
+			s3h_error("matmul: the LayerNorm input cannot be read by this GEMM");
+			return SAM3_EINVAL;
+		}
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream), "matmul skinny (LN)");
 	}
 	if (a_fmt == S3H_A_F16 && skinny_takes_f16(&g)) {
 		g.a_kind = S3K_F16;
@@ -984,11 +1023,22 @@ static int skinny_res_fits(int a_fmt, const struct s3k_gemm *g)
 	return a_fmt == S3H_A_PLAIN && s3k_gemm_path(g) == S3K_PATH_SKINNY;
 }
 
+/* s3h_matmul_res_ok / s3h_matmul_qkv_ok for A read as a LayerNorm's
+ * input: the streaming skinny kernel with S3K_A_LN. */
+static int ln_skinny_fits(int a_dt, const void *a, int b_dt, const void *b, int M, int N, int K,
+			  int flags)
+{
+	return a_dt == SAM3_DTYPE_F32 && s3h_matmul_ln_ok(b_dt, b, M, N, K, flags,
+							   (const struct s3h_ln_in *)a);
+}
+
 /* Whether s3h_matmul_fmt_to can add an f32 [M, N] residual to this GEMM's
  * f32 result in its epilogue (no row map). */
 int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags)
 {
+	if (a_fmt == S3H_A_LN)
+		return ln_skinny_fits(a_dt, a, b_dt, b, M, N, K, flags);
 	if (s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN))
 		return 1;
 	if (M <= 0 || N <= 0 || K <= 0 || !a || !b ||
@@ -1017,8 +1067,13 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 		s3h_error("matmul: cannot write form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
 		return SAM3_EINVAL;
 	}
+	if (a_fmt == S3H_A_LN && (out_fmt != S3H_A_PLAIN || row_map)) {
+		s3h_error("matmul: a LayerNorm input GEMM writes f32 rows only");
+		return SAM3_EINVAL;
+	}
 	struct s3k_gemm g;
-	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
+	fill_gemm(&g, a_dt, a_fmt == S3H_A_LN ? ((const struct s3h_ln_in *)a)->x : a, b_dt, b,
+		  SAM3_DTYPE_F32, c, M, N, K, bias, flags);
 	g.c_kind = out_fmt == S3H_A_PLANES ? S3K_C_PLANES
 		 : out_fmt == S3H_A_F16     ? S3K_C_F16OP
 					    : S3K_F32;
@@ -1041,6 +1096,11 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 		g.rm_g = row_map[0];
 		g.rm_d1 = row_map[1];
 		g.rm_d2 = row_map[2];
+	}
+	if (a_fmt == S3H_A_LN) {
+		use_ln_input(&g, (const struct s3h_ln_in *)a);
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
+			       "matmul skinny (LN)");
 	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
@@ -1077,6 +1137,8 @@ static int qkv_skinny(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 {
 	if (b_dt != SAM3_DTYPE_Q8_0 || a_dt != SAM3_DTYPE_F32 || !(flags & SAM3_HIP_B_NT))
 		return 0;
+	if (a_fmt == S3H_A_LN)
+		return ln_skinny_fits(a_dt, a, b_dt, b, M, N, K, flags);
 	static const char al[16] __attribute__((aligned(16)));
 	struct s3k_gemm g;
 	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
@@ -1107,7 +1169,7 @@ int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 			return 0;
 	if (!q->rope && qkv_skinny(a_fmt, a_dt, a, b_dt, b, M, N, K, flags))
 		return 1;
-	return K % 64 == 0 && q->S >= 32 &&
+	return a_fmt != S3H_A_LN && K % 64 == 0 && q->S >= 32 &&
 	       s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN);
 }
 
@@ -1121,11 +1183,14 @@ enum sam3_error s3h_matmul_qkv(int a_fmt, int a_dt, const void *a, int b_dt, con
 		return SAM3_EINVAL;
 	}
 	struct s3k_gemm g;
-	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, q->out[0], M, N, K, bias, flags);
+	fill_gemm(&g, a_dt, a_fmt == S3H_A_LN ? ((const struct s3h_ln_in *)a)->x : a, b_dt, b,
+		  SAM3_DTYPE_F32, q->out[0], M, N, K, bias, flags);
 	fill_qkv(&g, q);
 	if (!q->rope && qkv_skinny(a_fmt, a_dt, a, b_dt, b, M, N, K, flags)) {
 		if (a_fmt == S3H_A_F16)
 			g.a_kind = S3K_F16;
+		if (a_fmt == S3H_A_LN)
+			use_ln_input(&g, (const struct s3h_ln_in *)a);
 		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
 			       "matmul skinny (attention operands)");
 	}

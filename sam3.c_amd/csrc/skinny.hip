@@ -213,6 +213,11 @@ struct StreamArgs {
 	/* S3K_EPI_QKV without RoPE (struct s3k_gemm): the head-split stores */
 	float *qkv_out[3];
 	int qkv_S, qkv_H, qkv_dsh;
+	/* S3K_A_LN (f32 A only): A's rows are a LayerNorm's input, normalized
+	 * here with gamma ln_g and beta ln_b; ln bit 0 set, bits 1 and 2 when
+	 * gamma and beta are given */
+	int ln;
+	const float *ln_g, *ln_b;
 };
 
 template <int AK, int MR, int NT, int KC>
@@ -254,9 +259,18 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 	 * a power-of-two factor per row (scale_exp_of, as the row-scaled f16
 	 * copy uses): 2^-e before the rounding, 2^e in the epilogue */
 	constexpr bool SCALE = AK != S3K_F16;
+	/* S3K_A_LN (f32 A). Not built into the MR = 1, KC = 8 instance:
+	 * hipcc (ROCm 7.2) fails instruction selection on it ("operand has
+	 * incorrect register class"); stream_ln_ok keeps LN problems off it
+	 * (K % 512 == 0 makes one-row workgroups take KC = 16). */
+	constexpr bool LN = AK == S3K_F32 && !(MR == 1 && KC == 8);
 	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
 	__shared__ float rsc[SCALE ? 2 * MR : 1];
 	__shared__ float rmx[SCALE ? C::WV * MR : 1];
+	/* S3K_A_LN's LDS, allocated at launch (dynamic) only for it: gamma
+	 * and beta f32 [K] (loaded once), then each row's mean and 1 / std */
+	extern __shared__ __attribute__((aligned(16))) float lnsm[];
+	float *const lng = lnsm, *const lnb = lnsm + p.K, *const lnst = lnsm + 2 * p.K;
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 	const int g16 = lane >> 4, l16 = lane & 15;
 
@@ -334,16 +348,83 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 	for (int mt = 0; mt < C::MT; ++mt)
 		inv[mt] = 1.0f, amx[mt] = 0.0f;
 
-	auto pass = [&](bool track) {
+	/* S3K_A_LN: the row statistics of layernorm_v (blockops.hip) for rows
+	 * of K = 256 * slots f32 values, one wave per row: lane l sums its
+	 * 16-byte pieces (64 s + l) of each slot s in order, then the wave
+	 * sums; the same for the centred squares. The same operations in the
+	 * same order, so the normalized rows below have LayerNorm's bits. The
+	 * first chunks' loads are already in flight (the ring is primed
+	 * before), so the statistics' one round trip overlaps them. */
+	auto ln_stats = [&]() {
+		constexpr int RPW = (MR + WV - 1) / WV; /* rows per wave */
+		const int slots = p.K / 256;
+		float4 xv[RPW][8];
+#pragma unroll
+		for (int r = 0; r < RPW; ++r) {
+			const int m = wave + r * WV;
+			const float *xr = (const float *)(abase + (long long)(m < Mz ? m : 0) * p.lda_b);
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots && m < Mz)
+					xv[r][i] = *(const float4 *)(xr + (i * 64 + lane) * 4);
+		}
+#pragma unroll
+		for (int r = 0; r < RPW; ++r) {
+			const int m = wave + r * WV;
+			if (m >= Mz)
+				continue;
+			float sum = 0.0f;
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots) {
+					sum += xv[r][i].x;
+					sum += xv[r][i].y;
+					sum += xv[r][i].z;
+					sum += xv[r][i].w;
+				}
+#pragma unroll
+			for (int off = 32; off; off >>= 1)
+				sum += __shfl_xor(sum, off);
+			const float mean = sum / (float)p.K;
+			float var = 0.0f;
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots) {
+					float d = sub_rn(xv[r][i].x, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[r][i].y, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[r][i].z, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[r][i].w, mean);
+					var = fmaf(d, d, var);
+				}
+#pragma unroll
+			for (int off = 32; off; off >>= 1)
+				var += __shfl_xor(var, off);
+			if (lane == 0) {
+				lnst[2 * m] = mean;
+				lnst[2 * m + 1] = 1.0f / sqrtf(var / (float)p.K + 1e-5f);
+			}
+		}
+	};
+
+	auto prime = [&]() {
+#pragma unroll
+		for (int s = 0; s < C::ST - 1; ++s)
+			if (s < nch)
+				issue(s);
+	};
+
+	/* primed: the first ST - 1 chunks were issued before */
+	auto pass = [&](bool track, bool primed) {
 #pragma unroll
 		for (int t = 0; t < NT; ++t)
 #pragma unroll
 			for (int mt = 0; mt < C::MT; ++mt)
 				acc[t][mt] = (s3k_f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-		for (int s = 0; s < C::ST - 1; ++s)
-			if (s < nch)
-				issue(s);
+		if (!primed)
+			prime();
 
 		for (int ch = 0; ch < nch; ++ch) {
 			/* this wave's loads of chunk ch done (younger chunks may fly) */
@@ -382,6 +463,29 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 							v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
 							v[4] = __uint_as_float(y.x), v[5] = __uint_as_float(y.y);
 							v[6] = __uint_as_float(y.z), v[7] = __uint_as_float(y.w);
+							if (LN && p.ln && m < Mz) {
+								/* layernorm_v's (x - mean) * rstd * g + b,
+								 * each step rounded */
+								const int k0 = ch * (KC * 32) + kb * 32 + 8 * g16;
+								const float mean = lnst[2 * m], rstd = lnst[2 * m + 1];
+								float gv[8], bv[8];
+#pragma unroll
+								for (int e = 0; e < 8; e += 4) {
+									const float4 gq = *(const float4 *)(lng + k0 + e);
+									const float4 bq = *(const float4 *)(lnb + k0 + e);
+									gv[e] = gq.x, gv[e + 1] = gq.y, gv[e + 2] = gq.z, gv[e + 3] = gq.w;
+									bv[e] = bq.x, bv[e + 1] = bq.y, bv[e + 2] = bq.z, bv[e + 3] = bq.w;
+								}
+#pragma unroll
+								for (int e = 0; e < 8; ++e) {
+									float t = mul_rn(sub_rn(v[e], mean), rstd);
+									if (p.ln & 2)
+										t = mul_rn(t, gv[e]);
+									if (p.ln & 4)
+										t = add_rn(t, bv[e]);
+									v[e] = t;
+								}
+							}
 						} else if constexpr (AK == S3K_BF16) {
 							const int q0 = kb * 4 + g16;
 							const uint4 x = *(const uint4 *)(row + ((q0 ^ (m & 15)) << 4));
@@ -444,7 +548,29 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 		wg_barrier();
 	};
 
-	pass(SCALE);
+	if constexpr (LN) {
+		/* gamma and beta into LDS ahead of the ring's loads (older, so
+		 * the ring's waits cover them; K * 4 bytes each, 1 KiB per wave
+		 * load, piece j by wave j; absent ones are not read) */
+		if (p.ln) {
+			const int pieces = p.K / 256;
+			const s3k_i32x4 rg = buf_rsrc(p.ln_g, (p.ln & 2) ? (unsigned)p.K * 4u : 0u);
+			const s3k_i32x4 rb = buf_rsrc(p.ln_b, (p.ln & 4) ? (unsigned)p.K * 4u : 0u);
+			if (wave < pieces && (p.ln & 2))
+				dma16(lng + wave * 256, rg, (unsigned)(wave * 1024 + lane * 16));
+			else if (wave >= pieces && wave < 2 * pieces && (p.ln & 4))
+				dma16(lnb + (wave - pieces) * 256, rb,
+				      (unsigned)((wave - pieces) * 1024 + lane * 16));
+		}
+	}
+	prime();
+	if constexpr (LN) {
+		if (p.ln) {
+			ln_stats();
+			__syncthreads();
+		}
+	}
+	pass(SCALE, true);
 	if constexpr (SCALE) {
 		/* each row's largest |value|: over the 4 lanes of a wave that hold
 		 * it (g16), then over the waves through LDS; rsc = 2^-e, 2^e */
@@ -479,7 +605,7 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 				const int m = mt * 16 + l16;
 				inv[mt] = m < MR ? rsc[m] : 1.0f;
 			}
-			pass(false);
+			pass(false, false);
 		}
 	}
 
@@ -562,6 +688,17 @@ extern "C" int s3k_skinny_scales_rows(const struct s3k_gemm *g)
 	       !(g->flags & S3K_EPI_ROWSCALE);
 }
 
+/* S3K_A_LN's conditions: f32 rows that layernorm_v would normalize
+ * (K % 256 == 0, K <= 2048, 16-byte aligned rows, gamma and beta), one
+ * slice, on q8_stream, with K % 512 == 0 (see q8_stream's LN). */
+static bool stream_ln_ok(const struct s3k_gemm *g)
+{
+	return g->a_kind == S3K_F32 && stream_ok(g) && g->batch == 1 && g->K <= 2048 &&
+	       g->K % 512 == 0 &&
+	       g->lda == g->K && !((uintptr_t)g->a & 15u) && !((uintptr_t)g->ln_g & 15u) &&
+	       !((uintptr_t)g->ln_b & 15u) && !(g->flags & S3K_EPI_ROWSCALE);
+}
+
 extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 {
 	if (g->b_kind != S3K_Q8 || !(g->flags & S3K_B_NT) || g->c_kind != S3K_F32 || g->batch < 1)
@@ -574,6 +711,8 @@ extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 	if (((uintptr_t)g->a & 15u) || ((long long)g->lda * es) % 16 || ((uintptr_t)g->b & 3u))
 		return 0;
 	if (g->batch > 1 && !stream_ok(g))
+		return 0;
+	if ((g->flags & S3K_A_LN) && !stream_ln_ok(g))
 		return 0;
 	return 1;
 }
@@ -633,6 +772,9 @@ static int launch_mt(const SkinnyArgs &p, hipStream_t st)
 template <int AK, int MR, int NT, int KC>
 static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 {
+	/* the instances q8_stream builds S3K_A_LN into */
+	if ((g->flags & S3K_A_LN) && !(AK == S3K_F32 && !(MR == 1 && KC == 8)))
+		return (int)hipErrorInvalidValue;
 	const int es = AK == S3K_F32 ? 4 : 2;
 	StreamArgs p;
 	p.a = (const char *)g->a;
@@ -659,9 +801,15 @@ static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 	p.qkv_S = g->qkv_S;
 	p.qkv_H = g->qkv_H;
 	p.qkv_dsh = g->qkv_D > 0 ? __builtin_ctz((unsigned)g->qkv_D) : 0;
+	/* bit 0: normalize A's rows; bits 1, 2: gamma, beta given */
+	p.ln = (g->flags & S3K_A_LN) ? 1 | (g->ln_g ? 2 : 0) | (g->ln_b ? 4 : 0) : 0;
+	p.ln_g = g->ln_g;
+	p.ln_b = g->ln_b;
 	dim3 grid(p.groups * p.zsplit, g->batch);
+	/* S3K_A_LN's dynamic LDS: gamma, beta [K], row statistics [2 * MR] */
+	const size_t dyn = p.ln ? (size_t)(2 * g->K + 2 * MR) * 4 : 0;
 	hipLaunchKernelGGL((q8_stream<AK, MR, NT, KC>), grid,
-			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), 0, (hipStream_t)stream, p);
+			   dim3(StreamCfg<AK, MR, NT, KC>::WV * 64), dyn, (hipStream_t)stream, p);
 	return (int)hipGetLastError();
 }
 
@@ -766,6 +914,8 @@ static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
 
 extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 {
+	if ((g->flags & S3K_A_LN) && !stream_ln_ok(g))
+		return (int)hipErrorInvalidValue;
 	/* the head-split stores (no RoPE) exist in q8_stream only */
 	if ((g->flags & S3K_EPI_QKV) && (!stream_ok(g) || g->batch != 1 || g->qkv_rope))
 		return (int)hipErrorInvalidValue;

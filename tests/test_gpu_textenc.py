@@ -16,7 +16,7 @@ normwise each).
 import numpy as np
 import pytest
 
-from gpu_util import assert_f32_close, oracle, require_gpu
+from gpu_util import assert_f32_close, oracle, ref_q8, require_gpu
 from sam3_amd import abi, graph, hip, synth
 from test_gpu_blockops import out_array, reference_eval
 
@@ -134,3 +134,67 @@ def test_text_chain_forwarded_between_evals_matches_one_eval():
         be.close()
         xd.free()
     assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
+
+
+def _eval(G, out, shape):
+    be = hip.Backend(0)
+    try:
+        assert be.graph_eval(G.g) == abi.OK
+        st = be.stats()
+        assert st.host_nodes == 0
+        return out_array(out, shape), st
+    finally:
+        be.close()
+
+
+@pytest.mark.parametrize("seq", [1, 8, 32, 77])
+def test_layernorm_folded_into_the_gemv_keeps_the_bits(seq, env):
+    """The LayerNorms before the qkv and fc1 projections do not run on
+    their own when the Q8_0 GEMM that reads them streams on the skinny
+    kernel: the GEMM normalizes its input rows with the LayerNorm kernel's
+    arithmetic (same sums in the same order, each step rounded the same
+    way), so the layers' output must have the same bits as with the
+    LayerNorm kernel run first (SAM3_HIP_LN_GEMV_FOLD=0), with two fewer
+    kernels per layer."""
+    n_layers = 2
+    G, out = build(seq, n_layers, "q8", 1500 + seq)
+    on, st_on = _eval(G, out, (seq, W))
+    env.set("SAM3_HIP_LN_GEMV_FOLD", 0)
+    G, out = build(seq, n_layers, "q8", 1500 + seq)
+    off, st_off = _eval(G, out, (seq, W))
+    assert np.array_equal(on.view(np.uint32), off.view(np.uint32))
+    assert st_on.gpu_nodes == st_off.gpu_nodes - 2 * n_layers
+    assert st_on.fused_nodes == st_off.fused_nodes + 2 * n_layers
+
+
+@pytest.mark.parametrize("affine", ["none", "gamma"])
+@pytest.mark.parametrize("M,K", [(1, 1024), (5, 2048), (40, 512)])
+def test_layernorm_gemv_fold_without_beta(affine, M, K, env):
+    """LN -> RESHAPE -> Q8_0 linear with gamma only, or no affine terms:
+    folded and unfolded give the same bits, and both match the oracle's
+    LayerNorm followed by the Q8_0 product."""
+    O = oracle()
+    N = 768
+    x_h = synth.randn(1600 + M, (M, K)) * np.float32(3.0) + np.float32(0.5)
+    g_h = synth.randn(1601, (K,), 1.0)
+    w_h = O.q8_quantize(synth.randn(1602, (N, K), 0.03))
+
+    def run():
+        G = graph.Graph()
+        x = G.tensor(abi.F32, (M, K), x_h)
+        gm = G.tensor(abi.F32, (K,), g_h) if affine == "gamma" else None
+        w = G.tensor(abi.Q8_0, (N, K), w_h)
+        y = G.linear(G.reshape(G.layernorm(x, gm), [1, M, K]), w)
+        return _eval(G, y, (M, N))
+
+    on, st_on = run()
+    env.set("SAM3_HIP_LN_GEMV_FOLD", 0)
+    off, st_off = run()
+    assert np.array_equal(on.view(np.uint32), off.view(np.uint32))
+    assert st_on.gpu_nodes == st_off.gpu_nodes - 1
+    xf = x_h.astype(np.float64)
+    ln = (xf - xf.mean(1, keepdims=True)) / np.sqrt(xf.var(1, keepdims=True) + 1e-5)
+    if affine == "gamma":
+        ln = ln * g_h
+    assert_f32_close(on, ref_q8(ln.astype(np.float32), w_h, K, N, nt=True),
+                     what=f"LN gemv fold {affine} M={M} K={K}")
