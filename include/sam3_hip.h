@@ -378,14 +378,16 @@ enum sam3_error sam3_hip_matmul_on_path(int path, int a_dtype, const void *a,
  * (SAM3_DTYPE_F32, _F16 or _BF16); mask f32 [Sq, Sk] or NULL. A query
  * whose scores are all -inf gets zeros, as there. D = 64 with 16-byte
  * aligned tensors runs the MFMA kernel (f32 as three bf16 products per
- * step: hi*hi + lo*hi + hi*lo); other D up to 512 run a one-wave-per-row
- * f32 kernel. */
+ * step: hi*hi + lo*hi + hi*lo), or for f32 with at most 128 keys a
+ * latency-bound kernel in plain f32 arithmetic (the text encoder's
+ * attention); other D up to 512 run a one-wave-per-row f32 kernel. */
 enum sam3_error sam3_hip_sdpa(int dtype, const void *q, const void *k, const void *v,
 			      const float *mask, void *out, int BH, int Sq, int Sk, int D,
 			      void *stream);
 
 /* sam3_hip_sdpa on a forced kernel: 0 = best, 1 = MFMA (D = 64), 3 = the
- * any-D kernel. SAM3_EINVAL if that kernel cannot run the problem. */
+ * any-D kernel, 4 = the few-keys kernel (f32, D = 64, Sk <= 128, 16-byte
+ * aligned). SAM3_EINVAL if that kernel cannot run the problem. */
 enum sam3_error sam3_hip_sdpa_on_path(int path, int dtype, const void *q, const void *k,
 				      const void *v, const float *mask, void *out, int BH,
 				      int Sq, int Sk, int D, void *stream);

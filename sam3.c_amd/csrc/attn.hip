@@ -675,6 +675,9 @@ struct AttnGArgs {
 	int BH, Sq, Sk, D;
 	float scale;
 	int oh;                 /* > 0: output head-merged (at_out_row) */
+	int ofmt;               /* attn_small: AttnArgs' operand forms */
+	unsigned *ovf;
+	unsigned ovf_tag;
 };
 
 template <int DT>
@@ -780,6 +783,184 @@ __global__ void __launch_bounds__(256) attn_generic(AttnGArgs p)
 	}
 }
 
+/*
+ * Attention over few keys (Sk <= 128, D = 64, f32): the text encoder's
+ * shapes (cpu_sdpa.c:49-159 per query row, softmax over all keys), where
+ * a launch's time is its latency. One workgroup per 16 queries of a head:
+ * every load (K, V, the queries, the mask entries) is issued before the
+ * first use, so the kernel waits for memory once; K is stored transposed
+ * in LDS so that lane j's key j reads are bank-distinct. Wave w owns
+ * queries 4w..4w+3 in both phases, lane l keys l and l + 64 for the
+ * scores, then output element l. Arithmetic: dot = fmaf over d in
+ * order, s = dot * scale + mask, p = expf(s - max), l = butterfly sum,
+ * out = (fmaf over keys in order of p * v) * (1 / l), 0 when every score
+ * is -inf; for Sk <= 64 these are the steps (and bits) of attn_generic.
+ */
+constexpr int AS_QB = 16, AS_MAXK = 128, AS_KTP = AS_MAXK + 4;
+
+__global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
+{
+	__shared__ __attribute__((aligned(16))) float kt[AT_D][AS_KTP];
+	__shared__ __attribute__((aligned(16))) float vs[AS_MAXK][AT_D];
+	__shared__ __attribute__((aligned(16))) float qs[AS_QB][AT_D];
+	__shared__ __attribute__((aligned(16))) float ps[AS_QB][AS_MAXK];
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int nqb = (p.Sq + AS_QB - 1) / AS_QB;
+	const long long head = blockIdx.x / nqb;
+	const int q0 = (int)(blockIdx.x - head * nqb) * AS_QB;
+	const int nq = min(AS_QB, p.Sq - q0);
+	const float4 *K4 = (const float4 *)p.k + head * p.Sk * (AT_D / 4);
+	const float4 *V4 = (const float4 *)p.v + head * p.Sk * (AT_D / 4);
+	const float4 *Q4 = (const float4 *)p.q + (head * p.Sq + q0) * (AT_D / 4);
+	const int n4 = p.Sk * (AT_D / 4);
+
+	/* every load first */
+	float4 kr[AS_MAXK * AT_D / 4 / 256], vr[AS_MAXK * AT_D / 4 / 256];
+#pragma unroll
+	for (int i = 0; i < AS_MAXK * AT_D / 4 / 256; ++i) {
+		const int idx = i * 256 + tid;
+		if (idx < n4) {
+			kr[i] = K4[idx];
+			vr[i] = V4[idx];
+		}
+	}
+	const float4 qr = tid < nq * (AT_D / 4) ? Q4[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
+	float mk[4][2];
+#pragma unroll
+	for (int j = 0; j < 4; ++j)
+#pragma unroll
+		for (int c = 0; c < 2; ++c) {
+			const int q = q0 + 4 * wave + j, key = lane + 64 * c;
+			mk[j][c] = p.mask && q < p.Sq && key < p.Sk ? p.mask[(long long)q * p.Sk + key]
+								      : 0.0f;
+		}
+#pragma unroll
+	for (int i = 0; i < AS_MAXK * AT_D / 4 / 256; ++i) {
+		const int idx = i * 256 + tid;
+		if (idx < n4) {
+			const int key = idx >> 4, d0 = (idx & 15) * 4;
+			kt[d0][key] = kr[i].x;
+			kt[d0 + 1][key] = kr[i].y;
+			kt[d0 + 2][key] = kr[i].z;
+			kt[d0 + 3][key] = kr[i].w;
+			*(float4 *)&vs[key][d0] = vr[i];
+		}
+	}
+	*(float4 *)&qs[tid >> 4][(tid & 15) * 4] = qr;
+	__syncthreads();
+
+	/* scores of this wave's 4 queries against keys lane, lane + 64 */
+	float sc[4][2];
+#pragma unroll
+	for (int j = 0; j < 4; ++j)
+		sc[j][0] = sc[j][1] = 0.0f;
+	const bool hi = p.Sk > 64;
+#pragma unroll 2
+	for (int d = 0; d < AT_D; d += 4) {
+		float k0[4], k1[4];
+#pragma unroll
+		for (int e = 0; e < 4; ++e) {
+			k0[e] = kt[d + e][lane];
+			k1[e] = hi ? kt[d + e][lane + 64] : 0.0f;
+		}
+#pragma unroll
+		for (int j = 0; j < 4; ++j) {
+			const float4 q4 = *(const float4 *)&qs[4 * wave + j][d];
+			const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+			for (int e = 0; e < 4; ++e) {
+				sc[j][0] = fmaf(qv[e], k0[e], sc[j][0]);
+				sc[j][1] = fmaf(qv[e], k1[e], sc[j][1]);
+			}
+		}
+	}
+	float inv[4];
+#pragma unroll
+	for (int j = 0; j < 4; ++j) {
+		float s[2], m = -3.402823466e38f;
+#pragma unroll
+		for (int c = 0; c < 2; ++c) {
+			s[c] = -__builtin_inff();
+			if (lane + 64 * c < p.Sk) {
+				s[c] = sc[j][c] * p.scale;
+				if (p.mask)
+					s[c] += mk[j][c];
+			}
+			m = fmaxf(m, s[c]);
+		}
+#pragma unroll
+		for (int off = 32; off; off >>= 1)
+			m = fmaxf(m, __shfl_xor(m, off));
+		const float p0 = expf(s[0] - m), p1 = expf(s[1] - m);
+		float l = hi ? p0 + p1 : p0;
+#pragma unroll
+		for (int off = 32; off; off >>= 1)
+			l += __shfl_xor(l, off);
+		inv[j] = l > 0.0f ? 1.0f / l : 0.0f;
+		ps[4 * wave + j][lane] = p0;
+		ps[4 * wave + j][lane + 64] = p1;
+	}
+	__syncthreads();
+
+	/* out[q][lane] over the keys in order */
+	float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+	int key = 0;
+	for (; key + 4 <= p.Sk; key += 4) {
+		float v[4];
+#pragma unroll
+		for (int e = 0; e < 4; ++e)
+			v[e] = vs[key + e][lane];
+#pragma unroll
+		for (int j = 0; j < 4; ++j) {
+			const float4 w4 = *(const float4 *)&ps[4 * wave + j][key];
+			acc[j] = fmaf(w4.x, v[0], acc[j]);
+			acc[j] = fmaf(w4.y, v[1], acc[j]);
+			acc[j] = fmaf(w4.z, v[2], acc[j]);
+			acc[j] = fmaf(w4.w, v[3], acc[j]);
+		}
+	}
+	for (; key < p.Sk; ++key) {
+		const float v = vs[key][lane];
+#pragma unroll
+		for (int j = 0; j < 4; ++j)
+			acc[j] = fmaf(ps[4 * wave + j][key], v, acc[j]);
+	}
+#pragma unroll
+	for (int j = 0; j < 4; ++j) {
+		const int q = q0 + 4 * wave + j;
+		const float x = acc[j] * inv[j];
+		/* the neighbours of the operand forms' pairs and groups of four */
+		const float x1 = __shfl_xor(x, 1);
+		if (q >= p.Sq)
+			continue;
+		const long long orow = at_out_row(p.oh, head, p.Sq, q, AT_D);
+		if (p.ofmt == 0) {
+			((float *)p.out)[orow + lane] = x;
+		} else if (p.ofmt == 1) {
+			/* bf16 planes [hi|lo|hi] of the merged row, as attn_fwd */
+			if (!(lane & 1)) {
+				const long long K = (long long)p.oh * AT_D, r = orow / K;
+				uint16_t *dp = (uint16_t *)p.out + r * 3 * K + (orow - r * K) + lane;
+				uint32_t hi, lo;
+				split_bf16x2(x, x1, hi, lo);
+				*(uint32_t *)dp = hi;
+				*(uint32_t *)(dp + K) = lo;
+				*(uint32_t *)(dp + 2 * K) = hi;
+			}
+		} else {
+			/* f16, flagged per four values as attn_fwd flags them */
+			const float ax = __builtin_fabsf(x);
+			float mx = fmaxf(ax, __shfl_xor(ax, 1));
+			mx = fmaxf(mx, __shfl_xor(mx, 2));
+			const bool big = ax >= 32768.0f && ax <= 3.402823466e38f;
+			if (p.ovf && (big || (!(lane & 3) && mx > 0.0f && mx < 0x1p-10f)))
+				*p.ovf = p.ovf_tag;
+			if (!(lane & 1))
+				*(uint32_t *)((uint16_t *)p.out + orow + lane) = pack_f16x2(x, x1);
+		}
+	}
+}
+
 template <int DT>
 static void launch_generic(const AttnGArgs &g, hipStream_t st)
 {
@@ -822,11 +1003,49 @@ extern "C" int s3k_attn_path(int kind, const void *q, const void *k, const void 
 	return 0;
 }
 
+/* The few-keys kernel's conditions (attn_small). */
+static bool attn_small_ok(int kind, const void *q, const void *k, const void *v, void *out,
+			  int BH, int Sq, int Sk, int D)
+{
+	return kind == S3K_F32 && D == AT_D && Sk >= 1 && Sk <= AS_MAXK && BH >= 1 && Sq >= 1 &&
+	       (long long)BH * ((Sq + AS_QB - 1) / AS_QB) < (1LL << 31) &&
+	       !(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u);
+}
+
 extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
 			      const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
 			      int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream)
 {
 	const int best = s3k_attn_path(kind, q, k, v, out, BH, Sq, Sk, D);
+	const bool small = attn_small_ok(kind, q, k, v, out, BH, Sq, Sk, D);
+	const bool small_fmt = oh >= 0 && !(oh > 0 && BH % oh) && ofmt >= 0 && ofmt <= 2 &&
+			       !(ofmt && oh <= 0);
+	if (path == S3K_ATTN_SMALL) {
+		if (!small || !small_fmt)
+			return (int)hipErrorInvalidValue;
+	} else if (path == 0 && small && small_fmt) {
+		path = S3K_ATTN_SMALL; /* few keys: the latency-bound case */
+	}
+	if (path == S3K_ATTN_SMALL) {
+		AttnGArgs g{};
+		g.q = (const char *)q;
+		g.k = (const char *)k;
+		g.v = (const char *)v;
+		g.mask = mask;
+		g.out = (char *)out;
+		g.BH = BH;
+		g.Sq = Sq;
+		g.Sk = Sk;
+		g.D = D;
+		g.oh = oh;
+		g.ofmt = ofmt;
+		g.ovf = ovf;
+		g.ovf_tag = ovf_tag;
+		g.scale = 1.0f / sqrtf((float)D);
+		const dim3 grid((unsigned)((long long)BH * ((Sq + AS_QB - 1) / AS_QB)));
+		hipLaunchKernelGGL(attn_small, grid, dim3(256), 0, (hipStream_t)stream, g);
+		return (int)hipGetLastError();
+	}
 	if (!best || (path == S3K_ATTN_MFMA && best != S3K_ATTN_MFMA) ||
 	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC) || oh < 0 ||
 	    (oh > 0 && BH % oh) || ofmt < 0 || ofmt > 2 ||
@@ -838,7 +1057,7 @@ extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, 
 	if (path == 0)
 		path = best;
 	if (path == S3K_ATTN_GENERIC) {
-		AttnGArgs g;
+		AttnGArgs g{};
 		g.q = (const char *)q;
 		g.k = (const char *)k;
 		g.v = (const char *)v;

@@ -191,8 +191,11 @@ int s3k_cast_f16_rows(int kind, const void *src, long long lda, long long sa, vo
 /* Fused attention out = softmax(Q K^T / sqrt(D) + mask) V over BH heads:
  * Q and out [BH, Sq, D], K and V [BH, Sk, D], one dtype (S3K_F32, _BF16,
  * _F16); mask f32 [Sq, Sk] or NULL. s3k_attn_path gives the kernel that
- * runs the problem (0 = none); s3k_attn runs it on `path` (0 = best). */
-enum { S3K_ATTN_MFMA = 1, S3K_ATTN_GENERIC = 3 };
+ * runs the problem (0 = none); s3k_attn runs it on `path` (0 = best:
+ * S3K_ATTN_SMALL when it can run the problem with f32 output rows, else
+ * that kernel). S3K_ATTN_SMALL: f32, D = 64, 1 <= Sk <= 128, 16-byte
+ * aligned tensors, the latency-bound few-keys kernel. */
+enum { S3K_ATTN_MFMA = 1, S3K_ATTN_GENERIC = 3, S3K_ATTN_SMALL = 4 };
 int s3k_attn_path(int kind, const void *q, const void *k, const void *v, void *out,
 		  int BH, int Sq, int Sk, int D);
 int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,

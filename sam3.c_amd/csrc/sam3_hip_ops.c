@@ -1447,7 +1447,8 @@ enum sam3_error sam3_hip_sdpa_on_path(int path, int dtype, const void *q, const 
 		s3h_error("sdpa: no kernel for D=%d (D <= 512, element-aligned tensors)", D);
 		return SAM3_EINVAL;
 	}
-	if (path != 0 && path != S3K_ATTN_GENERIC && !(path == S3K_ATTN_MFMA && best == path)) {
+	if (path != 0 && path != S3K_ATTN_GENERIC && path != S3K_ATTN_SMALL &&
+	    !(path == S3K_ATTN_MFMA && best == path)) {
 		s3h_error("sdpa: kernel %d cannot run this problem", path);
 		return SAM3_EINVAL;
 	}

@@ -27,7 +27,7 @@ from sam3_amd import abi, hip, synth
 pytestmark = pytest.mark.gpu
 
 GOLD = np.load(Path(__file__).parent / "golden" / "matmul_golden.npz")
-MFMA, GENERIC = 1, 3
+MFMA, GENERIC, SMALL = 1, 3, 4
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -82,7 +82,7 @@ DT_ID = {abi.F32: "f32", abi.BF16: "bf16", abi.F16: "f16"}
 
 
 # ----------------------------------------------------------- golden vectors
-@pytest.mark.parametrize("path", [0, MFMA, GENERIC])
+@pytest.mark.parametrize("path", [0, MFMA, GENERIC, SMALL])
 def test_sdpa_golden(path):
     """The reference's own outputs (cpu_kernel_sdpa, 4-D, ragged Sk = 70)."""
     q, k, v, m = GOLD["sdpa_q"], GOLD["sdpa_k"], GOLD["sdpa_v"], GOLD["sdpa_mask"]
@@ -226,6 +226,71 @@ def test_sdpa_kernel_choice_errors():
     big = np.zeros((1, 2, 513), np.float32)
     with pytest.raises(hip.HipError):
         hip.sdpa(big, big, big, dtype=abi.F32)
+
+
+# ------------------------------------------------------ few-keys kernel
+SMALL_SAME = [(2, 1, 1), (16, 1, 1), (16, 8, 8), (16, 32, 32), (3, 37, 64), (1, 100, 17)]
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+@pytest.mark.parametrize("BH,Sq,Sk", SMALL_SAME)
+def test_sdpa_small_same_bits_as_generic(BH, Sq, Sk, masked):
+    """Up to 64 keys the few-keys kernel takes the any-D kernel's steps in
+    the same order (one 64-key tile there), so the outputs agree bit for
+    bit; both are checked against the oracle."""
+    q, k, v = inputs(1100 + Sq + Sk, BH, Sq, Sk, 64)
+    mask = None
+    if masked:
+        mask = synth.randn(1101, (Sq, Sk))
+        mask[np.triu_indices(Sq, 1, Sk)] = np.float32(-1e9)
+    a = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=SMALL)
+    b = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=GENERIC)
+    assert np.array_equal(bits32(a), bits32(b))
+    assert np.array_equal(bits32(hip.sdpa(q, k, v, mask, dtype=abi.F32)), bits32(a))
+    assert_f32_close(a, oracle().sdpa(q, k, v, mask, 8), what=f"small {BH}x{Sq}x{Sk}")
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+@pytest.mark.parametrize("BH,Sq,Sk", [(16, 77, 77), (2, 129, 65), (1, 200, 128), (5, 3, 100)])
+def test_sdpa_small_many_keys(BH, Sq, Sk, masked):
+    """65-128 keys: the softmax over all keys at once (the any-D kernel
+    rescales per 64-key tile), within the f32 bound of the oracle."""
+    q, k, v = inputs(1110 + Sq + Sk, BH, Sq, Sk, 64, qscale=2.0)
+    mask = None
+    if masked:
+        c = np.arange(Sk)
+        mask = np.where(c[None, :] > np.arange(Sq)[:, None] + (Sk - Sq), np.float32(-1e9),
+                        np.float32(0.0)).astype(np.float32)
+    got = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=SMALL)
+    assert_f32_close(got, oracle().sdpa(q, k, v, mask, 8), what=f"small {BH}x{Sq}x{Sk}")
+
+
+def test_sdpa_small_single_key_and_masked_rows():
+    """One unmasked key: weight exactly 1, the output is that V row bit for
+    bit; rows with every key masked are zero."""
+    BH, Sq, Sk, D = 3, 50, 100, 64
+    q, k, v = inputs(1120, BH, Sq, Sk, D)
+    pick = (np.arange(Sq) * 37 + 5) % Sk
+    mask = np.full((Sq, Sk), -np.inf, np.float32)
+    mask[np.arange(Sq), pick] = 0.0
+    mask[[7, 49]] = -np.inf
+    got = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=SMALL)
+    keep = np.setdiff1d(np.arange(Sq), [7, 49])
+    assert np.array_equal(bits32(got[:, keep]), bits32(v[:, pick[keep], :]))
+    assert np.all(got[:, [7, 49]] == 0)
+
+
+def test_sdpa_small_kernel_limits():
+    q = synth.randn(1130, (1, 4, 64))
+    k = synth.randn(1131, (1, 129, 64))
+    with pytest.raises(hip.HipError):
+        hip.sdpa(q, k, k, dtype=abi.F32, path=SMALL)   # 129 keys
+    q32 = synth.randn(1132, (1, 4, 32))
+    with pytest.raises(hip.HipError):
+        hip.sdpa(q32, q32, q32, dtype=abi.F32, path=SMALL)   # D = 32
+    qb, _ = to_dtype(q, abi.BF16)
+    with pytest.raises(hip.HipError):
+        hip.sdpa(qb, qb, qb, dtype=abi.BF16, path=SMALL)   # f32 only
 
 
 # ------------------------------------------------- node kernel and backend
