@@ -53,6 +53,17 @@ enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };
  * 64-bank model) to 22.4 extra cycles per read (no permutation):
  *   CPR 4 (64-B rows):  c ^ ((r >> 2) & 3)
  *   CPR 8 (128-B rows): c ^ ((r ^ (r >> 3)) & 7) */
+/* 16 bytes from the LDS byte address base + off (a 32-bit LDS address,
+ * so the offset can fold into the instruction's immediate) */
+typedef unsigned lds_u4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const lds_u4v lds_cu4;
+
+__device__ __forceinline__ uint4 lds_rd16(unsigned base, unsigned off)
+{
+	const lds_u4v v = *(lds_cu4 *)(size_t)(base + off);
+	return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <int CPR>
 __device__ __forceinline__ int lds_swz(int row)
 {

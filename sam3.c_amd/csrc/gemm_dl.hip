@@ -203,14 +203,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dl(GemmArgs p)
  *     peeled.
  * Same per-element accumulation order as gemm_dl, so the same bits.
  */
-typedef unsigned lds_u4v __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) const lds_u4v lds_cu4;
-
-__device__ __forceinline__ uint4 lds_rd16(unsigned base, unsigned off)
-{
-	const lds_u4v v = *(lds_cu4 *)(size_t)(base + off);
-	return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 /* QKV: the S3K_EPI_QKV epilogue (f32 output), instead of C */
 template <int BM, int BN, int WGM, int WGN, int FAM, int CK, bool INTER, bool QKV = false>

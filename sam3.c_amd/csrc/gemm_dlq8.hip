@@ -214,6 +214,237 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 	write_tile_ck<FM, FN, WTN, S3K_F32, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
 
+/*
+ * gemm_dlpq: the Q8 GEMM for many rows, on the k-step schedule of the
+ * pipelined f16 kernel (gemm_dlp, gemm_dl.hip): two stages, one wait and
+ * one barrier per k-step, and the fragments of sub-step ks + 1 read while
+ * the MFMAs of sub-step ks run (the non-interleaved order, whose grouped
+ * reads measured fastest there). The weight tile is gemm_dlq8's: the raw
+ * 72-byte segment of each row, 80 bytes per LDS row, moved by five
+ * direct-to-LDS pieces (padded to whole loads per wave; the spare ones
+ * load zeros into a trash KiB). A wave's B fragment is dequantized when
+ * it is read: q exactly in f16 by the byte permute, then multiplied by
+ * the block scale over the row factor rounded to f16 (gemm_dlq8's
+ * arithmetic, so the same bits as gemm_dlq8 per product; the sums run
+ * in the same k order). The block scales of a stage are read when the
+ * stage's first fragments are. 192x256 tiles of eight 96x64 wave tiles,
+ * one workgroup per CU, f32 C.
+ */
+template <int BM, int BN, int WGM, int WGN, bool INTER>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlpq(GemmArgs p)
+{
+	constexpr int NW = WGM * WGN, BK = 64, CPR = 8, PW = 5, KS = BK / 16;
+	constexpr int A_BYTES = BM * BK * 2;
+	constexpr int A_INS = BM * CPR / 64, B_INS = (BN * PW + 63) / 64;
+	constexpr int A_PER = (A_INS + NW - 1) / NW, B_PER = (B_INS + NW - 1) / NW;
+	constexpr int LOADS = A_PER + B_PER;
+	constexpr int B_BYTES = B_INS * 1024, B_BASE = 2 * A_BYTES;
+	constexpr int TRASH = B_BASE + 2 * B_BYTES, LDS_BYTES = TRASH + 1024;
+	constexpr int WTM = BM / WGM, WTN = BN / WGN;
+	constexpr int FM = WTM / 32, FN = WTN / 32, NMF = FM * FN;
+	static_assert(A_BYTES + (FM - 1) * 4096 < 65536, "fragment offsets fit the immediate");
+	static_assert(NW * 32 * (WTN + 8) * 4 <= LDS_BYTES, "epilogue staging fits");
+	static_assert(2 * LOADS < 64, "vmcnt range");
+	__shared__ __attribute__((aligned(1024))) char smem[LDS_BYTES];
+
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+	const int bz = blockIdx.y;
+	const unsigned lds0 = lds_addr_of(smem);
+	int tm, tn;
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
+	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
+	const unsigned rowbytes = (unsigned)(p.K / 32) * 36u;
+
+	/* per-lane source of DMA instruction t: A chunks (t < A_PER), then W
+	 * pieces; loads past the tile go to the trash KiB */
+	unsigned off[LOADS], dst[LOADS];
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t) {
+		const bool isa = t < A_PER;
+		const int j = (isa ? t : t - A_PER) * NW + wave;
+		const int s = j * 64 + lane;
+		unsigned o = S3K_OOB;
+		if (isa) {
+			const int row = s / CPR, c = (s % CPR) ^ lds_swz<CPR>(row);
+			const int g = tm * BM + row;
+			if (j < A_INS && g < p.M)
+				o = (unsigned)(g * p.lda_b + c * 16);
+			dst[t] = j < A_INS ? (unsigned)(j * 1024) : (unsigned)TRASH;
+		} else {
+			const int row = s / PW, q = s % PW;
+			const int n = tn * BN + row;
+			if (j < B_INS && s < BN * PW && n < p.N)
+				o = (unsigned)n * rowbytes + (unsigned)(q < 4 ? q * 16 : 56);
+			dst[t] = j < B_INS ? (unsigned)(B_BASE + j * 1024) : (unsigned)TRASH;
+		}
+		off[t] = o;
+	}
+	auto dma = [&](int kt, int t, int stg) {
+		const bool isa = t < A_PER;
+		const unsigned d = dst[t] == (unsigned)TRASH ? (unsigned)TRASH
+				 : dst[t] + (unsigned)(stg * (isa ? A_BYTES : B_BYTES));
+		dma16s(lds0 + d, isa ? ra : rb, off[t], isa ? (unsigned)(kt * BK * 2) : 72u * kt);
+	};
+
+	unsigned abase[4];
+	{
+		const int l32 = lane & 31, h = lane >> 5, r0 = wm0 + l32;
+#pragma unroll
+		for (int ks = 0; ks < 4; ++ks)
+			abase[ks] = lds0 + (unsigned)((r0 * CPR + ((2 * ks + h) ^ lds_swz<CPR>(r0))) << 4);
+	}
+	/* B fragment of sub-step ks: row n = lane & 31 of each 32-row tile, 8
+	 * q bytes at segment byte 36 (ks >> 1) + 4 + 16 (ks & 1) + 8 h (+8 past
+	 * byte 64), the scale of block ks >> 1 at 36 (ks >> 1) */
+	const int h = lane >> 5;
+	int qo[KS];
+#pragma unroll
+	for (int ks = 0; ks < KS; ++ks) {
+		const int b = 36 * (ks >> 1) + 4 + 16 * (ks & 1) + 8 * h;
+		qo[ks] = b + (b >= 64 ? 8 : 0);
+	}
+	int brow[FN];
+	float binv[FN];
+#pragma unroll
+	for (int j = 0; j < FN; ++j) {
+		brow[j] = B_BASE + (wn0 + j * 32 + (lane & 31)) * (PW * 16);
+		const int n = tn * BN + wn0 + j * 32 + (lane & 31);
+		binv[j] = (p.flags & S3K_EPI_COLSCALE) && n < p.N
+				  ? inv_pow2(p.cs[(long long)bz * p.cs_sb + n]) : 1.0f;
+	}
+
+	s3k_f32x16 acc[FM][FN];
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+
+	uint4 af[2][FM], bf[2][FN];
+	q8h2_t s2[FN][2];
+	auto scales = [&](int stg) {
+#pragma unroll
+		for (int j = 0; j < FN; ++j) {
+			const char *row = smem + stg * B_BYTES + brow[j];
+#pragma unroll
+			for (int blk = 0; blk < 2; ++blk) {
+				const _Float16 sh = (_Float16)(*(const float *)(row + 36 * blk) * binv[j]);
+				s2[j][blk] = (q8h2_t){sh, sh};
+			}
+		}
+	};
+	auto frag = [&](int buf, int stg, int ks, int r) {
+		if (r < FM) {
+			af[buf][r] = lds_rd16(abase[ks ^ (2 * (r & 1))], (unsigned)(stg * A_BYTES + r * 4096));
+		} else {
+			const int j = r - FM;
+			const char *row = smem + stg * B_BYTES + brow[j] + qo[ks];
+			const uint32_t w0 = *(const uint32_t *)row ^ 0x80808080u;
+			const uint32_t w1 = *(const uint32_t *)(row + 4) ^ 0x80808080u;
+			const q8h2_t sc = s2[j][ks >> 1];
+			bf[buf][j] = make_uint4(q8_pair_f16(w0, 0x04010400u, sc),
+						q8_pair_f16(w0, 0x04030402u, sc),
+						q8_pair_f16(w1, 0x04010400u, sc),
+						q8_pair_f16(w1, 0x04030402u, sc));
+		}
+	};
+
+	/* k-step kt from stage stg; next: a k-step follows; dmak: issue the
+	 * DMA of k-step kt + 2 into stg */
+	auto step = [&](int stg, int kt, bool next, bool dmak) {
+#pragma unroll
+		for (int ks = 0; ks < KS; ++ks) {
+			const int cur = ks & 1, nxt = cur ^ 1;
+			if (ks == 3) {
+				__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): own reads done */
+				if (next) {
+					wait_vm<0>();
+					wg_barrier();
+				}
+			}
+			__builtin_amdgcn_sched_barrier(0);
+			if (ks == 3 && next)
+				scales(stg ^ 1);
+			/* INTER: one fragment read (B: read and dequantization) or
+			 * DMA after each MFMA; else grouped after them */
+#pragma unroll
+			for (int m = 0; m < NMF; ++m) {
+				mfma_chunk<FAM_F16>(acc[m / FN][m % FN], bf[cur][m % FN], af[cur][m / FN]);
+				if (INTER) {
+					if (ks < 3) {
+						if (m < FM + FN)
+							frag(nxt, stg, ks + 1, m);
+					} else {
+						if (next && m < FM + FN)
+							frag(0, stg ^ 1, 0, m);
+						if (dmak && m < LOADS)
+							dma(kt + 2, m, stg);
+					}
+					__builtin_amdgcn_sched_barrier(0);
+				}
+			}
+			const int r0 = INTER ? NMF : 0;
+#pragma unroll
+			for (int r = r0; r < FM + FN; ++r) {
+				if (ks < 3)
+					frag(nxt, stg, ks + 1, r);
+				else if (next)
+					frag(0, stg ^ 1, 0, r);
+			}
+			if (ks == 3 && dmak) {
+#pragma unroll
+				for (int t = r0; t < LOADS; ++t)
+					dma(kt + 2, t, stg);
+			}
+		}
+	};
+
+	const int nk = p.K / BK;
+#pragma unroll
+	for (int t = 0; t < LOADS; ++t)
+		dma(0, t, 0);
+	if (nk > 1) {
+#pragma unroll
+		for (int t = 0; t < LOADS; ++t)
+			dma(1, t, 1);
+		wait_vm<LOADS>();
+	} else {
+		wait_vm<0>();
+	}
+	wg_barrier();
+	scales(0);
+#pragma unroll
+	for (int r = 0; r < FM + FN; ++r)
+		frag(0, 0, 0, r);
+	int kt = 0;
+	for (; kt + 2 < nk; ++kt)
+		step(kt & 1, kt, true, true);
+	if (kt + 1 < nk) {
+		step(kt & 1, kt, true, false);
+		++kt;
+	}
+	step(kt & 1, kt, false, false);
+
+	__syncthreads();
+	write_tile_ck<FM, FN, WTN, S3K_F32, true>(p, acc, smem, wave, lane, tm * BM + wm0,
+						 tn * BN + wn0, bz);
+}
+
+template <int BM, int BN, int WGM, int WGN, bool INTER = false>
+static int launch_dlpq_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
+{
+	p.tiles_m = (p.M + BM - 1) / BM;
+	p.tiles_n = (p.N + BN - 1) / BN;
+	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	hipLaunchKernelGGL((gemm_dlpq<BM, BN, WGM, WGN, INTER>), grid, dim3(64 * WGM * WGN), 0, st, p);
+	return (int)hipGetLastError();
+}
+
 template <int BM, int BN, int WGM, int WGN, int STAGES, int OCC>
 static int launch_dlq8_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 {
@@ -249,12 +480,16 @@ bool s3k_dlq8_ok(const struct s3k_gemm *g)
 }
 
 /*
- * Tile choice: 128x128 with 4 waves of 128x32 (one dequantized weight
- * fragment feeds 4 MFMAs) and two workgroups per CU measured fastest on
- * every ViT-L shape (fc1/fc2/qkv/proj at M = 5184), ahead of 256x256 and
- * 256x128 tiles with 8 waves and of 256-row waves. M <= 96 (batched
- * streams of weight copies) takes one tile of 32, 64 or 96 rows, so no
- * weight tile is read twice. SAM3_HIP_DLQ8_CFG forces another
+ * Tile choice. Above 96 rows the pipelined kernel with 128x256 tiles of
+ * eight 128x32 wave tiles (cfg 15; each wave dequantizes its own weight
+ * fragments, none twice; two workgroups fit a CU): fc1 5184x4096x1024
+ * with bf16 A 74-75 us per step against 87 for gemm_dlq8's 128x128 tiles
+ * (cfg 2), 75-76 for 192x256 in the same layout (13), 78-81 for 192x256
+ * and 192x128 with 2x4 waves (10, 11), 85-88 for 256x256 (12, 14); the
+ * interleaved schedule (16-18) gained nothing. Config 3 (32 ViT-L
+ * layers, every weight read as blocks): 7.99 ms against 8.84. M <= 96
+ * (batched streams of weight copies) takes one tile of 32, 64 or 96
+ * rows, so no weight tile is read twice. SAM3_HIP_DLQ8_CFG forces another
  * configuration (tests and tuning).
  */
 int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
@@ -265,7 +500,7 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	p.b_extent = (unsigned)((long long)g->N * (g->K / 32) * 36);
 	int cfg = s3h_settings()->dlq8_cfg;
 	if (cfg < 0)
-		cfg = g->M <= 32 ? 7 : g->M <= 64 ? 8 : g->M <= 96 ? 9 : 2;
+		cfg = g->M <= 32 ? 7 : g->M <= 64 ? 8 : g->M <= 96 ? 9 : 15;
 	switch (cfg) {
 	case 0:  return launch_dlq8_cfg<256, 256, 2, 4, 3, 1>(g, p, st);
 	case 1:  return launch_dlq8_cfg<256, 128, 2, 4, 3, 1>(g, p, st);
@@ -276,6 +511,15 @@ int s3k_dlq8_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	case 7:  return launch_dlq8_cfg<32, 128, 1, 4, 3, 2>(g, p, st);
 	case 8:  return launch_dlq8_cfg<64, 128, 1, 4, 3, 2>(g, p, st);
 	case 9:  return launch_dlq8_cfg<96, 128, 1, 4, 3, 2>(g, p, st);
+	case 10: return launch_dlpq_cfg<192, 256, 2, 4>(g, p, st);
+	case 11: return launch_dlpq_cfg<192, 128, 2, 4>(g, p, st);
+	case 12: return launch_dlpq_cfg<256, 256, 2, 4>(g, p, st);
+	case 13: return launch_dlpq_cfg<192, 256, 1, 8>(g, p, st);
+	case 14: return launch_dlpq_cfg<256, 256, 1, 8>(g, p, st);
+	case 15: return launch_dlpq_cfg<128, 256, 1, 8>(g, p, st);
+	case 16: return launch_dlpq_cfg<192, 256, 1, 8, true>(g, p, st);
+	case 17: return launch_dlpq_cfg<128, 256, 1, 8, true>(g, p, st);
+	case 18: return launch_dlpq_cfg<192, 256, 2, 4, true>(g, p, st);
 	default: return (int)hipErrorInvalidValue;
 	}
 }

@@ -361,7 +361,7 @@ def test_q8_nt_tiled_bf16_and_f16_activations(M, N, K):
     assert_f32_close(c, ref, what="q8 f16-act")
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 5, 6])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 5, 6, 10, 11, 12])
 @pytest.mark.parametrize("a_dt", [abi.F32, abi.BF16, abi.F16])
 def test_q8_dl_every_config(env, cfg, a_dt):
     """Direct-to-LDS Q8 GEMM (raw 36-byte blocks in LDS, dequantized per
@@ -386,6 +386,31 @@ def test_q8_dl_every_config(env, cfg, a_dt):
                    flags=hip.B_NT | hip.BIAS | hip.GELU, path=MFMA)
     ref = ref_q8(np.asarray(a_ref, np.float32), w, K, N, nt=True, bias=bias, gelu=True)
     assert_f32_close(c, ref, what=f"dlq8 cfg {cfg} a={a_dt}")
+
+
+@pytest.mark.parametrize("cfg", [10, 11, 12])
+def test_q8_pipelined_same_bits_as_dlq8(env, cfg):
+    """The pipelined Q8 kernel (gemm_dlpq) dequantizes each weight fragment
+    with gemm_dlq8's arithmetic and accumulates the k-steps in the same
+    order, so every output has gemm_dlq8's bits, whatever the tiles;
+    ragged M and N, K of 16 k-steps, weight rows with tiny scales (their
+    row factor) among them."""
+    O = oracle()
+    M, N, K = 1000, 520, 1024
+    a = O.f32_to_fp16(rnd(230, (M, K))).reshape(M, K)
+    wf = rnd(231, (N, K), 0.02)
+    wf[7] *= np.float32(1e-6)
+    w = q8(wf)
+    bias = rnd(232, N, 0.1)
+    env.set("SAM3_HIP_Q8_EXPAND", 0)
+    outs = []
+    for c in (2, cfg):
+        env.set("SAM3_HIP_DLQ8_CFG", str(c))
+        outs.append(hip.matmul(a, abi.F16, w, abi.Q8_0, abi.F32, M, N, K, bias=bias,
+                               flags=hip.B_NT | hip.BIAS, path=MFMA))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = ref_q8(O.fp16_to_f32(a).reshape(M, K), w, K, N, nt=True, bias=bias)
+    assert_f32_close(outs[1], ref, what=f"dlpq cfg {cfg}")
 
 
 def test_q8_dl_one_hot_rows():
