@@ -815,14 +815,13 @@ __global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
 	const int n4 = p.Sk * (AT_D / 4);
 
 	/* every load first */
-	float4 kr[AS_MAXK * AT_D / 4 / 256], vr[AS_MAXK * AT_D / 4 / 256];
+	constexpr int NL = AS_MAXK * AT_D / 4 / 256; /* float4 of K (and of V) per thread */
+	float4 kr[NL], vr[NL];
 #pragma unroll
-	for (int i = 0; i < AS_MAXK * AT_D / 4 / 256; ++i) {
-		const int idx = i * 256 + tid;
-		if (idx < n4) {
-			kr[i] = K4[idx];
-			vr[i] = V4[idx];
-		}
+	for (int i = 0; i < NL; ++i) {
+		const int idx = min(i * 256 + tid, n4 - 1); /* in bounds; the extra ones unused */
+		kr[i] = K4[idx];
+		vr[i] = V4[idx];
 	}
 	const float4 qr = tid < nq * (AT_D / 4) ? Q4[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
 	float mk[4][2];
@@ -835,7 +834,7 @@ __global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
 								      : 0.0f;
 		}
 #pragma unroll
-	for (int i = 0; i < AS_MAXK * AT_D / 4 / 256; ++i) {
+	for (int i = 0; i < NL; ++i) {
 		const int idx = i * 256 + tid;
 		if (idx < n4) {
 			const int key = idx >> 4, d0 = (idx & 15) * 4;
@@ -849,31 +848,46 @@ __global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
 	*(float4 *)&qs[tid >> 4][(tid & 15) * 4] = qr;
 	__syncthreads();
 
-	/* scores of this wave's 4 queries against keys lane, lane + 64 */
+	/* the wave's queries: nqw of 4 exist (wave-uniform); a wave without
+	 * any is done (no barrier follows) */
+	const int nqw = min(4, p.Sq - (q0 + 4 * wave));
+	if (nqw <= 0)
+		return;
+
+	/* scores of this wave's queries against keys lane, lane + 64 (the
+	 * second only when Sk > 64) */
 	float sc[4][2];
 #pragma unroll
 	for (int j = 0; j < 4; ++j)
 		sc[j][0] = sc[j][1] = 0.0f;
 	const bool hi = p.Sk > 64;
+	auto dots = [&](auto two) {
+		constexpr bool TWO = decltype(two)::value != 0;
 #pragma unroll 2
-	for (int d = 0; d < AT_D; d += 4) {
-		float k0[4], k1[4];
-#pragma unroll
-		for (int e = 0; e < 4; ++e) {
-			k0[e] = kt[d + e][lane];
-			k1[e] = hi ? kt[d + e][lane + 64] : 0.0f;
-		}
-#pragma unroll
-		for (int j = 0; j < 4; ++j) {
-			const float4 q4 = *(const float4 *)&qs[4 * wave + j][d];
-			const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+		for (int d = 0; d < AT_D; d += 4) {
+			float k0[4], k1[4];
 #pragma unroll
 			for (int e = 0; e < 4; ++e) {
-				sc[j][0] = fmaf(qv[e], k0[e], sc[j][0]);
-				sc[j][1] = fmaf(qv[e], k1[e], sc[j][1]);
+				k0[e] = kt[d + e][lane];
+				k1[e] = TWO ? kt[d + e][lane + 64] : 0.0f;
+			}
+#pragma unroll
+			for (int j = 0; j < 4; ++j) {
+				const float4 q4 = *(const float4 *)&qs[4 * wave + j][d];
+				const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+				for (int e = 0; e < 4; ++e) {
+					sc[j][0] = fmaf(qv[e], k0[e], sc[j][0]);
+					if (TWO)
+						sc[j][1] = fmaf(qv[e], k1[e], sc[j][1]);
+				}
 			}
 		}
-	}
+	};
+	if (hi)
+		dots(at_int<1>{});
+	else
+		dots(at_int<0>{});
 	float inv[4];
 #pragma unroll
 	for (int j = 0; j < 4; ++j) {
@@ -891,7 +905,7 @@ __global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
 #pragma unroll
 		for (int off = 32; off; off >>= 1)
 			m = fmaxf(m, __shfl_xor(m, off));
-		const float p0 = expf(s[0] - m), p1 = expf(s[1] - m);
+		const float p0 = expf(s[0] - m), p1 = hi ? expf(s[1] - m) : 0.0f;
 		float l = hi ? p0 + p1 : p0;
 #pragma unroll
 		for (int off = 32; off; off >>= 1)
@@ -900,7 +914,10 @@ __global__ void __launch_bounds__(256) attn_small(AttnGArgs p)
 		ps[4 * wave + j][lane] = p0;
 		ps[4 * wave + j][lane + 64] = p1;
 	}
-	__syncthreads();
+	/* the wave reads back only its own rows of ps: its LDS accesses run
+	 * in order, so waiting for its writes is enough */
+	__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+	__builtin_amdgcn_wave_barrier();
 
 	/* out[q][lane] over the keys in order */
 	float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1024,7 +1041,15 @@ extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, 
 		if (!small || !small_fmt)
 			return (int)hipErrorInvalidValue;
 	} else if (path == 0 && small && small_fmt) {
-		path = S3K_ATTN_SMALL; /* few keys: the latency-bound case */
+		/* latency-bound sizes, by measured launch time (16 heads, f32,
+		 * in a HIP graph): up to 64 scores per head the one-wave-per-row
+		 * kernel (1 / 8 queries and keys: 3.3 / 4.4 us against 6.4 /
+		 * 6.2 for attn_fwd), from 65 keys this kernel (77: 9.7 against
+		 * 11.0), attn_fwd in between (32: 6.5 against 8.5) */
+		if ((long long)Sq * Sk <= 64 && !ofmt)
+			path = S3K_ATTN_GENERIC;
+		else if (Sk > 64)
+			path = S3K_ATTN_SMALL;
 	}
 	if (path == S3K_ATTN_SMALL) {
 		AttnGArgs g{};

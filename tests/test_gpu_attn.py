@@ -246,8 +246,19 @@ def test_sdpa_small_same_bits_as_generic(BH, Sq, Sk, masked):
     a = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=SMALL)
     b = hip.sdpa(q, k, v, mask, dtype=abi.F32, path=GENERIC)
     assert np.array_equal(bits32(a), bits32(b))
-    assert np.array_equal(bits32(hip.sdpa(q, k, v, mask, dtype=abi.F32)), bits32(a))
     assert_f32_close(a, oracle().sdpa(q, k, v, mask, 8), what=f"small {BH}x{Sq}x{Sk}")
+
+
+@pytest.mark.parametrize("Sq,Sk,want", [(1, 1, GENERIC), (8, 8, GENERIC), (32, 32, MFMA),
+                                        (77, 77, SMALL), (3, 100, SMALL), (200, 300, MFMA)])
+def test_sdpa_best_kernel_by_size(Sq, Sk, want):
+    """f32, D = 64: path 0 takes the one-wave-per-row kernel up to 64
+    scores per head, the few-keys kernel from 65 keys to 128, the MFMA
+    kernel otherwise; its bits are that kernel's."""
+    q, k, v = inputs(1140 + Sq, 16, Sq, Sk, 64)
+    best = hip.sdpa(q, k, v, None, dtype=abi.F32)
+    forced = hip.sdpa(q, k, v, None, dtype=abi.F32, path=want)
+    assert np.array_equal(bits32(best), bits32(forced))
 
 
 @pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
