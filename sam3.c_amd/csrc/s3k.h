@@ -334,6 +334,9 @@ struct s3h_settings {
 	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
 	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
 	    permute_operand, partition_fold, qkv_fold, sdpa_merge, ln_gemv_fold;
+	int gemv_f32;                     /* SAM3_HIP_GEMV_F32: one f32 activation
+					   * row on the f32 VALU GEMV (1) or on
+					   * the f16 MFMA stream (0)           */
 	int readback_all;                 /* SAM3_HIP_READBACK=all               */
 	int quiet;                        /* SAM3_HIP_QUIET set                  */
 	int arena_mb;                     /* SAM3_HIP_ARENA_MB (0 = default)     */

@@ -40,6 +40,7 @@
  */
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "s3k.h"
 #include "s3k_dev.h"
@@ -658,6 +659,232 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 	}
 }
 
+/*
+ * q8_gemv: one f32 activation row times Q8_0 W[N,K] (the text encoder at
+ * one token, decoder steps, config 4's M = 1). The weights and the row
+ * stream through q8_stream's LDS ring (same chunks, loads and waits), but
+ * the products run on the VALU in f32: lane (row l16 of a 16-row tile,
+ * group g16) multiplies its 8 activations of a k-block by the 8 int8
+ * weights converted exactly to f32, sums them in order, and adds that
+ * sum times the block's f32 scale to its accumulator (cpu_matmul_q8.c:
+ * 124-131 forms a * q * scale in f32 as well). Nothing is rounded to f16,
+ * so there is no row factor and no second pass, and per chunk a wave
+ * issues about a quarter of q8_stream's instructions (no activation
+ * conversion, no MFMA operand packing), the cost that bounds a launch
+ * over few workgroups. The 4 lanes of a row then add their sums
+ * (xor 16, then 32) and the waves theirs through LDS in wave order:
+ * deterministic. S3K_A_LN normalizes the row as q8_stream does
+ * (layernorm_v's statistics and steps), with gamma and beta in LDS.
+ */
+template <int NT, int KC>
+__global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
+{
+	using C = StreamCfg<S3K_F32, 1, NT, KC>;
+	constexpr int WV = C::WV;
+	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+	extern __shared__ __attribute__((aligned(16))) float lnsm[];
+	float *const lng = lnsm, *const lnb = lnsm + p.K, *const lnst = lnsm + 2 * p.K;
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int g16 = lane >> 4, l16 = lane & 15;
+
+	/* workgroup -> weight-row group (one activation row: zsplit 1); ids
+	 * of a group of 8 row groups lie on the 8 XCDs, as in q8_stream */
+	const int gi = blockIdx.x;
+	const int n0 = gi * C::NR;
+	const int KB = p.K / 32;
+	const unsigned rowbytes = (unsigned)KB * 36u;
+	const char *abase = p.a + blockIdx.y * p.sa_b;
+	const s3k_i32x4 rw = buf_rsrc(p.w + blockIdx.y * p.sw_b, p.w_ext);
+	const s3k_i32x4 ra = buf_rsrc(abase, (unsigned)(p.K * 4));
+
+	/* the loads of a chunk, as q8_stream's (A: the one row, 16-B slots
+	 * unswizzled since row 0's swizzle is the identity) */
+	unsigned off[C::NPW];
+#pragma unroll
+	for (int t = 0; t < C::NPW; ++t) {
+		const int j = t * C::WV + wave;
+		unsigned o = S3K_OOB;
+		if (j < C::IW) {
+			const int i = j * 64 + lane;
+			const int r = i / C::PW, q = i % C::PW;
+			if (i < C::GW && q < C::GPRW && n0 + r < p.N)
+				o = (unsigned)(n0 + r) * rowbytes + (unsigned)q * 16u;
+		} else if (j < C::I) {
+			const int i = (j - C::IW) * 64 + lane;
+			if (i < C::GAR)
+				o = (unsigned)(i * 16);
+		}
+		off[t] = o;
+	}
+	auto issue = [&](int ch) {
+		char *st = smem + (ch % C::ST) * C::SB;
+		const unsigned wi = (unsigned)ch * (KC * 36);
+		const unsigned ai = (unsigned)ch * (KC * 32 * 4);
+#pragma unroll
+		for (int t = 0; t < C::NPW; ++t) {
+			const int j = t * C::WV + wave;
+			if (j < C::IW)
+				dma16(st + j * 1024, rw, off[t] + wi);
+			else if (j < C::I)
+				dma16(st + C::SW + (j - C::IW) * 1024, ra, off[t] + ai);
+			else
+				dma16(smem + C::ST * C::SB, rw, S3K_OOB);
+		}
+	};
+	const int nch = p.K / (KC * 32);
+
+	if (p.ln) {
+		const int pieces = p.K / 256;
+		const s3k_i32x4 rg = buf_rsrc(p.ln_g, (p.ln & 2) ? (unsigned)p.K * 4u : 0u);
+		const s3k_i32x4 rb = buf_rsrc(p.ln_b, (p.ln & 4) ? (unsigned)p.K * 4u : 0u);
+		if (wave < pieces && (p.ln & 2))
+			dma16(lng + wave * 256, rg, (unsigned)(wave * 1024 + lane * 16));
+		else if (wave >= pieces && wave < 2 * pieces && (p.ln & 4))
+			dma16(lnb + (wave - pieces) * 256, rb, (unsigned)((wave - pieces) * 1024 + lane * 16));
+	}
+#pragma unroll
+	for (int s = 0; s < C::ST - 1; ++s)
+		if (s < nch)
+			issue(s);
+	if (p.ln) {
+		/* layernorm_v's statistics of the row (wave 0), as q8_stream's */
+		if (wave == 0) {
+			const int slots = p.K / 256;
+			const float *xr = (const float *)abase;
+			float4 xv[8];
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots)
+					xv[i] = *(const float4 *)(xr + (i * 64 + lane) * 4);
+			float sum = 0.0f;
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots) {
+					sum += xv[i].x;
+					sum += xv[i].y;
+					sum += xv[i].z;
+					sum += xv[i].w;
+				}
+#pragma unroll
+			for (int o = 32; o; o >>= 1)
+				sum += __shfl_xor(sum, o);
+			const float mean = sum / (float)p.K;
+			float var = 0.0f;
+#pragma unroll
+			for (int i = 0; i < 8; ++i)
+				if (i < slots) {
+					float d = sub_rn(xv[i].x, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[i].y, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[i].z, mean);
+					var = fmaf(d, d, var);
+					d = sub_rn(xv[i].w, mean);
+					var = fmaf(d, d, var);
+				}
+#pragma unroll
+			for (int o = 32; o; o >>= 1)
+				var += __shfl_xor(var, o);
+			if (lane == 0) {
+				lnst[0] = mean;
+				lnst[1] = 1.0f / sqrtf(var / (float)p.K + 1e-5f);
+			}
+		}
+		__syncthreads();
+	}
+
+	float acc[NT];
+#pragma unroll
+	for (int t = 0; t < NT; ++t)
+		acc[t] = 0.0f;
+	for (int ch = 0; ch < nch; ++ch) {
+		if (ch + C::ST - 2 < nch)
+			wait_vm<(C::ST - 2) * C::NPW>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (ch + C::ST - 1 < nch)
+			issue(ch + C::ST - 1);
+		if (C::CW < WV && wave >= C::CW)
+			continue;
+		const char *Ws = smem + (ch % C::ST) * C::SB;
+		const char *As = Ws + C::SW;
+#pragma unroll
+		for (int u = 0; u < C::U; ++u) {
+			const int kb = u * C::CW + wave;
+			const int q0 = kb * 8 + 2 * g16;
+			const float4 x = *(const float4 *)(As + (q0 << 4));
+			const float4 y = *(const float4 *)(As + ((q0 + 1) << 4));
+			float a[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+			if (p.ln) {
+				/* layernorm_v's (x - mean) * rstd * g + b, each step rounded */
+				const int k0 = ch * (KC * 32) + kb * 32 + 8 * g16;
+				const float mean = lnst[0], rstd = lnst[1];
+#pragma unroll
+				for (int e = 0; e < 8; ++e) {
+					float t = mul_rn(sub_rn(a[e], mean), rstd);
+					if (p.ln & 2)
+						t = mul_rn(t, lng[k0 + e]);
+					if (p.ln & 4)
+						t = add_rn(t, lnb[k0 + e]);
+					a[e] = t;
+				}
+			}
+#pragma unroll
+			for (int t = 0; t < NT; ++t) {
+				const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
+				const float sc = *(const float *)blk;
+				const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16);
+				const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16);
+				float s8 = 0.0f;
+#pragma unroll
+				for (int e = 0; e < 4; ++e)
+					s8 = fmaf(a[e], (float)(int)(signed char)(w0 >> (8 * e)), s8);
+#pragma unroll
+				for (int e = 0; e < 4; ++e)
+					s8 = fmaf(a[4 + e], (float)(int)(signed char)(w1 >> (8 * e)), s8);
+				acc[t] = fmaf(sc, s8, acc[t]);
+			}
+		}
+	}
+
+	/* the row's 4 lanes, then the waves in order */
+	wait_vm<0>();
+	wg_barrier();
+	float *red = (float *)smem;
+#pragma unroll
+	for (int t = 0; t < NT; ++t) {
+		float v = acc[t] + __shfl_xor(acc[t], 16);
+		v += __shfl_xor(v, 32);
+		if (g16 == 0)
+			red[wave * C::NR + t * 16 + l16] = v;
+	}
+	__syncthreads();
+	if (threadIdx.x < C::NR) {
+		const int v = threadIdx.x, n = n0 + v;
+		if (n < p.N) {
+			float s = 0.0f;
+#pragma unroll
+			for (int w = 0; w < WV; ++w)
+				s += red[w * C::NR + v];
+			if (p.flags & S3K_EPI_ROWSCALE)
+				s *= p.rs[blockIdx.y * p.rs_sb];
+			const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
+			float o = epilogue<0>(s, bv, p.flags);
+			if (p.flags & S3K_EPI_RES)
+				o += p.res[n];
+			if (p.flags & S3K_EPI_QKV) {
+				const int D = 1 << p.qkv_dsh, E = p.qkv_H << p.qkv_dsh;
+				const int y = (n >= E) + (n >= 2 * E), r = n - y * E;
+				float *oy = y == 0 ? p.qkv_out[0] : y == 1 ? p.qkv_out[1] : p.qkv_out[2];
+				oy[(long long)(r >> p.qkv_dsh) * p.qkv_S * D + (r & (D - 1))] = o;
+			} else {
+				((float *)p.c + blockIdx.y * p.sc)[n] = o;
+			}
+		}
+	}
+}
+
 } /* namespace s3k */
 
 using namespace s3k;
@@ -813,6 +1040,45 @@ static int launch_stream_k(const struct s3k_gemm *g, void *stream)
 	return (int)hipGetLastError();
 }
 
+template <int NT, int KC>
+static int launch_gemv_k(const struct s3k_gemm *g, void *stream)
+{
+	using C = StreamCfg<S3K_F32, 1, NT, KC>;
+	StreamArgs p;
+	memset(&p, 0, sizeof p);
+	p.a = (const char *)g->a;
+	p.w = (const char *)g->b;
+	p.c = (char *)g->c;
+	p.bias = (const char *)g->bias;
+	p.M = 1;
+	p.N = g->N;
+	p.K = g->K;
+	p.lda_b = g->lda * 4;
+	p.ldc = g->ldc;
+	p.sa_b = g->stride_a * 4;
+	p.sw_b = g->stride_b;
+	p.sc = g->stride_c;
+	p.w_ext = (unsigned)((long long)g->N * (g->K / 32) * 36);
+	p.flags = g->flags;
+	p.groups = (g->N + C::NR - 1) / C::NR;
+	p.zsplit = 1;
+	p.rs = g->rs;
+	p.rs_sb = g->rs_sb;
+	p.res = (const float *)g->res;
+	for (int y = 0; y < 3; ++y)
+		p.qkv_out[y] = g->qkv_out[y];
+	p.qkv_S = g->qkv_S;
+	p.qkv_H = g->qkv_H;
+	p.qkv_dsh = g->qkv_D > 0 ? __builtin_ctz((unsigned)g->qkv_D) : 0;
+	p.ln = (g->flags & S3K_A_LN) ? 1 | (g->ln_g ? 2 : 0) | (g->ln_b ? 4 : 0) : 0;
+	p.ln_g = g->ln_g;
+	p.ln_b = g->ln_b;
+	const size_t dyn = p.ln ? (size_t)(2 * g->K + 2) * 4 : 0;
+	dim3 grid(p.groups, g->batch);
+	hipLaunchKernelGGL((q8_gemv<NT, KC>), grid, dim3(C::WV * 64), dyn, (hipStream_t)stream, p);
+	return (int)hipGetLastError();
+}
+
 template <int AK, int KC>
 static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *stream)
 {
@@ -925,6 +1191,14 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 		/* 16-block chunks where K allows and the LDS ring stays deep
 		 * enough; 8-block chunks otherwise */
 		const bool k16 = g->K % 512 == 0 && mr <= 16;
+		/* one f32 activation row: the f32 VALU kernel */
+		if (g->a_kind == S3K_F32 && g->M == 1 && g->lda % 4 == 0 && s3h_settings()->gemv_f32) {
+			if (nt == 1)
+				return k16 ? launch_gemv_k<1, 16>(g, stream) : launch_gemv_k<1, 8>(g, stream);
+			if (nt == 2)
+				return k16 ? launch_gemv_k<2, 16>(g, stream) : launch_gemv_k<2, 8>(g, stream);
+			return k16 ? launch_gemv_k<4, 16>(g, stream) : launch_gemv_k<4, 8>(g, stream);
+		}
 		switch (g->a_kind) {
 		case S3K_F32:
 			return k16 ? launch_stream_a<S3K_F32, 16>(g, mr, nt, stream)

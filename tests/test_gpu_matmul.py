@@ -540,12 +540,13 @@ def test_q8_batched_stream(shared_a):
         assert_f32_close(c[s], ref, what=f"q8 batched slice {s}")
 
 
-@pytest.mark.parametrize("M,K", [(1, 256), (2, 1024), (24, 1024), (77, 1024)])
+@pytest.mark.parametrize("M,K", [(2, 1024), (24, 1024), (77, 1024)])
 def test_q8_batched_shared_f32_cast_once(M, K):
     """Shared f32 activations of a batched skinny launch are cast to f16
     once before the launch; the kernel rounds f32 activations to f16 the
     same way, so the result has the same bits as passing the activations
-    as f16 (both batched, so the same workgroup shape runs)."""
+    as f16 (both batched, so the same workgroup shape runs). One row is
+    not cast: it runs on the f32 GEMV (test_q8_gemv_f32_one_row)."""
     B, N = 4, 128
     a = rnd(185, (M, K))
     ws = [q8(rnd(186 + s, (N, K), 0.02)) for s in range(B)]
@@ -562,6 +563,46 @@ def test_q8_batched_shared_f32_cast_once(M, K):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     for s in range(B):
         assert_f32_close(outs[0][s], ref_q8(a, ws[s], K, N, nt=True), what=f"slice {s}")
+
+
+@pytest.mark.parametrize("K,N", [(256, 2048), (1024, 1024), (1024, 3072), (4096, 1024),
+                                 (512, 80)])
+def test_q8_gemv_f32_one_row(env, K, N):
+    """One f32 activation row (q8_gemv): products a * q * scale in f32, no
+    rounding to f16, so within a few f32 ulps of the oracle's sums (the
+    order differs); bias + GELU and a residual in the epilogue; as one
+    launch and as a batch of weight copies sharing the row; rows far
+    outside the f16 range need no factor. With SAM3_HIP_GEMV_F32=0 the
+    f16 MFMA stream runs instead, within the f16 bound."""
+    O = oracle()
+    B = 3
+    for scale in (1.0, 1e6, 1e-7):
+        a = rnd(700 + K, (1, K)) * np.float32(scale)
+        ws = [q8(rnd(701 + s, (N, K), 0.02)) for s in range(B)]
+        bias = rnd(704, N, 0.1)
+        refs = [ref_q8(a, w, K, N, nt=True) for w in ws]
+        tol = 1e-5 * np.sqrt(K / 256)
+        c = hip.matmul(a, abi.F32, ws[0], abi.Q8_0, abi.F32, 1, N, K, flags=hip.B_NT)
+        err = np.max(np.abs(c - refs[0])) / np.max(np.abs(refs[0]))
+        assert err <= tol, (scale, err)
+        cb = hip.matmul(a, abi.F32, ws[0], abi.Q8_0, abi.F32, 1, N, K, bias=bias,
+                        flags=hip.B_NT | hip.BIAS | hip.GELU)
+        assert_f32_close(cb, O.gelu(O.bias_add(refs[0], bias, "f32"), "f32").reshape(1, N),
+                         what=f"gemv bias gelu {scale}")
+        dw = hip.DeviceBuffer.of(np.concatenate(ws))
+        da, dc = hip.DeviceBuffer.of(a), hip.DeviceBuffer(B * N * 4)
+        hip.q8_batched_dev(abi.F32, da.ptr, dw.ptr, dc.ptr, B, 1, N, K, 0, ws[0].nbytes, N)
+        hip.synchronize()
+        cbat = dc.download(np.float32, (B, 1, N))
+        for s_ in (da, dw, dc):
+            s_.free()
+        assert np.array_equal(cbat[0].view(np.uint32), c.view(np.uint32))
+        for s_ in range(B):
+            e = np.max(np.abs(cbat[s_] - refs[s_])) / np.max(np.abs(refs[s_]))
+            assert e <= tol, (scale, s_, e)
+    env.set("SAM3_HIP_GEMV_F32", 0)
+    c16 = hip.matmul(a, abi.F32, ws[0], abi.Q8_0, abi.F32, 1, N, K, flags=hip.B_NT)
+    assert_f32_close(c16, refs[0], what="f16 stream")
 
 
 def test_q8_batched_falls_back_per_slice():
