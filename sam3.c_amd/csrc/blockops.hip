@@ -45,10 +45,7 @@ __device__ __forceinline__ void bo_st(void *p, long long i, float v)
 
 __device__ __forceinline__ float bo_wave_sum(float v)
 {
-#pragma unroll
-	for (int off = 32; off; off >>= 1)
-		v += __shfl_xor(v, off);
-	return v;
+	return wave_xor_sum(v);
 }
 
 /* One wave per row; element j of the row is held by lane j % 64 in slot

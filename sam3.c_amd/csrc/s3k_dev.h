@@ -54,6 +54,27 @@ __device__ __forceinline__ float pow2f(int e)
 	return __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
+/* Sum over the wave as the xor butterfly computes it: v += v[lane ^ off]
+ * for off = 32, 16, 8, 4, 2, 1, so every lane ends with the same value
+ * (each step adds the same two operands on both lanes of a pair). The
+ * partner values come from v_permlane32_swap (32), ds_swizzle in its
+ * xor mode (16, 8, 4) and DPP quad permutes (2, 1) instead of
+ * ds_bpermute: the same sums, fewer LDS-pipe round trips. */
+__device__ __forceinline__ float wave_xor_sum(float v)
+{
+	{
+		const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+								 false, false);
+		v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+	}
+	v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)); /* ^16 */
+	v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F)); /* ^8  */
+	v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F)); /* ^4  */
+	v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)); /* ^2 */
+	v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)); /* ^1 */
+	return v;
+}
+
 /* |x| for the row scale; inf and NaN count as 0 (they do not set it) */
 __device__ __forceinline__ float finite_abs(float x)
 {

@@ -383,9 +383,7 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 					sum += xv[r][i].z;
 					sum += xv[r][i].w;
 				}
-#pragma unroll
-			for (int off = 32; off; off >>= 1)
-				sum += __shfl_xor(sum, off);
+			sum = wave_xor_sum(sum);
 			const float mean = sum / (float)p.K;
 			float var = 0.0f;
 #pragma unroll
@@ -400,9 +398,7 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
 					d = sub_rn(xv[r][i].w, mean);
 					var = fmaf(d, d, var);
 				}
-#pragma unroll
-			for (int off = 32; off; off >>= 1)
-				var += __shfl_xor(var, off);
+			var = wave_xor_sum(var);
 			if (lane == 0) {
 				lnst[2 * m] = mean;
 				lnst[2 * m + 1] = 1.0f / sqrtf(var / (float)p.K + 1e-5f);
@@ -765,9 +761,7 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 					sum += xv[i].z;
 					sum += xv[i].w;
 				}
-#pragma unroll
-			for (int o = 32; o; o >>= 1)
-				sum += __shfl_xor(sum, o);
+			sum = wave_xor_sum(sum);
 			const float mean = sum / (float)p.K;
 			float var = 0.0f;
 #pragma unroll
@@ -782,9 +776,7 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 					d = sub_rn(xv[i].w, mean);
 					var = fmaf(d, d, var);
 				}
-#pragma unroll
-			for (int o = 32; o; o >>= 1)
-				var += __shfl_xor(var, o);
+			var = wave_xor_sum(var);
 			if (lane == 0) {
 				lnst[0] = mean;
 				lnst[1] = 1.0f / sqrtf(var / (float)p.K + 1e-5f);
@@ -820,13 +812,21 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 				/* layernorm_v's (x - mean) * rstd * g + b, each step rounded */
 				const int k0 = ch * (KC * 32) + kb * 32 + 8 * g16;
 				const float mean = lnst[0], rstd = lnst[1];
+				float gv[8], bv[8];
+#pragma unroll
+				for (int e = 0; e < 8; e += 4) {
+					const float4 gq = *(const float4 *)(lng + k0 + e);
+					const float4 bq = *(const float4 *)(lnb + k0 + e);
+					gv[e] = gq.x, gv[e + 1] = gq.y, gv[e + 2] = gq.z, gv[e + 3] = gq.w;
+					bv[e] = bq.x, bv[e + 1] = bq.y, bv[e + 2] = bq.z, bv[e + 3] = bq.w;
+				}
 #pragma unroll
 				for (int e = 0; e < 8; ++e) {
 					float t = mul_rn(sub_rn(a[e], mean), rstd);
 					if (p.ln & 2)
-						t = mul_rn(t, lng[k0 + e]);
+						t = mul_rn(t, gv[e]);
 					if (p.ln & 4)
-						t = add_rn(t, lnb[k0 + e]);
+						t = add_rn(t, bv[e]);
 					a[e] = t;
 				}
 			}
@@ -854,8 +854,13 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 	float *red = (float *)smem;
 #pragma unroll
 	for (int t = 0; t < NT; ++t) {
-		float v = acc[t] + __shfl_xor(acc[t], 16);
-		v += __shfl_xor(v, 32);
+		float v = acc[t] + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(acc[t]),
+									      0x401F));
+		{
+			const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+									 __float_as_uint(v), false, false);
+			v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+		}
 		if (g16 == 0)
 			red[wave * C::NR + t * 16 + l16] = v;
 	}
