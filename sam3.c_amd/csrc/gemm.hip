@@ -706,7 +706,11 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	 * applies them (S3K_EPI_COLSCALE), and only the MFMA epilogue takes
 	 * them (the skinny and generic kernels keep q*scale in f32) */
 	if ((g->flags & S3K_EPI_COLSCALE) ? (path != S3K_PATH_MFMA || !g->cs)
-					  : (path == S3K_PATH_MFMA && g->b_kind == S3K_Q8))
+					  : (path == S3K_PATH_MFMA && g->b_kind == S3K_Q8 &&
+					     !((g->flags & S3K_Q8_WAUTO) && s3k_dlq8_ok(g))))
+		return (int)hipErrorInvalidValue;
+	if ((g->flags & S3K_Q8_WAUTO) &&
+	    ((g->flags & S3K_EPI_COLSCALE) || path != S3K_PATH_MFMA || !s3k_dlq8_ok(g)))
 		return (int)hipErrorInvalidValue;
 	/* a LayerNorm's input rows as A: the streaming skinny kernel only */
 	if ((g->flags & S3K_A_LN) && path != S3K_PATH_SKINNY)

@@ -39,6 +39,67 @@ __device__ __forceinline__ uint32_t q8_pair_f16(uint32_t wx, uint32_t sel, q8h2_
 	return __builtin_bit_cast(uint32_t, h);
 }
 
+/* S3K_Q8_WAUTO after a k-loop run with factor 1: each lane holds the
+ * largest |scale| of its B rows (row wn0 + 32 j + (lane & 31)); a row's
+ * factor is s3k_q8_wfactors' 2^wscale_exp_of(127 * that). When a row of
+ * the workgroup's tile needs one (rare: rows of tiny or huge scales),
+ * q8_wauto_again returns true (workgroup-uniform) with binv set and the
+ * accumulators cleared, the caller runs its k-loop again, and
+ * q8_wauto_scale multiplies the accumulators of each column by its
+ * factor, as the S3K_EPI_COLSCALE epilogue does: the same bits. */
+template <int FM, int FN>
+__device__ __forceinline__ bool q8_wauto_again(s3k_f32x16 (&acc)[FM][FN], const float (&smax)[FN],
+					       float (&binv)[FN], int (&e)[FN])
+{
+	int any = 0;
+#pragma unroll
+	for (int j = 0; j < FN; ++j) {
+		e[j] = wscale_exp_of(smax[j] * 127.0f);
+		any |= e[j] != 0;
+	}
+	if (!__syncthreads_or(any))
+		return false;
+#pragma unroll
+	for (int j = 0; j < FN; ++j)
+		binv[j] = e[j] ? inv_pow2(pow2f(e[j])) : 1.0f;
+#pragma unroll
+	for (int i = 0; i < FM; ++i)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+#pragma unroll
+			for (int r = 0; r < 16; ++r)
+				acc[i][j][r] = 0.0f;
+	return true;
+}
+
+/* The factors reach the lanes holding each column through LDS (smem,
+ * free after the k-loop). Transposed accumulators: lane l holds columns
+ * 8t + 4(l >> 5) + q of each 32-column block. */
+template <int FM, int FN>
+__device__ __forceinline__ void q8_wauto_scale(s3k_f32x16 (&acc)[FM][FN], const int (&e)[FN],
+					       char *smem, int lane, int wn0)
+{
+	__syncthreads();
+	float *fac = (float *)smem;
+	if (lane < 32)
+#pragma unroll
+		for (int j = 0; j < FN; ++j)
+			fac[wn0 + j * 32 + lane] = pow2f(e[j]);
+	__syncthreads();
+#pragma unroll
+	for (int j = 0; j < FN; ++j) {
+		s3k_f32x16 f;
+#pragma unroll
+		for (int t = 0; t < 4; ++t) {
+			const float4 f4 = *(const float4 *)(fac + wn0 + j * 32 + 8 * t + 4 * (lane >> 5));
+			f[4 * t] = f4.x, f[4 * t + 1] = f4.y, f[4 * t + 2] = f4.z, f[4 * t + 3] = f4.w;
+		}
+#pragma unroll
+		for (int i = 0; i < FM; ++i)
+			acc[i][j] *= f;
+	}
+}
+
 template <int BM, int BN, int WGM, int WGN, int STAGES, int OCC>
 __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 {
@@ -143,6 +204,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 				acc[i][j][r] = 0.0f;
 
 	const int nk = p.K / BK;
+	/* S3K_Q8_WAUTO: the largest |scale| of each of this lane's B rows */
+	const bool wauto = (p.flags & S3K_Q8_WAUTO) != 0;
+	float smax[FN];
+#pragma unroll
+	for (int j = 0; j < FN; ++j)
+		smax[j] = 0.0f;
+
+	int fe[FN];
+	bool again = false;
+	for (int pass = 0;; ++pass) {
 #pragma unroll
 	for (int s = 0; s < STAGES - 1; ++s)
 		if (s < nk)
@@ -171,7 +242,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 			q8h2_t s2[2];
 #pragma unroll
 			for (int blk = 0; blk < 2; ++blk) {
-				const _Float16 sh = (_Float16)(*(const float *)(row + 36 * blk) * binv[j]);
+				const float sv = *(const float *)(row + 36 * blk);
+				smax[j] = fmaxf(smax[j], finite_abs(sv));
+				const _Float16 sh = (_Float16)(sv * binv[j]);
 				s2[blk] = (q8h2_t){sh, sh};
 			}
 #pragma unroll
@@ -209,7 +282,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlq8(GemmArgs p)
 					mfma_chunk<FAM_F16>(acc[i][j], bfr[ks][j], af[cur][i]);
 		}
 	}
-
+	if (!wauto || pass == 1 || !(again = q8_wauto_again<FM, FN>(acc, smax, binv, fe)))
+		break;
+	}
+	if (again)
+		q8_wauto_scale<FM, FN>(acc, fe, smem, lane, wn0);
 	__syncthreads();
 	write_tile_ck<FM, FN, WTN, S3K_F32, true>(p, acc, smem, wave, lane, tm * BM + wm0, tn * BN + wn0, bz);
 }
@@ -327,13 +404,21 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlpq(GemmArgs p)
 
 	uint4 af[2][FM], bf[2][FN];
 	q8h2_t s2[FN][2];
+	/* S3K_Q8_WAUTO: the largest |scale| of each of this lane's B rows */
+	const bool wauto = (p.flags & S3K_Q8_WAUTO) != 0;
+	float smax[FN];
+#pragma unroll
+	for (int j = 0; j < FN; ++j)
+		smax[j] = 0.0f;
 	auto scales = [&](int stg) {
 #pragma unroll
 		for (int j = 0; j < FN; ++j) {
 			const char *row = smem + stg * B_BYTES + brow[j];
 #pragma unroll
 			for (int blk = 0; blk < 2; ++blk) {
-				const _Float16 sh = (_Float16)(*(const float *)(row + 36 * blk) * binv[j]);
+				const float sv = *(const float *)(row + 36 * blk);
+				smax[j] = fmaxf(smax[j], finite_abs(sv));
+				const _Float16 sh = (_Float16)(sv * binv[j]);
 				s2[j][blk] = (q8h2_t){sh, sh};
 			}
 		}
@@ -405,31 +490,40 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlpq(GemmArgs p)
 	};
 
 	const int nk = p.K / BK;
-#pragma unroll
-	for (int t = 0; t < LOADS; ++t)
-		dma(0, t, 0);
-	if (nk > 1) {
+	int fe[FN];
+	bool again = false;
+	for (int pass = 0;; ++pass) {
 #pragma unroll
 		for (int t = 0; t < LOADS; ++t)
-			dma(1, t, 1);
-		wait_vm<LOADS>();
-	} else {
-		wait_vm<0>();
-	}
-	wg_barrier();
-	scales(0);
+			dma(0, t, 0);
+		if (nk > 1) {
 #pragma unroll
-	for (int r = 0; r < FM + FN; ++r)
-		frag(0, 0, 0, r);
-	int kt = 0;
-	for (; kt + 2 < nk; ++kt)
-		step(kt & 1, kt, true, true);
-	if (kt + 1 < nk) {
-		step(kt & 1, kt, true, false);
-		++kt;
+			for (int t = 0; t < LOADS; ++t)
+				dma(1, t, 1);
+			wait_vm<LOADS>();
+		} else {
+			wait_vm<0>();
+		}
+		wg_barrier();
+		scales(0);
+#pragma unroll
+		for (int r = 0; r < FM + FN; ++r)
+			frag(0, 0, 0, r);
+		int kt = 0;
+		for (; kt + 2 < nk; ++kt)
+			step(kt & 1, kt, true, true);
+		if (kt + 1 < nk) {
+			step(kt & 1, kt, true, false);
+			++kt;
+		}
+		step(kt & 1, kt, false, false);
+		/* the barrier in q8_wauto_again also keeps the next pass's
+		 * loads behind every wave's last fragment reads */
+		if (!wauto || pass == 1 || !(again = q8_wauto_again<FM, FN>(acc, smax, binv, fe)))
+			break;
 	}
-	step(kt & 1, kt, false, false);
-
+	if (again)
+		q8_wauto_scale<FM, FN>(acc, fe, smem, lane, wn0);
 	__syncthreads();
 	write_tile_ck<FM, FN, WTN, S3K_F32, true>(p, acc, smem, wave, lane, tm * BM + wm0,
 						 tn * BN + wn0, bz);

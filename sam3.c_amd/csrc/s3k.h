@@ -42,6 +42,12 @@ enum s3k_kind {
 #define S3K_EPI_QKV 32  /* f32 out, batch 1, direct-to-LDS GEMM only: the
 			 * result is stored as the head-split attention
 			 * operands (struct s3k_gemm, qkv_*) instead of C */
+#define S3K_Q8_WAUTO 256 /* MFMA Q8 kernels (gemm_dlq8, gemm_dlpq) without
+			  * S3K_EPI_COLSCALE: the kernel finds the weight-row
+			  * factors itself (127 * the largest |scale| of each
+			  * row, as s3k_q8_wfactors), running with factor 1 and
+			  * again with the factors when a row of the tile needs
+			  * one: the bits of the S3K_EPI_COLSCALE path */
 #define S3K_A_LN    128 /* A holds a LayerNorm's f32 input rows: the kernel
 			  * normalizes each row (eps 1e-5, gamma ln_g, beta
 			  * ln_b, either NULL) with the LayerNorm kernel's
@@ -334,6 +340,9 @@ struct s3h_settings {
 	int f32_split;                    /* SAM3_HIP_F32_SPLIT                  */
 	int unpartition_fold, residual_fold, gemm_operand, qkv_chain, ln_operand,
 	    permute_operand, partition_fold, qkv_fold, sdpa_merge, ln_gemv_fold;
+	int q8_wauto;                     /* SAM3_HIP_Q8_WAUTO: per-call weight-row
+					   * factors found by the Q8 GEMM (1) or
+					   * by a pass of their own (0)         */
 	int gemv_f32;                     /* SAM3_HIP_GEMV_F32: one f32 activation
 					   * row on the f32 VALU GEMV (1) or on
 					   * the f16 MFMA stream (0)           */

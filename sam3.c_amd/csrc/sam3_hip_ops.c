@@ -430,7 +430,8 @@ static enum sam3_error q8_colscale(struct s3k_gemm *g, void **own, void *stream)
 static enum sam3_error launch_a_safe(const struct s3k_gemm *g, int path, const char *what,
 				     void *stream)
 {
-	if (g->b_kind == S3K_Q8 && path == S3K_PATH_MFMA && !(g->flags & S3K_EPI_COLSCALE)) {
+	if (g->b_kind == S3K_Q8 && path == S3K_PATH_MFMA &&
+	    !(g->flags & (S3K_EPI_COLSCALE | S3K_Q8_WAUTO))) {
 		/* the MFMA kernels round q*scale to f16: with the weight-row
 		 * factors */
 		struct s3k_gemm h = *g;
@@ -577,6 +578,14 @@ static int prep_q8_cs(const void *w, void *out, int rows, int k, int k_out, int 
  * once there), else computed into scratch that *own returns for the
  * caller to free. A batch of distinct weights (stride_b != 0) gets the
  * factors of every slice, cs_sb = N apart. */
+/* Whether the MFMA kernel that g (Q8_0 weight) reaches finds the
+ * weight-row factors itself (S3K_Q8_WAUTO: gemm_dlq8 / gemm_dlpq on f16
+ * activations, or on the f16 copy of f32 / bf16 ones). */
+static int q8_wauto_ok(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && s3h_settings()->q8_wauto && s3k_dlq8_eligible(g);
+}
+
 static enum sam3_error q8_colscale(struct s3k_gemm *g, void **own, void *stream)
 {
 	*own = NULL;
@@ -585,6 +594,13 @@ static enum sam3_error q8_colscale(struct s3k_gemm *g, void **own, void *stream)
 		return SAM3_EINVAL;
 	}
 	const int nb = g->batch > 1 && g->stride_b != 0 ? g->batch : 1;
+	/* factors that would be made for this call alone: the kernel finds
+	 * them itself when it can (no pass over the weights first) */
+	if (q8_wauto_ok(g) &&
+	    (nb > 1 || !s3h_prep_cacheable(g->b, ((size_t)g->N * g->K + 31) / 32 * 36))) {
+		g->flags |= S3K_Q8_WAUTO;
+		return SAM3_OK;
+	}
 	void *cs = NULL;
 	enum sam3_error err;
 	if (nb == 1) {
@@ -1408,7 +1424,9 @@ enum sam3_error sam3_hip_matmul_q8_noalloc(int a_dtype, const void *a, const voi
 		if (err != SAM3_OK)
 			return err;
 	}
-	if (fac) {
+	if (fac && q8_wauto_ok(&g)) {
+		h.flags |= S3K_Q8_WAUTO; /* the kernel finds the weight-row factors */
+	} else if (fac) {
 		float *cs = (float *)((char *)buf + abuf);
 		err = s3h_hip(s3k_q8_wfactors(w, cs, K, N, 1, 1, 0, stream),
 			      "matmul_q8_noalloc weight factors");

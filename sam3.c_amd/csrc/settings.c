@@ -60,6 +60,7 @@ static void parse(struct s3h_settings *s)
 	s->sdpa_merge = env_on("SAM3_HIP_SDPA_MERGE");
 	s->ln_gemv_fold = env_on("SAM3_HIP_LN_GEMV_FOLD");
 	s->gemv_f32 = env_on("SAM3_HIP_GEMV_F32");
+	s->q8_wauto = env_on("SAM3_HIP_Q8_WAUTO");
 	const char *rb = getenv("SAM3_HIP_READBACK");
 	s->readback_all = rb && rb[0] == 'a' && rb[1] == 'l' && rb[2] == 'l' && !rb[3];
 	s->quiet = getenv("SAM3_HIP_QUIET") != NULL;

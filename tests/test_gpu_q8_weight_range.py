@@ -21,7 +21,7 @@ cannot hide under the others.
 import numpy as np
 import pytest
 
-from gpu_util import bf16_to_f32, oracle, ref_q8, require_gpu
+from gpu_util import assert_f32_close, bf16_to_f32, oracle, ref_q8, require_gpu
 from sam3_amd import abi, graph, hip, synth
 
 pytestmark = pytest.mark.gpu
@@ -203,3 +203,34 @@ def test_graph_small_weights_twice(kind):
             check(_out(y, (M, N)), ref, ln, wrows(wq, K, N), what=f"{kind} graph eval {ev}")
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("cfg,M", [(2, 300), (15, 300), (7, 20), (9, 77)])
+def test_q8_kernel_found_weight_factors_same_bits(env, cfg, M):
+    """Per-call weight-row factors found by the Q8 GEMM itself
+    (S3K_Q8_WAUTO: a k-loop with factor 1, run again with the factors when
+    a row of the tile needs one) give the bits of the factors computed by
+    a pass of their own (SAM3_HIP_Q8_WAUTO=0), rows of tiny and of huge
+    scales among ordinary ones, for the 128x128, the pipelined and the
+    small-M tiles; both within the f32 bound of the oracle."""
+    O = oracle()
+    N, K = 300, 512
+    wf = synth.randn(800 + cfg, (N, K), 0.02)
+    wf[3] *= np.float32(1e-7)
+    wf[150] *= np.float32(1e5)
+    wf[299] *= np.float32(3e-6)
+    w = O.q8_quantize(wf)
+    a = O.f32_to_fp16(synth.randn(801, (M, K))).reshape(M, K)
+    env.set("SAM3_HIP_Q8_EXPAND", 0)
+    env.set("SAM3_HIP_DLQ8_CFG", cfg)
+    outs = []
+    for mode in (1, 0):
+        env.set("SAM3_HIP_Q8_WAUTO", mode)
+        outs.append(hip.matmul(a, abi.F16, w, abi.Q8_0, abi.F32, M, N, K, flags=hip.B_NT,
+                               path=hip.PATH_MFMA))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = ref_q8(O.fp16_to_f32(a).reshape(M, K), w, K, N, nt=True)
+    for r in (3, 150, 299):
+        assert_f32_close(outs[0][:, r:r + 1], ref[:, r:r + 1], what=f"row {r}")
+    rest = np.setdiff1d(np.arange(N), [3, 150, 299])
+    assert_f32_close(outs[0][:, rest], ref[:, rest], what=f"cfg {cfg}")
