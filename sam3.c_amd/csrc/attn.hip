@@ -1029,28 +1029,49 @@ static bool attn_small_ok(int kind, const void *q, const void *k, const void *v,
 	       !(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u);
 }
 
-extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
-			      const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
-			      int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream)
+/* The kernel s3k_attn_heads(path, ...) runs for these arguments (0: it
+ * refuses them). */
+static int attn_heads_pick(int path, int kind, const void *q, const void *k, const void *v,
+			   void *out, int BH, int Sq, int Sk, int D, int oh, int ofmt)
 {
 	const int best = s3k_attn_path(kind, q, k, v, out, BH, Sq, Sk, D);
 	const bool small = attn_small_ok(kind, q, k, v, out, BH, Sq, Sk, D);
 	const bool small_fmt = oh >= 0 && !(oh > 0 && BH % oh) && ofmt >= 0 && ofmt <= 2 &&
 			       !(ofmt && oh <= 0);
-	if (path == S3K_ATTN_SMALL) {
-		if (!small || !small_fmt)
-			return (int)hipErrorInvalidValue;
-	} else if (path == 0 && small && small_fmt) {
+	if (path == S3K_ATTN_SMALL)
+		return small && small_fmt ? S3K_ATTN_SMALL : 0;
+	if (path == 0 && small && small_fmt) {
 		/* latency-bound sizes, by measured launch time (16 heads, f32,
 		 * in a HIP graph): up to 64 scores per head the one-wave-per-row
 		 * kernel (1 / 8 queries and keys: 3.3 / 4.4 us against 6.4 /
-		 * 6.2 for attn_fwd), from 65 keys this kernel (77: 9.7 against
-		 * 11.0), attn_fwd in between (32: 6.5 against 8.5) */
+		 * 6.2 for attn_fwd), from 65 keys the few-keys kernel (77: 9.7
+		 * against 11.0), attn_fwd in between (32: 6.5 against 8.5) */
 		if ((long long)Sq * Sk <= 64 && !ofmt)
-			path = S3K_ATTN_GENERIC;
-		else if (Sk > 64)
-			path = S3K_ATTN_SMALL;
+			return S3K_ATTN_GENERIC;
+		if (Sk > 64)
+			return S3K_ATTN_SMALL;
 	}
+	if (!best || (path == S3K_ATTN_MFMA && best != S3K_ATTN_MFMA) ||
+	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC) || oh < 0 ||
+	    (oh > 0 && BH % oh) || ofmt < 0 || ofmt > 2 ||
+	    (ofmt && (oh <= 0 || kind != S3K_F32 || best != S3K_ATTN_MFMA || path == S3K_ATTN_GENERIC)))
+		return 0;
+	return path == 0 ? best : path;
+}
+
+extern "C" int s3k_attn_heads_path(int kind, const void *q, const void *k, const void *v,
+				   void *out, int BH, int Sq, int Sk, int D, int oh, int ofmt)
+{
+	return attn_heads_pick(0, kind, q, k, v, out, BH, Sq, Sk, D, oh, ofmt);
+}
+
+extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
+			      const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
+			      int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream)
+{
+	path = attn_heads_pick(path, kind, q, k, v, out, BH, Sq, Sk, D, oh, ofmt);
+	if (!path)
+		return (int)hipErrorInvalidValue;
 	if (path == S3K_ATTN_SMALL) {
 		AttnGArgs g{};
 		g.q = (const char *)q;
@@ -1071,16 +1092,9 @@ extern "C" int s3k_attn_heads(int path, int kind, const void *q, const void *k, 
 		hipLaunchKernelGGL(attn_small, grid, dim3(256), 0, (hipStream_t)stream, g);
 		return (int)hipGetLastError();
 	}
-	if (!best || (path == S3K_ATTN_MFMA && best != S3K_ATTN_MFMA) ||
-	    (path != 0 && path != S3K_ATTN_MFMA && path != S3K_ATTN_GENERIC) || oh < 0 ||
-	    (oh > 0 && BH % oh) || ofmt < 0 || ofmt > 2 ||
-	    (ofmt && (oh <= 0 || kind != S3K_F32 || best != S3K_ATTN_MFMA || path == S3K_ATTN_GENERIC)))
-		return (int)hipErrorInvalidValue;
 	if ((long long)BH * Sq == 0)
 		return (int)hipSuccess;
 	const hipStream_t st = (hipStream_t)stream;
-	if (path == 0)
-		path = best;
 	if (path == S3K_ATTN_GENERIC) {
 		AttnGArgs g{};
 		g.q = (const char *)q;

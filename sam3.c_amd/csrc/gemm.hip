@@ -712,8 +712,9 @@ extern "C" int s3k_gemm_launch_path(const struct s3k_gemm *g, int path, void *st
 	if ((g->flags & S3K_Q8_WAUTO) &&
 	    ((g->flags & S3K_EPI_COLSCALE) || path != S3K_PATH_MFMA || !s3k_dlq8_ok(g)))
 		return (int)hipErrorInvalidValue;
-	/* a LayerNorm's input rows as A: the streaming skinny kernel only */
-	if ((g->flags & S3K_A_LN) && path != S3K_PATH_SKINNY)
+	/* a LayerNorm's input rows, or the v of one-key attention, as A:
+	 * the skinny kernels only */
+	if ((g->flags & (S3K_A_LN | S3K_A_ATT1)) && path != S3K_PATH_SKINNY)
 		return (int)hipErrorInvalidValue;
 	if (path == S3K_PATH_SKINNY) {
 		if (!s3k_skinny_ok(g))

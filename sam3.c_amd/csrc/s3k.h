@@ -52,6 +52,13 @@ enum s3k_kind {
 			  * normalizes each row (eps 1e-5, gamma ln_g, beta
 			  * ln_b, either NULL) with the LayerNorm kernel's
 			  * arithmetic before use (q8_stream only) */
+#define S3K_A_ATT1  512 /* A (one f32 row, batch 1) holds v of attention
+			  * heads of one query and one key each (q, k, v
+			  * [K / att_D heads, att_D]): the kernel forms the
+			  * attention output from it, score = dot(q, k) *
+			  * att_scale (+ att_mask[0]), p = expf(score - max),
+			  * out = fmaf(p, v, 0) * (1 / p), with attn_generic's
+			  * steps for a one-key row (q8_gemv only) */
 #define S3K_EPI_COLSCALE 64 /* out = acc * cs[n] first (with the row factor):
 			     * the weight-row factors of a Q8_0 weight
 			     * (s3k_q8_wfactors). Kernels that round q*scale
@@ -97,6 +104,11 @@ struct s3k_gemm {
 	long long   cs_sb;
 	/* S3K_A_LN: LayerNorm gamma and beta, f32 [K], 16-byte aligned */
 	const float *ln_g, *ln_b;
+	/* S3K_A_ATT1: q and k f32 [K] (16-byte aligned), the mask entry of
+	 * the query's one key (or NULL), the score scale, the head size */
+	const float *att_q, *att_k, *att_mask;
+	float        att_scale;
+	int          att_D;
 	/* f16 operand output (S3K_C_F16OP): when ovf is set, a value the f16
 	 * copy cannot hold (|x| >= 2^15, finite) stores ovf_tag to *ovf; when
 	 * rowf is set, output row m's parts store ovf_tag to rowf[2m] if they
@@ -216,6 +228,10 @@ int s3k_attn(int path, int kind, const void *q, const void *k, const void *v,
 int s3k_attn_heads(int path, int kind, const void *q, const void *k, const void *v,
 		   const float *mask, void *out, int BH, int Sq, int Sk, int D, int oh,
 		   int ofmt, unsigned *ovf, unsigned ovf_tag, void *stream);
+/* The kernel s3k_attn_heads(0, ...) runs for these arguments (S3K_ATTN_*,
+ * 0 when it refuses them). */
+int s3k_attn_heads_path(int kind, const void *q, const void *k, const void *v, void *out, int BH,
+			int Sq, int Sk, int D, int oh, int ofmt);
 /* ViT block ops (blockops.hip). LayerNorm over the last dim of rows x
  * cols (gamma/beta of the input's kind or NULL, eps 1e-5); RoPE on
  * interleaved pairs of x [batch, seq, heads, hd] with f32 cos/sin
@@ -343,6 +359,9 @@ struct s3h_settings {
 	int q8_wauto;                     /* SAM3_HIP_Q8_WAUTO: per-call weight-row
 					   * factors found by the Q8 GEMM (1) or
 					   * by a pass of their own (0)         */
+	int att_gemv_fold;                /* SAM3_HIP_ATT_GEMV_FOLD: attention of
+					   * one query over one key left to the
+					   * Q8_0 GEMV reading its output      */
 	int gemv_f32;                     /* SAM3_HIP_GEMV_F32: one f32 activation
 					   * row on the f32 VALU GEMV (1) or on
 					   * the f16 MFMA stream (0)           */

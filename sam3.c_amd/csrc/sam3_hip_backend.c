@@ -46,6 +46,7 @@
 #include "s3k.h"
 
 #include <hip/hip_runtime_api.h>
+#include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -71,6 +72,9 @@ struct s3h_res {
 	const void *ln[3];       /* fmt S3H_A_LN: the LayerNorm's input,
 				  * gamma and beta on the device (the
 				  * consuming GEMM normalizes as it reads) */
+	struct s3h_att1_in att;  /* fmt S3H_A_ATT1: the one-key attention's
+				  * q, k, v, mask entry, scale and head size
+				  * (the consuming GEMV forms its output)  */
 };
 
 /* A prepared copy of a constant weight (s3h_prep_*). */
@@ -554,6 +558,7 @@ static int consumer_operand_form(struct sam3_hip_backend *hb, const struct sam3_
 				 int j, const struct sam3_tensor *t, int row_len,
 				 struct use_map *uses, int *k_out);
 static int next_reader(const struct sam3_graph *g, int j, const struct sam3_tensor *t);
+static int dims_are(const struct sam3_tensor *t, int B, int S, int H, int D);
 
 /* gh_multihead_attention_rope's q, k and v preparation
  * (graph_helpers.c:721-882): SLICE of the fused qkv output's columns ->
@@ -727,6 +732,7 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 	const struct s3h_res *ae = res_find(hb, a->data);
 	const int a_fmt = ae ? ae->fmt : S3H_A_PLAIN;
 	struct s3h_ln_in ln_a = {NULL, NULL, NULL};
+	struct s3h_att1_in att_a;
 	enum sam3_error err = dev_in(hb, a, &da);
 	if (err == SAM3_OK && a_fmt == S3H_A_LN) {
 		/* A is a LayerNorm's output that did not run: the GEMM reads
@@ -735,6 +741,11 @@ static enum sam3_error run_matmul(struct sam3_hip_backend *hb, const struct sam3
 		ln_a.gamma = ae->ln[1];
 		ln_a.beta = ae->ln[2];
 		da = &ln_a;
+	} else if (err == SAM3_OK && a_fmt == S3H_A_ATT1) {
+		/* A is a one-key attention's merged output that did not run:
+		 * the GEMV forms it from q, k and v (sdpa_gemv_form) */
+		att_a = ae->att;
+		da = &att_a;
 	}
 	if (err == SAM3_OK)
 		err = dev_in(hb, bsrc, &db);
@@ -1104,6 +1115,86 @@ static enum sam3_error run_layernorm_gemv(struct sam3_hip_backend *hb, const str
 	e->ln[1] = ln->gamma;
 	e->ln[2] = ln->beta;
 	hb->stats.fused_nodes++;
+	return SAM3_OK;
+}
+
+/* gh_sdpa (graph_helpers.c:688-717) of one query over one key per head
+ * (the text encoder at one token, text_encoder.c:588-652), f32, batch 1,
+ * whose head-merged output (TRANSPOSE (0,2,1,3), then RESHAPE views) only
+ * a Q8_0 GEMM of one row reads: the attention does not run. The f32 GEMV
+ * forms its output from q, k and v (S3H_A_ATT1) with the steps of the
+ * kernel that would have run (attn_generic), so the bits are the same.
+ * No later node may write q, k, v or the mask, which the GEMV reads when
+ * it runs. Returns the transpose's node index (or -1) and fills at with
+ * device addresses. */
+static int sdpa_gemv_form(struct sam3_hip_backend *hb, const struct sam3_graph *g, int i,
+			  struct use_map *uses, const unsigned char *done, struct s3h_att1_in *at)
+{
+	const struct sam3_node *n = &g->nodes[i];
+	if (!s3h_settings()->att_gemv_fold || !s3h_settings()->sdpa_merge || !s3h_sdpa_node_ok(n))
+		return -1;
+	const struct sam3_tensor *q = n->inputs[0], *k = n->inputs[1], *v = n->inputs[2];
+	const struct sam3_tensor *mk = n->n_inputs > 3 ? n->inputs[3] : NULL, *o = n->output;
+	const int D = n->params[0];
+	if (q->dtype != SAM3_DTYPE_F32 || q->n_dims != 4 || q->dims[0] != 1 || q->dims[2] != 1)
+		return -1;
+	const int H = q->dims[1];
+	if (!dims_are(q, 1, H, 1, D) || !dims_are(k, 1, H, 1, D) || !dims_are(v, 1, H, 1, D) ||
+	    !dims_are(o, 1, H, 1, D) || uses_of(uses, o) != 1 || (mk && s3h_nelems(mk) != 1))
+		return -1;
+	const int j = next_reader(g, i + 1, o);
+	if (j < 0 || done[j])
+		return -1;
+	const struct sam3_node *t = &g->nodes[j];
+	if (t->op != SAM3_OP_TRANSPOSE || t->n_inputs < 1 || t->inputs[0] != o || !t->output ||
+	    t->params[0] != 0 || t->params[1] != 2 || t->params[2] != 1 || t->params[3] != 3 ||
+	    t->output->dtype != SAM3_DTYPE_F32 || !dims_are(t->output, 1, 1, H, D))
+		return -1;
+	struct gemm_reader r;
+	if (!find_gemm_reader(g, j, j + 1, t->output, uses, &r) || !r.nt ||
+	    r.w->dtype != SAM3_DTYPE_Q8_0 || r.M != 1 || r.K != H * D || written_after(g, i, q) ||
+	    written_after(g, i, k) || written_after(g, i, v) || written_after(g, i, mk))
+		return -1;
+	for (int m = i + 1; m < j; m++) {
+		const struct sam3_node *x = &g->nodes[m];
+		if (same_data(x->output, t->output))
+			return -1;
+	}
+	void *dq = NULL, *dk = NULL, *dv = NULL, *dm = NULL, *dw = NULL;
+	if (dev_in(hb, q, &dq) != SAM3_OK || dev_in(hb, k, &dk) != SAM3_OK ||
+	    dev_in(hb, v, &dv) != SAM3_OK || (mk && dev_in(hb, mk, &dm) != SAM3_OK) ||
+	    dev_in(hb, r.w, &dw) != SAM3_OK)
+		return -1;
+	/* the kernel the unfolded node would run, writing aligned rows */
+	static const float al[4] __attribute__((aligned(16)));
+	if (s3k_attn_heads_path(S3K_F32, dq, dk, dv, (void *)al, H, 1, 1, D, H, 0) !=
+	    S3K_ATTN_GENERIC)
+		return -1;
+	at->q = dq;
+	at->k = dk;
+	at->v = dv;
+	at->mask = dm;
+	at->scale = 1.0f / sqrtf((float)D);
+	at->D = D;
+	return s3h_matmul_att1_ok(r.w->dtype, dw, r.M, r.N, r.K, SAM3_HIP_B_NT, at) ? j : -1;
+}
+
+/* SDPA (and its head-merge TRANSPOSE t) left to the consuming GEMV: t's
+ * output holds the form S3H_A_ATT1 and the device addresses in at. */
+static enum sam3_error run_sdpa_gemv(struct sam3_hip_backend *hb, const struct sam3_node *t,
+				     const struct s3h_att1_in *at)
+{
+	void *dy = NULL;
+	enum sam3_error err = dev_out_fmt(hb, t->output, 256, S3H_A_ATT1, &dy, NULL);
+	if (err != SAM3_OK)
+		return err;
+	struct s3h_res *e = res_find(hb, t->output->data);
+	if (!e) {
+		s3h_error("graph_eval: attention output not resident");
+		return SAM3_EBACKEND;
+	}
+	e->att = *at;
+	hb->stats.fused_nodes += 2;
 	return SAM3_OK;
 }
 
@@ -1693,6 +1784,7 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 	int lrm[3] = {0, 0, 0}, lchain[8], lnc = 0;
 	const struct sam3_tensor *lt = NULL;
 	struct s3h_ln_in lng;
+	struct s3h_att1_in att1;
 
 	for (int i = 0; i < g->n_nodes && err == SAM3_OK;) {
 		const struct sam3_node *n = &g->nodes[i];
@@ -1731,6 +1823,11 @@ static enum sam3_error run_nodes(struct sam3_hip_backend *hb, const struct sam3_
 		} else if (n->op == SAM3_OP_TRANSPOSE && !perm_plain &&
 			   (ln_fmt = permute_operand_form(hb, g, i, &uses, &perm_k)) != S3H_A_PLAIN) {
 			err = run_permute_as(hb, n, ln_fmt, perm_k);
+		} else if (n->op == SAM3_OP_SDPA &&
+			   (merge_j = sdpa_gemv_form(hb, g, i, &uses, done, &att1)) >= 0) {
+			err = run_sdpa_gemv(hb, &g->nodes[merge_j], &att1);
+			if (err == SAM3_OK)
+				done[merge_j] = 1;
 		} else if (n->op == SAM3_OP_SDPA &&
 			   (merge_j = sdpa_merge_target(hb, g, i, &uses, done, &merge_fmt)) >= 0) {
 			err = run_sdpa_merged(hb, n, &g->nodes[merge_j], merge_fmt);

@@ -85,7 +85,7 @@ enum sam3_error s3h_bias_add(const struct sam3_node *node, void *stream);
  * producing A can write that form directly: S3H_A_PLANES = bf16 [M, 3K]
  * [hi|lo|hi] (the split f32 GEMM), S3H_A_F16 = f16 [M, K] (the Q8 GEMM
  * with f32 activations). s3h_matmul_fmt runs the GEMM on A in that form. */
-enum { S3H_A_PLAIN = 0, S3H_A_PLANES = 1, S3H_A_F16 = 2, S3H_A_LN = 3 };
+enum { S3H_A_PLAIN = 0, S3H_A_PLANES = 1, S3H_A_F16 = 2, S3H_A_LN = 3, S3H_A_ATT1 = 4 };
 /* S3H_A_LN: A is the output of a LayerNorm that did not run; the skinny
  * Q8_0 GEMM normalizes its input rows itself (S3K_A_LN). With this form
  * the `a` argument of the s3h_matmul_* functions points to this host
@@ -98,6 +98,19 @@ struct s3h_ln_in {
  * S3K_A_LN, the normalization bit-identical to the LayerNorm kernel's. */
 int s3h_matmul_ln_ok(int b_dt, const void *b, int M, int N, int K, int flags,
 		     const struct s3h_ln_in *ln);
+/* S3H_A_ATT1: A is the head-merged output of an attention of one query
+ * over one key per head (q, k, v [K / D heads, D] f32, mask: the entry
+ * of that key, or NULL) that did not run; the f32 GEMV forms it from v
+ * with the attention kernel's steps (S3K_A_ATT1). With this form the `a`
+ * argument points to this host struct of device pointers. */
+struct s3h_att1_in {
+	const float *q, *k, *v, *mask;
+	float scale;
+	int D;
+};
+/* Whether a Q8_0 GEMM of one row (b on the device) can read A as at. */
+int s3h_matmul_att1_ok(int b_dt, const void *b, int M, int N, int K, int flags,
+		       const struct s3h_att1_in *at);
 int s3h_matmul_a_format(int a_dt, const void *a, int b_dt, const void *b, int c_dt, int M, int N,
 			int K, int flags);
 enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, const void *b,

@@ -900,7 +900,45 @@ static void use_ln_input(struct s3k_gemm *g, const struct s3h_ln_in *ln)
 	g->ln_b = ln->beta;
 }
 
-/* The skinny launch takes g with its A as a LayerNorm's input. */
+/* g reads A as v of one-key attention heads (S3K_A_ATT1). */
+static void use_att1_input(struct s3k_gemm *g, const struct s3h_att1_in *at)
+{
+	g->a = at->v;
+	g->a_kind = S3K_F32;
+	g->lda = g->K;
+	g->flags |= S3K_A_ATT1;
+	g->att_q = at->q;
+	g->att_k = at->k;
+	g->att_mask = at->mask;
+	g->att_scale = at->scale;
+	g->att_D = at->D;
+}
+
+/* The forms whose A is a node that did not run (S3H_A_LN, S3H_A_ATT1):
+ * the skinny kernel computes it from that node's inputs as it reads. */
+static int a_folded(int a_fmt)
+{
+	return a_fmt == S3H_A_LN || a_fmt == S3H_A_ATT1;
+}
+
+/* The device rows a GEMM with A in form a_fmt reads. */
+static const void *a_rows(int a_fmt, const void *a)
+{
+	return a_fmt == S3H_A_LN     ? (const void *)((const struct s3h_ln_in *)a)->x
+	       : a_fmt == S3H_A_ATT1 ? (const void *)((const struct s3h_att1_in *)a)->v
+				     : a;
+}
+
+static void use_folded_input(struct s3k_gemm *g, int a_fmt, const void *a)
+{
+	if (a_fmt == S3H_A_LN)
+		use_ln_input(g, (const struct s3h_ln_in *)a);
+	else
+		use_att1_input(g, (const struct s3h_att1_in *)a);
+}
+
+/* The skinny launch takes g with its A as a LayerNorm's input (or v of
+ * one-key attention). */
 static int skinny_takes_ln(const struct s3k_gemm *g)
 {
 	return g->b_kind == S3K_Q8 && g->batch == 1 && s3k_gemm_path(g) == S3K_PATH_SKINNY &&
@@ -917,6 +955,19 @@ int s3h_matmul_ln_ok(int b_dt, const void *b, int M, int N, int K, int flags,
 	fill_gemm(&g, SAM3_DTYPE_F32, ln->x, b_dt, b, SAM3_DTYPE_F32, (void *)ln->x, M, N, K, NULL,
 		  flags);
 	use_ln_input(&g, ln);
+	return skinny_takes_ln(&g);
+}
+
+int s3h_matmul_att1_ok(int b_dt, const void *b, int M, int N, int K, int flags,
+		       const struct s3h_att1_in *at)
+{
+	if (b_dt != SAM3_DTYPE_Q8_0 || !(flags & SAM3_HIP_B_NT) || !at || !at->q || !at->k ||
+	    !at->v || !b || M != 1 || N <= 0 || K <= 0 || !s3h_settings()->att_gemv_fold)
+		return 0;
+	struct s3k_gemm g;
+	fill_gemm(&g, SAM3_DTYPE_F32, at->v, b_dt, b, SAM3_DTYPE_F32, (void *)at->v, M, N, K, NULL,
+		  flags);
+	use_att1_input(&g, at);
 	return skinny_takes_ln(&g);
 }
 
@@ -965,13 +1016,14 @@ enum sam3_error s3h_matmul_fmt(int a_fmt, int a_dt, const void *a, int b_dt, con
 		}
 		return f32_split_gemm(&g, a, stream);
 	}
-	if (a_fmt == S3H_A_LN) {
-		use_ln_input(&g, (const struct s3h_ln_in *)a);
+	if (a_folded(a_fmt)) {
+		use_folded_input(&g, a_fmt, a);
 		if (!skinny_takes_ln(&g)) {
-			s3h_error("matmul: the LayerNorm input cannot be read by this GEMM");
+			s3h_error("matmul: the folded input form %d cannot be read by this GEMM", a_fmt);
 			return SAM3_EINVAL;
 		}
-		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream), "matmul skinny (LN)");
+		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
+			       "matmul skinny (folded input)");
 	}
 	if (a_fmt == S3H_A_F16 && skinny_takes_f16(&g)) {
 		g.a_kind = S3K_F16;
@@ -1040,12 +1092,16 @@ static int skinny_res_fits(int a_fmt, const struct s3k_gemm *g)
 }
 
 /* s3h_matmul_res_ok / s3h_matmul_qkv_ok for A read as a LayerNorm's
- * input: the streaming skinny kernel with S3K_A_LN. */
-static int ln_skinny_fits(int a_dt, const void *a, int b_dt, const void *b, int M, int N, int K,
-			  int flags)
+ * input (the streaming skinny kernel with S3K_A_LN) or as v of one-key
+ * attention (the f32 GEMV with S3K_A_ATT1). */
+static int ln_skinny_fits(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M,
+			  int N, int K, int flags)
 {
-	return a_dt == SAM3_DTYPE_F32 && s3h_matmul_ln_ok(b_dt, b, M, N, K, flags,
-							   (const struct s3h_ln_in *)a);
+	if (a_dt != SAM3_DTYPE_F32)
+		return 0;
+	return a_fmt == S3H_A_LN
+		       ? s3h_matmul_ln_ok(b_dt, b, M, N, K, flags, (const struct s3h_ln_in *)a)
+		       : s3h_matmul_att1_ok(b_dt, b, M, N, K, flags, (const struct s3h_att1_in *)a);
 }
 
 /* Whether s3h_matmul_fmt_to can add an f32 [M, N] residual to this GEMM's
@@ -1053,8 +1109,8 @@ static int ln_skinny_fits(int a_dt, const void *a, int b_dt, const void *b, int 
 int s3h_matmul_res_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags)
 {
-	if (a_fmt == S3H_A_LN)
-		return ln_skinny_fits(a_dt, a, b_dt, b, M, N, K, flags);
+	if (a_folded(a_fmt))
+		return ln_skinny_fits(a_fmt, a_dt, a, b_dt, b, M, N, K, flags);
 	if (s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN))
 		return 1;
 	if (M <= 0 || N <= 0 || K <= 0 || !a || !b ||
@@ -1083,13 +1139,12 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 		s3h_error("matmul: cannot write form %d (M=%d N=%d K=%d)", out_fmt, M, N, K);
 		return SAM3_EINVAL;
 	}
-	if (a_fmt == S3H_A_LN && (out_fmt != S3H_A_PLAIN || row_map)) {
-		s3h_error("matmul: a LayerNorm input GEMM writes f32 rows only");
+	if (a_folded(a_fmt) && (out_fmt != S3H_A_PLAIN || row_map)) {
+		s3h_error("matmul: a folded input GEMM writes f32 rows only");
 		return SAM3_EINVAL;
 	}
 	struct s3k_gemm g;
-	fill_gemm(&g, a_dt, a_fmt == S3H_A_LN ? ((const struct s3h_ln_in *)a)->x : a, b_dt, b,
-		  SAM3_DTYPE_F32, c, M, N, K, bias, flags);
+	fill_gemm(&g, a_dt, a_rows(a_fmt, a), b_dt, b, SAM3_DTYPE_F32, c, M, N, K, bias, flags);
 	g.c_kind = out_fmt == S3H_A_PLANES ? S3K_C_PLANES
 		 : out_fmt == S3H_A_F16     ? S3K_C_F16OP
 					    : S3K_F32;
@@ -1113,10 +1168,10 @@ enum sam3_error s3h_matmul_fmt_to(int a_fmt, int out_fmt, int a_dt, const void *
 		g.rm_d1 = row_map[1];
 		g.rm_d2 = row_map[2];
 	}
-	if (a_fmt == S3H_A_LN) {
-		use_ln_input(&g, (const struct s3h_ln_in *)a);
+	if (a_folded(a_fmt)) {
+		use_folded_input(&g, a_fmt, a);
 		return s3h_hip(s3k_gemm_launch_path(&g, S3K_PATH_SKINNY, stream),
-			       "matmul skinny (LN)");
+			       "matmul skinny (folded input)");
 	}
 	if (b_dt == SAM3_DTYPE_F32)
 		return f32_split_gemm(&g, a_fmt == S3H_A_PLANES ? a : NULL, stream);
@@ -1151,10 +1206,11 @@ static void fill_qkv(struct s3k_gemm *g, const struct s3h_qkv *q)
 static int qkv_skinny(int a_fmt, int a_dt, const void *a, int b_dt, const void *b, int M, int N,
 		      int K, int flags)
 {
-	if (b_dt != SAM3_DTYPE_Q8_0 || a_dt != SAM3_DTYPE_F32 || !(flags & SAM3_HIP_B_NT))
+	if (b_dt != SAM3_DTYPE_Q8_0 || a_dt != SAM3_DTYPE_F32 || !(flags & SAM3_HIP_B_NT) ||
+	    a_fmt == S3H_A_ATT1)
 		return 0;
 	if (a_fmt == S3H_A_LN)
-		return ln_skinny_fits(a_dt, a, b_dt, b, M, N, K, flags);
+		return ln_skinny_fits(a_fmt, a_dt, a, b_dt, b, M, N, K, flags);
 	static const char al[16] __attribute__((aligned(16)));
 	struct s3k_gemm g;
 	fill_gemm(&g, a_dt, a, b_dt, b, SAM3_DTYPE_F32, (void *)al, M, N, K, NULL, flags);
@@ -1185,7 +1241,7 @@ int s3h_matmul_qkv_ok(int a_fmt, int a_dt, const void *a, int b_dt, const void *
 			return 0;
 	if (!q->rope && qkv_skinny(a_fmt, a_dt, a, b_dt, b, M, N, K, flags))
 		return 1;
-	return a_fmt != S3H_A_LN && K % 64 == 0 && q->S >= 32 &&
+	return !a_folded(a_fmt) && K % 64 == 0 && q->S >= 32 &&
 	       s3h_matmul_out_ok(a_fmt, a_dt, a, b_dt, b, M, N, K, flags, S3H_A_PLAIN);
 }
 

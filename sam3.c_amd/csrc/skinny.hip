@@ -219,6 +219,11 @@ struct StreamArgs {
 	 * gamma and beta are given */
 	int ln;
 	const float *ln_g, *ln_b;
+	/* S3K_A_ATT1 (q8_gemv): A is v of one-key attention heads of
+	 * 1 << att_dsh elements, formed from q, k and the mask entry */
+	int att, att_dsh;
+	const float *att_q, *att_k, *att_mask;
+	float att_scale;
 };
 
 template <int AK, int MR, int NT, int KC>
@@ -671,6 +676,18 @@ __global__ void __launch_bounds__(1024) q8_stream(StreamArgs p)
  * (xor 16, then 32) and the waves theirs through LDS in wave order:
  * deterministic. S3K_A_LN normalizes the row as q8_stream does
  * (layernorm_v's statistics and steps), with gamma and beta in LDS.
+ *
+ * S3K_A_ATT1: the row is the attention output of one query over one key
+ * per head (the text encoder at one token), formed from v as the
+ * attention kernel forms it (cpu_sdpa.c:49-159 for a one-key row):
+ * waves 0.. load q and k into LDS ahead of the weight ring, 1024
+ * elements each, and D/16 lanes per head chain the dot product's fmaf
+ * over d in order (16 elements per lane, the running sum handed on by
+ * lane shifts); the score s = dot * scale (+ the mask entry) gives
+ * attn_generic's softmax weight p = expf(s - max(-FLT_MAX, s)) (NaN
+ * scores drop out of its max) and 1 / p (0 unless p > 0), stored per
+ * head in LDS before the first chunk's barrier; each element is then
+ * fmaf(p, v, 0) * (1 / p), the kernel's accumulate-and-normalize steps.
  */
 template <int NT, int KC>
 __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
@@ -680,6 +697,8 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 	__shared__ __attribute__((aligned(1024))) char smem[C::LDS];
 	extern __shared__ __attribute__((aligned(16))) float lnsm[];
 	float *const lng = lnsm, *const lnb = lnsm + p.K, *const lnst = lnsm + 2 * p.K;
+	/* S3K_A_ATT1: q, k and per head (p, 1 / p) in the same space */
+	float *const atq = lnsm, *const atk = lnsm + p.K, *const atst = lnsm + 2 * p.K;
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 	const int g16 = lane >> 4, l16 = lane & 15;
 
@@ -728,6 +747,21 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 		}
 	};
 	const int nch = p.K / (KC * 32);
+
+	/* S3K_A_ATT1: wave w loads q and k elements [1024 w, 1024 w + 1024) */
+	const bool att_wave = p.att && wave * 1024 < p.K;
+	if (att_wave) {
+		const s3k_i32x4 rq = buf_rsrc(p.att_q, (unsigned)p.K * 4u);
+		const s3k_i32x4 rk = buf_rsrc(p.att_k, (unsigned)p.K * 4u);
+#pragma unroll
+		for (int j = 0; j < 4; ++j) {
+			const int e0 = wave * 1024 + j * 256;
+			if (e0 < p.K) {
+				dma16(atq + e0, rq, (unsigned)(e0 * 4 + lane * 16));
+				dma16(atk + e0, rk, (unsigned)(e0 * 4 + lane * 16));
+			}
+		}
+	}
 
 	if (p.ln) {
 		const int pieces = p.K / 256;
@@ -784,6 +818,52 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 		}
 		__syncthreads();
 	}
+	if (att_wave) {
+		/* the mask entry by a scalar load (lgkmcnt, not the vmcnt that
+		 * counts the DMAs), then this wave's q and k, whose DMAs were
+		 * issued before the prime */
+		const float att_mv =
+			p.att_mask ? *(const __attribute__((address_space(4))) float *)p.att_mask : 0.0f;
+		if (nch >= C::ST - 1)
+			wait_vm<(C::ST - 1) * C::NPW>();
+		else
+			wait_vm<0>();
+		const int lph = (1 << p.att_dsh) >> 4; /* lanes per head */
+		const int seg = lane & (lph - 1);
+		const int e0 = wave * 1024 + lane * 16;
+		float qv[16], kv[16];
+#pragma unroll
+		for (int i = 0; i < 16; i += 4) {
+			const float4 a4 = *(const float4 *)(atq + e0 + i);
+			const float4 b4 = *(const float4 *)(atk + e0 + i);
+			qv[i] = a4.x, qv[i + 1] = a4.y, qv[i + 2] = a4.z, qv[i + 3] = a4.w;
+			kv[i] = b4.x, kv[i + 1] = b4.y, kv[i + 2] = b4.z, kv[i + 3] = b4.w;
+		}
+		/* the dot's fmaf chain over d in order: after step t the lanes
+		 * of segments <= t hold their prefix */
+		float dot = 0.0f;
+		for (int t = 0; t < lph; ++t) {
+			const float prev = __shfl_up(dot, 1);
+			float d = seg == 0 ? 0.0f : prev;
+#pragma unroll
+			for (int i = 0; i < 16; ++i)
+				d = fmaf(qv[i], kv[i], d);
+			dot = d;
+		}
+		if (seg == lph - 1 && e0 < p.K) {
+			float sc = dot * p.att_scale;
+			if (p.att_mask)
+				sc += att_mv;
+			const float mt = sc != sc ? -__builtin_inff() : sc;
+			const float m_new = fmaxf(-3.402823466e38f, mt);
+			const float pj = expf(sc - m_new);
+			const int h = e0 >> p.att_dsh;
+			atst[2 * h] = pj;
+			atst[2 * h + 1] = pj > 0.0f ? 1.0f / pj : 0.0f;
+		}
+		/* the stores land before the first chunk's barrier */
+		__builtin_amdgcn_s_waitcnt(0xC07F);
+	}
 
 	float acc[NT];
 #pragma unroll
@@ -829,6 +909,14 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 						t = add_rn(t, bv[e]);
 					a[e] = t;
 				}
+			}
+			if (p.att) {
+				/* the attention kernel's fmaf(p, v, 0) * (1 / p) */
+				const int k0 = ch * (KC * 32) + kb * 32 + 8 * g16;
+				const float2 pw = *(const float2 *)(atst + 2 * (k0 >> p.att_dsh));
+#pragma unroll
+				for (int e = 0; e < 8; ++e)
+					a[e] = fmaf(pw.x, a[e], 0.0f) * pw.y;
 			}
 #pragma unroll
 			for (int t = 0; t < NT; ++t) {
@@ -931,6 +1019,20 @@ static bool stream_ln_ok(const struct s3k_gemm *g)
 	       !((uintptr_t)g->ln_b & 15u) && !(g->flags & S3K_EPI_ROWSCALE);
 }
 
+/* S3K_A_ATT1's conditions: one f32 row of K = heads * D (D a power of
+ * two from 16 to 1024, K <= 4096) on q8_gemv, q, k and v 16-byte
+ * aligned, no other input form or row factor. */
+static bool gemv_att_ok(const struct s3k_gemm *g)
+{
+	const int D = g->att_D;
+	return g->a_kind == S3K_F32 && g->M == 1 && g->batch == 1 && stream_ok(g) &&
+	       g->lda == g->K && g->K <= 4096 && D >= 16 && D <= 1024 && !(D & (D - 1)) &&
+	       g->K % D == 0 && g->att_q && g->att_k && !((uintptr_t)g->a & 15u) &&
+	       !((uintptr_t)g->att_q & 15u) && !((uintptr_t)g->att_k & 15u) &&
+	       !((uintptr_t)g->att_mask & 3u) &&
+	       !(g->flags & (S3K_A_LN | S3K_EPI_ROWSCALE | S3K_EPI_QKV)) && s3h_settings()->gemv_f32;
+}
+
 extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 {
 	if (g->b_kind != S3K_Q8 || !(g->flags & S3K_B_NT) || g->c_kind != S3K_F32 || g->batch < 1)
@@ -945,6 +1047,8 @@ extern "C" int s3k_skinny_ok(const struct s3k_gemm *g)
 	if (g->batch > 1 && !stream_ok(g))
 		return 0;
 	if ((g->flags & S3K_A_LN) && !stream_ln_ok(g))
+		return 0;
+	if ((g->flags & S3K_A_ATT1) && !gemv_att_ok(g))
 		return 0;
 	return 1;
 }
@@ -1078,7 +1182,15 @@ static int launch_gemv_k(const struct s3k_gemm *g, void *stream)
 	p.ln = (g->flags & S3K_A_LN) ? 1 | (g->ln_g ? 2 : 0) | (g->ln_b ? 4 : 0) : 0;
 	p.ln_g = g->ln_g;
 	p.ln_b = g->ln_b;
-	const size_t dyn = p.ln ? (size_t)(2 * g->K + 2) * 4 : 0;
+	p.att = (g->flags & S3K_A_ATT1) ? 1 : 0;
+	p.att_dsh = p.att ? __builtin_ctz((unsigned)g->att_D) : 0;
+	p.att_q = g->att_q;
+	p.att_k = g->att_k;
+	p.att_mask = g->att_mask;
+	p.att_scale = g->att_scale;
+	const size_t dyn = p.ln    ? (size_t)(2 * g->K + 2) * 4
+			   : p.att ? (size_t)(2 * g->K + 2 * (g->K >> p.att_dsh)) * 4
+				   : 0;
 	dim3 grid(p.groups, g->batch);
 	hipLaunchKernelGGL((q8_gemv<NT, KC>), grid, dim3(C::WV * 64), dyn, (hipStream_t)stream, p);
 	return (int)hipGetLastError();
@@ -1185,7 +1297,8 @@ static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
 
 extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 {
-	if ((g->flags & S3K_A_LN) && !stream_ln_ok(g))
+	if (((g->flags & S3K_A_LN) && !stream_ln_ok(g)) ||
+	    ((g->flags & S3K_A_ATT1) && !gemv_att_ok(g)))
 		return (int)hipErrorInvalidValue;
 	/* the head-split stores (no RoPE) exist in q8_stream only */
 	if ((g->flags & S3K_EPI_QKV) && (!stream_ok(g) || g->batch != 1 || g->qkv_rope))

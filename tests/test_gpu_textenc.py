@@ -198,3 +198,87 @@ def test_layernorm_gemv_fold_without_beta(affine, M, K, env):
         ln = ln * g_h
     assert_f32_close(on, ref_q8(ln.astype(np.float32), w_h, K, N, nt=True),
                      what=f"LN gemv fold {affine} M={M} K={K}")
+
+
+def test_one_token_attention_folded_into_the_gemv_keeps_the_bits(env):
+    """At one token the attention (one query over one key per head) does
+    not run on its own: the proj GEMV forms its output from q, k and v
+    with the attention kernel's steps for a one-key row, so two layers
+    give the same bits as with the attention kernel run first
+    (SAM3_HIP_ATT_GEMV_FOLD=0), with one kernel fewer per layer."""
+    n_layers = 2
+    G, out = build(1, n_layers, "q8", 1700)
+    on, st_on = _eval(G, out, (1, W))
+    env.set("SAM3_HIP_ATT_GEMV_FOLD", 0)
+    G, out = build(1, n_layers, "q8", 1700)
+    off, st_off = _eval(G, out, (1, W))
+    assert np.array_equal(on.view(np.uint32), off.view(np.uint32))
+    assert st_on.gpu_nodes == st_off.gpu_nodes - n_layers
+    assert st_on.fused_nodes == st_off.fused_nodes + n_layers
+
+
+def _same_bits_or_nan(a, b):
+    na, nb = np.isnan(a), np.isnan(b)
+    assert np.array_equal(na, nb)
+    assert np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["plain", "nomask", "mask_neg_inf", "mask_big_neg", "score_inf",
+                                  "q_nan", "v_neg_zero"])
+@pytest.mark.parametrize("H,D", [(16, 64), (8, 32), (4, 128)])
+def test_one_key_attention_gemv_fold_cases(case, H, D, env):
+    """SDPA of one query over one key per head -> TRANSPOSE (0,2,1,3) ->
+    RESHAPE -> Q8_0 linear (+ bias), folded and unfolded: the same bits,
+    NaN where the attention kernel gives NaN. The reference's softmax of
+    one key (cpu_sdpa.c:49-159): weight 1 for a finite score, so the
+    output is v; a -inf score leaves the sum 0 and the output 0; an
+    infinite or NaN score gives NaN (checked against the oracle's Q8_0
+    product of those rows)."""
+    O = oracle()
+    K, N = H * D, 512
+    rng = np.random.default_rng(1800 + H)
+    q_h = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    k_h = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    v_h = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    m_h = np.zeros((1, 1), np.float32)
+    if case == "mask_neg_inf":
+        m_h[0, 0] = -np.inf
+    elif case == "mask_big_neg":
+        m_h[0, 0] = np.float32(-1e9)
+    elif case == "score_inf":
+        q_h[0, 1, 0, :] = np.float32(1e30)
+        k_h[0, 1, 0, :] = np.float32(1e30)
+    elif case == "q_nan":
+        q_h[0, 2, 0, 5] = np.nan
+    elif case == "v_neg_zero":
+        v_h[0, 0, 0, :8] = np.float32(-0.0)
+    w_h = O.q8_quantize(synth.randn(1801, (N, K), 0.03))
+    b_h = synth.randn(1802, (N,), 0.1)
+
+    def run():
+        G = graph.Graph()
+        q, k, v = (G.tensor(abi.F32, (1, H, 1, D), t) for t in (q_h, k_h, v_h))
+        m = None if case == "nomask" else G.tensor(abi.F32, (1, 1), m_h)
+        a = G.permute(G.sdpa(q, k, v, m, D), (0, 2, 1, 3))
+        y = G.linear(G.reshape(a, [1, K]), G.tensor(abi.Q8_0, (N, K), w_h),
+                     G.tensor(abi.F32, (N,), b_h))
+        return _eval(G, y, (1, N))
+
+    on, st_on = run()
+    env.set("SAM3_HIP_ATT_GEMV_FOLD", 0)
+    off, st_off = run()
+    _same_bits_or_nan(on, off)
+    assert st_on.gpu_nodes == st_off.gpu_nodes - 1
+    # the attention output the reference forms, per head
+    att = v_h.reshape(H, D).copy()
+    if case == "mask_neg_inf":
+        att[:] = 0.0
+    elif case == "score_inf":
+        att[1] = np.nan
+    elif case == "q_nan":
+        att[2] = np.nan
+    ref = ref_q8(att.reshape(1, K), w_h, K, N, nt=True, bias=b_h).reshape(1, N)
+    if case in ("score_inf", "q_nan"):
+        assert np.isnan(on).all()
+    else:
+        assert_f32_close(on, ref, what=f"one-key attention gemv {case} H={H} D={D}")
