@@ -362,6 +362,9 @@ struct s3h_settings {
 	int att_gemv_fold;                /* SAM3_HIP_ATT_GEMV_FOLD: attention of
 					   * one query over one key left to the
 					   * Q8_0 GEMV reading its output      */
+	int gemv_tasks;                   /* SAM3_HIP_GEMV_TASKS: batches of one-row
+					   * GEMVs on the persistent q8_gemv_tasks
+					   * (1) or one workgroup per task (0)  */
 	int gemv_f32;                     /* SAM3_HIP_GEMV_F32: one f32 activation
 					   * row on the f32 VALU GEMV (1) or on
 					   * the f16 MFMA stream (0)           */

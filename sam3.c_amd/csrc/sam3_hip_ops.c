@@ -1373,8 +1373,8 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 	g.stride_b = stride_w;
 	g.stride_c = stride_c;
 	/* one f32 activation row: the f32 GEMV reads it as it is (a stream of
-	 * K = 256 weights runs faster on the tiled GEMM below: 4.4 against
-	 * 3.2 TB/s) */
+	 * K = 256 weights runs faster on the tiled GEMM below: 3.7 against
+	 * 3.2-3.3 TB/s, the persistent q8_gemv_tasks included) */
 	if (a_dtype == SAM3_DTYPE_F32 && M == 1 && K % 256 == 0 && (K > 256 || batch == 1) &&
 	    s3h_settings()->gemv_f32 &&
 	    s3h_settings()->q8_batch_path != 2 && s3k_gemm_path(&g) == S3K_PATH_SKINNY)

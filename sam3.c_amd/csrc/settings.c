@@ -60,6 +60,7 @@ static void parse(struct s3h_settings *s)
 	s->sdpa_merge = env_on("SAM3_HIP_SDPA_MERGE");
 	s->ln_gemv_fold = env_on("SAM3_HIP_LN_GEMV_FOLD");
 	s->att_gemv_fold = env_on("SAM3_HIP_ATT_GEMV_FOLD");
+	s->gemv_tasks = env_on("SAM3_HIP_GEMV_TASKS");
 	s->gemv_f32 = env_on("SAM3_HIP_GEMV_F32");
 	s->q8_wauto = env_on("SAM3_HIP_Q8_WAUTO");
 	const char *rb = getenv("SAM3_HIP_READBACK");

@@ -224,9 +224,10 @@ struct StreamArgs {
 	int att, att_dsh;
 	const float *att_q, *att_k, *att_mask;
 	float att_scale;
+	int nbatch;                /* q8_gemv_tasks: weight matrices        */
 };
 
-template <int AK, int MR, int NT, int KC>
+template <int AK, int MR, int NT, int KC, int RKB = 76>
 struct StreamCfg {
 	static constexpr int ES = AK == S3K_F32 ? 4 : 2;
 	static constexpr int WV = 16;                    /* waves per workgroup      */
@@ -244,9 +245,11 @@ struct StreamCfg {
 	static constexpr int I = IW + IA;
 	static constexpr int NPW = (I + WV - 1) / WV;    /* loads per wave per chunk */
 	static constexpr int SW = IW * 1024, SB = I * 1024;
-	/* ring budget ~76 KiB: two workgroups per CU, so one's start hides
-	 * the other's drain (a deeper ring measured no faster) */
-	static constexpr int ST0 = (76 * 1024) / SB;
+	/* ring budget RKB KiB: 76 lets two workgroups share a CU, so one's
+	 * start hides the other's drain (a deeper ring measured no faster
+	 * for q8_stream and q8_gemv); q8_gemv_tasks, one workgroup per CU
+	 * for the whole launch, takes 144 */
+	static constexpr int ST0 = (RKB * 1024) / SB;
 	static constexpr int ST1 = ST0 < 2 ? 2 : ST0 > 16 ? 16 : ST0;
 	static constexpr int ST = (ST1 - 1) * NPW > 63 ? 63 / NPW + 1 : ST1; /* ring depth */
 	static constexpr int RED = WV * NT * MT * 1024;
@@ -978,6 +981,154 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
 	}
 }
 
+/*
+ * q8_gemv_tasks: q8_gemv over a batch of weight matrices (config 4's
+ * streams of one activation row) as a persistent grid of one workgroup
+ * per CU. The tasks are (copy z, weight-row group g), task t = z * groups
+ * + g; workgroup w runs tasks w, w + G, w + 2G, ... (G workgroups) and
+ * streams all their chunks through one ring, so the loads of a task's
+ * first chunks are in flight while the previous task's last chunks are
+ * multiplied; no workgroup starts or drains per task. At a task's last
+ * chunk the waves' sums go through LDS (the row's 4 lanes, then the
+ * waves in order) and the epilogue stores the task's outputs: the
+ * arithmetic of q8_gemv, so the same bits. Rows are whole groups (N %
+ * NR == 0) and K whole chunks; bias and GELU only.
+ */
+template <int NT, int KC>
+__global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
+{
+	using C = StreamCfg<S3K_F32, 1, NT, KC, 144>;
+	constexpr int WV = C::WV;
+	__shared__ __attribute__((aligned(1024))) char smem[C::ST * C::SB + 1024];
+	__shared__ float red[WV * C::NR];
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* wave-uniform LDS addresses */
+	const int g16 = lane >> 4, l16 = lane & 15;
+
+	const unsigned rowbytes = (unsigned)(p.K / 32) * 36u;
+	const int nch = p.K / (KC * 32);
+	const int ntask = p.groups * p.nbatch;
+	const int G = (int)gridDim.x;
+	const int mine = (ntask - (int)blockIdx.x + G - 1) / G;
+	const int total = mine * nch;
+
+	/* per-lane part of the loads of a chunk (the task's rows and k go in
+	 * the scalar offset) */
+	unsigned off[C::NPW];
+#pragma unroll
+	for (int t = 0; t < C::NPW; ++t) {
+		const int j = t * C::WV + wave;
+		unsigned o = S3K_OOB;
+		if (j < C::IW) {
+			const int i = j * 64 + lane;
+			const int r = i / C::PW, q = i % C::PW;
+			if (i < C::GW && q < C::GPRW)
+				o = (unsigned)r * rowbytes + (unsigned)q * 16u;
+		} else if (j < C::I) {
+			const int i = (j - C::IW) * 64 + lane;
+			if (i < C::GAR)
+				o = (unsigned)(i * 16);
+		}
+		off[t] = o;
+	}
+	const unsigned lds0 = lds_addr_of(smem);
+	auto issue = [&](int c) {
+		const int i = c / nch, ch = c - i * nch;
+		const int task = (int)blockIdx.x + i * G;
+		const int z = task / p.groups, g = task - z * p.groups;
+		const s3k_i32x4 rw = buf_rsrc(p.w + z * p.sw_b, p.w_ext);
+		const s3k_i32x4 ra = buf_rsrc(p.a + z * p.sa_b, (unsigned)(p.K * 4));
+		const unsigned wso = (unsigned)g * C::NR * rowbytes + (unsigned)ch * (KC * 36);
+		const unsigned aso = (unsigned)ch * (KC * 32 * 4);
+		const unsigned st = lds0 + (unsigned)((c % C::ST) * C::SB);
+#pragma unroll
+		for (int t = 0; t < C::NPW; ++t) {
+			const int j = t * C::WV + wave;
+			if (j < C::IW)
+				dma16s(st + j * 1024, rw, off[t], wso);
+			else if (j < C::I)
+				dma16s(st + C::SW + (j - C::IW) * 1024, ra, off[t], aso);
+			else
+				dma16s(lds0 + C::ST * C::SB, rw, S3K_OOB, 0);
+		}
+	};
+
+#pragma unroll
+	for (int s = 0; s < C::ST - 1; ++s)
+		if (s < total)
+			issue(s);
+
+	float acc[NT];
+#pragma unroll
+	for (int t = 0; t < NT; ++t)
+		acc[t] = 0.0f;
+	for (int c = 0; c < total; ++c) {
+		if (c + C::ST - 2 < total)
+			wait_vm<(C::ST - 2) * C::NPW>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (c + C::ST - 1 < total)
+			issue(c + C::ST - 1);
+		const int i = c / nch, ch = c - i * nch;
+		if (C::CW >= WV || wave < C::CW) {
+			const char *Ws = smem + (c % C::ST) * C::SB;
+			const char *As = Ws + C::SW;
+#pragma unroll
+			for (int u = 0; u < C::U; ++u) {
+				const int kb = u * C::CW + wave;
+				const int q0 = kb * 8 + 2 * g16;
+				const float4 x = *(const float4 *)(As + (q0 << 4));
+				const float4 y = *(const float4 *)(As + ((q0 + 1) << 4));
+				const float a[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+				for (int t = 0; t < NT; ++t) {
+					const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
+					const float sc = *(const float *)blk;
+					const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16);
+					const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16);
+					float s8 = 0.0f;
+#pragma unroll
+					for (int e = 0; e < 4; ++e)
+						s8 = fmaf(a[e], (float)(int)(signed char)(w0 >> (8 * e)), s8);
+#pragma unroll
+					for (int e = 0; e < 4; ++e)
+						s8 = fmaf(a[4 + e], (float)(int)(signed char)(w1 >> (8 * e)), s8);
+					acc[t] = fmaf(sc, s8, acc[t]);
+				}
+			}
+		}
+		if (ch == nch - 1) {
+			/* the task's sums: the row's 4 lanes, then the waves in order */
+#pragma unroll
+			for (int t = 0; t < NT; ++t) {
+				float v = acc[t] + __int_as_float(__builtin_amdgcn_ds_swizzle(
+							   __float_as_int(acc[t]), 0x401F));
+				const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+										 __float_as_uint(v), false, false);
+				v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+				if (g16 == 0)
+					red[wave * C::NR + t * 16 + l16] = v;
+				acc[t] = 0.0f;
+			}
+			__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+			wg_barrier();
+			if (threadIdx.x < C::NR) {
+				const int task = (int)blockIdx.x + i * G;
+				const int z = task / p.groups, g = task - z * p.groups;
+				const int n = g * C::NR + (int)threadIdx.x;
+				float sum = 0.0f;
+#pragma unroll
+				for (int w = 0; w < WV; ++w)
+					sum += red[w * C::NR + threadIdx.x];
+				const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
+				((float *)p.c + z * p.sc)[n] = epilogue<0>(sum, bv, p.flags);
+			}
+		}
+	}
+	wait_vm<0>();
+}
+
 } /* namespace s3k */
 
 using namespace s3k;
@@ -1196,6 +1347,51 @@ static int launch_gemv_k(const struct s3k_gemm *g, void *stream)
 	return (int)hipGetLastError();
 }
 
+/* q8_gemv_tasks' conditions: a batch of weight matrices times one f32
+ * row each (or one shared row), whole row groups of 16 * nt and whole
+ * chunks, bias and GELU only, enough tasks to keep one workgroup per CU
+ * busy. (Measured on config 4's streams against 64 rows and 16 k-blocks
+ * per chunk: 8-block chunks with 6 in flight 4.1-4.6 TB/s, 32-block
+ * chunks of 32 or 16 rows 3.5-6.1, against 5.5-6.3.) */
+static bool gemv_tasks_ok(const struct s3k_gemm *g, int nt, int kc)
+{
+	return g->a_kind == S3K_F32 && g->M == 1 && g->batch > 1 && g->N % (16 * nt) == 0 &&
+	       g->K % (kc * 32) == 0 && stream_ok(g) && s3h_settings()->gemv_tasks &&
+	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT)) &&
+	       (long long)(g->N / (16 * nt)) * g->batch >= 256;
+}
+
+template <int NT, int KC>
+static int launch_gemv_tasks_k(const struct s3k_gemm *g, void *stream)
+{
+	using C = StreamCfg<S3K_F32, 1, NT, KC, 144>;
+	StreamArgs p;
+	memset(&p, 0, sizeof p);
+	p.a = (const char *)g->a;
+	p.w = (const char *)g->b;
+	p.c = (char *)g->c;
+	p.bias = (const char *)g->bias;
+	p.M = 1;
+	p.N = g->N;
+	p.K = g->K;
+	p.lda_b = g->lda * 4;
+	p.ldc = g->ldc;
+	p.sa_b = g->stride_a * 4;
+	p.sw_b = g->stride_b;
+	p.sc = g->stride_c;
+	p.w_ext = (unsigned)((long long)g->N * (g->K / 32) * 36);
+	p.flags = g->flags;
+	p.groups = g->N / C::NR;
+	p.zsplit = 1;
+	p.nbatch = g->batch;
+	/* one workgroup per CU of the MI355X (256), fewer for fewer tasks */
+	const long long ntask = (long long)p.groups * g->batch;
+	const int grid = ntask < 256 ? (int)ntask : 256;
+	hipLaunchKernelGGL((q8_gemv_tasks<NT, KC>), dim3(grid), dim3(C::WV * 64), 0, (hipStream_t)stream,
+			   p);
+	return (int)hipGetLastError();
+}
+
 template <int AK, int KC>
 static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *stream)
 {
@@ -1311,6 +1507,10 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 		const bool k16 = g->K % 512 == 0 && mr <= 16;
 		/* one f32 activation row: the f32 VALU kernel */
 		if (g->a_kind == S3K_F32 && g->M == 1 && g->lda % 4 == 0 && s3h_settings()->gemv_f32) {
+			/* a batch: the persistent grid over (copy, row group) tasks */
+			if (gemv_tasks_ok(g, 4, k16 ? 16 : 8))
+				return k16 ? launch_gemv_tasks_k<4, 16>(g, stream)
+					   : launch_gemv_tasks_k<4, 8>(g, stream);
 			if (nt == 1)
 				return k16 ? launch_gemv_k<1, 16>(g, stream) : launch_gemv_k<1, 8>(g, stream);
 			if (nt == 2)

@@ -611,6 +611,47 @@ def test_q8_gemv_f32_one_row(env, K, N):
     assert_f32_close(c16, refs[0], what="f16 stream")
 
 
+@pytest.mark.parametrize("K,N,B,shared", [(1024, 1024, 20, True), (4096, 1024, 5, False),
+                                           (512, 256, 70, True), (512, 2048, 9, False)])
+def test_q8_gemv_tasks_persistent_batch(env, K, N, B, shared):
+    """A batch of one-row GEMVs with at least 256 (copy, 64-row group)
+    tasks runs on the persistent q8_gemv_tasks (one workgroup per CU,
+    workgroups taking one or several tasks): the same arithmetic as the
+    one-workgroup-per-task GEMV, so the same bits as each copy launched on
+    its own and as SAM3_HIP_GEMV_TASKS=0; bias and GELU in the epilogue;
+    the activations shared (stride 0) or one row per copy; within f32
+    rounding of the oracle."""
+    O = oracle()
+    a = rnd(720 + K, (1 if shared else B, K))
+    ws = [q8(rnd(721 + s_, (N, K), 0.02)) for s_ in range(B)]
+    bias = rnd(722, N, 0.1)
+    dw = hip.DeviceBuffer.of(np.concatenate(ws))
+    da, db = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(bias)
+
+    def run():
+        dc = hip.DeviceBuffer(B * N * 4)
+        hip.q8_batched_dev(abi.F32, da.ptr, dw.ptr, dc.ptr, B, 1, N, K, 0 if shared else K,
+                           ws[0].nbytes, N, bias_ptr=db.ptr, flags=hip.BIAS | hip.GELU)
+        hip.synchronize()
+        c = dc.download(np.float32, (B, N))
+        dc.free()
+        return c
+
+    c = run()
+    env.set("SAM3_HIP_GEMV_TASKS", 0)
+    c0 = run()
+    assert np.array_equal(c.view(np.uint32), c0.view(np.uint32))
+    for s_ in range(B):
+        row = a[0 if shared else s_].reshape(1, K)
+        one = hip.matmul(row, abi.F32, ws[s_], abi.Q8_0, abi.F32, 1, N, K, bias=bias,
+                         flags=hip.B_NT | hip.BIAS | hip.GELU)
+        assert np.array_equal(c[s_].view(np.uint32), one.reshape(N).view(np.uint32)), s_
+        ref = O.gelu(O.bias_add(ref_q8(row, ws[s_], K, N, nt=True), bias, "f32"), "f32")
+        assert_f32_close(c[s_].reshape(1, N), np.asarray(ref).reshape(1, N), what=f"task batch {s_}")
+    for b_ in (da, db, dw):
+        b_.free()
+
+
 def test_q8_batched_falls_back_per_slice():
     """M > 128 is not a skinny problem: one launch per slice, same result."""
     B, M, N, K = 2, 160, 64, 256
