@@ -244,7 +244,8 @@ def vit_block_bench(is_global, wkind, steps=5, warmup=2):
     fl = vit_block_flops(npos, e, heads, mlp, npos if is_global else window * window)
     return {"ms": round(ms, 3), "tokens_per_s": round(npos / (ms * 1e-3), 1),
             "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "nodes": G.g.n_nodes,
-            "gpu_nodes": st.gpu_nodes, "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes}
+            "gpu_nodes": st.gpu_nodes, "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes,
+            "range_reruns": st.range_reruns}
 
 
 def vit_trunk_bench(wkind, depth=32, per_graph=4, steps=3, warmup=1):
@@ -369,6 +370,7 @@ def text_encoder_bench(seqs=(1, 8, 32, 77), layers=24, per_graph=4, steps=3, war
         out[f"seq{seq}"] = {"ms": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
                             "weights_gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                             "gpu_nodes_per_eval": st.gpu_nodes, "fused_nodes_per_eval": st.fused_nodes,
+                            "range_reruns": st.range_reruns,
                             "nodes_per_eval": graphs[0].g.n_nodes}
         log(f"  seq {seq}: {out[f'seq{seq}']}")
     out["note"] = (f"{layers} layers, {per_graph} per graph_eval, Q8_0 weights "
@@ -617,7 +619,8 @@ def neck_bench(steps=10, warmup=2):
         xd.free()
     return {"ms": round(ms, 3), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
             "gflop": round(fl / 1e9, 1), "nodes": G.g.n_nodes, "gpu_nodes": st.gpu_nodes,
-            "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes}
+            "fused_nodes": st.fused_nodes, "host_nodes": st.host_nodes,
+            "range_reruns": st.range_reruns}
 
 
 def measured_traffic(key):
