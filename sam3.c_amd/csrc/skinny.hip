@@ -1425,8 +1425,10 @@ static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *strea
  *   - One small launch, M <= 32: its time is one workgroup's latency, so
  *     rows go to as many CUs as possible (NT = 1), with M split when that
  *     evens out the bytes a CU moves. Estimate: the largest of per-CU time
- *     ceil(WGs/256) * bytes per WG / 32 B/clk, HBM time weight bytes /
- *     2600 B/clk (about 6.2 TB/s) and L2 time WGs * bytes per WG /
+ *     ceil(WGs/256) * bytes per WG / 32 B/clk (activation bytes counted
+ *     at half: L2 serves them), HBM time weight bytes times
+ *     (1 + (groups - 1) / 2) / 2600 B/clk (about 6.2 TB/s; each group of
+ *     activation rows reads the weights) and L2 time WGs * bytes per WG /
  *     10000 B/clk; ties go to more workgroups.
  *   - One small launch, M > 32: MR = 32 with NT = 4 when that still makes
  *     128 workgroups, else MR = 16 with NT = 2.
@@ -1475,10 +1477,17 @@ static void stream_pick(const struct s3k_gemm *g, int *mr_out, int *nt_out)
 		const long long z = (g->M + mr - 1) / mr;
 		if (z > 8)
 			continue;
-		const double per = 16.0 * K * 1.125 + (mr < M ? mr : M) * K * es;
+		/* bytes a workgroup moves: its 16 weight rows from HBM, and its
+		 * activation rows, which every workgroup of the launch reads and
+		 * L2 serves, at half weight (the text encoder's qkv at 32 tokens,
+		 * N 3072: 32-row tiles 13.0 us, 16 15.6, 8 18.2) */
+		const double per = 16.0 * K * 1.125 + 0.5 * (mr < M ? mr : M) * K * es;
 		const long long wgs = (long long)((g->N + 15) / 16) * z;
 		double t = (double)((wgs + 255) / 256) * per / 32.0;
-		const double th = N * K * 1.125 / 2600.0, tl = (double)wgs * per / 10000.0;
+		/* HBM: each of the z activation groups reads the weights, and L2
+		 * catches about half of the repeats */
+		const double th = N * K * 1.125 * (1.0 + 0.5 * (double)(z - 1)) / 2600.0;
+		const double tl = (double)wgs * per / 10000.0;
 		t = t > th ? t : th;
 		t = t > tl ? t : tl;
 		if (t < best_t * 0.97 || (t <= best_t * 1.03 && wgs > best_w && wgs <= 512)) {
