@@ -278,6 +278,9 @@ int s3k_skinny_scales_rows(const struct s3k_gemm *g);
 /* Whether the skinny kernels take g as it is (shape, kinds, alignment,
  * and for S3K_A_LN the streaming kernel's conditions). */
 int s3k_skinny_ok(const struct s3k_gemm *g);
+/* Whether a batched one-row skinny launch of g runs on the persistent
+ * q8_gemv_tasks. */
+int s3k_gemv_tasks_take(const struct s3k_gemm *g);
 /* Attention operands [B, H, S, D] (f32), up to three (n_out) in one
  * launch: out[y] from columns col0[y].. of rows of `pitch` values holding
  * [B*S, H*D] (the q, k or v part of a fused qkv output), with RoPE

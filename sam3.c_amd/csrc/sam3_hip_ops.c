@@ -1373,9 +1373,10 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 	g.stride_b = stride_w;
 	g.stride_c = stride_c;
 	/* one f32 activation row: the f32 GEMV reads it as it is (a stream of
-	 * K = 256 weights runs faster on the tiled GEMM below: 3.7 against
-	 * 3.2-3.3 TB/s, the persistent q8_gemv_tasks included) */
-	if (a_dtype == SAM3_DTYPE_F32 && M == 1 && K % 256 == 0 && (K > 256 || batch == 1) &&
+	 * K = 256 weights only on the persistent q8_gemv_tasks, 4.35 TB/s;
+	 * one workgroup per task would give 3.2, the tiled GEMM below 3.7) */
+	if (a_dtype == SAM3_DTYPE_F32 && M == 1 && K % 256 == 0 &&
+	    (K > 256 || batch == 1 || s3k_gemv_tasks_take(&g)) &&
 	    s3h_settings()->gemv_f32 &&
 	    s3h_settings()->q8_batch_path != 2 && s3k_gemm_path(&g) == S3K_PATH_SKINNY)
 		return s3h_hip(s3k_gemm_launch(&g, stream), "matmul_q8_batched gemv");

@@ -991,8 +991,11 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
  * multiplied; no workgroup starts or drains per task. At a task's last
  * chunk the waves' sums go through LDS (the row's 4 lanes, then the
  * waves in order) and the epilogue stores the task's outputs: the
- * arithmetic of q8_gemv, so the same bits. Rows are whole groups (N %
- * NR == 0) and K whole chunks; bias and GELU only.
+ * arithmetic of q8_gemv<NT, KC>, so its bits (a launch of one copy runs
+ * 16-block chunks when K % 512 == 0, which split k over the waves
+ * differently from 8-block ones; with KC = 8 for such K the sums agree
+ * to a few ulps). Rows are whole groups (N % NR == 0) and K whole
+ * chunks; bias and GELU only.
  */
 template <int NT, int KC>
 __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
@@ -1351,14 +1354,35 @@ static int launch_gemv_k(const struct s3k_gemm *g, void *stream)
  * row each (or one shared row), whole row groups of 16 * nt and whole
  * chunks, bias and GELU only, enough tasks to keep one workgroup per CU
  * busy. (Measured on config 4's streams against 64 rows and 16 k-blocks
- * per chunk: 8-block chunks with 6 in flight 4.1-4.6 TB/s, 32-block
- * chunks of 32 or 16 rows 3.5-6.1, against 5.5-6.3.) */
+ * per chunk: 64 rows in 8-block chunks with 6 in flight 4.1-4.6 TB/s,
+ * 32-block chunks of 32 or 16 rows 3.5-6.1, against 5.5-6.3.) */
 static bool gemv_tasks_ok(const struct s3k_gemm *g, int nt, int kc)
 {
 	return g->a_kind == S3K_F32 && g->M == 1 && g->batch > 1 && g->N % (16 * nt) == 0 &&
 	       g->K % (kc * 32) == 0 && stream_ok(g) && s3h_settings()->gemv_tasks &&
 	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT)) &&
 	       (long long)(g->N / (16 * nt)) * g->batch >= 256;
+}
+
+/* The persistent GEMV's row groups for g: 128 rows in 8-block chunks up
+ * to K = 1024, 64 rows in 16-block chunks above (config 4's streams, one
+ * box: K 256 4.35 against 3.6-3.7 TB/s for 64-row tasks, K 1024
+ * 5.7-5.9 against 5.5, K 4096 6.1-6.2 against 6.3; giving the 8-block
+ * chunks the 16-block chunks' split of k over the waves, so that K 1024
+ * kept the bits of one copy's launch, measured 5.0-5.3); 0 when it does
+ * not take g. */
+static int gemv_tasks_nt(const struct s3k_gemm *g)
+{
+	const bool k16 = g->K % 512 == 0;
+	if ((!k16 || g->K <= 1024) && gemv_tasks_ok(g, 8, 8))
+		return 8;
+	return gemv_tasks_ok(g, 4, k16 ? 16 : 8) ? 4 : 0;
+}
+
+extern "C" int s3k_gemv_tasks_take(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && (g->flags & S3K_B_NT) && g->c_kind == S3K_F32 &&
+	       g->lda % 4 == 0 && s3h_settings()->gemv_f32 && gemv_tasks_nt(g) != 0;
 }
 
 template <int NT, int KC>
@@ -1517,7 +1541,10 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 		/* one f32 activation row: the f32 VALU kernel */
 		if (g->a_kind == S3K_F32 && g->M == 1 && g->lda % 4 == 0 && s3h_settings()->gemv_f32) {
 			/* a batch: the persistent grid over (copy, row group) tasks */
-			if (gemv_tasks_ok(g, 4, k16 ? 16 : 8))
+			const int tnt = gemv_tasks_nt(g);
+			if (tnt == 8)
+				return launch_gemv_tasks_k<8, 8>(g, stream);
+			if (tnt == 4)
 				return k16 ? launch_gemv_tasks_k<4, 16>(g, stream)
 					   : launch_gemv_tasks_k<4, 8>(g, stream);
 			if (nt == 1)
