@@ -281,6 +281,9 @@ int s3k_skinny_ok(const struct s3k_gemm *g);
 /* Whether a batched one-row skinny launch of g runs on the persistent
  * q8_gemv_tasks. */
 int s3k_gemv_tasks_take(const struct s3k_gemm *g);
+/* Whether a batched skinny launch of g (2-16 f16 activation rows) runs
+ * on the persistent q8_stream_tasks. */
+int s3k_stream_tasks_take(const struct s3k_gemm *g);
 /* Attention operands [B, H, S, D] (f32), up to three (n_out) in one
  * launch: out[y] from columns col0[y].. of rows of `pitch` values holding
  * [B*S, H*D] (the q, k or v part of a fused qkv output), with RoPE
@@ -365,9 +368,10 @@ struct s3h_settings {
 	int att_gemv_fold;                /* SAM3_HIP_ATT_GEMV_FOLD: attention of
 					   * one query over one key left to the
 					   * Q8_0 GEMV reading its output      */
-	int gemv_tasks;                   /* SAM3_HIP_GEMV_TASKS: batches of one-row
-					   * GEMVs on the persistent q8_gemv_tasks
-					   * (1) or one workgroup per task (0)  */
+	int gemv_tasks;                   /* SAM3_HIP_GEMV_TASKS: batches of 1-16
+					   * rows on the persistent q8_gemv_tasks
+					   * and q8_stream_tasks (1) or one
+					   * workgroup per task / the tiled GEMM */
 	int gemv_f32;                     /* SAM3_HIP_GEMV_F32: one f32 activation
 					   * row on the f32 VALU GEMV (1) or on
 					   * the f16 MFMA stream (0)           */

@@ -1391,7 +1391,10 @@ enum sam3_error sam3_hip_matmul_q8_batched(int a_dtype, const void *a, const voi
 			err = a_rows_f16(&h, &a16, stream);
 		if (err == SAM3_OK) {
 			const int force = s3h_settings()->q8_batch_path;
-			const int gemm = h.a_kind == S3K_F16 && batch > 1 &&
+			/* 2-16 rows over enough weight tasks: the persistent
+			 * q8_stream_tasks (skinny launch) before the GEMM */
+			const int tasks = force != 2 && s3k_stream_tasks_take(&h);
+			const int gemm = h.a_kind == S3K_F16 && batch > 1 && !tasks &&
 					 (force == 2 ||
 					  (force != 1 && (M >= S3H_Q8_BATCH_GEMM_M || K <= 256))) &&
 					 s3k_dlq8_eligible(&h);

@@ -1132,6 +1132,170 @@ __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 	wait_vm<0>();
 }
 
+/*
+ * q8_stream_tasks: a batch of weight matrices times 2-16 f16 activation
+ * rows each (config 4's streams of a few tokens), as a persistent grid
+ * with q8_gemv_tasks' walk: tasks (copy z, 128-row group g), task
+ * t = z * groups + g, workgroup w taking tasks w, w + G, ..., all their
+ * 8-block chunks (weight rows and the activation rows) through one
+ * ring. Every task covers all M <= MR rows. Wave w multiplies weight
+ * tile w & 7 (16 rows) by blocks 4 (w >> 3) .. + 3 of each chunk: per
+ * block one v_mfma_f32_16x16x32_f16 of the f16 activations and the exact
+ * integers q, times the block scale in f32 (q8_stream's products), added
+ * into the wave's accumulators block by block. At a task's last chunk
+ * the waves leave their accumulators in a buffer beside the ring (whose
+ * next chunks are in flight) and each output is the sum of its two
+ * halves of k. Rows are whole groups (N % 128 == 0) and K whole chunks;
+ * row factors (S3K_EPI_ROWSCALE), bias and GELU.
+ */
+template <int MR>
+__global__ void __launch_bounds__(1024) q8_stream_tasks(StreamArgs p)
+{
+	constexpr int NT = 8, KC = 8;
+	using C = StreamCfg<S3K_F16, MR, NT, KC, 140>;
+	constexpr int WV = C::WV;
+	static_assert(C::MT == 1 && WV == 2 * NT, "one 16-row A tile; two waves per weight tile");
+	__shared__ __attribute__((aligned(1024))) char smem[C::ST * C::SB + 1024];
+	__shared__ float red[WV * 4 * 64];
+	const int lane = threadIdx.x & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int g16 = lane >> 4, l16 = lane & 15;
+	const int wt = wave & 7, kh = wave >> 3;
+
+	const unsigned rowbytes = (unsigned)(p.K / 32) * 36u;
+	const int nch = p.K / (KC * 32);
+	const int ntask = p.groups * p.nbatch;
+	const int G = (int)gridDim.x;
+	const int mine = (ntask - (int)blockIdx.x + G - 1) / G;
+	const int total = mine * nch;
+
+	/* per-lane part of a chunk's loads: weight rows (PW slots each, the
+	 * last a zero pad), then the M activation rows (XOR-swizzled slots,
+	 * rows past M read zeros), then padding loads into the spare KiB */
+	unsigned off[C::NPW];
+#pragma unroll
+	for (int t = 0; t < C::NPW; ++t) {
+		const int j = t * C::WV + wave;
+		unsigned o = S3K_OOB;
+		if (j < C::IW) {
+			const int i = j * 64 + lane;
+			const int r = i / C::PW, q = i % C::PW;
+			if (i < C::GW && q < C::GPRW)
+				o = (unsigned)r * rowbytes + (unsigned)q * 16u;
+		} else if (j < C::I) {
+			const int i = (j - C::IW) * 64 + lane;
+			const int m = i / C::GAR, sl = i % C::GAR;
+			if (m < p.M)
+				o = (unsigned)(m * p.lda_b) + (unsigned)((sl ^ (m & 15)) * 16);
+		}
+		off[t] = o;
+	}
+	const unsigned lds0 = lds_addr_of(smem);
+	const unsigned aext = (unsigned)((p.M - 1) * p.lda_b + p.K * 2);
+	auto issue = [&](int c) {
+		const int i = c / nch, ch = c - i * nch;
+		const int task = (int)blockIdx.x + i * G;
+		const int z = task / p.groups, g = task - z * p.groups;
+		const s3k_i32x4 rw = buf_rsrc(p.w + z * p.sw_b, p.w_ext);
+		const s3k_i32x4 ra = buf_rsrc(p.a + z * p.sa_b, aext);
+		const unsigned wso = (unsigned)g * C::NR * rowbytes + (unsigned)ch * (KC * 36);
+		const unsigned aso = (unsigned)ch * (KC * 32 * 2);
+		const unsigned st = lds0 + (unsigned)((c % C::ST) * C::SB);
+#pragma unroll
+		for (int t = 0; t < C::NPW; ++t) {
+			const int j = t * C::WV + wave;
+			if (j < C::IW)
+				dma16s(st + j * 1024, rw, off[t], wso);
+			else if (j < C::I)
+				dma16s(st + C::SW + (j - C::IW) * 1024, ra, off[t], aso);
+			else
+				dma16s(lds0 + C::ST * C::SB, rw, S3K_OOB, 0);
+		}
+	};
+
+#pragma unroll
+	for (int s = 0; s < C::ST - 1; ++s)
+		if (s < total)
+			issue(s);
+
+	s3k_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+	for (int c = 0; c < total; ++c) {
+		if (c + C::ST - 2 < total)
+			wait_vm<(C::ST - 2) * C::NPW>();
+		else
+			wait_vm<0>();
+		wg_barrier();
+		if (c + C::ST - 1 < total)
+			issue(c + C::ST - 1);
+		const int i = c / nch, ch = c - i * nch;
+		{
+			const char *Ws = smem + (c % C::ST) * C::SB;
+			const char *As = Ws + C::SW;
+			/* the four blocks' operands first, then the MFMAs, then
+			 * the scale FMAs in block order */
+			uint4 af[4], wf[4];
+			float sc[4];
+#pragma unroll
+			for (int u = 0; u < 4; ++u) {
+				const int kb = 4 * kh + u;
+				af[u] = make_uint4(0, 0, 0, 0);
+				if (l16 < MR) {
+					const int q0 = kb * 4 + g16;
+					af[u] = *(const uint4 *)(As + l16 * (C::GAR * 16) + ((q0 ^ l16) << 4));
+				}
+				const char *blk = Ws + (wt * 16 + l16) * (C::PW * 16) + kb * 36;
+				sc[u] = *(const float *)blk;
+				const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16) ^ 0x80808080u;
+				const uint32_t w1 = *(const uint32_t *)(blk + 8 + 8 * g16) ^ 0x80808080u;
+				wf[u].x = q8pair_to_f16(w0, 0x04010400u);
+				wf[u].y = q8pair_to_f16(w0, 0x04030402u);
+				wf[u].z = q8pair_to_f16(w1, 0x04010400u);
+				wf[u].w = q8pair_to_f16(w1, 0x04030402u);
+			}
+			s3k_f32x4 part[4];
+#pragma unroll
+			for (int u = 0; u < 4; ++u)
+				part[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+					__builtin_bit_cast(s3k_f16x8, af[u]), __builtin_bit_cast(s3k_f16x8, wf[u]),
+					(s3k_f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+			for (int u = 0; u < 4; ++u)
+#pragma unroll
+				for (int j = 0; j < 4; ++j)
+					acc[j] += part[u][j] * sc[u];
+		}
+		if (ch == nch - 1) {
+			/* the task's outputs: each wave's accumulators into red,
+			 * then output o = (tile, j, lane) of the first half of k
+			 * plus the same of the second; two per thread */
+#pragma unroll
+			for (int j = 0; j < 4; ++j)
+				red[(wave * 4 + j) * 64 + lane] = acc[j];
+			acc = (s3k_f32x4){0.f, 0.f, 0.f, 0.f};
+			__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+			wg_barrier();
+			const int task = (int)blockIdx.x + i * G;
+			const int z = task / p.groups, g = task - z * p.groups;
+#pragma unroll
+			for (int h = 0; h < 2; ++h) {
+				const int o = (int)threadIdx.x + h * 1024;
+				float s = red[o] + red[o + NT * 4 * 64];
+				const int ln = o & 63, j = (o >> 6) & 3, t = o >> 8;
+				const int m = 4 * (ln >> 4) + j;
+				const int n = g * C::NR + t * 16 + (ln & 15);
+				if (m < p.M) {
+					if (p.flags & S3K_EPI_ROWSCALE)
+						s *= p.rs[z * p.rs_sb + m];
+					const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
+					((float *)p.c + z * p.sc)[(long long)m * p.ldc + n] =
+						epilogue<0>(s, bv, p.flags);
+				}
+			}
+		}
+	}
+	wait_vm<0>();
+}
+
 } /* namespace s3k */
 
 using namespace s3k;
@@ -1416,6 +1580,55 @@ static int launch_gemv_tasks_k(const struct s3k_gemm *g, void *stream)
 	return (int)hipGetLastError();
 }
 
+/* q8_stream_tasks' conditions: a batch of weight matrices times 2-16 f16
+ * activation rows each (or shared), whole 128-row groups and 256-k
+ * chunks, row factors, bias and GELU only, enough tasks to keep one
+ * workgroup per CU busy. */
+static bool stream_tasks_ok(const struct s3k_gemm *g)
+{
+	return g->a_kind == S3K_F16 && g->M >= 2 && g->M <= 16 && g->batch > 1 && g->N % 128 == 0 &&
+	       stream_ok(g) && s3h_settings()->gemv_tasks &&
+	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_ROWSCALE | S3K_B_NT)) &&
+	       (long long)(g->N / 128) * g->batch >= 256;
+}
+
+extern "C" int s3k_stream_tasks_take(const struct s3k_gemm *g)
+{
+	return g->b_kind == S3K_Q8 && (g->flags & S3K_B_NT) && g->c_kind == S3K_F32 &&
+	       s3k_skinny_ok(g) && stream_tasks_ok(g);
+}
+
+template <int MR>
+static int launch_stream_tasks_k(const struct s3k_gemm *g, void *stream)
+{
+	StreamArgs p;
+	memset(&p, 0, sizeof p);
+	p.a = (const char *)g->a;
+	p.w = (const char *)g->b;
+	p.c = (char *)g->c;
+	p.bias = (const char *)g->bias;
+	p.M = g->M;
+	p.N = g->N;
+	p.K = g->K;
+	p.lda_b = g->lda * 2;
+	p.ldc = g->ldc;
+	p.sa_b = g->stride_a * 2;
+	p.sw_b = g->stride_b;
+	p.sc = g->stride_c;
+	p.w_ext = (unsigned)((long long)g->N * (g->K / 32) * 36);
+	p.flags = g->flags;
+	p.groups = g->N / 128;
+	p.zsplit = 1;
+	p.rs = g->rs;
+	p.rs_sb = g->rs_sb;
+	p.nbatch = g->batch;
+	/* one workgroup per CU of the MI355X (256), fewer for fewer tasks */
+	const long long ntask = (long long)p.groups * g->batch;
+	const int grid = ntask < 256 ? (int)ntask : 256;
+	hipLaunchKernelGGL((q8_stream_tasks<MR>), dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
+	return (int)hipGetLastError();
+}
+
 template <int AK, int KC>
 static int launch_stream_a(const struct s3k_gemm *g, int mr, int nt, void *stream)
 {
@@ -1553,6 +1766,10 @@ extern "C" int s3k_skinny_launch(const struct s3k_gemm *g, void *stream)
 				return k16 ? launch_gemv_k<2, 16>(g, stream) : launch_gemv_k<2, 8>(g, stream);
 			return k16 ? launch_gemv_k<4, 16>(g, stream) : launch_gemv_k<4, 8>(g, stream);
 		}
+		/* a batch of a few f16 rows: the persistent grid over tasks */
+		if (stream_tasks_ok(g))
+			return g->M <= 8 ? launch_stream_tasks_k<8>(g, stream)
+					 : launch_stream_tasks_k<16>(g, stream);
 		switch (g->a_kind) {
 		case S3K_F32:
 			return k16 ? launch_stream_a<S3K_F32, 16>(g, mr, nt, stream)

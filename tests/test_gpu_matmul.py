@@ -670,6 +670,52 @@ def test_q8_gemv_tasks_persistent_batch(env, K, N, B, shared):
         b_.free()
 
 
+@pytest.mark.parametrize("M,K,N,B,shared", [(8, 256, 1024, 32, True), (8, 1024, 1024, 33, False),
+                                             (2, 512, 2048, 16, True), (13, 256, 256, 130, False),
+                                             (16, 2048, 1024, 32, True), (5, 1024, 4096, 8, False)])
+def test_q8_stream_tasks_persistent_batch(env, M, K, N, B, shared):
+    """A batch of 2-16 f32 activation rows over weight copies with at
+    least 256 (copy, 128-row group) tasks runs on the persistent
+    q8_stream_tasks after the row-scaled f16 copy of the rows: every row
+    within the f16-operand bound of the oracle (one row scaled past the
+    f16 range, its factor undone in the epilogue), bias and GELU in the
+    epilogue, the activations shared (stride 0) or one set per copy; and
+    close to the path that runs without it (SAM3_HIP_GEMV_TASKS=0: the
+    tiled GEMM, whose q * scale is rounded to f16, or the per-task
+    q8_stream)."""
+    O = oracle()
+    a = rnd(730 + M, (1 if shared else B, M, K))
+    a[:, M // 2] *= np.float32(1e6)
+    ws = [q8(rnd(731 + s_, (N, K), 0.02)) for s_ in range(B)]
+    bias = rnd(732, N, 0.1)
+    dw = hip.DeviceBuffer.of(np.concatenate(ws))
+    da, db = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(bias)
+
+    def run():
+        dc = hip.DeviceBuffer(B * M * N * 4)
+        hip.q8_batched_dev(abi.F32, da.ptr, dw.ptr, dc.ptr, B, M, N, K, 0 if shared else M * K,
+                           ws[0].nbytes, M * N, bias_ptr=db.ptr, flags=hip.BIAS | hip.GELU)
+        hip.synchronize()
+        c = dc.download(np.float32, (B, M, N))
+        dc.free()
+        return c
+
+    c = run()
+    for s_ in range(B):
+        rows = a[0 if shared else s_]
+        ref = O.gelu(O.bias_add(ref_q8(rows, ws[s_], K, N, nt=True), bias, "f32"), "f32")
+        ref = np.asarray(ref).reshape(M, N)
+        for m in range(M):
+            # rows of very different scales: each against its own size
+            assert_f32_close(c[s_, m:m + 1], ref[m:m + 1], what=f"task batch {s_} row {m}")
+    env.set("SAM3_HIP_GEMV_TASKS", 0)
+    c0 = run()
+    for m in range(M):
+        assert_f32_close(c[:, m], c0[:, m], what=f"tasks against the other path, row {m}")
+    for b_ in (da, db, dw):
+        b_.free()
+
+
 def test_q8_batched_falls_back_per_slice():
     """M > 128 is not a skinny problem: one launch per slice, same result."""
     B, M, N, K = 2, 160, 64, 256
