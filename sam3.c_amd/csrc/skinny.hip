@@ -988,25 +988,35 @@ __global__ void __launch_bounds__(1024) q8_gemv(StreamArgs p)
  * + g; workgroup w runs tasks w, w + G, w + 2G, ... (G workgroups) and
  * streams all their chunks through one ring, so the loads of a task's
  * first chunks are in flight while the previous task's last chunks are
- * multiplied; no workgroup starts or drains per task. At a task's last
- * chunk the waves' sums go through LDS (the row's 4 lanes, then the
- * waves in order) and the epilogue stores the task's outputs: the
+ * multiplied; no workgroup starts or drains per task. With 8-block
+ * chunks and TSPLIT the two waves of a block take half the row tiles
+ * each (q8_gemv leaves 8 of its 16 waves idle there). At a
+ * task's last chunk the sums go through LDS (the row's 4 lanes, then the
+ * blocks in order) and the epilogue stores the task's outputs: the
  * arithmetic of q8_gemv<NT, KC>, so its bits (a launch of one copy runs
  * 16-block chunks when K % 512 == 0, which split k over the waves
  * differently from 8-block ones; with KC = 8 for such K the sums agree
  * to a few ulps). Rows are whole groups (N % NR == 0) and K whole
  * chunks; bias and GELU only.
  */
-template <int NT, int KC>
+template <int NT, int KC, bool TSPLIT>
 __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 {
 	using C = StreamCfg<S3K_F32, 1, NT, KC, 144>;
 	constexpr int WV = C::WV;
+	/* TSPLIT: every wave multiplies; with fewer k-blocks per chunk than
+	 * waves (KC = 8) the waves of block kb split the row tiles, TS ways.
+	 * Otherwise waves past CW only load. */
+	constexpr int TS = TSPLIT ? WV / C::CW : 1, NTW = NT / TS;
+	static_assert(C::U == 1 || TS == 1, "tiles split only with one block per wave");
+	static_assert(NT % TS == 0, "tiles split evenly");
 	__shared__ __attribute__((aligned(1024))) char smem[C::ST * C::SB + 1024];
-	__shared__ float red[WV * C::NR];
+	__shared__ float red[C::CW * C::NR];
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* wave-uniform LDS addresses */
 	const int g16 = lane >> 4, l16 = lane & 15;
+	const int kw = wave % C::CW, t0 = (wave / C::CW) * NTW; /* block slot, first tile */
+	const bool active = wave < C::CW * TS;
 
 	const unsigned rowbytes = (unsigned)(p.K / 32) * 36u;
 	const int nch = p.K / (KC * 32);
@@ -1061,9 +1071,9 @@ __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 		if (s < total)
 			issue(s);
 
-	float acc[NT];
+	float acc[NTW];
 #pragma unroll
-	for (int t = 0; t < NT; ++t)
+	for (int t = 0; t < NTW; ++t)
 		acc[t] = 0.0f;
 	for (int c = 0; c < total; ++c) {
 		if (c + C::ST - 2 < total)
@@ -1074,18 +1084,19 @@ __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 		if (c + C::ST - 1 < total)
 			issue(c + C::ST - 1);
 		const int i = c / nch, ch = c - i * nch;
-		if (C::CW >= WV || wave < C::CW) {
+		if (active) {
 			const char *Ws = smem + (c % C::ST) * C::SB;
 			const char *As = Ws + C::SW;
 #pragma unroll
 			for (int u = 0; u < C::U; ++u) {
-				const int kb = u * C::CW + wave;
+				const int kb = u * C::CW + kw;
 				const int q0 = kb * 8 + 2 * g16;
 				const float4 x = *(const float4 *)(As + (q0 << 4));
 				const float4 y = *(const float4 *)(As + ((q0 + 1) << 4));
 				const float a[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
 #pragma unroll
-				for (int t = 0; t < NT; ++t) {
+				for (int tt = 0; tt < NTW; ++tt) {
+					const int t = t0 + tt;
 					const char *blk = Ws + (t * 16 + l16) * (C::PW * 16) + kb * 36;
 					const float sc = *(const float *)blk;
 					const uint32_t w0 = *(const uint32_t *)(blk + 4 + 8 * g16);
@@ -1097,22 +1108,23 @@ __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 #pragma unroll
 					for (int e = 0; e < 4; ++e)
 						s8 = fmaf(a[4 + e], (float)(int)(signed char)(w1 >> (8 * e)), s8);
-					acc[t] = fmaf(sc, s8, acc[t]);
+					acc[tt] = fmaf(sc, s8, acc[tt]);
 				}
 			}
 		}
 		if (ch == nch - 1) {
-			/* the task's sums: the row's 4 lanes, then the waves in order */
+			/* the task's sums: the row's 4 lanes, then the block slots
+			 * in order */
 #pragma unroll
-			for (int t = 0; t < NT; ++t) {
-				float v = acc[t] + __int_as_float(__builtin_amdgcn_ds_swizzle(
-							   __float_as_int(acc[t]), 0x401F));
+			for (int tt = 0; tt < NTW; ++tt) {
+				float v = acc[tt] + __int_as_float(__builtin_amdgcn_ds_swizzle(
+							    __float_as_int(acc[tt]), 0x401F));
 				const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
 										 __float_as_uint(v), false, false);
 				v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-				if (g16 == 0)
-					red[wave * C::NR + t * 16 + l16] = v;
-				acc[t] = 0.0f;
+				if (g16 == 0 && active)
+					red[kw * C::NR + (t0 + tt) * 16 + l16] = v;
+				acc[tt] = 0.0f;
 			}
 			__builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
 			wg_barrier();
@@ -1122,7 +1134,7 @@ __global__ void __launch_bounds__(1024) q8_gemv_tasks(StreamArgs p)
 				const int n = g * C::NR + (int)threadIdx.x;
 				float sum = 0.0f;
 #pragma unroll
-				for (int w = 0; w < WV; ++w)
+				for (int w = 0; w < C::CW; ++w)
 					sum += red[w * C::NR + threadIdx.x];
 				const float bv = (p.flags & S3K_EPI_BIAS) ? ((const float *)p.bias)[n] : 0.0f;
 				((float *)p.c + z * p.sc)[n] = epilogue<0>(sum, bv, p.flags);
@@ -1575,8 +1587,16 @@ static int launch_gemv_tasks_k(const struct s3k_gemm *g, void *stream)
 	/* one workgroup per CU of the MI355X (256), fewer for fewer tasks */
 	const long long ntask = (long long)p.groups * g->batch;
 	const int grid = ntask < 256 ? (int)ntask : 256;
-	hipLaunchKernelGGL((q8_gemv_tasks<NT, KC>), dim3(grid), dim3(C::WV * 64), 0, (hipStream_t)stream,
-			   p);
+	/* tasks of one chunk (K = 256): all waves multiply, split over the
+	 * row tiles (config 4, K 256: 4.8 against 4.35 TB/s); from two
+	 * chunks on the idle half measured faster (K 1024: 5.85 against 5.7),
+	 * same bits either way */
+	if (g->K == KC * 32)
+		hipLaunchKernelGGL((q8_gemv_tasks<NT, KC, true>), dim3(grid), dim3(C::WV * 64), 0,
+				   (hipStream_t)stream, p);
+	else
+		hipLaunchKernelGGL((q8_gemv_tasks<NT, KC, false>), dim3(grid), dim3(C::WV * 64), 0,
+				   (hipStream_t)stream, p);
 	return (int)hipGetLastError();
 }
 
