@@ -1534,10 +1534,11 @@ static int launch_gemv_k(const struct s3k_gemm *g, void *stream)
  * 32-block chunks of 32 or 16 rows 3.5-6.1, against 5.5-6.3.) */
 static bool gemv_tasks_ok(const struct s3k_gemm *g, int nt, int kc)
 {
+	const long long ntask = (long long)(g->N / (16 * nt)) * g->batch;
 	return g->a_kind == S3K_F32 && g->M == 1 && g->batch > 1 && g->N % (16 * nt) == 0 &&
 	       g->K % (kc * 32) == 0 && stream_ok(g) && s3h_settings()->gemv_tasks &&
-	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT)) &&
-	       (long long)(g->N / (16 * nt)) * g->batch >= 256;
+	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_B_NT)) && ntask >= 256 &&
+	       ntask * (g->K / (kc * 32)) < (1LL << 31); /* tasks and chunks in int */
 }
 
 /* The persistent GEMV's row groups for g: 128 rows in 8-block chunks up
@@ -1606,10 +1607,11 @@ static int launch_gemv_tasks_k(const struct s3k_gemm *g, void *stream)
  * workgroup per CU busy. */
 static bool stream_tasks_ok(const struct s3k_gemm *g)
 {
+	const long long ntask = (long long)(g->N / 128) * g->batch;
 	return g->a_kind == S3K_F16 && g->M >= 2 && g->M <= 16 && g->batch > 1 && g->N % 128 == 0 &&
 	       stream_ok(g) && s3h_settings()->gemv_tasks &&
 	       !(g->flags & ~(S3K_EPI_BIAS | S3K_EPI_GELU | S3K_EPI_ROWSCALE | S3K_B_NT)) &&
-	       (long long)(g->N / 128) * g->batch >= 256;
+	       ntask >= 256 && ntask * (g->K / 256) < (1LL << 31); /* tasks and chunks in int */
 }
 
 extern "C" int s3k_stream_tasks_take(const struct s3k_gemm *g)
