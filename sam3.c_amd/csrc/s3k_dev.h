@@ -16,6 +16,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 s3k_bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 s3k_f16x8;
 typedef __attribute__((ext_vector_type(16))) float s3k_f32x16;
 typedef __attribute__((ext_vector_type(4))) float s3k_f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned s3k_u32x4;
 
 namespace s3k {
 
