@@ -542,7 +542,12 @@ __device__ __forceinline__ void write_tile_ck(const GemmArgs &p, s3k_f32x16 (&ac
 					 * written once and not read back by this kernel,
 					 * so it need not displace the operand panels
 					 * other workgroups still read from the caches
-					 * (fc1 983 -> 994 TFLOP/s, config 1 30.4 -> 29.0 us) */
+					 * (fc1 983 -> 994 TFLOP/s, config 1 30.4 -> 29.0 us,
+					 * Q K^T scores 241 -> 208 us). The general path
+					 * below keeps plain stores: its operand copies
+					 * and residual sums are read by the next kernel
+					 * at once, and streaming stores there made the
+					 * ViT block 3 % slower. */
 					const long long o = (long long)m * p.ldc + n;
 					if constexpr (CK == S3K_F32) {
 						__builtin_nontemporal_store((s3k_f32x4){v[it][0], v[it][1], v[it][2], v[it][3]},
