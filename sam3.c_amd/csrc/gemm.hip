@@ -504,6 +504,7 @@ extern "C" int s3k_gemm_path(const struct s3k_gemm *g)
 static GemmArgs make_args(const struct s3k_gemm *g)
 {
 	GemmArgs p;
+	p.tstrip = 0;
 	const int ea = esize(g->a_kind);
 	p.a = (const char *)g->a;
 	p.b = (const char *)g->b;

@@ -39,6 +39,7 @@ struct GemmArgs {
 	float *qkv_out[3];
 	const float *qkv_cos, *qkv_sin;
 	int qkv_S, qkv_H, qkv_dsh, qkv_rope;
+	int tstrip;   /* tile order (tile_of): 0, or N strips of this many tiles */
 };
 
 enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };
@@ -101,12 +102,29 @@ __device__ __forceinline__ void mfma_chunk(s3k_f32x16 &acc, const uint4 &a, cons
  * the 8 XCDs; ids are regrouped so each XCD gets a contiguous range of
  * tiles, walked in groups of 8 tile-rows so that workgroups resident on
  * one XCD share A rows and B columns in that XCD's L2. */
-__device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int &tm, int &tn)
+__device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int &tm, int &tn,
+					int strip = 0)
 {
 	const int nwg = tiles_m * tiles_n;
 	int t = wg;
 	if ((nwg & 7) == 0)
 		t = (wg & 7) * (nwg >> 3) + (wg >> 3);
+	if (strip > 0 && (nwg & 7) == 0) {
+		/* N strips of `strip` tile columns, each walked row by row, cut
+		 * into the XCDs' runs of nwg / 8 */
+		const int full = tiles_n / strip, per = tiles_m * strip;
+		const int s = t / per;
+		if (s < full) {
+			const int i = t - s * per;
+			tm = i / strip;
+			tn = s * strip + i % strip;
+		} else {
+			const int w = tiles_n - full * strip, i = t - full * per;
+			tm = i / w;
+			tn = full * strip + i % w;
+		}
+		return;
+	}
 	const int G = 8;
 	const int per_group = G * tiles_n;
 	const int g = t / per_group;

@@ -226,7 +226,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) gemm_dlp(GemmArgs p)
 	const int bz = blockIdx.y;
 	const unsigned lds0 = lds_addr_of(smem);
 	int tm, tn;
-	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn, p.tstrip);
 	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
 	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
 
@@ -722,6 +722,14 @@ static int launch_dlp_cfg(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 		return (int)hipErrorInvalidValue;
 	p.tiles_m = (p.M + BM - 1) / BM;
 	p.tiles_n = (p.N + BN - 1) / BN;
+	/* tiles in N strips of 8 columns, cut into the XCDs' runs: each XCD
+	 * reads fewer distinct A and W panels (fc1: a floor of 57 MB of
+	 * fetches against 68 for the grouped order). One box, three
+	 * interleaved runs: fc2 821-835 -> 840-849 TFLOP/s, config 1
+	 * 28.4-28.9 -> 27.9-28.1 us, f16 fc1 +0.8 %, fc1 +0.4 % (within
+	 * noise); 6-column strips favoured fc1 (+0.9 %) but not config 1
+	 * or the Q8 step */
+	p.tstrip = 8;
 	if (g->a_kind == S3K_BF16)
 		return launch_dlp_fam<BM, BN, WGM, WGN, INTER, FAM_BF16>(g, p, st);
 	return launch_dlp_fam<BM, BN, WGM, WGN, INTER, FAM_F16>(g, p, st);
