@@ -505,6 +505,7 @@ static GemmArgs make_args(const struct s3k_gemm *g)
 {
 	GemmArgs p;
 	p.tstrip = 0;
+	p.xwalk = 0;
 	const int ea = esize(g->a_kind);
 	p.a = (const char *)g->a;
 	p.b = (const char *)g->b;

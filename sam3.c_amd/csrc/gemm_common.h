@@ -40,6 +40,7 @@ struct GemmArgs {
 	const float *qkv_cos, *qkv_sin;
 	int qkv_S, qkv_H, qkv_dsh, qkv_rope;
 	int tstrip;   /* tile order (tile_of): 0, or N strips of this many tiles */
+	int xwalk;    /* gemm_dlk: each slice's tiles on one XCD (1) */
 };
 
 enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };

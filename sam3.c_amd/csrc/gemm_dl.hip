@@ -436,11 +436,27 @@ __global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
 		}
 	}
 
-	int t = blockIdx.x;
-	if (t >= total)
+	/* the walk: tile t = w, w + G, ... (G workgroups); or (xcd walk,
+	 * G % 8 == 0) workgroup w, the (w / 8)-th of XCD w % 8 (workgroups
+	 * are dispatched to the 8 XCDs round-robin), takes items w / 8,
+	 * w / 8 + G / 8, ... of its XCD's list, the tiles of slices
+	 * w % 8, w % 8 + 8, ...: a slice's tiles run on one XCD, whose L2
+	 * then serves its panels to all of them */
+	const bool xw = p.xwalk && (gridDim.x & 7) == 0;
+	const int xr = (int)gridDim.x >> 3, xx = (int)blockIdx.x & 7;
+	const int nslice = total / per_slice;
+	const int xn = xw ? ((nslice - xx + 7) >> 3) * per_slice : 0;
+	auto tile_at = [&](int q) { /* item q of this XCD's list */
+		const int sl = q / per_slice;
+		return (xx + 8 * sl) * per_slice + (q - sl * per_slice);
+	};
+	int q = xw ? (int)blockIdx.x >> 3 : (int)blockIdx.x;
+	const int qend = xw ? xn : total, qstep = xw ? xr : (int)gridDim.x;
+	if (q >= qend)
 		return;
+	int t = xw ? tile_at(q) : q;
 	load_tile(t, 0);
-	for (int i = 0; t < total; ++i, t += gridDim.x) {
+	for (int i = 0; q < qend; ++i, q += qstep, t = xw ? tile_at(q) : q) {
 		const int b = i & 1;
 		/* this tile's panels: issued before the previous tile's stores */
 		if (i == 0)
@@ -477,9 +493,8 @@ __global__ void __launch_bounds__(128 * WGN, 1) gemm_dlk(GemmArgs p, int total)
 		/* every wave is done with buffer b ^ 1 (read in the previous
 		 * tile) and with its own fragment reads of b */
 		wg_barrier();
-		const int tn2 = t + (int)gridDim.x;
-		if (tn2 < total)
-			load_tile(tn2, b ^ 1);
+		if (q + qstep < qend)
+			load_tile(xw ? tile_at(q + qstep) : q + qstep, b ^ 1);
 		int bz, tm, tn;
 		coords(t, bz, tm, tn);
 		write_tile_ck<FM, FN, WTN, CK, true>(p, acc, smem + 2 * STAGE, wave, lane, tm * BM + wm0,
@@ -674,6 +689,9 @@ static int launch_dlk(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	}
 	const dim3 grid((unsigned)(total < cus ? total : cus));
 	const dim3 block(128 * WGN);
+	/* a slice's tiles on one XCD: Q K^T over 1296 slices of 576 x 576,
+	 * 206-209 -> 188-190 us (one box, three interleaved runs) */
+	p.xwalk = 1;
 	if (g->c_kind == S3K_F32)
 		hipLaunchKernelGGL((gemm_dlk<FAM, S3K_F32, WGN>), grid, block, 0, st, p, total);
 	else if (FAM == FAM_BF16)
