@@ -40,7 +40,8 @@ struct GemmArgs {
 	const float *qkv_cos, *qkv_sin;
 	int qkv_S, qkv_H, qkv_dsh, qkv_rope;
 	int tstrip;   /* tile order (tile_of): 0, or N strips of this many tiles */
-	int xwalk;    /* gemm_dlk: each slice's tiles on one XCD (1) */
+	int xwalk;    /* each slice's tiles on one XCD: gemm_dlk 1; gemm_dlt the
+		       * slice count of its grouped 1-D grid; 0 off */
 };
 
 enum { FAM_BF16 = 0, FAM_F16 = 1, FAM_F32 = 2 };

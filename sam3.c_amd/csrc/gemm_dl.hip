@@ -549,10 +549,31 @@ __global__ void __launch_bounds__(64 * WGM * WGN, OCC) gemm_dlt(GemmArgs p)
 	const int lane = threadIdx.x & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
-	const int bz = blockIdx.y;
+	/* slice bz, tile tt: a 2-D grid (tiles, slices), or with xwalk a 1-D
+	 * one in which the tiles of 8 slices in a row form a group, ordered
+	 * so that each slice's tiles share a residue mod 8: workgroups go to
+	 * the 8 XCDs round-robin, so a slice's tiles run on one XCD and its
+	 * panels are fetched into one L2 */
+	int bz = blockIdx.y, tt = blockIdx.x;
+	if (p.xwalk) {
+		const int ps = p.tiles_m * p.tiles_n, L = blockIdx.x;
+		const int g8 = (p.xwalk >> 3) * 8 * ps; /* p.xwalk: the slice count */
+		if (L < g8) {
+			const int g = L / (8 * ps), r = L - g * 8 * ps;
+			bz = 8 * g + (r & 7);
+			tt = r >> 3;
+		} else {
+			bz = (p.xwalk >> 3) * 8 + (L - g8) / ps;
+			tt = (L - g8) % ps;
+		}
+		/* uniform, but the integer division leaves them in vector
+		 * registers: the direct-to-LDS loads need scalar ones */
+		bz = __builtin_amdgcn_readfirstlane(bz);
+		tt = __builtin_amdgcn_readfirstlane(tt);
+	}
 	const unsigned lds0 = lds_addr_of(smem);
 	int tm, tn;
-	tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+	tile_of(tt, p.tiles_m, p.tiles_n, tm, tn);
 	const s3k_i32x4 ra = buf_rsrc(p.a + bz * p.sa_b, p.a_extent);
 	const s3k_i32x4 rb = buf_rsrc(p.b + bz * p.sb_b, p.b_extent);
 
@@ -841,7 +862,16 @@ int s3k_dlt_launch(const struct s3k_gemm *g, GemmArgs p, hipStream_t st)
 	const bool narrow = dlt_narrow(g);
 	p.tiles_m = (g->M + 191) / 192;
 	p.tiles_n = g->N / (narrow ? 64 : 256);
-	const dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	dim3 grid(p.tiles_m * p.tiles_n, g->batch);
+	/* 8 slices or more: the 1-D grid whose groups keep each slice's
+	 * tiles on one XCD (attention P V over 1296 slices: 195-199 -> 188-191
+	 * us, one box, three interleaved runs) */
+	const long long nwg = (long long)p.tiles_m * p.tiles_n * g->batch;
+	p.xwalk = 0;
+	if (g->batch >= 8 && nwg < (1LL << 31)) {
+		p.xwalk = g->batch;
+		grid = dim3((unsigned)nwg, 1);
+	}
 	if (!(g->c_kind == S3K_F32 || g->c_kind == g->a_kind))
 		return (int)hipErrorInvalidValue;
 #define S3K_DLT(BN_, WGN_, OCC_, FAM_, CK_)                                                  \
