@@ -614,7 +614,8 @@ def test_q8_gemv_f32_one_row(env, K, N):
 @pytest.mark.parametrize("K,N,B,shared", [(1024, 1024, 20, True), (4096, 1024, 5, False),
                                            (512, 256, 70, True), (512, 2048, 9, False),
                                            (1024, 2048, 20, True), (256, 256, 130, False),
-                                           (256, 2048, 17, True)])
+                                           (256, 2048, 17, True), (768, 1024, 37, False),
+                                           (1536, 2048, 19, True)])
 def test_q8_gemv_tasks_persistent_batch(env, K, N, B, shared):
     """A batch of one-row GEMVs with at least 256 (copy, 64- or 128-row
     group) tasks runs on the persistent q8_gemv_tasks (one workgroup per
@@ -672,7 +673,8 @@ def test_q8_gemv_tasks_persistent_batch(env, K, N, B, shared):
 
 @pytest.mark.parametrize("M,K,N,B,shared", [(8, 256, 1024, 32, True), (8, 1024, 1024, 33, False),
                                              (2, 512, 2048, 16, True), (13, 256, 256, 130, False),
-                                             (16, 2048, 1024, 32, True), (5, 1024, 4096, 8, False)])
+                                             (16, 2048, 1024, 32, True), (5, 1024, 4096, 8, False),
+                                             (4, 768, 2048, 19, False), (11, 768, 1024, 37, True)])
 def test_q8_stream_tasks_persistent_batch(env, M, K, N, B, shared):
     """A batch of 2-16 f32 activation rows over weight copies with at
     least 256 (copy, 128-row group) tasks runs on the persistent
